@@ -1,0 +1,234 @@
+"""BitLinear benchmark on one MI355X.
+
+Default workload: the Llama-3-8B decode GEMV set at M=1.
+32 distinct layers of absmean-ternarised N(0, 0.02) weights (1.745 GB packed, far
+above the 256 MB Infinity Cache); per layer the dependency-ordered launches a
+decoder issues:
+    q|k|v  (one grouped launch, 4096 -> 4096+1024+1024)
+    o      (4096 -> 4096)
+    w1|w3  (one grouped launch, 4096 -> 2 x 14336)
+    w2     (14336 -> 4096)
+bf16 activations N(0,1) with 0.1% outliers at +-20 in, bf16 out, W1.58-A8 arithmetic
+(per-token absmax int8 activations, exact int32 accumulation).  One step = one token
+through all 32 layers (224 projections, 128 launches) replayed from a HIP graph.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py --config prefill|sweep   (secondary workloads, own JSON line)
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "bit-ttt-engine_amd"))
+
+import bitlinear as bl  # noqa: E402
+
+HIDDEN, INTER, KV = 4096, 14336, 1024
+LAYERS = 32
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+METRIC = "BitLinear GEMV/GEMM µs & % HBM/int8-MFMA roofline; tok/s, Llama-3-8B shapes"
+
+
+def synth_packed(n, k, gen, device):
+    """Absmean-ternarise N(0, 0.02) weights and pack them in the reference layout,
+    on the GPU with torch (synthetic-data plumbing, mirrors PackedTensor::pack)."""
+    w = torch.randn((n, k), device=device, generator=gen, dtype=torch.float32) * 0.02
+    scale = np.float32(np.float32(w.abs().double().mean().item()) + np.float32(1e-6))
+    inv = float(np.float32(1.0 / np.float64(scale)))
+    v = w * inv
+    del w
+    t = (torch.sign(v) * torch.floor(v.abs() + 0.5)).clamp_(-1, 1)
+    del v
+    codes = torch.where(t > 0.5, 1, torch.where(t < -0.5, 2, 0)).to(torch.uint8).view(-1, 4)
+    del t
+    packed = codes[:, 0] | (codes[:, 1] << 2) | (codes[:, 2] << 4) | (codes[:, 3] << 6)
+    return bl.PackedTensor(packed.contiguous(), float(scale), (n, k), device)
+
+
+def synth_act(m, k, gen, device):
+    x = torch.randn((m, k), device=device, generator=gen, dtype=torch.float32)
+    cnt = int(np.ceil(0.001 * k))
+    for i in range(m):
+        pos = torch.randperm(k, device=device, generator=gen)[:cnt]
+        sign = torch.where(torch.rand(cnt, device=device, generator=gen) < 0.5, -20.0, 20.0)
+        x[i, pos] = sign
+    return x.to(torch.bfloat16)
+
+
+class Call:
+    """A pre-bound C-ABI call (pointers resolved once, so graph capture and timing
+    loops pay no Python argument handling)."""
+
+    def __init__(self, layers, x, outs):
+        import ctypes
+        self.cs = [l.as_c() for l in layers]
+        self.n = len(layers)
+        self.arr = (ctypes.POINTER(bl.BtlPacked) * self.n)(*[ctypes.pointer(c) for c in self.cs])
+        self.ys = (ctypes.c_void_p * self.n)(*[o.data_ptr() for o in outs])
+        self.x = x
+        self.m, self.k = x.shape
+        self.bytes = sum(l.data.numel() for l in layers) + x.numel() * x.element_size() + sum(
+            o.numel() * o.element_size() for o in outs)
+
+    def __call__(self, stream):
+        bl.check(bl.lib.btl_linear_group(self.arr, self.ys, self.n, self.x.data_ptr(), bl.BTL_BF16,
+                                         self.m, self.k, bl.BTL_BF16, None, 0, stream))
+
+
+def event_time_us(fn, reps, stream):
+    """Average duration of fn's launch, from HIP events recorded on its stream."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        fn(stream)
+        b.record()
+    torch.cuda.synchronize()
+    return 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / reps
+
+
+def cpu_baseline(host_layers, seconds):
+    """The reference's CPU BitLinear (cpu.rs, restated with AVX2 intrinsics and a
+    thread pool, oracle/) on a bounded sample: the 7 projections of 4 of the 32
+    layers, fp32 activations, repeated for about `seconds`."""
+    from oracle import oracle as orc
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(0)
+    xs = {k: rng.standard_normal((1, k)).astype(np.float32) for k in (HIDDEN, INTER)}
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for proj in host_layers:
+            for (wb, n, k, s) in proj:
+                orc.forward_f32_avx2(xs[k], wb, n, s, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and reps >= 2:
+            break
+    per_token = el / reps * (LAYERS / len(host_layers))
+    return {"value": round(1.0 / per_token, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "%d reps of layers 0-%d of 32 (7 projections each, %.0f MB packed), M=1 fp32, "
+                      "cpu.rs algorithm restated in C with AVX2+FMA intrinsics, %d threads; %.1f s"
+                      % (reps, len(host_layers) - 1,
+                         sum(wb.size for p in host_layers for (wb, _, _, _) in p) / 1e6, threads, el)}
+
+
+def run_decode(args):
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bl.check(bl.lib.btl_init(0))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xB17EB17E)
+    shapes = {"q": (HIDDEN, HIDDEN), "k": (KV, HIDDEN), "v": (KV, HIDDEN), "o": (HIDDEN, HIDDEN),
+              "gate": (INTER, HIDDEN), "up": (INTER, HIDDEN), "down": (HIDDEN, INTER)}
+    layers = []
+    for _ in range(LAYERS):
+        layers.append({name: synth_packed(n, k, gen, dev) for name, (n, k) in shapes.items()})
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    calls = {"qkv": [], "o": [], "gate_up": [], "down": []}
+    for L in layers:
+        xq, xo, xg, xd = (synth_act(1, HIDDEN, gen, dev), synth_act(1, HIDDEN, gen, dev),
+                          synth_act(1, HIDDEN, gen, dev), synth_act(1, INTER, gen, dev))
+        calls["qkv"].append(Call([L["q"], L["k"], L["v"]], xq,
+                                 [torch.empty((1, HIDDEN), **bf), torch.empty((1, KV), **bf),
+                                  torch.empty((1, KV), **bf)]))
+        calls["o"].append(Call([L["o"]], xo, [torch.empty((1, HIDDEN), **bf)]))
+        calls["gate_up"].append(Call([L["gate"], L["up"]], xg,
+                                     [torch.empty((1, INTER), **bf), torch.empty((1, INTER), **bf)]))
+        calls["down"].append(Call([L["down"]], xd, [torch.empty((1, HIDDEN), **bf)]))
+    order = [calls[c][l] for l in range(LAYERS) for c in ("qkv", "o", "gate_up", "down")]
+    step_bytes = sum(c.bytes for c in order)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream().cuda_stream
+    for c in order:  # sizes the library workspace before capture
+        c(stream)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            s = torch.cuda.current_stream().cuda_stream
+            for c in order:
+                c(s)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+
+    # per-kernel durations (HIP events on the launch stream), one launch per layer
+    kern = {}
+    for name in ("qkv", "o", "gate_up", "down"):
+        us = 0.0
+        for l in range(LAYERS):
+            us += event_time_us(calls[name][l], 1, stream)
+        us /= LAYERS
+        b = calls[name][0].bytes
+        kern[name] = {"us": round(us, 2), "bytes": b, "GB_s": round(b / us / 1e3, 1),
+                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+    dom = kern["gate_up"]
+    result = {
+        "metric": METRIC, "value": round(1000.0 / ms, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8",
+        "data": "synthetic (seeded N(0,0.02) weights absmean-ternarised on the GPU; N(0,1) bf16 "
+                "activations with 0.1% +-20 outliers)",
+        "config": {"workload": "cfg2: Llama-3-8B decode GEMV set, M=1, 32 distinct layers x "
+                               "{q|k|v grouped, o, gate|up grouped, down}, bf16 in/out, W1.58-A8; "
+                               "one step = one token (224 projections, 128 launches, HIP graph)",
+                   "layers": LAYERS, "m": 1, "hidden": HIDDEN, "intermediate": INTER, "kv": KV,
+                   "bytes_per_step": step_bytes,
+                   "step_GB_s": round(step_bytes / ms / 1e6, 1),
+                   "step_frac_hbm": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 3)},
+        "roofline": {"bound": "hbm", "kernel": "k_gemv<XK_BF16,YK_BF16> gate|up 4096->2x14336",
+                     "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["frac_hbm"], "traffic": None,
+                     "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"]},
+        "kernels": kern,
+    }
+    if args.cpu_baseline:
+        host = []
+        for L in layers[:4]:
+            host.append([(L[nm].data.cpu().numpy(), shapes[nm][0], shapes[nm][1], L[nm].scale)
+                         for nm in ("q", "k", "v", "o", "gate", "up", "down")])
+        result["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="decode", choices=["decode"])
+    ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every box here has one GPU); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        sys.exit(1)
+    run_decode(args)
+
+
+if __name__ == "__main__":
+    main()

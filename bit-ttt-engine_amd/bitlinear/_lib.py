@@ -1,0 +1,87 @@
+"""ctypes binding of libbitlinear_hip.so (the C ABI declared in include/bitlinear.h).
+
+The library is required: importing this module raises if it is missing, so no
+code path can silently fall back to a CPU implementation.
+"""
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_PKG), "libbitlinear_hip.so")
+
+BTL_OK = 0
+BTL_ERR_SHAPE = 1
+BTL_ERR_DTYPE = 2
+BTL_ERR_LAYOUT = 3
+BTL_ERR_DEVICE = 4
+BTL_ERR_HIP = 5
+BTL_ERR_ARG = 6
+BTL_ERR_WORKSPACE = 7
+
+BTL_F32 = 0
+BTL_BF16 = 1
+
+BTL_ACT_F32_REF = 0
+BTL_ACT_I8 = 1
+
+# Every symbol include/bitlinear.h declares.
+EXPORTS = (
+    "btl_version", "btl_last_error", "btl_status_string", "btl_init", "btl_packed_bytes",
+    "btl_pack_host", "btl_unpack_host", "btl_unpack_device", "btl_quantize_act", "btl_linear",
+    "btl_linear_i8", "btl_linear_group", "btl_workspace_bytes", "btl_workspace_clear",
+)
+
+
+class BtlPacked(ctypes.Structure):
+    """btl_packed_t: mirrors the reference's PackedTensor (kernels/packing.rs:14-21)."""
+    _fields_ = [("data", ctypes.c_void_p), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("scale", ctypes.c_float)]
+
+
+class BitLinearError(RuntimeError):
+    """A non-zero status from the C ABI; .status holds the code."""
+
+    def __init__(self, status, message):
+        super().__init__(message)
+        self.status = status
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError("libbitlinear_hip.so not built at %s (run bit-ttt-engine_amd/build.py)" % LIB_PATH)
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, i64, i32, f32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    P = ctypes.POINTER
+    sig = {
+        "btl_version": (i32, []),
+        "btl_last_error": (ctypes.c_char_p, []),
+        "btl_status_string": (ctypes.c_char_p, [i32]),
+        "btl_init": (i32, [i32]),
+        "btl_packed_bytes": (i64, [i64, i64]),
+        "btl_pack_host": (i32, [vp, i64, i64, vp, P(f32)]),
+        "btl_unpack_host": (i32, [vp, i64, i64, f32, vp]),
+        "btl_unpack_device": (i32, [P(BtlPacked), vp, vp]),
+        "btl_quantize_act": (i32, [vp, i32, i64, i64, vp, vp, vp]),
+        "btl_linear": (i32, [P(BtlPacked), vp, i32, i64, i64, vp, i32, i32, vp, vp, sz, vp]),
+        "btl_linear_i8": (i32, [P(BtlPacked), vp, vp, i64, i64, vp, i32, vp, vp, sz, vp]),
+        "btl_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, i32, i64, i64, i32, vp, sz, vp]),
+        "btl_workspace_bytes": (sz, [i64, i64, i64, i32]),
+        "btl_workspace_clear": (i32, [vp, sz, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def check(status):
+    """Raise BitLinearError for a non-zero status, with the library's message."""
+    if status != BTL_OK:
+        msg = lib.btl_last_error().decode("utf-8", "replace")
+        name = lib.btl_status_string(status).decode()
+        raise BitLinearError(status, "%s: %s" % (name, msg))
+    return status

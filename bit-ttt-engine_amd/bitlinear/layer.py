@@ -1,0 +1,169 @@
+"""BitLinear layer and its HIP kernel arm (layers/bit_linear.rs, kernels/{cpu,cuda}.rs)."""
+import ctypes
+import warnings
+
+import torch
+
+from ._lib import (
+    BTL_ACT_F32_REF, BTL_ACT_I8, BTL_BF16, BTL_ERR_DEVICE, BTL_ERR_DTYPE, BTL_ERR_LAYOUT, BTL_F32,
+    BitLinearError, BtlPacked, check, lib,
+)
+from .packed import PackedTensor
+
+_DT = {torch.float32: BTL_F32, torch.bfloat16: BTL_BF16}
+_MODES = {"i8": BTL_ACT_I8, "f32_ref": BTL_ACT_F32_REF}
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dtype_code(t, what):
+    if t.dtype not in _DT:
+        raise BitLinearError(BTL_ERR_DTYPE, "%s dtype %s is not float32/bfloat16" % (what, t.dtype))
+    return _DT[t.dtype]
+
+
+def _on_gpu(t, what):
+    if t.device.type != "cuda":
+        # bit_linear.rs:76-84: packed weights on a device without a kernel
+        raise BitLinearError(BTL_ERR_DEVICE, "Packed params present but Custom Kernel not implemented "
+                             "for this device (%s on %s)" % (what, t.device))
+    if not t.is_contiguous():
+        raise BitLinearError(BTL_ERR_LAYOUT, "%s must be contiguous" % what)
+
+
+class Workspace:
+    """A caller-owned workspace for btl_linear* (zeroed once at creation)."""
+
+    def __init__(self, m, n, k, device="cuda", mode=BTL_ACT_I8):
+        self.nbytes = int(lib.btl_workspace_bytes(m, n, k, mode))
+        self.buf = torch.empty(max(self.nbytes, 256), dtype=torch.uint8, device=device)
+        check(lib.btl_workspace_clear(self.buf.data_ptr(), self.nbytes, _stream(self.buf.device)))
+
+    def args(self):
+        return ctypes.c_void_p(self.buf.data_ptr()), self.nbytes
+
+
+def _ws_args(ws):
+    return (None, 0) if ws is None else ws.args()
+
+
+class BitLinearHip:
+    """The HIP arm next to BitLinearCpu::forward (cpu.rs:17) / BitLinearCuda::forward (cuda.rs:21)."""
+
+    @staticmethod
+    def forward(input, weights, mode="i8", out_dtype=None, acc_out=None, workspace=None):
+        """Y = X W^T.  input [M, K] float32/bfloat16 on the GPU, weights a PackedTensor
+        [N, K] on the GPU.  Returns a new [M, N] tensor (dtype out_dtype, default
+        the input's).  mode "i8": W1.58-A8; mode "f32_ref": the reference's fp32
+        semantics and summation order.  acc_out: optional int32 [M, N] tensor that
+        receives the exact accumulators (mode "i8")."""
+        if input.dim() != 2:
+            raise BitLinearError(1, "input must be 2-D, got %s" % (tuple(input.shape),))
+        m, k = input.shape
+        n, kw = weights.dims2()
+        _on_gpu(input, "input")
+        _on_gpu(weights.data, "weights")
+        xdt = _dtype_code(input, "input")
+        out_dtype = out_dtype or input.dtype
+        y = torch.empty((m, n), dtype=out_dtype, device=input.device)
+        ydt = _dtype_code(y, "output")
+        if mode not in _MODES:
+            raise BitLinearError(BTL_ERR_DTYPE, "unknown mode %r" % (mode,))
+        acc_ptr = None
+        if acc_out is not None:
+            if acc_out.dtype != torch.int32 or tuple(acc_out.shape) != (m, n) or not acc_out.is_contiguous():
+                raise BitLinearError(BTL_ERR_LAYOUT, "acc_out must be a contiguous int32 [M, N] tensor")
+            acc_ptr = acc_out.data_ptr()
+        c = weights.as_c()
+        wsp, wsn = _ws_args(workspace)
+        check(lib.btl_linear(ctypes.byref(c), input.data_ptr() if input.numel() else None, xdt, m, k,
+                             y.data_ptr() if y.numel() else None, ydt, _MODES[mode], acc_ptr, wsp, wsn,
+                             _stream(input.device)))
+        return y
+
+
+def quantize_act(x):
+    """Per-token absmax int8 quantisation on the GPU -> (q int8 [M, K], s float32 [M])."""
+    _on_gpu(x, "input")
+    m, k = x.shape
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    check(lib.btl_quantize_act(x.data_ptr() if x.numel() else None, _dtype_code(x, "input"), m, k,
+                               q.data_ptr() if q.numel() else None, s.data_ptr() if m else None,
+                               _stream(x.device)))
+    return q, s
+
+
+def linear_i8(q, s, weights, out_dtype=torch.float32, acc_out=None, workspace=None):
+    """Contraction of pre-quantised activations (btl_linear_i8)."""
+    _on_gpu(q, "input")
+    m, k = q.shape
+    n, _ = weights.dims2()
+    y = torch.empty((m, n), dtype=out_dtype, device=q.device)
+    c = weights.as_c()
+    wsp, wsn = _ws_args(workspace)
+    check(lib.btl_linear_i8(ctypes.byref(c), q.data_ptr() if q.numel() else None,
+                            s.data_ptr() if s.numel() else None, m, k, y.data_ptr() if y.numel() else None,
+                            _dtype_code(y, "output"), acc_out.data_ptr() if acc_out is not None else None,
+                            wsp, wsn, _stream(q.device)))
+    return y
+
+
+def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None):
+    """Several layers reading the same input in one launch (q|k|v, w1|w3)."""
+    _on_gpu(x, "input")
+    m, k = x.shape
+    out_dtype = out_dtype or x.dtype
+    if outputs is None:
+        outputs = [torch.empty((m, w.dims2()[0]), dtype=out_dtype, device=x.device) for w in weights]
+    cs = [w.as_c() for w in weights]
+    arr = (ctypes.POINTER(BtlPacked) * len(cs))(*[ctypes.pointer(c) for c in cs])
+    ys = (ctypes.c_void_p * len(cs))(*[o.data_ptr() for o in outputs])
+    wsp, wsn = _ws_args(workspace)
+    check(lib.btl_linear_group(arr, ys, len(cs), x.data_ptr(), _dtype_code(x, "input"), m, k,
+                               _dtype_code(outputs[0], "output"), wsp, wsn, _stream(x.device)))
+    return outputs
+
+
+class BitLinear:
+    """1.58-bit linear layer (layers/bit_linear.rs:12-21)."""
+
+    def __init__(self, weight, in_features, out_features):
+        self.weight = weight
+        self.in_features = in_features
+        self.out_features = out_features
+        self.packed_params = None
+
+    @staticmethod
+    def load(in_dim, out_dim, weight, device="cuda"):
+        """bit_linear.rs:24-41, with the dense [out_dim, in_dim] weight given directly."""
+        if tuple(weight.shape) != (out_dim, in_dim):
+            raise BitLinearError(1, "weight shape %s is not [%d, %d]" % (tuple(weight.shape), out_dim, in_dim))
+        return BitLinear(weight.to(device, torch.float32).contiguous(), in_dim, out_dim)
+
+    def precompute_packed(self):
+        """bit_linear.rs:44-50: absmean-ternarise and pack once."""
+        self.packed_params = PackedTensor.pack(self.weight)
+
+    def forward(self, x, mode="i8"):
+        """bit_linear.rs:52-119: flatten rank > 2 to [B*T, K], run the packed kernel,
+        reshape back.  Without packed params this is the reference's STE training
+        path (x @ round(W/mean|W|).clamp(-1,1)^T, no scale; bit_linear.rs:98-118)."""
+        orig = None
+        inp = x
+        if x.dim() > 2:
+            orig = list(x.shape)
+            inp = x.reshape(-1, x.shape[-1])
+        if self.packed_params is not None:
+            y = BitLinearHip.forward(inp.contiguous(), self.packed_params, mode=mode)
+            if orig is not None:
+                orig[-1] = y.shape[1]
+                return y.reshape(orig)
+            return y
+        warnings.warn("BitLinear: no packed params, using the STE training path", stacklevel=2)
+        w = self.weight
+        v = w / w.abs().mean()
+        w_q = (torch.sign(v) * torch.floor(v.abs() + 0.5)).clamp(-1.0, 1.0)  # f32::round, half away
+        return x.to(torch.float32) @ w_q.t()

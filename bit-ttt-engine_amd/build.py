@@ -1,0 +1,73 @@
+"""Build libbitlinear_hip.so (gfx950) in-tree.
+
+    python bit-ttt-engine_amd/build.py
+
+Kernels (btl_kernels.hip) are compiled by hipcc for gfx950 only; the C-ABI layer
+(btl_api.cpp) is host C++.  The shared library lands next to this file so that
+it travels with the source tree to the GPU box.
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libbitlinear_hip.so")
+
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+
+# -ffp-contract=off: fp32 results are defined operation by operation (the
+# quantiser and the reference-order path must match the CPU restatement bit
+# for bit).  -packed-fp32-ops: no v_pk_*_f32 in the device code.
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+             "-I" + os.path.join(ROCM, "include")]
+
+KERNEL_SOURCES = ["btl_kernels.hip"]
+HOST_SOURCES = ["btl_api.cpp"]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in res.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if res.returncode != 0:
+        raise RuntimeError("command failed (%d): %s\n%s" % (res.returncode, " ".join(cmd), out))
+    if verbose and out.strip():
+        print(out)
+
+
+def build(verbose=False):
+    """Compile every source and link libbitlinear_hip.so; returns its path."""
+    os.makedirs(BUILD, exist_ok=True)
+    objs = []
+    inc = ["-I" + INCLUDE, "-I" + CSRC]
+    for src in KERNEL_SOURCES:
+        obj = os.path.join(BUILD, src + ".o")
+        _run([HIPCC] + HIP_FLAGS + inc + ["-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        objs.append(obj)
+    cxx = shutil.which("g++") or "g++"
+    for src in HOST_SOURCES:
+        obj = os.path.join(BUILD, src + ".o")
+        _run([cxx] + CXX_FLAGS + inc + ["-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp] + objs +
+         ["-Wl,-soname,libbitlinear_hip.so"], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,483 @@
+// btl_api.cpp -- the C ABI (include/bitlinear.h): validation, error reporting,
+// workspace management, host-side packing and kernel dispatch.
+//
+// Host-side counterpart of the reference's BitLinearCpu/BitLinearCuda::forward
+// (crates/rust_engine/src/kernels/cpu.rs:17-127, cuda.rs:21-47) and
+// PackedTensor::{pack, unpack} (kernels/packing.rs:50-133).
+#include "bitlinear.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "btl_internal.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    return fail(BTL_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+    bool probed = false;
+    bool ok = false;
+    int cus = 0;
+    std::string arch;
+    void* ws = nullptr;  // library-owned workspace (zero outside calls)
+    size_t ws_bytes = 0;
+};
+
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+
+int probe_device(int dev)
+{
+    if (dev < 0 || dev >= kMaxDevices) return fail(BTL_ERR_DEVICE, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState& d = g_dev[dev];
+    if (!d.probed) {
+        d.probed = true;
+        hipDeviceProp_t prop;
+        hipError_t e = hipGetDeviceProperties(&prop, dev);
+        if (e != hipSuccess) {
+            d.ok = false;
+            return hip_fail(e, "hipGetDeviceProperties");
+        }
+        d.arch = prop.gcnArchName;
+        d.cus = prop.multiProcessorCount;
+        d.ok = d.arch.compare(0, 6, "gfx950") == 0;
+    }
+    if (!d.ok)
+        return fail(BTL_ERR_DEVICE, "device %d is '%s'; this library is built for gfx950 only", dev,
+                    d.arch.c_str());
+    return BTL_OK;
+}
+
+int current_device(int* dev)
+{
+    hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    return probe_device(*dev);
+}
+
+int env_int(const char* name, int dflt)
+{
+    const char* v = getenv(name);
+    if (!v || !*v) return dflt;
+    return atoi(v);
+}
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Workspace layout.  The split-K region (partials + counters) comes first and
+// is all-zero between calls (each call's last workgroup clears what it used);
+// the quantised-activation region after it is scratch.
+struct WsLayout {
+    size_t partial_off, counter_off, q_off, s_off, total;
+};
+
+WsLayout ws_layout(int64_t m, int64_t nsum, int64_t k, int64_t rb_total)
+{
+    WsLayout l;
+    const int64_t mtiles = ceil_div(m, btl::kGemvMaxM);
+    l.partial_off = 0;
+    l.counter_off = align_up((size_t)(4 * m * nsum), 256);
+    l.q_off = l.counter_off + align_up((size_t)(4 * mtiles * rb_total), 256);
+    l.s_off = l.q_off + align_up((size_t)(m * k), 256);
+    l.total = l.s_off + align_up((size_t)(4 * m), 256);
+    return l;
+}
+
+int64_t rb_bound(int64_t nsum) { return ceil_div(nsum, btl::kGemvRows) + btl::kMaxGroup; }
+
+// Library-owned per-device workspace, grown on demand.
+int library_ws(int dev, size_t need, void** out)
+{
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState& d = g_dev[dev];
+    if (d.ws_bytes < need) {
+        size_t bytes = align_up(need, (size_t)1 << 20);
+        hipError_t e;
+        if (d.ws) {
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize (workspace growth)");
+            (void)hipFree(d.ws);
+            d.ws = nullptr;
+            d.ws_bytes = 0;
+        }
+        void* p = nullptr;
+        e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc (workspace)");
+        e = hipMemset(p, 0, bytes);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return hip_fail(e, "hipMemset (workspace)");
+        }
+        d.ws = p;
+        d.ws_bytes = bytes;
+    }
+    *out = d.ws;
+    return BTL_OK;
+}
+
+int get_ws(int dev, void* ws, size_t ws_bytes, size_t need, void** out)
+{
+    if (!ws) return library_ws(dev, need, out);
+    if (ws_bytes < need)
+        return fail(BTL_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu needed", ws_bytes,
+                    need);
+    if (((uintptr_t)ws & 255u) != 0) return fail(BTL_ERR_LAYOUT, "workspace must be 256-byte aligned");
+    *out = ws;
+    return BTL_OK;
+}
+
+int check_dtype(int dt, const char* what)
+{
+    if (dt != BTL_F32 && dt != BTL_BF16) return fail(BTL_ERR_DTYPE, "%s dtype %d is not BTL_F32/BTL_BF16", what, dt);
+    return BTL_OK;
+}
+
+int check_packed(const btl_packed_t* w, int64_t m, int64_t k)
+{
+    if (!w) return fail(BTL_ERR_ARG, "null weights");
+    if (w->n < 0 || w->k < 0 || m < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    if (k != w->k)  // cpu.rs:22-30, cuda.rs:27-35
+        return fail(BTL_ERR_SHAPE, "Shape mismatch: Input [%lld, %lld] vs Weight [%lld, %lld]",
+                    (long long)m, (long long)k, (long long)w->n, (long long)w->k);
+    if (k % 4 != 0)
+        return fail(BTL_ERR_SHAPE,
+                    "in_features %lld is not a multiple of 4: the packed rows are not byte aligned",
+                    (long long)k);
+    if (w->n > INT32_MAX || k > INT32_MAX || m > INT32_MAX)
+        return fail(BTL_ERR_SHAPE, "dimension exceeds 2^31-1");
+    if (!w->data && w->n * k > 0) return fail(BTL_ERR_LAYOUT, "null weight data");
+    return BTL_OK;
+}
+
+struct Layer {
+    const btl_packed_t* w;
+    void* y;
+    int32_t* acc;
+};
+
+// W1.58-A8 contraction of `count` layers sharing one input.
+int run_i8(const Layer* layers, int count, const void* x, int xkind, const float* xs, int64_t m,
+           int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st)
+{
+    int dev;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    int64_t nsum = 0, rb_total = 0;
+    bool fast = k >= 64 && k % 64 == 0 && aligned16(x);
+    for (int i = 0; i < count; ++i) {
+        nsum += layers[i].w->n;
+        rb_total += ceil_div(layers[i].w->n, btl::kGemvRows);
+        fast = fast && aligned16(layers[i].w->data);
+    }
+    if (m == 0 || nsum == 0) return BTL_OK;
+    if (!x) return fail(BTL_ERR_LAYOUT, "null input");
+    const WsLayout L = ws_layout(m, nsum, k, rb_bound(nsum));
+    void* ws = nullptr;
+    rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws);
+    if (rc) return rc;
+    uint8_t* wsb = (uint8_t*)ws;
+    int8_t* wq = (int8_t*)(wsb + L.q_off);
+    float* wsc = (float*)(wsb + L.s_off);
+    hipError_t e;
+
+    if (!fast) {
+        const int8_t* q = (const int8_t*)x;
+        const float* s = xs;
+        if (xkind != btl::XK_I8) {
+            e = btl::launch_quant_act(x, xkind, m, k, wq, wsc, st);
+            if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
+            q = wq;
+            s = wsc;
+        }
+        for (int i = 0; i < count; ++i) {
+            if (layers[i].w->n == 0) continue;
+            e = btl::launch_generic_i8(q, s, m, k, layers[i].w->data, layers[i].w->n, layers[i].w->scale,
+                                       layers[i].y, ykind, layers[i].acc, st);
+            if (e != hipSuccess) return hip_fail(e, "generic int8 kernel launch");
+        }
+        return BTL_OK;
+    }
+
+    // More than one 16-token tile: quantise once into the workspace.
+    if (m > btl::kGemvMaxM && xkind != btl::XK_I8) {
+        e = btl::launch_quant_act(x, xkind, m, k, wq, wsc, st);
+        if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
+        x = wq;
+        xs = wsc;
+        xkind = btl::XK_I8;
+    }
+    if (xkind == btl::XK_I8 && !aligned16(x)) return fail(BTL_ERR_LAYOUT, "int8 input must be 16-byte aligned");
+
+    const int64_t mtiles = ceil_div(m, btl::kGemvMaxM);
+    const int64_t mt = m < btl::kGemvMaxM ? m : btl::kGemvMaxM;
+    int cus;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        cus = g_dev[dev].cus;
+    }
+    // K split: aim for `target` workgroups in flight, each slice >= 256 weights.
+    const int64_t target = env_int("BTL_GEMV_WG_TARGET", 2 * cus);
+    const int64_t wgs = rb_total * mtiles;
+    int64_t S = (target + wgs / 2) / wgs;
+    const int forced = env_int("BTL_GEMV_SPLITS", 0);
+    if (forced > 0) S = forced;
+    if (S < 1) S = 1;
+    if (S > k / btl::kStepWeights) S = k / btl::kStepWeights > 0 ? k / btl::kStepWeights : 1;
+    int64_t slice = ceil_div(ceil_div(k, S), btl::kStepWeights) * btl::kStepWeights;
+    while (mt * (slice + 16) > btl::kGemvLdsMax && slice > btl::kStepWeights) slice -= btl::kStepWeights;
+    S = ceil_div(k, slice);
+    if (rb_total * S > INT32_MAX / 2) return fail(BTL_ERR_SHAPE, "problem too large for the GEMV grid");
+
+    btl::GemvArgs a;
+    memset(&a, 0, sizeof(a));
+    int rb = 0;
+    int64_t poff = 0;
+    int np = 0;
+    for (int i = 0; i < count; ++i) {
+        const int64_t n = layers[i].w->n;
+        if (n == 0) continue;
+        btl::GemvProblem& p = a.p[np++];
+        p.w = layers[i].w->data;
+        p.y = layers[i].y;
+        p.acc_out = layers[i].acc;
+        p.partial = (int32_t*)(wsb + L.partial_off) + poff;
+        p.sw = layers[i].w->scale;
+        p.n = (int)n;
+        p.rb_begin = rb;
+        rb += (int)ceil_div(n, btl::kGemvRows);
+        poff += m * n;
+    }
+    a.nprob = np;
+    a.x = x;
+    a.xs = xs;
+    a.counter = (uint32_t*)(wsb + L.counter_off);
+    a.m = (int)m;
+    a.k = (int)k;
+    a.rb_total = rb;
+    a.splits = (int)S;
+    a.slice = (int)slice;
+    e = btl::launch_gemv(a, xkind, ykind, (int)mtiles, st);
+    if (e != hipSuccess) return hip_fail(e, "gemv kernel launch");
+    return BTL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int btl_version(void) { return BTL_VERSION; }
+
+const char* btl_last_error(void) { return g_err.c_str(); }
+
+const char* btl_status_string(int status)
+{
+    switch (status) {
+    case BTL_OK: return "BTL_OK";
+    case BTL_ERR_SHAPE: return "BTL_ERR_SHAPE";
+    case BTL_ERR_DTYPE: return "BTL_ERR_DTYPE";
+    case BTL_ERR_LAYOUT: return "BTL_ERR_LAYOUT";
+    case BTL_ERR_DEVICE: return "BTL_ERR_DEVICE";
+    case BTL_ERR_HIP: return "BTL_ERR_HIP";
+    case BTL_ERR_ARG: return "BTL_ERR_ARG";
+    case BTL_ERR_WORKSPACE: return "BTL_ERR_WORKSPACE";
+    default: return "BTL_ERR_UNKNOWN";
+    }
+}
+
+int btl_init(int device)
+{
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count) return fail(BTL_ERR_DEVICE, "device %d not present (%d devices)", device, count);
+    return probe_device(device);
+}
+
+int64_t btl_packed_bytes(int64_t n, int64_t k)
+{
+    if (n < 0 || k < 0) return -1;
+    return (n * k + 3) / 4;
+}
+
+// PackedTensor::pack (packing.rs:50-105).  The mean of |w| is accumulated in
+// double and rounded once; 1/scale is taken in double and rounded to f32, as
+// candle's `tensor / f64` multiplies by the reciprocal (packing.rs:61).
+int btl_pack_host(const float* w, int64_t n, int64_t k, uint8_t* out, float* scale)
+{
+    if (n < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    const int64_t numel = n * k;
+    if ((numel && (!w || !out)) || !scale) return fail(BTL_ERR_ARG, "null pointer");
+    double acc = 0.0;
+    for (int64_t i = 0; i < numel; ++i) acc += std::fabs((double)w[i]);
+    const float mean = numel ? (float)(acc / (double)numel) : 0.0f;
+    const float s = mean + 1e-6f;  // EPSILON, packing.rs:4
+    const float inv = (float)(1.0 / (double)s);
+    const int64_t nbytes = (numel + 3) / 4;
+    for (int64_t b = 0; b < nbytes; ++b) {
+        uint8_t byte = 0;
+        for (int i = 0; i < 4; ++i) {
+            const int64_t e = 4 * b + i;
+            if (e >= numel) break;
+            float v = std::round(w[e] * inv);  // f32::round: half away from zero
+            v = v > 1.0f ? 1.0f : (v < -1.0f ? -1.0f : v);
+            const uint8_t code = v > 0.5f ? 1 : (v < -0.5f ? 2 : 0);
+            byte |= (uint8_t)(code << (2 * i));
+        }
+        out[b] = byte;
+    }
+    *scale = s;
+    return BTL_OK;
+}
+
+int btl_unpack_host(const uint8_t* data, int64_t n, int64_t k, float scale, float* out)
+{
+    if (n < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    const int64_t numel = n * k;
+    if (numel && (!data || !out)) return fail(BTL_ERR_ARG, "null pointer");
+    for (int64_t e = 0; e < numel; ++e) {
+        const int code = (data[e >> 2] >> (2 * (e & 3))) & 3;
+        const float v = code == 1 ? 1.0f : (code == 2 ? -1.0f : 0.0f);
+        out[e] = v * scale;
+    }
+    return BTL_OK;
+}
+
+int btl_unpack_device(const btl_packed_t* w, float* out, void* stream)
+{
+    if (!w) return fail(BTL_ERR_ARG, "null weights");
+    if (w->n < 0 || w->k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    const int64_t numel = w->n * w->k;
+    if (numel == 0) return BTL_OK;
+    if (!w->data || !out) return fail(BTL_ERR_LAYOUT, "null pointer");
+    int dev;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_unpack(w->data, numel, w->scale, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "unpack kernel launch");
+    return BTL_OK;
+}
+
+int btl_quantize_act(const void* x, int xdtype, int64_t m, int64_t k, int8_t* xq, float* xscale,
+                     void* stream)
+{
+    int rc = check_dtype(xdtype, "input");
+    if (rc) return rc;
+    if (m < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    if (m == 0) return BTL_OK;
+    if (!xscale || (k > 0 && (!x || !xq))) return fail(BTL_ERR_LAYOUT, "null pointer");
+    int dev;
+    rc = current_device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_quant_act(x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, m, k, xq, xscale,
+                                         (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
+    return BTL_OK;
+}
+
+int btl_linear(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int64_t k, void* y,
+               int ydtype, int mode, int32_t* acc_out, void* ws, size_t ws_bytes, void* stream)
+{
+    int rc = check_packed(w, m, k);
+    if (rc) return rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_dtype(ydtype, "output"))) return rc;
+    if (mode != BTL_ACT_F32_REF && mode != BTL_ACT_I8) return fail(BTL_ERR_DTYPE, "unknown mode %d", mode);
+    if (mode == BTL_ACT_F32_REF && acc_out)
+        return fail(BTL_ERR_ARG, "acc_out is only defined for BTL_ACT_I8");
+    if (m == 0 || w->n == 0) return BTL_OK;
+    if (!y || (k > 0 && !x)) return fail(BTL_ERR_LAYOUT, "null input or output");
+    const hipStream_t st = (hipStream_t)stream;
+    const int xk = xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32;
+    const int yk = ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32;
+    if (mode == BTL_ACT_F32_REF) {
+        int dev;
+        rc = current_device(&dev);
+        if (rc) return rc;
+        hipError_t e = btl::launch_ref_f32(x, xk, m, k, w->data, w->n, w->scale, y, yk, st);
+        if (e != hipSuccess) return hip_fail(e, "reference-order kernel launch");
+        return BTL_OK;
+    }
+    Layer l = {w, y, acc_out};
+    return run_i8(&l, 1, x, xk, nullptr, m, k, yk, ws, ws_bytes, st);
+}
+
+int btl_linear_i8(const btl_packed_t* w, const int8_t* xq, const float* xscale, int64_t m, int64_t k,
+                  void* y, int ydtype, int32_t* acc_out, void* ws, size_t ws_bytes, void* stream)
+{
+    int rc = check_packed(w, m, k);
+    if (rc) return rc;
+    if ((rc = check_dtype(ydtype, "output"))) return rc;
+    if (m == 0 || w->n == 0) return BTL_OK;
+    if (!y || !xscale || (k > 0 && !xq)) return fail(BTL_ERR_LAYOUT, "null input or output");
+    Layer l = {w, y, acc_out};
+    return run_i8(&l, 1, xq, btl::XK_I8, xscale, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws,
+                  ws_bytes, (hipStream_t)stream);
+}
+
+int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* x,
+                     int xdtype, int64_t m, int64_t k, int ydtype, void* ws, size_t ws_bytes,
+                     void* stream)
+{
+    if (count < 1 || count > btl::kMaxGroup) return fail(BTL_ERR_ARG, "count %d not in 1..%d", count, btl::kMaxGroup);
+    if (!w || !y) return fail(BTL_ERR_ARG, "null layer array");
+    int rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_dtype(ydtype, "output"))) return rc;
+    Layer ls[btl::kMaxGroup];
+    for (int i = 0; i < count; ++i) {
+        if ((rc = check_packed(w[i], m, k))) return rc;
+        if (!y[i] && m > 0 && w[i]->n > 0) return fail(BTL_ERR_LAYOUT, "null output %d", i);
+        ls[i] = Layer{w[i], y[i], nullptr};
+    }
+    return run_i8(ls, count, x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k,
+                  ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream);
+}
+
+size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)
+{
+    if (m < 0 || n < 0 || k < 0) return 0;
+    if (mode == BTL_ACT_F32_REF) return 0;
+    return ws_layout(m, n, k, rb_bound(n)).total;
+}
+
+int btl_workspace_clear(void* ws, size_t ws_bytes, void* stream)
+{
+    if (!ws && ws_bytes) return fail(BTL_ERR_ARG, "null workspace");
+    if (((uintptr_t)ws & 255u) != 0) return fail(BTL_ERR_LAYOUT, "workspace must be 256-byte aligned");
+    int dev;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_fill_zero(ws, ws_bytes, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "fill kernel launch");
+    return BTL_OK;
+}
+
+}  // extern "C"

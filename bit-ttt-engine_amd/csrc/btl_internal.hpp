@@ -1,0 +1,60 @@
+// btl_internal.hpp -- shared declarations between the C-ABI layer (btl_api.cpp)
+// and the gfx950 kernels (btl_kernels.hip).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace btl {
+
+constexpr int kMaxGroup = 4;       // layers per grouped launch (q|k|v, w1|w3)
+constexpr int kGemvRows = 64;      // output rows per GEMV workgroup: 4 waves x 16
+constexpr int kStepWeights = 256;  // weights of one row consumed per wave-load (64 B)
+constexpr int kGemvMaxM = 16;      // token rows per GEMV tile (MFMA 16x16 B operand)
+constexpr int kGemvLdsMax = 61440; // bytes of LDS the activation tile may use
+
+enum XKind { XK_F32 = 0, XK_BF16 = 1, XK_I8 = 2 };
+enum YKind { YK_F32 = 0, YK_BF16 = 1 };
+
+// One layer of a (possibly grouped) GEMV launch.
+struct GemvProblem {
+    const uint8_t* w;  // packed rows, row stride k/4 bytes, 16-byte aligned base
+    void* y;           // [m, n] output
+    int32_t* acc_out;  // optional [m, n] int32 accumulators
+    int32_t* partial;  // split-K partial sums [m, n] (all zero on entry), or null
+    float sw;          // per-tensor weight scale
+    int n;             // output rows of this layer
+    int rb_begin;      // first global row-block (64 rows) of this layer
+};
+
+struct GemvArgs {
+    GemvProblem p[kMaxGroup];
+    int nprob;
+    const void* x;       // [m, k]: f32 / bf16 (fused quantisation) or int8 (XK_I8)
+    const float* xs;     // XK_I8 only: per-row activation scales [m]
+    uint32_t* counter;   // split-K arrival counters [mtiles * rb_total] (zero on entry)
+    int m, k;
+    int rb_total;        // row-blocks over all layers
+    int splits;          // K slices per row-block
+    int slice;           // weights per slice (multiple of 256)
+};
+
+hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipStream_t s);
+
+hipError_t launch_quant_act(const void* x, int xkind, int64_t m, int64_t k, int8_t* q,
+                            float* s, hipStream_t st);
+
+hipError_t launch_ref_f32(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* w,
+                          int64_t n, float scale, void* y, int ykind, hipStream_t st);
+
+hipError_t launch_generic_i8(const int8_t* q, const float* xs, int64_t m, int64_t k,
+                             const uint8_t* w, int64_t n, float sw, void* y, int ykind,
+                             int32_t* acc_out, hipStream_t st);
+
+hipError_t launch_unpack(const uint8_t* w, int64_t numel, float scale, float* out,
+                         hipStream_t st);
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t st);
+
+}  // namespace btl

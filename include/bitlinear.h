@@ -1,0 +1,175 @@
+/*
+ * bitlinear.h -- C ABI of the MI355X (gfx950) BitLinear engine.
+ *
+ * Drop-in boundary for the packed-ternary linear layer of
+ * imonoonoko/Bit-TTT-Engine (crate crates/rust_engine).  The reference's seam is
+ * Rust, not a C ABI:
+ *
+ *   BitLinear::forward(&self, x) -> Result<Tensor>        src/layers/bit_linear.rs:52-119
+ *     -> BitLinearCpu::forward(input, &PackedTensor)       src/kernels/cpu.rs:17-127
+ *     -> BitLinearCuda::forward(input, &PackedTensor)      src/kernels/cuda.rs:21-47
+ *     -> bail!("... Custom Kernel not implemented ...")    src/layers/bit_linear.rs:76-84
+ *
+ * A Rust FFI crate calls the functions below from a new `Device::Hip` arm of
+ * BitLinear::forward; rank flattening and reshaping stay in Rust
+ * (bit_linear.rs:54-62, 88-95).
+ *
+ * Conventions (all functions):
+ *  - Return 0 (BTL_OK) on success, a BTL_ERR_* code otherwise; the message of
+ *    the last failure on the calling thread is returned by btl_last_error().
+ *    This mirrors the reference's int-status C ABI precedent
+ *    (dist/binaries/README.md:49-58: nonzero return means error) and carries
+ *    the reference's error texts (e.g. cpu.rs:22-30 "Shape mismatch: ...").
+ *  - Tensors are dense and row-major.  "Device pointer" means memory on the
+ *    current HIP device (hipMalloc / torch.cuda); "host pointer" means CPU memory.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream); every
+ *    device function is asynchronous with respect to the host and stream ordered.
+ *  - Nothing here allocates or frees caller memory.  Functions that take a
+ *    workspace accept ws == NULL, in which case the library uses a per-device
+ *    workspace it owns (allocated and grown with hipMalloc, zeroed once;
+ *    calls that share it must be ordered on one stream).
+ *  - Functions are reentrant: no per-call global state besides that workspace
+ *    and the per-thread error message.
+ */
+#ifndef BITLINEAR_H
+#define BITLINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BTL_VERSION 1
+
+/* Status codes. */
+#define BTL_OK 0
+#define BTL_ERR_SHAPE 1     /* k != w.k ("Shape mismatch"), k % 4 != 0, negative sizes */
+#define BTL_ERR_DTYPE 2     /* unsupported dtype / mode enum */
+#define BTL_ERR_LAYOUT 3    /* null or misaligned pointer where one is required */
+#define BTL_ERR_DEVICE 4    /* no usable gfx950 device / pointer not on the device */
+#define BTL_ERR_HIP 5       /* a HIP runtime call failed */
+#define BTL_ERR_ARG 6       /* any other invalid argument */
+#define BTL_ERR_WORKSPACE 7 /* caller workspace smaller than btl_workspace_bytes() */
+
+/* Element types of activations and outputs. */
+#define BTL_F32 0
+#define BTL_BF16 1
+
+/* Arithmetic modes of btl_linear. */
+#define BTL_ACT_F32_REF 0 /* reference semantics: fp32 x, y = scale * sum_k x*t in
+                             the exact summation order of cpu.rs:86-123 */
+#define BTL_ACT_I8 1      /* W1.58-A8: per-token absmax int8 x, exact int32 sum,
+                             y = (float)acc * (s_x * s_w) */
+
+/*
+ * Packed ternary weights: the reference's PackedTensor (kernels/packing.rs:14-21).
+ * data: device pointer to ceil(n*k/4) bytes.  Element e = row*k + col of the
+ *       row-major [n, k] matrix sits in byte e/4 at bits 2*(e%4); codes
+ *       00 = 0, 01 = +1, 10 = -1, 11 = 0 (packing.rs:6-13, 74-92, cpu.rs:59).
+ * n, k: the reference's `shape` [out_dim, in_dim].
+ * scale: the per-tensor absmean scale mean|W| + 1e-6 (packing.rs:56-57).
+ */
+typedef struct btl_packed {
+    const uint8_t* data;
+    int64_t n;
+    int64_t k;
+    float scale;
+} btl_packed_t;
+
+/* Library version (BTL_VERSION). */
+int btl_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* btl_last_error(void);
+
+/* Short name of a status code. */
+const char* btl_status_string(int status);
+
+/*
+ * Check that `device` is a usable gfx950 GPU and cache its properties.
+ * Idempotent and thread-safe; every device function also initialises lazily.
+ */
+int btl_init(int device);
+
+/* Number of packed bytes for an [n, k] weight: ceil(n*k/4) (packing.rs:36,71). */
+int64_t btl_packed_bytes(int64_t n, int64_t k);
+
+/*
+ * Host-side packing, PackedTensor::pack (packing.rs:50-105): host pointers.
+ * w: [n, k] f32; out: btl_packed_bytes(n, k) bytes; *scale = mean|w| + 1e-6.
+ * t = clamp(round(w * (1/scale)), -1, 1), round half away from zero.
+ */
+int btl_pack_host(const float* w, int64_t n, int64_t k, uint8_t* out, float* scale);
+
+/* Host-side PackedTensor::unpack (packing.rs:108-133): out[n*k] = t * scale. */
+int btl_unpack_host(const uint8_t* data, int64_t n, int64_t k, float scale, float* out);
+
+/*
+ * Device-side unpack to dense f32 [n, k] (what BitLinearCuda::forward builds
+ * on the host on every call, cuda.rs:40 -> packing.rs:108-133).
+ */
+int btl_unpack_device(const btl_packed_t* w, float* out, void* stream);
+
+/*
+ * Per-token absmax int8 quantisation (no reference counterpart on the BitLinear
+ * path; convention of kv_cache.rs:95-119 / BitNet b1.58).  Device pointers.
+ * x: [m, k] of xdtype; xq: [m, k] int8; xscale: [m] f32.
+ *   a = max|x[row]|;  a non-finite -> s = NaN, q = 0;  a < 2^-100 -> s = 0, q = 0;
+ *   else q = clamp(round_half_away(x * (127/a)), -127, 127), s = a / 127.
+ */
+int btl_quantize_act(const void* x, int xdtype, int64_t m, int64_t k, int8_t* xq, float* xscale,
+                     void* stream);
+
+/*
+ * BitLinear forward, y = x @ W^T: the replacement of BitLinearCpu::forward /
+ * BitLinearCuda::forward (cpu.rs:17, cuda.rs:21).  Device pointers.
+ * w:   packed weights; w->k must equal k (else BTL_ERR_SHAPE with the
+ *      reference's "Shape mismatch: Input [m, k] vs Weight [n, k_w]").
+ * x:   [m, k] of xdtype;  y: [m, w->n] of ydtype.
+ * mode BTL_ACT_F32_REF: reference semantics (bf16 x is widened exactly first).
+ * mode BTL_ACT_I8:      W1.58-A8 (quantisation as btl_quantize_act).
+ * acc_out: optional [m, n] int32 accumulators (BTL_ACT_I8 only; else NULL).
+ * ws / ws_bytes: optional workspace, see btl_workspace_bytes.
+ * k must be a multiple of 4 (the reference's CPU row stride ceil(k/4), cpu.rs:81,
+ * only agrees with its flat packing, packing.rs:74, when k % 4 == 0).
+ */
+int btl_linear(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int64_t k, void* y,
+               int ydtype, int mode, int32_t* acc_out, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Same contraction for pre-quantised activations (as produced by
+ * btl_quantize_act, or fused into a producer kernel): xq [m, k] int8,
+ * xscale [m] f32.  y = (float)acc * (xscale[row] * w->scale).
+ */
+int btl_linear_i8(const btl_packed_t* w, const int8_t* xq, const float* xscale, int64_t m,
+                  int64_t k, void* y, int ydtype, int32_t* acc_out, void* ws, size_t ws_bytes,
+                  void* stream);
+
+/*
+ * Several BitLinear layers that read the same input in one launch (the q/k/v
+ * projections of BitAttention, attention.rs:159-162; the w1/w3 projections of
+ * SwiGLU, swiglu.rs:29-35).  BTL_ACT_I8 semantics; each layer keeps its own
+ * scale.  y[i] is a [m, w[i]->n] output of ydtype.  count in 1..4.
+ */
+int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* x,
+                     int xdtype, int64_t m, int64_t k, int ydtype, void* ws, size_t ws_bytes,
+                     void* stream);
+
+/*
+ * Workspace bytes needed by btl_linear / btl_linear_i8 for this shape and mode
+ * (for btl_linear_group pass n = sum of the layers' n).  A caller-provided
+ * workspace must be cleared once with btl_workspace_clear before its first use;
+ * every successful call leaves it cleared again.
+ */
+size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode);
+
+/* Zero a caller-provided workspace (a fill kernel on `stream`). */
+int btl_workspace_clear(void* ws, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BITLINEAR_H */

@@ -1,0 +1,153 @@
+"""ctypes binding of oracle/libbitlinear_oracle.so (see bitlinear_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py.  The product package never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbitlinear_oracle.so")
+
+
+def build():
+    """Compile the oracle with its Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", HERE, "-B"], check=True)
+    return LIB_PATH
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, i64, f32, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
+    sigs = {
+        "orc_pack": (i32, [vp, i64, vp, ctypes.POINTER(f32)]),
+        "orc_unpack": (None, [vp, i64, f32, vp]),
+        "orc_forward_f32": (i32, [vp, i64, i64, vp, i64, i64, f32, vp, i32]),
+        "orc_forward_f32_avx2": (i32, [vp, i64, i64, vp, i64, i64, f32, vp, i32]),
+        "orc_has_avx2": (i32, []),
+        "orc_quantize_act": (None, [vp, i64, i64, vp, vp]),
+        "orc_contract_i8": (None, [vp, i64, i64, vp, i64, vp]),
+        "orc_epilogue": (None, [vp, vp, f32, i64, i64, vp]),
+        "orc_forward_i8": (i32, [vp, i64, i64, vp, i64, f32, vp, vp, vp, vp]),
+        "orc_bf16_to_f32_array": (None, [vp, i64, vp]),
+        "orc_f32_to_bf16_array": (None, [vp, i64, vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a.size else None
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def pack(w):
+    """PackedTensor::pack -> (uint8 bytes, scale)."""
+    w = _f32(w).reshape(-1)
+    out = np.zeros(((w.size + 3) // 4,), dtype=np.uint8)
+    s = ctypes.c_float(0)
+    rc = lib.orc_pack(_p(w), w.size, _p(out), ctypes.byref(s))
+    assert rc == 0
+    return out, s.value
+
+
+def unpack(data, numel, scale):
+    out = np.zeros((numel,), dtype=np.float32)
+    lib.orc_unpack(_p(np.ascontiguousarray(data, np.uint8)), numel, scale, _p(out))
+    return out
+
+
+def forward_f32(x, w, n, scale, avx2_order=True, wbytes=None):
+    """BitLinearCpu::forward in the exact fp32 order; x [m,k] f32, w packed bytes."""
+    x = _f32(x)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, np.uint8)
+    y = np.zeros((m, n), dtype=np.float32)
+    rc = lib.orc_forward_f32(_p(x), m, k, _p(w), n, w.size if wbytes is None else wbytes, scale, _p(y),
+                             1 if avx2_order else 0)
+    if rc != 0:
+        raise ValueError("orc_forward_f32 status %d" % rc)
+    return y
+
+
+def forward_f32_avx2(x, w, n, scale, threads=1):
+    """Intrinsics + threads restatement (the timed baseline)."""
+    x = _f32(x)
+    m, k = x.shape
+    w = np.ascontiguousarray(w, np.uint8)
+    y = np.zeros((m, n), dtype=np.float32)
+    rc = lib.orc_forward_f32_avx2(_p(x), m, k, _p(w), n, w.size, scale, _p(y), threads)
+    if rc != 0:
+        raise ValueError("orc_forward_f32_avx2 status %d" % rc)
+    return y
+
+
+def has_avx2():
+    return bool(lib.orc_has_avx2())
+
+
+def quantize_act(x):
+    x = _f32(x)
+    m, k = x.shape
+    q = np.zeros((m, k), dtype=np.int8)
+    s = np.zeros((m,), dtype=np.float32)
+    lib.orc_quantize_act(_p(x), m, k, _p(q), _p(s))
+    return q, s
+
+
+def contract_i8(q, w, n):
+    q = np.ascontiguousarray(q, np.int8)
+    m, k = q.shape
+    acc = np.zeros((m, n), dtype=np.int32)
+    lib.orc_contract_i8(_p(q), m, k, _p(np.ascontiguousarray(w, np.uint8)), n, _p(acc))
+    return acc
+
+
+def epilogue(acc, sx, sw):
+    acc = np.ascontiguousarray(acc, np.int32)
+    m, n = acc.shape
+    y = np.zeros((m, n), dtype=np.float32)
+    lib.orc_epilogue(_p(acc), _p(_f32(sx)), sw, m, n, _p(y))
+    return y
+
+
+def forward_i8(x, w, n, sw):
+    """W1.58-A8 forward -> (y f32, q int8, s_x f32, acc int32)."""
+    x = _f32(x)
+    m, k = x.shape
+    y = np.zeros((m, n), dtype=np.float32)
+    q = np.zeros((m, k), dtype=np.int8)
+    s = np.zeros((m,), dtype=np.float32)
+    acc = np.zeros((m, n), dtype=np.int32)
+    rc = lib.orc_forward_i8(_p(x), m, k, _p(np.ascontiguousarray(w, np.uint8)), n, sw, _p(y), _p(q), _p(s),
+                            _p(acc))
+    assert rc == 0
+    return y, q, s, acc
+
+
+def bf16_to_f32(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    out = np.zeros(h.shape, dtype=np.float32)
+    lib.orc_bf16_to_f32_array(_p(h), h.size, _p(out))
+    return out
+
+
+def f32_to_bf16(f):
+    f = _f32(f)
+    out = np.zeros(f.shape, dtype=np.uint16)
+    lib.orc_f32_to_bf16_array(_p(f), f.size, _p(out))
+    return out

@@ -1,0 +1,118 @@
+"""CPU tests of the C ABI: the library loads, exports what include/bitlinear.h declares,
+its host-side packing matches the oracle, and argument validation fails before any
+device work with the reference's error texts."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+import bitlinear as bl
+from datagen import weights
+from oracle import oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "bitlinear.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(btl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_python_exports():
+    assert header_functions() == sorted(bl.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", bl.LIB_PATH], stdout=subprocess.PIPE, text=True,
+                         check=True).stdout
+    syms = set(l.split()[-1] for l in out.splitlines() if l.strip())
+    missing = [f for f in header_functions() if f not in syms]
+    assert not missing, missing
+    for f in header_functions():
+        assert hasattr(bl.lib, f)
+
+
+def test_version_and_status_strings():
+    assert bl.lib.btl_version() == 1
+    assert bl.lib.btl_status_string(bl.BTL_ERR_SHAPE) == b"BTL_ERR_SHAPE"
+    assert bl.lib.btl_status_string(99) == b"BTL_ERR_UNKNOWN"
+
+
+def test_packed_bytes():
+    assert bl.lib.btl_packed_bytes(5632, 2048) == 5632 * 2048 // 4
+    assert bl.lib.btl_packed_bytes(1, 5) == 2
+    assert bl.lib.btl_packed_bytes(-1, 5) == -1
+
+
+@pytest.mark.parametrize("shape", [(40, 64), (7, 33), (1, 5), (256, 2048)])
+def test_pack_host_matches_oracle(shape):
+    w = weights(*shape, seed=21)
+    out = np.zeros((w.size + 3) // 4, np.uint8)
+    s = ctypes.c_float()
+    bl.check(bl.lib.btl_pack_host(w.ctypes.data, shape[0], shape[1], out.ctypes.data, ctypes.byref(s)))
+    ob, osc = orc.pack(w)
+    assert np.array_equal(out, ob)
+    assert s.value == osc
+
+
+def test_unpack_host_matches_oracle():
+    data = np.arange(256, dtype=np.uint8)
+    out = np.zeros(1023, np.float32)
+    bl.check(bl.lib.btl_unpack_host(data.ctypes.data, 3, 341, ctypes.c_float(0.37), out.ctypes.data))
+    assert np.array_equal(out, orc.unpack(data, 1023, np.float32(0.37)))
+
+
+def test_workspace_bytes():
+    assert bl.lib.btl_workspace_bytes(1, 4096, 4096, bl.BTL_ACT_F32_REF) == 0
+    a = bl.lib.btl_workspace_bytes(1, 4096, 4096, bl.BTL_ACT_I8)
+    b = bl.lib.btl_workspace_bytes(2048, 4096, 4096, bl.BTL_ACT_I8)
+    assert 0 < a < b
+    assert b >= 2048 * 4096 + 4 * 2048 * 4096
+    assert bl.lib.btl_workspace_bytes(-1, 1, 1, bl.BTL_ACT_I8) == 0
+
+
+def _packed(n, k, data=1):
+    return bl.BtlPacked(data, n, k, 1.0)
+
+
+def _linear(w, m, k, xdt=bl.BTL_F32, ydt=bl.BTL_F32, mode=bl.BTL_ACT_I8, acc=None):
+    return bl.lib.btl_linear(ctypes.byref(w), 16, xdt, m, k, 16, ydt, mode, acc, None, 0, None)
+
+
+def test_shape_mismatch_message():
+    # cpu.rs:22-30: "Shape mismatch: Input [m, k] vs Weight [n, k_w]"
+    w = _packed(5632, 2048)
+    rc = _linear(w, 1, 2044)
+    assert rc == bl.BTL_ERR_SHAPE
+    assert bl.lib.btl_last_error() == b"Shape mismatch: Input [1, 2044] vs Weight [5632, 2048]"
+    with pytest.raises(bl.BitLinearError, match="Shape mismatch"):
+        bl.check(rc)
+
+
+def test_validation_errors_before_device_work():
+    assert _linear(_packed(8, 6), 1, 6) == bl.BTL_ERR_SHAPE  # k % 4
+    assert _linear(_packed(8, 8), -1, 8) == bl.BTL_ERR_SHAPE
+    assert _linear(_packed(8, 8), 1, 8, xdt=7) == bl.BTL_ERR_DTYPE
+    assert _linear(_packed(8, 8), 1, 8, ydt=3) == bl.BTL_ERR_DTYPE
+    assert _linear(_packed(8, 8), 1, 8, mode=5) == bl.BTL_ERR_DTYPE
+    assert _linear(_packed(8, 8), 1, 8, mode=bl.BTL_ACT_F32_REF, acc=16) == bl.BTL_ERR_ARG
+    assert _linear(_packed(8, 8, data=None), 1, 8) == bl.BTL_ERR_LAYOUT
+    assert bl.lib.btl_linear(None, 16, 0, 1, 8, 16, 0, 1, None, None, 0, None) == bl.BTL_ERR_ARG
+    # empty problems are successful no-ops (nothing to launch)
+    assert _linear(_packed(8, 8), 0, 8) == bl.BTL_OK
+    assert _linear(_packed(0, 8), 3, 8) == bl.BTL_OK
+    assert bl.lib.btl_linear_group(None, None, 0, 16, 0, 1, 8, 0, None, 0, None) == bl.BTL_ERR_ARG
+    assert bl.lib.btl_linear_group(None, None, 5, 16, 0, 1, 8, 0, None, 0, None) == bl.BTL_ERR_ARG
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
+def test_no_device_is_an_error():
+    rc = bl.lib.btl_init(0)
+    assert rc in (bl.BTL_ERR_HIP, bl.BTL_ERR_DEVICE)
+    assert bl.lib.btl_last_error() != b""

@@ -1,0 +1,269 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on the same
+seeded inputs.  Bar: int8 activations, int32 accumulators and the int-path fp32
+outputs bit-exact; reference-mode fp32 outputs bit-exact (the kernel reproduces the
+8-lane order of cpu.rs); bf16 outputs equal to the oracle's f32 rounded to nearest even
+(tolerance 0, tighter than the 1e-2 the task allows)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import bitlinear as bl
+from datagen import activations, random_codes, ternary, weights
+from oracle import oracle as orc
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")]
+
+DEV = "cuda"
+
+
+def _bits(a):
+    a = np.ascontiguousarray(a, np.float32).copy()
+    a[np.isnan(a)] = np.float32("nan")  # canonical NaN
+    return a.view(np.uint32)
+
+
+def assert_f32_identical(got, ref):
+    got = got.detach().cpu().numpy() if torch.is_tensor(got) else got
+    g, r = _bits(got), _bits(ref)
+    bad = np.flatnonzero(g != r)
+    assert bad.size == 0, "%d mismatches, first at %d: %r vs %r" % (
+        bad.size, bad[0], got.reshape(-1)[bad[0]], ref.reshape(-1)[bad[0]])
+
+
+def assert_bf16_matches(got, ref_f32):
+    g = got.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+    r = orc.f32_to_bf16(ref_f32)
+    bad = np.flatnonzero(g.reshape(-1) != r.reshape(-1))
+    assert bad.size == 0, "%d bf16 mismatches" % bad.size
+
+
+def make_layer(n, k, seed, dev=DEV):
+    wb, sw = orc.pack(weights(n, k, seed))
+    return bl.PackedTensor(torch.from_numpy(wb).to(dev), sw, (n, k), dev), wb, sw
+
+
+def to_dev(x, dtype):
+    t = torch.from_numpy(x).to(DEV)
+    return t.to(dtype)
+
+
+def host_x(xt):
+    return xt.float().cpu().numpy()
+
+
+# --- activation quantisation ----------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,k", [(1, 4096), (3, 1000), (16, 14336), (5, 4)])
+def test_quantize_act_bitexact(dtype, m, k):
+    print("quantize", dtype, m, k, flush=True)
+    x = activations(m, k, seed=m * 7 + k)
+    if m >= 3:
+        x[1] = 0.0
+        x[2, 0] = np.nan
+    xt = to_dev(x, dtype)
+    q, s = bl.quantize_act(xt)
+    qr, sr = orc.quantize_act(host_x(xt))
+    assert np.array_equal(q.cpu().numpy(), qr)
+    assert_f32_identical(s, sr)
+
+
+# --- W1.58-A8 linear -------------------------------------------------------------
+
+I8_SHAPES = [
+    (1, 2048, 5632),   # config 1 (TinyLlama gate/up shape)
+    (1, 4096, 1024),   # Llama-3-8B k/v
+    (1, 14336, 4096),  # Llama-3-8B down
+    (1, 100, 37),      # k % 64 != 0: generic path
+    (3, 36, 5),
+    (2, 68, 130),
+    (5, 320, 70),      # k % 256 != 0: partial last wave-load
+    (16, 512, 200),
+    (17, 256, 64),     # two 16-token tiles
+    (33, 1024, 300),
+]
+
+
+@pytest.mark.parametrize("m,k,n", I8_SHAPES)
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                     (torch.bfloat16, torch.float32)])
+def test_linear_i8_matches_oracle(m, k, n, xdt, ydt):
+    print("linear_i8", m, k, n, xdt, ydt, flush=True)
+    x = activations(m, k, seed=m + k + n)
+    pt, wb, sw = make_layer(n, k, seed=k * 3 + n)
+    xt = to_dev(x, xdt)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, mode="i8", out_dtype=ydt, acc_out=acc)
+    yr, qr, sr, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    if ydt == torch.float32:
+        assert_f32_identical(y, yr)
+    else:
+        assert_bf16_matches(y, yr)
+
+
+def test_linear_i8_special_rows():
+    m, k, n = 4, 4096, 256
+    x = activations(m, k, seed=3)
+    x[1] = 0.0
+    x[2, 5] = np.inf
+    x[3] *= np.float32(1e-35)
+    pt, wb, sw = make_layer(n, k, seed=4)
+    y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, mode="i8")
+    yr, _, _, _ = orc.forward_i8(x, wb, n, sw)
+    assert_f32_identical(y, yr)
+    assert np.all(np.isnan(y[2].cpu().numpy()))
+    assert np.all(y[1].cpu().numpy() == 0)
+
+
+@pytest.mark.parametrize("splits", ["1", "2", "3", "7", "16"])
+def test_split_k_is_exact(splits, monkeypatch):
+    m, k, n = 2, 4096, 320
+    x = activations(m, k, seed=11)
+    pt, wb, sw = make_layer(n, k, seed=12)
+    monkeypatch.setenv("BTL_GEMV_SPLITS", splits)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert_f32_identical(y, yr)
+
+
+def test_caller_workspace_left_clear():
+    m, k, n = 3, 4096, 1000
+    x = to_dev(activations(m, k, seed=1), torch.bfloat16)
+    pt, wb, sw = make_layer(n, k, seed=2)
+    ws = bl.Workspace(m, n, k, device=DEV)
+    os.environ["BTL_GEMV_SPLITS"] = "4"
+    try:
+        y1 = bl.BitLinearHip.forward(x, pt, workspace=ws)
+        y2 = bl.BitLinearHip.forward(x, pt, workspace=ws)
+    finally:
+        del os.environ["BTL_GEMV_SPLITS"]
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    # the split-K region (partial sums, then arrival counters) is zero again
+    zero_region = -(-4 * m * n // 256) * 256 + 256
+    assert int(ws.buf[:zero_region].count_nonzero()) == 0
+    yr, _, _, _ = orc.forward_i8(host_x(x), wb, n, sw)
+    assert_bf16_matches(y1, yr)
+
+
+def test_linear_i8_prequantized_equals_fused():
+    m, k, n = 2, 2048, 5632
+    x = to_dev(activations(m, k, seed=5), torch.bfloat16)
+    pt, wb, sw = make_layer(n, k, seed=6)
+    q, s = bl.quantize_act(x)
+    acc1 = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    acc2 = torch.empty_like(acc1)
+    y1 = bl.linear_i8(q, s, pt, acc_out=acc1)
+    y2 = bl.BitLinearHip.forward(x, pt, out_dtype=torch.float32, acc_out=acc2)
+    assert torch.equal(acc1, acc2)
+    assert torch.equal(y1, y2)
+
+
+def test_group_matches_single_layers():
+    m, k = 1, 4096
+    x = to_dev(activations(m, k, seed=7), torch.bfloat16)
+    layers = [make_layer(n, k, seed=20 + i) for i, n in enumerate((512, 128, 192))]
+    outs = bl.linear_group([l[0] for l in layers], x)
+    for (pt, wb, sw), y in zip(layers, outs):
+        ys = bl.BitLinearHip.forward(x, pt)
+        assert torch.equal(y, ys)
+        yr, _, _, _ = orc.forward_i8(host_x(x), wb, pt.shape[0], sw)
+        assert_bf16_matches(y, yr)
+
+
+def test_codes_3_and_extremes():
+    # code 3 decodes to 0; |acc| reaches 127*K without overflow
+    m, k, n = 1, 14336, 64
+    wb = random_codes(n, k, seed=1, p_zero=0.2, p3=0.3)
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), 0.02, (n, k), DEV)
+    x = np.full((m, k), -3.0, np.float32)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
+    t = ternary(wb, n * k).reshape(n, k).astype(np.int64)
+    assert np.array_equal(acc.cpu().numpy()[0], (-127 * t.sum(axis=1)).astype(np.int32))
+
+
+def test_large_m_sampled_rows():
+    m, k, n = 256, 4096, 1024
+    x = to_dev(activations(m, k, seed=9), torch.bfloat16)
+    pt, wb, sw = make_layer(n, k, seed=10)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    bl.BitLinearHip.forward(x, pt, acc_out=acc)
+    rows = np.random.default_rng(0).choice(m, 12, replace=False)
+    xs = host_x(x)[rows]
+    _, _, _, accr = orc.forward_i8(xs, wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy()[rows], accr)
+
+
+# --- reference fp32 semantics ---------------------------------------------------------
+
+F32_SHAPES = [(1, 2048, 5632), (3, 100, 17), (2, 36, 9), (4, 4096, 64), (1, 4, 3), (2, 8192, 8)]
+
+
+@pytest.mark.parametrize("m,k,n", F32_SHAPES)
+def test_linear_f32_ref_bitexact(m, k, n):
+    print("f32_ref", m, k, n, flush=True)
+    x = activations(m, k, seed=k + n)
+    pt, wb, sw = make_layer(n, k, seed=n + 1)
+    y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, mode="f32_ref")
+    assert_f32_identical(y, orc.forward_f32(x, wb, n, sw))
+
+
+def test_linear_f32_ref_order_cases():
+    # the lane-order / lane-sum / tail known answers of the oracle tests
+    k = 36
+    x = np.zeros((2, k), np.float32)
+    x[0, 0], x[0, 1], x[0, 2], x[0, 8] = 2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)
+    x[1, 0], x[1, 1], x[1, 2], x[1, 32] = 2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)
+    codes = np.zeros(2 * k, np.uint8)
+    codes[[0, 1, 2, 8, 32]] = 1
+    codes[k + np.array([0, 1, 2, 8, 32])] = 1
+    from datagen import pack_codes
+    wb = pack_codes(codes)
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), 1.0, (2, k), DEV)
+    y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, mode="f32_ref").cpu().numpy()
+    assert_f32_identical(y, orc.forward_f32(x, wb, 2, 1.0))
+
+
+def test_linear_f32_ref_reference_bench_input():
+    # bench_cpu_kernel.rs:33,47,50 at a reduced N: y[n] = 0.5 * sum_k t[n,k]
+    k, n = 8192, 512
+    wb = (np.arange(n * k // 4) % 255).astype(np.uint8)
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), 1.0, (n, k), DEV)
+    y = bl.BitLinearHip.forward(torch.full((1, k), 0.5, device=DEV), pt, mode="f32_ref")
+    t = ternary(wb, n * k).reshape(n, k).astype(np.int64)
+    assert np.array_equal(y.cpu().numpy()[0].astype(np.float64), 0.5 * t.sum(axis=1))
+
+
+# --- PackedTensor / BitLinear host mirror on the GPU ------------------------------------
+
+def test_unpack_device_matches_host():
+    pt, wb, sw = make_layer(37, 100, seed=3)
+    dense = pt.unpack("cpu").numpy().reshape(-1)
+    assert_f32_identical(dense, orc.unpack(wb, 3700, sw))
+
+
+def test_bitlinear_layer_forward():
+    w = torch.from_numpy(weights(96, 256, seed=4))
+    layer = bl.BitLinear.load(256, 96, w, device=DEV)
+    layer.precompute_packed()
+    x = to_dev(activations(6, 256, seed=5), torch.float32).reshape(2, 3, 256)
+    y = layer.forward(x)
+    assert tuple(y.shape) == (2, 3, 96)
+    wb, sw = orc.pack(w.numpy())
+    yr, _, _, _ = orc.forward_i8(x.reshape(6, 256).cpu().numpy(), wb, 96, sw)
+    assert_f32_identical(y.reshape(6, 96), yr)
+    y_ref = layer.forward(x, mode="f32_ref")
+    assert_f32_identical(y_ref.reshape(6, 96), orc.forward_f32(x.reshape(6, 256).cpu().numpy(), wb, 96, sw))
+
+
+def test_shape_mismatch_raises_on_gpu():
+    pt, _, _ = make_layer(8, 64, seed=1)
+    with pytest.raises(bl.BitLinearError, match=r"Shape mismatch: Input \[1, 60\] vs Weight \[8, 64\]"):
+        bl.BitLinearHip.forward(torch.zeros((1, 60), device=DEV), pt)
