@@ -141,6 +141,7 @@ def run_decode(args):
         calls["gate_up"].append(Call([L["gate"], L["up"]], xg,
                                      [torch.empty((1, INTER), **bf), torch.empty((1, INTER), **bf)]))
         calls["down"].append(Call([L["down"]], xd, [torch.empty((1, HIDDEN), **bf)]))
+    print("bench: %d layers of weights and inputs ready" % LAYERS, file=sys.stderr, flush=True)
     order = [calls[c][l] for l in range(LAYERS) for c in ("qkv", "o", "gate_up", "down")]
     step_bytes = sum(c.bytes for c in order)
     torch.cuda.synchronize()
@@ -169,6 +170,7 @@ def run_decode(args):
     t1.record()
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1) / args.steps
+    print("bench: %d graph replays, %.4f ms/step" % (args.steps, ms), file=sys.stderr, flush=True)
 
     # per-kernel durations (HIP events on the launch stream), one launch per layer
     kern = {}
@@ -201,6 +203,7 @@ def run_decode(args):
         "kernels": kern,
     }
     if args.cpu_baseline:
+        print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         host = []
         for L in layers[:4]:
             host.append([(L[nm].data.cpu().numpy(), shapes[nm][0], shapes[nm][1], L[nm].scale)

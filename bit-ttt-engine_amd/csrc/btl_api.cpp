@@ -93,26 +93,22 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Workspace layout.  The split-K region (partials + counters) comes first and
-// is all-zero between calls (each call's last workgroup clears what it used);
-// the quantised-activation region after it is scratch.
+// Workspace contract: every byte is zero between calls.  A call that needs
+// scratch (the int8 activations + scales, when it quantises once for several
+// token tiles or for the generic path) zeroes it with a fill kernel queued
+// after the kernels that read it, so one workspace serves calls of any shapes.
 struct WsLayout {
-    size_t partial_off, counter_off, q_off, s_off, total;
+    size_t q_off, s_off, total;
 };
 
-WsLayout ws_layout(int64_t m, int64_t nsum, int64_t k, int64_t rb_total)
+WsLayout ws_layout(int64_t m, int64_t k)
 {
     WsLayout l;
-    const int64_t mtiles = ceil_div(m, btl::kGemvMaxM);
-    l.partial_off = 0;
-    l.counter_off = align_up((size_t)(4 * m * nsum), 256);
-    l.q_off = l.counter_off + align_up((size_t)(4 * mtiles * rb_total), 256);
-    l.s_off = l.q_off + align_up((size_t)(m * k), 256);
+    l.q_off = 0;
+    l.s_off = align_up((size_t)(m * k), 256);
     l.total = l.s_off + align_up((size_t)(4 * m), 256);
     return l;
 }
-
-int64_t rb_bound(int64_t nsum) { return ceil_div(nsum, btl::kGemvRows) + btl::kMaxGroup; }
 
 // Library-owned per-device workspace, grown on demand.
 int library_ws(int dev, size_t need, void** out)
@@ -185,6 +181,14 @@ struct Layer {
     int32_t* acc;
 };
 
+// Token rows per GEMV tile: the [rows, k] activation tile must fit in LDS.
+int64_t gemv_mrows(int64_t m, int64_t k)
+{
+    int64_t r = m < btl::kGemvMaxM ? m : btl::kGemvMaxM;
+    while (r > 1 && r * (k + 16) > btl::kGemvLdsMax) r = (r + 1) / 2;
+    return r * (k + 16) <= btl::kGemvLdsMax ? r : 0;
+}
+
 // W1.58-A8 contraction of `count` layers sharing one input.
 int run_i8(const Layer* layers, int count, const void* x, int xkind, const float* xs, int64_t m,
            int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st)
@@ -192,32 +196,30 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     int dev;
     int rc = current_device(&dev);
     if (rc) return rc;
-    int64_t nsum = 0, rb_total = 0;
-    bool fast = k >= 64 && k % 64 == 0 && aligned16(x);
+    int64_t nsum = 0;
+    const int64_t mrows = gemv_mrows(m, k);
+    bool fast = k >= 64 && k % 64 == 0 && aligned16(x) && mrows > 0;
     for (int i = 0; i < count; ++i) {
         nsum += layers[i].w->n;
-        rb_total += ceil_div(layers[i].w->n, btl::kGemvRows);
         fast = fast && aligned16(layers[i].w->data);
     }
     if (m == 0 || nsum == 0) return BTL_OK;
     if (!x) return fail(BTL_ERR_LAYOUT, "null input");
-    const WsLayout L = ws_layout(m, nsum, k, rb_bound(nsum));
-    void* ws = nullptr;
-    rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws);
-    if (rc) return rc;
-    uint8_t* wsb = (uint8_t*)ws;
-    int8_t* wq = (int8_t*)(wsb + L.q_off);
-    float* wsc = (float*)(wsb + L.s_off);
     hipError_t e;
 
     if (!fast) {
+        // any k % 4 == 0 / any alignment: quantise once into scratch, one wave per output
+        const bool scratch = xkind != btl::XK_I8;
+        const WsLayout L = ws_layout(m, k);
+        void* ws = nullptr;
+        if (scratch && (rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
         const int8_t* q = (const int8_t*)x;
         const float* s = xs;
-        if (xkind != btl::XK_I8) {
-            e = btl::launch_quant_act(x, xkind, m, k, wq, wsc, st);
+        if (scratch) {
+            q = (const int8_t*)ws + L.q_off;
+            s = (const float*)((uint8_t*)ws + L.s_off);
+            e = btl::launch_quant_act(x, xkind, m, k, (int8_t*)q, (float*)s, st);
             if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
-            q = wq;
-            s = wsc;
         }
         for (int i = 0; i < count; ++i) {
             if (layers[i].w->n == 0) continue;
@@ -225,43 +227,118 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
                                        layers[i].y, ykind, layers[i].acc, st);
             if (e != hipSuccess) return hip_fail(e, "generic int8 kernel launch");
         }
+        if (scratch && (e = btl::launch_fill_zero(ws, L.total, st)) != hipSuccess)
+            return hip_fail(e, "workspace clear");
         return BTL_OK;
     }
 
-    // More than one 16-token tile: quantise once into the workspace.
-    if (m > btl::kGemvMaxM && xkind != btl::XK_I8) {
+    int cus;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        cus = g_dev[dev].cus;
+    }
+
+    // Decode (1..4 token rows): 16*tiles rows per workgroup, its waves split K.
+    if (m <= 4 && env_int("BTL_GEMV_DEC", 1) != 0) {
+        int wv = 0;
+        for (int w = 4; w <= 8; w *= 2) {
+            const int64_t kp = ceil_div(ceil_div(k, w), btl::kStepWeights) * btl::kStepWeights;
+            if (m * kp <= btl::kDecMaxPart) {
+                wv = w;
+                break;
+            }
+        }
+        if (wv > 0) {
+            int64_t kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
+            // tiles per wave: the most (fewest prologues per weight byte) that
+            // keeps `target` waves in flight and <= 16 wave-loads per lane
+            const int64_t steps = ceil_div(kpart, btl::kStepWeights);
+            const int64_t target = env_int("BTL_GEMV_DEC_WAVES", 6 * cus);
+            int rt = 1;
+            for (int t = 4; t >= 1; t /= 2) {
+                int64_t blocks = 0;
+                for (int i = 0; i < count; ++i) blocks += ceil_div(layers[i].w->n, 16 * t);
+                if ((blocks * wv >= target && t * steps <= 16 && (steps <= 4 || t <= 2)) || t == 1) {
+                    rt = t;
+                    break;
+                }
+            }
+            const int frt = env_int("BTL_GEMV_DEC_TILES", 0);
+            if (frt == 1 || frt == 2 || frt == 4) rt = frt;
+            const int fwv = env_int("BTL_GEMV_DEC_PARTS", 0);
+            if ((fwv == 4 || fwv == 8) && m * ceil_div(ceil_div(k, fwv), 256) * 256 <= btl::kDecMaxPart) {
+                wv = fwv;
+                kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
+            }
+            btl::GemvArgs a;
+            memset(&a, 0, sizeof(a));
+            int rb = 0, np = 0;
+            for (int i = 0; i < count; ++i) {
+                const int64_t n = layers[i].w->n;
+                if (n == 0) continue;
+                btl::GemvProblem& p = a.p[np++];
+                p.w = layers[i].w->data;
+                p.y = layers[i].y;
+                p.acc_out = layers[i].acc;
+                p.sw = layers[i].w->scale;
+                p.n = (int)n;
+                p.rb_begin = rb;
+                rb += (int)ceil_div(n, 16 * rt);
+            }
+            a.nprob = np;
+            a.x = x;
+            a.xs = xs;
+            a.m = (int)m;
+            a.k = (int)k;
+            a.rb_total = rb;
+            a.tiles = rt;
+            a.parts = wv;
+            a.kpart = (int)kpart;
+            a.mrows = (int)m;
+            a.ykind = ykind;
+            e = btl::launch_gemv_dec(a, xkind, 1, st);
+            if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
+            return BTL_OK;
+        }
+    }
+
+    const int64_t mtiles = ceil_div(m, mrows);
+    // 16-row tiles per workgroup: the most (fewest activation prologues per
+    // weight row) that still gives `target` workgroups; the 4 waves of a
+    // workgroup split K by 4 / tiles.
+    const int64_t target = env_int("BTL_GEMV_WG_TARGET", 3 * cus / 2);
+    int tiles = 1;
+    for (int t = 4; t >= 1; t /= 2) {
+        int64_t blocks = 0;
+        for (int i = 0; i < count; ++i) blocks += ceil_div(layers[i].w->n, 16 * t);
+        if (blocks * mtiles >= target || t == 1) {
+            tiles = t;
+            break;
+        }
+    }
+    const int forced = env_int("BTL_GEMV_TILES", 0);
+    if (forced == 1 || forced == 2 || forced == 4) tiles = forced;
+    const int parts = 4 / tiles;
+    const int64_t kpart = ceil_div(ceil_div(k, parts), btl::kStepWeights) * btl::kStepWeights;
+
+    // Several token tiles: quantise once into scratch.
+    const bool scratch = mtiles > 1 && xkind != btl::XK_I8;
+    const WsLayout L = ws_layout(m, k);
+    void* ws = nullptr;
+    if (scratch) {
+        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
+        int8_t* wq = (int8_t*)ws + L.q_off;
+        float* wsc = (float*)((uint8_t*)ws + L.s_off);
         e = btl::launch_quant_act(x, xkind, m, k, wq, wsc, st);
         if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
         x = wq;
         xs = wsc;
         xkind = btl::XK_I8;
     }
-    if (xkind == btl::XK_I8 && !aligned16(x)) return fail(BTL_ERR_LAYOUT, "int8 input must be 16-byte aligned");
-
-    const int64_t mtiles = ceil_div(m, btl::kGemvMaxM);
-    const int64_t mt = m < btl::kGemvMaxM ? m : btl::kGemvMaxM;
-    int cus;
-    {
-        std::lock_guard<std::mutex> lock(g_mu);
-        cus = g_dev[dev].cus;
-    }
-    // K split: aim for `target` workgroups in flight, each slice >= 256 weights.
-    const int64_t target = env_int("BTL_GEMV_WG_TARGET", 2 * cus);
-    const int64_t wgs = rb_total * mtiles;
-    int64_t S = (target + wgs / 2) / wgs;
-    const int forced = env_int("BTL_GEMV_SPLITS", 0);
-    if (forced > 0) S = forced;
-    if (S < 1) S = 1;
-    if (S > k / btl::kStepWeights) S = k / btl::kStepWeights > 0 ? k / btl::kStepWeights : 1;
-    int64_t slice = ceil_div(ceil_div(k, S), btl::kStepWeights) * btl::kStepWeights;
-    while (mt * (slice + 16) > btl::kGemvLdsMax && slice > btl::kStepWeights) slice -= btl::kStepWeights;
-    S = ceil_div(k, slice);
-    if (rb_total * S > INT32_MAX / 2) return fail(BTL_ERR_SHAPE, "problem too large for the GEMV grid");
 
     btl::GemvArgs a;
     memset(&a, 0, sizeof(a));
     int rb = 0;
-    int64_t poff = 0;
     int np = 0;
     for (int i = 0; i < count; ++i) {
         const int64_t n = layers[i].w->n;
@@ -270,24 +347,25 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         p.w = layers[i].w->data;
         p.y = layers[i].y;
         p.acc_out = layers[i].acc;
-        p.partial = (int32_t*)(wsb + L.partial_off) + poff;
         p.sw = layers[i].w->scale;
         p.n = (int)n;
         p.rb_begin = rb;
-        rb += (int)ceil_div(n, btl::kGemvRows);
-        poff += m * n;
+        rb += (int)ceil_div(n, 16 * tiles);
     }
     a.nprob = np;
     a.x = x;
     a.xs = xs;
-    a.counter = (uint32_t*)(wsb + L.counter_off);
     a.m = (int)m;
     a.k = (int)k;
     a.rb_total = rb;
-    a.splits = (int)S;
-    a.slice = (int)slice;
+    a.tiles = tiles;
+    a.parts = parts;
+    a.kpart = (int)kpart;
+    a.mrows = (int)mrows;
     e = btl::launch_gemv(a, xkind, ykind, (int)mtiles, st);
     if (e != hipSuccess) return hip_fail(e, "gemv kernel launch");
+    if (scratch && (e = btl::launch_fill_zero(ws, L.total, st)) != hipSuccess)
+        return hip_fail(e, "workspace clear");
     return BTL_OK;
 }
 
@@ -465,7 +543,8 @@ size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)
 {
     if (m < 0 || n < 0 || k < 0) return 0;
     if (mode == BTL_ACT_F32_REF) return 0;
-    return ws_layout(m, n, k, rb_bound(n)).total;
+    (void)n;
+    return ws_layout(m, k).total;
 }
 
 int btl_workspace_clear(void* ws, size_t ws_bytes, void* stream)

@@ -9,7 +9,6 @@
 namespace btl {
 
 constexpr int kMaxGroup = 4;       // layers per grouped launch (q|k|v, w1|w3)
-constexpr int kGemvRows = 64;      // output rows per GEMV workgroup: 4 waves x 16
 constexpr int kStepWeights = 256;  // weights of one row consumed per wave-load (64 B)
 constexpr int kGemvMaxM = 16;      // token rows per GEMV tile (MFMA 16x16 B operand)
 constexpr int kGemvLdsMax = 61440; // bytes of LDS the activation tile may use
@@ -22,25 +21,32 @@ struct GemvProblem {
     const uint8_t* w;  // packed rows, row stride k/4 bytes, 16-byte aligned base
     void* y;           // [m, n] output
     int32_t* acc_out;  // optional [m, n] int32 accumulators
-    int32_t* partial;  // split-K partial sums [m, n] (all zero on entry), or null
     float sw;          // per-tensor weight scale
     int n;             // output rows of this layer
-    int rb_begin;      // first global row-block (64 rows) of this layer
+    int rb_begin;      // first global row-block of this layer
 };
 
 struct GemvArgs {
     GemvProblem p[kMaxGroup];
     int nprob;
-    const void* x;       // [m, k]: f32 / bf16 (fused quantisation) or int8 (XK_I8)
-    const float* xs;     // XK_I8 only: per-row activation scales [m]
-    uint32_t* counter;   // split-K arrival counters [mtiles * rb_total] (zero on entry)
+    const void* x;    // [m, k]: f32 / bf16 (fused quantisation) or int8 (XK_I8)
+    const float* xs;  // XK_I8 only: per-row activation scales [m]
     int m, k;
-    int rb_total;        // row-blocks over all layers
-    int splits;          // K slices per row-block
-    int slice;           // weights per slice (multiple of 256)
+    int rb_total;     // row-blocks over all layers (grid.x)
+    int tiles;        // 16-row tiles per row-block (1, 2 or 4)
+    int parts;        // K parts per tile (4 / tiles)
+    int kpart;        // weights per K part (multiple of 256)
+    int mrows;        // token rows per grid.y tile (<= 16)
+    int ykind;        // YK_F32 / YK_BF16 (k_gemv_dec only; k_gemv takes it as a template)
 };
 
 hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipStream_t s);
+
+// Decode variant: a.tiles (1, 2, 4) 16-row tiles per wave, a.parts (4 or 8)
+// waves split K, a.mrows <= 4, a.mrows * a.kpart <= kDecMaxPart and
+// a.tiles * ceil(a.kpart / 256) <= 16 wave-loads per lane.
+constexpr int kDecMaxPart = 2048;
+hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s);
 
 hipError_t launch_quant_act(const void* x, int xkind, int64_t m, int64_t k, int8_t* q,
                             float* s, hipStream_t st);

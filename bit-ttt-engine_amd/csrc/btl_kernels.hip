@@ -8,8 +8,11 @@
 // Kernels:
 //   k_gemv<XK,YK>     decode / small-M contraction on the int8 MFMA
 //                     (v_mfma_i32_16x16x64_i8), weights unpacked in registers,
-//                     activations quantised (or copied) into LDS, split-K with
-//                     exact int32 atomics and a self-cleaning last-block epilogue.
+//                     activations quantised (or copied) into LDS, K split over
+//                     the waves of a workgroup and summed exactly through LDS.
+//   k_gemv_dec<XK,YK,WV>  the decode case (1..4 token rows): one 16-row tile
+//                     per workgroup, WV waves split K, activations quantised
+//                     per wave from registers loaded ahead of the weights.
 //   k_quant_act<XK>   per-token absmax int8 quantisation, natural layout.
 //   k_ref_f32<XK,YK>  reference-semantics fp32 path: bit-identical to the
 //                     8-lane FMA order of cpu.rs.
@@ -130,18 +133,6 @@ __device__ __forceinline__ v4i unpack16(uint32_t w)
     return r;
 }
 
-// 16 int8 values q[0..15] (natural k order) -> the transposed operand order.
-__device__ __forceinline__ uint4 pack_transposed(const int* q)
-{
-    uint4 o;
-    uint32_t* ow = (uint32_t*)&o;
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-        ow[v] = ((uint32_t)(q[v] & 0xFF)) | ((uint32_t)(q[4 + v] & 0xFF) << 8) |
-                ((uint32_t)(q[8 + v] & 0xFF) << 16) | ((uint32_t)(q[12 + v] & 0xFF) << 24);
-    return o;
-}
-
 // 16 int8 bytes in natural order (4 words, word b = k 4b..4b+3) -> transposed.
 __device__ __forceinline__ uint4 transpose16(uint4 a)
 {
@@ -161,60 +152,74 @@ __device__ __forceinline__ uint4 transpose16(uint4 a)
 // ---------------------------------------------------------------------------
 // k_gemv: small-M ternary contraction on the int8 MFMA
 // ---------------------------------------------------------------------------
-// Grid: x = rb_total * splits (row-block major, slice minor), y = M tiles of 16.
-// Workgroup: 4 waves; wave w owns rows [64*rb + 16*w, +16) of its layer and the
-// K slice [slice*s, +slice).  Per wave-load, lane (r = lane&15, kq = lane>>4)
-// reads 16 bytes (64 weights) of row r at byte 64*j + 16*kq of the slice, i.e.
-// each row contributes 64 contiguous bytes and a wave-load covers 16 x 256
-// weights.  Each 4-byte word becomes one A operand (16 rows x 64 k) of
-// v_mfma_i32_16x16x64_i8; the B operand is 16 token rows x 64 k from LDS.
-// D lane l, element v = row 4*(l>>4)+v, token l&15.
-constexpr int kPF = 4;  // wave-loads kept in flight per lane
+// Grid: x = row-blocks of 16*tiles rows (over all layers of a group), y = token
+// tiles of `mrows` rows.  Workgroup: 4 waves = tiles x parts; wave w owns the
+// 16-row tile w / parts and the K part w % parts (kpart weights, a multiple of
+// 256).  Per wave-load, lane (r = lane&15, kq = lane>>4) reads 16 bytes (64
+// weights) of row r at byte 64*j + 16*kq of its part: each row contributes 64
+// contiguous bytes, a wave-load covers 16 rows x 256 weights.  Each 4-byte
+// word becomes one A operand (16 rows x 64 k) of v_mfma_i32_16x16x64_i8; the B
+// operand (token rows x 64 k) comes from the quantised activation tile in LDS.
+// D lane l, element v = row 4*(l>>4)+v, token l&15.  Parts of one tile are
+// summed through LDS (exact int32); no cross-workgroup communication.
+constexpr int kPF = 16;  // wave-loads kept in flight per lane (64 VGPRs)
+
+// round_half_away(x*r) as an int, for a finite row (see quant1)
+__device__ __forceinline__ int quant_fast(float x, float r)
+{
+    const float y = __fmul_rn(x, r);
+    return (int)__fadd_rn(y, __builtin_copysignf(0.49999997f, y));
+}
+
+// bytes {q[v], q[4+v], q[8+v], q[12+v]} of four ints -> one word
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d)
+{
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0C0C0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000C0Cu);
+    return lo | hi;
+}
+
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 template <int XK>
-__device__ __forceinline__ void gemv_prologue(const GemvArgs& a, uint8_t* sq, int lp, int m0,
-                                              int mt, int k0, int len, float* s_sx,
-                                              uint32_t (*s_amax)[kGemvMaxM], float* s_r,
+__device__ __forceinline__ void gemv_prologue(const GemvArgs& a, uint8_t* sq, int lp, int m0, int mt,
+                                              float* s_sx, uint32_t (*s_amax)[kGemvMaxM], float* s_r,
                                               int* s_ok)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.k;
-    const int groups = len >> 4;  // len % 64 == 0
+    const int groups = K >> 4;  // K % 64 == 0
     if (XK == XK_I8) {
         const int8_t* xq = (const int8_t*)a.x;
         if (tid < mt) s_sx[tid] = a.xs[m0 + tid];
         for (int g = tid; g < mt * groups; g += 256) {
             const int m = g / groups, gi = g - m * groups;
-            uint4 v = *(const uint4*)(xq + (int64_t)(m0 + m) * K + k0 + gi * 16);
+            uint4 v = *(const uint4*)(xq + (int64_t)(m0 + m) * K + gi * 16);
             *(uint4*)(sq + m * lp + gi * 16) = transpose16(v);
         }
         return;
     }
-    // 1. absmax of each token row over the full K
+    // 1. absmax of each token row (IEEE bit patterns, sign cleared)
     for (int m = 0; m < mt; ++m) {
         uint32_t amax = 0;
         if (XK == XK_BF16) {
             const uint4* xr = (const uint4*)((const uint16_t*)a.x + (int64_t)(m0 + m) * K);
+            us2 mx = {0, 0};
             for (int i = tid; i < (K >> 3); i += 256) {
-                uint4 v = xr[i];
-                const uint32_t* u = (const uint32_t*)&v;
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    uint32_t lo = (u[h] << 16) & 0x7FFF0000u, hi = u[h] & 0x7FFF0000u;
-                    amax = lo > amax ? lo : amax;
-                    amax = hi > amax ? hi : amax;
-                }
+                const uint4 v = xr[i];
+                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.x & 0x7FFF7FFFu));
+                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.y & 0x7FFF7FFFu));
+                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.z & 0x7FFF7FFFu));
+                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.w & 0x7FFF7FFFu));
             }
+            amax = (uint32_t)(mx.x > mx.y ? mx.x : mx.y) << 16;
         } else {
             const uint4* xr = (const uint4*)((const float*)a.x + (int64_t)(m0 + m) * K);
             for (int i = tid; i < (K >> 2); i += 256) {
-                uint4 v = xr[i];
-                const uint32_t* u = (const uint32_t*)&v;
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    uint32_t b = u[h] & 0x7FFFFFFFu;
-                    amax = b > amax ? b : amax;
-                }
+                const uint4 v = xr[i];
+                const uint32_t b0 = v.x & 0x7FFFFFFFu, b1 = v.y & 0x7FFFFFFFu;
+                const uint32_t b2 = v.z & 0x7FFFFFFFu, b3 = v.w & 0x7FFFFFFFu;
+                amax = max(amax, max(max(b0, b1), max(b2, b3)));
             }
         }
         amax = wave_max_u32(amax);
@@ -225,92 +230,91 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs& a, uint8_t* sq, in
         uint32_t am = s_amax[0][tid];
 #pragma unroll
         for (int w = 1; w < 4; ++w) am = s_amax[w][tid] > am ? s_amax[w][tid] : am;
-        QParams qp = qparams(am);
+        const QParams qp = qparams(am);
         s_r[tid] = qp.r;
         s_sx[tid] = qp.s;
         s_ok[tid] = qp.ok;
     }
     __syncthreads();
-    // 2. quantise this K slice into LDS in operand order
+    // 2. quantise the rows into LDS, 16 values per thread per step, operand order
     for (int g = tid; g < mt * groups; g += 256) {
         const int m = g / groups, gi = g - m * groups;
         const float r = s_r[m];
-        const int ok = s_ok[m];
-        int q[16];
-        if (XK == XK_BF16) {
-            const uint4* src =
-                (const uint4*)((const uint16_t*)a.x + (int64_t)(m0 + m) * K + k0 + gi * 16);
-            uint4 v0 = src[0], v1 = src[1];
-            const uint32_t* u0 = (const uint32_t*)&v0;
-            const uint32_t* u1 = (const uint32_t*)&v1;
+        uint4 out = {0u, 0u, 0u, 0u};
+        if (s_ok[m]) {
+            float f[16];
+            if (XK == XK_BF16) {
+                const uint4* src = (const uint4*)((const uint16_t*)a.x + (int64_t)(m0 + m) * K + gi * 16);
+                const uint4 v0 = src[0], v1 = src[1];
+                const uint32_t u[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                q[2 * h] = quant1(bf16_to_f32(u0[h] & 0xFFFFu), r, ok);
-                q[2 * h + 1] = quant1(bf16_to_f32(u0[h] >> 16), r, ok);
-                q[8 + 2 * h] = quant1(bf16_to_f32(u1[h] & 0xFFFFu), r, ok);
-                q[8 + 2 * h + 1] = quant1(bf16_to_f32(u1[h] >> 16), r, ok);
-            }
-        } else {
-            const float4* src =
-                (const float4*)((const float*)a.x + (int64_t)(m0 + m) * K + k0 + gi * 16);
+                for (int h = 0; h < 8; ++h) {
+                    f[2 * h] = __uint_as_float(u[h] << 16);
+                    f[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
+                }
+            } else {
+                const float4* src = (const float4*)((const float*)a.x + (int64_t)(m0 + m) * K + gi * 16);
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                float4 v = src[h];
-                q[4 * h] = quant1(v.x, r, ok);
-                q[4 * h + 1] = quant1(v.y, r, ok);
-                q[4 * h + 2] = quant1(v.z, r, ok);
-                q[4 * h + 3] = quant1(v.w, r, ok);
+                for (int h = 0; h < 4; ++h) {
+                    const float4 v = src[h];
+                    f[4 * h] = v.x; f[4 * h + 1] = v.y; f[4 * h + 2] = v.z; f[4 * h + 3] = v.w;
+                }
             }
+            int q[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[i] = quant_fast(f[i], r);
+            out.x = pack4(q[0], q[4], q[8], q[12]);
+            out.y = pack4(q[1], q[5], q[9], q[13]);
+            out.z = pack4(q[2], q[6], q[10], q[14]);
+            out.w = pack4(q[3], q[7], q[11], q[15]);
         }
-        *(uint4*)(sq + m * lp + gi * 16) = pack_transposed(q);
+        *(uint4*)(sq + m * lp + gi * 16) = out;
     }
 }
 
 template <int XK, int YK>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
 {
-    extern __shared__ __align__(16) uint8_t sq[];  // [mt][lp] int8 activation tile
+    extern __shared__ __align__(16) uint8_t sq[];  // [mt][k + 16] int8 activation tile
     __shared__ uint32_t s_amax[4][kGemvMaxM];
     __shared__ float s_r[kGemvMaxM], s_sx[kGemvMaxM];
     __shared__ int s_ok[kGemvMaxM];
-    __shared__ int s_last;
+    __shared__ v4i s_red[3][64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int S = a.splits;
-    const int rbg = blockIdx.x / S;
-    const int sidx = blockIdx.x - rbg * S;
-    const int mtile = blockIdx.y;
-    const int m0 = mtile * kGemvMaxM;
-    const int mt = min(kGemvMaxM, a.m - m0);
+    const int rbg = blockIdx.x;
+    const int m0 = blockIdx.y * a.mrows;
+    const int mt = min(a.mrows, a.m - m0);
 
     // layer of this row-block (uniform; explicit selects keep the kernel
     // arguments in scalar registers)
     const uint8_t* W = a.p[0].w;
     void* Y = a.p[0].y;
     int32_t* ACC = a.p[0].acc_out;
-    int32_t* PART = a.p[0].partial;
     float SW = a.p[0].sw;
     int N = a.p[0].n;
     int RB0 = a.p[0].rb_begin;
 #pragma unroll
     for (int i = 1; i < kMaxGroup; ++i) {
         if (i < a.nprob && rbg >= a.p[i].rb_begin) {
-            W = a.p[i].w; Y = a.p[i].y; ACC = a.p[i].acc_out; PART = a.p[i].partial;
+            W = a.p[i].w; Y = a.p[i].y; ACC = a.p[i].acc_out;
             SW = a.p[i].sw; N = a.p[i].n; RB0 = a.p[i].rb_begin;
         }
     }
-    const int rb = rbg - RB0;
     const int K = a.k;
-    const int k0 = sidx * a.slice;
-    const int len = min(a.slice, K - k0);
-    const int steps = (len + kStepWeights - 1) / kStepWeights;
-    const int lp = a.slice + 16;
+    const int parts = a.parts;
+    const int t = wave / parts, part = wave - t * parts;
+    const int kb = part * a.kpart;
+    const int len = min(a.kpart, K - kb);
+    const int steps = len > 0 ? (len + kStepWeights - 1) / kStepWeights : 0;
+    const int lp = K + 16;
 
-    // 1. put the first weight loads in flight before the activation prologue
+    // 1. put this wave's weight loads in flight before the activation prologue
     const int r = lane & 15, kq = lane >> 4;
-    const int nrow = rb * kGemvRows + wave * 16 + r;
+    const int row0 = (rbg - RB0) * (16 * a.tiles) + t * 16;
+    const int nrow = row0 + r;
     const bool row_ok = nrow < N;
-    const uint8_t* wp = W + (int64_t)(row_ok ? nrow : 0) * (K >> 2) + (k0 >> 2) + kq * 16;
+    const uint8_t* wp = W + (int64_t)(row_ok ? nrow : 0) * (K >> 2) + (kb >> 2) + kq * 16;
     auto ld = [&](int j) -> uint4 {
         uint4 v = {0u, 0u, 0u, 0u};
         if (row_ok && j * kStepWeights + kq * 64 < len) v = *(const uint4*)(wp + j * 64);
@@ -321,13 +325,13 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
     for (int i = 0; i < kPF; ++i) buf[i] = ld(i);
 
     // 2. activation tile
-    gemv_prologue<XK>(a, sq, lp, m0, mt, k0, len, s_sx, s_amax, s_r, s_ok);
+    gemv_prologue<XK>(a, sq, lp, m0, mt, s_sx, s_amax, s_r, s_ok);
     __syncthreads();
 
     // 3. main loop
     const int mcol = lane & 15;
     const bool m_ok = mcol < mt;
-    const uint8_t* bq = sq + mcol * lp + kq * 64;
+    const uint8_t* bq = sq + mcol * lp + kb + kq * 64;
     v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     const v4i zero = {0, 0, 0, 0};
     for (int j0 = 0; j0 < steps; j0 += kPF) {
@@ -338,10 +342,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
                 const uint4 cur = buf[i];
                 buf[i] = ld(j + kPF);
                 const uint8_t* bj = bq + j * kStepWeights;
-                v4i b0 = m_ok ? *(const v4i*)(bj + 0) : zero;
-                v4i b1 = m_ok ? *(const v4i*)(bj + 16) : zero;
-                v4i b2 = m_ok ? *(const v4i*)(bj + 32) : zero;
-                v4i b3 = m_ok ? *(const v4i*)(bj + 48) : zero;
+                const v4i b0 = m_ok ? *(const v4i*)(bj + 0) : zero;
+                const v4i b1 = m_ok ? *(const v4i*)(bj + 16) : zero;
+                const v4i b2 = m_ok ? *(const v4i*)(bj + 32) : zero;
+                const v4i b3 = m_ok ? *(const v4i*)(bj + 48) : zero;
                 acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc0, 0, 0, 0);
                 acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc1, 0, 0, 0);
                 acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc0, 0, 0, 0);
@@ -349,61 +353,343 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
             }
         }
     }
-    const v4i acc = acc0 + acc1;
+    v4i acc = acc0 + acc1;
 
-    // 4. epilogue
+    // 4. sum the K parts of each tile (exact), then the epilogue
+    if (parts > 1) {
+        if (part > 0) s_red[(part - 1) * a.tiles + t][lane] = acc;
+        __syncthreads();
+        if (part > 0) return;
+        for (int p = 1; p < parts; ++p) acc += s_red[(p - 1) * a.tiles + t][lane];
+    }
+    if (!m_ok) return;
     const int gm = m0 + mcol;
-    const int nb = rb * kGemvRows + wave * 16 + 4 * (lane >> 4);
-    if (S == 1) {
-        if (m_ok) {
-            const float c = __fmul_rn(s_sx[mcol], SW);
+    const float c = __fmul_rn(s_sx[mcol], SW);
+    const int nb = row0 + 4 * (lane >> 4);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int n = nb + v;
-                if (n < N) {
-                    const int64_t o = (int64_t)gm * N + n;
-                    store_y<YK>(Y, o, __fmul_rn((float)acc[v], c));
-                    if (ACC) ACC[o] = acc[v];
-                }
+    for (int v = 0; v < 4; ++v) {
+        const int n = nb + v;
+        if (n < N) {
+            const int64_t o = (int64_t)gm * N + n;
+            store_y<YK>(Y, o, __fmul_rn((float)acc[v], c));
+            if (ACC) ACC[o] = acc[v];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_gemv_dec: decode (1..4 token rows), one 16-row tile per workgroup
+// ---------------------------------------------------------------------------
+// The WV waves of a workgroup split K into parts of kpart weights; wave p owns
+// part p of the same 16 rows.  Each wave first loads its part of the
+// activations into registers (at most kDecGroups 16-element groups per lane),
+// then puts all its weight loads in flight, so the activation prologue waits
+// only for its own loads.  The partial absmax of the WV parts meet in LDS (one
+// barrier); every wave then quantises its own part into a wave-private LDS
+// region in operand order.  Parts are summed exactly through LDS at the end.
+constexpr int kDecGroups = 2;  // 16-element activation groups per lane
+
+template <int XK>
+struct DecX {
+    static constexpr int kVec = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);  // uint4 per group
+};
+
+template <int XK>
+__device__ __forceinline__ uint32_t group_absmax(const uint4* v)
+{
+    if (XK == XK_BF16) {
+        us2 mx = __builtin_bit_cast(us2, v[0].x & 0x7FFF7FFFu);
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v[0].y & 0x7FFF7FFFu));
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v[0].z & 0x7FFF7FFFu));
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v[0].w & 0x7FFF7FFFu));
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v[1].x & 0x7FFF7FFFu));
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v[1].y & 0x7FFF7FFFu));
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v[1].z & 0x7FFF7FFFu));
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v[1].w & 0x7FFF7FFFu));
+        return (uint32_t)(mx.x > mx.y ? mx.x : mx.y) << 16;
+    }
+    uint32_t m = 0;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        m = max(m, max(max(v[h].x & 0x7FFFFFFFu, v[h].y & 0x7FFFFFFFu),
+                       max(v[h].z & 0x7FFFFFFFu, v[h].w & 0x7FFFFFFFu)));
+    }
+    return m;
+}
+
+// 16 activations of one group -> operand-order int8 word quadruple
+template <int XK>
+__device__ __forceinline__ uint4 group_quant(const uint4* v, float r)
+{
+    if (XK == XK_I8) return transpose16(v[0]);
+    float f[16];
+    if (XK == XK_BF16) {
+        const uint32_t u[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            f[2 * h] = __uint_as_float(u[h] << 16);
+            f[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            f[4 * h] = __uint_as_float(v[h].x); f[4 * h + 1] = __uint_as_float(v[h].y);
+            f[4 * h + 2] = __uint_as_float(v[h].z); f[4 * h + 3] = __uint_as_float(v[h].w);
+        }
+    }
+    int q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = quant_fast(f[i], r);
+    uint4 o;
+    o.x = pack4(q[0], q[4], q[8], q[12]);
+    o.y = pack4(q[1], q[5], q[9], q[13]);
+    o.z = pack4(q[2], q[6], q[10], q[14]);
+    o.w = pack4(q[3], q[7], q[11], q[15]);
+    return o;
+}
+
+// Raw buffer loads: a per-workgroup resource descriptor bounds every access,
+// and an out-of-range offset reads zeros without a branch, so the compiler can
+// count the loads in flight exactly (s_waitcnt vmcnt(N) per step).
+constexpr int kOOB = 0x7FFFFFF0;  // offset outside every descriptor range
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, int off)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Max of a u32 over the wave, via DPP (quad perms, row rotations, row
+// broadcasts); the result is read from lane 63.
+__device__ __forceinline__ uint32_t wave_max_dpp(uint32_t v)
+{
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xF, 0xF, false));  // row_ror:4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xF, 0xF, false));  // row_ror:8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));  // row_bcast:15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));  // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// ST: wave-loads per row tile per wave (compile time, >= the part's steps;
+// the loads past the part read zeros, so every step runs unconditionally).
+// RT: 16-row tiles per wave (they share the activation prologue and the
+// B-operand reads).  MT: token rows, 1 or up to 4.  The workgroup covers
+// 16*RT rows; its WV waves split K.
+template <int XK, int WV, int ST, int RT, int MT>
+__global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
+{
+    extern __shared__ __align__(16) uint8_t sq[];  // [WV][mt][kpart + 16]
+    __shared__ uint32_t s_amax[WV][MT];
+    __shared__ v4i s_red[WV > 1 ? (WV - 1) * RT : 1][64];
+
+    const int tid = threadIdx.x, lane = tid & 63, part = tid >> 6;
+    const int rbg = blockIdx.x;
+    const int mt = MT == 1 ? 1 : min(MT, a.m);
+
+    const uint8_t* W = a.p[0].w;
+    void* Y = a.p[0].y;
+    int32_t* ACC = a.p[0].acc_out;
+    float SW = a.p[0].sw;
+    int N = a.p[0].n;
+    int RB0 = a.p[0].rb_begin;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i) {
+        if (i < a.nprob && rbg >= a.p[i].rb_begin) {
+            W = a.p[i].w; Y = a.p[i].y; ACC = a.p[i].acc_out;
+            SW = a.p[i].sw; N = a.p[i].n; RB0 = a.p[i].rb_begin;
+        }
+    }
+    const int K = a.k;
+    const int kp = a.kpart;
+    const int kb = part * kp;
+    const int len = max(0, min(kp, K - kb));
+    const int lpw = kp + 16;
+    uint8_t* myq = sq + part * (mt * lpw);
+
+    // 1. this wave's activations -> registers (issued before the weight loads)
+    constexpr int NV = DecX<XK>::kVec;
+    constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);  // bytes per element
+    const int gpr = len >> 4;  // 16-element groups per token row in this part
+    const int ng = mt * gpr;
+    int gm_[kDecGroups], gc_[kDecGroups];
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(mt * K * ES));
+    uint4 xv[kDecGroups][NV];
+#pragma unroll
+    for (int gi = 0; gi < kDecGroups; ++gi) {
+        const int g = lane + 64 * gi;
+        const int m = MT == 1 ? 0 : g / max(gpr, 1);
+        gm_[gi] = m;
+        gc_[gi] = g - m * gpr;
+        const int off = g < ng ? (m * K + kb + 16 * gc_[gi]) * ES : kOOB;
+#pragma unroll
+        for (int h = 0; h < NV; ++h) xv[gi][h] = gi == 0 || 64 * gi < ng ? bload(xr, off + 16 * h) : uint4{0u, 0u, 0u, 0u};
+    }
+
+    // 2. every weight load of this wave in flight
+    const int r = lane & 15, kq = lane >> 4;
+    const int row0 = (rbg - RB0) * (16 * RT);
+    const int rows = min(16 * RT, N - row0);
+    const int rb_bytes = K >> 2;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(W + (int64_t)row0 * rb_bytes, (uint32_t)(rows * rb_bytes));
+    uint4 buf[RT][ST];
+#pragma unroll
+    for (int j = 0; j < ST; ++j) {
+        const bool kin = j * kStepWeights + kq * 64 < len;
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+            buf[t][j] = bload(wr, kin ? (t * 16 + r) * rb_bytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
+    }
+
+    // 3. absmax of each token row: per-wave partials meet in LDS; lane m then
+    //    holds the quantisation parameters of token row m
+    float r_l = 0.0f, s_l = 0.0f;
+    if (XK != XK_I8) {
+        uint32_t am[MT];
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm) am[mm] = 0u;
+#pragma unroll
+        for (int gi = 0; gi < kDecGroups; ++gi) {
+            if (gi == 0 || 64 * gi < ng) {
+                const uint32_t v = lane + 64 * gi < ng ? group_absmax<XK>(xv[gi]) : 0u;
+#pragma unroll
+                for (int mm = 0; mm < MT; ++mm) am[mm] = (MT == 1 || mm == gm_[gi]) ? max(am[mm], v) : am[mm];
             }
         }
-        return;
-    }
-    if (m_ok) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = nb + v;
-            if (n < N) atomicAdd(&PART[(int64_t)gm * N + n], acc[v]);
+        for (int mm = 0; mm < MT; ++mm) {
+            if (mm < mt) {
+                const uint32_t v = wave_max_dpp(am[mm]);
+                if (lane == 0) s_amax[part][mm] = v;
+            }
+        }
+        __syncthreads();
+        const int lm = MT == 1 ? 0 : min(lane, mt - 1);
+        uint32_t v = 0;
+#pragma unroll
+        for (int p = 0; p < WV; ++p) v = max(v, s_amax[p][lm]);
+        const QParams qp = qparams(v);
+        r_l = qp.ok ? qp.r : 0.0f;
+        s_l = qp.s;
+    } else {
+        s_l = a.xs[MT == 1 ? 0 : min(lane, mt - 1)];
+    }
+
+    // 4. quantise this wave's part into its LDS region (wave-private: no barrier)
+#pragma unroll
+    for (int gi = 0; gi < kDecGroups; ++gi) {
+        if (gi == 0 || 64 * gi < ng) {
+            const int g = lane + 64 * gi;
+            float rm = r_l;
+            if (MT > 1) rm = __shfl(r_l, gm_[gi], 64);
+            uint4 q = group_quant<XK>(xv[gi], rm);
+            if (XK != XK_I8 && rm == 0.0f) q = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
+            if (g < ng) *(uint4*)(myq + gm_[gi] * lpw + 16 * gc_[gi]) = q;
         }
     }
-    __threadfence();
-    __syncthreads();
-    uint32_t* cnt = a.counter + (int64_t)mtile * a.rb_total + rbg;
-    if (tid == 0) s_last = (atomicAdd(cnt, 1u) == (uint32_t)(S - 1));
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    if (m_ok) {
-        const float c = __fmul_rn(s_sx[mcol], SW);
+
+    // 5. contraction.  B lanes of token columns >= mt read row 0: those
+    //    columns of D are never stored.
+    const int mcol = lane & 15;
+    const bool m_ok = mcol < mt;
+    const uint8_t* bq = myq + (m_ok ? mcol : 0) * lpw + kq * 64;
+    v4i acc[RT][2];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[t][0] = acc[t][1] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < ST; ++j) {
+        const uint8_t* bj = bq + j * kStepWeights;
+        const v4i b0 = *(const v4i*)(bj + 0);
+        const v4i b1 = *(const v4i*)(bj + 16);
+        const v4i b2 = *(const v4i*)(bj + 32);
+        const v4i b3 = *(const v4i*)(bj + 48);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const uint4 cur = buf[t][j];
+            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc[t][1], 0, 0, 0);
+            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc[t][1], 0, 0, 0);
+        }
+    }
+    v4i res[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) res[t] = acc[t][0] + acc[t][1];
+
+    // 6. sum the parts (exact), epilogue by wave 0
+    if (WV > 1) {
+        if (part > 0) {
+#pragma unroll
+            for (int t = 0; t < RT; ++t) s_red[(part - 1) * RT + t][lane] = res[t];
+        }
+        __syncthreads();
+        if (part > 0) return;
+#pragma unroll
+        for (int p = 1; p < WV; ++p)
+#pragma unroll
+            for (int t = 0; t < RT; ++t) res[t] += s_red[(p - 1) * RT + t][lane];
+    }
+    const float sx = MT == 1 ? s_l : __shfl(s_l, mcol < mt ? mcol : 0, 64);
+    if (!m_ok) return;
+    const float c = __fmul_rn(sx, SW);
+    const bool ybf = a.ykind == YK_BF16;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+        const int nb = row0 + 16 * t + 4 * (lane >> 4);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int n = nb + v;
             if (n < N) {
-                const int64_t o = (int64_t)gm * N + n;
-                const int tot = atomicExch(&PART[o], 0);
-                store_y<YK>(Y, o, __fmul_rn((float)tot, c));
-                if (ACC) ACC[o] = tot;
+                const int64_t o = (int64_t)mcol * N + n;
+                const float yv = __fmul_rn((float)res[t][v], c);
+                if (ybf) ((uint16_t*)Y)[o] = f32_to_bf16(yv);
+                else ((float*)Y)[o] = yv;
+                if (ACC) ACC[o] = res[t][v];
             }
         }
     }
-    if (tid == 0) atomicExch(cnt, 0u);
+}
+
+hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s)
+{
+    (void)mtiles;
+    dim3 grid((unsigned)a.rb_total);
+    const int mt = a.m;
+    const int wv = a.parts, rt = a.tiles;
+    const int st_need = (a.kpart + kStepWeights - 1) / kStepWeights;
+    const int st = st_need <= 2 ? 2 : st_need <= 4 ? 4 : 8;
+    const int mtk = mt == 1 ? 1 : 4;
+    const size_t lds = (size_t)wv * mt * (size_t)(a.kpart + 16);
+#define BTL_DEC_CASE(XKV, WVV, STV, RTV, MTV)                                                        \
+    if (xkind == XKV && wv == WVV && st == STV && rt == RTV && mtk == MTV) {                         \
+        hipLaunchKernelGGL((k_gemv_dec<XKV, WVV, STV, RTV, MTV>), grid, dim3(WVV * 64), lds, s, a);  \
+        return hipGetLastError();                                                                    \
+    }
+#define BTL_DEC_SHAPES(XKV, WVV, MTV)                                                                   \
+    BTL_DEC_CASE(XKV, WVV, 2, 1, MTV) BTL_DEC_CASE(XKV, WVV, 2, 2, MTV) BTL_DEC_CASE(XKV, WVV, 2, 4, MTV)  \
+    BTL_DEC_CASE(XKV, WVV, 4, 1, MTV) BTL_DEC_CASE(XKV, WVV, 4, 2, MTV) BTL_DEC_CASE(XKV, WVV, 4, 4, MTV)  \
+    BTL_DEC_CASE(XKV, WVV, 8, 1, MTV) BTL_DEC_CASE(XKV, WVV, 8, 2, MTV)
+#define BTL_DEC_WV(WVV, MTV) BTL_DEC_SHAPES(XK_F32, WVV, MTV) BTL_DEC_SHAPES(XK_BF16, WVV, MTV) BTL_DEC_SHAPES(XK_I8, WVV, MTV)
+    BTL_DEC_WV(4, 1)
+    BTL_DEC_WV(8, 1)
+    BTL_DEC_WV(4, 4)
+    BTL_DEC_WV(8, 4)
+#undef BTL_DEC_WV
+#undef BTL_DEC_SHAPES
+#undef BTL_DEC_CASE
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipStream_t s)
 {
-    dim3 grid((unsigned)(a.rb_total * a.splits), (unsigned)mtiles);
-    const int mt = a.m < kGemvMaxM ? a.m : kGemvMaxM;
-    const size_t lds = (size_t)mt * (size_t)(a.slice + 16);
+    dim3 grid((unsigned)a.rb_total, (unsigned)mtiles);
+    const int mt = a.m < a.mrows ? a.m : a.mrows;
+    const size_t lds = (size_t)mt * (size_t)(a.k + 16);
 #define BTL_GEMV_CASE(XKV, YKV)                                              \
     if (xkind == XKV && ykind == YKV) {                                      \
         hipLaunchKernelGGL((k_gemv<XKV, YKV>), grid, dim3(256), lds, s, a);  \

@@ -159,9 +159,12 @@ int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, co
 
 /*
  * Workspace bytes needed by btl_linear / btl_linear_i8 for this shape and mode
- * (for btl_linear_group pass n = sum of the layers' n).  A caller-provided
- * workspace must be cleared once with btl_workspace_clear before its first use;
- * every successful call leaves it cleared again.
+ * (for btl_linear_group pass n = sum of the layers' n).  Contract: a workspace
+ * is all-zero between calls.  Clear a caller-provided one once with
+ * btl_workspace_clear before its first use; every call leaves every byte it
+ * touched zero again (split-K partial sums are cleared by the kernel that
+ * consumes them, scratch activations by a fill kernel queued after their
+ * readers), so one workspace can serve calls of any shapes that fit in it.
  */
 size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode);
 

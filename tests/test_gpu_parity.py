@@ -119,12 +119,14 @@ def test_linear_i8_special_rows():
     assert np.all(y[1].cpu().numpy() == 0)
 
 
-@pytest.mark.parametrize("splits", ["1", "2", "3", "7", "16"])
-def test_split_k_is_exact(splits, monkeypatch):
-    m, k, n = 2, 4096, 320
+@pytest.mark.parametrize("tiles", ["1", "2", "4"])
+@pytest.mark.parametrize("k", [4096, 14336, 320])
+def test_k_split_is_exact(tiles, k, monkeypatch):
+    # 4 / tiles waves of a workgroup split K and are summed through LDS
+    m, n = 2, 320
     x = activations(m, k, seed=11)
     pt, wb, sw = make_layer(n, k, seed=12)
-    monkeypatch.setenv("BTL_GEMV_SPLITS", splits)
+    monkeypatch.setenv("BTL_GEMV_TILES", tiles)
     acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
@@ -133,23 +135,36 @@ def test_split_k_is_exact(splits, monkeypatch):
 
 
 def test_caller_workspace_left_clear():
-    m, k, n = 3, 4096, 1000
+    m, k, n = 40, 4096, 1000
     x = to_dev(activations(m, k, seed=1), torch.bfloat16)
     pt, wb, sw = make_layer(n, k, seed=2)
     ws = bl.Workspace(m, n, k, device=DEV)
-    os.environ["BTL_GEMV_SPLITS"] = "4"
-    try:
-        y1 = bl.BitLinearHip.forward(x, pt, workspace=ws)
-        y2 = bl.BitLinearHip.forward(x, pt, workspace=ws)
-    finally:
-        del os.environ["BTL_GEMV_SPLITS"]
+    y1 = bl.BitLinearHip.forward(x, pt, workspace=ws)
+    y2 = bl.BitLinearHip.forward(x, pt, workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
-    # the split-K region (partial sums, then arrival counters) is zero again
-    zero_region = -(-4 * m * n // 256) * 256 + 256
-    assert int(ws.buf[:zero_region].count_nonzero()) == 0
+    # the whole workspace is zero again (contract of btl_workspace_bytes)
+    assert int(ws.buf.count_nonzero()) == 0
     yr, _, _, _ = orc.forward_i8(host_x(x), wb, n, sw)
     assert_bf16_matches(y1, yr)
+
+
+@pytest.mark.parametrize("use_caller_ws", [False, True])
+def test_workspace_shared_across_shapes(use_caller_ws, monkeypatch):
+    # scratch users (ragged k, m > 16) and fused-prologue calls share one
+    # workspace; each call must leave it all-zero for the next
+    ws = bl.Workspace(40, 2048, 4096, device=DEV) if use_caller_ws else None
+    for (m, k, n) in [(2, 68, 130), (40, 1024, 300), (16, 512, 200), (3, 36, 500), (16, 4096, 2048),
+                      (33, 256, 64), (1, 4096, 1024)]:
+        x = activations(m, k, seed=m * k + n)
+        pt, wb, sw = make_layer(n, k, seed=n)
+        acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+        y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc, workspace=ws)
+        yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
+        assert np.array_equal(acc.cpu().numpy(), accr), (m, k, n)
+        assert_f32_identical(y, yr)
+        if ws is not None:
+            assert int(ws.buf.count_nonzero()) == 0, (m, k, n)
 
 
 def test_linear_i8_prequantized_equals_fused():
