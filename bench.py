@@ -82,17 +82,6 @@ class Call:
                                          self.m, self.k, bl.BTL_BF16, None, 0, stream))
 
 
-def event_time_us(fn, reps, stream):
-    """Average duration of fn's launch, from HIP events recorded on its stream."""
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in evs:
-        a.record()
-        fn(stream)
-        b.record()
-    torch.cuda.synchronize()
-    return 1000.0 * sum(a.elapsed_time(b) for a, b in evs) / reps
-
-
 def cpu_baseline(host_layers, seconds):
     """The reference's CPU BitLinear (cpu.rs, restated with AVX2 intrinsics and a
     thread pool, oracle/) on a bounded sample: the 7 projections of 4 of the 32
@@ -172,13 +161,27 @@ def run_decode(args):
     ms = t0.elapsed_time(t1) / args.steps
     print("bench: %d graph replays, %.4f ms/step" % (args.steps, ms), file=sys.stderr, flush=True)
 
-    # per-kernel durations (HIP events on the launch stream), one launch per layer
+    # per-kernel durations: the 32 launches of one kind back to back in their
+    # own HIP graph, HIP events on the stream the kernels run on
     kern = {}
     for name in ("qkv", "o", "gate_up", "down"):
-        us = 0.0
-        for l in range(LAYERS):
-            us += event_time_us(calls[name][l], 1, stream)
-        us /= LAYERS
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(cap):
+            with torch.cuda.graph(g, stream=cap):
+                s2 = torch.cuda.current_stream().cuda_stream
+                for l in range(LAYERS):
+                    calls[name][l](s2)
+        torch.cuda.synchronize()
+        g.replay()
+        reps = 10
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / (reps * LAYERS)
         b = calls[name][0].bytes
         kern[name] = {"us": round(us, 2), "bytes": b, "GB_s": round(b / us / 1e3, 1),
                       "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
@@ -196,7 +199,7 @@ def run_decode(args):
                    "bytes_per_step": step_bytes,
                    "step_GB_s": round(step_bytes / ms / 1e6, 1),
                    "step_frac_hbm": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 3)},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv<XK_BF16,YK_BF16> gate|up 4096->2x14336",
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_dec<XK_BF16> gate|up 4096->2x14336 (W1.58-A8)",
                      "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom["frac_hbm"], "traffic": None,
                      "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"]},

@@ -249,20 +249,10 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             }
         }
         if (wv > 0) {
+            // defaults measured on MI355X (Llama-3-8B shapes): the fewest waves
+            // that hold a part in registers, one 16-row tile per wave
             int64_t kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
-            // tiles per wave: the most (fewest prologues per weight byte) that
-            // keeps `target` waves in flight and <= 16 wave-loads per lane
-            const int64_t steps = ceil_div(kpart, btl::kStepWeights);
-            const int64_t target = env_int("BTL_GEMV_DEC_WAVES", 6 * cus);
             int rt = 1;
-            for (int t = 4; t >= 1; t /= 2) {
-                int64_t blocks = 0;
-                for (int i = 0; i < count; ++i) blocks += ceil_div(layers[i].w->n, 16 * t);
-                if ((blocks * wv >= target && t * steps <= 16 && (steps <= 4 || t <= 2)) || t == 1) {
-                    rt = t;
-                    break;
-                }
-            }
             const int frt = env_int("BTL_GEMV_DEC_TILES", 0);
             if (frt == 1 || frt == 2 || frt == 4) rt = frt;
             const int fwv = env_int("BTL_GEMV_DEC_PARTS", 0);
