@@ -48,6 +48,26 @@ hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipS
 constexpr int kDecMaxPart = 2048;
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s);
 
+// Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op),
+// k % 64 == 0, 16-byte aligned q and w.
+struct GemmArgs {
+    const int8_t* q;   // [m, k] quantised activations, operand order
+    const float* sx;   // [m] activation scales
+    const uint8_t* w;  // packed [n, k/4]
+    float sw;
+    void* y;           // [m, n]
+    int32_t* acc_out;  // optional [m, n]
+    int m, n, k;
+    int ykind;
+    int tiles_n;       // ceil(n / 128)
+    int a_natural;     // 1: q is in natural k order (transposed while staged)
+    int bm;            // token rows per workgroup tile: 128 or 256
+};
+
+hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s);
+hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,
+                           hipStream_t st);
+
 hipError_t launch_quant_act(const void* x, int xkind, int64_t m, int64_t k, int8_t* q,
                             float* s, hipStream_t st);
 

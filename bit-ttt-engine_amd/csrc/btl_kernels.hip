@@ -13,6 +13,9 @@
 //   k_gemv_dec<XK,YK,WV>  the decode case (1..4 token rows): one 16-row tile
 //                     per workgroup, WV waves split K, activations quantised
 //                     per wave from registers loaded ahead of the weights.
+//   k_gemm_i8         prefill GEMM (many token rows): LDS-tiled int8 MFMA with
+//                     the packed weight tile unpacked per wave; k_quant_op
+//                     quantises the tokens ahead of it in operand order.
 //   k_quant_act<XK>   per-token absmax int8 quantisation, natural layout.
 //   k_ref_f32<XK,YK>  reference-semantics fp32 path: bit-identical to the
 //                     8-lane FMA order of cpu.rs.
@@ -703,6 +706,214 @@ hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipS
     BTL_GEMV_CASE(XK_I8, YK_BF16)
 #undef BTL_GEMV_CASE
     return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// k_quant_op: per-token quantisation into MFMA operand order (prefill)
+// ---------------------------------------------------------------------------
+// One workgroup per token row; the arithmetic of k_quant_act, but every group
+// of 16 consecutive k is stored in the operand k order [0,4,8,12, 1,5,9,13,
+// ...] that unpack16 gives the weights, so the GEMM copies it to LDS as is.
+template <int XK>
+__global__ __launch_bounds__(256) void k_quant_op(const void* x, int k, int8_t* q, float* s)
+{
+    __shared__ uint32_t s_w[4];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int groups = k >> 4;  // k % 16 == 0
+    constexpr int NV = XK == XK_F32 ? 4 : 2;
+    const uint4* xr = XK == XK_F32 ? (const uint4*)((const float*)x + row * k)
+                                   : (const uint4*)((const uint16_t*)x + row * k);
+    uint32_t amax = 0;
+    for (int g = tid; g < groups; g += 256) {
+        uint4 v[NV];
+#pragma unroll
+        for (int h = 0; h < NV; ++h) v[h] = xr[g * NV + h];
+        if (XK == XK_BF16) amax = max(amax, group_absmax<XK_BF16>(v));
+        else amax = max(amax, group_absmax<XK_F32>(v));
+    }
+    amax = wave_max_dpp(amax);
+    if ((tid & 63) == 0) s_w[tid >> 6] = amax;
+    __syncthreads();
+    amax = max(max(s_w[0], s_w[1]), max(s_w[2], s_w[3]));
+    const QParams qp = qparams(amax);
+    if (tid == 0) s[row] = qp.s;
+    uint4* qr = (uint4*)(q + row * k);
+    for (int g = tid; g < groups; g += 256) {
+        uint4 o = {0u, 0u, 0u, 0u};
+        if (qp.ok) {
+            uint4 v[NV];
+#pragma unroll
+            for (int h = 0; h < NV; ++h) v[h] = xr[g * NV + h];
+            o = XK == XK_BF16 ? group_quant<XK_BF16>(v, qp.r) : group_quant<XK_F32>(v, qp.r);
+        }
+        qr[g] = o;
+    }
+}
+
+hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,
+                           hipStream_t st)
+{
+    if (m <= 0) return hipSuccess;
+    if (xkind == XK_BF16) hipLaunchKernelGGL(k_quant_op<XK_BF16>, dim3((unsigned)m), dim3(256), 0, st, x, (int)k, q, s);
+    else hipLaunchKernelGGL(k_quant_op<XK_F32>, dim3((unsigned)m), dim3(256), 0, st, x, (int)k, q, s);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_gemm_i8: prefill GEMM, int8 activations x packed ternary weights
+// ---------------------------------------------------------------------------
+// Workgroup tile 256 (tokens) x 128 (output rows), K steps of 64; 4 waves in a
+// 2x2 grid, wave tile 128 x 64 = 8 x 4 blocks of v_mfma_i32_16x16x64_i8 with
+// the activations as A and the weights as B (D[m][n]).  Per K step the LDS
+// holds the int8 activation tile (BM x 64, operand order; 16-byte slot s of
+// row r stored at slot s ^ ((r >> 1) & 3), which makes the MFMA-operand reads
+// -- 16 rows x 4 slots per instruction -- bank-conflict free) and the packed
+// weight tile (128 rows x 16 bytes, stored word-major so lane c of a column
+// block reads word kq of column c without bank conflicts);
+// each wave unpacks only the 4 weight words it needs.  Both tiles are double
+// buffered: the global loads of step s+1 are in flight while step s computes,
+// one barrier per step.
+constexpr int kBN = 128, kBK = 64, kALd = kBK;  // A rows unpadded, 16-B slots swizzled
+constexpr int kGemmPF = 2;  // K steps of global loads in flight (register ring)
+constexpr int kBLd = kBN + 16;  // packed-weight LDS row pitch in words (bank spread)
+
+template <int NAT, int BM>
+__global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
+{
+    constexpr int kBM = BM;      // token rows per workgroup (128 or 256)
+    constexpr int WB = BM / 32;  // 16-row A blocks per wave (wave tile BM/2 x 64)
+    __shared__ __align__(16) uint8_t sA[2][kBM * kALd];
+    __shared__ __align__(16) uint32_t sB[2][4][kBLd];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    // consecutive workgroups go to consecutive XCDs: with tm = bid % tiles_m
+    // each XCD keeps re-reading the same activation row tile from its L2
+    const int tiles_m = (a.m + kBM - 1) / kBM;
+    const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
+    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int K = a.k;
+    const int rows_a = min(kBM, a.m - m0), rows_b = min(kBN, a.n - n0);
+    const __amdgpu_buffer_rsrc_t ra_rs = make_rsrc(a.q + (int64_t)m0 * K, (uint32_t)(rows_a * K));
+    const __amdgpu_buffer_rsrc_t rb_rs = make_rsrc(a.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
+    const int steps = K / kBK;
+
+    // global -> register ring: per K step A 4 x 16 B per thread, B 16 B for
+    // threads < 128; steps past K read zeros (descriptor range), no branches
+    constexpr int AL = kBM / 64;  // A loads (16 B) per thread per K step
+    uint4 ga[kGemmPF][AL], gb[kGemmPF];
+    const int arow = tid >> 2, aseg = (tid & 3) * 16;
+    const int aoff = arow * K + aseg, boff = tid < kBN ? tid * (K >> 2) : kOOB;
+    auto gload = [&](int slot, int st) {
+        const int ko = st < steps ? st * kBK : kOOB;
+#pragma unroll
+        for (int i = 0; i < AL; ++i) ga[slot][i] = bload(ra_rs, ko == kOOB ? kOOB : aoff + 64 * i * K + ko);
+        gb[slot] = bload(rb_rs, ko == kOOB || boff == kOOB ? kOOB : boff + (ko >> 2));
+    };
+    const int aswz = (((tid & 3) ^ ((arow >> 1) & 3)) * 16);  // 64*i keeps (row >> 1) & 3
+    auto lstore = [&](int slot, int buf) {
+#pragma unroll
+        for (int i = 0; i < AL; ++i)
+            *(uint4*)&sA[buf][(arow + 64 * i) * kALd + aswz] = NAT ? transpose16(ga[slot][i]) : ga[slot][i];
+        if (tid < kBN) {
+            sB[buf][0][tid] = gb[slot].x;
+            sB[buf][1][tid] = gb[slot].y;
+            sB[buf][2][tid] = gb[slot].z;
+            sB[buf][3][tid] = gb[slot].w;
+        }
+    };
+
+    v4i acc[WB][4];
+#pragma unroll
+    for (int b = 0; b < WB; ++b)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[b][c] = v4i{0, 0, 0, 0};
+
+    const int r16 = lane & 15, kq = lane >> 4;
+    auto compute = [&](int cur) {
+        v4i bop[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bop[c] = unpack16(sB[cur][kq][wn * 64 + c * 16 + r16]);
+        // row = wm*BM/2 + 16*b + r16, so (row >> 1) & 3 == (r16 >> 1) & 3
+        const uint8_t* abase = &sA[cur][(wm * (kBM / 2) + r16) * kALd + ((kq ^ ((r16 >> 1) & 3)) * 16)];
+#pragma unroll
+        for (int b = 0; b < WB; ++b) {
+            const v4i aop = *(const v4i*)(abase + b * 16 * kALd);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                acc[b][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop[c], acc[b][c], 0, 0, 0);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < kGemmPF; ++i) gload(i, i);
+    lstore(0, 0);
+    gload(0, kGemmPF);
+    __syncthreads();
+    // iteration st computes step st from LDS buffer st&1, stages step st+1
+    // (ring slot (st+1)%PF, loaded PF-1 iterations earlier) into the other
+    // buffer and refills that slot with step st+1+PF.  The main loop runs
+    // whole groups of PF steps without branches (slots stay static).
+    const int full = (steps - 1) / kGemmPF * kGemmPF;
+    for (int s0 = 0; s0 < full; s0 += kGemmPF) {
+#pragma unroll
+        for (int u = 0; u < kGemmPF; ++u) {
+            compute(u & 1);
+            lstore((u + 1) % kGemmPF, (u + 1) & 1);
+            gload((u + 1) % kGemmPF, s0 + u + 1 + kGemmPF);
+            __syncthreads();
+        }
+    }
+    // tail: steps full .. steps-1 (slot of step st is st % PF, buffer st & 1)
+    for (int st = full; st < steps; ++st) {
+        compute(st & 1);
+        if (st + 1 < steps) {
+#pragma unroll
+            for (int u = 0; u < kGemmPF; ++u)
+                if (u == (st + 1) % kGemmPF) lstore(u, (st + 1) & 1);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: y = (float)acc * (s_x[m] * s_w)
+    const bool ybf = a.ykind == YK_BF16;
+#pragma unroll
+    for (int b = 0; b < WB; ++b) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int m = m0 + wm * (kBM / 2) + b * 16 + 4 * kq + v;
+            if (m < a.m) {
+                const float cm = __fmul_rn(a.sx[m], a.sw);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int n = n0 + wn * 64 + c * 16 + r16;
+                    if (n < a.n) {
+                        const int64_t o = (int64_t)m * a.n + n;
+                        const float yv = __fmul_rn((float)acc[b][c][v], cm);
+                        if (ybf) ((uint16_t*)a.y)[o] = f32_to_bf16(yv);
+                        else ((float*)a.y)[o] = yv;
+                        if (a.acc_out) a.acc_out[o] = acc[b][c][v];
+                    }
+                }
+            }
+        }
+    }
+}
+
+hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
+{
+    const int bm = a.bm == 128 ? 128 : 256;
+    const int tiles_m = (a.m + bm - 1) / bm;
+    const dim3 grid((unsigned)(tiles_m * a.tiles_n));
+    if (bm == 128) {
+        if (a.a_natural) hipLaunchKernelGGL((k_gemm_i8<1, 128>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_i8<0, 128>), grid, dim3(256), 0, s, a);
+    } else {
+        if (a.a_natural) hipLaunchKernelGGL((k_gemm_i8<1, 256>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_i8<0, 256>), grid, dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
