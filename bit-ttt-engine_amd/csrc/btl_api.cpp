@@ -238,21 +238,21 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         cus = g_dev[dev].cus;
     }
 
-    // Prefill (many token rows): quantise once in operand order, then the
-    // LDS-tiled GEMM per layer.
-    if (m > env_int("BTL_GEMM_MIN_M", 64) && k % 64 == 0) {
-        const bool scratch = xkind != btl::XK_I8;
+    // Prefill (many token rows): quantise once in operand order (or reorder
+    // pre-quantised rows) into the workspace, then one GEMM per layer.
+    if (m > env_int("BTL_GEMM_MIN_M", 64) && k % 64 == 0 && k < (1 << 24)) {
         const WsLayout L = ws_layout(m, k);
         void* ws = nullptr;
-        const int8_t* q = (const int8_t*)x;
+        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
+        const int8_t* q = (const int8_t*)ws + L.q_off;
         const float* sxp = xs;
-        if (scratch) {
-            if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
-            q = (const int8_t*)ws + L.q_off;
+        if (xkind == btl::XK_I8) {
+            e = btl::launch_op_order((const int8_t*)x, m, k, (int8_t*)q, st);
+        } else {
             sxp = (const float*)((uint8_t*)ws + L.s_off);
             e = btl::launch_quant_op(x, xkind, m, k, (int8_t*)q, (float*)sxp, st);
-            if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
         }
+        if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
         for (int i = 0; i < count; ++i) {
             const int64_t n = layers[i].w->n;
             if (n == 0) continue;
@@ -268,18 +268,10 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             g.n = (int)n;
             g.k = (int)k;
             g.ykind = ykind;
-            g.tiles_n = (int)ceil_div(n, 128);
-            g.a_natural = scratch ? 0 : 1;
-            // 256-row tiles when they still give two workgroups per CU, else 128
-            const int64_t tiles256 = ceil_div(m, 256) * g.tiles_n;
-            g.bm = tiles256 >= 2 * cus ? 256 : 128;
-            const int fbm = env_int("BTL_GEMM_BM", 0);
-            if (fbm == 128 || fbm == 256) g.bm = fbm;
             e = btl::launch_gemm_i8(g, st);
             if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
         }
-        if (scratch && (e = btl::launch_fill_zero(ws, L.total, st)) != hipSuccess)
-            return hip_fail(e, "workspace clear");
+        if ((e = btl::launch_fill_zero(ws, L.total, st)) != hipSuccess) return hip_fail(e, "workspace clear");
         return BTL_OK;
     }
 

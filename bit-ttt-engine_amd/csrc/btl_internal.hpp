@@ -48,8 +48,8 @@ hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipS
 constexpr int kDecMaxPart = 2048;
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s);
 
-// Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op),
-// k % 64 == 0, 16-byte aligned q and w.
+// Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op or
+// k_op_order), k % 64 == 0, k < 2^24, 16-byte aligned q and w.
 struct GemmArgs {
     const int8_t* q;   // [m, k] quantised activations, operand order
     const float* sx;   // [m] activation scales
@@ -59,12 +59,11 @@ struct GemmArgs {
     int32_t* acc_out;  // optional [m, n]
     int m, n, k;
     int ykind;
-    int tiles_n;       // ceil(n / 128)
-    int a_natural;     // 1: q is in natural k order (transposed while staged)
-    int bm;            // token rows per workgroup tile: 128 or 256
 };
 
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s);
+// natural-order int8 rows -> operand order (k % 16 == 0, 16-byte aligned)
+hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, hipStream_t st);
 hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,
                            hipStream_t st);
 

@@ -13,9 +13,11 @@
 //   k_gemv_dec<XK,YK,WV>  the decode case (1..4 token rows): one 16-row tile
 //                     per workgroup, WV waves split K, activations quantised
 //                     per wave from registers loaded ahead of the weights.
-//   k_gemm_i8         prefill GEMM (many token rows): LDS-tiled int8 MFMA with
-//                     the packed weight tile unpacked per wave; k_quant_op
-//                     quantises the tokens ahead of it in operand order.
+//   k_gemm_i8         prefill GEMM (many token rows): int8 MFMA on 128x128
+//                     tiles fed by direct global->LDS copies, the packed
+//                     weight tile unpacked per wave; k_quant_op quantises the
+//                     tokens ahead of it in operand order (k_op_order
+//                     reorders pre-quantised ones).
 //   k_quant_act<XK>   per-token absmax int8 quantisation, natural layout.
 //   k_ref_f32<XK,YK>  reference-semantics fp32 path: bit-identical to the
 //                     8-lane FMA order of cpu.rs.
@@ -761,128 +763,145 @@ hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_
 }
 
 // ---------------------------------------------------------------------------
+// k_op_order: natural-order int8 activations -> operand order (prefill)
+// ---------------------------------------------------------------------------
+// Pre-quantised activations (btl_linear_i8) arrive with k in natural order;
+// the GEMM's LDS tile expects every 16-k group in unpack16's order.
+__global__ __launch_bounds__(256) void k_op_order(const uint4* q, uint4* out, int64_t groups)
+{
+    for (int64_t g = blockIdx.x * 256ll + threadIdx.x; g < groups; g += (int64_t)gridDim.x * 256)
+        out[g] = transpose16(q[g]);
+}
+
+hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, hipStream_t st)
+{
+    const int64_t groups = m * (k >> 4);  // k % 16 == 0
+    if (groups <= 0) return hipSuccess;
+    const int64_t blocks = groups / 256 + 1;
+    hipLaunchKernelGGL(k_op_order, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, st,
+                       (const uint4*)q, (uint4*)out, groups);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // k_gemm_i8: prefill GEMM, int8 activations x packed ternary weights
 // ---------------------------------------------------------------------------
-// Workgroup tile 256 (tokens) x 128 (output rows), K steps of 64; 4 waves in a
-// 2x2 grid, wave tile 128 x 64 = 8 x 4 blocks of v_mfma_i32_16x16x64_i8 with
-// the activations as A and the weights as B (D[m][n]).  Per K step the LDS
-// holds the int8 activation tile (BM x 64, operand order; 16-byte slot s of
-// row r stored at slot s ^ ((r >> 1) & 3), which makes the MFMA-operand reads
-// -- 16 rows x 4 slots per instruction -- bank-conflict free) and the packed
-// weight tile (128 rows x 16 bytes, stored word-major so lane c of a column
-// block reads word kq of column c without bank conflicts);
-// each wave unpacks only the 4 weight words it needs.  Both tiles are double
-// buffered: the global loads of step s+1 are in flight while step s computes,
-// one barrier per step.
-constexpr int kBN = 128, kBK = 64, kALd = kBK;  // A rows unpadded, 16-B slots swizzled
-constexpr int kGemmPF = 2;  // K steps of global loads in flight (register ring)
-constexpr int kBLd = kBN + 16;  // packed-weight LDS row pitch in words (bank spread)
+// Workgroup tile 128 (tokens) x 128 (output rows), K steps of 128; 4 waves in
+// a 2x2 grid, wave tile 64 x 64 = 4 x 4 blocks of v_mfma_i32_16x16x64_i8 with
+// the activations as A and the weights as B (D[m][n]).
+//
+// Global memory is copied straight into LDS by buffer_load_dwordx4 ... lds
+// (each lane's 16 bytes land at M0 + 16 * lane), so no register staging sits
+// between HBM/L2 and the matrix cores.  Two LDS stages of 20 KB: the copies of
+// step s+1 are issued right after the barrier that opens step s and have the
+// whole of step s to land.  One barrier per step; 40 KB of LDS and ~110 VGPRs
+// leave room for 3-4 workgroups per CU.
+//
+// Stage layout (the lane -> global mapping of the copies produces it):
+//   A [half j (k 64j..64j+63)][row 0..127][64 B]: 16-byte slot s of row r
+//     holds k group s ^ ((r >> 1) & 3), so the MFMA-operand reads (16 rows x
+//     4 slots per instruction) hit every bank once;
+//   B [half j][column 0..127][16 B]: the packed word kq of a column at byte
+//     4 kq, so a read of 16 columns x 4 words covers the 64 banks once.
+// Each wave unpacks the 4 weight words of its 64 columns per half step.
+constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 128;
+constexpr int kGemmABytes = kGemmBM * kGemmBK;      // 16 KB
+constexpr int kGemmBBytes = kGemmBN * kGemmBK / 4;  // 4 KB
+constexpr int kGemmStage = kGemmABytes + kGemmBBytes;
+constexpr int kGemmACh = kGemmABytes / 1024 / 4;    // A copies (1 KB) per wave per step
 
-template <int NAT, int BM>
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane, global (descriptor r, byte offset voff) -> LDS lds + 16 * lane.
+// Offsets outside the descriptor range read as zero.
+__device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int voff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): every global load (and LDS copy) of this wave has landed.
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
 {
-    constexpr int kBM = BM;      // token rows per workgroup (128 or 256)
-    constexpr int WB = BM / 32;  // 16-row A blocks per wave (wave tile BM/2 x 64)
-    __shared__ __align__(16) uint8_t sA[2][kBM * kALd];
-    __shared__ __align__(16) uint32_t sB[2][4][kBLd];
+    __shared__ __align__(1024) uint8_t lds[2 * kGemmStage];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     // consecutive workgroups go to consecutive XCDs: with tm = bid % tiles_m
-    // each XCD keeps re-reading the same activation row tile from its L2
-    const int tiles_m = (a.m + kBM - 1) / kBM;
+    // each XCD keeps re-reading the same activation row tiles from its L2
+    const int tiles_m = (a.m + kGemmBM - 1) / kGemmBM;
     const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
-    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
     const int K = a.k;
-    const int rows_a = min(kBM, a.m - m0), rows_b = min(kBN, a.n - n0);
-    const __amdgpu_buffer_rsrc_t ra_rs = make_rsrc(a.q + (int64_t)m0 * K, (uint32_t)(rows_a * K));
-    const __amdgpu_buffer_rsrc_t rb_rs = make_rsrc(a.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
-    const int steps = K / kBK;
+    const int rows_a = min(kGemmBM, a.m - m0), rows_b = min(kGemmBN, a.n - n0);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.q + (int64_t)m0 * K, (uint32_t)(rows_a * K));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
+    const int steps = (K + kGemmBK - 1) / kGemmBK;
 
-    // global -> register ring: per K step A 4 x 16 B per thread, B 16 B for
-    // threads < 128; steps past K read zeros (descriptor range), no branches
-    constexpr int AL = kBM / 64;  // A loads (16 B) per thread per K step
-    uint4 ga[kGemmPF][AL], gb[kGemmPF];
-    const int arow = tid >> 2, aseg = (tid & 3) * 16;
-    const int aoff = arow * K + aseg, boff = tid < kBN ? tid * (K >> 2) : kOOB;
-    auto gload = [&](int slot, int st) {
-        const int ko = st < steps ? st * kBK : kOOB;
+    // source offsets (relative to the step's first k) of this wave's copies:
+    // A chunk c = 16 rows x 64 B of half j; lane -> (row, slot) as laid out above
+    int aoff[kGemmACh];
 #pragma unroll
-        for (int i = 0; i < AL; ++i) ga[slot][i] = bload(ra_rs, ko == kOOB ? kOOB : aoff + 64 * i * K + ko);
-        gb[slot] = bload(rb_rs, ko == kOOB || boff == kOOB ? kOOB : boff + (ko >> 2));
-    };
-    const int aswz = (((tid & 3) ^ ((arow >> 1) & 3)) * 16);  // 64*i keeps (row >> 1) & 3
-    auto lstore = [&](int slot, int buf) {
+    for (int i = 0; i < kGemmACh; ++i) {
+        const int c = wave * kGemmACh + i;
+        const int j = c / (kGemmBM / 16), row = (c % (kGemmBM / 16)) * 16 + (lane >> 2);
+        const int grp = (lane & 3) ^ ((row >> 1) & 3);
+        aoff[i] = row * K + j * 64 + grp * 16;
+    }
+    // B: wave w fills half w / 2, columns 64 (w % 2) + lane
+    const int boff = ((wave & 1) * 64 + lane) * (K >> 2) + (wave >> 1) * 16;
+
+    auto issue = [&](int st, int stage) {
+        const int ko = st * kGemmBK;
+        uint8_t* base = lds + stage * kGemmStage;
 #pragma unroll
-        for (int i = 0; i < AL; ++i)
-            *(uint4*)&sA[buf][(arow + 64 * i) * kALd + aswz] = NAT ? transpose16(ga[slot][i]) : ga[slot][i];
-        if (tid < kBN) {
-            sB[buf][0][tid] = gb[slot].x;
-            sB[buf][1][tid] = gb[slot].y;
-            sB[buf][2][tid] = gb[slot].z;
-            sB[buf][3][tid] = gb[slot].w;
-        }
+        for (int i = 0; i < kGemmACh; ++i) copy_to_lds(ra, base + (wave * kGemmACh + i) * 1024, aoff[i] + ko);
+        copy_to_lds(rb, base + kGemmABytes + wave * 1024, boff + (ko >> 2));
     };
 
-    v4i acc[WB][4];
+    v4i acc[4][4];
 #pragma unroll
-    for (int b = 0; b < WB; ++b)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[b][c] = v4i{0, 0, 0, 0};
 
     const int r16 = lane & 15, kq = lane >> 4;
-    auto compute = [&](int cur) {
+    // row = 64 wm + 16 b + r16, so (row >> 1) & 3 == (r16 >> 1) & 3
+    const int aread = (wm * 64 + r16) * 64 + ((kq ^ ((r16 >> 1) & 3)) * 16);
+    const int bread = kGemmABytes + (wn * 64 + r16) * 16 + kq * 4;
+    auto compute_half = [&](const uint8_t* base, int j) {
         v4i bop[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) bop[c] = unpack16(sB[cur][kq][wn * 64 + c * 16 + r16]);
-        // row = wm*BM/2 + 16*b + r16, so (row >> 1) & 3 == (r16 >> 1) & 3
-        const uint8_t* abase = &sA[cur][(wm * (kBM / 2) + r16) * kALd + ((kq ^ ((r16 >> 1) & 3)) * 16)];
+        for (int c = 0; c < 4; ++c) bop[c] = unpack16(*(const uint32_t*)(base + bread + j * 2048 + c * 256));
+        const uint8_t* ab = base + j * (kGemmBM * 64) + aread;
 #pragma unroll
-        for (int b = 0; b < WB; ++b) {
-            const v4i aop = *(const v4i*)(abase + b * 16 * kALd);
+        for (int b = 0; b < 4; ++b) {
+            const v4i aop = *(const v4i*)(ab + b * 1024);
 #pragma unroll
             for (int c = 0; c < 4; ++c)
                 acc[b][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop[c], acc[b][c], 0, 0, 0);
         }
     };
 
-#pragma unroll
-    for (int i = 0; i < kGemmPF; ++i) gload(i, i);
-    lstore(0, 0);
-    gload(0, kGemmPF);
-    __syncthreads();
-    // iteration st computes step st from LDS buffer st&1, stages step st+1
-    // (ring slot (st+1)%PF, loaded PF-1 iterations earlier) into the other
-    // buffer and refills that slot with step st+1+PF.  The main loop runs
-    // whole groups of PF steps without branches (slots stay static).
-    const int full = (steps - 1) / kGemmPF * kGemmPF;
-    for (int s0 = 0; s0 < full; s0 += kGemmPF) {
-#pragma unroll
-        for (int u = 0; u < kGemmPF; ++u) {
-            compute(u & 1);
-            lstore((u + 1) % kGemmPF, (u + 1) & 1);
-            gload((u + 1) % kGemmPF, s0 + u + 1 + kGemmPF);
-            __syncthreads();
-        }
-    }
-    // tail: steps full .. steps-1 (slot of step st is st % PF, buffer st & 1)
-    for (int st = full; st < steps; ++st) {
-        compute(st & 1);
-        if (st + 1 < steps) {
-#pragma unroll
-            for (int u = 0; u < kGemmPF; ++u)
-                if (u == (st + 1) % kGemmPF) lstore(u, (st + 1) & 1);
-        }
-        __syncthreads();
+    issue(0, 0);
+    for (int st = 0; st < steps; ++st) {
+        wait_loads();     // this wave's copies of step st are in LDS
+        __syncthreads();  // ... every wave's; and stage (st+1)&1 is no longer read
+        if (st + 1 < steps) issue(st + 1, (st + 1) & 1);
+        const uint8_t* base = lds + (st & 1) * kGemmStage;
+        compute_half(base, 0);
+        if (st * kGemmBK + 64 < K) compute_half(base, 1);  // k % 128 == 64: last step is half
     }
 
     // epilogue: y = (float)acc * (s_x[m] * s_w)
     const bool ybf = a.ykind == YK_BF16;
 #pragma unroll
-    for (int b = 0; b < WB; ++b) {
+    for (int b = 0; b < 4; ++b) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int m = m0 + wm * (kBM / 2) + b * 16 + 4 * kq + v;
+            const int m = m0 + wm * 64 + b * 16 + 4 * kq + v;
             if (m < a.m) {
                 const float cm = __fmul_rn(a.sx[m], a.sw);
 #pragma unroll
@@ -903,16 +922,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
 
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
 {
-    const int bm = a.bm == 128 ? 128 : 256;
-    const int tiles_m = (a.m + bm - 1) / bm;
-    const dim3 grid((unsigned)(tiles_m * a.tiles_n));
-    if (bm == 128) {
-        if (a.a_natural) hipLaunchKernelGGL((k_gemm_i8<1, 128>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_i8<0, 128>), grid, dim3(256), 0, s, a);
-    } else {
-        if (a.a_natural) hipLaunchKernelGGL((k_gemm_i8<1, 256>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_i8<0, 256>), grid, dim3(256), 0, s, a);
-    }
+    const int64_t tiles = (int64_t)((a.m + kGemmBM - 1) / kGemmBM) * ((a.n + kGemmBN - 1) / kGemmBN);
+    if (tiles <= 0) return hipSuccess;
+    if (tiles > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gemm_i8, dim3((unsigned)tiles), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

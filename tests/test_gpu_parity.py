@@ -286,7 +286,9 @@ def test_shape_mismatch_raises_on_gpu():
 
 # --- prefill GEMM (many token rows) -------------------------------------------------
 
-GEMM_SHAPES = [(65, 64, 100), (300, 320, 128), (129, 4096, 1000), (257, 1024, 130)]
+# k % 128 == 64 (a half last K step), ragged token / output tiles, exact tiles, long k
+GEMM_SHAPES = [(65, 64, 100), (300, 320, 128), (129, 4096, 1000), (257, 1024, 130),
+               (300, 1088, 257), (128, 192, 128), (131, 14336, 64)]
 
 
 @pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
@@ -307,10 +309,10 @@ def test_gemm_matches_oracle(m, k, n, xdt, ydt):
         assert_bf16_matches(y, yr)
 
 
-def test_gemm_prequantized_natural_layout():
+@pytest.mark.parametrize("m,k,n", [(200, 512, 96), (130, 1088, 200)])
+def test_gemm_prequantized_natural_layout(m, k, n):
     # btl_linear_i8 hands the GEMM natural-order int8 rows
-    m, k, n = 200, 512, 96
-    x = to_dev(activations(m, k, seed=21), torch.bfloat16)
+    x = to_dev(activations(m, k, seed=21 + k), torch.bfloat16)
     pt, wb, sw = make_layer(n, k, seed=22)
     q, s = bl.quantize_act(x)
     acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
