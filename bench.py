@@ -12,8 +12,10 @@ bf16 activations N(0,1) with 0.1% outliers at +-20 in, bf16 out, W1.58-A8 arithm
 (per-token absmax int8 activations, exact int32 accumulation).  One step = one token
 through all 32 layers (224 projections, 128 launches) replayed from a HIP graph.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
-    python bench.py --config prefill|sweep   (secondary workloads, own JSON line)
+The same line carries a "prefill" section (cfg4, M=2048 on the same 32 layers, its own
+int8-MFMA roofline).
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-prefill]
 """
 import argparse
 import json
@@ -53,12 +55,12 @@ def synth_packed(n, k, gen, device):
 
 
 def synth_act(m, k, gen, device):
+    """N(0,1) bf16 activations with 0.1% of each row set to +-20."""
     x = torch.randn((m, k), device=device, generator=gen, dtype=torch.float32)
     cnt = int(np.ceil(0.001 * k))
-    for i in range(m):
-        pos = torch.randperm(k, device=device, generator=gen)[:cnt]
-        sign = torch.where(torch.rand(cnt, device=device, generator=gen) < 0.5, -20.0, 20.0)
-        x[i, pos] = sign
+    pos = torch.rand((m, k), device=device, generator=gen).topk(cnt, dim=1).indices
+    sign = torch.where(torch.rand((m, cnt), device=device, generator=gen) < 0.5, -20.0, 20.0)
+    x.scatter_(1, pos, sign)
     return x.to(torch.bfloat16)
 
 
@@ -80,6 +82,42 @@ class Call:
     def __call__(self, stream):
         bl.check(bl.lib.btl_linear_group(self.arr, self.ys, self.n, self.x.data_ptr(), bl.BTL_BF16,
                                          self.m, self.k, bl.BTL_BF16, None, 0, stream))
+
+
+class OpCall:
+    """A pre-bound btl_linear_i8_op call: the prefill GEMM alone (one launch for the
+    layers of a group) on operand-order int8 activations."""
+
+    def __init__(self, layers, q, s, outs):
+        import ctypes
+        self.cs = [l.as_c() for l in layers]
+        self.n = len(layers)
+        self.arr = (ctypes.POINTER(bl.BtlPacked) * self.n)(*[ctypes.pointer(c) for c in self.cs])
+        self.ys = (ctypes.c_void_p * self.n)(*[o.data_ptr() for o in outs])
+        self.q, self.s = q, s
+        self.m, self.k = q.shape
+        self.ns = [l.dims2()[0] for l in layers]
+        self.ops = 2.0 * self.m * self.k * sum(self.ns)
+
+    def __call__(self, stream):
+        bl.check(bl.lib.btl_linear_i8_op(self.arr, self.ys, None, self.n, self.q.data_ptr(), self.s.data_ptr(),
+                                         self.m, self.k, bl.BTL_BF16, stream))
+
+
+def time_launches(fn, reps, stream_obj):
+    """Average µs of `fn(stream)` over `reps` back-to-back launches, HIP events
+    recorded on the stream the kernels run on."""
+    with torch.cuda.stream(stream_obj):
+        s = stream_obj.cuda_stream
+        fn(s)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream_obj)
+        for _ in range(reps):
+            fn(s)
+        e1.record(stream_obj)
+    torch.cuda.synchronize()
+    return 1000.0 * e0.elapsed_time(e1) / reps
 
 
 def cpu_baseline(host_layers, seconds):
@@ -205,6 +243,8 @@ def run_decode(args):
                      "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"]},
         "kernels": kern,
     }
+    if args.prefill:
+        result["prefill"] = run_prefill(layers, gen, dev, args)
     if args.cpu_baseline:
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         host = []
@@ -217,6 +257,86 @@ def run_decode(args):
     print(json.dumps(result), flush=True)
 
 
+def run_prefill(layers, gen, dev, args):
+    """cfg4: M=2048 prefill on the seven Llama-3-8B projection shapes, the same 32
+    layers of weights.  One step = the 7 projections of all 32 layers as a decoder
+    issues them (btl_linear_group q|k|v, btl_linear o, btl_linear_group gate|up,
+    btl_linear down: each quantises its bf16 input, then the GEMM), HIP graph.
+    Per kernel kind: the GEMM alone (btl_linear_i8_op) and the quantiser alone."""
+    M = args.prefill_m
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    xh = synth_act(M, HIDDEN, gen, dev)
+    xi = synth_act(M, INTER, gen, dev)
+    groups = {"qkv": ("q", "k", "v"), "o": ("o",), "gate_up": ("gate", "up"), "down": ("down",)}
+    outs = {g: [torch.empty((M, layers[0][nm].dims2()[0]), **bf) for nm in names] for g, names in groups.items()}
+    calls = []
+    for L in layers:
+        for g, names in groups.items():
+            calls.append(Call([L[nm] for nm in names], xi if g == "down" else xh, outs[g]))
+    stream = torch.cuda.current_stream().cuda_stream
+    for c in calls[:4]:  # sizes the library workspace before capture
+        c(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            s = torch.cuda.current_stream().cuda_stream
+            for c in calls:
+                c(s)
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup // 2)):
+        graph.replay()
+    torch.cuda.synchronize()
+    psteps = max(2, args.steps // 10)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(psteps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / psteps
+    print("bench: prefill M=%d, %d graph replays, %.3f ms/step" % (M, psteps, ms), file=sys.stderr, flush=True)
+
+    # the GEMM alone per kind (layer 0's weights; operand-order activations)
+    qh, sh = bl.quantize_act_op(xh)
+    qi, si = bl.quantize_act_op(xi)
+    kern = {}
+    for g, names in groups.items():
+        oc = OpCall([layers[0][nm] for nm in names], qi if g == "down" else qh,
+                    si if g == "down" else sh, outs[g])
+        us = time_launches(oc, 20, cap)
+        kern[g] = {"us": round(us, 2), "TOPS": round(oc.ops / us / 1e6, 1),
+                   "frac_int8": round(oc.ops / us / 1e6 / INT8_PEAK_TOPS, 3), "ops": oc.ops,
+                   "n": oc.ns, "k": oc.k}
+    for name, x in (("quant_op_k4096", xh), ("quant_op_k14336", xi)):
+        qq, ss = (qh, sh) if x is xh else (qi, si)
+        fn = lambda st, x=x, qq=qq, ss=ss: bl.check(bl.lib.btl_quantize_act_op(
+            x.data_ptr(), bl.BTL_BF16, M, x.shape[1], qq.data_ptr(), ss.data_ptr(), st))
+        us = time_launches(fn, 20, cap)
+        b = x.numel() * 2 + qq.numel() + ss.numel() * 4
+        kern[name] = {"us": round(us, 2), "bytes": b, "GB_s": round(b / us / 1e3, 1),
+                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+    gemm_us = sum(kern[g]["us"] for g in groups)
+    layer_ops = sum(kern[g]["ops"] for g in groups)
+    dom = kern["gate_up"]
+    return {
+        "workload": "cfg4: Llama-3-8B prefill, M=%d tokens, 7 projections x 32 layers as 4 calls per "
+                    "layer (q|k|v and gate|up grouped), bf16 in/out, W1.58-A8" % M,
+        "value": round(M / ms * 1000.0, 1), "unit": "tok/s", "ms_per_step": round(ms, 3),
+        "step_TOPS": round(LAYERS * layer_ops / ms / 1e9, 1),
+        "step_frac_int8": round(LAYERS * layer_ops / ms / 1e9 / INT8_PEAK_TOPS, 3),
+        "gemm_only_layer_us": round(gemm_us, 2),
+        "gemm_only_frac_int8": round(layer_ops / gemm_us / 1e6 / INT8_PEAK_TOPS, 3),
+        "roofline": {"bound": "mfma", "kernel": "k_gemm_i8 gate|up 2048 x (2 x 14336) x 4096, one launch",
+                     "achieved": dom["TOPS"], "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": dom["frac_int8"], "traffic": None, "algorithmic_ops": dom["ops"],
+                     "avg_us": dom["us"]},
+        "kernels": kern,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -224,6 +344,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="decode", choices=["decode"])
     ap.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    ap.add_argument("--no-prefill", dest="prefill", action="store_false",
+                    help="skip the cfg4 prefill section of the JSON line")
+    ap.add_argument("--prefill-m", type=int, default=2048)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:

@@ -18,5 +18,6 @@ from ._lib import (  # noqa: F401
 )
 from .packed import PackedTensor  # noqa: F401
 from .layer import (  # noqa: F401
-    BitLinear, BitLinearHip, Workspace, linear_group, linear_i8, quantize_act,
+    BitLinear, BitLinearHip, Workspace, linear_group, linear_i8, linear_i8_op, quantize_act,
+    quantize_act_op,
 )

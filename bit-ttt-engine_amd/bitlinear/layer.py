@@ -34,7 +34,8 @@ def _on_gpu(t, what):
 
 
 class Workspace:
-    """A caller-owned workspace for btl_linear* (zeroed once at creation)."""
+    """A caller-owned workspace for btl_linear* (zeroed once at creation; the calls
+    do not rely on its contents)."""
 
     def __init__(self, m, n, k, device="cuda", mode=BTL_ACT_I8):
         self.nbytes = int(lib.btl_workspace_bytes(m, n, k, mode))
@@ -109,6 +110,37 @@ def linear_i8(q, s, weights, out_dtype=torch.float32, acc_out=None, workspace=No
                             _dtype_code(y, "output"), acc_out.data_ptr() if acc_out is not None else None,
                             wsp, wsn, _stream(q.device)))
     return y
+
+
+def quantize_act_op(x):
+    """btl_quantize_act_op: (q int8 [M, K] in operand order, s float32 [M])."""
+    _on_gpu(x, "input")
+    m, k = x.shape
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    check(lib.btl_quantize_act_op(x.data_ptr() if x.numel() else None, _dtype_code(x, "input"), m, k,
+                                  q.data_ptr() if q.numel() else None, s.data_ptr() if m else None,
+                                  _stream(x.device)))
+    return q, s
+
+
+def linear_i8_op(q, s, weights, out_dtype=torch.float32, acc_out=None, outputs=None):
+    """btl_linear_i8_op: the prefill GEMM on operand-order activations, one launch
+    for the list of layers `weights` (1..4).  Returns the list of outputs."""
+    _on_gpu(q, "input")
+    m, k = q.shape
+    if outputs is None:
+        outputs = [torch.empty((m, w.dims2()[0]), dtype=out_dtype, device=q.device) for w in weights]
+    cs = [w.as_c() for w in weights]
+    arr = (ctypes.POINTER(BtlPacked) * len(cs))(*[ctypes.pointer(c) for c in cs])
+    ys = (ctypes.c_void_p * len(cs))(*[o.data_ptr() if o.numel() else None for o in outputs])
+    accs = None
+    if acc_out is not None:
+        accs = (ctypes.c_void_p * len(cs))(*[a.data_ptr() if a is not None else None for a in acc_out])
+    check(lib.btl_linear_i8_op(arr, ys, accs, len(cs), q.data_ptr() if q.numel() else None,
+                               s.data_ptr() if s.numel() else None, m, k, _dtype_code(outputs[0], "output"),
+                               _stream(q.device)))
+    return outputs
 
 
 def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None):

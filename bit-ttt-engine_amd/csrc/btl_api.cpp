@@ -45,7 +45,7 @@ struct DeviceState {
     bool ok = false;
     int cus = 0;
     std::string arch;
-    void* ws = nullptr;  // library-owned workspace (zero outside calls)
+    void* ws = nullptr;  // library-owned workspace
     size_t ws_bytes = 0;
 };
 
@@ -93,10 +93,10 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Workspace contract: every byte is zero between calls.  A call that needs
-// scratch (the int8 activations + scales, when it quantises once for several
-// token tiles or for the generic path) zeroes it with a fill kernel queued
-// after the kernels that read it, so one workspace serves calls of any shapes.
+// Workspace: scratch for the int8 activations + scales when a call quantises
+// once for several token tiles (GEMM, multi-tile GEMV, generic path).  Every
+// kernel writes the scratch it reads in the same call, so its contents between
+// calls do not matter and one workspace serves calls of any shapes.
 struct WsLayout {
     size_t q_off, s_off, total;
 };
@@ -189,6 +189,29 @@ int64_t gemv_mrows(int64_t m, int64_t k)
     return r * (k + 16) <= btl::kGemvLdsMax ? r : 0;
 }
 
+// One k_gemm_i8 launch over the layers of a group (operand-order q).
+hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const float* sx, int64_t m,
+                       int64_t k, int ykind, hipStream_t st)
+{
+    btl::GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.q = q;
+    g.sx = sx;
+    g.m = (int)m;
+    g.k = (int)k;
+    g.ykind = ykind;
+    for (int i = 0; i < count; ++i) {
+        if (layers[i].w->n == 0) continue;
+        btl::GemmLayer& L = g.L[g.nl++];
+        L.w = layers[i].w->data;
+        L.sw = layers[i].w->scale;
+        L.n = (int)layers[i].w->n;
+        L.y = layers[i].y;
+        L.acc_out = layers[i].acc;
+    }
+    return g.nl ? btl::launch_gemm_i8(g, st) : hipSuccess;
+}
+
 // W1.58-A8 contraction of `count` layers sharing one input.
 int run_i8(const Layer* layers, int count, const void* x, int xkind, const float* xs, int64_t m,
            int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st)
@@ -227,8 +250,6 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
                                        layers[i].y, ykind, layers[i].acc, st);
             if (e != hipSuccess) return hip_fail(e, "generic int8 kernel launch");
         }
-        if (scratch && (e = btl::launch_fill_zero(ws, L.total, st)) != hipSuccess)
-            return hip_fail(e, "workspace clear");
         return BTL_OK;
     }
 
@@ -253,25 +274,8 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             e = btl::launch_quant_op(x, xkind, m, k, (int8_t*)q, (float*)sxp, st);
         }
         if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
-        for (int i = 0; i < count; ++i) {
-            const int64_t n = layers[i].w->n;
-            if (n == 0) continue;
-            btl::GemmArgs g;
-            memset(&g, 0, sizeof(g));
-            g.q = q;
-            g.sx = sxp;
-            g.w = layers[i].w->data;
-            g.sw = layers[i].w->scale;
-            g.y = layers[i].y;
-            g.acc_out = layers[i].acc;
-            g.m = (int)m;
-            g.n = (int)n;
-            g.k = (int)k;
-            g.ykind = ykind;
-            e = btl::launch_gemm_i8(g, st);
-            if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
-        }
-        if ((e = btl::launch_fill_zero(ws, L.total, st)) != hipSuccess) return hip_fail(e, "workspace clear");
+        e = launch_gemm(layers, count, q, sxp, m, k, ykind, st);
+        if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
         return BTL_OK;
     }
 
@@ -391,8 +395,6 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     a.mrows = (int)mrows;
     e = btl::launch_gemv(a, xkind, ykind, (int)mtiles, st);
     if (e != hipSuccess) return hip_fail(e, "gemv kernel launch");
-    if (scratch && (e = btl::launch_fill_zero(ws, L.total, st)) != hipSuccess)
-        return hip_fail(e, "workspace clear");
     return BTL_OK;
 }
 
@@ -564,6 +566,58 @@ int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, co
     }
     return run_i8(ls, count, x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k,
                   ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int btl_quantize_act_op(const void* x, int xdtype, int64_t m, int64_t k, int8_t* xq, float* xscale,
+                        void* stream)
+{
+    int rc = check_dtype(xdtype, "input");
+    if (rc) return rc;
+    if (m < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    if (k % 64 != 0 || k >= (1 << 24))
+        return fail(BTL_ERR_SHAPE, "operand-order layout needs k %% 64 == 0 and k < 2^24, got k = %lld",
+                    (long long)k);
+    if (m > INT32_MAX) return fail(BTL_ERR_SHAPE, "dimension exceeds 2^31-1");
+    if (m == 0 || k == 0) return BTL_OK;
+    if (!x || !xq || !xscale) return fail(BTL_ERR_LAYOUT, "null pointer");
+    if (!aligned16(x) || !aligned16(xq)) return fail(BTL_ERR_LAYOUT, "x and xq must be 16-byte aligned");
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    hipError_t e = btl::launch_quant_op(x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, m, k, xq, xscale,
+                                        (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
+    return BTL_OK;
+}
+
+int btl_linear_i8_op(const btl_packed_t* const* w, void* const* y, int32_t* const* acc_out, int count,
+                     const int8_t* xq, const float* xscale, int64_t m, int64_t k, int ydtype, void* stream)
+{
+    if (count < 1 || count > btl::kMaxGroup) return fail(BTL_ERR_ARG, "count %d not in 1..%d", count, btl::kMaxGroup);
+    if (!w || !y) return fail(BTL_ERR_ARG, "null layer array");
+    int rc;
+    if ((rc = check_dtype(ydtype, "output"))) return rc;
+    Layer ls[btl::kMaxGroup];
+    int64_t nsum = 0;
+    for (int i = 0; i < count; ++i) {
+        if ((rc = check_packed(w[i], m, k))) return rc;
+        if (!y[i] && m > 0 && w[i]->n > 0) return fail(BTL_ERR_LAYOUT, "null output %d", i);
+        if (w[i]->n > 0 && k > 0 && !aligned16(w[i]->data))
+            return fail(BTL_ERR_LAYOUT, "packed weights %d must be 16-byte aligned", i);
+        ls[i] = Layer{w[i], y[i], acc_out ? acc_out[i] : nullptr};
+        nsum += w[i]->n;
+    }
+    if (k % 64 != 0 || k >= (1 << 24))
+        return fail(BTL_ERR_SHAPE, "operand-order layout needs k %% 64 == 0 and k < 2^24, got k = %lld",
+                    (long long)k);
+    if (m == 0 || nsum == 0) return BTL_OK;
+    if (k > 0 && (!xq || !xscale)) return fail(BTL_ERR_LAYOUT, "null input");
+    if (!aligned16(xq)) return fail(BTL_ERR_LAYOUT, "xq must be 16-byte aligned");
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    hipError_t e = launch_gemm(ls, count, xq, xscale, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32,
+                               (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
+    return BTL_OK;
 }
 
 size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)

@@ -49,15 +49,22 @@ constexpr int kDecMaxPart = 2048;
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s);
 
 // Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op or
-// k_op_order), k % 64 == 0, k < 2^24, 16-byte aligned q and w.
+// k_op_order), k % 64 == 0, k < 2^24, 16-byte aligned q and w.  Up to
+// kMaxGroup layers that share q run in one launch.
+struct GemmLayer {
+    const uint8_t* w;  // packed [n, k/4]
+    float sw;
+    int n;
+    void* y;           // [m, n]
+    int32_t* acc_out;  // optional [m, n]
+    int tile0;         // first output tile of this layer (set by launch_gemm_i8)
+};
 struct GemmArgs {
     const int8_t* q;   // [m, k] quantised activations, operand order
     const float* sx;   // [m] activation scales
-    const uint8_t* w;  // packed [n, k/4]
-    float sw;
-    void* y;           // [m, n]
-    int32_t* acc_out;  // optional [m, n]
-    int m, n, k;
+    GemmLayer L[kMaxGroup];
+    int nl;
+    int m, k;
     int ykind;
 };
 

@@ -832,12 +832,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
     // consecutive workgroups go to consecutive XCDs: with tm = bid % tiles_m
     // each XCD keeps re-reading the same activation row tiles from its L2
     const int tiles_m = (a.m + kGemmBM - 1) / kGemmBM;
-    const int tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
+    const int tm = blockIdx.x % tiles_m;
+    int tn = blockIdx.x / tiles_m;
+    // the layers of a group share the activations: output tiles are numbered
+    // across them (layer l owns tiles tile0[l] .. tile0[l+1]-1)
+    GemmLayer Lw = a.L[0];
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i)
+        if (i < a.nl && tn >= a.L[i].tile0) Lw = a.L[i];
+    tn -= Lw.tile0;
     const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
-    const int K = a.k;
-    const int rows_a = min(kGemmBM, a.m - m0), rows_b = min(kGemmBN, a.n - n0);
+    const int K = a.k, N = Lw.n;
+    const int rows_a = min(kGemmBM, a.m - m0), rows_b = min(kGemmBN, N - n0);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.q + (int64_t)m0 * K, (uint32_t)(rows_a * K));
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Lw.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
     const int steps = (K + kGemmBK - 1) / kGemmBK;
 
     // source offsets (relative to the step's first k) of this wave's copies:
@@ -903,16 +911,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
         for (int v = 0; v < 4; ++v) {
             const int m = m0 + wm * 64 + b * 16 + 4 * kq + v;
             if (m < a.m) {
-                const float cm = __fmul_rn(a.sx[m], a.sw);
+                const float cm = __fmul_rn(a.sx[m], Lw.sw);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const int n = n0 + wn * 64 + c * 16 + r16;
-                    if (n < a.n) {
-                        const int64_t o = (int64_t)m * a.n + n;
+                    if (n < N) {
+                        const int64_t o = (int64_t)m * N + n;
                         const float yv = __fmul_rn((float)acc[b][c][v], cm);
-                        if (ybf) ((uint16_t*)a.y)[o] = f32_to_bf16(yv);
-                        else ((float*)a.y)[o] = yv;
-                        if (a.acc_out) a.acc_out[o] = acc[b][c][v];
+                        if (ybf) ((uint16_t*)Lw.y)[o] = f32_to_bf16(yv);
+                        else ((float*)Lw.y)[o] = yv;
+                        if (Lw.acc_out) Lw.acc_out[o] = acc[b][c][v];
                     }
                 }
             }
@@ -922,10 +930,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
 
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
 {
-    const int64_t tiles = (int64_t)((a.m + kGemmBM - 1) / kGemmBM) * ((a.n + kGemmBN - 1) / kGemmBN);
+    // tile0 of every layer is filled in here from the layers' n
+    GemmArgs g = a;
+    int64_t tn = 0;
+    for (int l = 0; l < g.nl; ++l) {
+        g.L[l].tile0 = (int)tn;
+        tn += (g.L[l].n + kGemmBN - 1) / kGemmBN;
+    }
+    const int64_t tiles = (int64_t)((g.m + kGemmBM - 1) / kGemmBM) * tn;
     if (tiles <= 0) return hipSuccess;
-    if (tiles > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_i8, dim3((unsigned)tiles), dim3(256), 0, s, a);
+    if (tiles > INT32_MAX || g.nl < 1 || g.nl > kMaxGroup) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gemm_i8, dim3((unsigned)tiles), dim3(256), 0, s, g);
     return hipGetLastError();
 }
 

@@ -26,8 +26,8 @@
  *    device function is asynchronous with respect to the host and stream ordered.
  *  - Nothing here allocates or frees caller memory.  Functions that take a
  *    workspace accept ws == NULL, in which case the library uses a per-device
- *    workspace it owns (allocated and grown with hipMalloc, zeroed once;
- *    calls that share it must be ordered on one stream).
+ *    workspace it owns (allocated and grown with hipMalloc; calls that share
+ *    it must be ordered on one stream).
  *  - Functions are reentrant: no per-call global state besides that workspace
  *    and the per-thread error message.
  */
@@ -158,17 +158,41 @@ int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, co
                      void* stream);
 
 /*
- * Workspace bytes needed by btl_linear / btl_linear_i8 for this shape and mode
- * (for btl_linear_group pass n = sum of the layers' n).  Contract: a workspace
- * is all-zero between calls.  Clear a caller-provided one once with
- * btl_workspace_clear before its first use; every call leaves every byte it
- * touched zero again (split-K partial sums are cleared by the kernel that
- * consumes them, scratch activations by a fill kernel queued after their
- * readers), so one workspace can serve calls of any shapes that fit in it.
+ * Operand-order activations for prefill (many token rows).  No reference
+ * counterpart: the reference quantises nothing on this path.  The prefill GEMM
+ * reads every 16-element group of k in the order its unpacked weights take,
+ * k = 16g + [0,4,8,12, 1,5,9,13, 2,6,10,14, 3,7,11,15]; producing that layout
+ * once lets several contractions (or a producer kernel that fuses the
+ * quantisation) skip the reordering.  Values and scales are exactly those of
+ * btl_quantize_act; only the byte order within each 16-group differs.
+ * k % 64 == 0, k < 2^24; x and xq 16-byte aligned.
+ */
+int btl_quantize_act_op(const void* x, int xdtype, int64_t m, int64_t k, int8_t* xq, float* xscale,
+                        void* stream);
+
+/*
+ * The prefill GEMM alone on operand-order activations (btl_quantize_act_op):
+ * `count` (1..4) layers that share xq in one launch, y[i] = [m, w[i]->n] of
+ * ydtype, acc_out NULL or an array of count optional int32 [m, w[i]->n]
+ * outputs.  Results are those of btl_linear_i8 on the natural-order data.
+ * k % 64 == 0, k < 2^24; xq and every w[i]->data 16-byte aligned.  Needs no
+ * workspace.
+ */
+int btl_linear_i8_op(const btl_packed_t* const* w, void* const* y, int32_t* const* acc_out, int count,
+                     const int8_t* xq, const float* xscale, int64_t m, int64_t k, int ydtype,
+                     void* stream);
+
+/*
+ * Workspace bytes needed by btl_linear / btl_linear_i8 / btl_linear_group for
+ * this shape and mode (for btl_linear_group pass n = sum of the layers' n):
+ * scratch for the quantised activations.  Its contents between calls do not
+ * matter (every call writes the scratch it reads), so one workspace serves
+ * calls of any shapes that fit in it; calls that share one must be ordered on
+ * one stream.
  */
 size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode);
 
-/* Zero a caller-provided workspace (a fill kernel on `stream`). */
+/* Zero a caller-provided workspace (a fill kernel on `stream`).  Optional. */
 int btl_workspace_clear(void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus

@@ -111,6 +111,33 @@ def test_validation_errors_before_device_work():
     assert bl.lib.btl_linear_group(None, None, 5, 16, 0, 1, 8, 0, None, 0, None) == bl.BTL_ERR_ARG
 
 
+def test_operand_order_entry_validation():
+    w = _packed(64, 128, data=16)
+    arr = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(w))
+    ys = (ctypes.c_void_p * 1)(16)
+    op = bl.lib.btl_linear_i8_op
+    assert op(arr, ys, None, 0, 16, 16, 4, 128, 0, None) == bl.BTL_ERR_ARG       # count
+    assert op(arr, ys, None, 5, 16, 16, 4, 128, 0, None) == bl.BTL_ERR_ARG
+    assert op(None, ys, None, 1, 16, 16, 4, 128, 0, None) == bl.BTL_ERR_ARG
+    assert op(arr, ys, None, 1, 16, 16, 4, 128, 9, None) == bl.BTL_ERR_DTYPE     # ydtype
+    assert op(arr, ys, None, 1, 16, 16, 4, 124, 0, None) == bl.BTL_ERR_SHAPE     # k != w.k
+    assert bl.lib.btl_last_error().startswith(b"Shape mismatch: Input [4, 124] vs Weight [64, 128]")
+    w96 = _packed(64, 96, data=16)
+    arr96 = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(w96))
+    assert op(arr96, ys, None, 1, 16, 16, 4, 96, 0, None) == bl.BTL_ERR_SHAPE    # k % 64
+    w_mis = _packed(64, 128, data=24)
+    arr_mis = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(w_mis))
+    assert op(arr_mis, ys, None, 1, 16, 16, 4, 128, 0, None) == bl.BTL_ERR_LAYOUT  # alignment
+    assert op(arr, ys, None, 1, 24, 16, 4, 128, 0, None) == bl.BTL_ERR_LAYOUT
+    assert op(arr, ys, None, 1, 16, 16, 0, 128, 0, None) == bl.BTL_OK             # m == 0
+    q = bl.lib.btl_quantize_act_op
+    assert q(16, 0, 4, 96, 16, 16, None) == bl.BTL_ERR_SHAPE                      # k % 64
+    assert q(16, 3, 4, 128, 16, 16, None) == bl.BTL_ERR_DTYPE
+    assert q(24, 0, 4, 128, 16, 16, None) == bl.BTL_ERR_LAYOUT                    # alignment
+    assert q(None, 0, 4, 128, 16, 16, None) == bl.BTL_ERR_LAYOUT
+    assert q(16, 0, 0, 128, 16, 16, None) == bl.BTL_OK
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
 def test_no_device_is_an_error():
     rc = bl.lib.btl_init(0)
