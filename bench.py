@@ -13,9 +13,9 @@ bf16 activations N(0,1) with 0.1% outliers at +-20 in, bf16 out, W1.58-A8 arithm
 through all 32 layers (224 projections, 128 launches) replayed from a HIP graph.
 
 The same line carries a "prefill" section (cfg4, M=2048 on the same 32 layers, its own
-int8-MFMA roofline).
+int8-MFMA roofline) and a "batched_decode" section (cfg3, M = 1..64 on the MLP shapes).
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-prefill]
+    python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-prefill] [--no-sweep]
 """
 import argparse
 import json
@@ -138,7 +138,14 @@ def cpu_baseline(host_layers, seconds):
         if el >= seconds and reps >= 2:
             break
     per_token = el / reps * (LAYERS / len(host_layers))
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), model)
+    except OSError:
+        pass
     return {"value": round(1.0 / per_token, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "cpu": "%s, %d logical CPUs visible" % (model, os.cpu_count() or 0),
             "sample": "%d reps of layers 0-%d of 32 (7 projections each, %.0f MB packed), M=1 fp32, "
                       "cpu.rs algorithm restated in C with AVX2+FMA intrinsics, %d threads; %.1f s"
                       % (reps, len(host_layers) - 1,
@@ -245,6 +252,8 @@ def run_decode(args):
     }
     if args.prefill:
         result["prefill"] = run_prefill(layers, gen, dev, args)
+    if args.sweep:
+        result["batched_decode"] = run_sweep(layers, gen, dev, args)
     if args.cpu_baseline:
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         host = []
@@ -337,6 +346,55 @@ def run_prefill(layers, gen, dev, args):
     }
 
 
+def run_sweep(layers, gen, dev, args):
+    """cfg3: batched decode M in {1,2,4,8,16,32,64} on the MLP shapes (gate|up grouped
+    4096 -> 2 x 14336, down 14336 -> 4096) of the same 32 layers, HIP graph per M.
+    Locates where the HBM-bound GEMV hands over to the MFMA GEMM."""
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    rows = []
+    cap = torch.cuda.Stream()
+    for m in (1, 2, 4, 8, 16, 32, 64):
+        xg, xd = synth_act(m, HIDDEN, gen, dev), synth_act(m, INTER, gen, dev)
+        og = [torch.empty((m, INTER), **bf), torch.empty((m, INTER), **bf)]
+        od = [torch.empty((m, HIDDEN), **bf)]
+        calls = []
+        for L in layers:
+            calls.append(Call([L["gate"], L["up"]], xg, og))
+            calls.append(Call([L["down"]], xd, od))
+        stream = torch.cuda.current_stream().cuda_stream
+        for c in calls[:2]:
+            c(stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(cap):
+            with torch.cuda.graph(g, stream=cap):
+                s = torch.cuda.current_stream().cuda_stream
+                for c in calls:
+                    c(s)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        reps = 10
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / (reps * LAYERS)
+        b = calls[0].bytes + calls[1].bytes
+        ops = 2.0 * m * (2 * INTER * HIDDEN + HIDDEN * INTER)
+        rows.append({"m": m, "mlp_us": round(us, 2), "tok_s": round(m * 1e6 / (us * LAYERS), 1),
+                     "GB_s": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3),
+                     "TOPS": round(ops / us / 1e6, 2)})
+        del g
+    print("bench: batched-decode sweep done", file=sys.stderr, flush=True)
+    return {"workload": "cfg3: batched decode, MLP of 32 layers (gate|up grouped, down), bf16 in/out, "
+                        "W1.58-A8; per M: µs per layer MLP, tokens/s through the 32 MLPs",
+            "rows": rows}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -347,6 +405,8 @@ def main():
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="skip the cfg4 prefill section of the JSON line")
     ap.add_argument("--prefill-m", type=int, default=2048)
+    ap.add_argument("--no-sweep", dest="sweep", action="store_false",
+                    help="skip the cfg3 batched-decode section of the JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:

@@ -98,15 +98,17 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // kernel writes the scratch it reads in the same call, so its contents between
 // calls do not matter and one workspace serves calls of any shapes.
 struct WsLayout {
-    size_t q_off, s_off, total;
+    size_t q_off, s_off, p_off, total;
 };
 
-WsLayout ws_layout(int64_t m, int64_t k)
+// q [m, k] int8, s [m] f32, then `part_bytes` of split-K partial sums
+WsLayout ws_layout(int64_t m, int64_t k, size_t part_bytes)
 {
     WsLayout l;
     l.q_off = 0;
     l.s_off = align_up((size_t)(m * k), 256);
-    l.total = l.s_off + align_up((size_t)(4 * m), 256);
+    l.p_off = l.s_off + align_up((size_t)(4 * m), 256);
+    l.total = l.p_off + align_up(part_bytes, 256);
     return l;
 }
 
@@ -181,17 +183,12 @@ struct Layer {
     int32_t* acc;
 };
 
-// Token rows per GEMV tile: the [rows, k] activation tile must fit in LDS.
-int64_t gemv_mrows(int64_t m, int64_t k)
-{
-    int64_t r = m < btl::kGemvMaxM ? m : btl::kGemvMaxM;
-    while (r > 1 && r * (k + 16) > btl::kGemvLdsMax) r = (r + 1) / 2;
-    return r * (k + 16) <= btl::kGemvLdsMax ? r : 0;
-}
-
-// One k_gemm_i8 launch over the layers of a group (operand-order q).
+// One k_gemm_i8 (or, bat, k_gemv_bat) launch over the layers of a group
+// (operand-order q); with splits > 1, the partial sums go to `part` and a
+// reduce kernel follows.
 hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const float* sx, int64_t m,
-                       int64_t k, int ykind, hipStream_t st)
+                       int64_t k, int ykind, int splits, int split_steps, int32_t* part, bool bat,
+                       hipStream_t st)
 {
     btl::GemmArgs g;
     memset(&g, 0, sizeof(g));
@@ -200,6 +197,9 @@ hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const fl
     g.m = (int)m;
     g.k = (int)k;
     g.ykind = ykind;
+    g.splits = splits;
+    g.split_steps = split_steps;
+    g.part = part;
     for (int i = 0; i < count; ++i) {
         if (layers[i].w->n == 0) continue;
         btl::GemmLayer& L = g.L[g.nl++];
@@ -209,10 +209,39 @@ hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const fl
         L.y = layers[i].y;
         L.acc_out = layers[i].acc;
     }
-    return g.nl ? btl::launch_gemm_i8(g, st) : hipSuccess;
+    if (!g.nl) return hipSuccess;
+    return bat ? btl::launch_gemv_bat(g, st) : btl::launch_gemm_i8(g, st);
+}
+
+int64_t gemm_tiles_n(const Layer* layers, int count)
+{
+    int64_t t = 0;
+    for (int i = 0; i < count; ++i) t += ceil_div(layers[i].w->n, 128);
+    return t;
+}
+
+int64_t gemv_row_blocks(const Layer* layers, int count)
+{
+    int64_t t = 0;
+    for (int i = 0; i < count; ++i) t += ceil_div(layers[i].w->n, 64);
+    return t;
+}
+
+// Decode kernel geometry for m <= 4 token rows: the fewest waves (4 or 8)
+// whose K parts hold the part's activations in registers; 0 when none does.
+int dec_waves(int64_t m, int64_t k)
+{
+    if (m > 4) return 0;
+    for (int w = 4; w <= 8; w *= 2)
+        if (m * (ceil_div(ceil_div(k, w), btl::kStepWeights) * btl::kStepWeights) <= btl::kDecMaxPart) return w;
+    return 0;
 }
 
 // W1.58-A8 contraction of `count` layers sharing one input.
+//   any k % 4 == 0 / any alignment .... quantise into scratch, k_generic_i8
+//   m <= 4 (decode) ................... k_gemv_dec, quantisation fused
+//   otherwise (batched decode, prefill)  quantise in operand order into the
+//                                        workspace, one (split-K) GEMM launch
 int run_i8(const Layer* layers, int count, const void* x, int xkind, const float* xs, int64_t m,
            int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st)
 {
@@ -220,8 +249,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     int rc = current_device(&dev);
     if (rc) return rc;
     int64_t nsum = 0;
-    const int64_t mrows = gemv_mrows(m, k);
-    bool fast = k >= 64 && k % 64 == 0 && aligned16(x) && mrows > 0;
+    bool fast = k >= 64 && k % 64 == 0 && k < (1 << 24) && aligned16(x);
     for (int i = 0; i < count; ++i) {
         nsum += layers[i].w->n;
         fast = fast && aligned16(layers[i].w->data);
@@ -233,7 +261,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     if (!fast) {
         // any k % 4 == 0 / any alignment: quantise once into scratch, one wave per output
         const bool scratch = xkind != btl::XK_I8;
-        const WsLayout L = ws_layout(m, k);
+        const WsLayout L = ws_layout(m, k, 0);
         void* ws = nullptr;
         if (scratch && (rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
         const int8_t* q = (const int8_t*)x;
@@ -253,148 +281,73 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         return BTL_OK;
     }
 
-    int cus;
-    {
-        std::lock_guard<std::mutex> lock(g_mu);
-        cus = g_dev[dev].cus;
-    }
-
-    // Prefill (many token rows): quantise once in operand order (or reorder
-    // pre-quantised rows) into the workspace, then one GEMM per layer.
-    if (m > env_int("BTL_GEMM_MIN_M", 64) && k % 64 == 0 && k < (1 << 24)) {
-        const WsLayout L = ws_layout(m, k);
-        void* ws = nullptr;
-        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
-        const int8_t* q = (const int8_t*)ws + L.q_off;
-        const float* sxp = xs;
-        if (xkind == btl::XK_I8) {
-            e = btl::launch_op_order((const int8_t*)x, m, k, (int8_t*)q, st);
-        } else {
-            sxp = (const float*)((uint8_t*)ws + L.s_off);
-            e = btl::launch_quant_op(x, xkind, m, k, (int8_t*)q, (float*)sxp, st);
+    // Decode (1..4 token rows): 16*tiles rows per workgroup, its waves split K.
+    int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k) : 0;
+    if (wv > 0) {
+        // defaults measured on MI355X (Llama-3-8B shapes): the fewest waves
+        // that hold a part in registers, one 16-row tile per wave
+        int64_t kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
+        int rt = 1;
+        const int frt = env_int("BTL_GEMV_DEC_TILES", 0);
+        if (frt == 1 || frt == 2 || frt == 4) rt = frt;
+        const int fwv = env_int("BTL_GEMV_DEC_PARTS", 0);
+        if ((fwv == 4 || fwv == 8) && m * ceil_div(ceil_div(k, fwv), 256) * 256 <= btl::kDecMaxPart) {
+            wv = fwv;
+            kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
         }
-        if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
-        e = launch_gemm(layers, count, q, sxp, m, k, ykind, st);
-        if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
+        btl::GemvArgs a;
+        memset(&a, 0, sizeof(a));
+        int rb = 0, np = 0;
+        for (int i = 0; i < count; ++i) {
+            const int64_t n = layers[i].w->n;
+            if (n == 0) continue;
+            btl::GemvProblem& p = a.p[np++];
+            p.w = layers[i].w->data;
+            p.y = layers[i].y;
+            p.acc_out = layers[i].acc;
+            p.sw = layers[i].w->scale;
+            p.n = (int)n;
+            p.rb_begin = rb;
+            rb += (int)ceil_div(n, 16 * rt);
+        }
+        a.nprob = np;
+        a.x = x;
+        a.xs = xs;
+        a.m = (int)m;
+        a.k = (int)k;
+        a.rb_total = rb;
+        a.tiles = rt;
+        a.parts = wv;
+        a.kpart = (int)kpart;
+        a.ykind = ykind;
+        e = btl::launch_gemv_dec(a, xkind, 1, st);
+        if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
         return BTL_OK;
     }
 
-    // Decode (1..4 token rows): 16*tiles rows per workgroup, its waves split K.
-    if (m <= 4 && env_int("BTL_GEMV_DEC", 1) != 0) {
-        int wv = 0;
-        for (int w = 4; w <= 8; w *= 2) {
-            const int64_t kp = ceil_div(ceil_div(k, w), btl::kStepWeights) * btl::kStepWeights;
-            if (m * kp <= btl::kDecMaxPart) {
-                wv = w;
-                break;
-            }
-        }
-        if (wv > 0) {
-            // defaults measured on MI355X (Llama-3-8B shapes): the fewest waves
-            // that hold a part in registers, one 16-row tile per wave
-            int64_t kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
-            int rt = 1;
-            const int frt = env_int("BTL_GEMV_DEC_TILES", 0);
-            if (frt == 1 || frt == 2 || frt == 4) rt = frt;
-            const int fwv = env_int("BTL_GEMV_DEC_PARTS", 0);
-            if ((fwv == 4 || fwv == 8) && m * ceil_div(ceil_div(k, fwv), 256) * 256 <= btl::kDecMaxPart) {
-                wv = fwv;
-                kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
-            }
-            btl::GemvArgs a;
-            memset(&a, 0, sizeof(a));
-            int rb = 0, np = 0;
-            for (int i = 0; i < count; ++i) {
-                const int64_t n = layers[i].w->n;
-                if (n == 0) continue;
-                btl::GemvProblem& p = a.p[np++];
-                p.w = layers[i].w->data;
-                p.y = layers[i].y;
-                p.acc_out = layers[i].acc;
-                p.sw = layers[i].w->scale;
-                p.n = (int)n;
-                p.rb_begin = rb;
-                rb += (int)ceil_div(n, 16 * rt);
-            }
-            a.nprob = np;
-            a.x = x;
-            a.xs = xs;
-            a.m = (int)m;
-            a.k = (int)k;
-            a.rb_total = rb;
-            a.tiles = rt;
-            a.parts = wv;
-            a.kpart = (int)kpart;
-            a.mrows = (int)m;
-            a.ykind = ykind;
-            e = btl::launch_gemv_dec(a, xkind, 1, st);
-            if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
-            return BTL_OK;
-        }
-    }
-
-    const int64_t mtiles = ceil_div(m, mrows);
-    // 16-row tiles per workgroup: the most (fewest activation prologues per
-    // weight row) that still gives `target` workgroups; the 4 waves of a
-    // workgroup split K by 4 / tiles.
-    const int64_t target = env_int("BTL_GEMV_WG_TARGET", 3 * cus / 2);
-    int tiles = 1;
-    for (int t = 4; t >= 1; t /= 2) {
-        int64_t blocks = 0;
-        for (int i = 0; i < count; ++i) blocks += ceil_div(layers[i].w->n, 16 * t);
-        if (blocks * mtiles >= target || t == 1) {
-            tiles = t;
-            break;
-        }
-    }
-    const int forced = env_int("BTL_GEMV_TILES", 0);
-    if (forced == 1 || forced == 2 || forced == 4) tiles = forced;
-    const int parts = 4 / tiles;
-    const int64_t kpart = ceil_div(ceil_div(k, parts), btl::kStepWeights) * btl::kStepWeights;
-
-    // Several token tiles: quantise once into scratch.
-    const bool scratch = mtiles > 1 && xkind != btl::XK_I8;
-    const WsLayout L = ws_layout(m, k);
+    // Batched decode (m <= 32; measured on MI355X: the GEMM is faster from
+    // m = 64, Llama-3-8B MLP shapes) and GEMM: quantise once in operand order
+    // (or reorder pre-quantised rows) into the workspace; split K over
+    // workgroups when the output has few tiles.
+    const bool bat = m <= env_int("BTL_GEMV_BAT_MAX_M", 32) && m <= 64 && env_int("BTL_GEMV_BAT", 1) != 0;
+    int split_steps = 0;
+    const int splits = bat ? btl::gemv_bat_split(m, gemv_row_blocks(layers, count), k, &split_steps)
+                           : btl::gemm_splits(m, gemm_tiles_n(layers, count), k, &split_steps);
+    const WsLayout L = ws_layout(m, k, splits > 1 ? (size_t)splits * m * nsum * 4 : 0);
     void* ws = nullptr;
-    if (scratch) {
-        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
-        int8_t* wq = (int8_t*)ws + L.q_off;
-        float* wsc = (float*)((uint8_t*)ws + L.s_off);
-        e = btl::launch_quant_act(x, xkind, m, k, wq, wsc, st);
-        if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
-        x = wq;
-        xs = wsc;
-        xkind = btl::XK_I8;
+    if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
+    const int8_t* q = (const int8_t*)ws + L.q_off;
+    const float* sxp = xs;
+    if (xkind == btl::XK_I8) {
+        e = btl::launch_op_order((const int8_t*)x, m, k, (int8_t*)q, st);
+    } else {
+        sxp = (const float*)((uint8_t*)ws + L.s_off);
+        e = btl::launch_quant_op(x, xkind, m, k, (int8_t*)q, (float*)sxp, st);
     }
-
-    btl::GemvArgs a;
-    memset(&a, 0, sizeof(a));
-    int rb = 0;
-    int np = 0;
-    for (int i = 0; i < count; ++i) {
-        const int64_t n = layers[i].w->n;
-        if (n == 0) continue;
-        btl::GemvProblem& p = a.p[np++];
-        p.w = layers[i].w->data;
-        p.y = layers[i].y;
-        p.acc_out = layers[i].acc;
-        p.sw = layers[i].w->scale;
-        p.n = (int)n;
-        p.rb_begin = rb;
-        rb += (int)ceil_div(n, 16 * tiles);
-    }
-    a.nprob = np;
-    a.x = x;
-    a.xs = xs;
-    a.m = (int)m;
-    a.k = (int)k;
-    a.rb_total = rb;
-    a.tiles = tiles;
-    a.parts = parts;
-    a.kpart = (int)kpart;
-    a.mrows = (int)mrows;
-    e = btl::launch_gemv(a, xkind, ykind, (int)mtiles, st);
-    if (e != hipSuccess) return hip_fail(e, "gemv kernel launch");
+    if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
+    e = launch_gemm(layers, count, q, sxp, m, k, ykind, splits, split_steps,
+                    splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr, bat, st);
+    if (e != hipSuccess) return hip_fail(e, bat ? "batched gemv kernel launch" : "gemm kernel launch");
     return BTL_OK;
 }
 
@@ -615,7 +568,7 @@ int btl_linear_i8_op(const btl_packed_t* const* w, void* const* y, int32_t* cons
     int dev;
     if ((rc = current_device(&dev))) return rc;
     hipError_t e = launch_gemm(ls, count, xq, xscale, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32,
-                               (hipStream_t)stream);
+                               1, 0, nullptr, false, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
     return BTL_OK;
 }
@@ -624,8 +577,15 @@ size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)
 {
     if (m < 0 || n < 0 || k < 0) return 0;
     if (mode == BTL_ACT_F32_REF) return 0;
-    (void)n;
-    return ws_layout(m, k).total;
+    // split-K partials of the GEMM / batched-decode routes; a group's layers
+    // have at least ceil(n / 128) (ceil(n / 64)) output tiles in total and the
+    // splits only fall as tiles are added, so this bounds them
+    int splits = btl::gemm_splits(m, ceil_div(n, 128), k, nullptr);
+    if (m <= 64) {  // any BTL_GEMV_BAT_MAX_M
+        const int sb = btl::gemv_bat_split(m, ceil_div(n, 64), k, nullptr);
+        splits = sb > splits ? sb : splits;
+    }
+    return ws_layout(m, k, splits > 1 ? (size_t)splits * m * n * 4 : 0).total;
 }
 
 int btl_workspace_clear(void* ws, size_t ws_bytes, void* stream)

@@ -10,13 +10,11 @@ namespace btl {
 
 constexpr int kMaxGroup = 4;       // layers per grouped launch (q|k|v, w1|w3)
 constexpr int kStepWeights = 256;  // weights of one row consumed per wave-load (64 B)
-constexpr int kGemvMaxM = 16;      // token rows per GEMV tile (MFMA 16x16 B operand)
-constexpr int kGemvLdsMax = 61440; // bytes of LDS the activation tile may use
 
 enum XKind { XK_F32 = 0, XK_BF16 = 1, XK_I8 = 2 };
 enum YKind { YK_F32 = 0, YK_BF16 = 1 };
 
-// One layer of a (possibly grouped) GEMV launch.
+// One layer of a (possibly grouped) decode launch.
 struct GemvProblem {
     const uint8_t* w;  // packed rows, row stride k/4 bytes, 16-byte aligned base
     void* y;           // [m, n] output
@@ -34,16 +32,13 @@ struct GemvArgs {
     int m, k;
     int rb_total;     // row-blocks over all layers (grid.x)
     int tiles;        // 16-row tiles per row-block (1, 2 or 4)
-    int parts;        // K parts per tile (4 / tiles)
+    int parts;        // waves per workgroup, each one K part (4 or 8)
     int kpart;        // weights per K part (multiple of 256)
-    int mrows;        // token rows per grid.y tile (<= 16)
-    int ykind;        // YK_F32 / YK_BF16 (k_gemv_dec only; k_gemv takes it as a template)
+    int ykind;        // YK_F32 / YK_BF16
 };
 
-hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipStream_t s);
-
-// Decode variant: a.tiles (1, 2, 4) 16-row tiles per wave, a.parts (4 or 8)
-// waves split K, a.mrows <= 4, a.mrows * a.kpart <= kDecMaxPart and
+// Decode (k_gemv_dec): a.tiles (1, 2, 4) 16-row tiles per wave, a.parts (4 or
+// 8) waves split K, a.m <= 4, a.m * a.kpart <= kDecMaxPart and
 // a.tiles * ceil(a.kpart / 256) <= 16 wave-loads per lane.
 constexpr int kDecMaxPart = 2048;
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s);
@@ -58,6 +53,7 @@ struct GemmLayer {
     void* y;           // [m, n]
     int32_t* acc_out;  // optional [m, n]
     int tile0;         // first output tile of this layer (set by launch_gemm_i8)
+    int col0;          // first column of this layer in the partial-sum rows (set by launch_gemm_i8)
 };
 struct GemmArgs {
     const int8_t* q;   // [m, k] quantised activations, operand order
@@ -66,9 +62,26 @@ struct GemmArgs {
     int nl;
     int m, k;
     int ykind;
+    // split-K: splits > 1 runs `splits` workgroups per output tile, each over
+    // split_steps K steps of 128, writing exact int32 partial sums to
+    // part[split][m][ncols] (ncols = sum of the layers' n); a reduce kernel
+    // adds them and applies the epilogue.  splits == 1: part unused.
+    int splits, split_steps;
+    int32_t* part;
 };
 
+constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for
+// K splits for an (m, ncols, k) GEMM: enough workgroups to cover the chip when
+// the output has few tiles (small m); 1 when it already has kGemmSplitTarget.
+int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps);
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s);
+
+// Batched decode (k_gemv_bat): the GemmArgs of a GEMM with m <= 64, k % 64
+// == 0; split_steps = 4, 8 or 16 steps of 256 weights per K split and splits
+// = ceil(k / (256 split_steps)) from gemv_bat_split; row_blocks = sum of
+// ceil(n / 64) over the layers.
+int gemv_bat_split(int64_t m, int64_t row_blocks, int64_t k, int* steps);
+hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s);
 // natural-order int8 rows -> operand order (k % 16 == 0, 16-byte aligned)
 hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, hipStream_t st);
 hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,

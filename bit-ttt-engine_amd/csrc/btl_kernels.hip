@@ -6,10 +6,6 @@
 //   absmax convention ............ src/layers/kv_cache.rs:95-119
 //
 // Kernels:
-//   k_gemv<XK,YK>     decode / small-M contraction on the int8 MFMA
-//                     (v_mfma_i32_16x16x64_i8), weights unpacked in registers,
-//                     activations quantised (or copied) into LDS, K split over
-//                     the waves of a workgroup and summed exactly through LDS.
 //   k_gemv_dec<XK,YK,WV>  the decode case (1..4 token rows): one 16-row tile
 //                     per workgroup, WV waves split K, activations quantised
 //                     per wave from registers loaded ahead of the weights.
@@ -154,21 +150,6 @@ __device__ __forceinline__ uint4 transpose16(uint4 a)
     return o;
 }
 
-// ---------------------------------------------------------------------------
-// k_gemv: small-M ternary contraction on the int8 MFMA
-// ---------------------------------------------------------------------------
-// Grid: x = row-blocks of 16*tiles rows (over all layers of a group), y = token
-// tiles of `mrows` rows.  Workgroup: 4 waves = tiles x parts; wave w owns the
-// 16-row tile w / parts and the K part w % parts (kpart weights, a multiple of
-// 256).  Per wave-load, lane (r = lane&15, kq = lane>>4) reads 16 bytes (64
-// weights) of row r at byte 64*j + 16*kq of its part: each row contributes 64
-// contiguous bytes, a wave-load covers 16 rows x 256 weights.  Each 4-byte
-// word becomes one A operand (16 rows x 64 k) of v_mfma_i32_16x16x64_i8; the B
-// operand (token rows x 64 k) comes from the quantised activation tile in LDS.
-// D lane l, element v = row 4*(l>>4)+v, token l&15.  Parts of one tile are
-// summed through LDS (exact int32); no cross-workgroup communication.
-constexpr int kPF = 16;  // wave-loads kept in flight per lane (64 VGPRs)
-
 // round_half_away(x*r) as an int, for a finite row (see quant1)
 __device__ __forceinline__ int quant_fast(float x, float r)
 {
@@ -185,202 +166,6 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d)
 }
 
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-
-template <int XK>
-__device__ __forceinline__ void gemv_prologue(const GemvArgs& a, uint8_t* sq, int lp, int m0, int mt,
-                                              float* s_sx, uint32_t (*s_amax)[kGemvMaxM], float* s_r,
-                                              int* s_ok)
-{
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int K = a.k;
-    const int groups = K >> 4;  // K % 64 == 0
-    if (XK == XK_I8) {
-        const int8_t* xq = (const int8_t*)a.x;
-        if (tid < mt) s_sx[tid] = a.xs[m0 + tid];
-        for (int g = tid; g < mt * groups; g += 256) {
-            const int m = g / groups, gi = g - m * groups;
-            uint4 v = *(const uint4*)(xq + (int64_t)(m0 + m) * K + gi * 16);
-            *(uint4*)(sq + m * lp + gi * 16) = transpose16(v);
-        }
-        return;
-    }
-    // 1. absmax of each token row (IEEE bit patterns, sign cleared)
-    for (int m = 0; m < mt; ++m) {
-        uint32_t amax = 0;
-        if (XK == XK_BF16) {
-            const uint4* xr = (const uint4*)((const uint16_t*)a.x + (int64_t)(m0 + m) * K);
-            us2 mx = {0, 0};
-            for (int i = tid; i < (K >> 3); i += 256) {
-                const uint4 v = xr[i];
-                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.x & 0x7FFF7FFFu));
-                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.y & 0x7FFF7FFFu));
-                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.z & 0x7FFF7FFFu));
-                mx = __builtin_elementwise_max(mx, __builtin_bit_cast(us2, v.w & 0x7FFF7FFFu));
-            }
-            amax = (uint32_t)(mx.x > mx.y ? mx.x : mx.y) << 16;
-        } else {
-            const uint4* xr = (const uint4*)((const float*)a.x + (int64_t)(m0 + m) * K);
-            for (int i = tid; i < (K >> 2); i += 256) {
-                const uint4 v = xr[i];
-                const uint32_t b0 = v.x & 0x7FFFFFFFu, b1 = v.y & 0x7FFFFFFFu;
-                const uint32_t b2 = v.z & 0x7FFFFFFFu, b3 = v.w & 0x7FFFFFFFu;
-                amax = max(amax, max(max(b0, b1), max(b2, b3)));
-            }
-        }
-        amax = wave_max_u32(amax);
-        if (lane == 0) s_amax[wave][m] = amax;
-    }
-    __syncthreads();
-    if (tid < mt) {
-        uint32_t am = s_amax[0][tid];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) am = s_amax[w][tid] > am ? s_amax[w][tid] : am;
-        const QParams qp = qparams(am);
-        s_r[tid] = qp.r;
-        s_sx[tid] = qp.s;
-        s_ok[tid] = qp.ok;
-    }
-    __syncthreads();
-    // 2. quantise the rows into LDS, 16 values per thread per step, operand order
-    for (int g = tid; g < mt * groups; g += 256) {
-        const int m = g / groups, gi = g - m * groups;
-        const float r = s_r[m];
-        uint4 out = {0u, 0u, 0u, 0u};
-        if (s_ok[m]) {
-            float f[16];
-            if (XK == XK_BF16) {
-                const uint4* src = (const uint4*)((const uint16_t*)a.x + (int64_t)(m0 + m) * K + gi * 16);
-                const uint4 v0 = src[0], v1 = src[1];
-                const uint32_t u[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-                for (int h = 0; h < 8; ++h) {
-                    f[2 * h] = __uint_as_float(u[h] << 16);
-                    f[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
-                }
-            } else {
-                const float4* src = (const float4*)((const float*)a.x + (int64_t)(m0 + m) * K + gi * 16);
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    const float4 v = src[h];
-                    f[4 * h] = v.x; f[4 * h + 1] = v.y; f[4 * h + 2] = v.z; f[4 * h + 3] = v.w;
-                }
-            }
-            int q[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) q[i] = quant_fast(f[i], r);
-            out.x = pack4(q[0], q[4], q[8], q[12]);
-            out.y = pack4(q[1], q[5], q[9], q[13]);
-            out.z = pack4(q[2], q[6], q[10], q[14]);
-            out.w = pack4(q[3], q[7], q[11], q[15]);
-        }
-        *(uint4*)(sq + m * lp + gi * 16) = out;
-    }
-}
-
-template <int XK, int YK>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a)
-{
-    extern __shared__ __align__(16) uint8_t sq[];  // [mt][k + 16] int8 activation tile
-    __shared__ uint32_t s_amax[4][kGemvMaxM];
-    __shared__ float s_r[kGemvMaxM], s_sx[kGemvMaxM];
-    __shared__ int s_ok[kGemvMaxM];
-    __shared__ v4i s_red[3][64];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rbg = blockIdx.x;
-    const int m0 = blockIdx.y * a.mrows;
-    const int mt = min(a.mrows, a.m - m0);
-
-    // layer of this row-block (uniform; explicit selects keep the kernel
-    // arguments in scalar registers)
-    const uint8_t* W = a.p[0].w;
-    void* Y = a.p[0].y;
-    int32_t* ACC = a.p[0].acc_out;
-    float SW = a.p[0].sw;
-    int N = a.p[0].n;
-    int RB0 = a.p[0].rb_begin;
-#pragma unroll
-    for (int i = 1; i < kMaxGroup; ++i) {
-        if (i < a.nprob && rbg >= a.p[i].rb_begin) {
-            W = a.p[i].w; Y = a.p[i].y; ACC = a.p[i].acc_out;
-            SW = a.p[i].sw; N = a.p[i].n; RB0 = a.p[i].rb_begin;
-        }
-    }
-    const int K = a.k;
-    const int parts = a.parts;
-    const int t = wave / parts, part = wave - t * parts;
-    const int kb = part * a.kpart;
-    const int len = min(a.kpart, K - kb);
-    const int steps = len > 0 ? (len + kStepWeights - 1) / kStepWeights : 0;
-    const int lp = K + 16;
-
-    // 1. put this wave's weight loads in flight before the activation prologue
-    const int r = lane & 15, kq = lane >> 4;
-    const int row0 = (rbg - RB0) * (16 * a.tiles) + t * 16;
-    const int nrow = row0 + r;
-    const bool row_ok = nrow < N;
-    const uint8_t* wp = W + (int64_t)(row_ok ? nrow : 0) * (K >> 2) + (kb >> 2) + kq * 16;
-    auto ld = [&](int j) -> uint4 {
-        uint4 v = {0u, 0u, 0u, 0u};
-        if (row_ok && j * kStepWeights + kq * 64 < len) v = *(const uint4*)(wp + j * 64);
-        return v;
-    };
-    uint4 buf[kPF];
-#pragma unroll
-    for (int i = 0; i < kPF; ++i) buf[i] = ld(i);
-
-    // 2. activation tile
-    gemv_prologue<XK>(a, sq, lp, m0, mt, s_sx, s_amax, s_r, s_ok);
-    __syncthreads();
-
-    // 3. main loop
-    const int mcol = lane & 15;
-    const bool m_ok = mcol < mt;
-    const uint8_t* bq = sq + mcol * lp + kb + kq * 64;
-    v4i acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
-    const v4i zero = {0, 0, 0, 0};
-    for (int j0 = 0; j0 < steps; j0 += kPF) {
-#pragma unroll
-        for (int i = 0; i < kPF; ++i) {
-            const int j = j0 + i;
-            if (j < steps) {
-                const uint4 cur = buf[i];
-                buf[i] = ld(j + kPF);
-                const uint8_t* bj = bq + j * kStepWeights;
-                const v4i b0 = m_ok ? *(const v4i*)(bj + 0) : zero;
-                const v4i b1 = m_ok ? *(const v4i*)(bj + 16) : zero;
-                const v4i b2 = m_ok ? *(const v4i*)(bj + 32) : zero;
-                const v4i b3 = m_ok ? *(const v4i*)(bj + 48) : zero;
-                acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc1, 0, 0, 0);
-                acc0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc1, 0, 0, 0);
-            }
-        }
-    }
-    v4i acc = acc0 + acc1;
-
-    // 4. sum the K parts of each tile (exact), then the epilogue
-    if (parts > 1) {
-        if (part > 0) s_red[(part - 1) * a.tiles + t][lane] = acc;
-        __syncthreads();
-        if (part > 0) return;
-        for (int p = 1; p < parts; ++p) acc += s_red[(p - 1) * a.tiles + t][lane];
-    }
-    if (!m_ok) return;
-    const int gm = m0 + mcol;
-    const float c = __fmul_rn(s_sx[mcol], SW);
-    const int nb = row0 + 4 * (lane >> 4);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const int n = nb + v;
-        if (n < N) {
-            const int64_t o = (int64_t)gm * N + n;
-            store_y<YK>(Y, o, __fmul_rn((float)acc[v], c));
-            if (ACC) ACC[o] = acc[v];
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // k_gemv_dec: decode (1..4 token rows), one 16-row tile per workgroup
@@ -690,26 +475,6 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv(const GemvArgs& a, int xkind, int ykind, int mtiles, hipStream_t s)
-{
-    dim3 grid((unsigned)a.rb_total, (unsigned)mtiles);
-    const int mt = a.m < a.mrows ? a.m : a.mrows;
-    const size_t lds = (size_t)mt * (size_t)(a.k + 16);
-#define BTL_GEMV_CASE(XKV, YKV)                                              \
-    if (xkind == XKV && ykind == YKV) {                                      \
-        hipLaunchKernelGGL((k_gemv<XKV, YKV>), grid, dim3(256), lds, s, a);  \
-        return hipGetLastError();                                            \
-    }
-    BTL_GEMV_CASE(XK_F32, YK_F32)
-    BTL_GEMV_CASE(XK_F32, YK_BF16)
-    BTL_GEMV_CASE(XK_BF16, YK_F32)
-    BTL_GEMV_CASE(XK_BF16, YK_BF16)
-    BTL_GEMV_CASE(XK_I8, YK_F32)
-    BTL_GEMV_CASE(XK_I8, YK_BF16)
-#undef BTL_GEMV_CASE
-    return hipErrorInvalidValue;
-}
-
 // ---------------------------------------------------------------------------
 // k_quant_op: per-token quantisation into MFMA operand order (prefill)
 // ---------------------------------------------------------------------------
@@ -753,12 +518,65 @@ __global__ __launch_bounds__(256) void k_quant_op(const void* x, int k, int8_t* 
     }
 }
 
+// Single pass: one workgroup per token row (64 * ceil(k / 1024) threads, at
+// most 1024) holds G 16-element groups per thread in registers (k <= 16384 G),
+// so x is read once.
+template <int XK, int G>
+__global__ __launch_bounds__(1024) void k_quant_op1(const void* x, int k, int8_t* q, float* s)
+{
+    __shared__ uint32_t s_w[16];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int groups = k >> 4;  // k % 16 == 0
+    constexpr int NV = XK == XK_F32 ? 4 : 2;
+    constexpr int ES = XK == XK_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc((const uint8_t*)x + row * k * ES, (uint32_t)(k * ES));
+    uint4 v[G][NV];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int gi = tid + nt * g;
+        const int off = gi < groups ? gi * 16 * ES : kOOB;
+#pragma unroll
+        for (int h = 0; h < NV; ++h) v[g][h] = bload(xr, off + 16 * h);
+    }
+    uint32_t amax = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) amax = max(amax, group_absmax<XK>(v[g]));  // zeros past k
+    amax = wave_max_dpp(amax);
+    if ((tid & 63) == 0) s_w[tid >> 6] = amax;
+    __syncthreads();
+    amax = s_w[0];
+    for (int w = 1; w < (nt >> 6); ++w) amax = max(amax, s_w[w]);
+    const QParams qp = qparams(amax);
+    if (tid == 0) s[row] = qp.s;
+    uint4* qr = (uint4*)(q + row * k);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int gi = tid + nt * g;
+        if (gi < groups) qr[gi] = qp.ok ? group_quant<XK>(v[g], qp.r) : uint4{0u, 0u, 0u, 0u};
+    }
+}
+
 hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,
                            hipStream_t st)
 {
     if (m <= 0) return hipSuccess;
-    if (xkind == XK_BF16) hipLaunchKernelGGL(k_quant_op<XK_BF16>, dim3((unsigned)m), dim3(256), 0, st, x, (int)k, q, s);
-    else hipLaunchKernelGGL(k_quant_op<XK_F32>, dim3((unsigned)m), dim3(256), 0, st, x, (int)k, q, s);
+    const int64_t groups = k >> 4;
+    const dim3 grid((unsigned)m);
+    const int nt = groups <= 1024 ? (int)((groups + 63) / 64 * 64) : 1024;
+#define BTL_QOP1(XKV, GV)                                                                \
+    if (groups <= 1024 * GV) {                                                           \
+        hipLaunchKernelGGL((k_quant_op1<XKV, GV>), grid, dim3(nt), 0, st, x, (int)k, q, s); \
+        return hipGetLastError();                                                        \
+    }
+    if (xkind == XK_BF16) {
+        BTL_QOP1(XK_BF16, 1) BTL_QOP1(XK_BF16, 2) BTL_QOP1(XK_BF16, 4)
+        hipLaunchKernelGGL(k_quant_op<XK_BF16>, grid, dim3(256), 0, st, x, (int)k, q, s);
+    } else {
+        BTL_QOP1(XK_F32, 1) BTL_QOP1(XK_F32, 2) BTL_QOP1(XK_F32, 4)
+        hipLaunchKernelGGL(k_quant_op<XK_F32>, grid, dim3(256), 0, st, x, (int)k, q, s);
+    }
+#undef BTL_QOP1
     return hipGetLastError();
 }
 
@@ -819,8 +637,12 @@ __device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t r, uint8_t* l
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
 }
 
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 layout: vmcnt bits
+// 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
 // s_waitcnt vmcnt(0): every global load (and LDS copy) of this wave has landed.
-__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); }
 
 __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
 {
@@ -844,9 +666,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
     const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
     const int K = a.k, N = Lw.n;
     const int rows_a = min(kGemmBM, a.m - m0), rows_b = min(kGemmBN, N - n0);
+    const int split = blockIdx.y;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.q + (int64_t)m0 * K, (uint32_t)(rows_a * K));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(Lw.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
-    const int steps = (K + kGemmBK - 1) / kGemmBK;
+    const int st_begin = split * a.split_steps;
+    const int st_end = min((K + kGemmBK - 1) / kGemmBK, st_begin + a.split_steps);
 
     // source offsets (relative to the step's first k) of this wave's copies:
     // A chunk c = 16 rows x 64 B of half j; lane -> (row, slot) as laid out above
@@ -893,14 +717,35 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
         }
     };
 
-    issue(0, 0);
-    for (int st = 0; st < steps; ++st) {
+    if (st_begin < st_end) issue(st_begin, 0);
+    for (int st = st_begin; st < st_end; ++st) {
+        const int stage = (st - st_begin) & 1;
         wait_loads();     // this wave's copies of step st are in LDS
-        __syncthreads();  // ... every wave's; and stage (st+1)&1 is no longer read
-        if (st + 1 < steps) issue(st + 1, (st + 1) & 1);
-        const uint8_t* base = lds + (st & 1) * kGemmStage;
+        __syncthreads();  // ... every wave's; and the other stage is no longer read
+        if (st + 1 < st_end) issue(st + 1, stage ^ 1);
+        const uint8_t* base = lds + stage * kGemmStage;
         compute_half(base, 0);
         if (st * kGemmBK + 64 < K) compute_half(base, 1);  // k % 128 == 64: last step is half
+    }
+
+    if (a.splits > 1) {
+        // exact int32 partial sums; k_gemm_reduce adds the splits
+        const int ncols = a.L[a.nl - 1].col0 + a.L[a.nl - 1].n;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = m0 + wm * 64 + b * 16 + 4 * kq + v;
+                if (m < a.m) {
+                    int32_t* prow = a.part + ((int64_t)split * a.m + m) * ncols + Lw.col0;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int n = n0 + wn * 64 + c * 16 + r16;
+                        if (n < N) prow[n] = acc[b][c][v];
+                    }
+                }
+            }
+        return;
     }
 
     // epilogue: y = (float)acc * (s_x[m] * s_w)
@@ -928,19 +773,240 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
     }
 }
 
+// k_gemm_reduce: sum the split-K partials of every output, then the epilogue
+// y = (float)acc * (s_x[m] * s_w) of its layer.  One thread per output, the
+// splits' loads issued 8 at a time.
+__global__ __launch_bounds__(256) void k_gemm_reduce(GemmArgs a, int ncols)
+{
+    const int64_t total = (int64_t)a.m * ncols;
+    const bool ybf = a.ykind == YK_BF16;
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int m = (int)(i / ncols), col = (int)(i - (int64_t)m * ncols);
+        int32_t acc = 0;
+        int sp = 0;
+        for (; sp + 8 <= a.splits; sp += 8) {
+            int32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = a.part[(sp + u) * total + i];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; sp < a.splits; ++sp) acc += a.part[sp * total + i];
+        GemmLayer Lw = a.L[0];
+#pragma unroll
+        for (int l = 1; l < kMaxGroup; ++l)
+            if (l < a.nl && col >= a.L[l].col0) Lw = a.L[l];
+        const int n = col - Lw.col0;
+        const int64_t o = (int64_t)m * Lw.n + n;
+        const float yv = __fmul_rn((float)acc, __fmul_rn(a.sx[m], Lw.sw));
+        if (ybf) ((uint16_t*)Lw.y)[o] = f32_to_bf16(yv);
+        else ((float*)Lw.y)[o] = yv;
+        if (Lw.acc_out) Lw.acc_out[o] = acc;
+    }
+}
+
+int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps)
+{
+    const int64_t steps = (k + kGemmBK - 1) / kGemmBK;
+    const int64_t tiles = (m + kGemmBM - 1) / kGemmBM * tiles_n;
+    int64_t s = tiles >= kGemmSplitTarget || tiles <= 0 ? 1 : (kGemmSplitTarget + tiles - 1) / tiles;
+    if (s > steps / 2) s = steps / 2;  // at least two K steps per split
+    if (s < 1) s = 1;
+    const int64_t per = (steps + s - 1) / s;
+    if (split_steps) *split_steps = (int)per;
+    return (int)((steps + per - 1) / per);  // no empty split
+}
+
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
 {
-    // tile0 of every layer is filled in here from the layers' n
+    // tile0 / col0 of every layer are filled in here from the layers' n
     GemmArgs g = a;
-    int64_t tn = 0;
+    int64_t tn = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
         g.L[l].tile0 = (int)tn;
+        g.L[l].col0 = (int)cols;
         tn += (g.L[l].n + kGemmBN - 1) / kGemmBN;
+        cols += g.L[l].n;
     }
     const int64_t tiles = (int64_t)((g.m + kGemmBM - 1) / kGemmBM) * tn;
     if (tiles <= 0) return hipSuccess;
-    if (tiles > INT32_MAX || g.nl < 1 || g.nl > kMaxGroup) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_i8, dim3((unsigned)tiles), dim3(256), 0, s, g);
+    if (tiles > INT32_MAX || g.nl < 1 || g.nl > kMaxGroup || cols > INT32_MAX) return hipErrorInvalidValue;
+    if (g.splits < 1) g.splits = 1;
+    if (g.splits == 1) g.split_steps = (g.k + kGemmBK - 1) / kGemmBK;
+    if (g.splits > 1 && (!g.part || g.split_steps < 1 || (int64_t)g.splits * g.m * cols > INT32_MAX))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gemm_i8, dim3((unsigned)tiles, (unsigned)g.splits), dim3(256), 0, s, g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || g.splits == 1) return e;
+    const int64_t outs = (int64_t)g.m * cols;
+    const int64_t blocks = (outs + 255) / 256;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, s, g, (int)cols);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_gemv_bat: batched decode (5..64 token rows, or 2..4 where k_gemv_dec's
+// register budget does not hold the part)
+// ---------------------------------------------------------------------------
+// Weight-stationary like k_gemv_dec, with the tokens pre-quantised in operand
+// order (k_quant_op).  Workgroup: 4 waves x one 16-row weight tile = 64 rows,
+// over one K range of 256 ST weights (grid.y = K splits).  Each wave first
+// copies its share of the token rows of that range into LDS (direct
+// global->LDS copies), then puts all ST of its weight loads in flight, so the
+// copies wait only for themselves.  The tokens are the B operand: MTB blocks of
+// 16 token columns per unpacked weight word.  LDS row t holds the range's
+// ks bytes of token t with 16-byte slot s stored at slot s ^ (t & 15): the 16
+// lanes of a quarter-wave read 16 different token rows at one k without bank
+// conflicts.  One split: the epilogue stores y; several: exact int32 partial
+// sums for k_gemm_reduce.
+template <int ST, int MTB>
+__global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
+{
+    extern __shared__ __align__(1024) uint8_t sx_lds[];  // [16 MTB][ks], swizzled slots
+    constexpr int KS = ST * kStepWeights;                 // weights of the K range
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int split = blockIdx.y;
+    int rb = blockIdx.x;
+    GemmLayer Lw = a.L[0];
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i)
+        if (i < a.nl && rb >= a.L[i].tile0) Lw = a.L[i];
+    rb -= Lw.tile0;
+    const int K = a.k, M = a.m, N = Lw.n;
+    const int kb = split * KS;
+    const int len = min(KS, K - kb);
+
+    // 1. token rows [0, M) x k in [kb, kb + KS) -> LDS, 1 KB (64 slots) per copy;
+    //    slots past k read zeros or the next row: their weights are zero
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.q, (uint32_t)(M * K));
+    constexpr int CPR = KS / 1024;  // copies per token row
+    for (int c = wave; c < M * CPR; c += 4) {
+        const int t = c / CPR, slot = (c - t * CPR) * 64 + lane;
+        const int src = slot ^ (t & 15);
+        copy_to_lds(xr, sx_lds + c * 1024, t * K + kb + src * 16);
+    }
+    __asm__ volatile("" ::: "memory");  // the copies stay ahead of the weight loads
+
+    // 2. every weight load of this wave in flight: lane (r, kq) holds row r,
+    //    k in [kb + 256 j + 64 kq, +64) of step j
+    const int r = lane & 15, kq = lane >> 4;
+    const int row0 = rb * 64 + wave * 16;
+    // (uniform; readfirstlane keeps the clamp, and so the descriptor, scalar)
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, N - row0)));
+    const int rbytes = K >> 2;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(Lw.w + (int64_t)row0 * rbytes, (uint32_t)(rows * rbytes));
+    uint4 buf[ST];
+#pragma unroll
+    for (int j = 0; j < ST; ++j)
+        buf[j] = bload(wr, j * kStepWeights + kq * 64 < len ? r * rbytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
+    __builtin_amdgcn_sched_barrier(0);  // all ST loads issue before any of them is consumed
+
+    // 3. the copies (issued first) have landed once at most ST loads are outstanding
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(ST));
+    __syncthreads();
+
+    // 4. contraction: A = 16 weight rows, B = 16 token columns per block
+    v4i acc[MTB];
+#pragma unroll
+    for (int tb = 0; tb < MTB; ++tb) acc[tb] = v4i{0, 0, 0, 0};
+    const int tsw = lane & 15;  // (t & 15) of this lane's token row
+    const uint8_t* brow = sx_lds + (lane & 15) * KS;
+#pragma unroll
+    for (int j = 0; j < ST; ++j) {
+        const uint32_t wd[4] = {buf[j].x, buf[j].y, buf[j].z, buf[j].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const v4i av = unpack16(wd[w]);
+            const int slot = (16 * j + 4 * kq + w) ^ tsw;
+#pragma unroll
+            for (int tb = 0; tb < MTB; ++tb) {
+                const v4i bv = *(const v4i*)(brow + tb * 16 * KS + slot * 16);
+                acc[tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[tb], 0, 0, 0);
+            }
+        }
+    }
+
+    // 5. D lane l element v: weight row 4 (l >> 4) + v, token column l & 15
+    const int nb = row0 + 4 * kq;
+    if (a.splits > 1) {
+        const int ncols = a.L[a.nl - 1].col0 + a.L[a.nl - 1].n;
+#pragma unroll
+        for (int tb = 0; tb < MTB; ++tb) {
+            const int t = tb * 16 + (lane & 15);
+            if (t < M) {
+                int32_t* prow = a.part + ((int64_t)split * M + t) * ncols + Lw.col0;
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (nb + v < N) prow[nb + v] = acc[tb][v];
+            }
+        }
+        return;
+    }
+    const bool ybf = a.ykind == YK_BF16;
+#pragma unroll
+    for (int tb = 0; tb < MTB; ++tb) {
+        const int t = tb * 16 + (lane & 15);
+        if (t < M) {
+            const float c = __fmul_rn(a.sx[t], Lw.sw);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = nb + v;
+                if (n < N) {
+                    const int64_t o = (int64_t)t * N + n;
+                    const float yv = __fmul_rn((float)acc[tb][v], c);
+                    if (ybf) ((uint16_t*)Lw.y)[o] = f32_to_bf16(yv);
+                    else ((float*)Lw.y)[o] = yv;
+                    if (Lw.acc_out) Lw.acc_out[o] = acc[tb][v];
+                }
+            }
+        }
+    }
+}
+
+int gemv_bat_split(int64_t m, int64_t row_blocks, int64_t k, int* steps)
+{
+    // LDS holds the token rows of whole 16-row blocks (16, 32 or 64 rows) x ks
+    // bytes (<= 64 KB); ks shrinks from 4096 until the launch has ~448 workgroups
+    const int64_t mr = m <= 16 ? 16 : m <= 32 ? 32 : 64;
+    int64_t ks = 4096;
+    while (ks > 1024 && (mr * ks > 65536 || row_blocks * ((k + ks - 1) / ks) < 448)) ks >>= 1;
+    if (steps) *steps = (int)(ks / kStepWeights);
+    return (int)((k + ks - 1) / ks);
+}
+
+hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s)
+{
+    GemmArgs g = a;
+    int64_t rbs = 0, cols = 0;
+    for (int l = 0; l < g.nl; ++l) {
+        g.L[l].tile0 = (int)rbs;
+        g.L[l].col0 = (int)cols;
+        rbs += (g.L[l].n + 63) / 64;
+        cols += g.L[l].n;
+    }
+    if (rbs <= 0 || g.m <= 0) return hipSuccess;
+    const int mtb = (g.m + 15) / 16;
+    const int mr = mtb == 3 ? 64 : 16 * mtb;  // token rows the LDS tile spans (MTB = 1, 2, 4)
+    const int st = g.split_steps;
+    if (g.m > 64 || g.nl < 1 || g.nl > kMaxGroup || (st != 4 && st != 8 && st != 16) ||
+        (int64_t)mr * st * kStepWeights > 65536 || rbs > INT32_MAX ||
+        g.splits != (g.k + st * kStepWeights - 1) / (st * kStepWeights) || (g.splits > 1 && !g.part))
+        return hipErrorInvalidValue;
+    const size_t lds = (size_t)mr * st * kStepWeights;
+    const dim3 grid((unsigned)rbs, (unsigned)g.splits);
+#define BTL_BAT(STV, MTV)                                                                    \
+    if (st == STV && (mtb == MTV || (MTV == 4 && mtb == 3))) {                               \
+        hipLaunchKernelGGL((k_gemv_bat<STV, MTV>), grid, dim3(256), lds, s, g);              \
+    } else
+    BTL_BAT(4, 1) BTL_BAT(4, 2) BTL_BAT(4, 4) BTL_BAT(8, 1) BTL_BAT(8, 2) BTL_BAT(8, 4)
+    BTL_BAT(16, 1) BTL_BAT(16, 2) BTL_BAT(16, 4) return hipErrorInvalidValue;
+#undef BTL_BAT
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || g.splits == 1) return e;
+    const int64_t outs = (int64_t)g.m * cols;
+    const int64_t blocks = (outs + 255) / 256;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, s, g, (int)cols);
     return hipGetLastError();
 }
 

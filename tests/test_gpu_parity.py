@@ -119,19 +119,63 @@ def test_linear_i8_special_rows():
     assert np.all(y[1].cpu().numpy() == 0)
 
 
-@pytest.mark.parametrize("tiles", ["1", "2", "4"])
-@pytest.mark.parametrize("k", [4096, 14336, 320])
-def test_k_split_is_exact(tiles, k, monkeypatch):
-    # 4 / tiles waves of a workgroup split K and are summed through LDS
+@pytest.mark.parametrize("parts", ["4", "8"])
+@pytest.mark.parametrize("k", [4096, 1024, 320])
+def test_decode_k_parts_are_exact(parts, k, monkeypatch):
+    # the waves of a decode workgroup split K and are summed through LDS
     m, n = 2, 320
     x = activations(m, k, seed=11)
     pt, wb, sw = make_layer(n, k, seed=12)
-    monkeypatch.setenv("BTL_GEMV_TILES", tiles)
+    monkeypatch.setenv("BTL_GEMV_DEC_PARTS", parts)
     acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
     assert np.array_equal(acc.cpu().numpy(), accr)
     assert_f32_identical(y, yr)
+
+
+# batched decode / small prefill: k_gemv_bat (m <= 64) and the GEMM, both with
+# K split over workgroups.  (m, k, n): many splits; a K range past k; a half
+# last GEMM step; m = 2..4 where the decode kernel does not fit k = 14336;
+# exactly one 128-row tile; 17..32 and 33..64 token rows (2 and 4 B blocks)
+SPLIT_SHAPES = [(16, 14336, 256), (5, 4096, 300), (64, 1088, 1000), (2, 14336, 130), (4, 14336, 64),
+                (128, 2048, 130), (33, 256, 64), (20, 192, 70), (48, 8192, 200)]
+
+
+@pytest.mark.parametrize("route", ["bat", "gemm"])
+@pytest.mark.parametrize("m,k,n", SPLIT_SHAPES)
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
+def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, monkeypatch):
+    print("split-k", route, m, k, n, xdt, ydt, flush=True)
+    if route == "gemm":
+        monkeypatch.setenv("BTL_GEMV_BAT", "0")
+    else:
+        monkeypatch.setenv("BTL_GEMV_BAT_MAX_M", "64")  # the 33..64-row blocks too
+    x = activations(m, k, seed=m * 5 + k + n)
+    pt, wb, sw = make_layer(n, k, seed=n * 3 + k)
+    xt = to_dev(x, xdt)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, out_dtype=ydt, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    if ydt == torch.float32:
+        assert_f32_identical(y, yr)
+    else:
+        assert_bf16_matches(y, yr)
+
+
+@pytest.mark.parametrize("m,k,ns", [(20, 2048, (100, 64, 64)), (7, 14336, (300, 64)), (64, 4096, (1000, 200, 200))])
+def test_split_k_group_with_exact_caller_workspace(m, k, ns):
+    # a group's layers share one split-K launch; btl_workspace_bytes(m, sum n, k)
+    # is enough for it
+    x = to_dev(activations(m, k, seed=77), torch.bfloat16)
+    layers = [make_layer(n, k, seed=n + i) for i, n in enumerate(ns)]
+    ws = bl.Workspace(m, sum(ns), k, device=DEV)
+    ws.buf.fill_(0x5A)
+    outs = bl.linear_group([l[0] for l in layers], x, out_dtype=torch.float32, workspace=ws)
+    for (pt, wb, sw), n, y in zip(layers, ns, outs):
+        yr, _, _, _ = orc.forward_i8(host_x(x), wb, n, sw)
+        assert_f32_identical(y, yr)
 
 
 def test_caller_workspace_contents_do_not_matter():
