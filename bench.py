@@ -120,6 +120,20 @@ def time_launches(fn, reps, stream_obj):
     return 1000.0 * e0.elapsed_time(e1) / reps
 
 
+def profiled_traffic(name):
+    """HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE counter runs
+    summarised in profiles/<name> (see the commands there); None if absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(host_layers, seconds):
     """The reference's CPU BitLinear (cpu.rs, restated with AVX2 intrinsics and a
     thread pool, oracle/) on a bounded sample: the 7 projections of 4 of the 32
@@ -246,7 +260,10 @@ def run_decode(args):
                    "step_frac_hbm": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 3)},
         "roofline": {"bound": "hbm", "kernel": "k_gemv_dec<XK_BF16> gate|up 4096->2x14336 (W1.58-A8)",
                      "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dom["frac_hbm"], "traffic": None,
+                     "frac": dom["frac_hbm"],
+                     "traffic": profiled_traffic("k_gemv_dec_gate_up_decode_traffic.md"),
+                     "traffic_source": "profiles/k_gemv_dec_gate_up_decode_traffic.md (FETCH_SIZE x copy-calibrated "
+                                       "factor + WRITE_SIZE, bytes per launch)",
                      "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"]},
         "kernels": kern,
     }
@@ -340,8 +357,11 @@ def run_prefill(layers, gen, dev, args):
         "gemm_only_frac_int8": round(layer_ops / gemm_us / 1e6 / INT8_PEAK_TOPS, 3),
         "roofline": {"bound": "mfma", "kernel": "k_gemm_i8 gate|up 2048 x (2 x 14336) x 4096, one launch",
                      "achieved": dom["TOPS"], "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                     "frac": dom["frac_int8"], "traffic": None, "algorithmic_ops": dom["ops"],
-                     "avg_us": dom["us"]},
+                     "frac": dom["frac_int8"],
+                     "traffic": profiled_traffic("k_gemm_i8_gate_up_prefill_traffic.md"),
+                     "traffic_source": "profiles/k_gemm_i8_gate_up_prefill_traffic.md (bytes per launch crossing "
+                                       "the L2s; the 8 XCDs each fetch the weights once)",
+                     "algorithmic_ops": dom["ops"], "avg_us": dom["us"]},
         "kernels": kern,
     }
 
@@ -395,6 +415,39 @@ def run_sweep(layers, gen, dev, args):
             "rows": rows}
 
 
+def run_probe(args):
+    """A few launches of one workload, plus a plain copy of known size, for
+    counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy reads and
+    writes 256 MiB per dispatch and calibrates the counters.  Prints what ran."""
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bl.check(bl.lib.btl_init(0))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xB17EB17E)
+    stream = torch.cuda.current_stream().cuda_stream
+    gate, up = synth_packed(INTER, HIDDEN, gen, dev), synth_packed(INTER, HIDDEN, gen, dev)
+    if args.probe == "decode_gate_up":
+        x = synth_act(1, HIDDEN, gen, dev)
+        outs = [torch.empty((1, INTER), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+        call = Call([gate, up], x, outs)
+        what = "btl_linear_group gate|up, M=1, 4096 -> 2 x 14336, bf16 (k_gemv_dec)"
+    else:
+        x = synth_act(args.prefill_m, HIDDEN, gen, dev)
+        q, s = bl.quantize_act_op(x)
+        outs = [torch.empty((args.prefill_m, INTER), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+        call = OpCall([gate, up], q, s, outs)
+        what = "btl_linear_i8_op gate|up, M=%d, 4096 -> 2 x 14336, bf16 (k_gemm_i8)" % args.prefill_m
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(7)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        call(stream)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("probe: %d x %s; 3 x copy of 268435456 bytes" % (args.steps, what), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -407,6 +460,8 @@ def main():
     ap.add_argument("--prefill-m", type=int, default=2048)
     ap.add_argument("--no-sweep", dest="sweep", action="store_false",
                     help="skip the cfg3 batched-decode section of the JSON line")
+    ap.add_argument("--probe", choices=["decode_gate_up", "prefill_gate_up"], default=None,
+                    help="counter-run mode: --steps launches of one workload and a 256 MiB copy; no JSON")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -416,6 +471,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         sys.exit(1)
+    if args.probe:
+        run_probe(args)
+        return
     run_decode(args)
 
 
