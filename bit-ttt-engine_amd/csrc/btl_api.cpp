@@ -227,14 +227,24 @@ int64_t gemv_row_blocks(const Layer* layers, int count)
     return t;
 }
 
-// Decode kernel geometry for m <= 4 token rows: the fewest waves (4 or 8)
-// whose K parts hold the part's activations in registers; 0 when none does.
-int dec_waves(int64_t m, int64_t k)
+// Decode kernel geometry for m <= 4 token rows (measured on MI355X with the
+// Llama-3-8B shapes): K parts of 1024 weights, or of 2048 where that would
+// take more than 8 waves (k > 8192); RB = 4 / WV row blocks per workgroup
+// when WV divides 4, else 1.  BTL_GEMV_DEC_PARTS forces WV (1..16).  0 when
+// the tokens do not fit the prologue or the parts exceed 2048 weights.
+int dec_waves(int64_t m, int64_t k, int* rb_out)
 {
-    if (m > 4) return 0;
-    for (int w = 4; w <= 8; w *= 2)
-        if (m * (ceil_div(ceil_div(k, w), btl::kStepWeights) * btl::kStepWeights) <= btl::kDecMaxPart) return w;
-    return 0;
+    if (m < 1 || m > 4 || k <= 0) return 0;
+    int w = (int)ceil_div(k, 1024);
+    if (w > 8) w = (int)ceil_div(k, 2048);
+    const int forced = env_int("BTL_GEMV_DEC_PARTS", 0);
+    if (forced >= 1 && forced <= 16) w = forced;
+    const int rb = (w == 1 || w == 2 || w == 4) ? 4 / w : 1;
+    const int64_t kp = ceil_div(ceil_div(k, w), btl::kStepWeights) * btl::kStepWeights;
+    if (w > 16 || w * rb > 16 || kp > 8 * btl::kStepWeights || m * (k / 16) > (int64_t)btl::kDecGroups * 64 * w * rb)
+        return 0;
+    *rb_out = rb;
+    return w;
 }
 
 // W1.58-A8 contraction of `count` layers sharing one input.
@@ -281,20 +291,12 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         return BTL_OK;
     }
 
-    // Decode (1..4 token rows): 16*tiles rows per workgroup, its waves split K.
-    int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k) : 0;
+    // Decode (1..4 token rows): RB row blocks of 16 rows per workgroup, WV
+    // waves per row block splitting K.
+    int rbw = 1;
+    const int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k, &rbw) : 0;
     if (wv > 0) {
-        // defaults measured on MI355X (Llama-3-8B shapes): the fewest waves
-        // that hold a part in registers, one 16-row tile per wave
-        int64_t kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
-        int rt = 1;
-        const int frt = env_int("BTL_GEMV_DEC_TILES", 0);
-        if (frt == 1 || frt == 2 || frt == 4) rt = frt;
-        const int fwv = env_int("BTL_GEMV_DEC_PARTS", 0);
-        if ((fwv == 4 || fwv == 8) && m * ceil_div(ceil_div(k, fwv), 256) * 256 <= btl::kDecMaxPart) {
-            wv = fwv;
-            kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
-        }
+        const int64_t kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
         btl::GemvArgs a;
         memset(&a, 0, sizeof(a));
         int rb = 0, np = 0;
@@ -308,7 +310,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             p.sw = layers[i].w->scale;
             p.n = (int)n;
             p.rb_begin = rb;
-            rb += (int)ceil_div(n, 16 * rt);
+            rb += (int)ceil_div(n, 16);
         }
         a.nprob = np;
         a.x = x;
@@ -316,7 +318,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.m = (int)m;
         a.k = (int)k;
         a.rb_total = rb;
-        a.tiles = rt;
+        a.tiles = rbw;
         a.parts = wv;
         a.kpart = (int)kpart;
         a.ykind = ykind;

@@ -30,17 +30,16 @@ struct GemvArgs {
     const void* x;    // [m, k]: f32 / bf16 (fused quantisation) or int8 (XK_I8)
     const float* xs;  // XK_I8 only: per-row activation scales [m]
     int m, k;
-    int rb_total;     // row-blocks over all layers (grid.x)
-    int tiles;        // 16-row tiles per row-block (1, 2 or 4)
-    int parts;        // waves per workgroup, each one K part (4 or 8)
-    int kpart;        // weights per K part (multiple of 256)
+    int rb_total;     // 16-row blocks over all layers
+    int tiles;        // RB: row blocks per workgroup
+    int parts;        // WV: waves per row block, each one K part (WV * RB <= 16)
+    int kpart;        // weights per K part (multiple of 256, at most 2048)
     int ykind;        // YK_F32 / YK_BF16
 };
 
-// Decode (k_gemv_dec): a.tiles (1, 2, 4) 16-row tiles per wave, a.parts (4 or
-// 8) waves split K, a.m <= 4, a.m * a.kpart <= kDecMaxPart and
-// a.tiles * ceil(a.kpart / 256) <= 16 wave-loads per lane.
-constexpr int kDecMaxPart = 2048;
+// Decode (k_gemv_dec): parts * tiles <= 16, parts * kpart >= k, kpart <= 2048,
+// a.m <= 4, a.m * k / 16 <= kDecGroups * 64 * parts * tiles.
+constexpr int kDecGroups = 4;  // 16-element token groups per thread in the prologue
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s);
 
 // Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op or

@@ -168,17 +168,17 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d)
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
-// k_gemv_dec: decode (1..4 token rows), one 16-row tile per workgroup
+// k_gemv_dec: decode (1..4 token rows)
 // ---------------------------------------------------------------------------
-// The WV waves of a workgroup split K into parts of kpart weights; wave p owns
-// part p of the same 16 rows.  Each wave first loads its part of the
-// activations into registers (at most kDecGroups 16-element groups per lane),
-// then puts all its weight loads in flight, so the activation prologue waits
-// only for its own loads.  The partial absmax of the WV parts meet in LDS (one
-// barrier); every wave then quantises its own part into a wave-private LDS
-// region in operand order.  Parts are summed exactly through LDS at the end.
-constexpr int kDecGroups = 2;  // 16-element activation groups per lane
-
+// A workgroup owns RB row blocks of 16 weight rows and splits K into WV parts
+// (both runtime, WV * RB <= 16): wave w works on row block w / WV, K part
+// w % WV (kpart weights, at most ST loads of 256 weights per lane).  The workgroup first loads the token rows (every
+// thread a few 16-element groups, issued before the weights), then each wave
+// puts all of its weight loads in flight; the absmax of each row is reduced
+// over the workgroup (DPP + LDS), and every thread quantises its groups into
+// one shared LDS copy of the rows in operand order -- once per workgroup, so
+// RB > 1 amortises this prologue over more weights.  The K parts of a row
+// block are summed exactly through LDS; the part-0 wave applies the epilogue.
 template <int XK>
 struct DecX {
     static constexpr int kVec = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);  // uint4 per group
@@ -266,20 +266,20 @@ __device__ __forceinline__ uint32_t wave_max_dpp(uint32_t v)
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-// ST: wave-loads per row tile per wave (compile time, >= the part's steps;
-// the loads past the part read zeros, so every step runs unconditionally).
-// RT: 16-row tiles per wave (they share the activation prologue and the
-// B-operand reads).  MT: token rows, 1 or up to 4.  The workgroup covers
-// 16*RT rows; its WV waves split K.
-template <int XK, int WV, int ST, int RT, int MT>
-__global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
-{
-    extern __shared__ __align__(16) uint8_t sq[];  // [WV][mt][kpart + 16]
-    __shared__ uint32_t s_amax[WV][MT];
-    __shared__ v4i s_red[WV > 1 ? (WV - 1) * RT : 1][64];
 
-    const int tid = threadIdx.x, lane = tid & 63, part = tid >> 6;
-    const int rbg = blockIdx.x;
+template <int XK, int ST, int MT>
+__global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
+{
+    const int WV = a.parts, RB = a.tiles;  // NW = WV * RB <= 16 waves
+    const int NW = WV * RB, NT = NW * 64;
+    extern __shared__ __align__(16) uint8_t sq[];  // [mt][k + 16], operand order
+    __shared__ uint32_t s_amax[16][MT];
+    __shared__ v4i s_red[16][64];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rbi = wave / WV, part = wave - rbi * WV;
+    const int rbg = blockIdx.x * RB + rbi;  // past rb_total: no rows (zero loads, no stores)
     const int mt = MT == 1 ? 1 : min(MT, a.m);
 
     const uint8_t* W = a.p[0].w;
@@ -299,45 +299,41 @@ __global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
     const int kp = a.kpart;
     const int kb = part * kp;
     const int len = max(0, min(kp, K - kb));
-    const int lpw = kp + 16;
-    uint8_t* myq = sq + part * (mt * lpw);
+    const int lp = K + 16;
 
-    // 1. this wave's activations -> registers (issued before the weight loads)
+    // 1. the token rows -> registers, kDecGroups 16-element groups per thread at
+    //    most (issued before the weight loads)
     constexpr int NV = DecX<XK>::kVec;
     constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);  // bytes per element
-    const int gpr = len >> 4;  // 16-element groups per token row in this part
+    const int gpr = K >> 4;  // groups per token row
     const int ng = mt * gpr;
     int gm_[kDecGroups], gc_[kDecGroups];
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(mt * K * ES));
     uint4 xv[kDecGroups][NV];
 #pragma unroll
     for (int gi = 0; gi < kDecGroups; ++gi) {
-        const int g = lane + 64 * gi;
+        const int g = tid + NT * gi;
         const int m = MT == 1 ? 0 : g / max(gpr, 1);
         gm_[gi] = m;
         gc_[gi] = g - m * gpr;
-        const int off = g < ng ? (m * K + kb + 16 * gc_[gi]) * ES : kOOB;
+        const int off = g < ng ? (m * K + 16 * gc_[gi]) * ES : kOOB;
 #pragma unroll
-        for (int h = 0; h < NV; ++h) xv[gi][h] = gi == 0 || 64 * gi < ng ? bload(xr, off + 16 * h) : uint4{0u, 0u, 0u, 0u};
+        for (int h = 0; h < NV; ++h) xv[gi][h] = gi == 0 || NT * gi < ng ? bload(xr, off + 16 * h) : uint4{0u, 0u, 0u, 0u};
     }
 
     // 2. every weight load of this wave in flight
     const int r = lane & 15, kq = lane >> 4;
-    const int row0 = (rbg - RB0) * (16 * RT);
-    const int rows = min(16 * RT, N - row0);
+    const int row0 = (rbg - RB0) * 16;
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, N - row0)));
     const int rb_bytes = K >> 2;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(W + (int64_t)row0 * rb_bytes, (uint32_t)(rows * rb_bytes));
-    uint4 buf[RT][ST];
+    uint4 buf[ST];
 #pragma unroll
-    for (int j = 0; j < ST; ++j) {
-        const bool kin = j * kStepWeights + kq * 64 < len;
-#pragma unroll
-        for (int t = 0; t < RT; ++t)
-            buf[t][j] = bload(wr, kin ? (t * 16 + r) * rb_bytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
-    }
+    for (int j = 0; j < ST; ++j)
+        buf[j] = bload(wr, j * kStepWeights + kq * 64 < len ? r * rb_bytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
 
-    // 3. absmax of each token row: per-wave partials meet in LDS; lane m then
-    //    holds the quantisation parameters of token row m
+    // 3. absmax of each token row over the workgroup; lane m then holds the
+    //    quantisation parameters of token row m
     float r_l = 0.0f, s_l = 0.0f;
     if (XK != XK_I8) {
         uint32_t am[MT];
@@ -345,8 +341,8 @@ __global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
         for (int mm = 0; mm < MT; ++mm) am[mm] = 0u;
 #pragma unroll
         for (int gi = 0; gi < kDecGroups; ++gi) {
-            if (gi == 0 || 64 * gi < ng) {
-                const uint32_t v = lane + 64 * gi < ng ? group_absmax<XK>(xv[gi]) : 0u;
+            if (gi == 0 || NT * gi < ng) {
+                const uint32_t v = tid + NT * gi < ng ? group_absmax<XK>(xv[gi]) : 0u;
 #pragma unroll
                 for (int mm = 0; mm < MT; ++mm) am[mm] = (MT == 1 || mm == gm_[gi]) ? max(am[mm], v) : am[mm];
             }
@@ -355,14 +351,13 @@ __global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
         for (int mm = 0; mm < MT; ++mm) {
             if (mm < mt) {
                 const uint32_t v = wave_max_dpp(am[mm]);
-                if (lane == 0) s_amax[part][mm] = v;
+                if (lane == 0) s_amax[wave][mm] = v;
             }
         }
         __syncthreads();
         const int lm = MT == 1 ? 0 : min(lane, mt - 1);
         uint32_t v = 0;
-#pragma unroll
-        for (int p = 0; p < WV; ++p) v = max(v, s_amax[p][lm]);
+        for (int w = 0; w < NW; ++w) v = max(v, s_amax[w][lm]);
         const QParams qp = qparams(v);
         r_l = qp.ok ? qp.r : 0.0f;
         s_l = qp.s;
@@ -370,27 +365,27 @@ __global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
         s_l = a.xs[MT == 1 ? 0 : min(lane, mt - 1)];
     }
 
-    // 4. quantise this wave's part into its LDS region (wave-private: no barrier)
+    // 4. quantise this thread's groups into the shared rows
 #pragma unroll
     for (int gi = 0; gi < kDecGroups; ++gi) {
-        if (gi == 0 || 64 * gi < ng) {
-            const int g = lane + 64 * gi;
+        if (gi == 0 || NT * gi < ng) {
+            const int g = tid + NT * gi;
             float rm = r_l;
             if (MT > 1) rm = __shfl(r_l, gm_[gi], 64);
             uint4 q = group_quant<XK>(xv[gi], rm);
             if (XK != XK_I8 && rm == 0.0f) q = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
-            if (g < ng) *(uint4*)(myq + gm_[gi] * lpw + 16 * gc_[gi]) = q;
+            if (g < ng) *(uint4*)(sq + gm_[gi] * lp + 16 * gc_[gi]) = q;
         }
     }
+    __syncthreads();
 
     // 5. contraction.  B lanes of token columns >= mt read row 0: those
     //    columns of D are never stored.
     const int mcol = lane & 15;
     const bool m_ok = mcol < mt;
-    const uint8_t* bq = myq + (m_ok ? mcol : 0) * lpw + kq * 64;
-    v4i acc[RT][2];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) acc[t][0] = acc[t][1] = v4i{0, 0, 0, 0};
+    const uint8_t* bq = sq + (m_ok ? mcol : 0) * lp + kb + kq * 64;
+    v4i acc[2];
+    acc[0] = acc[1] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < ST; ++j) {
         const uint8_t* bj = bq + j * kStepWeights;
@@ -398,49 +393,35 @@ __global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
         const v4i b1 = *(const v4i*)(bj + 16);
         const v4i b2 = *(const v4i*)(bj + 32);
         const v4i b3 = *(const v4i*)(bj + 48);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const uint4 cur = buf[t][j];
-            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc[t][1], 0, 0, 0);
-            acc[t][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc[t][1], 0, 0, 0);
-        }
+        const uint4 cur = buf[j];
+        acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc[1], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc[1], 0, 0, 0);
     }
-    v4i res[RT];
-#pragma unroll
-    for (int t = 0; t < RT; ++t) res[t] = acc[t][0] + acc[t][1];
+    v4i res = acc[0] + acc[1];
 
-    // 6. sum the parts (exact), epilogue by wave 0
+    // 6. sum the K parts of each row block (exact), epilogue by its part-0 wave
     if (WV > 1) {
-        if (part > 0) {
-#pragma unroll
-            for (int t = 0; t < RT; ++t) s_red[(part - 1) * RT + t][lane] = res[t];
-        }
+        if (part > 0) s_red[wave][lane] = res;
         __syncthreads();
         if (part > 0) return;
-#pragma unroll
-        for (int p = 1; p < WV; ++p)
-#pragma unroll
-            for (int t = 0; t < RT; ++t) res[t] += s_red[(p - 1) * RT + t][lane];
+        for (int p = 1; p < WV; ++p) res += s_red[wave + p][lane];
     }
     const float sx = MT == 1 ? s_l : __shfl(s_l, mcol < mt ? mcol : 0, 64);
     if (!m_ok) return;
     const float c = __fmul_rn(sx, SW);
     const bool ybf = a.ykind == YK_BF16;
+    const int nb = row0 + 4 * (lane >> 4);
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        const int nb = row0 + 16 * t + 4 * (lane >> 4);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = nb + v;
-            if (n < N) {
-                const int64_t o = (int64_t)mcol * N + n;
-                const float yv = __fmul_rn((float)res[t][v], c);
-                if (ybf) ((uint16_t*)Y)[o] = f32_to_bf16(yv);
-                else ((float*)Y)[o] = yv;
-                if (ACC) ACC[o] = res[t][v];
-            }
+    for (int v = 0; v < 4; ++v) {
+        const int n = nb + v;
+        if (n < N) {
+            const int64_t o = (int64_t)mcol * N + n;
+            const float yv = __fmul_rn((float)res[v], c);
+            if (ybf) ((uint16_t*)Y)[o] = f32_to_bf16(yv);
+            else ((float*)Y)[o] = yv;
+            if (ACC) ACC[o] = res[v];
         }
     }
 }
@@ -448,29 +429,24 @@ __global__ __launch_bounds__(WV * 64) void k_gemv_dec(GemvArgs a)
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s)
 {
     (void)mtiles;
-    dim3 grid((unsigned)a.rb_total);
-    const int mt = a.m;
-    const int wv = a.parts, rt = a.tiles;
+    const int wv = a.parts, rb = a.tiles;
     const int st_need = (a.kpart + kStepWeights - 1) / kStepWeights;
-    const int st = st_need <= 2 ? 2 : st_need <= 4 ? 4 : 8;
-    const int mtk = mt == 1 ? 1 : 4;
-    const size_t lds = (size_t)wv * mt * (size_t)(a.kpart + 16);
-#define BTL_DEC_CASE(XKV, WVV, STV, RTV, MTV)                                                        \
-    if (xkind == XKV && wv == WVV && st == STV && rt == RTV && mtk == MTV) {                         \
-        hipLaunchKernelGGL((k_gemv_dec<XKV, WVV, STV, RTV, MTV>), grid, dim3(WVV * 64), lds, s, a);  \
-        return hipGetLastError();                                                                    \
+    if (wv < 1 || rb < 1 || wv * rb > 16 || st_need > 8 || a.m < 1 || a.m > 4 ||
+        (int64_t)wv * a.kpart < a.k || (int64_t)a.m * (a.k >> 4) > (int64_t)kDecGroups * wv * rb * 64)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.rb_total + rb - 1) / rb)), block((unsigned)(wv * rb * 64));
+    const size_t lds = (size_t)a.m * (size_t)(a.k + 16);
+    const bool st4 = st_need <= 4;
+    const bool mt1 = a.m == 1;
+#define BTL_DEC_CASE(XKV)                                                                             \
+    if (xkind == XKV) {                                                                               \
+        if (st4 && mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 1>), grid, block, lds, s, a);          \
+        else if (st4) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 4>), grid, block, lds, s, a);            \
+        else if (mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 1>), grid, block, lds, s, a);            \
+        else hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 4>), grid, block, lds, s, a);                     \
+        return hipGetLastError();                                                                     \
     }
-#define BTL_DEC_SHAPES(XKV, WVV, MTV)                                                                   \
-    BTL_DEC_CASE(XKV, WVV, 2, 1, MTV) BTL_DEC_CASE(XKV, WVV, 2, 2, MTV) BTL_DEC_CASE(XKV, WVV, 2, 4, MTV)  \
-    BTL_DEC_CASE(XKV, WVV, 4, 1, MTV) BTL_DEC_CASE(XKV, WVV, 4, 2, MTV) BTL_DEC_CASE(XKV, WVV, 4, 4, MTV)  \
-    BTL_DEC_CASE(XKV, WVV, 8, 1, MTV) BTL_DEC_CASE(XKV, WVV, 8, 2, MTV)
-#define BTL_DEC_WV(WVV, MTV) BTL_DEC_SHAPES(XK_F32, WVV, MTV) BTL_DEC_SHAPES(XK_BF16, WVV, MTV) BTL_DEC_SHAPES(XK_I8, WVV, MTV)
-    BTL_DEC_WV(4, 1)
-    BTL_DEC_WV(8, 1)
-    BTL_DEC_WV(4, 4)
-    BTL_DEC_WV(8, 4)
-#undef BTL_DEC_WV
-#undef BTL_DEC_SHAPES
+    BTL_DEC_CASE(XK_BF16) BTL_DEC_CASE(XK_F32) BTL_DEC_CASE(XK_I8)
 #undef BTL_DEC_CASE
     return hipErrorInvalidValue;
 }

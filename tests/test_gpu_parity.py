@@ -119,11 +119,15 @@ def test_linear_i8_special_rows():
     assert np.all(y[1].cpu().numpy() == 0)
 
 
-@pytest.mark.parametrize("parts", ["4", "8"])
-@pytest.mark.parametrize("k", [4096, 1024, 320])
-def test_decode_k_parts_are_exact(parts, k, monkeypatch):
-    # the waves of a decode workgroup split K and are summed through LDS
-    m, n = 2, 320
+@pytest.mark.parametrize("k,parts", [(4096, "2"), (4096, "3"), (4096, "4"), (4096, "16"), (1024, "1"),
+                                     (1024, "4"), (320, "1"), (14336, "7"), (14336, "8"), (14336, "14")])
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_decode_k_parts_are_exact(parts, k, m, monkeypatch):
+    # a decode workgroup: 4 / parts row blocks (when parts divides 4), each
+    # split into `parts` K parts summed through LDS; n = 330 leaves a partial
+    # row block and a workgroup with row blocks past the end.  Shapes whose
+    # tokens do not fit the prologue take the batched route instead.
+    n = 330
     x = activations(m, k, seed=11)
     pt, wb, sw = make_layer(n, k, seed=12)
     monkeypatch.setenv("BTL_GEMV_DEC_PARTS", parts)
