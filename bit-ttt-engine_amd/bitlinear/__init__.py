@@ -19,5 +19,5 @@ from ._lib import (  # noqa: F401
 from .packed import PackedTensor  # noqa: F401
 from .layer import (  # noqa: F401
     BitLinear, BitLinearHip, Workspace, linear_group, linear_i8, linear_i8_op, quantize_act,
-    quantize_act_op,
+    quantize_act_op, rmsnorm_linear_group, swiglu_linear_group,
 )

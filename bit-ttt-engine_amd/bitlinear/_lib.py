@@ -29,6 +29,7 @@ EXPORTS = (
     "btl_version", "btl_last_error", "btl_status_string", "btl_init", "btl_packed_bytes",
     "btl_pack_host", "btl_unpack_host", "btl_unpack_device", "btl_quantize_act", "btl_linear",
     "btl_linear_i8", "btl_linear_group", "btl_quantize_act_op", "btl_linear_i8_op",
+    "btl_rmsnorm_linear_group", "btl_swiglu_linear_group",
     "btl_workspace_bytes", "btl_workspace_clear",
 )
 
@@ -68,6 +69,9 @@ def _load():
         "btl_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, i32, i64, i64, i32, vp, sz, vp]),
         "btl_quantize_act_op": (i32, [vp, i32, i64, i64, vp, vp, vp]),
         "btl_linear_i8_op": (i32, [P(P(BtlPacked)), P(vp), P(vp), i32, vp, vp, i64, i64, i32, vp]),
+        "btl_rmsnorm_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, i32, vp, f32, i64, i64, i32, vp, sz,
+                                           vp]),
+        "btl_swiglu_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, i32, i64, i64, i32, vp, sz, vp]),
         "btl_workspace_bytes": (sz, [i64, i64, i64, i32]),
         "btl_workspace_clear": (i32, [vp, sz, vp]),
     }

@@ -143,6 +143,47 @@ def linear_i8_op(q, s, weights, out_dtype=torch.float32, acc_out=None, outputs=N
     return outputs
 
 
+def _group_args(weights, m, dtype, device, outputs):
+    if outputs is None:
+        outputs = [torch.empty((m, w.dims2()[0]), dtype=dtype, device=device) for w in weights]
+    cs = [w.as_c() for w in weights]
+    arr = (ctypes.POINTER(BtlPacked) * len(cs))(*[ctypes.pointer(c) for c in cs])
+    ys = (ctypes.c_void_p * len(cs))(*[o.data_ptr() if o.numel() else None for o in outputs])
+    return outputs, cs, arr, ys
+
+
+def rmsnorm_linear_group(weights, x, g, eps, out_dtype=None, workspace=None, outputs=None):
+    """btl_rmsnorm_linear_group: BitLinear layers applied to RMSNorm(x) * g
+    (rms_norm.rs:33-56) without materialising the normalised tensor."""
+    _on_gpu(x, "input")
+    m, k = x.shape
+    out_dtype = out_dtype or x.dtype
+    g = g.to(device=x.device, dtype=torch.float32).contiguous()
+    outputs, cs, arr, ys = _group_args(weights, m, out_dtype, x.device, outputs)
+    wsp, wsn = _ws_args(workspace)
+    check(lib.btl_rmsnorm_linear_group(arr, ys, len(cs), x.data_ptr() if x.numel() else None,
+                                       _dtype_code(x, "input"), g.data_ptr(), float(eps), m, k,
+                                       _dtype_code(outputs[0], "output"), wsp, wsn, _stream(x.device)))
+    return outputs
+
+
+def swiglu_linear_group(weights, gate, up, out_dtype=None, workspace=None, outputs=None):
+    """btl_swiglu_linear_group: BitLinear layers applied to silu(gate) * up
+    (swiglu.rs:29-35) without materialising the hidden tensor."""
+    _on_gpu(gate, "gate")
+    _on_gpu(up, "up")
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise BitLinearError(1, "gate and up must have the same shape and dtype")
+    m, k = gate.shape
+    out_dtype = out_dtype or gate.dtype
+    outputs, cs, arr, ys = _group_args(weights, m, out_dtype, gate.device, outputs)
+    wsp, wsn = _ws_args(workspace)
+    check(lib.btl_swiglu_linear_group(arr, ys, len(cs), gate.data_ptr() if gate.numel() else None,
+                                      up.data_ptr() if up.numel() else None, _dtype_code(gate, "input"), m, k,
+                                      _dtype_code(outputs[0], "output"), wsp, wsn, _stream(gate.device)))
+    return outputs
+
+
 def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None):
     """Several layers reading the same input in one launch (q|k|v, w1|w3)."""
     _on_gpu(x, "input")

@@ -247,13 +247,26 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
     return w;
 }
 
+// Activation transform fused ahead of the quantisation (btl_rmsnorm_linear_group,
+// btl_swiglu_linear_group).
+struct Xform {
+    int kind;        // btl::XF_*
+    const void* x2;  // XF_SWIGLU: the up projection's output
+    const float* g;  // XF_RMSNORM: the norm weight [k]
+    float eps;
+};
+
 // W1.58-A8 contraction of `count` layers sharing one input.
 //   any k % 4 == 0 / any alignment .... quantise into scratch, k_generic_i8
 //   m <= 4 (decode) ................... k_gemv_dec, quantisation fused
 //   otherwise (batched decode, prefill)  quantise in operand order into the
-//                                        workspace, one (split-K) GEMM launch
+//                                        workspace, one (split-K) launch of
+//                                        k_gemv_bat (m <= 32) or k_gemm_i8
+// With a transform (xf), the transform + quantisation runs first into the
+// workspace on every route (k % 64 == 0 and aligned inputs are checked by the
+// caller) and the decode kernel reads the operand-order rows.
 int run_i8(const Layer* layers, int count, const void* x, int xkind, const float* xs, int64_t m,
-           int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st)
+           int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st, const Xform* xf = nullptr)
 {
     int dev;
     int rc = current_device(&dev);
@@ -266,6 +279,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     }
     if (m == 0 || nsum == 0) return BTL_OK;
     if (!x) return fail(BTL_ERR_LAYOUT, "null input");
+    if (xf && !fast) return fail(BTL_ERR_LAYOUT, "fused transform needs k %% 64 == 0 and 16-byte aligned tensors");
     hipError_t e;
 
     if (!fast) {
@@ -291,11 +305,41 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         return BTL_OK;
     }
 
-    // Decode (1..4 token rows): RB row blocks of 16 rows per workgroup, WV
-    // waves per row block splitting K.
+    // Route.  Decode (1..4 token rows): RB row blocks of 16 rows per
+    // workgroup, WV waves per row block splitting K.  Batched decode (m <= 32;
+    // measured on MI355X: the GEMM is faster from m = 64, Llama-3-8B MLP
+    // shapes) and GEMM: K split over workgroups when the output has few tiles.
     int rbw = 1;
     const int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k, &rbw) : 0;
-    if (wv > 0) {
+    const bool dec = wv > 0;
+    const bool bat = !dec && m <= env_int("BTL_GEMV_BAT_MAX_M", 32) && m <= 64 && env_int("BTL_GEMV_BAT", 1) != 0;
+    int split_steps = 0, splits = 1;
+    if (!dec)
+        splits = bat ? btl::gemv_bat_split(m, gemv_row_blocks(layers, count), k, &split_steps)
+                     : btl::gemm_splits(m, gemm_tiles_n(layers, count), k, &split_steps);
+
+    // operand-order quantisation into the workspace (all routes but plain decode)
+    const bool pre = xf || !dec;
+    const int8_t* q = nullptr;
+    const float* sxp = xs;
+    void* ws = nullptr;
+    WsLayout L = ws_layout(m, k, splits > 1 ? (size_t)splits * m * nsum * 4 : 0);
+    if (pre) {
+        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
+        q = (const int8_t*)ws + L.q_off;
+        if (xf) {
+            sxp = (const float*)((uint8_t*)ws + L.s_off);
+            e = btl::launch_xform_quant(x, xf->x2, xkind, xf->kind, xf->g, xf->eps, m, k, (int8_t*)q, (float*)sxp, st);
+        } else if (xkind == btl::XK_I8) {
+            e = btl::launch_op_order((const int8_t*)x, m, k, (int8_t*)q, st);
+        } else {
+            sxp = (const float*)((uint8_t*)ws + L.s_off);
+            e = btl::launch_quant_op(x, xkind, m, k, (int8_t*)q, (float*)sxp, st);
+        }
+        if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
+    }
+
+    if (dec) {
         const int64_t kpart = ceil_div(ceil_div(k, wv), btl::kStepWeights) * btl::kStepWeights;
         btl::GemvArgs a;
         memset(&a, 0, sizeof(a));
@@ -313,8 +357,8 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             rb += (int)ceil_div(n, 16);
         }
         a.nprob = np;
-        a.x = x;
-        a.xs = xs;
+        a.x = pre ? (const void*)q : x;
+        a.xs = sxp;
         a.m = (int)m;
         a.k = (int)k;
         a.rb_total = rb;
@@ -322,34 +366,37 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.parts = wv;
         a.kpart = (int)kpart;
         a.ykind = ykind;
-        e = btl::launch_gemv_dec(a, xkind, 1, st);
+        e = btl::launch_gemv_dec(a, pre ? (int)btl::XK_I8O : xkind, 1, st);
         if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
         return BTL_OK;
     }
-
-    // Batched decode (m <= 32; measured on MI355X: the GEMM is faster from
-    // m = 64, Llama-3-8B MLP shapes) and GEMM: quantise once in operand order
-    // (or reorder pre-quantised rows) into the workspace; split K over
-    // workgroups when the output has few tiles.
-    const bool bat = m <= env_int("BTL_GEMV_BAT_MAX_M", 32) && m <= 64 && env_int("BTL_GEMV_BAT", 1) != 0;
-    int split_steps = 0;
-    const int splits = bat ? btl::gemv_bat_split(m, gemv_row_blocks(layers, count), k, &split_steps)
-                           : btl::gemm_splits(m, gemm_tiles_n(layers, count), k, &split_steps);
-    const WsLayout L = ws_layout(m, k, splits > 1 ? (size_t)splits * m * nsum * 4 : 0);
-    void* ws = nullptr;
-    if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
-    const int8_t* q = (const int8_t*)ws + L.q_off;
-    const float* sxp = xs;
-    if (xkind == btl::XK_I8) {
-        e = btl::launch_op_order((const int8_t*)x, m, k, (int8_t*)q, st);
-    } else {
-        sxp = (const float*)((uint8_t*)ws + L.s_off);
-        e = btl::launch_quant_op(x, xkind, m, k, (int8_t*)q, (float*)sxp, st);
-    }
-    if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
     e = launch_gemm(layers, count, q, sxp, m, k, ykind, splits, split_steps,
                     splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr, bat, st);
     if (e != hipSuccess) return hip_fail(e, bat ? "batched gemv kernel launch" : "gemm kernel launch");
+    return BTL_OK;
+}
+
+// Shared validation of the fused entry points; fills `ls`.
+int check_group(const btl_packed_t* const* w, void* const* y, int count, int64_t m, int64_t k,
+                int ydtype, Layer* ls)
+{
+    if (count < 1 || count > btl::kMaxGroup) return fail(BTL_ERR_ARG, "count %d not in 1..%d", count, btl::kMaxGroup);
+    if (!w || !y) return fail(BTL_ERR_ARG, "null layer array");
+    int rc;
+    if ((rc = check_dtype(ydtype, "output"))) return rc;
+    for (int i = 0; i < count; ++i) {
+        if ((rc = check_packed(w[i], m, k))) return rc;
+        if (!y[i] && m > 0 && w[i]->n > 0) return fail(BTL_ERR_LAYOUT, "null output %d", i);
+        ls[i] = Layer{w[i], y[i], nullptr};
+    }
+    return BTL_OK;
+}
+
+int check_fused_shape(int64_t k, int64_t kmax, const char* what)
+{
+    if (k % 64 != 0 || k < 64 || k > kmax)
+        return fail(BTL_ERR_SHAPE, "%s needs k %% 64 == 0 and 64 <= k <= %lld, got k = %lld", what,
+                    (long long)kmax, (long long)k);
     return BTL_OK;
 }
 
@@ -573,6 +620,38 @@ int btl_linear_i8_op(const btl_packed_t* const* w, void* const* y, int32_t* cons
                                1, 0, nullptr, false, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
     return BTL_OK;
+}
+
+int btl_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* x,
+                             int xdtype, const float* g, float eps, int64_t m, int64_t k, int ydtype,
+                             void* ws, size_t ws_bytes, void* stream)
+{
+    Layer ls[btl::kMaxGroup];
+    int rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_group(w, y, count, m, k, ydtype, ls))) return rc;
+    if ((rc = check_fused_shape(k, 65536, "fused RMSNorm"))) return rc;
+    if (m == 0) return BTL_OK;
+    if (!x || !g) return fail(BTL_ERR_LAYOUT, "null input or norm weight");
+    if (!aligned16(x) || !aligned16(g)) return fail(BTL_ERR_LAYOUT, "x and g must be 16-byte aligned");
+    const Xform xf{btl::XF_RMSNORM, nullptr, g, eps};
+    return run_i8(ls, count, x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k,
+                  ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream, &xf);
+}
+
+int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* gate,
+                            const void* up, int xdtype, int64_t m, int64_t k, int ydtype, void* ws,
+                            size_t ws_bytes, void* stream)
+{
+    Layer ls[btl::kMaxGroup];
+    int rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_group(w, y, count, m, k, ydtype, ls))) return rc;
+    if ((rc = check_fused_shape(k, 32768, "fused SwiGLU"))) return rc;
+    if (m == 0) return BTL_OK;
+    if (!gate || !up) return fail(BTL_ERR_LAYOUT, "null gate or up input");
+    if (!aligned16(gate) || !aligned16(up)) return fail(BTL_ERR_LAYOUT, "gate and up must be 16-byte aligned");
+    const Xform xf{btl::XF_SWIGLU, up, nullptr, 0.0f};
+    return run_i8(ls, count, gate, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k,
+                  ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream, &xf);
 }
 
 size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)

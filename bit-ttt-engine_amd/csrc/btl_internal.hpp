@@ -11,7 +11,11 @@ namespace btl {
 constexpr int kMaxGroup = 4;       // layers per grouped launch (q|k|v, w1|w3)
 constexpr int kStepWeights = 256;  // weights of one row consumed per wave-load (64 B)
 
-enum XKind { XK_F32 = 0, XK_BF16 = 1, XK_I8 = 2 };
+// token input kinds: f32 / bf16 (quantised in the kernel), int8 + scales in
+// natural k order (XK_I8) or already in operand order (XK_I8O)
+enum XKind { XK_F32 = 0, XK_BF16 = 1, XK_I8 = 2, XK_I8O = 3 };
+// activation transforms fused ahead of the quantisation
+enum XForm { XF_NONE = 0, XF_RMSNORM = 1, XF_SWIGLU = 2 };
 enum YKind { YK_F32 = 0, YK_BF16 = 1 };
 
 // One layer of a (possibly grouped) decode launch.
@@ -85,6 +89,11 @@ hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s);
 hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, hipStream_t st);
 hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,
                            hipStream_t st);
+// fused transform + operand-order quantisation, one workgroup per token row:
+// XF_RMSNORM: x / sqrt(pairwise_sum(x*x) * (f32)(1/k) + eps) * g (g: [k] f32);
+// XF_SWIGLU:  silu(x) * x2.  k % 64 == 0, k <= 65536; x (and x2) 16-byte aligned.
+hipError_t launch_xform_quant(const void* x, const void* x2, int xkind, int xform, const float* g,
+                              float eps, int64_t m, int64_t k, int8_t* q, float* s, hipStream_t st);
 
 hipError_t launch_quant_act(const void* x, int xkind, int64_t m, int64_t k, int8_t* q,
                             float* s, hipStream_t st);

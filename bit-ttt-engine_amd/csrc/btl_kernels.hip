@@ -182,6 +182,7 @@ typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 template <int XK>
 struct DecX {
     static constexpr int kVec = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);  // uint4 per group
+    static constexpr bool kPreq = XK == XK_I8 || XK == XK_I8O;              // quantised by the caller
 };
 
 template <int XK>
@@ -212,6 +213,7 @@ template <int XK>
 __device__ __forceinline__ uint4 group_quant(const uint4* v, float r)
 {
     if (XK == XK_I8) return transpose16(v[0]);
+    if (XK == XK_I8O) return v[0];
     float f[16];
     if (XK == XK_BF16) {
         const uint32_t u[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
@@ -305,6 +307,7 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
     //    most (issued before the weight loads)
     constexpr int NV = DecX<XK>::kVec;
     constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);  // bytes per element
+    constexpr bool PREQ = DecX<XK>::kPreq;
     const int gpr = K >> 4;  // groups per token row
     const int ng = mt * gpr;
     int gm_[kDecGroups], gc_[kDecGroups];
@@ -335,7 +338,7 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
     // 3. absmax of each token row over the workgroup; lane m then holds the
     //    quantisation parameters of token row m
     float r_l = 0.0f, s_l = 0.0f;
-    if (XK != XK_I8) {
+    if (!PREQ) {
         uint32_t am[MT];
 #pragma unroll
         for (int mm = 0; mm < MT; ++mm) am[mm] = 0u;
@@ -373,7 +376,7 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
             float rm = r_l;
             if (MT > 1) rm = __shfl(r_l, gm_[gi], 64);
             uint4 q = group_quant<XK>(xv[gi], rm);
-            if (XK != XK_I8 && rm == 0.0f) q = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
+            if (!PREQ && rm == 0.0f) q = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
             if (g < ng) *(uint4*)(sq + gm_[gi] * lp + 16 * gc_[gi]) = q;
         }
     }
@@ -446,7 +449,7 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t
         else hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 4>), grid, block, lds, s, a);                     \
         return hipGetLastError();                                                                     \
     }
-    BTL_DEC_CASE(XK_BF16) BTL_DEC_CASE(XK_F32) BTL_DEC_CASE(XK_I8)
+    BTL_DEC_CASE(XK_BF16) BTL_DEC_CASE(XK_F32) BTL_DEC_CASE(XK_I8) BTL_DEC_CASE(XK_I8O)
 #undef BTL_DEC_CASE
     return hipErrorInvalidValue;
 }
@@ -554,6 +557,245 @@ hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_
     }
 #undef BTL_QOP1
     return hipGetLastError();
+}
+
+// exp(x) in f32: Cody-Waite reduction x = n ln2 + r (ln2 = hi + lo, hi with 15
+// significant bits so n*hi is exact), e^r by its Taylor polynomial to r^7/7!
+// in Horner form, scaled by 2^n through exponent bits (two exact steps outside
+// the normal range).  Every step is one rounded f32 operation, so the CPU
+// oracle's restatement gives the same bits.
+__device__ __forceinline__ float btl_expf(float x)
+{
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __uint_as_float(0x7F800000u);
+    if (x < -103.97208404541016f) return 0.0f;
+    const float n = __builtin_rintf(__fmul_rn(x, 1.44269502162933349609375f));
+    const float r = __fsub_rn(__fsub_rn(x, __fmul_rn(n, 0.693145751953125f)),
+                              __fmul_rn(n, 1.428606765330187045037746429443359375e-6f));
+    float p = 1.98412701138295233249664306640625e-4f;
+    p = __fadd_rn(__fmul_rn(p, r), 1.3888889225199818611145019531250e-3f);
+    p = __fadd_rn(__fmul_rn(p, r), 8.3333337679505348205566406250e-3f);
+    p = __fadd_rn(__fmul_rn(p, r), 4.1666667908430099487304687500e-2f);
+    p = __fadd_rn(__fmul_rn(p, r), 0.16666667163372039794921875f);
+    p = __fadd_rn(__fmul_rn(p, r), 0.5f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
+    const int ni = (int)n;
+    if (ni > 127) return __fmul_rn(__fmul_rn(p, __uint_as_float(254u << 23)), __uint_as_float((uint32_t)(ni + 127 - 127) << 23));
+    if (ni < -126) return __fmul_rn(__fmul_rn(p, __uint_as_float((uint32_t)(ni + 64 + 127) << 23)), __uint_as_float(63u << 23));
+    return __fmul_rn(p, __uint_as_float((uint32_t)(ni + 127) << 23));
+}
+
+// Correctly rounded sqrt of an f32 (the hardware v_sqrt_f32 is not): for a
+// positive finite x = M * 2^(2h) with M an integer in [2^46, 2^48), r =
+// isqrt(M) is found from an f32 estimate corrected with exact 64-bit squares,
+// rounded up when M - r^2 > r (the midpoint (r + 1/2)^2 = r^2 + r + 1/4 is
+// never an integer), and r * 2^h is exact.  Zero, negative, inf and NaN
+// inputs take the hardware sqrt, which is exact for them.
+__device__ __forceinline__ float sqrt_rn(float x)
+{
+    const uint32_t b = __float_as_uint(x);
+    if (!(x > 0.0f) || b >= 0x7F800000u) return __builtin_sqrtf(x);
+    int e = (int)(b >> 23);
+    uint32_t mant = b & 0x7FFFFFu;
+    if (e == 0) {  // subnormal: normalise
+        const int sh = __clz(mant) - 8;
+        mant <<= sh;
+        e = 1 - sh;
+    } else {
+        mant |= 0x800000u;
+    }
+    int ex = e - 150;                   // x = mant * 2^ex, mant in [2^23, 2^24)
+    const int sft = (ex & 1) ? 23 : 24;  // ex - sft even
+    const uint64_t M = (uint64_t)mant << sft;
+    const int h = (ex - sft) / 2;
+    uint64_t r = (uint64_t)__builtin_sqrtf((float)M);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (r * r > M) r -= 1;
+        if ((r + 1) * (r + 1) <= M) r += 1;
+    }
+    if (M - r * r > r) r += 1;
+    return __fmul_rn((float)r, __uint_as_float((uint32_t)(h + 127) << 23));
+}
+
+template <int XK>
+__device__ __forceinline__ void widen16(const uint4* v, float* f)
+{
+    if (XK == XK_BF16) {
+        const uint32_t u[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            f[2 * h] = __uint_as_float(u[h] << 16);
+            f[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            f[4 * h] = __uint_as_float(v[h].x); f[4 * h + 1] = __uint_as_float(v[h].y);
+            f[4 * h + 2] = __uint_as_float(v[h].z); f[4 * h + 3] = __uint_as_float(v[h].w);
+        }
+    }
+}
+
+// Pairwise sum over the lanes of a wave (xor butterfly: at level j lane i adds
+// lane i ^ 2^j, which is the pairwise tree over lanes in index order -- float
+// addition commutes).  Every lane ends with the wave's sum.
+__device__ __forceinline__ float wave_pairwise_sum(float v)
+{
+#pragma unroll
+    for (int j = 1; j < 64; j <<= 1) v = __fadd_rn(v, __shfl_xor(v, j, 64));
+    return v;
+}
+
+// k_xform_quant: transform + operand-order quantisation of one token row per
+// workgroup.  Thread t holds the G consecutive 16-element groups [tG, tG+G) in
+// registers, so the sum of squares can follow the pairwise tree in index order:
+// in-thread pairwise over its 16G elements, xor butterfly over the 64 lanes,
+// then pairwise over the waves (zero-padded to a power of two) -- the tree the
+// oracle computes over the row zero-padded to any power of two.
+template <int XK, int XF, int G>
+__global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void* x2, const float* g, float eps,
+                                                       int k, int8_t* q, float* s)
+{
+    __shared__ float s_part[16];
+    __shared__ uint32_t s_w[16];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwv = blockDim.x >> 6;
+    const int groups = k >> 4;
+    constexpr int NV = XK == XK_F32 ? 4 : 2;
+    constexpr int ES = XK == XK_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc((const uint8_t*)x + row * k * ES, (uint32_t)(k * ES));
+    float f[G][16];
+    {
+        uint4 v[G][NV];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const int gg = tid * G + gi;
+            const int off = gg < groups ? gg * 16 * ES : kOOB;
+#pragma unroll
+            for (int h = 0; h < NV; ++h) v[gi][h] = bload(xr, off + 16 * h);
+        }
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) widen16<XK>(v[gi], f[gi]);
+    }
+    if (XF == XF_SWIGLU) {
+        const __amdgpu_buffer_rsrc_t ur = make_rsrc((const uint8_t*)x2 + row * k * ES, (uint32_t)(k * ES));
+        uint4 v[G][NV];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const int gg = tid * G + gi;
+            const int off = gg < groups ? gg * 16 * ES : kOOB;
+#pragma unroll
+            for (int h = 0; h < NV; ++h) v[gi][h] = bload(ur, off + 16 * h);
+        }
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            float u[16];
+            widen16<XK>(v[gi], u);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float vv = f[gi][e];
+                const float si = __fdiv_rn(vv, __fadd_rn(1.0f, btl_expf(-vv)));  // silu (candle: v / (1 + exp(-v)))
+                f[gi][e] = __fmul_rn(si, u[e]);
+            }
+        }
+    }
+    if (XF == XF_RMSNORM) {
+        // pairwise sum of squares: 16G leaves per thread (zeros past k), lanes, waves
+        float t[16 * G];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t[gi * 16 + e] = __fmul_rn(f[gi][e], f[gi][e]);
+#pragma unroll
+        for (int len = 16 * G; len > 1; len >>= 1)
+#pragma unroll
+            for (int i = 0; i < len / 2; ++i) t[i] = __fadd_rn(t[2 * i], t[2 * i + 1]);
+        const float ws = wave_pairwise_sum(t[0]);
+        if (lane == 0) s_part[wave] = ws;
+        __syncthreads();
+        float p[16];
+#pragma unroll
+        for (int w = 0; w < 16; ++w) p[w] = w < nwv ? s_part[w] : 0.0f;
+#pragma unroll
+        for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+            for (int i = 0; i < len / 2; ++i) p[i] = __fadd_rn(p[2 * i], p[2 * i + 1]);
+        // rms_norm.rs:39-42 with candle's scalar ops: ss * (f32)(1/k), + eps, sqrt, x / d, * g
+        const float inv_k = (float)(1.0 / (double)k);
+        const float d = sqrt_rn(__fadd_rn(__fmul_rn(p[0], inv_k), eps));
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const int gg = tid * G + gi;
+            if (gg < groups) {
+                const float4* gp = (const float4*)(g + gg * 16);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const float4 gv = gp[h];
+                    f[gi][4 * h + 0] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 0], d), gv.x);
+                    f[gi][4 * h + 1] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 1], d), gv.y);
+                    f[gi][4 * h + 2] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 2], d), gv.z);
+                    f[gi][4 * h + 3] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 3], d), gv.w);
+                }
+            }
+        }
+    }
+    // absmax of the transformed row (bit patterns, sign cleared; zeros past k)
+    uint32_t amax = 0;
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
+        if (tid * G + gi < groups)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) amax = max(amax, __float_as_uint(f[gi][e]) & 0x7FFFFFFFu);
+    amax = wave_max_dpp(amax);
+    if (lane == 0) s_w[wave] = amax;
+    __syncthreads();
+    amax = s_w[0];
+    for (int w = 1; w < nwv; ++w) amax = max(amax, s_w[w]);
+    const QParams qp = qparams(amax);
+    if (tid == 0) s[row] = qp.s;
+    uint4* qr = (uint4*)(q + row * k);
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        const int gg = tid * G + gi;
+        if (gg < groups) {
+            uint4 o = {0u, 0u, 0u, 0u};
+            if (qp.ok) {
+                int qi[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) qi[e] = quant_fast(f[gi][e], qp.r);
+                o.x = pack4(qi[0], qi[4], qi[8], qi[12]);
+                o.y = pack4(qi[1], qi[5], qi[9], qi[13]);
+                o.z = pack4(qi[2], qi[6], qi[10], qi[14]);
+                o.w = pack4(qi[3], qi[7], qi[11], qi[15]);
+            }
+            qr[gg] = o;
+        }
+    }
+}
+
+hipError_t launch_xform_quant(const void* x, const void* x2, int xkind, int xform, const float* g,
+                              float eps, int64_t m, int64_t k, int8_t* q, float* s, hipStream_t st)
+{
+    if (m <= 0) return hipSuccess;
+    const int64_t groups = k >> 4;
+    if (k % 64 != 0 || groups > (xform == XF_SWIGLU ? 2048 : 4096) || (xkind != XK_F32 && xkind != XK_BF16))
+        return hipErrorInvalidValue;
+    const int G = groups <= 1024 ? 1 : groups <= 2048 ? 2 : 4;  // groups per thread (a power of two)
+    const int threads = (int)((groups / G + 63) / 64 * 64);
+    const dim3 grid((unsigned)m), block((unsigned)threads);
+#define BTL_XQ(XKV, XFV, GV)                                                                            \
+    if (xkind == XKV && xform == XFV && G == GV) {                                                      \
+        hipLaunchKernelGGL((k_xform_quant<XKV, XFV, GV>), grid, block, 0, st, x, x2, g, eps, (int)k, q, s); \
+        return hipGetLastError();                                                                       \
+    }
+#define BTL_XQ_G(XKV, XFV) BTL_XQ(XKV, XFV, 1) BTL_XQ(XKV, XFV, 2) BTL_XQ(XKV, XFV, 4)
+    BTL_XQ_G(XK_BF16, XF_RMSNORM) BTL_XQ_G(XK_F32, XF_RMSNORM)
+    BTL_XQ(XK_BF16, XF_SWIGLU, 1) BTL_XQ(XK_BF16, XF_SWIGLU, 2) BTL_XQ(XK_F32, XF_SWIGLU, 1) BTL_XQ(XK_F32, XF_SWIGLU, 2)
+#undef BTL_XQ_G
+#undef BTL_XQ
+    return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------

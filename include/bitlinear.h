@@ -183,8 +183,36 @@ int btl_linear_i8_op(const btl_packed_t* const* w, void* const* y, int32_t* cons
                      void* stream);
 
 /*
- * Workspace bytes needed by btl_linear / btl_linear_i8 / btl_linear_group for
- * this shape and mode (for btl_linear_group pass n = sum of the layers' n):
+ * RMSNorm fused ahead of a BitLinear group: the activations the reference's
+ * BitLlamaBlock feeds q/k/v and w1/w3 (block.rs:98,121 -> rms_norm.rs:33-56,
+ * then attention.rs:159-162 / swiglu.rs:29-35), without the normalised tensor
+ * in between.  Per token row:
+ *   xn = x / sqrt(ss * (f32)(1/k) + eps) * g,  ss = sum of x*x (products
+ *        rounded to f32) summed as the pairwise tree over the row in index
+ *        order, zero-padded to a power of two;
+ * every operation a separately rounded f32 operation (candle 0.8's scalar ops:
+ * Tensor / f64 and + f64 are affine(1/d, 0) and affine(1, eps)); then
+ * W1.58-A8 with each layer as btl_linear_group.  g: [k] f32 (device).
+ * k % 64 == 0, 64 <= k <= 65536; x, g and the packed weights 16-byte aligned.
+ */
+int btl_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* x,
+                             int xdtype, const float* g, float eps, int64_t m, int64_t k, int ydtype,
+                             void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * SwiGLU fused ahead of a BitLinear group (swiglu.rs:29-35: w2(silu(w1 x) * w3 x)):
+ * h = silu(gate) * up with silu(v) = v / (1 + exp(-v)), then W1.58-A8 with each
+ * layer.  exp is this library's f32 exp (Cody-Waite reduction, Taylor polynomial
+ * to degree 7; within 2 ulp of the exact value).  gate, up: [m, k] of xdtype.
+ * k % 64 == 0, 64 <= k <= 32768; gate, up and the packed weights 16-byte aligned.
+ */
+int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* gate,
+                            const void* up, int xdtype, int64_t m, int64_t k, int ydtype, void* ws,
+                            size_t ws_bytes, void* stream);
+
+/*
+ * Workspace bytes needed by btl_linear / btl_linear_i8 / btl_linear_group (and
+ * the fused RMSNorm / SwiGLU groups) for this shape and mode (for btl_linear_group pass n = sum of the layers' n):
  * scratch for the quantised activations.  Its contents between calls do not
  * matter (every call writes the scratch it reads), so one workspace serves
  * calls of any shapes that fit in it; calls that share one must be ordered on

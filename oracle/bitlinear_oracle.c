@@ -25,6 +25,22 @@
  *   orc_contract_i8      exact int32 ternary contraction acc = sum_k q*t
  *   orc_epilogue         y = (float)acc * (s_x * s_w), fixed op order
  *   orc_bf16_*           bf16 <-> f32 (round-to-nearest-even)
+ *   orc_pairwise_sum     the fixed reduction order of the fused RMSNorm: a
+ *                        pairwise tree over the elements in index order,
+ *                        zero-padded to a power of two
+ *   orc_rmsnorm          src/layers/rms_norm.rs:33-56 (RMSNorm::forward) with
+ *                        candle 0.8's scalar ops (Tensor / f64 and + f64 are
+ *                        affine(1/d, 0) and affine(1, eps) in f32): x / sqrt(
+ *                        sum(x*x) * (f32)(1/k) + (f32)eps) * g; the sum in the
+ *                        pairwise order above (candle's own reduction order is
+ *                        not vendored: its last ulp is parity unpinned)
+ *   orc_expf             exp in f32 by Cody-Waite reduction and a degree-7
+ *                        Taylor polynomial (textbook method), every step a
+ *                        separately rounded f32 operation; the GPU kernels run
+ *                        the same sequence, so the two agree bit for bit
+ *   orc_swiglu           src/layers/swiglu.rs:29-35: silu(g) * u with candle's
+ *                        silu v / (1 + exp(-v)), exp from orc_expf (Rust's
+ *                        f32::exp is libm's: ulp-level parity unpinned)
  *
  * Parity status of each function, and what pins it, is listed in the header
  * of tests/test_oracle.py; the short version: the packing layout, codes and the
@@ -386,6 +402,78 @@ void orc_epilogue(const int32_t* acc, const float* sx, float sw, int64_t m, int6
     for (int64_t i = 0; i < m; ++i) {
         float c = sx[i] * sw;
         for (int64_t j = 0; j < n; ++j) y[i * n + j] = (float)acc[i * n + j] * c;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Fused activation transforms (RMSNorm, SwiGLU) ahead of quantisation */
+/* ------------------------------------------------------------------ */
+/* sum of v[0..n) as the pairwise tree over `len` (a power of two >= n) leaves,
+ * leaves past n being +0: sum(v[a, a+2h)) = sum(v[a, a+h)) + sum(v[a+h, a+2h)). */
+static float orc_pairwise(const float* v, int64_t n, int64_t len)
+{
+    if (len == 1) return n > 0 ? v[0] : 0.0f;
+    const int64_t h = len / 2;
+    const float a = orc_pairwise(v, n < h ? n : h, h);
+    const float b = n > h ? orc_pairwise(v + h, n - h, h) : 0.0f;
+    return a + b;
+}
+
+float orc_pairwise_sum(const float* v, int64_t n)
+{
+    int64_t len = 1;
+    while (len < n) len *= 2;
+    return orc_pairwise(v, n, len);
+}
+
+/* rms_norm.rs:33-56: out = x / sqrt(ss * (f32)(1/k) + (f32)eps) * g per row,
+ * ss = pairwise sum of x*x (products rounded to f32 first). */
+void orc_rmsnorm(const float* x, int64_t m, int64_t k, const float* g, float eps, float* out)
+{
+    float* sq = (float*)malloc(sizeof(float) * (size_t)(k > 0 ? k : 1));
+    const float inv_k = (float)(1.0 / (double)k);
+    for (int64_t i = 0; i < m; ++i) {
+        const float* xr = x + i * k;
+        for (int64_t j = 0; j < k; ++j) sq[j] = xr[j] * xr[j];
+        const float ms = orc_pairwise_sum(sq, k) * inv_k;
+        const float d = sqrtf(ms + eps);
+        for (int64_t j = 0; j < k; ++j) out[i * k + j] = (xr[j] / d) * g[j];
+    }
+    free(sq);
+}
+
+/* exp(x), Cody-Waite: x = n ln2 + r with ln2 = hi + lo (hi has 15 significant
+ * bits, so n*hi is exact for |n| < 512), |r| <= ln2/2; e^r by the Taylor
+ * polynomial to r^7/7! (truncation < 2^-27) in Horner form; the result scaled
+ * by 2^n through exponent bits (two exact steps below 2^-126 or above 2^127). */
+float orc_expf(float x)
+{
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return u2f(0x7F800000u);
+    if (x < -103.97208404541016f) return 0.0f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187045037746429443359375e-6f;
+    float p = 1.98412701138295233249664306640625e-4f;  /* 1/5040 */
+    p = p * r + 1.3888889225199818611145019531250e-3f; /* 1/720 */
+    p = p * r + 8.3333337679505348205566406250e-3f;    /* 1/120 */
+    p = p * r + 4.1666667908430099487304687500e-2f;    /* 1/24 */
+    p = p * r + 0.16666667163372039794921875f;         /* 1/6 */
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    const int ni = (int)n;
+    if (ni > 127) return (p * u2f((uint32_t)(127 + 127) << 23)) * u2f((uint32_t)(ni - 127 + 127) << 23);
+    if (ni < -126) return (p * u2f((uint32_t)(ni + 64 + 127) << 23)) * u2f((uint32_t)(-64 + 127) << 23);
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* swiglu.rs:29-35 (candle silu = v / (1 + exp(-v))): out = silu(g) * u. */
+void orc_swiglu(const float* g, const float* u, int64_t n, float* out)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = g[i];
+        const float si = v / (1.0f + orc_expf(-v));
+        out[i] = si * u[i];
     }
 }
 

@@ -35,6 +35,10 @@ def _load():
         "orc_epilogue": (None, [vp, vp, f32, i64, i64, vp]),
         "orc_forward_i8": (i32, [vp, i64, i64, vp, i64, f32, vp, vp, vp, vp]),
         "orc_bf16_to_f32_array": (None, [vp, i64, vp]),
+        "orc_pairwise_sum": (f32, [vp, i64]),
+        "orc_rmsnorm": (None, [vp, i64, i64, vp, f32, vp]),
+        "orc_expf": (f32, [f32]),
+        "orc_swiglu": (None, [vp, vp, i64, vp]),
         "orc_f32_to_bf16_array": (None, [vp, i64, vp]),
     }
     for name, (res, args) in sigs.items():
@@ -150,4 +154,36 @@ def f32_to_bf16(f):
     f = _f32(f)
     out = np.zeros(f.shape, dtype=np.uint16)
     lib.orc_f32_to_bf16_array(_p(f), f.size, _p(out))
+    return out
+
+
+def pairwise_sum(v):
+    """Pairwise-tree sum in index order, zero-padded to a power of two (float32)."""
+    v = _f32(v).ravel()
+    return np.float32(lib.orc_pairwise_sum(_p(v), v.size))
+
+
+def rmsnorm(x, g, eps):
+    """rms_norm.rs:33-56 restated (see the C header): float32 [M, K] -> [M, K]."""
+    x = _f32(x)
+    m, k = x.shape
+    g = _f32(g).ravel()
+    assert g.size == k
+    out = np.empty_like(x)
+    lib.orc_rmsnorm(_p(x), m, k, _p(g), float(np.float32(eps)), _p(out))
+    return out
+
+
+def expf(x):
+    """The build's float32 exp (Cody-Waite + Taylor), elementwise."""
+    x = _f32(x)
+    return np.array([lib.orc_expf(float(v)) for v in x.ravel()], dtype=np.float32).reshape(x.shape)
+
+
+def swiglu(g, u):
+    """swiglu.rs:29-35: silu(g) * u, float32."""
+    g, u = _f32(g), _f32(u)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    lib.orc_swiglu(_p(g), _p(u), g.size, _p(out))
     return out

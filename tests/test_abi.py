@@ -138,6 +138,32 @@ def test_operand_order_entry_validation():
     assert q(16, 0, 0, 128, 16, 16, None) == bl.BTL_OK
 
 
+def test_fused_entry_validation():
+    w = _packed(64, 128, data=16)
+    arr = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(w))
+    ys = (ctypes.c_void_p * 1)(16)
+    rms = bl.lib.btl_rmsnorm_linear_group
+    swi = bl.lib.btl_swiglu_linear_group
+    assert rms(arr, ys, 0, 16, 0, 16, 1e-5, 4, 128, 0, None, 0, None) == bl.BTL_ERR_ARG      # count
+    assert rms(arr, ys, 1, 16, 5, 16, 1e-5, 4, 128, 0, None, 0, None) == bl.BTL_ERR_DTYPE    # xdtype
+    assert rms(arr, ys, 1, 16, 0, 16, 1e-5, 4, 124, 0, None, 0, None) == bl.BTL_ERR_SHAPE    # k != w.k
+    w96 = _packed(64, 96, data=16)
+    arr96 = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(w96))
+    assert rms(arr96, ys, 1, 16, 0, 16, 1e-5, 4, 96, 0, None, 0, None) == bl.BTL_ERR_SHAPE   # k % 64
+    big = _packed(64, 65600, data=16)
+    arrb = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(big))
+    assert rms(arrb, ys, 1, 16, 0, 16, 1e-5, 4, 65600, 0, None, 0, None) == bl.BTL_ERR_SHAPE
+    assert rms(arr, ys, 1, 16, 0, None, 1e-5, 4, 128, 0, None, 0, None) == bl.BTL_ERR_LAYOUT  # null g
+    assert rms(arr, ys, 1, 24, 0, 16, 1e-5, 4, 128, 0, None, 0, None) == bl.BTL_ERR_LAYOUT    # alignment
+    assert rms(arr, ys, 1, 16, 0, 16, 1e-5, 0, 128, 0, None, 0, None) == bl.BTL_OK           # m == 0
+    assert swi(arr, ys, 1, 16, None, 0, 4, 128, 0, None, 0, None) == bl.BTL_ERR_LAYOUT       # null up
+    assert swi(arr, ys, 1, 16, 24, 0, 4, 128, 0, None, 0, None) == bl.BTL_ERR_LAYOUT         # alignment
+    wsw = _packed(64, 32832, data=16)
+    arrs = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(wsw))
+    assert swi(arrs, ys, 1, 16, 16, 0, 4, 32832, 0, None, 0, None) == bl.BTL_ERR_SHAPE       # k > 32768
+    assert swi(arr, ys, 1, 16, 16, 0, 0, 128, 0, None, 0, None) == bl.BTL_OK
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
 def test_no_device_is_an_error():
     rc = bl.lib.btl_init(0)

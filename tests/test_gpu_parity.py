@@ -420,3 +420,120 @@ def test_gemm_prefill_shape_sampled_rows():
     for r in (0, 1000, 2047):
         bl.BitLinearHip.forward(x[r:r + 1].contiguous(), pt, acc_out=acc1)
         assert torch.equal(acc1[0], acc[r])
+
+
+# --- fused RMSNorm / SwiGLU ahead of the contraction ----------------------------
+
+def _rms_reference(x, g, eps, layers):
+    xn = orc.rmsnorm(x, g, eps)
+    return [orc.forward_i8(xn, wb, pt.dims2()[0], sw)[0] for (pt, wb, sw) in layers]
+
+
+# decode (m <= 4), batched (5..32), GEMM (> 32); k from one MFMA step to 2 groups per thread
+FUSED_SHAPES = [(1, 4096, (256, 64, 64)), (2, 1024, (300,)), (4, 4096, (130,)), (7, 2048, (200, 100)),
+                (32, 4096, (64,)), (65, 1024, (300,)), (300, 4096, (128,)), (3, 64, (80,)), (1, 16384, (64,)),
+                (2, 32768, (32,))]
+
+
+@pytest.mark.parametrize("m,k,ns", FUSED_SHAPES)
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
+def test_rmsnorm_linear_group_matches_oracle(m, k, ns, xdt, ydt):
+    print("rmsnorm", m, k, ns, xdt, ydt, flush=True)
+    rng = np.random.default_rng(m * 7 + k)
+    x = (rng.standard_normal((m, k)) * rng.uniform(0.2, 40, (m, 1))).astype(np.float32)
+    x[m // 2, : k // 3] = 0.0
+    g = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    eps = 1e-5
+    layers = [make_layer(n, k, seed=n * 11 + i) for i, n in enumerate(ns)]
+    xt = to_dev(x, xdt)
+    ys = bl.rmsnorm_linear_group([l[0] for l in layers], xt, torch.from_numpy(g), eps, out_dtype=ydt)
+    refs = _rms_reference(host_x(xt), g, eps, layers)
+    for y, yr in zip(ys, refs):
+        if ydt == torch.float32:
+            assert_f32_identical(y, yr)
+        else:
+            assert_bf16_matches(y, yr)
+
+
+def test_rmsnorm_many_rows_exercise_the_sqrt():
+    # 256 rows whose mean squares span many binades: the per-row sqrt must be
+    # correctly rounded (the hardware sqrt is not) for the scales to match
+    m, k, n = 256, 64, 48
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-12, 12, (m, 1)))).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    pt, wb, sw = make_layer(n, k, seed=5)
+    y = bl.rmsnorm_linear_group([pt], to_dev(x, torch.float32), torch.from_numpy(g), 1e-6,
+                                out_dtype=torch.float32)[0]
+    assert_f32_identical(y, _rms_reference(x, g, 1e-6, [(pt, wb, sw)])[0])
+
+
+def test_rmsnorm_special_rows():
+    # zero row (0 / sqrt(eps) = 0 -> scale 0), an inf row (non-finite -> NaN),
+    # huge and tiny magnitudes; eps = 0 on a zero row gives 0/0 = NaN
+    m, k, n = 4, 1024, 96
+    x = np.random.default_rng(9).standard_normal((m, k)).astype(np.float32)
+    x[0] = 0.0
+    x[1, 5] = np.inf
+    x[2] *= np.float32(1e30)
+    x[3] *= np.float32(1e-30)
+    g = np.ones(k, np.float32)
+    pt, wb, sw = make_layer(n, k, seed=4)
+    for eps in (1e-5, 0.0):
+        y = bl.rmsnorm_linear_group([pt], to_dev(x, torch.float32), torch.from_numpy(g), eps,
+                                    out_dtype=torch.float32)[0]
+        yr = _rms_reference(x, g, eps, [(pt, wb, sw)])[0]
+        assert_f32_identical(y, yr)
+
+
+@pytest.mark.parametrize("m,k,ns", [(1, 14336, (4096,)), (2, 14336, (300,)), (4, 4096, (130, 64)),
+                                    (16, 14336, (256,)), (64, 4096, (200,)), (130, 1024, (100,)),
+                                    (3, 64, (80,)), (1, 32768, (64,))])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
+def test_swiglu_linear_group_matches_oracle(m, k, ns, xdt, ydt):
+    print("swiglu", m, k, ns, xdt, ydt, flush=True)
+    rng = np.random.default_rng(m * 13 + k)
+    gate = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    up = rng.standard_normal((m, k)).astype(np.float32)
+    gate[0, :7] = np.array([0, -0.0, 90, -90, 200, -200, 1e-30], np.float32)
+    layers = [make_layer(n, k, seed=n * 3 + i) for i, n in enumerate(ns)]
+    gt, ut = to_dev(gate, xdt), to_dev(up, xdt)
+    ys = bl.swiglu_linear_group([l[0] for l in layers], gt, ut, out_dtype=ydt)
+    h = orc.swiglu(host_x(gt), host_x(ut))
+    for y, (pt, wb, sw) in zip(ys, layers):
+        yr = orc.forward_i8(h, wb, pt.dims2()[0], sw)[0]
+        if ydt == torch.float32:
+            assert_f32_identical(y, yr)
+        else:
+            assert_bf16_matches(y, yr)
+
+
+def test_fused_with_caller_workspace_and_graph_replays():
+    # caller workspace of exactly btl_workspace_bytes, garbage between calls,
+    # and the same calls captured in a HIP graph and replayed
+    m, k, n = 6, 4096, 512
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    pt, wb, sw = make_layer(n, k, seed=8)
+    ws = bl.Workspace(m, n, k, device=DEV)
+    ws.buf.fill_(0x77)
+    xt = to_dev(x, torch.bfloat16)
+    gt = torch.from_numpy(g).to(DEV)
+    out = [torch.empty((m, n), dtype=torch.float32, device=DEV)]
+    bl.rmsnorm_linear_group([pt], xt, gt, 1e-5, workspace=ws, outputs=out)
+    torch.cuda.synchronize()
+    yr = _rms_reference(host_x(xt), g, 1e-5, [(pt, wb, sw)])[0]
+    assert_f32_identical(out[0], yr)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            bl.rmsnorm_linear_group([pt], xt, gt, 1e-5, workspace=ws, outputs=out)
+    for _ in range(3):
+        out[0].zero_()
+        ws.buf.fill_(0x33)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_f32_identical(out[0], yr)

@@ -17,6 +17,17 @@ What pins each oracle function (reference = imonoonoko/Bit-TTT-Engine, crates/ru
   orc_contract_i8         numpy int64 matmul of the unpacked ternary matrix.
   orc_epilogue            numpy float32 arithmetic.
   bf16 helpers            torch's round-to-nearest-even bfloat16 conversion.
+  orc_pairwise_sum        inputs whose float32 sum differs between the pairwise tree and a
+                          sequential sum or another tree split (so only the defined order
+                          passes); zero-padding invariance; exact integer sums.
+  orc_expf                float64 exp rounded to float32: within 2 ulp over a dense sweep
+                          of the whole range incl. subnormal results; exp(0) = 1; overflow,
+                          underflow, NaN.  Rust's f32::exp (libm) is the reference's: the
+                          last ulps are parity unpinned (a documented tolerance).
+  orc_swiglu              float64 closed form silu(g)*u (relative 1e-6); limits.
+  orc_rmsnorm             float64 closed form (relative 1e-6); a known answer; zero row;
+                          the eps and weight terms; scale invariance.  Candle's own sum
+                          order is not vendored: its last ulp is parity unpinned.
 """
 import numpy as np
 import pytest
@@ -272,3 +283,86 @@ def test_bf16_conversions_match_torch():
     back = orc.bf16_to_f32(got)
     assert np.array_equal(back, torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).float().numpy())
     assert orc.f32_to_bf16(np.array([np.nan], np.float32))[0] == 0x7FC0
+
+
+# --- fused activation transforms (RMSNorm, SwiGLU) ------------------------------
+
+def test_pairwise_sum_follows_the_pairwise_tree():
+    # (1 + 1) + (1e8 - 1e8) = 2 in float32; a sequential sum loses the 2 in 1e8
+    v4 = np.array([1, 1, 1e8, -1e8], np.float32)
+    assert orc.pairwise_sum(v4) == np.float32(2.0)
+    seq = np.float32(0)
+    for v in v4:
+        seq = np.float32(seq + v)
+    assert seq == np.float32(0.0)
+    # five leaves padded to eight: ((a+b)+(c+d)) + e.  A 3+2 split gives 0.
+    v = np.array([1e8, 1, 1, -1e8, 1], np.float32)
+    assert orc.pairwise_sum(v) == np.float32(1.0)
+    three_two = np.float32(np.float32(np.float32(1e8) + np.float32(1)) + np.float32(1))
+    three_two = np.float32(three_two + np.float32(np.float32(-1e8) + np.float32(1)))
+    assert three_two == np.float32(0.0)
+    # zero padding to a longer power of two changes nothing
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(1000).astype(np.float32)
+    assert orc.pairwise_sum(x) == orc.pairwise_sum(np.concatenate([x, np.zeros(3000, np.float32)]))
+    # exact for small integers, and close to float64 in general
+    assert orc.pairwise_sum(np.arange(1000, dtype=np.float32)) == 499500.0
+    assert abs(float(orc.pairwise_sum(x)) - float(x.astype(np.float64).sum())) < 1e-4
+
+
+def _ulp_diff(a, b):
+    ai = a.view(np.int32).astype(np.int64)
+    bi = b.view(np.int32).astype(np.int64)
+    ai = np.where(ai < 0, -(ai & 0x7FFFFFFF), ai)
+    bi = np.where(bi < 0, -(bi & 0x7FFFFFFF), bi)
+    return np.abs(ai - bi)
+
+
+def test_expf_within_two_ulp():
+    x = np.concatenate([np.linspace(-103.9, 88.72, 200001, dtype=np.float32),
+                        np.array([-1e-6, 1e-6, 0.34657359, -0.34657359, 1.0, -1.0, 10.0], np.float32)])
+    got = orc.expf(x)
+    ref = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert int(_ulp_diff(got, ref).max()) <= 2
+    assert orc.expf(np.array([0.0], np.float32))[0] == 1.0
+    assert np.isinf(orc.expf(np.array([88.8, 1e30, np.inf], np.float32))).all()
+    assert (orc.expf(np.array([-104.0, -1e30, -np.inf], np.float32)) == 0).all()
+    assert np.isnan(orc.expf(np.array([np.nan], np.float32)))[0]
+    # largest finite result and a subnormal one
+    assert np.isfinite(orc.expf(np.array([88.72283], np.float32)))[0]
+    sub = orc.expf(np.array([-100.0], np.float32))[0]
+    assert 0 < sub < np.finfo(np.float32).tiny and abs(float(sub) - np.exp(-100.0)) <= 1.5e-45
+
+
+def test_swiglu_closed_form():
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(50000) * 4).astype(np.float32)
+    u = rng.standard_normal(50000).astype(np.float32)
+    got = orc.swiglu(g, u).astype(np.float64)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    ref = g64 / (1 + np.exp(-g64)) * u64
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 1e-6
+    lim = orc.swiglu(np.array([0.0, 200.0, -200.0, 1e30], np.float32), np.ones(4, np.float32))
+    assert lim[0] == 0 and lim[1] == 200.0 and lim[2] == 0 and lim[3] == np.float32(1e30)
+
+
+def test_rmsnorm_closed_form_and_known_answer():
+    # known answer: x = [3, 4], g = 1, eps = 0 -> ms = 12.5, d = sqrt(12.5)
+    out = orc.rmsnorm(np.array([[3.0, 4.0]], np.float32), np.ones(2, np.float32), 0.0)
+    d = np.sqrt(np.float32(12.5))
+    assert np.array_equal(out[0], np.array([np.float32(3.0) / d, np.float32(4.0) / d], np.float32))
+    rng = np.random.default_rng(6)
+    m, k = 5, 4096
+    x = (rng.standard_normal((m, k)) * rng.uniform(0.1, 30, (m, 1))).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    for eps in (1e-5, 1e-2):
+        got = orc.rmsnorm(x, g, eps).astype(np.float64)
+        x64 = x.astype(np.float64)
+        ref = x64 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + np.float32(eps)) * g
+        assert np.max(np.abs(got - ref) / np.abs(ref).max()) < 1e-6
+    # zero row: 0 / sqrt(eps) = 0; scale invariance when eps is negligible
+    z = orc.rmsnorm(np.zeros((1, 64), np.float32), np.ones(64, np.float32), 1e-5)
+    assert not z.any()
+    a = orc.rmsnorm(x[:1], g, 1e-30)
+    b = orc.rmsnorm(x[:1] * np.float32(4.0), g, 1e-30)
+    assert np.array_equal(a, b)  # the factor 4 is exact in every step
