@@ -271,6 +271,8 @@ def run_decode(args):
         result["prefill"] = run_prefill(layers, gen, dev, args)
     if args.sweep:
         result["batched_decode"] = run_sweep(layers, gen, dev, args)
+    if args.pack:
+        result["pack"] = run_pack(gen, dev)
     if args.cpu_baseline:
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         host = []
@@ -415,6 +417,30 @@ def run_sweep(layers, gen, dev, args):
             "rows": rows}
 
 
+def run_pack(gen, dev):
+    """PackedTensor::pack on the device (btl_pack_device) of one f32 weight of the
+    MLP up shape 14336 x 4096: the load-time quantisation a checkpoint loader
+    runs once per layer.  Algorithmic bytes = the f32 read once + the packed
+    bytes written; the kernels read the f32 tensor twice (the absmean reduction,
+    then the code pass), so the HBM-bound ceiling is about half the peak."""
+    n, k = INTER, HIDDEN
+    w = torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32) * 0.02
+    out = torch.empty(((n * k + 3) // 4,), dtype=torch.uint8, device=dev)
+    sc = torch.empty((1,), dtype=torch.float32, device=dev)
+    wsb = bl.lib.btl_pack_workspace_bytes(n, k)
+    ws = torch.empty((wsb,), dtype=torch.uint8, device=dev)
+
+    def fn(stream):
+        bl.check(bl.lib.btl_pack_device(w.data_ptr(), n, k, out.data_ptr(), sc.data_ptr(), ws.data_ptr(), wsb,
+                                        stream))
+    us = time_launches(fn, 20, torch.cuda.Stream())
+    b = n * k * 4 + (n * k) // 4
+    print("bench: device pack %.1f us" % us, file=sys.stderr, flush=True)
+    return {"workload": "btl_pack_device, f32 [14336, 4096] -> packed 2-bit + absmean scale",
+            "us": round(us, 2), "algorithmic_bytes": b, "GB_s": round(b / us / 1e3, 1),
+            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3), "kernels": "k_abs_sum x2 levels + k_pack_codes"}
+
+
 def run_probe(args):
     """A few launches of one workload, plus a plain copy of known size, for
     counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy reads and
@@ -458,6 +484,8 @@ def main():
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="skip the cfg4 prefill section of the JSON line")
     ap.add_argument("--prefill-m", type=int, default=2048)
+    ap.add_argument("--no-pack", dest="pack", action="store_false",
+                    help="skip the device-pack (PackedTensor::pack) timing")
     ap.add_argument("--no-sweep", dest="sweep", action="store_false",
                     help="skip the cfg3 batched-decode section of the JSON line")
     ap.add_argument("--probe", choices=["decode_gate_up", "prefill_gate_up"], default=None,

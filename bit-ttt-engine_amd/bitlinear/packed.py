@@ -56,6 +56,23 @@ class PackedTensor:
                                 out.data_ptr() if numel else None, ctypes.byref(scale)))
         return PackedTensor(out.to(device), scale.value, tuple(host.shape), device)
 
+    @staticmethod
+    def pack_device(tensor):
+        """PackedTensor::pack on the GPU (btl_pack_device): bit-identical to pack()
+        for a float32 tensor already on the device."""
+        if tensor.device.type != "cuda":
+            raise BitLinearError(2, "pack_device needs a GPU tensor")
+        from .layer import _stream
+        w = tensor.detach().to(torch.float32).contiguous()
+        numel = w.numel()
+        out = torch.empty(((numel + 3) // 4,), dtype=torch.uint8, device=w.device)
+        scale = torch.empty((1,), dtype=torch.float32, device=w.device)
+        n = w.shape[0] if w.dim() == 2 else 1
+        k = w.shape[1] if w.dim() == 2 else numel
+        check(lib.btl_pack_device(w.data_ptr() if numel else None, n, k, out.data_ptr() if numel else None,
+                                  scale.data_ptr(), None, 0, _stream(w.device)))
+        return PackedTensor(out, float(scale.item()), tuple(w.shape), w.device)
+
     # packing.rs:108-133
     def unpack(self, device=None):
         """Dense float32 weights t*scale with the original shape."""

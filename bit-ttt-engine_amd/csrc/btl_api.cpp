@@ -400,6 +400,25 @@ int check_fused_shape(int64_t k, int64_t kmax, const char* what)
     return BTL_OK;
 }
 
+// sum of |w| in double as the pairwise tree over the elements in index order,
+// zero-padded to a power of two (the order btl_pack_device reproduces)
+double abs_pairwise_rec(const float* w, int64_t numel, int64_t a, int64_t len)
+{
+    if (len == 1) return a < numel ? std::fabs((double)w[a]) : 0.0;
+    const int64_t h = len / 2;
+    const double lo = abs_pairwise_rec(w, numel, a, h);
+    const double hi = a + h < numel ? abs_pairwise_rec(w, numel, a + h, h) : 0.0;
+    return lo + hi;
+}
+
+double abs_pairwise(const float* w, int64_t numel)
+{
+    if (numel <= 0) return 0.0;
+    int64_t len = 1;
+    while (len < numel) len *= 2;
+    return abs_pairwise_rec(w, numel, 0, len);
+}
+
 }  // namespace
 
 extern "C" {
@@ -446,8 +465,7 @@ int btl_pack_host(const float* w, int64_t n, int64_t k, uint8_t* out, float* sca
     if (n < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
     const int64_t numel = n * k;
     if ((numel && (!w || !out)) || !scale) return fail(BTL_ERR_ARG, "null pointer");
-    double acc = 0.0;
-    for (int64_t i = 0; i < numel; ++i) acc += std::fabs((double)w[i]);
+    const double acc = abs_pairwise(w, numel);
     const float mean = numel ? (float)(acc / (double)numel) : 0.0f;
     const float s = mean + 1e-6f;  // EPSILON, packing.rs:4
     const float inv = (float)(1.0 / (double)s);
@@ -478,6 +496,36 @@ int btl_unpack_host(const uint8_t* data, int64_t n, int64_t k, float scale, floa
         const float v = code == 1 ? 1.0f : (code == 2 ? -1.0f : 0.0f);
         out[e] = v * scale;
     }
+    return BTL_OK;
+}
+
+size_t btl_pack_workspace_bytes(int64_t n, int64_t k)
+{
+    if (n < 0 || k < 0 || n * k == 0) return 0;
+    return (size_t)btl::pack_partials(n * k) * sizeof(double);
+}
+
+int btl_pack_device(const float* w, int64_t n, int64_t k, uint8_t* out, float* scale, void* ws, size_t ws_bytes,
+                    void* stream)
+{
+    if (n < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    const int64_t numel = n * k;
+    if (!scale || (numel && (!w || !out))) return fail(BTL_ERR_ARG, "null pointer");
+    if (!aligned16(w) || ((uintptr_t)out & 3u)) return fail(BTL_ERR_LAYOUT, "w must be 16-byte and out 4-byte aligned");
+    int dev;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    hipError_t e;
+    if (numel == 0) {  // mean of nothing: 0, scale = 1e-6
+        const float s = 1e-6f;
+        e = hipMemcpyAsync(scale, &s, sizeof(float), hipMemcpyHostToDevice, (hipStream_t)stream);
+        if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+        return e == hipSuccess ? BTL_OK : hip_fail(e, "scale copy");
+    }
+    void* wsp = nullptr;
+    if ((rc = get_ws(dev, ws, ws_bytes, btl_pack_workspace_bytes(n, k), &wsp))) return rc;
+    e = btl::launch_pack(w, numel, out, scale, (double*)wsp, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "pack kernel launch");
     return BTL_OK;
 }
 

@@ -105,6 +105,10 @@ hipError_t launch_generic_i8(const int8_t* q, const float* xs, int64_t m, int64_
                              const uint8_t* w, int64_t n, float sw, void* y, int ykind,
                              int32_t* acc_out, hipStream_t st);
 
+// PackedTensor::pack on the device: `partials` holds pack_partials(numel) doubles.
+int64_t pack_partials(int64_t numel);
+hipError_t launch_pack(const float* w, int64_t numel, uint8_t* out, float* scale_out, double* partials,
+                       hipStream_t st);
 hipError_t launch_unpack(const uint8_t* w, int64_t numel, float scale, float* out,
                          hipStream_t st);
 

@@ -1387,6 +1387,140 @@ hipError_t launch_generic_i8(const int8_t* q, const float* xs, int64_t m, int64_
 }
 
 // ---------------------------------------------------------------------------
+// k_abs_sum / k_pack_codes: PackedTensor::pack on the device
+// ---------------------------------------------------------------------------
+// The mean of |w| is the pairwise tree in double over the elements in index
+// order (zero-padded to a power of two) -- the order btl_pack_host and the CPU
+// oracle use, so the scale is bit-identical.  A workgroup sums an aligned block
+// of 4096 elements: wave w the 1024 at 1024w, its load j the 256 at 1024w+256j,
+// lane l the 4 at 4l of those (one coalesced 16-byte load).  The lane's 4 are
+// an aligned subtree; the xor butterfly over the 64 lanes is the pairwise tree
+// of the 256; then (j0+j1)+(j2+j3) per wave and (w0+w1)+(w2+w3) per block.
+// Level 0 reads |w| (f32), later levels the block sums of the level below
+// (doubles), 4096 at a time until one is left -- each block an aligned subtree.
+template <int LEVEL0>
+__global__ __launch_bounds__(256) void k_abs_sum(const void* in, int64_t n, double* out)
+{
+    __shared__ double s_part[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t base = blockIdx.x * 4096ll + wave * 1024 + lane * 4;
+    double s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t idx = base + 256 * j;
+        double v0 = 0.0, v1 = 0.0, v2 = 0.0, v3 = 0.0;
+        if (LEVEL0) {
+            const float* f = (const float*)in;
+            if (idx + 4 <= n) {
+                const float4 q = *(const float4*)(f + idx);  // f 16-byte aligned, idx % 4 == 0
+                v0 = fabs((double)q.x); v1 = fabs((double)q.y); v2 = fabs((double)q.z); v3 = fabs((double)q.w);
+            } else {
+                if (idx < n) v0 = fabs((double)f[idx]);
+                if (idx + 1 < n) v1 = fabs((double)f[idx + 1]);
+                if (idx + 2 < n) v2 = fabs((double)f[idx + 2]);
+            }
+        } else {
+            const double* d = (const double*)in;
+            if (idx < n) v0 = d[idx];
+            if (idx + 1 < n) v1 = d[idx + 1];
+            if (idx + 2 < n) v2 = d[idx + 2];
+            if (idx + 3 < n) v3 = d[idx + 3];
+        }
+        s[j] = __dadd_rn(__dadd_rn(v0, v1), __dadd_rn(v2, v3));
+    }
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[j] = __dadd_rn(s[j], __shfl_xor(s[j], sh, 64));
+    if (lane == 0) s_part[wave] = __dadd_rn(__dadd_rn(s[0], s[1]), __dadd_rn(s[2], s[3]));
+    __syncthreads();
+    if (tid == 0) out[blockIdx.x] = __dadd_rn(__dadd_rn(s_part[0], s_part[1]), __dadd_rn(s_part[2], s_part[3]));
+}
+
+// scale = (f32)(sum / numel) + 1e-6, y = w * (f32)(1 / (double)scale); code 1 if
+// round_half_away(y) clamped to [-1, 1] is 1 (y >= 0.5), 2 if it is -1
+// (y <= -0.5), else 0 (packing.rs:56-92).  One packed byte = 4 elements = one
+// 16-byte load; a workgroup covers 1024 bytes per pass (4 per thread, lanes
+// on consecutive bytes), grid-stride over the tensor.
+__device__ __forceinline__ uint32_t pack_code(float x, float inv)
+{
+    const float y = __fmul_rn(x, inv);
+    return y >= 0.5f ? 1u : (y <= -0.5f ? 2u : 0u);
+}
+
+__global__ __launch_bounds__(256) void k_pack_codes(const float* w, int64_t numel, const double* total,
+                                                     uint8_t* out, float* scale_out)
+{
+    const double acc = *total;
+    const float mean = numel ? (float)(acc / (double)numel) : 0.0f;
+    const float sc = __fadd_rn(mean, 1e-6f);
+    const float inv = (float)(1.0 / (double)sc);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = sc;
+    const int64_t nbytes = (numel + 3) / 4;
+    for (int64_t b0 = blockIdx.x * 1024ll; b0 < nbytes; b0 += (int64_t)gridDim.x * 1024) {
+        float4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t b = b0 + 256 * j + threadIdx.x, e = 4 * b;
+            v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (e + 4 <= numel) {
+                v[j] = *(const float4*)(w + e);  // w 16-byte aligned
+            } else if (e < numel) {
+                v[j].x = w[e];
+                if (e + 1 < numel) v[j].y = w[e + 1];
+                if (e + 2 < numel) v[j].z = w[e + 2];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t b = b0 + 256 * j + threadIdx.x;
+            if (b < nbytes)
+                out[b] = (uint8_t)(pack_code(v[j].x, inv) | pack_code(v[j].y, inv) << 2 |
+                                   pack_code(v[j].z, inv) << 4 | pack_code(v[j].w, inv) << 6);
+        }
+    }
+}
+
+int64_t pack_partials(int64_t numel)
+{
+    int64_t total = 0;
+    for (int64_t n = numel; ; ) {
+        const int64_t p = (n + 4095) / 4096;
+        total += p;
+        if (p <= 1) break;
+        n = p;
+    }
+    return total;
+}
+
+hipError_t launch_pack(const float* w, int64_t numel, uint8_t* out, float* scale_out, double* partials,
+                       hipStream_t st)
+{
+    if (numel <= 0) return hipErrorInvalidValue;
+    const void* in = w;
+    int64_t n = numel;
+    double* dst = partials;
+    bool level0 = true;
+    for (;;) {
+        const int64_t p = (n + 4095) / 4096;
+        if (p > INT32_MAX) return hipErrorInvalidValue;
+        if (level0) hipLaunchKernelGGL((k_abs_sum<1>), dim3((unsigned)p), dim3(256), 0, st, in, n, dst);
+        else hipLaunchKernelGGL((k_abs_sum<0>), dim3((unsigned)p), dim3(256), 0, st, in, n, dst);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        if (p == 1) break;
+        in = dst;
+        dst += p;
+        n = p;
+        level0 = false;
+    }
+    const int64_t blocks = ((numel + 3) / 4 + 1023) / 1024;
+    hipLaunchKernelGGL(k_pack_codes, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, st, w, numel,
+                       dst, out, scale_out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // k_unpack: PackedTensor::unpack on the device (packing.rs:113-132)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_unpack(const uint8_t* w, int64_t numel, float scale,

@@ -98,13 +98,27 @@ int64_t btl_packed_bytes(int64_t n, int64_t k);
 
 /*
  * Host-side packing, PackedTensor::pack (packing.rs:50-105): host pointers.
- * w: [n, k] f32; out: btl_packed_bytes(n, k) bytes; *scale = mean|w| + 1e-6.
+ * w: [n, k] f32; out: btl_packed_bytes(n, k) bytes; *scale = mean|w| + 1e-6,
+ * the mean summed in double as the pairwise tree over |w| in index order.
  * t = clamp(round(w * (1/scale)), -1, 1), round half away from zero.
  */
 int btl_pack_host(const float* w, int64_t n, int64_t k, uint8_t* out, float* scale);
 
 /* Host-side PackedTensor::unpack (packing.rs:108-133): out[n*k] = t * scale. */
 int btl_unpack_host(const uint8_t* data, int64_t n, int64_t k, float scale, float* out);
+
+/*
+ * PackedTensor::pack (packing.rs:50-105) on the device, for load-time packing of
+ * weights already on the GPU.  w: [n, k] f32 device (16-byte aligned); out:
+ * btl_packed_bytes(n, k) device bytes (4-byte aligned); *scale: a device f32
+ * that receives mean|w| + 1e-6.  Bit-identical to btl_pack_host: the mean is
+ * the pairwise tree in double over |w| in index order (zero-padded to a power
+ * of two), rounded once to f32.  ws / ws_bytes: optional workspace of
+ * btl_pack_workspace_bytes(n, k) bytes for the partial sums.
+ */
+int btl_pack_device(const float* w, int64_t n, int64_t k, uint8_t* out, float* scale, void* ws, size_t ws_bytes,
+                    void* stream);
+size_t btl_pack_workspace_bytes(int64_t n, int64_t k);
 
 /*
  * Device-side unpack to dense f32 [n, k] (what BitLinearCuda::forward builds

@@ -101,16 +101,28 @@ void orc_f32_to_bf16_array(const float* f, int64_t n, uint16_t* out)
  * byte e/4 holds element e at bits 2*(e%4), little end first (packing.rs:74-92);
  * the last byte's unused fields stay 00.
  *
- * The mean is accumulated in double and rounded once to f32.  candle's
- * mean_all accumulates in f32 in an order set by its CPU reduction kernel,
- * which is not vendored with the reference, so the last ulp of the scale is
- * parity unpinned (pinned to 1e-3 by packing.rs:166,184 and by closed forms).
+ * The mean is accumulated in double as the pairwise tree over |w| in index
+ * order (zero-padded to a power of two: any thread count reproduces it) and
+ * rounded once to f32.  candle's mean_all accumulates in f32 in an order set by
+ * its CPU reduction kernel, which is not vendored with the reference, so the
+ * last ulp of the scale is parity unpinned (pinned to 1e-3 by
+ * packing.rs:166,184 and by closed forms).
  */
+static double orc_abs_pairwise(const float* w, int64_t numel, int64_t a, int64_t len)
+{
+    if (len == 1) return a < numel ? fabs((double)w[a]) : 0.0;
+    const int64_t h = len / 2;
+    const double lo = orc_abs_pairwise(w, numel, a, h);
+    const double hi = a + h < numel ? orc_abs_pairwise(w, numel, a + h, h) : 0.0;
+    return lo + hi;
+}
+
 int orc_pack(const float* w, int64_t numel, uint8_t* out, float* scale_out)
 {
     if (numel < 0 || (!w && numel) || !scale_out) return ORC_ERR_ARG;
-    double acc = 0.0;
-    for (int64_t i = 0; i < numel; ++i) acc += fabs((double)w[i]);
+    int64_t len = 1;
+    while (len < numel) len *= 2;
+    const double acc = numel ? orc_abs_pairwise(w, numel, 0, len) : 0.0;
     float mean = numel ? (float)(acc / (double)numel) : 0.0f;
     float scale = mean + 1e-6f;
     float inv = (float)(1.0 / (double)scale);

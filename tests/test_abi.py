@@ -169,3 +169,17 @@ def test_no_device_is_an_error():
     rc = bl.lib.btl_init(0)
     assert rc in (bl.BTL_ERR_HIP, bl.BTL_ERR_DEVICE)
     assert bl.lib.btl_last_error() != b""
+
+
+def test_pack_device_validation():
+    p = bl.lib.btl_pack_device
+    assert p(16, -1, 4, 16, 16, None, 0, None) == bl.BTL_ERR_SHAPE
+    assert p(None, 2, 4, 16, 16, None, 0, None) == bl.BTL_ERR_ARG                # w
+    assert p(16, 2, 4, None, 16, None, 0, None) == bl.BTL_ERR_ARG                # out
+    assert p(16, 2, 4, 16, None, None, 0, None) == bl.BTL_ERR_ARG                # scale
+    assert p(20, 2, 4, 16, 16, None, 0, None) == bl.BTL_ERR_LAYOUT               # w 16 B
+    assert p(16, 2, 4, 18, 16, None, 0, None) == bl.BTL_ERR_LAYOUT               # out 4 B
+    ws = bl.lib.btl_pack_workspace_bytes
+    assert ws(0, 5) == 0 and ws(-1, 5) == 0
+    assert ws(1, 4096) == 8 and ws(1, 4097) == 3 * 8
+    assert ws(4096, 14336) == (14336 + 4 + 1) * 8

@@ -537,3 +537,31 @@ def test_fused_with_caller_workspace_and_graph_replays():
         graph.replay()
         torch.cuda.synchronize()
         assert_f32_identical(out[0], yr)
+
+
+# --- PackedTensor::pack on the device ---------------------------------------------
+
+@pytest.mark.parametrize("shape", [(1, 4), (3, 5), (17, 33), (300, 4096), (4096, 14336)])
+def test_pack_device_equals_pack_host(shape):
+    print("pack_device", shape, flush=True)
+    rng = np.random.default_rng(shape[0] + shape[1])
+    w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    if w.size > 8:
+        w.reshape(-1)[:4] = 0.0
+    host = bl.PackedTensor.pack(torch.from_numpy(w))
+    dev = bl.PackedTensor.pack_device(torch.from_numpy(w).to(DEV))
+    assert np.float32(dev.scale).view(np.uint32) == np.float32(host.scale).view(np.uint32)
+    assert torch.equal(dev.data.cpu(), host.data)
+    if w.size <= 300 * 4096:
+        wb, sw = orc.pack(w)
+        assert np.array_equal(host.data.numpy(), wb) and np.float32(sw) == np.float32(host.scale)
+
+
+def test_pack_device_ties_and_specials():
+    # |w / s| exactly 0.5 rounds away from zero (packing.rs: f32::round); 1.5 and beyond clamp
+    w = np.array([[2.0, -2.0, 1.0, -1.0, 0.0, 6.0, -6.0, 4.0]], np.float32)
+    host = bl.PackedTensor.pack(torch.from_numpy(w))
+    dev = bl.PackedTensor.pack_device(torch.from_numpy(w).to(DEV))
+    assert torch.equal(dev.data.cpu(), host.data) and dev.scale == host.scale
+    wb, sw = orc.pack(w)
+    assert np.array_equal(host.data.numpy(), wb)
