@@ -31,6 +31,31 @@ def test_oracle_reproduces_golden(g):
     assert np.array_equal(orc.f32_to_bf16(y), g["dec_y_bf16"])
 
 
+def test_pack_golden(g):
+    w = g["pack_w"]
+    wb, sw = orc.pack(w)
+    assert np.array_equal(wb, g["pack_b"]) and np.float32(sw).view(np.uint32) == g["pack_s"].view(np.uint32)
+    inv = np.float32(1.0 / np.float64(g["pack_s"]))
+    # the planted ties: w * inv == +-0.5 exactly, which f32::round takes away from zero
+    assert np.float32(w[1, 5] * inv) == 0.5 and np.float32(w[2, 7] * inv) == -0.5
+    codes = lambda e: (int(g["pack_b"][e // 4]) >> (2 * (e % 4))) & 3
+    assert codes(1 * 129 + 5) == 1 and codes(2 * 129 + 7) == 2 and codes(1) == 0 and codes(2) == 0
+    # the last byte's unused fields stay 00
+    assert w.size % 4 == 1 and int(g["pack_b"][-1]) >> 2 == 0
+    import bitlinear as bl
+    host = bl.PackedTensor.pack(torch.from_numpy(w))
+    assert np.array_equal(host.data.numpy(), g["pack_b"]) and np.float32(host.scale) == g["pack_s"]
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")
+def test_gpu_pack_matches_golden(g):
+    import bitlinear as bl
+    dev = bl.PackedTensor.pack_device(torch.from_numpy(g["pack_w"]).to("cuda"))
+    assert np.array_equal(dev.data.cpu().numpy(), g["pack_b"])
+    assert np.float32(dev.scale).view(np.uint32) == g["pack_s"].view(np.uint32)
+
+
 @pytest.mark.gpu
 @pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")
 def test_gpu_matches_golden(g):

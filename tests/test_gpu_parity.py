@@ -557,8 +557,8 @@ def test_pack_device_equals_pack_host(shape):
         assert np.array_equal(host.data.numpy(), wb) and np.float32(sw) == np.float32(host.scale)
 
 
-def test_pack_device_ties_and_specials():
-    # |w / s| exactly 0.5 rounds away from zero (packing.rs: f32::round); 1.5 and beyond clamp
+def test_pack_device_clamps_and_zeros():
+    # |w / s| beyond 1.5 clamps to +-1, small values go to 0 (exact ties: test_golden.py)
     w = np.array([[2.0, -2.0, 1.0, -1.0, 0.0, 6.0, -6.0, 4.0]], np.float32)
     host = bl.PackedTensor.pack(torch.from_numpy(w))
     dev = bl.PackedTensor.pack_device(torch.from_numpy(w).to(DEV))
