@@ -273,6 +273,8 @@ def run_decode(args):
         result["batched_decode"] = run_sweep(layers, gen, dev, args)
     if args.pack:
         result["pack"] = run_pack(gen, dev)
+    if args.e2e:
+        result["e2e"] = run_e2e(layers, gen, dev, args)
     if args.cpu_baseline:
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         host = []
@@ -417,6 +419,72 @@ def run_sweep(layers, gen, dev, args):
             "rows": rows}
 
 
+def run_e2e(layers, gen, dev, args):
+    """cfg5: the end-to-end ternary decoder (bitlinear.model.BitLlamaHip) with
+    Llama-3-8B shapes on the same 32 layers of packed weights, plus seeded norm
+    weights, an f32 embedding table and a ternary lm_head (vocab 128256): a
+    prompt of 512 uniform random ids prefilled in one batch, then 256 greedy
+    decode steps at batch 1, each a HIP-graph replay of one step with the
+    position and next id on the device (no host synchronisation between steps).
+    Timed separately: the prefill (HIP events around it) and the decode steps
+    after the first (events around the replays)."""
+    from bitlinear.model import BitLlamaHip, LlamaConfig
+    prompt_len, gen_len = args.e2e_prompt, args.e2e_tokens
+    cfg = LlamaConfig.llama3_8b(max_seq=prompt_len + gen_len + 1)
+
+    def norm():
+        return (1.0 + 0.1 * torch.randn((HIDDEN,), generator=gen, device=dev)).contiguous()
+
+    w = torch.randn((cfg.vocab, HIDDEN), generator=gen, device=dev) * 0.02
+    head = bl.PackedTensor.pack_device(w)
+    del w
+    weights = {"embed": torch.randn((cfg.vocab, HIDDEN), generator=gen, device=dev), "norm_f": norm(),
+               "lm_head": head,
+               "layers": [dict(L, norm1=norm(), norm2=norm()) for L in layers]}
+    model = BitLlamaHip(cfg, weights, dev, max_rows=prompt_len)
+    prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=gen, device=dev).cpu().numpy()
+    model.reset()
+    model.prefill(prompt)  # warm-up (sizes the library workspace)
+    torch.cuda.synchronize()
+    model.reset()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    model.prefill(prompt)
+    e1.record()
+    torch.cuda.synchronize()
+    prefill_ms = e0.elapsed_time(e1)
+    model.greedy()
+    start = model.pos
+    model.start_decode()
+    model.decode_steps(1, use_graph=False)
+    model.capture_decode()
+    torch.cuda.synchronize()
+    e0.record()
+    model.decode_steps(gen_len - 2, use_graph=True)
+    e1.record()
+    torch.cuda.synchronize()
+    dec_ms = e0.elapsed_time(e1) / (gen_len - 2)
+    toks = model.log[start:start + gen_len].cpu().numpy()
+    print("bench: e2e prefill %d tokens %.2f ms, decode %.3f ms/token" % (prompt_len, prefill_ms, dec_ms),
+          file=sys.stderr, flush=True)
+    # per-step bytes: the 32 layers' packed weights + lm_head + the Q8 KV rows read at the mean context
+    wbytes = sum(L[nm].data.numel() for L in layers for nm in ("q", "k", "v", "o", "gate", "up", "down"))
+    mean_ctx = prompt_len + gen_len / 2
+    kv_bytes = LAYERS * 2 * cfg.n_kv_heads * mean_ctx * (cfg.head_dim + 4)
+    step_bytes = wbytes + head.data.numel() + kv_bytes
+    del model
+    return {"workload": "cfg5: Llama-3-8B-shaped ternary decoder, 32 layers, hidden 4096, 32/8 heads x 128, "
+                        "intermediate 14336, vocab 128256, every linear BitLinear W1.58-A8 (lm_head too), Q8 KV "
+                        "cache; %d-token uniform random prompt prefilled in one batch, %d greedy tokens at batch 1 "
+                        "(HIP-graph step, device-side position)" % (prompt_len, gen_len),
+            "prefill_tok_s": round(prompt_len / prefill_ms * 1000.0, 1), "prefill_ms": round(prefill_ms, 3),
+            "decode_tok_s": round(1000.0 / dec_ms, 1), "decode_ms_per_token": round(dec_ms, 4),
+            "decode_bytes_per_token": int(step_bytes),
+            "decode_frac_hbm": round(step_bytes / dec_ms / 1e6 / HBM_PEAK_GBS, 3),
+            "launches_per_token": 1 + LAYERS * 10 + 3,
+            "first_tokens": [int(t) for t in toks[:8]]}
+
+
 def run_pack(gen, dev):
     """PackedTensor::pack on the device (btl_pack_device) of one f32 weight of the
     MLP up shape 14336 x 4096: the load-time quantisation a checkpoint loader
@@ -490,6 +558,10 @@ def main():
                     help="skip the cfg3 batched-decode section of the JSON line")
     ap.add_argument("--probe", choices=["decode_gate_up", "prefill_gate_up"], default=None,
                     help="counter-run mode: --steps launches of one workload and a 256 MiB copy; no JSON")
+    ap.add_argument("--no-e2e", dest="e2e", action="store_false",
+                    help="skip the cfg5 end-to-end decoder section of the JSON line")
+    ap.add_argument("--e2e-prompt", type=int, default=512)
+    ap.add_argument("--e2e-tokens", type=int, default=256)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1:

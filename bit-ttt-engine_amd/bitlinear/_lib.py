@@ -32,6 +32,9 @@ EXPORTS = (
     "btl_linear_i8", "btl_linear_group", "btl_quantize_act_op", "btl_linear_i8_op",
     "btl_rmsnorm_linear_group", "btl_swiglu_linear_group",
     "btl_workspace_bytes", "btl_workspace_clear",
+    # include/bitllama.h
+    "btl_rope_table", "btl_rope_kv_append", "btl_attention_workspace_bytes", "btl_attention",
+    "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm_linear_group",
 )
 
 
@@ -39,6 +42,13 @@ class BtlPacked(ctypes.Structure):
     """btl_packed_t: mirrors the reference's PackedTensor (kernels/packing.rs:14-21)."""
     _fields_ = [("data", ctypes.c_void_p), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
                 ("scale", ctypes.c_float)]
+
+
+class BtlKvQ8(ctypes.Structure):
+    """btl_kv_q8_t: one layer of the reference's QuantizedKVCache (kv_cache.rs:14-22)."""
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("k_scale", ctypes.c_void_p),
+                ("v_scale", ctypes.c_void_p), ("n_kv_heads", ctypes.c_int64), ("max_seq", ctypes.c_int64),
+                ("head_dim", ctypes.c_int64)]
 
 
 class BitLinearError(RuntimeError):
@@ -77,6 +87,14 @@ def _load():
         "btl_swiglu_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, i32, i64, i64, i32, vp, sz, vp]),
         "btl_workspace_bytes": (sz, [i64, i64, i64, i32]),
         "btl_workspace_clear": (i32, [vp, sz, vp]),
+        "btl_rope_table": (i32, [ctypes.c_double, i64, i64, vp, vp]),
+        "btl_rope_kv_append": (i32, [vp, vp, vp, i64, i64, P(BtlKvQ8), i64, vp, vp, vp, vp, vp]),
+        "btl_attention_workspace_bytes": (sz, [i64, i64, P(BtlKvQ8)]),
+        "btl_attention": (i32, [vp, i64, i64, P(BtlKvQ8), i64, vp, vp, vp, sz, vp]),
+        "btl_embedding": (i32, [vp, i32, i64, i64, vp, i64, vp, vp]),
+        "btl_greedy_next": (i32, [vp, i64, vp, vp, vp, i64, vp]),
+        "btl_add_rmsnorm_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, vp, f32, i64, i64, i32, vp, sz,
+                                               vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

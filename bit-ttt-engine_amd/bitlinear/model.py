@@ -1,0 +1,306 @@
+"""A Llama-shaped ternary decoder on the C ABI: the host side of the reference's
+BitLlama inference path with every BitLinear and the ops around it on the GPU.
+
+Reference (imonoonoko/Bit-TTT-Engine, crates/rust_engine/src):
+  BitLlama::forward_one            model/llama.rs:201-271   (embedding, blocks, norm, lm_head)
+  BitLlamaBlock::forward           model/block.rs:90-138    (norm1, attention, residual, norm2, MLP, residual)
+  BitAttention::forward            layers/attention.rs:149-224 (q/k/v, RoPE, Q8 cache, softmax, o_proj)
+  QuantizedKVCache                 layers/kv_cache.rs:14-128
+  SwiGLU::forward                  layers/swiglu.rs:29-35
+  Llama::stream_completion         model/llama.rs:471-530   (prefill, then greedy decode)
+
+Mapping of the block onto the C ABI (one row of activations per token, f32 between ops):
+  h += mlp_out(l-1); q,k,v = BitLinear(RMSNorm1(h))   btl_add_rmsnorm_linear_group
+  RoPE(q, k); cache.append(k, v)                       btl_rope_kv_append
+  attn = softmax(q k^T / sqrt(d)) v                    btl_attention
+  o = BitLinear_o(attn)                                btl_linear_group
+  h += o; gate, up = BitLinear(RMSNorm2(h))            btl_add_rmsnorm_linear_group
+  mlp_out = BitLinear_down(silu(gate) * up)            btl_swiglu_linear_group
+and after the last block h += mlp_out, logits = lm_head(RMSNorm_f(h)) in one
+more btl_add_rmsnorm_linear_group.  Every linear is a BitLinear (W1.58-A8),
+the lm_head included.
+
+Deliberate differences from the reference, all on the host side:
+  * the prompt is prefilled as one batch of rows (the reference feeds it token by
+    token through forward_one, llama.rs:489-493); every op is row-independent or
+    causal, so the state and logits are the same bits as token-by-token steps
+    (a GPU test checks this);
+  * the first decode step feeds the token chosen from the prompt's last logits
+    (the reference feeds the last prompt token a second time, llama.rs:496-499);
+  * the TTT layer variant and sampling with temperature are not built.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from ._lib import BTL_F32, BTL_BF16, BtlKvQ8, BtlPacked, check, lib
+from .packed import PackedTensor
+
+RMS_NORM_EPS = 1e-5  # block.rs:10
+
+
+class LlamaConfig:
+    """The shape fields of BitLlamaConfig (model/config.rs) the decoder needs."""
+
+    def __init__(self, hidden, n_layers, n_heads, n_kv_heads, intermediate, vocab, rope_theta=500000.0,
+                 max_seq=1024, eps=RMS_NORM_EPS):
+        self.hidden = hidden
+        self.n_layers = n_layers
+        self.n_heads = n_heads
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = hidden // n_heads
+        self.intermediate = intermediate
+        self.vocab = vocab
+        self.rope_theta = rope_theta
+        self.max_seq = max_seq
+        self.eps = eps
+
+    @staticmethod
+    def llama3_8b(max_seq=1024):
+        """models/Meta-Llama-3-8B/config.json shapes."""
+        return LlamaConfig(4096, 32, 32, 8, 14336, 128256, 500000.0, max_seq)
+
+
+class KVCacheQ8:
+    """QuantizedKVCache (kv_cache.rs:14-128) of one layer, allocated for max_seq rows."""
+
+    def __init__(self, n_kv_heads, max_seq, head_dim, device):
+        self.k = torch.zeros((n_kv_heads, max_seq, head_dim), dtype=torch.uint8, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.k_scale = torch.zeros((n_kv_heads, max_seq), dtype=torch.float32, device=device)
+        self.v_scale = torch.zeros_like(self.k_scale)
+        self.c = BtlKvQ8(self.k.data_ptr(), self.v.data_ptr(), self.k_scale.data_ptr(), self.v_scale.data_ptr(),
+                         n_kv_heads, max_seq, head_dim)
+
+    def reset(self):
+        """kv_cache.rs:38-45 (rows are overwritten by the next appends)."""
+        self.k.zero_()
+        self.v.zero_()
+        self.k_scale.zero_()
+        self.v_scale.zero_()
+
+
+def _arr(packed):
+    cs = [p.as_c() for p in packed]
+    return cs, (ctypes.POINTER(BtlPacked) * len(cs))(*[ctypes.pointer(c) for c in cs])
+
+
+def _ptrs(ts):
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+
+class BitLlamaHip:
+    """BitLlama with attention blocks (ModelArch::Llama), all linears packed ternary.
+
+    weights: dict with
+      "embed" [vocab, hidden] float32 or bfloat16 (GPU),
+      "norm_f" [hidden] float32, "lm_head" PackedTensor [vocab, hidden],
+      "layers": list of dicts {"norm1", "norm2": [hidden] f32,
+                               "q", "k", "v", "o", "gate", "up", "down": PackedTensor}.
+    """
+
+    def __init__(self, cfg, weights, device="cuda", max_rows=512):
+        self.cfg = cfg
+        self.dev = torch.device(device)
+        self.w = weights
+        self.max_rows = max_rows
+        c = cfg
+        f32 = dict(dtype=torch.float32, device=self.dev)
+        M = max_rows
+        self.h = torch.zeros((M, c.hidden), **f32)
+        self.q = torch.zeros((M, c.n_heads * c.head_dim), **f32)
+        self.k = torch.zeros((M, c.n_kv_heads * c.head_dim), **f32)
+        self.v = torch.zeros((M, c.n_kv_heads * c.head_dim), **f32)
+        self.attn = torch.zeros((M, c.n_heads * c.head_dim), **f32)
+        self.o = torch.zeros((M, c.hidden), **f32)
+        self.gate = torch.zeros((M, c.intermediate), **f32)
+        self.up = torch.zeros((M, c.intermediate), **f32)
+        self.down = torch.zeros((M, c.hidden), **f32)
+        self.logits = torch.zeros((1, c.vocab), **f32)
+        self.ids = torch.zeros((M,), dtype=torch.int32, device=self.dev)
+        self.next_id = torch.zeros((1,), dtype=torch.int32, device=self.dev)
+        self.d_pos = torch.zeros((1,), dtype=torch.int32, device=self.dev)
+        self.log = torch.zeros((c.max_seq + 1,), dtype=torch.int32, device=self.dev)
+        cos = np.zeros((c.max_seq, c.head_dim // 2), np.float32)
+        sin = np.zeros_like(cos)
+        check(lib.btl_rope_table(float(c.rope_theta), c.head_dim, c.max_seq, cos.ctypes.data, sin.ctypes.data))
+        self.rope_cos = torch.from_numpy(cos).to(self.dev)
+        self.rope_sin = torch.from_numpy(sin).to(self.dev)
+        self.caches = [KVCacheQ8(c.n_kv_heads, c.max_seq, c.head_dim, self.dev) for _ in range(c.n_layers)]
+        emb = weights["embed"]
+        self.emb_dtype = BTL_BF16 if emb.dtype == torch.bfloat16 else BTL_F32
+        # pre-bound C arguments (pointers resolved once)
+        self._layers = []
+        for L in weights["layers"]:
+            qkv_c, qkv = _arr([L["q"], L["k"], L["v"]])
+            o_c, o = _arr([L["o"]])
+            gu_c, gu = _arr([L["gate"], L["up"]])
+            d_c, d = _arr([L["down"]])
+            self._layers.append(dict(keep=(qkv_c, o_c, gu_c, d_c), qkv=qkv, o=o, gu=gu, down=d,
+                                     n1=L["norm1"].data_ptr(), n2=L["norm2"].data_ptr()))
+        self._head_c, self._head = _arr([weights["lm_head"]])
+        self._y_qkv = _ptrs([self.q, self.k, self.v])
+        self._y_o = _ptrs([self.o])
+        self._y_gu = _ptrs([self.gate, self.up])
+        self._y_down = _ptrs([self.down])
+        self._y_logits = _ptrs([self.logits])
+        self.pos = 0
+        self.graph = None
+
+    # ------------------------------------------------------------------ steps
+    def _stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+
+    def _run(self, m, pos, d_pos, ids):
+        """One forward of m rows, token ids in the device int32 tensor `ids`, at
+        positions pos.. (or *d_pos.. when d_pos is a device tensor); leaves the last
+        row's logits in self.logits."""
+        c, st = self.cfg, self._stream()
+        dp = ctypes.c_void_p(d_pos.data_ptr()) if d_pos is not None else None
+        hid = c.hidden
+        check(lib.btl_embedding(self.w["embed"].data_ptr(), self.emb_dtype, c.vocab, hid, ids.data_ptr(), m,
+                                self.h.data_ptr(), st))
+        for li, L in enumerate(self._layers):
+            cache = self.caches[li].c
+            delta = self.down.data_ptr() if li > 0 else None
+            check(lib.btl_add_rmsnorm_linear_group(L["qkv"], self._y_qkv, 3, self.h.data_ptr(), delta, L["n1"],
+                                                   c.eps, m, hid, BTL_F32, None, 0, st))
+            check(lib.btl_rope_kv_append(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), m, c.n_heads,
+                                         ctypes.byref(cache), pos, dp, self.rope_cos.data_ptr(),
+                                         self.rope_sin.data_ptr(), self.q.data_ptr(), st))
+            check(lib.btl_attention(self.q.data_ptr(), m, c.n_heads, ctypes.byref(cache), pos, dp,
+                                    self.attn.data_ptr(), None, 0, st))
+            check(lib.btl_linear_group(L["o"], self._y_o, 1, self.attn.data_ptr(), BTL_F32, m,
+                                       c.n_heads * c.head_dim, BTL_F32, None, 0, st))
+            check(lib.btl_add_rmsnorm_linear_group(L["gu"], self._y_gu, 2, self.h.data_ptr(), self.o.data_ptr(),
+                                                   L["n2"], c.eps, m, hid, BTL_F32, None, 0, st))
+            check(lib.btl_swiglu_linear_group(L["down"], self._y_down, 1, self.gate.data_ptr(), self.up.data_ptr(),
+                                              BTL_F32, m, c.intermediate, BTL_F32, None, 0, st))
+        last = m - 1
+        check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, self.h[last].data_ptr(),
+                                               self.down[last].data_ptr(), self.w["norm_f"].data_ptr(), c.eps, 1,
+                                               hid, BTL_F32, None, 0, st))
+
+    def reset(self):
+        """Llama::reset_state / BitLlama::reset_kv_cache (llama.rs:179-186, 460-468)."""
+        for cache in self.caches:
+            cache.reset()
+        self.pos = 0
+        self.graph = None
+
+    def forward_one(self, token):
+        """BitLlama::forward_one (llama.rs:201-271): one token at the current position;
+        returns the logits [vocab] (a view of the model's buffer)."""
+        if self.pos >= self.cfg.max_seq:
+            raise ValueError("the cache of %d rows is full" % self.cfg.max_seq)
+        self.ids[0] = int(token)
+        self._run(1, self.pos, None, self.ids)
+        self.pos += 1
+        return self.logits[0]
+
+    def prefill(self, ids):
+        """The prompt in batches of up to max_rows rows; returns the last logits."""
+        ids = torch.as_tensor(np.asarray(ids, dtype=np.int32)).to(self.dev)
+        n = ids.numel()
+        if n == 0 or self.pos + n > self.cfg.max_seq:
+            raise ValueError("prompt of %d tokens does not fit the cache (%d rows, %d used)"
+                             % (n, self.cfg.max_seq, self.pos))
+        for s in range(0, n, self.max_rows):
+            m = min(self.max_rows, n - s)
+            self.ids[:m] = ids[s:s + m]
+            self._run(m, self.pos, None, self.ids)
+            self.pos += m
+        return self.logits[0]
+
+    def greedy(self):
+        """The greedy pick of the current logits on the device (llama.rs:509-515)
+        into self.next_id; returns it as an int (synchronises)."""
+        check(lib.btl_greedy_next(self.logits.data_ptr(), self.cfg.vocab, self.next_id.data_ptr(), None, None, 0,
+                                  self._stream()))
+        return int(self.next_id.item())
+
+    # ------------------------------------------------------- device decode loop
+    def _step_device(self):
+        """One decode step with the position on the device: the token in next_id at
+        position *d_pos through the blocks and the head, then the greedy pick
+        (next_id, log[*d_pos + 1], ++*d_pos)."""
+        self._run(1, 0, self.d_pos, self.next_id)
+        check(lib.btl_greedy_next(self.logits.data_ptr(), self.cfg.vocab, self.next_id.data_ptr(),
+                                  self.d_pos.data_ptr(), self.log.data_ptr(), self.log.numel(), self._stream()))
+
+    def capture_decode(self):
+        """Capture one device-position decode step in a HIP graph.  The library
+        workspace must already be large enough (any earlier forward sizes it)."""
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream(self.dev)
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self._step_device()
+        torch.cuda.synchronize(self.dev)
+        self.graph = g
+        return g
+
+    def start_decode(self):
+        """Seed the device loop from the host state: *d_pos = pos, log[pos] = next_id."""
+        self.d_pos.fill_(self.pos)
+        if self.pos < self.log.numel():
+            self.log[self.pos:self.pos + 1].copy_(self.next_id)
+
+    def decode_steps(self, n, use_graph=True):
+        """n greedy steps on the device, no host synchronisation in between; the
+        tokens accumulate in self.log."""
+        if self.pos + n > self.cfg.max_seq:
+            raise ValueError("%d steps from position %d overflow the cache of %d rows" % (n, self.pos, self.cfg.max_seq))
+        for _ in range(n):
+            if use_graph and self.graph is not None:
+                self.graph.replay()
+            else:
+                self._step_device()
+        self.pos += n
+
+    def generate(self, prompt_ids, max_tokens, use_graph=True):
+        """Llama::stream_completion at temperature 0 (llama.rs:471-530): prefill, then
+        greedy decode.  Returns the max_tokens generated ids."""
+        self.reset()
+        self.prefill(prompt_ids)
+        self.greedy()
+        start = self.pos
+        self.start_decode()
+        if max_tokens > 1:
+            if use_graph:
+                self.capture_decode()
+            self.decode_steps(max_tokens - 1, use_graph=use_graph)
+        torch.cuda.synchronize(self.dev)
+        return self.log[start:start + max_tokens].cpu().numpy().copy()
+
+
+def random_weights(cfg, device="cuda", seed=0, std=0.02, embed_dtype=torch.float32):
+    """Seeded synthetic weights of the architecture: N(0, std) dense weights
+    absmean-ternarised on the GPU (btl_pack_device), N(0, 1) embedding rows and
+    norm weights 1 + N(0, 0.1) (no checkpoint loading here)."""
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    c = cfg
+
+    def lin(n, k):
+        w = torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32) * std
+        p = PackedTensor.pack_device(w)
+        del w
+        return p
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn((n,), generator=gen, device=dev, dtype=torch.float32)).contiguous()
+
+    kvd = c.n_kv_heads * c.head_dim
+    layers = []
+    for _ in range(c.n_layers):
+        layers.append({"norm1": norm(c.hidden), "norm2": norm(c.hidden),
+                       "q": lin(c.n_heads * c.head_dim, c.hidden), "k": lin(kvd, c.hidden), "v": lin(kvd, c.hidden),
+                       "o": lin(c.hidden, c.n_heads * c.head_dim), "gate": lin(c.intermediate, c.hidden),
+                       "up": lin(c.intermediate, c.hidden), "down": lin(c.hidden, c.intermediate)})
+    embed = torch.randn((c.vocab, c.hidden), generator=gen, device=dev, dtype=torch.float32).to(embed_dtype)
+    return {"embed": embed.contiguous(), "norm_f": norm(c.hidden), "lm_head": lin(c.vocab, c.hidden),
+            "layers": layers}

@@ -32,8 +32,8 @@ HIP_FLAGS = [
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
              "-I" + os.path.join(ROCM, "include")]
 
-KERNEL_SOURCES = ["btl_kernels.hip"]
-HOST_SOURCES = ["btl_api.cpp"]
+KERNEL_SOURCES = ["btl_kernels.hip", "btl_model.hip"]
+HOST_SOURCES = ["btl_api.cpp", "btl_model_api.cpp"]
 
 
 def _run(cmd, verbose):

@@ -5,6 +5,7 @@
 // (crates/rust_engine/src/kernels/cpu.rs:17-127, cuda.rs:21-47) and
 // PackedTensor::{pack, unpack} (kernels/packing.rs:50-133).
 #include "bitlinear.h"
+#include "bitllama.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -16,6 +17,7 @@
 #include <mutex>
 #include <string>
 
+#include "btl_host.hpp"
 #include "btl_internal.hpp"
 
 namespace {
@@ -251,9 +253,10 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
 // btl_swiglu_linear_group).
 struct Xform {
     int kind;        // btl::XF_*
-    const void* x2;  // XF_SWIGLU: the up projection's output
-    const float* g;  // XF_RMSNORM: the norm weight [k]
+    const void* x2;  // XF_SWIGLU: the up projection's output; XF_ADD_RMSNORM: the delta
+    const float* g;  // XF_RMSNORM / XF_ADD_RMSNORM: the norm weight [k]
     float eps;
+    float* hout;     // XF_ADD_RMSNORM: the summed residual stream (may alias x)
 };
 
 // W1.58-A8 contraction of `count` layers sharing one input.
@@ -329,7 +332,8 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         q = (const int8_t*)ws + L.q_off;
         if (xf) {
             sxp = (const float*)((uint8_t*)ws + L.s_off);
-            e = btl::launch_xform_quant(x, xf->x2, xkind, xf->kind, xf->g, xf->eps, m, k, (int8_t*)q, (float*)sxp, st);
+            e = btl::launch_xform_quant(x, xf->x2, xkind, xf->kind, xf->g, xf->eps, m, k, (int8_t*)q, (float*)sxp, st,
+                                        xf->hout);
         } else if (xkind == btl::XK_I8) {
             e = btl::launch_op_order((const int8_t*)x, m, k, (int8_t*)q, st);
         } else {
@@ -681,9 +685,26 @@ int btl_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int c
     if (m == 0) return BTL_OK;
     if (!x || !g) return fail(BTL_ERR_LAYOUT, "null input or norm weight");
     if (!aligned16(x) || !aligned16(g)) return fail(BTL_ERR_LAYOUT, "x and g must be 16-byte aligned");
-    const Xform xf{btl::XF_RMSNORM, nullptr, g, eps};
+    const Xform xf{btl::XF_RMSNORM, nullptr, g, eps, nullptr};
     return run_i8(ls, count, x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k,
                   ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream, &xf);
+}
+
+int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, float* h,
+                                 const float* delta, const float* g, float eps, int64_t m, int64_t k, int ydtype,
+                                 void* ws, size_t ws_bytes, void* stream)
+{
+    Layer ls[btl::kMaxGroup];
+    int rc;
+    if ((rc = check_group(w, y, count, m, k, ydtype, ls))) return rc;
+    if ((rc = check_fused_shape(k, 65536, "fused residual + RMSNorm"))) return rc;
+    if (m == 0) return BTL_OK;
+    if (!h || !g) return fail(BTL_ERR_LAYOUT, "null residual or norm weight");
+    if (!aligned16(h) || !aligned16(g) || (delta && !aligned16(delta)))
+        return fail(BTL_ERR_LAYOUT, "h, delta and g must be 16-byte aligned");
+    const Xform xf{delta ? btl::XF_ADD_RMSNORM : btl::XF_RMSNORM, delta, g, eps, h};
+    return run_i8(ls, count, h, btl::XK_F32, nullptr, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws,
+                  ws_bytes, (hipStream_t)stream, &xf);
 }
 
 int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* gate,
@@ -697,7 +718,7 @@ int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int co
     if (m == 0) return BTL_OK;
     if (!gate || !up) return fail(BTL_ERR_LAYOUT, "null gate or up input");
     if (!aligned16(gate) || !aligned16(up)) return fail(BTL_ERR_LAYOUT, "gate and up must be 16-byte aligned");
-    const Xform xf{btl::XF_SWIGLU, up, nullptr, 0.0f};
+    const Xform xf{btl::XF_SWIGLU, up, nullptr, 0.0f, nullptr};
     return run_i8(ls, count, gate, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k,
                   ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream, &xf);
 }
@@ -730,3 +751,18 @@ int btl_workspace_clear(void* ws, size_t ws_bytes, void* stream)
 }
 
 }  // extern "C"
+
+// Error reporting, device and workspace helpers for the other C-ABI source
+// (btl_model_api.cpp), which shares this file's per-thread message and
+// per-device workspace.
+namespace btl {
+namespace host {
+int fail_msg(int code, const char* msg) { return fail(code, "%s", msg); }
+int hip_error(hipError_t e, const char* what) { return hip_fail(e, what); }
+int device(int* dev) { return current_device(dev); }
+int workspace(int dev, void* ws, size_t ws_bytes, size_t need, void** out)
+{
+    return get_ws(dev, ws, ws_bytes, need, out);
+}
+}  // namespace host
+}  // namespace btl

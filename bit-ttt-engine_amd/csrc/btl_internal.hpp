@@ -15,7 +15,8 @@ constexpr int kStepWeights = 256;  // weights of one row consumed per wave-load 
 // natural k order (XK_I8) or already in operand order (XK_I8O)
 enum XKind { XK_F32 = 0, XK_BF16 = 1, XK_I8 = 2, XK_I8O = 3 };
 // activation transforms fused ahead of the quantisation
-enum XForm { XF_NONE = 0, XF_RMSNORM = 1, XF_SWIGLU = 2 };
+// XF_ADD_RMSNORM: h = x + x2 (f32 residual + f32 delta, stored to hout), then RMSNorm of h
+enum XForm { XF_NONE = 0, XF_RMSNORM = 1, XF_SWIGLU = 2, XF_ADD_RMSNORM = 3 };
 enum YKind { YK_F32 = 0, YK_BF16 = 1 };
 
 // One layer of a (possibly grouped) decode launch.
@@ -91,9 +92,11 @@ hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_
                            hipStream_t st);
 // fused transform + operand-order quantisation, one workgroup per token row:
 // XF_RMSNORM: x / sqrt(pairwise_sum(x*x) * (f32)(1/k) + eps) * g (g: [k] f32);
-// XF_SWIGLU:  silu(x) * x2.  k % 64 == 0, k <= 65536; x (and x2) 16-byte aligned.
+// XF_SWIGLU:  silu(x) * x2;  XF_ADD_RMSNORM: hout = x + x2 (f32 both; hout may alias
+// x), then XF_RMSNORM of it.  k % 64 == 0, k <= 65536; x (and x2) 16-byte aligned.
 hipError_t launch_xform_quant(const void* x, const void* x2, int xkind, int xform, const float* g,
-                              float eps, int64_t m, int64_t k, int8_t* q, float* s, hipStream_t st);
+                              float eps, int64_t m, int64_t k, int8_t* q, float* s, hipStream_t st,
+                              float* hout = nullptr);
 
 hipError_t launch_quant_act(const void* x, int xkind, int64_t m, int64_t k, int8_t* q,
                             float* s, hipStream_t st);
@@ -113,5 +116,52 @@ hipError_t launch_unpack(const uint8_t* w, int64_t numel, float scale, float* ou
                          hipStream_t st);
 
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t st);
+
+// ---------------------------------------------------------------------------
+// decoder ops around the BitLinear path (btl_model.hip)
+// ---------------------------------------------------------------------------
+// RoPE on q / k rows of m new tokens, then the Q8 append of k and v into the
+// cache of one layer ([nkv][max_seq][hd] u8 codes, [nkv][max_seq] f32 scales).
+struct KvArgs {
+    const float* q;        // [m, nh * hd]
+    const float* k;        // [m, nkv * hd]
+    const float* v;        // [m, nkv * hd]
+    float* q_out;          // [m, nh * hd] rotated q (may alias q)
+    uint8_t* kc;
+    uint8_t* vc;
+    float* ksc;
+    float* vsc;
+    const float* cos_t;    // [max_seq, hd / 2]
+    const float* sin_t;
+    const int32_t* d_pos;  // position of token 0 on the device, or NULL: `pos`
+    int pos;
+    int m, nh, nkv, hd, max_seq;
+};
+hipError_t launch_rope_kv_q8(const KvArgs& a, hipStream_t st);
+
+// Attention of m queries (positions pos0 .. pos0 + m - 1, causal) over the Q8
+// cache of one layer: chunk partials into `part` ([m][nh][cmax][hd + 2] f32),
+// then their merge into out [m, nh * hd].
+struct AttnArgs {
+    const float* q;        // [m, nh * hd] rotated queries
+    const uint8_t* kc;
+    const uint8_t* vc;
+    const float* ksc;
+    const float* vsc;
+    const int32_t* d_pos;  // position of query 0 on the device, or NULL: `pos`
+    int pos;
+    int m, nh, nkv, hd, max_seq;
+    int cmax;              // chunk slots per (query, head): ceil(max_seq / 64)
+    int qb;                // queries per workgroup
+    float scal;            // (f32)(1 / sqrt(hd))
+    float* part;
+    float* out;
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+
+hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
+                        float* out, hipStream_t st);
+hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,
+                         int64_t log_len, hipStream_t st);
 
 }  // namespace btl

@@ -25,6 +25,7 @@
 // written (the oracle restates the same operations in C).
 #include <hip/hip_runtime.h>
 
+#include "btl_device.hpp"
 #include "btl_internal.hpp"
 
 namespace btl {
@@ -240,33 +241,6 @@ __device__ __forceinline__ uint4 group_quant(const uint4* v, float r)
     return o;
 }
 
-// Raw buffer loads: a per-workgroup resource descriptor bounds every access,
-// and an out-of-range offset reads zeros without a branch, so the compiler can
-// count the loads in flight exactly (s_waitcnt vmcnt(N) per step).
-constexpr int kOOB = 0x7FFFFFF0;  // offset outside every descriptor range
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, int off)
-{
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-
-// Max of a u32 over the wave, via DPP (quad perms, row rotations, row
-// broadcasts); the result is read from lane 63.
-__device__ __forceinline__ uint32_t wave_max_dpp(uint32_t v)
-{
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xF, 0xF, false));  // row_ror:4
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xF, 0xF, false));  // row_ror:8
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));  // row_bcast:15
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));  // row_bcast:31
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
 
 
 template <int XK, int ST, int MT>
@@ -559,32 +533,6 @@ hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_
     return hipGetLastError();
 }
 
-// exp(x) in f32: Cody-Waite reduction x = n ln2 + r (ln2 = hi + lo, hi with 15
-// significant bits so n*hi is exact), e^r by its Taylor polynomial to r^7/7!
-// in Horner form, scaled by 2^n through exponent bits (two exact steps outside
-// the normal range).  Every step is one rounded f32 operation, so the CPU
-// oracle's restatement gives the same bits.
-__device__ __forceinline__ float btl_expf(float x)
-{
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __uint_as_float(0x7F800000u);
-    if (x < -103.97208404541016f) return 0.0f;
-    const float n = __builtin_rintf(__fmul_rn(x, 1.44269502162933349609375f));
-    const float r = __fsub_rn(__fsub_rn(x, __fmul_rn(n, 0.693145751953125f)),
-                              __fmul_rn(n, 1.428606765330187045037746429443359375e-6f));
-    float p = 1.98412701138295233249664306640625e-4f;
-    p = __fadd_rn(__fmul_rn(p, r), 1.3888889225199818611145019531250e-3f);
-    p = __fadd_rn(__fmul_rn(p, r), 8.3333337679505348205566406250e-3f);
-    p = __fadd_rn(__fmul_rn(p, r), 4.1666667908430099487304687500e-2f);
-    p = __fadd_rn(__fmul_rn(p, r), 0.16666667163372039794921875f);
-    p = __fadd_rn(__fmul_rn(p, r), 0.5f);
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    p = __fadd_rn(__fmul_rn(p, r), 1.0f);
-    const int ni = (int)n;
-    if (ni > 127) return __fmul_rn(__fmul_rn(p, __uint_as_float(254u << 23)), __uint_as_float((uint32_t)(ni + 127 - 127) << 23));
-    if (ni < -126) return __fmul_rn(__fmul_rn(p, __uint_as_float((uint32_t)(ni + 64 + 127) << 23)), __uint_as_float(63u << 23));
-    return __fmul_rn(p, __uint_as_float((uint32_t)(ni + 127) << 23));
-}
 
 // Correctly rounded sqrt of an f32 (the hardware v_sqrt_f32 is not): for a
 // positive finite x = M * 2^(2h) with M an integer in [2^46, 2^48), r =
@@ -638,15 +586,6 @@ __device__ __forceinline__ void widen16(const uint4* v, float* f)
     }
 }
 
-// Pairwise sum over the lanes of a wave (xor butterfly: at level j lane i adds
-// lane i ^ 2^j, which is the pairwise tree over lanes in index order -- float
-// addition commutes).  Every lane ends with the wave's sum.
-__device__ __forceinline__ float wave_pairwise_sum(float v)
-{
-#pragma unroll
-    for (int j = 1; j < 64; j <<= 1) v = __fadd_rn(v, __shfl_xor(v, j, 64));
-    return v;
-}
 
 // k_xform_quant: transform + operand-order quantisation of one token row per
 // workgroup.  Thread t holds the G consecutive 16-element groups [tG, tG+G) in
@@ -656,7 +595,7 @@ __device__ __forceinline__ float wave_pairwise_sum(float v)
 // oracle computes over the row zero-padded to any power of two.
 template <int XK, int XF, int G>
 __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void* x2, const float* g, float eps,
-                                                       int k, int8_t* q, float* s)
+                                                       int k, int8_t* q, float* s, float* hout)
 {
     __shared__ float s_part[16];
     __shared__ uint32_t s_w[16];
@@ -701,7 +640,30 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
             }
         }
     }
-    if (XF == XF_RMSNORM) {
+    if (XF == XF_ADD_RMSNORM) {
+        // residual connection (block.rs:122,137: residual + mixed_out), f32 + f32
+        const __amdgpu_buffer_rsrc_t dr = make_rsrc((const uint8_t*)x2 + row * k * 4, (uint32_t)(k * 4));
+        float* hr = hout + row * k;
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const int gg = tid * G + gi;
+            const int off = gg < groups ? gg * 64 : kOOB;
+            uint4 v[4];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) v[h] = bload(dr, off + 16 * h);
+            float u[16];
+            widen16<XK_F32>(v, u);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) f[gi][e] = __fadd_rn(f[gi][e], u[e]);
+            if (gg < groups) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    *(float4*)(hr + gg * 16 + 4 * h) =
+                        make_float4(f[gi][4 * h], f[gi][4 * h + 1], f[gi][4 * h + 2], f[gi][4 * h + 3]);
+            }
+        }
+    }
+    if (XF == XF_RMSNORM || XF == XF_ADD_RMSNORM) {
         // pairwise sum of squares: 16G leaves per thread (zeros past k), lanes, waves
         float t[16 * G];
 #pragma unroll
@@ -776,8 +738,9 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
 }
 
 hipError_t launch_xform_quant(const void* x, const void* x2, int xkind, int xform, const float* g,
-                              float eps, int64_t m, int64_t k, int8_t* q, float* s, hipStream_t st)
+                              float eps, int64_t m, int64_t k, int8_t* q, float* s, hipStream_t st, float* hout)
 {
+    if (xform == XF_ADD_RMSNORM && (xkind != XK_F32 || !x2 || !hout)) return hipErrorInvalidValue;
     if (m <= 0) return hipSuccess;
     const int64_t groups = k >> 4;
     if (k % 64 != 0 || groups > (xform == XF_SWIGLU ? 2048 : 4096) || (xkind != XK_F32 && xkind != XK_BF16))
@@ -787,11 +750,11 @@ hipError_t launch_xform_quant(const void* x, const void* x2, int xkind, int xfor
     const dim3 grid((unsigned)m), block((unsigned)threads);
 #define BTL_XQ(XKV, XFV, GV)                                                                            \
     if (xkind == XKV && xform == XFV && G == GV) {                                                      \
-        hipLaunchKernelGGL((k_xform_quant<XKV, XFV, GV>), grid, block, 0, st, x, x2, g, eps, (int)k, q, s); \
+        hipLaunchKernelGGL((k_xform_quant<XKV, XFV, GV>), grid, block, 0, st, x, x2, g, eps, (int)k, q, s, hout); \
         return hipGetLastError();                                                                       \
     }
 #define BTL_XQ_G(XKV, XFV) BTL_XQ(XKV, XFV, 1) BTL_XQ(XKV, XFV, 2) BTL_XQ(XKV, XFV, 4)
-    BTL_XQ_G(XK_BF16, XF_RMSNORM) BTL_XQ_G(XK_F32, XF_RMSNORM)
+    BTL_XQ_G(XK_BF16, XF_RMSNORM) BTL_XQ_G(XK_F32, XF_RMSNORM) BTL_XQ_G(XK_F32, XF_ADD_RMSNORM)
     BTL_XQ(XK_BF16, XF_SWIGLU, 1) BTL_XQ(XK_BF16, XF_SWIGLU, 2) BTL_XQ(XK_F32, XF_SWIGLU, 1) BTL_XQ(XK_F32, XF_SWIGLU, 2)
 #undef BTL_XQ_G
 #undef BTL_XQ

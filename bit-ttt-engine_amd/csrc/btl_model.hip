@@ -1,0 +1,329 @@
+// btl_model.hip -- gfx950 kernels of the decoder ops around the BitLinear path.
+//
+// Reference (imonoonoko/Bit-TTT-Engine, crates/rust_engine):
+//   rotary embedding ........ src/layers/attention.rs:15-87
+//   Q8 KV cache ............. src/layers/kv_cache.rs:49-128
+//   attention ............... src/layers/attention.rs:149-239
+//   embedding / greedy pick . src/model/llama.rs:201-271, 509-515
+//
+// Kernels:
+//   k_rope_kv_q8     RoPE on the new q and k rows, then QuantizedKVCache::append
+//                    of k and v (per token-head absmax, zero point 128) into the
+//                    cache rows at their positions.  One wave per (token, head).
+//   k_attn_part      attention of a block of queries against one 64-key chunk of
+//                    one KV head: the chunk is dequantised once into LDS, each
+//                    wave is one query head of the GQA group.  Writes the chunk's
+//                    (max, sum, weighted values) per query and head.
+//   k_attn_combine   merges the chunk partials of each (query, head).
+//   k_embed          token ids -> f32 rows of the embedding table.
+//   k_greedy         argmax over the logits (last maximum wins), next id and
+//                    position bookkeeping for a device-resident decode loop.
+//
+// Compiled with -ffp-contract=off: every f32 operation is rounded as written and
+// the CPU oracle (oracle/bitllama_oracle.c) restates the same operations.
+#include <hip/hip_runtime.h>
+
+#include "btl_device.hpp"
+#include "btl_internal.hpp"
+
+namespace btl {
+
+// f32 max over the wave via DPP; every value finite or -inf.  Result from lane 63.
+__device__ __forceinline__ float wave_max_f32(float v)
+{
+#define BTL_FMAX_DPP(CTRL, RM)                                                                                 \
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, RM, 0xF, false)))
+    BTL_FMAX_DPP(0xB1, 0xF);
+    BTL_FMAX_DPP(0x4E, 0xF);
+    BTL_FMAX_DPP(0x124, 0xF);
+    BTL_FMAX_DPP(0x128, 0xF);
+    BTL_FMAX_DPP(0x142, 0xA);
+    BTL_FMAX_DPP(0x143, 0xC);
+#undef BTL_FMAX_DPP
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Rust `f32 as u8`: saturating, NaN -> 0 (kv_cache.rs:114 to_dtype(U8))
+__device__ __forceinline__ uint32_t sat_u8(float r)
+{
+    if (!(r > 0.0f)) return 0u;
+    if (r >= 255.0f) return 255u;
+    return (uint32_t)r;
+}
+
+// ---------------------------------------------------------------------------
+// k_rope_kv_q8
+// ---------------------------------------------------------------------------
+// grid (m, nh + 2 nkv), block 64.  Slot s < nh: q head s (RoPE, f32 out);
+// nh <= s < nh + nkv: k head (RoPE, then Q8 into the cache); else v head (Q8).
+// Lane i < hd/2 holds the pair (i, i + hd/2) that RotaryEmbedding::apply
+// rotates together (attention.rs:67-83).
+__global__ __launch_bounds__(64) void k_rope_kv_q8(KvArgs a)
+{
+    const int t = blockIdx.x, slot = blockIdx.y, lane = threadIdx.x;
+    const int pos = (a.d_pos ? *a.d_pos : a.pos) + t;
+    if (pos < 0 || pos >= a.max_seq) return;  // uniform per workgroup
+    const int hd = a.hd, half = hd >> 1;
+    const bool act = lane < half;
+    int kind, head;
+    const float* src;
+    if (slot < a.nh) {
+        kind = 0; head = slot;
+        src = a.q + ((int64_t)t * a.nh + head) * hd;
+    } else if (slot < a.nh + a.nkv) {
+        kind = 1; head = slot - a.nh;
+        src = a.k + ((int64_t)t * a.nkv + head) * hd;
+    } else {
+        kind = 2; head = slot - a.nh - a.nkv;
+        src = a.v + ((int64_t)t * a.nkv + head) * hd;
+    }
+    float x1 = act ? src[lane] : 0.0f, x2 = act ? src[lane + half] : 0.0f;
+    if (kind < 2 && act) {
+        const float c = a.cos_t[(int64_t)pos * half + lane], s = a.sin_t[(int64_t)pos * half + lane];
+        const float o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+        const float o2 = __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c));
+        x1 = o1;
+        x2 = o2;
+    }
+    if (kind == 0) {
+        if (act) {
+            float* dst = a.q_out + ((int64_t)t * a.nh + head) * hd;
+            dst[lane] = x1;
+            dst[lane + half] = x2;
+        }
+        return;
+    }
+    // quantize_q8 (kv_cache.rs:95-119): s = max|x| / 127, code = u8(round(x / s) + 128)
+    const uint32_t am = wave_max_dpp(max(__float_as_uint(x1) & 0x7FFFFFFFu, __float_as_uint(x2) & 0x7FFFFFFFu));
+    const float s = __fdiv_rn(__uint_as_float(am), 127.0f);
+    const int64_t row = (int64_t)head * a.max_seq + pos;
+    uint8_t* cache = (kind == 1 ? a.kc : a.vc) + row * hd;
+    if (act) {
+        cache[lane] = (uint8_t)sat_u8(__fadd_rn(__builtin_roundf(__fdiv_rn(x1, s)), 128.0f));
+        cache[lane + half] = (uint8_t)sat_u8(__fadd_rn(__builtin_roundf(__fdiv_rn(x2, s)), 128.0f));
+    }
+    if (lane == 0) (kind == 1 ? a.ksc : a.vsc)[row] = s;
+}
+
+hipError_t launch_rope_kv_q8(const KvArgs& a, hipStream_t st)
+{
+    if (a.m <= 0) return hipSuccess;
+    if (a.hd < 2 || a.hd > 128 || (a.hd & 1) || a.nh < 1 || a.nkv < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rope_kv_q8, dim3((unsigned)a.m, (unsigned)(a.nh + 2 * a.nkv)), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_attn_part: one 64-key chunk of one KV head against a block of queries
+// ---------------------------------------------------------------------------
+// grid (nkv, cmax, ceil(m / qb)), block 64 * rep (rep = nh / nkv query heads
+// share the KV head, repeat_kv attention.rs:227-239).  Query i sits at
+// position pos0 + i and sees keys [0, pos0 + i] (the causal mask of
+// attention.rs:245-270; a single decode query sees the whole cache).
+//   chunk keys dequantised once: kd = ((f32)code - 128) * s (kv_cache.rs:122-128)
+//   s_j   = (sum_d q[d] * kd[j][d], sequential over d) * scal      (lane j)
+//   m_c   = max_j s_j;  p_j = exp(s_j - m_c);  l_c = pairwise sum over the lanes
+//   o_c[d] = sum_j p_j * vd[j][d], sequential over j                (lane: d)
+constexpr int kAttnChunk = 64;
+constexpr int kAttnMaxHd = 128;
+constexpr int kAttnMaxRep = 16;
+
+__global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
+{
+    __shared__ float s_k[kAttnChunk][kAttnMaxHd + 1];
+    __shared__ float s_v[kAttnChunk][kAttnMaxHd];
+    __shared__ float s_q[kAttnMaxRep][kAttnMaxHd];
+    __shared__ float s_p[kAttnMaxRep][kAttnChunk];
+    const int g = blockIdx.x, c = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = blockDim.x;
+    const int hd = a.hd, rep = a.nh / a.nkv;
+    const int h = g * rep + wave;
+    const int pos0 = a.d_pos ? *a.d_pos : a.pos;
+    const int i_begin = blockIdx.z * a.qb;
+    const int i_end = min(a.m, i_begin + a.qb);
+    const int j0 = c * kAttnChunk;
+    const int t_last = min(pos0 + i_end, a.max_seq);  // keys any query of the block sees
+    if (j0 >= t_last) return;                           // uniform
+    const int nstage = min(kAttnChunk, t_last - j0);
+
+    // dequantise the chunk's keys and values into LDS
+    const int64_t base = (int64_t)g * a.max_seq + j0;
+    for (int idx = tid; idx < nstage * hd; idx += nthr) {
+        const int j = idx / hd, d = idx - j * hd;
+        const int64_t r = base + j;
+        s_k[j][d] = __fmul_rn(__fsub_rn((float)a.kc[r * hd + d], 128.0f), a.ksc[r]);
+        s_v[j][d] = __fmul_rn(__fsub_rn((float)a.vc[r * hd + d], 128.0f), a.vsc[r]);
+    }
+
+    for (int i = i_begin; i < i_end; ++i) {
+        const int T = min(pos0 + i + 1, a.max_seq);
+        if (j0 >= T) continue;  // uniform
+        const int nj = min(kAttnChunk, T - j0);
+        const float* qg = a.q + ((int64_t)i * a.nh + h) * hd;
+        for (int d = lane; d < hd; d += 64) s_q[wave][d] = qg[d];
+        __syncthreads();
+        float sc = -__builtin_inff();
+        if (lane < nj) {
+            float acc = 0.0f;
+            for (int d = 0; d < hd; ++d) acc = __fadd_rn(acc, __fmul_rn(s_q[wave][d], s_k[lane][d]));
+            sc = __fadd_rn(__fmul_rn(acc, a.scal), 0.0f);  // candle affine(scal, 0)
+        }
+        const float mc = wave_max_f32(sc);
+        const float p = lane < nj ? btl_expf(__fsub_rn(sc, mc)) : 0.0f;
+        const float lc = wave_pairwise_sum(p);
+        s_p[wave][lane] = p;
+        __syncthreads();
+        float* part = a.part + (((int64_t)i * a.nh + h) * a.cmax + c) * (hd + 2);
+        for (int d = lane; d < hd; d += 64) {
+            float o = 0.0f;
+            for (int j = 0; j < nj; ++j) o = __fadd_rn(o, __fmul_rn(s_p[wave][j], s_v[j][d]));
+            part[2 + d] = o;
+        }
+        if (lane == 0) {
+            part[0] = mc;
+            part[1] = lc;
+        }
+        __syncthreads();  // s_q / s_p are rewritten by the next query
+    }
+}
+
+// grid (m, nh), block 64: y[d] = (sum_c w_c o_c[d]) / (sum_c w_c l_c),
+// w_c = exp(m_c - max_c m_c), sums sequential over the chunks.
+__global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a)
+{
+    const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int hd = a.hd;
+    const int pos0 = a.d_pos ? *a.d_pos : a.pos;
+    const int T = min(pos0 + i + 1, a.max_seq);
+    float* y = a.out + ((int64_t)i * a.nh + h) * hd;
+    if (T <= 0) {
+        for (int d = lane; d < hd; d += 64) y[d] = __builtin_nanf("");
+        return;
+    }
+    const int C = (T + kAttnChunk - 1) / kAttnChunk;
+    const float* part = a.part + ((int64_t)i * a.nh + h) * a.cmax * (hd + 2);
+    float M = -__builtin_inff();
+    for (int c = 0; c < C; ++c) M = fmaxf(M, part[c * (hd + 2)]);
+    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+    const int d0 = lane, d1 = lane + 64;
+    for (int c = 0; c < C; ++c) {
+        const float* pc = part + c * (hd + 2);
+        const float w = btl_expf(__fsub_rn(pc[0], M));
+        L = __fadd_rn(L, __fmul_rn(w, pc[1]));
+        if (d0 < hd) O0 = __fadd_rn(O0, __fmul_rn(w, pc[2 + d0]));
+        if (d1 < hd) O1 = __fadd_rn(O1, __fmul_rn(w, pc[2 + d1]));
+    }
+    if (d0 < hd) y[d0] = __fdiv_rn(O0, L);
+    if (d1 < hd) y[d1] = __fdiv_rn(O1, L);
+}
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st)
+{
+    if (a.m <= 0) return hipSuccess;
+    const int rep = a.nh / a.nkv;
+    if (a.hd < 1 || a.hd > kAttnMaxHd || a.nkv < 1 || a.nh % a.nkv != 0 || rep > kAttnMaxRep || a.qb < 1 ||
+        a.cmax < 1)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)a.nkv, (unsigned)a.cmax, (unsigned)((a.m + a.qb - 1) / a.qb));
+    hipLaunchKernelGGL(k_attn_part, grid, dim3((unsigned)(64 * rep)), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)a.m, (unsigned)a.nh), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_embed: candle_nn::Embedding::forward (llama.rs:208) -> f32 rows
+// ---------------------------------------------------------------------------
+// grid (m), block 256.  An id outside [0, vocab) gives a zero row (the
+// reference's index_select would fail; ids from k_greedy are always in range).
+template <int XK>
+__global__ __launch_bounds__(256) void k_embed(const void* table, int64_t vocab, int dim, const int32_t* ids,
+                                               float* out)
+{
+    const int t = blockIdx.x;
+    const int64_t id = ids[t];
+    const bool ok = id >= 0 && id < vocab;
+    float* y = out + (int64_t)t * dim;
+    for (int d = threadIdx.x; d < dim; d += 256) {
+        float v = 0.0f;
+        if (ok) {
+            if (XK == XK_BF16) v = __uint_as_float((uint32_t)((const uint16_t*)table)[id * dim + d] << 16);
+            else v = ((const float*)table)[id * dim + d];
+        }
+        y[d] = v;
+    }
+}
+
+hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
+                        float* out, hipStream_t st)
+{
+    if (m <= 0) return hipSuccess;
+    if (xkind == XK_BF16) hipLaunchKernelGGL(k_embed<XK_BF16>, dim3((unsigned)m), dim3(256), 0, st, table, vocab, (int)dim, ids, out);
+    else hipLaunchKernelGGL(k_embed<XK_F32>, dim3((unsigned)m), dim3(256), 0, st, table, vocab, (int)dim, ids, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_greedy: the greedy pick of stream_completion (llama.rs:509-515)
+// ---------------------------------------------------------------------------
+// One workgroup of 1024 threads.  Each value maps to a key that orders floats
+// totally (-0 taken as +0; NaN above +inf: the reference's partial_cmp would
+// panic there); (key, index) pairs compare lexicographically, so equal maxima
+// resolve to the largest index, as Iterator::max_by does.  Thread 0 writes the
+// id; with d_pos it also stores it at log[*d_pos + 1] (the sequence position
+// the token will take) and advances *d_pos.
+__device__ __forceinline__ uint64_t greedy_key(float f, uint32_t idx)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) == 0u) u = 0u;
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | idx;
+}
+
+__global__ __launch_bounds__(1024) void k_greedy(const float* x, int n, int32_t* next_id, int32_t* d_pos,
+                                                 int32_t* log, int log_len)
+{
+    __shared__ uint64_t s_best[16];
+    const int tid = threadIdx.x;
+    uint64_t best = 0;
+    const int n4 = n >> 2;
+    for (int i = tid; i < n4; i += 1024) {
+        const float4 v = ((const float4*)x)[i];
+        best = max(best, greedy_key(v.x, 4 * i));
+        best = max(best, greedy_key(v.y, 4 * i + 1));
+        best = max(best, greedy_key(v.z, 4 * i + 2));
+        best = max(best, greedy_key(v.w, 4 * i + 3));
+    }
+    for (int i = 4 * n4 + tid; i < n; i += 1024) best = max(best, greedy_key(x[i], i));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, off, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(best >> 32), off, 64);
+        best = max(best, ((uint64_t)hi << 32) | lo);
+    }
+    if ((tid & 63) == 0) s_best[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w) best = max(best, s_best[w]);
+        const int32_t id = (int32_t)(uint32_t)best;
+        next_id[0] = id;
+        if (d_pos) {
+            const int32_t p = *d_pos;
+            if (log && p + 1 >= 0 && p + 1 < log_len) log[p + 1] = id;
+            *d_pos = p + 1;
+        }
+    }
+}
+
+hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log, int64_t log_len,
+                         hipStream_t st)
+{
+    if (n <= 0 || n > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_greedy, dim3(1), dim3(1024), 0, st, x, (int)n, next_id, d_pos, log,
+                       (int)(log_len > INT32_MAX ? INT32_MAX : log_len));
+    return hipGetLastError();
+}
+
+}  // namespace btl

@@ -1,0 +1,196 @@
+// btl_model_api.cpp -- C ABI of the decoder ops (include/bitllama.h): validation
+// and dispatch to the kernels of btl_model.hip.
+//
+// Host-side counterparts of the reference's RotaryEmbedding, QuantizedKVCache,
+// BitAttention::forward, Embedding and greedy pick (crates/rust_engine:
+// src/layers/attention.rs:15-239, src/layers/kv_cache.rs:49-128,
+// src/model/llama.rs:208, 509-515).
+#include "bitllama.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdio>
+#include <vector>
+
+#include "btl_host.hpp"
+#include "btl_internal.hpp"
+
+namespace {
+
+using btl::host::fail_msg;
+using btl::host::hip_error;
+
+template <typename... A>
+int failf(int code, const char* fmt, A... args)
+{
+    char buf[512];
+    snprintf(buf, sizeof(buf), fmt, args...);
+    return fail_msg(code, buf);
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+constexpr int64_t kChunk = 64;  // keys per attention chunk (k_attn_part)
+
+int check_cache(const btl_kv_q8_t* c, int64_t n_heads)
+{
+    if (!c) return fail_msg(BTL_ERR_ARG, "null KV cache");
+    if (!c->k || !c->v || !c->k_scale || !c->v_scale) return fail_msg(BTL_ERR_LAYOUT, "null KV cache buffer");
+    if (c->n_kv_heads < 1 || c->max_seq < 1 || c->head_dim < 2 || c->head_dim > 128 || (c->head_dim & 1))
+        return failf(BTL_ERR_SHAPE, "KV cache needs n_kv_heads >= 1, max_seq >= 1 and an even head_dim in 2..128 "
+                                    "(got %lld, %lld, %lld)",
+                     (long long)c->n_kv_heads, (long long)c->max_seq, (long long)c->head_dim);
+    if (n_heads < 1 || n_heads % c->n_kv_heads != 0 || n_heads / c->n_kv_heads > 16)
+        return failf(BTL_ERR_SHAPE, "n_heads %lld must be a multiple of n_kv_heads %lld, at most 16 times it",
+                     (long long)n_heads, (long long)c->n_kv_heads);
+    if (c->max_seq > (1 << 24) || c->n_kv_heads * c->max_seq * c->head_dim > ((int64_t)1 << 40))
+        return fail_msg(BTL_ERR_SHAPE, "KV cache too large");
+    return BTL_OK;
+}
+
+int check_pos(int64_t pos, int64_t m, const int32_t* d_pos, const btl_kv_q8_t* c)
+{
+    if (d_pos) return BTL_OK;  // read on the device; rows past max_seq are skipped there
+    if (pos < 0 || pos + m > c->max_seq)
+        return failf(BTL_ERR_SHAPE, "positions %lld..%lld outside the cache of %lld rows", (long long)pos,
+                     (long long)(pos + m - 1), (long long)c->max_seq);
+    return BTL_OK;
+}
+
+// queries per workgroup of k_attn_part: enough to reuse each dequantised chunk,
+// few enough that the grid still covers the chip
+int attn_qb(int64_t m) { return m <= 1 ? 1 : (m <= 64 ? 4 : 16); }
+
+}  // namespace
+
+extern "C" {
+
+int btl_rope_table(double theta, int64_t head_dim, int64_t max_seq, float* cos_out, float* sin_out)
+{
+    if (head_dim < 2 || (head_dim & 1) || max_seq < 0) return fail_msg(BTL_ERR_SHAPE, "head_dim must be even, max_seq >= 0");
+    if (!(theta > 0.0)) return fail_msg(BTL_ERR_ARG, "theta must be positive");
+    if (max_seq && (!cos_out || !sin_out)) return fail_msg(BTL_ERR_ARG, "null output");
+    const int64_t half = head_dim / 2;
+    std::vector<float> inv((size_t)half);
+    for (int64_t i = 0; i < half; ++i) inv[(size_t)i] = (float)(1.0 / std::pow(theta, (double)(2 * i) / (double)head_dim));
+    for (int64_t p = 0; p < max_seq; ++p)
+        for (int64_t i = 0; i < half; ++i) {
+            const float f = (float)p * inv[(size_t)i];
+            cos_out[p * half + i] = cosf(f);
+            sin_out[p * half + i] = sinf(f);
+        }
+    return BTL_OK;
+}
+
+int btl_rope_kv_append(const float* q, const float* k, const float* v, int64_t m, int64_t n_heads,
+                       const btl_kv_q8_t* cache, int64_t pos, const int32_t* d_pos, const float* rope_cos,
+                       const float* rope_sin, float* q_out, void* stream)
+{
+    int rc;
+    if ((rc = check_cache(cache, n_heads))) return rc;
+    if (m < 0 || m > (1 << 24)) return fail_msg(BTL_ERR_SHAPE, "token count out of range");
+    if ((rc = check_pos(pos, m, d_pos, cache))) return rc;
+    if (m == 0) return BTL_OK;
+    if (!q || !k || !v || !q_out || !rope_cos || !rope_sin) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    int dev;
+    if ((rc = btl::host::device(&dev))) return rc;
+    btl::KvArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.q_out = q_out;
+    a.kc = cache->k;
+    a.vc = cache->v;
+    a.ksc = cache->k_scale;
+    a.vsc = cache->v_scale;
+    a.cos_t = rope_cos;
+    a.sin_t = rope_sin;
+    a.d_pos = d_pos;
+    a.pos = (int)pos;
+    a.m = (int)m;
+    a.nh = (int)n_heads;
+    a.nkv = (int)cache->n_kv_heads;
+    a.hd = (int)cache->head_dim;
+    a.max_seq = (int)cache->max_seq;
+    hipError_t e = btl::launch_rope_kv_q8(a, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "rope / kv append kernel launch");
+    return BTL_OK;
+}
+
+size_t btl_attention_workspace_bytes(int64_t m, int64_t n_heads, const btl_kv_q8_t* cache)
+{
+    if (!cache || m < 0 || n_heads < 0 || cache->max_seq < 1) return 0;
+    const int64_t cmax = (cache->max_seq + kChunk - 1) / kChunk;
+    return (size_t)(m * n_heads * cmax * (cache->head_dim + 2) * 4);
+}
+
+int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t* cache, int64_t pos,
+                  const int32_t* d_pos, float* out, void* ws, size_t ws_bytes, void* stream)
+{
+    int rc;
+    if ((rc = check_cache(cache, n_heads))) return rc;
+    if (m < 0 || m > (1 << 20)) return fail_msg(BTL_ERR_SHAPE, "query count out of range");
+    if ((rc = check_pos(pos, m, d_pos, cache))) return rc;
+    if (m == 0) return BTL_OK;
+    if (!q || !out) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    int dev;
+    if ((rc = btl::host::device(&dev))) return rc;
+    void* part = nullptr;
+    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &part)))
+        return rc;
+    btl::AttnArgs a{};
+    a.q = q;
+    a.kc = cache->k;
+    a.vc = cache->v;
+    a.ksc = cache->k_scale;
+    a.vsc = cache->v_scale;
+    a.d_pos = d_pos;
+    a.pos = (int)pos;
+    a.m = (int)m;
+    a.nh = (int)n_heads;
+    a.nkv = (int)cache->n_kv_heads;
+    a.hd = (int)cache->head_dim;
+    a.max_seq = (int)cache->max_seq;
+    a.cmax = (int)((cache->max_seq + kChunk - 1) / kChunk);
+    a.qb = attn_qb(m);
+    a.scal = (float)(1.0 / std::sqrt((double)cache->head_dim));  // attention.rs:133, as candle's affine f32
+    a.part = (float*)part;
+    a.out = out;
+    hipError_t e = btl::launch_attention(a, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "attention kernel launch");
+    return BTL_OK;
+}
+
+int btl_embedding(const void* table, int dtype, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
+                  float* out, void* stream)
+{
+    if (dtype != BTL_F32 && dtype != BTL_BF16) return failf(BTL_ERR_DTYPE, "table dtype %d is not BTL_F32/BTL_BF16", dtype);
+    if (vocab < 0 || dim < 0 || m < 0 || dim > (1 << 24) || m > (1 << 24)) return fail_msg(BTL_ERR_SHAPE, "size out of range");
+    if (m == 0 || dim == 0) return BTL_OK;
+    if (!table || !ids || !out) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    int dev;
+    int rc = btl::host::device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_embed(table, dtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, vocab, dim, ids, m, out,
+                                     (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "embedding kernel launch");
+    return BTL_OK;
+}
+
+int btl_greedy_next(const float* logits, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,
+                    int64_t log_len, void* stream)
+{
+    if (n < 1 || n > INT32_MAX) return fail_msg(BTL_ERR_SHAPE, "logit count out of range");
+    if (!logits || !next_id) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    if (!aligned16(logits)) return fail_msg(BTL_ERR_LAYOUT, "logits must be 16-byte aligned");
+    if (log && log_len < 0) return fail_msg(BTL_ERR_ARG, "negative log length");
+    int dev;
+    int rc = btl::host::device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_greedy(logits, n, next_id, d_pos, log, log ? log_len : 0, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "greedy kernel launch");
+    return BTL_OK;
+}
+
+}  // extern "C"

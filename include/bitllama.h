@@ -1,0 +1,129 @@
+/*
+ * bitllama.h -- C ABI of the decoder ops around the BitLinear path
+ * (MI355X / gfx950), the neighbours that a Llama-shaped decoder built on
+ * bitlinear.h needs to run end to end on the device.
+ *
+ * Reference seams (imonoonoko/Bit-TTT-Engine, crate crates/rust_engine; Rust,
+ * not a C ABI):
+ *
+ *   RotaryEmbedding::{new, apply}            src/layers/attention.rs:15-87
+ *   QuantizedKVCache::{append, quantize_q8, dequantize_q8}
+ *                                            src/layers/kv_cache.rs:49-128
+ *   BitAttention::forward (after q/k/v, before o_proj)
+ *                                            src/layers/attention.rs:149-224
+ *   BitLlamaBlock::forward residual + norm2  src/model/block.rs:122-137
+ *   BitLlama::forward_one embedding          src/model/llama.rs:208
+ *   Llama::stream_completion greedy pick     src/model/llama.rs:509-515
+ *
+ * Conventions are those of bitlinear.h: int status (BTL_OK / BTL_ERR_*),
+ * btl_last_error(), device pointers, `stream` a hipStream_t as void*, nothing
+ * allocated or freed on the caller's behalf except the library workspace when
+ * ws == NULL.
+ *
+ * Positions.  Functions that place tokens in the sequence take `pos` (host) and
+ * `d_pos` (a device int32, or NULL).  With d_pos != NULL the kernels read the
+ * position from the device, so a captured HIP graph of one decode step can be
+ * replayed as the position advances (btl_greedy_next advances it).
+ */
+#ifndef BITLLAMA_H
+#define BITLLAMA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "bitlinear.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * The Q8 KV cache of one layer (QuantizedKVCache, kv_cache.rs:14-22): codes
+ * u8 = round(x / s) + 128, s = max|x| / 127 per (token, KV head).
+ * k, v:       device [n_kv_heads, max_seq, head_dim] u8
+ * k_scale, v_scale: device [n_kv_heads, max_seq] f32
+ * The reference grows its cache with Tensor::cat on every append
+ * (kv_cache.rs:57-77); here the caller allocates max_seq rows once and the
+ * append writes rows in place.
+ */
+typedef struct btl_kv_q8 {
+    uint8_t* k;
+    uint8_t* v;
+    float* k_scale;
+    float* v_scale;
+    int64_t n_kv_heads;
+    int64_t max_seq;
+    int64_t head_dim;
+} btl_kv_q8_t;
+
+/*
+ * RotaryEmbedding::new (attention.rs:15-42), host pointers:
+ * inv_freq[i] = (f32)(1 / theta^(2i / head_dim)) in double, freq = (f32)p * inv_freq[i],
+ * cos_out / sin_out [max_seq, head_dim / 2] = cosf / sinf of freq.
+ */
+int btl_rope_table(double theta, int64_t head_dim, int64_t max_seq, float* cos_out, float* sin_out);
+
+/*
+ * RoPE of m new tokens at positions p .. p + m - 1 (p = d_pos ? *d_pos : pos)
+ * on q [m, n_heads * head_dim] -> q_out (may alias q) and on
+ * k [m, n_kv * head_dim], then QuantizedKVCache::append of k and v
+ * [m, n_kv * head_dim] (quantize_q8, kv_cache.rs:95-119) into the cache rows
+ * of those positions.  RoPE per head pairs (i, i + head_dim/2):
+ * [x1*cos - x2*sin, x1*sin + x2*cos] (attention.rs:67-83), every product and
+ * sum an f32 rounding.  rope_cos / rope_sin: device copies of btl_rope_table.
+ * head_dim even, 2..128.  Rows at positions >= max_seq are not written.
+ */
+int btl_rope_kv_append(const float* q, const float* k, const float* v, int64_t m, int64_t n_heads,
+                       const btl_kv_q8_t* cache, int64_t pos, const int32_t* d_pos, const float* rope_cos,
+                       const float* rope_sin, float* q_out, void* stream);
+
+/*
+ * Attention of m queries (rotated, [m, n_heads * head_dim] f32) at positions
+ * p .. p + m - 1 over the Q8 cache, query i seeing keys [0, p + i] (the causal
+ * mask of attention.rs:245-270; one decode query sees the whole cache):
+ * softmax(q . k_deq * (f32)(1/sqrt(head_dim))) . v_deq, GQA head h reading KV
+ * head h / (n_heads / n_kv) (repeat_kv, attention.rs:227-239).
+ * out: [m, n_heads * head_dim] f32, heads in order (the reshape of
+ * attention.rs:219).  Summation order (fixed, so results are reproducible bit
+ * for bit): dot products sequential over head_dim; keys in chunks of 64, each
+ * chunk's (max m_c, sum l_c of exp(s - m_c), values o_c) merged with weights
+ * exp(m_c - max_c m_c) in chunk order; o = O / L.  n_heads % n_kv == 0,
+ * n_heads / n_kv <= 16, head_dim <= 128.  ws: btl_attention_workspace_bytes.
+ */
+size_t btl_attention_workspace_bytes(int64_t m, int64_t n_heads, const btl_kv_q8_t* cache);
+int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t* cache, int64_t pos,
+                  const int32_t* d_pos, float* out, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Embedding::forward (llama.rs:208): out[t] = (f32) table[ids[t]] for
+ * t < m.  table [vocab, dim] of dtype (BTL_F32 / BTL_BF16), ids device int32.
+ * An id outside [0, vocab) gives a zero row.
+ */
+int btl_embedding(const void* table, int dtype, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
+                  float* out, void* stream);
+
+/*
+ * Greedy pick (llama.rs:509-515): next_id[0] = argmax(logits[0..n)), the last
+ * index among equal maxima (Iterator::max_by).  With d_pos != NULL, also
+ * log[*d_pos + 1] = id when it is inside log[0..log_len), then *d_pos += 1:
+ * one decode step's bookkeeping on the device.  logits 16-byte aligned.
+ */
+int btl_greedy_next(const float* logits, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,
+                    int64_t log_len, void* stream);
+
+/*
+ * Residual connection fused ahead of RMSNorm and a BitLinear group
+ * (block.rs:122-123,137 then the next norm): h += delta (f32, in place), then
+ * btl_rmsnorm_linear_group on h.  delta == NULL: plain RMSNorm of h (h not
+ * written).  h, delta [m, k] f32, g [k] f32.  k % 64 == 0, 64 <= k <= 65536;
+ * h, delta and g 16-byte aligned.
+ */
+int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, float* h,
+                                 const float* delta, const float* g, float eps, int64_t m, int64_t k, int ydtype,
+                                 void* ws, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BITLLAMA_H */

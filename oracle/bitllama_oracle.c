@@ -1,0 +1,164 @@
+/*
+ * bitllama_oracle.c -- CPU restatement of the reference's decoder ops around
+ * the BitLinear path (rotary embedding, the Q8 KV cache, attention, greedy
+ * argmax).
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker.
+ * The product library (libbitlinear_hip.so) never links, loads or calls it.
+ *
+ * Restated from (paths inside imonoonoko/Bit-TTT-Engine, crate crates/rust_engine):
+ *
+ *   orc_rope_table   src/layers/attention.rs:15-42 (RotaryEmbedding::new):
+ *                    inv_freq in f64 rounded to f32, freq = (f32)p * inv_freq,
+ *                    cos / sin in f32 (cosf / sinf, the libm Rust's f32::cos
+ *                    calls on Linux)
+ *   orc_rope_apply   src/layers/attention.rs:46-87 (RotaryEmbedding::apply):
+ *                    [x1*cos - x2*sin, x1*sin + x2*cos], every op rounded
+ *   orc_q8_quant     src/layers/kv_cache.rs:95-119 (quantize_q8): s = max|x|/127,
+ *                    code = u8(round(x / s) + 128) with Rust's saturating
+ *                    `as u8` (NaN -> 0)
+ *   orc_q8_dequant   src/layers/kv_cache.rs:122-128 (dequantize_q8):
+ *                    ((f32)code - 128) * s
+ *   orc_attn_decode  src/layers/attention.rs:149-224 (BitAttention::forward at
+ *                    one query position): softmax(q.k * (1/sqrt(hd))) . v over
+ *                    the dequantised cache, GQA head h -> kv head h / (nh/nkv)
+ *                    (repeat_kv, :227-239).  The reference's sums run in candle's
+ *                    gemm order (not vendored); this restatement fixes the order
+ *                    the GPU kernels use, so the two agree bit for bit:
+ *                      dot(q, k_j) sequential over d, scaled by (f32)(1/sqrt(hd));
+ *                      keys in chunks of 64: m_c = max, p_j = exp(s_j - m_c),
+ *                      l_c = pairwise tree over the 64 lanes (zero-padded),
+ *                      o_c[d] = sum_j p_j * v_j[d] sequential over j;
+ *                      M = max_c m_c, w_c = exp(m_c - M), L = sum_c w_c * l_c,
+ *                      O[d] = sum_c w_c * o_c[d] (sequential over c), y = O / L.
+ *                    exp is orc_expf (bitlinear_oracle.c).  tests/test_model_oracle.py
+ *                    pins the result against a float64 softmax-attention.
+ *   orc_argmax       the greedy pick of Llama::stream_completion (llama.rs:509-515):
+ *                    Iterator::max_by(partial_cmp) returns the LAST maximum
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+float orc_expf(float x);
+float orc_pairwise_sum(const float* v, int64_t n);
+
+void orc_rope_table(double theta, int64_t hd, int64_t max_seq, float* cos_t, float* sin_t)
+{
+    const int64_t half = hd / 2;
+    float* inv = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
+    for (int64_t i = 0; i < half; ++i) inv[i] = (float)(1.0 / pow(theta, (double)(2 * i) / (double)hd));
+    for (int64_t p = 0; p < max_seq; ++p)
+        for (int64_t i = 0; i < half; ++i) {
+            const float f = (float)p * inv[i];
+            cos_t[p * half + i] = cosf(f);
+            sin_t[p * half + i] = sinf(f);
+        }
+    free(inv);
+}
+
+void orc_rope_apply(const float* x, int64_t hd, const float* c, const float* s, float* out)
+{
+    const int64_t half = hd / 2;
+    for (int64_t i = 0; i < half; ++i) {
+        const float x1 = x[i], x2 = x[i + half];
+        const float a = x1 * c[i], b = x2 * s[i];
+        const float e = x1 * s[i], f = x2 * c[i];
+        out[i] = a - b;
+        out[i + half] = e + f;
+    }
+}
+
+static uint8_t sat_u8(float r)
+{
+    if (r != r || r <= 0.0f) return 0;
+    if (r >= 255.0f) return 255;
+    return (uint8_t)r;
+}
+
+void orc_q8_quant(const float* x, int64_t hd, uint8_t* q, float* s_out)
+{
+    float amax = fabsf(x[0]);
+    for (int64_t d = 1; d < hd; ++d) {
+        const float a = fabsf(x[d]);
+        if (a > amax) amax = a;
+    }
+    const float s = amax / 127.0f;
+    for (int64_t d = 0; d < hd; ++d) q[d] = sat_u8(roundf(x[d] / s) + 128.0f);
+    *s_out = s;
+}
+
+void orc_q8_dequant(const uint8_t* q, int64_t hd, float s, float* out)
+{
+    for (int64_t d = 0; d < hd; ++d) out[d] = ((float)q[d] - 128.0f) * s;
+}
+
+#define ORC_CHUNK 64
+
+/* q: [nh * hd] (rotated); cache arrays of ONE layer: kq/vq [nkv][max_seq][hd],
+ * ks/vs [nkv][max_seq]; keys [0, T).  out: [nh * hd]. */
+void orc_attn_decode(const float* q, const uint8_t* kq, const float* ks, const uint8_t* vq, const float* vs,
+                     int64_t nh, int64_t nkv, int64_t hd, int64_t max_seq, int64_t T, float* out)
+{
+    const int64_t rep = nh / nkv;
+    const float scal = (float)(1.0 / sqrt((double)hd));
+    const int64_t C = (T + ORC_CHUNK - 1) / ORC_CHUNK;
+    float* mc = (float*)malloc(sizeof(float) * (size_t)(C + 1));
+    float* lc = (float*)malloc(sizeof(float) * (size_t)(C + 1));
+    float* oc = (float*)malloc(sizeof(float) * (size_t)((C + 1) * hd));
+    float* kd = (float*)malloc(sizeof(float) * (size_t)hd);
+    float sc[ORC_CHUNK], p[ORC_CHUNK];
+    for (int64_t h = 0; h < nh; ++h) {
+        const int64_t g = h / rep;
+        const float* qh = q + h * hd;
+        for (int64_t c = 0; c < C; ++c) {
+            const int64_t j0 = c * ORC_CHUNK;
+            const int64_t nj = T - j0 < ORC_CHUNK ? T - j0 : ORC_CHUNK;
+            float m = -INFINITY;
+            for (int64_t j = 0; j < nj; ++j) {
+                const int64_t row = g * max_seq + j0 + j;
+                orc_q8_dequant(kq + row * hd, hd, ks[row], kd);
+                float acc = 0.0f;
+                for (int64_t d = 0; d < hd; ++d) acc = acc + qh[d] * kd[d];
+                sc[j] = acc * scal + 0.0f; /* candle affine(mul, add): v * mul + add */
+                if (sc[j] > m) m = sc[j];
+            }
+            for (int64_t j = 0; j < ORC_CHUNK; ++j) p[j] = j < nj ? orc_expf(sc[j] - m) : 0.0f;
+            mc[c] = m;
+            lc[c] = orc_pairwise_sum(p, ORC_CHUNK);
+            for (int64_t d = 0; d < hd; ++d) {
+                float acc = 0.0f;
+                for (int64_t j = 0; j < nj; ++j) {
+                    const int64_t row = g * max_seq + j0 + j;
+                    const float vd = ((float)vq[row * hd + d] - 128.0f) * vs[row];
+                    acc = acc + p[j] * vd;
+                }
+                oc[c * hd + d] = acc;
+            }
+        }
+        float M = -INFINITY;
+        for (int64_t c = 0; c < C; ++c)
+            if (mc[c] > M) M = mc[c];
+        float L = 0.0f;
+        for (int64_t c = 0; c < C; ++c) L = L + orc_expf(mc[c] - M) * lc[c];
+        for (int64_t d = 0; d < hd; ++d) {
+            float O = 0.0f;
+            for (int64_t c = 0; c < C; ++c) O = O + orc_expf(mc[c] - M) * oc[c * hd + d];
+            out[h * hd + d] = O / L;
+        }
+    }
+    free(mc);
+    free(lc);
+    free(oc);
+    free(kd);
+}
+
+int64_t orc_argmax(const float* x, int64_t n)
+{
+    int64_t best = 0;
+    for (int64_t i = 1; i < n; ++i)
+        if (!(x[i] < x[best])) best = i;  /* max_by keeps the later of equal elements */
+    return best;
+}

@@ -40,6 +40,12 @@ def _load():
         "orc_expf": (f32, [f32]),
         "orc_swiglu": (None, [vp, vp, i64, vp]),
         "orc_f32_to_bf16_array": (None, [vp, i64, vp]),
+        "orc_rope_table": (None, [ctypes.c_double, i64, i64, vp, vp]),
+        "orc_rope_apply": (None, [vp, i64, vp, vp, vp]),
+        "orc_q8_quant": (None, [vp, i64, vp, vp]),
+        "orc_q8_dequant": (None, [vp, i64, f32, vp]),
+        "orc_attn_decode": (None, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp]),
+        "orc_argmax": (i64, [vp, i64]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -187,3 +193,78 @@ def swiglu(g, u):
     out = np.empty_like(g)
     lib.orc_swiglu(_p(g), _p(u), g.size, _p(out))
     return out
+
+
+# ---------------------------------------------------------------------------
+# decoder ops around the BitLinear path (bitllama_oracle.c)
+# ---------------------------------------------------------------------------
+def rope_table(theta, head_dim, max_seq):
+    """RotaryEmbedding::new (attention.rs:15-42): (cos, sin) float32 [max_seq, head_dim/2]."""
+    half = head_dim // 2
+    c = np.zeros((max_seq, half), dtype=np.float32)
+    s = np.zeros((max_seq, half), dtype=np.float32)
+    lib.orc_rope_table(float(theta), head_dim, max_seq, _p(c), _p(s))
+    return c, s
+
+
+def rope_apply(x, cos_row, sin_row):
+    """RotaryEmbedding::apply (attention.rs:46-87) on the last axis of x at one position."""
+    x = _f32(x)
+    hd = x.shape[-1]
+    out = np.empty_like(x)
+    xf, of = x.reshape(-1, hd), out.reshape(-1, hd)
+    c, s = _f32(cos_row), _f32(sin_row)
+    for i in range(xf.shape[0]):
+        row = np.ascontiguousarray(xf[i])
+        o = np.empty_like(row)
+        lib.orc_rope_apply(_p(row), hd, _p(c), _p(s), _p(o))
+        of[i] = o
+    return out
+
+
+def q8_quant(x):
+    """QuantizedKVCache::quantize_q8 (kv_cache.rs:95-119) per row of the last axis -> (u8 codes, f32 scales)."""
+    x = _f32(x)
+    hd = x.shape[-1]
+    xf = x.reshape(-1, hd)
+    q = np.zeros(xf.shape, dtype=np.uint8)
+    s = np.zeros((xf.shape[0],), dtype=np.float32)
+    for i in range(xf.shape[0]):
+        row = np.ascontiguousarray(xf[i])
+        qi = np.zeros((hd,), dtype=np.uint8)
+        si = np.zeros((1,), dtype=np.float32)
+        lib.orc_q8_quant(_p(row), hd, _p(qi), _p(si))
+        q[i], s[i] = qi, si[0]
+    return q.reshape(x.shape), s.reshape(x.shape[:-1])
+
+
+def q8_dequant(q, s):
+    """dequantize_q8 (kv_cache.rs:122-128): ((f32)q - 128) * s per row."""
+    q = np.ascontiguousarray(q, np.uint8)
+    hd = q.shape[-1]
+    qf = q.reshape(-1, hd)
+    sf = _f32(s).reshape(-1)
+    out = np.zeros(qf.shape, dtype=np.float32)
+    for i in range(qf.shape[0]):
+        o = np.zeros((hd,), dtype=np.float32)
+        lib.orc_q8_dequant(_p(np.ascontiguousarray(qf[i])), hd, float(sf[i]), _p(o))
+        out[i] = o
+    return out.reshape(q.shape)
+
+
+def attn_decode(q, kq, ks, vq, vs, n_heads, T):
+    """One query position of BitAttention::forward over a Q8 cache (fixed GPU order).
+    q [nh*hd] f32; kq/vq [nkv, max_seq, hd] u8; ks/vs [nkv, max_seq] f32."""
+    kq, vq = np.ascontiguousarray(kq, np.uint8), np.ascontiguousarray(vq, np.uint8)
+    ks, vs = _f32(ks), _f32(vs)
+    nkv, max_seq, hd = kq.shape
+    q = _f32(q).reshape(-1)
+    out = np.zeros((n_heads * hd,), dtype=np.float32)
+    lib.orc_attn_decode(_p(q), _p(kq), _p(ks), _p(vq), _p(vs), n_heads, nkv, hd, max_seq, T, _p(out))
+    return out
+
+
+def argmax(x):
+    """Greedy pick of stream_completion (llama.rs:509-515): the last maximum."""
+    x = _f32(x).reshape(-1)
+    return int(lib.orc_argmax(_p(x), x.size))

@@ -1,0 +1,307 @@
+"""GPU parity of the decoder ops (include/bitllama.h) and of the end-to-end ternary
+decoder (bitlinear.model.BitLlamaHip) against the CPU oracle.
+
+Bar: everything bit-exact.  The RoPE rows, the Q8 cache codes and scales, the
+attention outputs (the oracle restates the kernels' fixed summation order), the
+residual stream, the logits and the greedy tokens.  The attention order itself is
+pinned against float64 in test_model_oracle.py (relative 2e-6)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import bitlinear as bl
+from bitlinear.model import BitLlamaHip
+from oracle import oracle as orc
+from oracle.llama_oracle import OracleLlama
+from test_model_oracle import TinyCfg, tiny_weights
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")]
+
+DEV = "cuda"
+
+
+def _bits(a):
+    a = np.ascontiguousarray(a, np.float32).copy()
+    a[np.isnan(a)] = np.float32("nan")
+    return a.view(np.uint32)
+
+
+def assert_same(got, ref, what=""):
+    got = got.detach().cpu().numpy() if torch.is_tensor(got) else np.asarray(got)
+    g, r = _bits(got), _bits(ref)
+    bad = np.flatnonzero(g.reshape(-1) != r.reshape(-1))
+    assert bad.size == 0, "%s: %d mismatches, first at %d: %r vs %r" % (
+        what, bad.size, bad[0], got.reshape(-1)[bad[0]], np.asarray(ref).reshape(-1)[bad[0]])
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Cache:
+    def __init__(self, nkv, S, hd):
+        self.k = torch.full((nkv, S, hd), 7, dtype=torch.uint8, device=DEV)
+        self.v = torch.full((nkv, S, hd), 9, dtype=torch.uint8, device=DEV)
+        self.ks = torch.full((nkv, S), 0.5, dtype=torch.float32, device=DEV)
+        self.vs = torch.full((nkv, S), 0.25, dtype=torch.float32, device=DEV)
+        self.c = bl.BtlKvQ8(self.k.data_ptr(), self.v.data_ptr(), self.ks.data_ptr(), self.vs.data_ptr(), nkv, S, hd)
+
+    def host(self):
+        return (self.k.cpu().numpy(), self.ks.cpu().numpy(), self.v.cpu().numpy(), self.vs.cpu().numpy())
+
+
+def rope_dev(theta, hd, S):
+    c = np.zeros((S, hd // 2), np.float32)
+    s = np.zeros_like(c)
+    bl.check(bl.lib.btl_rope_table(theta, hd, S, c.ctypes.data, s.ctypes.data))
+    return c, s, torch.from_numpy(c).to(DEV), torch.from_numpy(s).to(DEV)
+
+
+def test_rope_table_matches_oracle():
+    c, s, _, _ = rope_dev(500000.0, 128, 700)
+    oc, osn = orc.rope_table(500000.0, 128, 700)
+    assert np.array_equal(c, oc) and np.array_equal(s, osn)
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(4, 2, 64), (32, 8, 128), (3, 1, 2)])
+@pytest.mark.parametrize("m,pos,dpos", [(1, 0, False), (1, 37, True), (5, 60, False), (70, 0, False)])
+def test_rope_kv_append_bitexact(nh, nkv, hd, m, pos, dpos):
+    print("rope_kv_append", nh, nkv, hd, m, pos, dpos, flush=True)
+    S = 160
+    rng = np.random.default_rng(m * 100 + pos + hd)
+    q = rng.standard_normal((m, nh * hd)).astype(np.float32)
+    k = (rng.standard_normal((m, nkv * hd)) * 3).astype(np.float32)
+    v = rng.standard_normal((m, nkv * hd)).astype(np.float32)
+    if m > 1:
+        v[1, :hd] = 0.0  # a zero head row: codes 0, scale 0
+    cos, sin, dc, ds = rope_dev(10000.0, hd, S)
+    cache = Cache(nkv, S, hd)
+    qt, kt, vt = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
+    qo = torch.empty_like(qt)
+    d_pos = torch.tensor([pos], dtype=torch.int32, device=DEV) if dpos else None
+    bl.check(bl.lib.btl_rope_kv_append(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), m, nh, ctypes.byref(cache.c),
+                                       0 if dpos else pos, d_pos.data_ptr() if dpos else None, dc.data_ptr(),
+                                       ds.data_ptr(), qo.data_ptr(), stream()))
+    kq, ks, vq, vs = cache.host()
+    for t in range(m):
+        p = pos + t
+        assert_same(qo[t], orc.rope_apply(q[t].reshape(nh, hd), cos[p], sin[p]).reshape(-1), "q rope")
+        kr = orc.rope_apply(k[t].reshape(nkv, hd), cos[p], sin[p])
+        ekq, eks = orc.q8_quant(kr)
+        evq, evs = orc.q8_quant(v[t].reshape(nkv, hd))
+        assert np.array_equal(kq[:, p], ekq) and np.array_equal(vq[:, p], evq)
+        assert_same(ks[:, p], eks, "k scale")
+        assert_same(vs[:, p], evs, "v scale")
+    # rows outside [pos, pos + m) untouched
+    untouched = [r for r in range(S) if not pos <= r < pos + m]
+    assert np.all(kq[:, untouched] == 7) and np.all(ks[:, untouched] == 0.5)
+
+
+def test_rope_kv_append_rejects_out_of_range_positions():
+    cache = Cache(2, 16, 64)
+    x = torch.zeros((4, 4 * 64), device=DEV)
+    y = torch.zeros((4, 2 * 64), device=DEV)
+    _, _, dc, ds = rope_dev(10000.0, 64, 16)
+    st = bl.lib.btl_rope_kv_append(x.data_ptr(), y.data_ptr(), y.data_ptr(), 4, 4, ctypes.byref(cache.c), 14, None,
+                                   dc.data_ptr(), ds.data_ptr(), x.data_ptr(), stream())
+    assert st == bl.BTL_ERR_SHAPE
+    assert b"outside the cache" in bl.lib.btl_last_error()
+
+
+def _fill_cache(cache, T, seed):
+    nkv, S, hd = cache.k.shape
+    rng = np.random.default_rng(seed)
+    k = (rng.standard_normal((nkv, S, hd)) * 2).astype(np.float32)
+    v = rng.standard_normal((nkv, S, hd)).astype(np.float32)
+    kq, ks = orc.q8_quant(k)
+    vq, vs = orc.q8_quant(v)
+    cache.k.copy_(torch.from_numpy(kq))
+    cache.v.copy_(torch.from_numpy(vq))
+    cache.ks.copy_(torch.from_numpy(ks))
+    cache.vs.copy_(torch.from_numpy(vs))
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(4, 2, 64), (32, 8, 128), (16, 1, 128)])
+@pytest.mark.parametrize("m,pos", [(1, 0), (1, 63), (1, 64), (1, 199), (3, 61), (70, 0), (40, 100)])
+def test_attention_bitexact(nh, nkv, hd, m, pos):
+    print("attention", nh, nkv, hd, m, pos, flush=True)
+    S = 256
+    cache = Cache(nkv, S, hd)
+    _fill_cache(cache, S, seed=nh + m + pos)
+    q = np.random.default_rng(pos + 5).standard_normal((m, nh * hd)).astype(np.float32)
+    qt = torch.from_numpy(q).to(DEV)
+    out = torch.full((m, nh * hd), 3.0, device=DEV)
+    ws_bytes = bl.lib.btl_attention_workspace_bytes(m, nh, ctypes.byref(cache.c))
+    ws = torch.full((ws_bytes // 4 + 64,), 1234.5, dtype=torch.float32, device=DEV)  # garbage is fine
+    bl.check(bl.lib.btl_attention(qt.data_ptr(), m, nh, ctypes.byref(cache.c), pos, None, out.data_ptr(),
+                                  ws.data_ptr(), ws_bytes, stream()))
+    kq, ks, vq, vs = cache.host()
+    o = out.cpu().numpy()
+    for i in range(m):
+        e = orc.attn_decode(q[i], kq, ks, vq, vs, nh, pos + i + 1)
+        assert_same(o[i], e, "query %d" % i)
+
+
+def test_attention_device_position():
+    nh, nkv, hd, S = 8, 2, 128, 300
+    cache = Cache(nkv, S, hd)
+    _fill_cache(cache, S, seed=11)
+    q = np.random.default_rng(12).standard_normal((1, nh * hd)).astype(np.float32)
+    qt = torch.from_numpy(q).to(DEV)
+    kq, ks, vq, vs = cache.host()
+    for p in (0, 130, 299):
+        d_pos = torch.tensor([p], dtype=torch.int32, device=DEV)
+        out = torch.empty((1, nh * hd), device=DEV)
+        bl.check(bl.lib.btl_attention(qt.data_ptr(), 1, nh, ctypes.byref(cache.c), 0, d_pos.data_ptr(),
+                                      out.data_ptr(), None, 0, stream()))
+        assert_same(out[0], orc.attn_decode(q[0], kq, ks, vq, vs, nh, p + 1), "pos %d" % p)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_embedding(dtype):
+    vocab, dim = 1000, 320
+    table = torch.randn((vocab, dim), device=DEV).to(dtype)
+    ids = torch.tensor([5, 999, 0, -1, 1000, 5], dtype=torch.int32, device=DEV)
+    out = torch.full((6, dim), 7.0, device=DEV)
+    bl.check(bl.lib.btl_embedding(table.data_ptr(), bl.BTL_BF16 if dtype == torch.bfloat16 else bl.BTL_F32, vocab,
+                                  dim, ids.data_ptr(), 6, out.data_ptr(), stream()))
+    t = table.float()
+    exp = torch.stack([t[5], t[999], t[0], torch.zeros(dim, device=DEV), torch.zeros(dim, device=DEV), t[5]])
+    assert torch.equal(out, exp)
+
+
+def test_greedy_next():
+    cases = [np.array([1, 5, 2, 5, 0], np.float32), np.array([-3, -1, -1, -7], np.float32),
+             np.array([0.0, -0.0, -1.0, 0.0, -0.0], np.float32)]
+    rng = np.random.default_rng(1)
+    big = rng.standard_normal(128256).astype(np.float32)
+    big[77777] = big[1234] = 9.0  # tie: the later index wins
+    cases.append(big)
+    cases.append(rng.standard_normal(1001).astype(np.float32))  # tail of n % 4
+    for x in cases:
+        xt = torch.from_numpy(x).to(DEV)
+        nid = torch.full((1,), -5, dtype=torch.int32, device=DEV)
+        bl.check(bl.lib.btl_greedy_next(xt.data_ptr(), x.size, nid.data_ptr(), None, None, 0, stream()))
+        assert int(nid.item()) == orc.argmax(x)
+    # device bookkeeping: log[pos + 1] = id, ++pos
+    x = torch.from_numpy(cases[0]).to(DEV)
+    nid = torch.zeros((1,), dtype=torch.int32, device=DEV)
+    pos = torch.tensor([4], dtype=torch.int32, device=DEV)
+    log = torch.full((8,), -1, dtype=torch.int32, device=DEV)
+    for _ in range(4):
+        bl.check(bl.lib.btl_greedy_next(x.data_ptr(), 5, nid.data_ptr(), pos.data_ptr(), log.data_ptr(), 8, stream()))
+    assert int(pos.item()) == 8
+    assert log.cpu().tolist() == [-1, -1, -1, -1, -1, 3, 3, 3]  # log[8] is outside: not written
+
+
+@pytest.mark.parametrize("m,k", [(1, 256), (3, 4096), (70, 512)])
+def test_add_rmsnorm_linear_group(m, k):
+    rng = np.random.default_rng(m + k)
+    h = rng.standard_normal((m, k)).astype(np.float32)
+    d = rng.standard_normal((m, k)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    layers = []
+    for i, n in enumerate((96, 40)):
+        wb, sw = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        layers.append((bl.PackedTensor(torch.from_numpy(wb).to(DEV), sw, (n, k), DEV), wb, sw, n))
+    ht, dt, gt = (torch.from_numpy(a).to(DEV) for a in (h, d, g))
+    outs = [torch.empty((m, n), device=DEV) for (_, _, _, n) in layers]
+    cs = [L[0].as_c() for L in layers]
+    arr = (ctypes.POINTER(bl.BtlPacked) * 2)(*[ctypes.pointer(c) for c in cs])
+    ys = (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs])
+    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 2, ht.data_ptr(), dt.data_ptr(), gt.data_ptr(), 1e-5, m,
+                                                 k, bl.BTL_F32, None, 0, stream()))
+    hs = (h + d).astype(np.float32)
+    assert_same(ht, hs, "residual")
+    xn = orc.rmsnorm(hs, g, 1e-5)
+    for o, (_, wb, sw, n) in zip(outs, layers):
+        assert_same(o, orc.forward_i8(xn, wb, n, sw)[0], "layer")
+    # delta = NULL: RMSNorm of h only, h untouched
+    h2 = torch.from_numpy(h).to(DEV)
+    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 2, h2.data_ptr(), None, gt.data_ptr(), 1e-5, m, k,
+                                                 bl.BTL_F32, None, 0, stream()))
+    assert_same(h2, h, "h untouched")
+    assert_same(outs[0], orc.forward_i8(orc.rmsnorm(h, g, 1e-5), layers[0][1], 96, layers[0][2])[0], "plain")
+
+
+# --- the decoder end to end ----------------------------------------------------
+
+class Tiny2(TinyCfg):
+    # hidden 128 = 1 head of 128 (GQA rep 1), odd vocab, a chunk boundary inside the prompt
+    hidden, n_layers, n_heads, n_kv_heads, head_dim = 256, 2, 2, 1, 128
+    intermediate, vocab, rope_theta, max_seq, eps = 512, 1001, 500000.0, 160, 1e-5
+
+
+def gpu_model(cfg, w, max_rows=512):
+    def lin(pk, n, k):
+        return bl.PackedTensor(torch.from_numpy(pk[0]).to(DEV), pk[1], (n, k), DEV)
+
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    qd = cfg.n_heads * cfg.head_dim
+    layers = [{"norm1": torch.from_numpy(L["norm1"]).to(DEV), "norm2": torch.from_numpy(L["norm2"]).to(DEV),
+               "q": lin(L["q"], qd, cfg.hidden), "k": lin(L["k"], kvd, cfg.hidden), "v": lin(L["v"], kvd, cfg.hidden),
+               "o": lin(L["o"], cfg.hidden, qd), "gate": lin(L["gate"], cfg.intermediate, cfg.hidden),
+               "up": lin(L["up"], cfg.intermediate, cfg.hidden), "down": lin(L["down"], cfg.hidden, cfg.intermediate)}
+              for L in w["layers"]]
+    gw = {"embed": torch.from_numpy(w["embed"]).to(DEV), "norm_f": torch.from_numpy(w["norm_f"]).to(DEV),
+          "lm_head": lin(w["lm_head"], cfg.vocab, cfg.hidden), "layers": layers}
+    return BitLlamaHip(cfg, gw, DEV, max_rows=max_rows)
+
+
+class TinyA(TinyCfg):
+    hidden, n_layers, n_heads, n_kv_heads, head_dim = 256, 2, 4, 2, 64
+    intermediate, vocab, rope_theta, max_seq, eps = 512, 1000, 10000.0, 160, 1e-5
+
+
+@pytest.mark.parametrize("cfg_cls", [TinyA, Tiny2])
+def test_decoder_forward_one_matches_oracle(cfg_cls):
+    cfg = cfg_cls()
+    w = tiny_weights(cfg, seed=5)
+    gm = gpu_model(cfg, w)
+    om = OracleLlama(cfg, w)
+    rng = np.random.default_rng(9)
+    toks = rng.integers(0, cfg.vocab, 70)
+    for i, t in enumerate(toks):
+        print("forward_one step", i, flush=True)
+        lg = gm.forward_one(int(t))
+        lo = om.forward_one(int(t))
+        assert_same(lg, lo, "step %d logits" % i)
+    for li in range(cfg.n_layers):
+        c = gm.caches[li]
+        assert np.array_equal(c.k.cpu().numpy()[:, :70], om.caches[li]["kq"][:, :70])
+        assert_same(c.v_scale.cpu().numpy()[:, :70], om.caches[li]["vs"][:, :70], "v scales")
+
+
+@pytest.mark.parametrize("cfg_cls", [TinyA, Tiny2])
+def test_decoder_prefill_equals_token_by_token(cfg_cls):
+    cfg = cfg_cls()
+    w = tiny_weights(cfg, seed=6)
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab, 75)
+    a = gpu_model(cfg, w, max_rows=32)  # 75 tokens: batches of 32, 32, 11
+    la = a.prefill(prompt).clone()
+    b = gpu_model(cfg, w)
+    for t in prompt:
+        lb = b.forward_one(int(t))
+    assert_same(la, lb.cpu().numpy(), "prefill vs token-by-token logits")
+    for li in range(cfg.n_layers):
+        assert torch.equal(a.caches[li].k, b.caches[li].k) and torch.equal(a.caches[li].v, b.caches[li].v)
+        assert torch.equal(a.caches[li].k_scale, b.caches[li].k_scale)
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_decoder_generate_matches_oracle(use_graph):
+    cfg = TinyA()
+    w = tiny_weights(cfg, seed=7)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab, 66)
+    gm = gpu_model(cfg, w)
+    got = gm.generate(prompt, 24, use_graph=use_graph)
+    exp = OracleLlama(cfg, w).generate(prompt, 24)
+    assert np.array_equal(got, exp), (got, exp)
+    if use_graph:
+        # replays again after eager work in between: the same continuation as the oracle's
+        torch.cuda.synchronize()
+        again = gm.generate(prompt, 24, use_graph=True)
+        assert np.array_equal(again, exp)

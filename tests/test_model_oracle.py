@@ -1,0 +1,202 @@
+"""Pins the decoder-op oracle (oracle/bitllama_oracle.c, oracle/llama_oracle.py)
+before the GPU decoder is checked against it.
+
+What pins each function (reference = imonoonoko/Bit-TTT-Engine, crates/rust_engine):
+  orc_rope_table    float64 closed form of RotaryEmbedding::new (attention.rs:15-42):
+                    inv_freq rounded to f32 once, freq = (f32)p * inv_freq exactly, cos/sin
+                    within 1 ulp of the float64 values (glibc cosf/sinf, which Rust's
+                    f32::cos/sin call on Linux); the Llama-3 theta 500000.
+  orc_rope_apply    float64 rotation (relative 1e-6), norm preservation, position 0 is
+                    the identity, the half-split pairing (i, i + hd/2) of attention.rs:67-72
+                    (an interleaved (2i, 2i+1) pairing fails).
+  orc_q8_quant /    kv_cache.rs:95-128 closed form: the max element -> code 255 or 1, codes
+  orc_q8_dequant    in [1, 255], |dequant - x| <= s/2, s = max|x|/127; the round-half-away
+                    tie; a zero row (0/0 -> NaN -> code 0 by Rust's saturating cast,
+                    dequantised to 0).
+  orc_attn_decode   float64 softmax attention over the dequantised cache with the GQA map
+                    of repeat_kv (attention.rs:227-239), relative 2e-6 of the output scale,
+                    at chunk boundaries T = 1, 63, 64, 65, 129; per-head planted values
+                    that a wrong head map (h % nkv instead of h // rep) gets wrong.
+                    The reference's own summation order (candle gemm) is not vendored:
+                    its last ulps are parity unpinned (tolerance above).
+  orc_argmax        Iterator::max_by semantics: the last of equal maxima.
+  OracleLlama       composition only; pinned by the functions above and by
+                    test_oracle.py (BitLinear, RMSNorm, SwiGLU); checked here for the
+                    causal invariant that token t's logits do not depend on later tokens.
+"""
+import numpy as np
+import pytest
+
+from datagen import weights
+from oracle import oracle as orc
+from oracle.llama_oracle import OracleLlama
+
+
+def _ulp_diff(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+@pytest.mark.parametrize("theta,hd", [(500000.0, 128), (10000.0, 64), (10000.0, 2)])
+def test_rope_table_closed_form(theta, hd):
+    S = 300
+    c, s = orc.rope_table(theta, hd, S)
+    half = hd // 2
+    inv = np.array([np.float32(1.0 / theta ** (2 * i / hd)) for i in range(half)], np.float32)
+    freq = (np.arange(S, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    assert np.all(_ulp_diff(c, np.cos(freq.astype(np.float64)).astype(np.float32)) <= 1)
+    assert np.all(_ulp_diff(s, np.sin(freq.astype(np.float64)).astype(np.float32)) <= 1)
+    assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
+    # i = 0 is the fastest rotation: angle p radians
+    np.testing.assert_allclose(c[:, 0], np.cos(np.arange(S)), rtol=0, atol=1e-6)
+
+
+def test_rope_apply_rotation():
+    hd = 128
+    c, s = orc.rope_table(500000.0, hd, 64)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, hd)).astype(np.float32)
+    for p in (0, 1, 37, 63):
+        y = orc.rope_apply(x, c[p], s[p])
+        x64, c64, s64 = x.astype(np.float64), c[p].astype(np.float64), s[p].astype(np.float64)
+        h = hd // 2
+        e1 = x64[:, :h] * c64 - x64[:, h:] * s64
+        e2 = x64[:, :h] * s64 + x64[:, h:] * c64
+        np.testing.assert_allclose(y, np.concatenate([e1, e2], 1), rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(np.linalg.norm(y, axis=1), np.linalg.norm(x64, axis=1), rtol=1e-6)
+        if p == 0:
+            assert np.array_equal(y, x)
+    # the pairing is (i, i + hd/2): a vector living in the first half rotates into the second
+    e = np.zeros((1, hd), np.float32)
+    e[0, 0] = 1.0
+    y = orc.rope_apply(e, c[1], s[1])
+    assert y[0, hd // 2] == s[1][0] and y[0, 1] == 0.0
+
+
+def test_q8_quant_closed_form():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((50, 128)).astype(np.float32)
+    q, s = orc.q8_quant(x)
+    amax = np.abs(x).max(1)
+    assert np.array_equal(s, (amax / np.float32(127)).astype(np.float32))
+    assert q.min() >= 1 and q.max() <= 255
+    idx = np.abs(x).argmax(1)
+    top = q[np.arange(50), idx]
+    assert np.all(np.where(x[np.arange(50), idx] > 0, top == 255, top == 1))
+    d = orc.q8_dequant(q, s)
+    assert np.all(np.abs(d - x) <= s[:, None] * 0.5000001)
+    # codes: round half away of x/s, + 128
+    r = x / s[:, None]
+    exp_codes = (np.sign(r) * np.floor(np.abs(r) + 0.5) + 128).astype(np.uint8)
+    assert np.array_equal(q, exp_codes)
+
+
+def test_q8_quant_tie_and_zero_row():
+    # s = 127/127 = 1: x = 2.5 -> 3 (half away), -2.5 -> -3
+    x = np.zeros((1, 8), np.float32)
+    x[0, :4] = [127.0, 2.5, -2.5, 0.5]
+    q, s = orc.q8_quant(x)
+    assert s[0] == 1.0
+    assert list(q[0, :4]) == [255, 131, 125, 129]
+    z, zs = orc.q8_quant(np.zeros((1, 16), np.float32))
+    assert zs[0] == 0.0 and np.all(z == 0)
+    assert np.all(orc.q8_dequant(z, zs) == 0.0)
+
+
+def _attn64(q, kq, ks, vq, vs, nh, T):
+    nkv, _, hd = kq.shape
+    rep = nh // nkv
+    k = (kq[:, :T].astype(np.float64) - 128.0) * ks[:, :T, None]
+    v = (vq[:, :T].astype(np.float64) - 128.0) * vs[:, :T, None]
+    out = np.zeros((nh, hd))
+    for h in range(nh):
+        g = h // rep
+        sc = (k[g] @ q.reshape(nh, hd)[h].astype(np.float64)) / np.sqrt(hd)
+        p = np.exp(sc - sc.max())
+        out[h] = (p / p.sum()) @ v[g]
+    return out.reshape(-1)
+
+
+def _cache(nkv, S, hd, seed):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((nkv, S, hd)).astype(np.float32) * 2
+    v = rng.standard_normal((nkv, S, hd)).astype(np.float32)
+    kq, ks = orc.q8_quant(k)
+    vq, vs = orc.q8_quant(v)
+    return kq, ks, vq, vs
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 129])
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 2, 64), (4, 4, 128), (32, 8, 128)])
+def test_attn_decode_matches_float64(T, nh, nkv, hd):
+    S = 160
+    kq, ks, vq, vs = _cache(nkv, S, hd, seed=T + nh)
+    q = np.random.default_rng(7).standard_normal(nh * hd).astype(np.float32)
+    y = orc.attn_decode(q, kq, ks, vq, vs, nh, T)
+    e = _attn64(q, kq, ks, vq, vs, nh, T)
+    scale = np.abs(e).reshape(nh, hd).max(1, keepdims=True)
+    assert np.all(np.abs(y.reshape(nh, hd) - e.reshape(nh, hd)) <= 2e-6 * scale + 1e-30)
+
+
+def test_attn_decode_gqa_head_map():
+    # each KV head holds one constant value vector: output of head h must be that of kv head h // rep
+    nh, nkv, hd, S, T = 8, 2, 64, 70, 70
+    kq = np.full((nkv, S, hd), 128, np.uint8)
+    ks = np.ones((nkv, S), np.float32)
+    vq = np.zeros((nkv, S, hd), np.uint8)
+    vq[0] = 128 + 10
+    vq[1] = 128 - 20
+    vs = np.ones((nkv, S), np.float32)
+    y = orc.attn_decode(np.ones(nh * hd, np.float32), kq, ks, vq, vs, nh, T).reshape(nh, hd)
+    rep = nh // nkv
+    for h in range(nh):
+        assert np.all(y[h] == (10.0 if h // rep == 0 else -20.0)), h
+
+
+def test_argmax_last_of_equal_maxima():
+    assert orc.argmax(np.array([1, 5, 2, 5, 0], np.float32)) == 3
+    assert orc.argmax(np.array([-3, -1, -1], np.float32)) == 2
+    assert orc.argmax(np.array([7.0], np.float32)) == 0
+    assert orc.argmax(np.array([0.0, -0.0], np.float32)) == 1
+
+
+class TinyCfg:
+    hidden, n_layers, n_heads, n_kv_heads, head_dim = 64, 2, 4, 2, 16
+    intermediate, vocab, rope_theta, max_seq, eps = 128, 50, 10000.0, 80, 1e-5
+
+
+def tiny_weights(cfg, seed=0):
+    rng = np.random.default_rng(seed)
+
+    def lin(n, k):
+        return orc.pack(weights(n, k, int(rng.integers(1 << 30))))
+
+    def norm(n):
+        return (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+
+    kvd = cfg.n_kv_heads * cfg.head_dim
+    layers = [{"norm1": norm(cfg.hidden), "norm2": norm(cfg.hidden),
+               "q": lin(cfg.n_heads * cfg.head_dim, cfg.hidden), "k": lin(kvd, cfg.hidden),
+               "v": lin(kvd, cfg.hidden), "o": lin(cfg.hidden, cfg.n_heads * cfg.head_dim),
+               "gate": lin(cfg.intermediate, cfg.hidden), "up": lin(cfg.intermediate, cfg.hidden),
+               "down": lin(cfg.hidden, cfg.intermediate)} for _ in range(cfg.n_layers)]
+    return {"embed": rng.standard_normal((cfg.vocab, cfg.hidden)).astype(np.float32),
+            "norm_f": norm(cfg.hidden), "lm_head": lin(cfg.vocab, cfg.hidden), "layers": layers}
+
+
+def test_oracle_llama_is_causal_and_deterministic():
+    cfg = TinyCfg()
+    w = tiny_weights(cfg)
+    prompt = [3, 14, 15, 9, 26, 5]
+    a = OracleLlama(cfg, w)
+    la = [a.forward_one(t) for t in prompt]
+    b = OracleLlama(cfg, w)
+    lb = [b.forward_one(t) for t in prompt[:3] + [0, 0]]
+    for i in range(3):
+        assert np.array_equal(la[i], lb[i])   # later tokens do not change earlier logits
+    assert not np.array_equal(la[3], lb[3])
+    g1 = OracleLlama(cfg, w).generate(prompt, 5)
+    g2 = OracleLlama(cfg, w).generate(prompt, 5)
+    assert np.array_equal(g1, g2) and g1.shape == (5,)
+    assert np.all((g1 >= 0) & (g1 < cfg.vocab))
