@@ -34,6 +34,7 @@ EXPORTS = (
     "btl_workspace_bytes", "btl_workspace_clear",
     # include/bitllama.h
     "btl_rope_table", "btl_rope_kv_append", "btl_attention_workspace_bytes", "btl_attention",
+    "btl_rope_append_attention",
     "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm_linear_group",
 )
 
@@ -91,10 +92,11 @@ def _load():
         "btl_rope_kv_append": (i32, [vp, vp, vp, i64, i64, P(BtlKvQ8), i64, vp, vp, vp, vp, vp]),
         "btl_attention_workspace_bytes": (sz, [i64, i64, P(BtlKvQ8)]),
         "btl_attention": (i32, [vp, i64, i64, P(BtlKvQ8), i64, vp, vp, vp, sz, vp]),
+        "btl_rope_append_attention": (i32, [vp, vp, vp, i64, i64, P(BtlKvQ8), i64, vp, vp, vp, vp, vp, sz, vp]),
         "btl_embedding": (i32, [vp, i32, i64, i64, vp, i64, vp, vp]),
         "btl_greedy_next": (i32, [vp, i64, vp, vp, vp, i64, vp]),
-        "btl_add_rmsnorm_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, vp, f32, i64, i64, i32, vp, sz,
-                                               vp]),
+        "btl_add_rmsnorm_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, vp, vp, f32, i64, i64, i32, vp,
+                                               sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -10,15 +10,18 @@ Reference (imonoonoko/Bit-TTT-Engine, crates/rust_engine/src):
   Llama::stream_completion         model/llama.rs:471-530   (prefill, then greedy decode)
 
 Mapping of the block onto the C ABI (one row of activations per token, f32 between ops):
-  h += mlp_out(l-1); q,k,v = BitLinear(RMSNorm1(h))   btl_add_rmsnorm_linear_group
-  RoPE(q, k); cache.append(k, v)                       btl_rope_kv_append
-  attn = softmax(q k^T / sqrt(d)) v                    btl_attention
-  o = BitLinear_o(attn)                                btl_linear_group
-  h += o; gate, up = BitLinear(RMSNorm2(h))            btl_add_rmsnorm_linear_group
-  mlp_out = BitLinear_down(silu(gate) * up)            btl_swiglu_linear_group
-and after the last block h += mlp_out, logits = lm_head(RMSNorm_f(h)) in one
-more btl_add_rmsnorm_linear_group.  Every linear is a BitLinear (W1.58-A8),
-the lm_head included.
+  x = h + mlp_out(l-1); q,k,v = BitLinear(RMSNorm1(x))   btl_add_rmsnorm_linear_group
+  RoPE(q, k); cache.append(k, v);
+  attn = softmax(q k^T / sqrt(d)) v                      btl_rope_append_attention
+  o = BitLinear_o(attn)                                  btl_linear_group
+  x' = x + o; gate, up = BitLinear(RMSNorm2(x'))         btl_add_rmsnorm_linear_group
+  mlp_out = BitLinear_down(silu(gate) * up)              btl_swiglu_linear_group
+and after the last block logits = lm_head(RMSNorm_f(x' + mlp_out)) in one more
+btl_add_rmsnorm_linear_group.  The residual stream alternates between two
+buffers (each add writes the other one), so for a one-token step the add +
+norm and the SwiGLU can run inside the contraction kernel's prologue (the
+library does so for launches of up to 512 workgroups).  Every linear is a
+BitLinear (W1.58-A8), the lm_head included.
 
 Deliberate differences from the reference, all on the host side:
   * the prompt is prefilled as one batch of rows (the reference feeds it token by
@@ -108,7 +111,8 @@ class BitLlamaHip:
         c = cfg
         f32 = dict(dtype=torch.float32, device=self.dev)
         M = max_rows
-        self.h = torch.zeros((M, c.hidden), **f32)
+        self.h = torch.zeros((M, c.hidden), **f32)   # residual stream, alternating with h2
+        self.h2 = torch.zeros((M, c.hidden), **f32)
         self.q = torch.zeros((M, c.n_heads * c.head_dim), **f32)
         self.k = torch.zeros((M, c.n_kv_heads * c.head_dim), **f32)
         self.v = torch.zeros((M, c.n_kv_heads * c.head_dim), **f32)
@@ -161,26 +165,30 @@ class BitLlamaHip:
         hid = c.hidden
         check(lib.btl_embedding(self.w["embed"].data_ptr(), self.emb_dtype, c.vocab, hid, ids.data_ptr(), m,
                                 self.h.data_ptr(), st))
+        cur, nxt = self.h, self.h2  # each add writes the other buffer (lets a one-token step fuse it)
         for li, L in enumerate(self._layers):
             cache = self.caches[li].c
-            delta = self.down.data_ptr() if li > 0 else None
-            check(lib.btl_add_rmsnorm_linear_group(L["qkv"], self._y_qkv, 3, self.h.data_ptr(), delta, L["n1"],
-                                                   c.eps, m, hid, BTL_F32, None, 0, st))
-            check(lib.btl_rope_kv_append(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), m, c.n_heads,
-                                         ctypes.byref(cache), pos, dp, self.rope_cos.data_ptr(),
-                                         self.rope_sin.data_ptr(), self.q.data_ptr(), st))
-            check(lib.btl_attention(self.q.data_ptr(), m, c.n_heads, ctypes.byref(cache), pos, dp,
-                                    self.attn.data_ptr(), None, 0, st))
+            if li > 0:
+                check(lib.btl_add_rmsnorm_linear_group(L["qkv"], self._y_qkv, 3, cur.data_ptr(), self.down.data_ptr(),
+                                                       nxt.data_ptr(), L["n1"], c.eps, m, hid, BTL_F32, None, 0, st))
+                cur, nxt = nxt, cur
+            else:
+                check(lib.btl_add_rmsnorm_linear_group(L["qkv"], self._y_qkv, 3, cur.data_ptr(), None, None, L["n1"],
+                                                       c.eps, m, hid, BTL_F32, None, 0, st))
+            check(lib.btl_rope_append_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), m,
+                                                c.n_heads, ctypes.byref(cache), pos, dp, self.rope_cos.data_ptr(),
+                                                self.rope_sin.data_ptr(), self.attn.data_ptr(), None, 0, st))
             check(lib.btl_linear_group(L["o"], self._y_o, 1, self.attn.data_ptr(), BTL_F32, m,
                                        c.n_heads * c.head_dim, BTL_F32, None, 0, st))
-            check(lib.btl_add_rmsnorm_linear_group(L["gu"], self._y_gu, 2, self.h.data_ptr(), self.o.data_ptr(),
-                                                   L["n2"], c.eps, m, hid, BTL_F32, None, 0, st))
+            check(lib.btl_add_rmsnorm_linear_group(L["gu"], self._y_gu, 2, cur.data_ptr(), self.o.data_ptr(),
+                                                   nxt.data_ptr(), L["n2"], c.eps, m, hid, BTL_F32, None, 0, st))
+            cur, nxt = nxt, cur
             check(lib.btl_swiglu_linear_group(L["down"], self._y_down, 1, self.gate.data_ptr(), self.up.data_ptr(),
                                               BTL_F32, m, c.intermediate, BTL_F32, None, 0, st))
         last = m - 1
-        check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, self.h[last].data_ptr(),
-                                               self.down[last].data_ptr(), self.w["norm_f"].data_ptr(), c.eps, 1,
-                                               hid, BTL_F32, None, 0, st))
+        check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, cur[last].data_ptr(),
+                                               self.down[last].data_ptr(), None, self.w["norm_f"].data_ptr(), c.eps,
+                                               1, hid, BTL_F32, None, 0, st))
 
     def reset(self):
         """Llama::reset_state / BitLlama::reset_kv_cache (llama.rs:179-186, 460-468)."""

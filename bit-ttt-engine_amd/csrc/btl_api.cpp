@@ -321,8 +321,25 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         splits = bat ? btl::gemv_bat_split(m, gemv_row_blocks(layers, count), k, &split_steps)
                      : btl::gemm_splits(m, gemm_tiles_n(layers, count), k, &split_steps);
 
+    // One-token decode with a transform: the decode kernel applies it in its own
+    // prologue (every workgroup on its copy of the row), no separate launch --
+    // for f32 input, when the row fits the workgroup for the norm's pairwise
+    // sum, and (residual add) when the summed stream goes to another buffer.
+    // Every workgroup repeats the transform, so it pays only for launches of
+    // at most kFuseMaxWg workgroups (measured on MI355X, Llama-3-8B shapes:
+    // q|k|v with 384 and down with 256 gain ~2 us; gate|up with 1792 and the
+    // 128256-row head lose 2-20 us against the separate one-workgroup
+    // transform kernel).
+    constexpr int64_t kFuseMaxWg = 512;
+    int64_t dec_rb = 0;
+    for (int i = 0; i < count; ++i) dec_rb += ceil_div(layers[i].w->n, 16);
+    const bool fuse = dec && xf && m == 1 && xkind == btl::XK_F32 && env_int("BTL_FUSE_DEC", 1) != 0 &&
+                      ceil_div(dec_rb, rbw) <= env_int("BTL_FUSE_MAX_WG", (int)kFuseMaxWg) &&
+                      wv * rbw <= 8 && k / 16 <= (int64_t)(xf->kind == btl::XF_SWIGLU ? 2 : 1) * wv * rbw * 64 &&
+                      !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
+
     // operand-order quantisation into the workspace (all routes but plain decode)
-    const bool pre = xf || !dec;
+    const bool pre = (xf && !fuse) || !dec;
     const int8_t* q = nullptr;
     const float* sxp = xs;
     void* ws = nullptr;
@@ -370,7 +387,15 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.parts = wv;
         a.kpart = (int)kpart;
         a.ykind = ykind;
-        e = btl::launch_gemv_dec(a, pre ? (int)btl::XK_I8O : xkind, 1, st);
+        int xform = btl::XF_NONE;
+        if (fuse) {
+            xform = xf->kind;
+            a.x2 = (const float*)xf->x2;
+            a.g = xf->g;
+            a.eps = xf->eps;
+            a.hout = xf->hout;
+        }
+        e = btl::launch_gemv_dec(a, pre ? (int)btl::XK_I8O : xkind, xform, st);
         if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
         return BTL_OK;
     }
@@ -690,9 +715,9 @@ int btl_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int c
                   ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream, &xf);
 }
 
-int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, float* h,
-                                 const float* delta, const float* g, float eps, int64_t m, int64_t k, int ydtype,
-                                 void* ws, size_t ws_bytes, void* stream)
+int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, const float* h,
+                                 const float* delta, float* h_out, const float* g, float eps, int64_t m, int64_t k,
+                                 int ydtype, void* ws, size_t ws_bytes, void* stream)
 {
     Layer ls[btl::kMaxGroup];
     int rc;
@@ -700,9 +725,13 @@ int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, i
     if ((rc = check_fused_shape(k, 65536, "fused residual + RMSNorm"))) return rc;
     if (m == 0) return BTL_OK;
     if (!h || !g) return fail(BTL_ERR_LAYOUT, "null residual or norm weight");
-    if (!aligned16(h) || !aligned16(g) || (delta && !aligned16(delta)))
-        return fail(BTL_ERR_LAYOUT, "h, delta and g must be 16-byte aligned");
-    const Xform xf{delta ? btl::XF_ADD_RMSNORM : btl::XF_RMSNORM, delta, g, eps, h};
+    if (!aligned16(h) || !aligned16(g) || (delta && !aligned16(delta)) || (delta && h_out && !aligned16(h_out)))
+        return fail(BTL_ERR_LAYOUT, "h, delta, h_out and g must be 16-byte aligned");
+    if (delta && h_out && h_out != h) {
+        const uintptr_t a0 = (uintptr_t)h, a1 = (uintptr_t)h_out, nb = (uintptr_t)(m * k * 4);
+        if (a0 < a1 + nb && a1 < a0 + nb) return fail(BTL_ERR_LAYOUT, "h_out overlaps h without being h");
+    }
+    const Xform xf{delta ? btl::XF_ADD_RMSNORM : btl::XF_RMSNORM, delta, g, eps, delta ? h_out : nullptr};
     return run_i8(ls, count, h, btl::XK_F32, nullptr, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws,
                   ws_bytes, (hipStream_t)stream, &xf);
 }

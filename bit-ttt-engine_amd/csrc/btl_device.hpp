@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "btl_internal.hpp"
+
 namespace btl {
 
 // Raw buffer loads: a per-workgroup resource descriptor bounds every access,
@@ -70,6 +72,58 @@ __device__ __forceinline__ float wave_pairwise_sum(float v)
 #pragma unroll
     for (int j = 1; j < 64; j <<= 1) v = __fadd_rn(v, __shfl_xor(v, j, 64));
     return v;
+}
+
+// Correctly rounded sqrt of an f32 (the hardware v_sqrt_f32 is not): for a
+// positive finite x = M * 2^(2h) with M an integer in [2^46, 2^48), r =
+// isqrt(M) is found from an f32 estimate corrected with exact 64-bit squares,
+// rounded up when M - r^2 > r (the midpoint (r + 1/2)^2 = r^2 + r + 1/4 is
+// never an integer), and r * 2^h is exact.  Zero, negative, inf and NaN
+// inputs take the hardware sqrt, which is exact for them.
+__device__ __forceinline__ float sqrt_rn(float x)
+{
+    const uint32_t b = __float_as_uint(x);
+    if (!(x > 0.0f) || b >= 0x7F800000u) return __builtin_sqrtf(x);
+    int e = (int)(b >> 23);
+    uint32_t mant = b & 0x7FFFFFu;
+    if (e == 0) {  // subnormal: normalise
+        const int sh = __clz(mant) - 8;
+        mant <<= sh;
+        e = 1 - sh;
+    } else {
+        mant |= 0x800000u;
+    }
+    int ex = e - 150;                   // x = mant * 2^ex, mant in [2^23, 2^24)
+    const int sft = (ex & 1) ? 23 : 24;  // ex - sft even
+    const uint64_t M = (uint64_t)mant << sft;
+    const int h = (ex - sft) / 2;
+    uint64_t r = (uint64_t)__builtin_sqrtf((float)M);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (r * r > M) r -= 1;
+        if ((r + 1) * (r + 1) <= M) r += 1;
+    }
+    if (M - r * r > r) r += 1;
+    return __fmul_rn((float)r, __uint_as_float((uint32_t)(h + 127) << 23));
+}
+
+template <int XK>
+__device__ __forceinline__ void widen16(const uint4* v, float* f)
+{
+    if (XK == XK_BF16) {
+        const uint32_t u[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            f[2 * h] = __uint_as_float(u[h] << 16);
+            f[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            f[4 * h] = __uint_as_float(v[h].x); f[4 * h + 1] = __uint_as_float(v[h].y);
+            f[4 * h + 2] = __uint_as_float(v[h].z); f[4 * h + 3] = __uint_as_float(v[h].w);
+        }
+    }
 }
 
 }  // namespace btl

@@ -40,12 +40,20 @@ struct GemvArgs {
     int parts;        // WV: waves per row block, each one K part (WV * RB <= 16)
     int kpart;        // weights per K part (multiple of 256, at most 2048)
     int ykind;        // YK_F32 / YK_BF16
+    // transform fused into the prologue (m == 1, f32 x; XF_RMSNORM and
+    // XF_ADD_RMSNORM need k / 16 <= threads): the second input (delta or up),
+    // the norm weight, eps, and the summed residual written by workgroup 0
+    // (XF_ADD_RMSNORM; must not alias x)
+    const float* x2;
+    const float* g;
+    float eps;
+    float* hout;
 };
 
 // Decode (k_gemv_dec): parts * tiles <= 16, parts * kpart >= k, kpart <= 2048,
 // a.m <= 4, a.m * k / 16 <= kDecGroups * 64 * parts * tiles.
 constexpr int kDecGroups = 4;  // 16-element token groups per thread in the prologue
-hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s);
+hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t s);
 
 // Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op or
 // k_op_order), k % 64 == 0, k < 2^24, 16-byte aligned q and w.  Up to
@@ -158,6 +166,20 @@ struct AttnArgs {
     float* out;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+// One decode token: RoPE of q and of the new k, the Q8 append of k / v and the
+// attention chunk partials in one kernel, then the merge (m == 1, hd % 16 == 0).
+struct DecKv {
+    const float* q;      // [nh * hd] raw (before RoPE)
+    const float* k;      // [nkv * hd] raw
+    const float* v;      // [nkv * hd]
+    const float* cos_t;  // [max_seq, hd / 2]
+    const float* sin_t;
+    uint8_t* kc_w;       // the cache, written at the position (same buffers as AttnArgs)
+    uint8_t* vc_w;
+    float* ksc_w;
+    float* vsc_w;
+};
+hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t st);
 
 hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
                         float* out, hipStream_t st);

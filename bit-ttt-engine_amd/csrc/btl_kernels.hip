@@ -209,6 +209,20 @@ __device__ __forceinline__ uint32_t group_absmax(const uint4* v)
     return m;
 }
 
+// 16 f32 values -> operand-order int8 word quadruple (finite row, r = 127/a)
+__device__ __forceinline__ uint4 group_quant_f(const float* f, float r)
+{
+    int q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = quant_fast(f[i], r);
+    uint4 o;
+    o.x = pack4(q[0], q[4], q[8], q[12]);
+    o.y = pack4(q[1], q[5], q[9], q[13]);
+    o.z = pack4(q[2], q[6], q[10], q[14]);
+    o.w = pack4(q[3], q[7], q[11], q[15]);
+    return o;
+}
+
 // 16 activations of one group -> operand-order int8 word quadruple
 template <int XK>
 __device__ __forceinline__ uint4 group_quant(const uint4* v, float r)
@@ -230,27 +244,28 @@ __device__ __forceinline__ uint4 group_quant(const uint4* v, float r)
             f[4 * h + 2] = __uint_as_float(v[h].z); f[4 * h + 3] = __uint_as_float(v[h].w);
         }
     }
-    int q[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) q[i] = quant_fast(f[i], r);
-    uint4 o;
-    o.x = pack4(q[0], q[4], q[8], q[12]);
-    o.y = pack4(q[1], q[5], q[9], q[13]);
-    o.z = pack4(q[2], q[6], q[10], q[14]);
-    o.w = pack4(q[3], q[7], q[11], q[15]);
-    return o;
+    return group_quant_f(f, r);
 }
 
 
 
-template <int XK, int ST, int MT>
-__global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
+// Group slots per thread in the prologue: kDecGroups; a fused transform holds
+// its row in fewer (the host checks k / 16 <= DG * threads) and launches at
+// most 512 threads, leaving 256 registers per lane.
+template <int XF>
+struct DecXf {
+    static constexpr int kGroups = XF == XF_NONE ? kDecGroups : (XF == XF_SWIGLU ? 2 : 1);
+};
+
+template <int XK, int ST, int MT, int XF>
+__global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArgs a)
 {
     const int WV = a.parts, RB = a.tiles;  // NW = WV * RB <= 16 waves
     const int NW = WV * RB, NT = NW * 64;
     extern __shared__ __align__(16) uint8_t sq[];  // [mt][k + 16], operand order
     __shared__ uint32_t s_amax[16][MT];
     __shared__ v4i s_red[16][64];
+    __shared__ float s_ss[16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -284,11 +299,12 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
     constexpr bool PREQ = DecX<XK>::kPreq;
     const int gpr = K >> 4;  // groups per token row
     const int ng = mt * gpr;
-    int gm_[kDecGroups], gc_[kDecGroups];
+    constexpr int DG = DecXf<XF>::kGroups;
+    int gm_[DG], gc_[DG];
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(mt * K * ES));
-    uint4 xv[kDecGroups][NV];
+    uint4 xv[DG][NV];
 #pragma unroll
-    for (int gi = 0; gi < kDecGroups; ++gi) {
+    for (int gi = 0; gi < DG; ++gi) {
         const int g = tid + NT * gi;
         const int m = MT == 1 ? 0 : g / max(gpr, 1);
         gm_[gi] = m;
@@ -296,6 +312,18 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
         const int off = g < ng ? (m * K + 16 * gc_[gi]) * ES : kOOB;
 #pragma unroll
         for (int h = 0; h < NV; ++h) xv[gi][h] = gi == 0 || NT * gi < ng ? bload(xr, off + 16 * h) : uint4{0u, 0u, 0u, 0u};
+    }
+    // fused transform input (one token row, f32): delta / up
+    uint4 x2v[DG][4];
+    if (XF == XF_ADD_RMSNORM || XF == XF_SWIGLU) {
+        const __amdgpu_buffer_rsrc_t x2r = make_rsrc(a.x2, (uint32_t)(K * 4));
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi) {
+            const int off = tid + NT * gi < ng ? 64 * (tid + NT * gi) : kOOB;
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                x2v[gi][h] = gi == 0 || NT * gi < ng ? bload(x2r, off + 16 * h) : uint4{0u, 0u, 0u, 0u};
+        }
     }
 
     // 2. every weight load of this wave in flight
@@ -312,12 +340,86 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
     // 3. absmax of each token row over the workgroup; lane m then holds the
     //    quantisation parameters of token row m
     float r_l = 0.0f, s_l = 0.0f;
-    if (!PREQ) {
+    float fv[XF != XF_NONE ? DG : 1][16];
+    if (XF != XF_NONE) {
+        // the transform of k_xform_quant, per workgroup on its own copy of the row
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi) {
+            if (gi == 0 || NT * gi < ng) {
+                widen16<XK_F32>(xv[gi], fv[gi]);
+                if (XF == XF_ADD_RMSNORM || XF == XF_SWIGLU) {
+                    float u[16];
+                    widen16<XK_F32>(x2v[gi], u);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float v = fv[gi][e];
+                        fv[gi][e] = XF == XF_SWIGLU ? __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, btl_expf(-v))), u[e])
+                                                    : __fadd_rn(v, u[e]);
+                    }
+                    if (XF == XF_ADD_RMSNORM && a.hout && blockIdx.x == 0 && tid + NT * gi < ng) {
+                        float4* hp = (float4*)(a.hout + 16 * (tid + NT * gi));
+#pragma unroll
+                        for (int h = 0; h < 4; ++h)
+                            hp[h] = make_float4(fv[gi][4 * h], fv[gi][4 * h + 1], fv[gi][4 * h + 2], fv[gi][4 * h + 3]);
+                    }
+                }
+            }
+        }
+        if (XF == XF_RMSNORM || XF == XF_ADD_RMSNORM) {
+            // sum of squares in the pairwise order of k_xform_quant: the host
+            // launches this only when k / 16 <= NT, so thread t holds elements
+            // [16t, 16t + 16) (zeros past k)
+            float t[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t[e] = __fmul_rn(fv[0][e], fv[0][e]);
+#pragma unroll
+            for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+                for (int i = 0; i < len / 2; ++i) t[i] = __fadd_rn(t[2 * i], t[2 * i + 1]);
+            const float ws = wave_pairwise_sum(t[0]);
+            if (lane == 0) s_ss[wave] = ws;
+            uint4 gv[4];  // the norm weight, loaded only now (fewer live registers while loads fly)
+            {
+                const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
+                const int off = tid < ng ? 64 * tid : kOOB;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) gv[h] = bload(gr, off + 16 * h);
+            }
+            __syncthreads();
+            float p[16];
+#pragma unroll
+            for (int w = 0; w < 16; ++w) p[w] = w < NW ? s_ss[w] : 0.0f;
+#pragma unroll
+            for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+                for (int i = 0; i < len / 2; ++i) p[i] = __fadd_rn(p[2 * i], p[2 * i + 1]);
+            const float inv_k = (float)(1.0 / (double)K);
+            const float d = sqrt_rn(__fadd_rn(__fmul_rn(p[0], inv_k), a.eps));
+            float gf[16];
+            widen16<XK_F32>(gv, gf);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) fv[0][e] = __fmul_rn(__fdiv_rn(fv[0][e], d), gf[e]);
+        }
+        uint32_t am = 0;
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi)
+            if (tid + NT * gi < ng)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) am = max(am, __float_as_uint(fv[gi][e]) & 0x7FFFFFFFu);
+        const uint32_t v = wave_max_dpp(am);
+        if (lane == 0) s_amax[wave][0] = v;
+        __syncthreads();
+        uint32_t vm = 0;
+        for (int w = 0; w < NW; ++w) vm = max(vm, s_amax[w][0]);
+        const QParams qp = qparams(vm);
+        r_l = qp.ok ? qp.r : 0.0f;
+        s_l = qp.s;
+    } else if (!PREQ) {
         uint32_t am[MT];
 #pragma unroll
         for (int mm = 0; mm < MT; ++mm) am[mm] = 0u;
 #pragma unroll
-        for (int gi = 0; gi < kDecGroups; ++gi) {
+        for (int gi = 0; gi < DG; ++gi) {
             if (gi == 0 || NT * gi < ng) {
                 const uint32_t v = tid + NT * gi < ng ? group_absmax<XK>(xv[gi]) : 0u;
 #pragma unroll
@@ -344,12 +446,13 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
 
     // 4. quantise this thread's groups into the shared rows
 #pragma unroll
-    for (int gi = 0; gi < kDecGroups; ++gi) {
+    for (int gi = 0; gi < DG; ++gi) {
         if (gi == 0 || NT * gi < ng) {
             const int g = tid + NT * gi;
             float rm = r_l;
             if (MT > 1) rm = __shfl(r_l, gm_[gi], 64);
-            uint4 q = group_quant<XK>(xv[gi], rm);
+            uint4 q = XF != XF_NONE ? (rm != 0.0f ? group_quant_f(fv[XF != XF_NONE ? gi : 0], rm) : uint4{0u, 0u, 0u, 0u})
+                                    : group_quant<XK>(xv[gi], rm);
             if (!PREQ && rm == 0.0f) q = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
             if (g < ng) *(uint4*)(sq + gm_[gi] * lp + 16 * gc_[gi]) = q;
         }
@@ -403,24 +506,36 @@ __global__ __launch_bounds__(1024) void k_gemv_dec(GemvArgs a)
     }
 }
 
-hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int mtiles, hipStream_t s)
+hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t s)
 {
-    (void)mtiles;
     const int wv = a.parts, rb = a.tiles;
     const int st_need = (a.kpart + kStepWeights - 1) / kStepWeights;
     if (wv < 1 || rb < 1 || wv * rb > 16 || st_need > 8 || a.m < 1 || a.m > 4 ||
         (int64_t)wv * a.kpart < a.k || (int64_t)a.m * (a.k >> 4) > (int64_t)kDecGroups * wv * rb * 64)
         return hipErrorInvalidValue;
+    if (xform != XF_NONE &&
+        (xkind != XK_F32 || a.m != 1 || wv * rb > 8 || !a.x2 == (xform == XF_ADD_RMSNORM || xform == XF_SWIGLU) ||
+         ((xform == XF_RMSNORM || xform == XF_ADD_RMSNORM) && (!a.g || (a.k >> 4) > wv * rb * 64)) ||
+         (xform == XF_SWIGLU && (a.k >> 4) > 2 * wv * rb * 64) || (a.hout && (const void*)a.hout == a.x)))
+        return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.rb_total + rb - 1) / rb)), block((unsigned)(wv * rb * 64));
     const size_t lds = (size_t)a.m * (size_t)(a.k + 16);
     const bool st4 = st_need <= 4;
     const bool mt1 = a.m == 1;
+#define BTL_DEC_XF(XFV)                                                                               \
+    if (xform == XFV) {                                                                               \
+        if (st4) hipLaunchKernelGGL((k_gemv_dec<XK_F32, 4, 1, XFV>), grid, block, lds, s, a);         \
+        else hipLaunchKernelGGL((k_gemv_dec<XK_F32, 8, 1, XFV>), grid, block, lds, s, a);             \
+        return hipGetLastError();                                                                     \
+    }
+    BTL_DEC_XF(XF_RMSNORM) BTL_DEC_XF(XF_ADD_RMSNORM) BTL_DEC_XF(XF_SWIGLU)
+#undef BTL_DEC_XF
 #define BTL_DEC_CASE(XKV)                                                                             \
     if (xkind == XKV) {                                                                               \
-        if (st4 && mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 1>), grid, block, lds, s, a);          \
-        else if (st4) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 4>), grid, block, lds, s, a);            \
-        else if (mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 1>), grid, block, lds, s, a);            \
-        else hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 4>), grid, block, lds, s, a);                     \
+        if (st4 && mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 1, XF_NONE>), grid, block, lds, s, a); \
+        else if (st4) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 4, XF_NONE>), grid, block, lds, s, a);   \
+        else if (mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 1, XF_NONE>), grid, block, lds, s, a);   \
+        else hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 4, XF_NONE>), grid, block, lds, s, a);            \
         return hipGetLastError();                                                                     \
     }
     BTL_DEC_CASE(XK_BF16) BTL_DEC_CASE(XK_F32) BTL_DEC_CASE(XK_I8) BTL_DEC_CASE(XK_I8O)
@@ -534,57 +649,7 @@ hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_
 }
 
 
-// Correctly rounded sqrt of an f32 (the hardware v_sqrt_f32 is not): for a
-// positive finite x = M * 2^(2h) with M an integer in [2^46, 2^48), r =
-// isqrt(M) is found from an f32 estimate corrected with exact 64-bit squares,
-// rounded up when M - r^2 > r (the midpoint (r + 1/2)^2 = r^2 + r + 1/4 is
-// never an integer), and r * 2^h is exact.  Zero, negative, inf and NaN
-// inputs take the hardware sqrt, which is exact for them.
-__device__ __forceinline__ float sqrt_rn(float x)
-{
-    const uint32_t b = __float_as_uint(x);
-    if (!(x > 0.0f) || b >= 0x7F800000u) return __builtin_sqrtf(x);
-    int e = (int)(b >> 23);
-    uint32_t mant = b & 0x7FFFFFu;
-    if (e == 0) {  // subnormal: normalise
-        const int sh = __clz(mant) - 8;
-        mant <<= sh;
-        e = 1 - sh;
-    } else {
-        mant |= 0x800000u;
-    }
-    int ex = e - 150;                   // x = mant * 2^ex, mant in [2^23, 2^24)
-    const int sft = (ex & 1) ? 23 : 24;  // ex - sft even
-    const uint64_t M = (uint64_t)mant << sft;
-    const int h = (ex - sft) / 2;
-    uint64_t r = (uint64_t)__builtin_sqrtf((float)M);
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        if (r * r > M) r -= 1;
-        if ((r + 1) * (r + 1) <= M) r += 1;
-    }
-    if (M - r * r > r) r += 1;
-    return __fmul_rn((float)r, __uint_as_float((uint32_t)(h + 127) << 23));
-}
 
-template <int XK>
-__device__ __forceinline__ void widen16(const uint4* v, float* f)
-{
-    if (XK == XK_BF16) {
-        const uint32_t u[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
-#pragma unroll
-        for (int h = 0; h < 8; ++h) {
-            f[2 * h] = __uint_as_float(u[h] << 16);
-            f[2 * h + 1] = __uint_as_float(u[h] & 0xFFFF0000u);
-        }
-    } else {
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            f[4 * h] = __uint_as_float(v[h].x); f[4 * h + 1] = __uint_as_float(v[h].y);
-            f[4 * h + 2] = __uint_as_float(v[h].z); f[4 * h + 3] = __uint_as_float(v[h].w);
-        }
-    }
-}
 
 
 // k_xform_quant: transform + operand-order quantisation of one token row per
@@ -643,7 +708,7 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
     if (XF == XF_ADD_RMSNORM) {
         // residual connection (block.rs:122,137: residual + mixed_out), f32 + f32
         const __amdgpu_buffer_rsrc_t dr = make_rsrc((const uint8_t*)x2 + row * k * 4, (uint32_t)(k * 4));
-        float* hr = hout + row * k;
+        float* hr = hout ? hout + row * k : nullptr;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             const int gg = tid * G + gi;
@@ -655,7 +720,7 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
             widen16<XK_F32>(v, u);
 #pragma unroll
             for (int e = 0; e < 16; ++e) f[gi][e] = __fadd_rn(f[gi][e], u[e]);
-            if (gg < groups) {
+            if (hr && gg < groups) {
 #pragma unroll
                 for (int h = 0; h < 4; ++h)
                     *(float4*)(hr + gg * 16 + 4 * h) =
@@ -740,7 +805,7 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
 hipError_t launch_xform_quant(const void* x, const void* x2, int xkind, int xform, const float* g,
                               float eps, int64_t m, int64_t k, int8_t* q, float* s, hipStream_t st, float* hout)
 {
-    if (xform == XF_ADD_RMSNORM && (xkind != XK_F32 || !x2 || !hout)) return hipErrorInvalidValue;
+    if (xform == XF_ADD_RMSNORM && (xkind != XK_F32 || !x2)) return hipErrorInvalidValue;
     if (m <= 0) return hipSuccess;
     const int64_t groups = k >> 4;
     if (k % 64 != 0 || groups > (xform == XF_SWIGLU ? 2048 : 4096) || (xkind != XK_F32 && xkind != XK_BF16))

@@ -127,13 +127,81 @@ hipError_t launch_rope_kv_q8(const KvArgs& a, hipStream_t st)
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxHd = 128;
 constexpr int kAttnMaxRep = 16;
+constexpr int kAttnKs = kAttnMaxHd + 4;  // LDS key row stride (floats): 16-byte rows, conflict-free b128 reads
 
+// One query of one head against the staged chunk (nj valid keys):
+//   s_j   = (sum_d q[d] * kd[j][d], sequential over d) * scal      (lane j)
+//   m_c   = max_j s_j;  p_j = exp(s_j - m_c);  l_c = pairwise sum over the lanes
+//   o_c[d] = sum_j p_j * vd[j][d], sequential over j                (lanes: d, d + 64)
+// and (m_c, l_c, o_c) to part.  Called by every thread of the workgroup (it
+// holds a barrier); sq / sp are this wave's rows of s_q / s_p.
+template <int HD>
+__device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], const float (*s_v)[kAttnMaxHd],
+                                                 const float* sq, float* sp, int nj, int hd_rt, float scal, int lane,
+                                                 float* part)
+{
+    const int hd = HD ? HD : hd_rt;  // HD > 0: the loops unroll and the LDS reads batch
+    float sc = -__builtin_inff();
+    if (lane < nj) {
+        float acc = 0.0f;
+        if ((hd & 3) == 0) {
+#pragma unroll
+            for (int d = 0; d < hd; d += 4) {
+                const float4 q4 = *(const float4*)&sq[d];
+                const float4 k4 = *(const float4*)&s_k[lane][d];
+                acc = __fadd_rn(acc, __fmul_rn(q4.x, k4.x));
+                acc = __fadd_rn(acc, __fmul_rn(q4.y, k4.y));
+                acc = __fadd_rn(acc, __fmul_rn(q4.z, k4.z));
+                acc = __fadd_rn(acc, __fmul_rn(q4.w, k4.w));
+            }
+        } else {
+            for (int d = 0; d < hd; ++d) acc = __fadd_rn(acc, __fmul_rn(sq[d], s_k[lane][d]));
+        }
+        sc = __fadd_rn(__fmul_rn(acc, scal), 0.0f);  // candle affine(scal, 0)
+    }
+    const float mc = wave_max_f32(sc);
+    const float p = lane < nj ? btl_expf(__fsub_rn(sc, mc)) : 0.0f;
+    const float lc = wave_pairwise_sum(p);
+    sp[lane] = p;
+    __syncthreads();
+    const int d0 = lane, d1 = lane + 64;
+    float o0 = 0.0f, o1 = 0.0f;
+    const bool h0 = d0 < hd, h1 = d1 < hd;
+    const int c0 = h0 ? d0 : 0, c1 = h1 ? d1 : 0;  // clamped columns (values unused when out of range)
+    int j = 0;
+    for (; j + 4 <= nj; j += 4) {
+        const float4 p4 = *(const float4*)&sp[j];
+        const float a0 = s_v[j][c0], a1 = s_v[j + 1][c0], a2 = s_v[j + 2][c0], a3 = s_v[j + 3][c0];
+        const float b0 = s_v[j][c1], b1 = s_v[j + 1][c1], b2 = s_v[j + 2][c1], b3 = s_v[j + 3][c1];
+        o0 = __fadd_rn(o0, __fmul_rn(p4.x, a0));
+        o0 = __fadd_rn(o0, __fmul_rn(p4.y, a1));
+        o0 = __fadd_rn(o0, __fmul_rn(p4.z, a2));
+        o0 = __fadd_rn(o0, __fmul_rn(p4.w, a3));
+        o1 = __fadd_rn(o1, __fmul_rn(p4.x, b0));
+        o1 = __fadd_rn(o1, __fmul_rn(p4.y, b1));
+        o1 = __fadd_rn(o1, __fmul_rn(p4.z, b2));
+        o1 = __fadd_rn(o1, __fmul_rn(p4.w, b3));
+    }
+    for (; j < nj; ++j) {
+        const float pj = sp[j];
+        o0 = __fadd_rn(o0, __fmul_rn(pj, s_v[j][c0]));
+        o1 = __fadd_rn(o1, __fmul_rn(pj, s_v[j][c1]));
+    }
+    if (h0) part[2 + d0] = o0;
+    if (h1) part[2 + d1] = o1;
+    if (lane == 0) {
+        part[0] = mc;
+        part[1] = lc;
+    }
+}
+
+template <int HD>
 __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
 {
-    __shared__ float s_k[kAttnChunk][kAttnMaxHd + 1];
-    __shared__ float s_v[kAttnChunk][kAttnMaxHd];
-    __shared__ float s_q[kAttnMaxRep][kAttnMaxHd];
-    __shared__ float s_p[kAttnMaxRep][kAttnChunk];
+    __shared__ __align__(16) float s_k[kAttnChunk][kAttnKs];
+    __shared__ __align__(16) float s_v[kAttnChunk][kAttnMaxHd];
+    __shared__ __align__(16) float s_q[kAttnMaxRep][kAttnMaxHd];
+    __shared__ __align__(16) float s_p[kAttnMaxRep][kAttnChunk];
     const int g = blockIdx.x, c = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nthr = blockDim.x;
@@ -147,13 +215,55 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
     if (j0 >= t_last) return;                           // uniform
     const int nstage = min(kAttnChunk, t_last - j0);
 
-    // dequantise the chunk's keys and values into LDS
+    // dequantise the chunk's keys and values into LDS:
+    // kd = ((f32)code - 128) * s (kv_cache.rs:122-128)
     const int64_t base = (int64_t)g * a.max_seq + j0;
-    for (int idx = tid; idx < nstage * hd; idx += nthr) {
-        const int j = idx / hd, d = idx - j * hd;
-        const int64_t r = base + j;
-        s_k[j][d] = __fmul_rn(__fsub_rn((float)a.kc[r * hd + d], 128.0f), a.ksc[r]);
-        s_v[j][d] = __fmul_rn(__fsub_rn((float)a.vc[r * hd + d], 128.0f), a.vsc[r]);
+    if ((hd & 15) == 0) {
+        // 16-byte loads, all in flight before the first conversion
+        const int vpr = hd >> 4, nvec = nstage * vpr;
+        uint4 kv[8], vv[8];
+        float ks[8], vs[8];
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int idx = tid + it * nthr;
+            if (idx < nvec) {
+                const int j = idx / vpr;
+                kv[it] = ((const uint4*)(a.kc + (base + j) * hd))[idx - j * vpr];
+                vv[it] = ((const uint4*)(a.vc + (base + j) * hd))[idx - j * vpr];
+                ks[it] = a.ksc[base + j];
+                vs[it] = a.vsc[base + j];
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int idx = tid + it * nthr;
+            if (idx < nvec) {
+                const int j = idx / vpr, e0 = (idx - j * vpr) * 16;
+                const uint32_t kw[4] = {kv[it].x, kv[it].y, kv[it].z, kv[it].w};
+                const uint32_t vw[4] = {vv[it].x, vv[it].y, vv[it].z, vv[it].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float4 kf, vf;
+                    kf.x = __fmul_rn(__fsub_rn((float)(kw[q] & 255u), 128.0f), ks[it]);
+                    kf.y = __fmul_rn(__fsub_rn((float)((kw[q] >> 8) & 255u), 128.0f), ks[it]);
+                    kf.z = __fmul_rn(__fsub_rn((float)((kw[q] >> 16) & 255u), 128.0f), ks[it]);
+                    kf.w = __fmul_rn(__fsub_rn((float)(kw[q] >> 24), 128.0f), ks[it]);
+                    vf.x = __fmul_rn(__fsub_rn((float)(vw[q] & 255u), 128.0f), vs[it]);
+                    vf.y = __fmul_rn(__fsub_rn((float)((vw[q] >> 8) & 255u), 128.0f), vs[it]);
+                    vf.z = __fmul_rn(__fsub_rn((float)((vw[q] >> 16) & 255u), 128.0f), vs[it]);
+                    vf.w = __fmul_rn(__fsub_rn((float)(vw[q] >> 24), 128.0f), vs[it]);
+                    *(float4*)&s_k[j][e0 + 4 * q] = kf;
+                    *(float4*)&s_v[j][e0 + 4 * q] = vf;
+                }
+            }
+        }
+    } else {
+        for (int idx = tid; idx < nstage * hd; idx += nthr) {
+            const int j = idx / hd, d = idx - j * hd;
+            const int64_t r = base + j;
+            s_k[j][d] = __fmul_rn(__fsub_rn((float)a.kc[r * hd + d], 128.0f), a.ksc[r]);
+            s_v[j][d] = __fmul_rn(__fsub_rn((float)a.vc[r * hd + d], 128.0f), a.vsc[r]);
+        }
     }
 
     for (int i = i_begin; i < i_end; ++i) {
@@ -163,59 +273,218 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
         const float* qg = a.q + ((int64_t)i * a.nh + h) * hd;
         for (int d = lane; d < hd; d += 64) s_q[wave][d] = qg[d];
         __syncthreads();
-        float sc = -__builtin_inff();
-        if (lane < nj) {
-            float acc = 0.0f;
-            for (int d = 0; d < hd; ++d) acc = __fadd_rn(acc, __fmul_rn(s_q[wave][d], s_k[lane][d]));
-            sc = __fadd_rn(__fmul_rn(acc, a.scal), 0.0f);  // candle affine(scal, 0)
-        }
-        const float mc = wave_max_f32(sc);
-        const float p = lane < nj ? btl_expf(__fsub_rn(sc, mc)) : 0.0f;
-        const float lc = wave_pairwise_sum(p);
-        s_p[wave][lane] = p;
-        __syncthreads();
         float* part = a.part + (((int64_t)i * a.nh + h) * a.cmax + c) * (hd + 2);
-        for (int d = lane; d < hd; d += 64) {
-            float o = 0.0f;
-            for (int j = 0; j < nj; ++j) o = __fadd_rn(o, __fmul_rn(s_p[wave][j], s_v[j][d]));
-            part[2 + d] = o;
-        }
-        if (lane == 0) {
-            part[0] = mc;
-            part[1] = lc;
-        }
+        attn_chunk_query<HD>(s_k, s_v, s_q[wave], s_p[wave], nj, hd, a.scal, lane, part);
         __syncthreads();  // s_q / s_p are rewritten by the next query
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_attn_dec1: one decode token -- RoPE, the Q8 append and the chunk partials
+// ---------------------------------------------------------------------------
+// grid (nkv, cmax), block 64 * rep.  The work of k_rope_kv_q8 + k_attn_part for
+// m = 1 in one launch: every workgroup rotates its query heads itself; the
+// workgroup whose chunk holds the position rotates and quantises the new k and
+// v row, writes it to the cache and patches its LDS copy of the chunk with the
+// dequantised row (the reference attends over the dequantised cache, new row
+// included: kv_cache.rs:82-86).  Loads that do not depend on the position (the
+// raw q / k / v rows and the chunk's cache rows) are issued before it arrives.
+template <int HD>
+__global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
+{
+    __shared__ __align__(16) float s_k[kAttnChunk][kAttnKs];
+    __shared__ __align__(16) float s_v[kAttnChunk][kAttnMaxHd];
+    __shared__ __align__(16) float s_q[kAttnMaxRep][kAttnMaxHd];
+    __shared__ __align__(16) float s_p[kAttnMaxRep][kAttnChunk];
+    const int g = blockIdx.x, c = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = blockDim.x;
+    const int hd = a.hd, half = hd >> 1, rep = a.nh / a.nkv;
+    const int h = g * rep + wave;
+    const int j0 = c * kAttnChunk;
+    if (j0 >= a.max_seq) return;  // uniform
+    const bool act = lane < half;
+
+    // position-independent loads: raw q of this wave's head, raw k / v of the KV head, the chunk rows
+    float q1 = act ? kv.q[h * hd + lane] : 0.0f, q2 = act ? kv.q[h * hd + lane + half] : 0.0f;
+    float k1 = act ? kv.k[g * hd + lane] : 0.0f, k2 = act ? kv.k[g * hd + lane + half] : 0.0f;
+    float v1 = act ? kv.v[g * hd + lane] : 0.0f, v2 = act ? kv.v[g * hd + lane + half] : 0.0f;
+    const int nrows = min(kAttnChunk, a.max_seq - j0);
+    const int64_t base = (int64_t)g * a.max_seq + j0;
+    const int vpr = hd >> 4, nvec = nrows * vpr;  // hd % 16 == 0 (host)
+    uint4 kvv[8], vvv[8];
+    float ks[8], vs[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const int idx = tid + it * nthr;
+        if (idx < nvec) {
+            const int j = idx / vpr;
+            kvv[it] = ((const uint4*)(a.kc + (base + j) * hd))[idx - j * vpr];
+            vvv[it] = ((const uint4*)(a.vc + (base + j) * hd))[idx - j * vpr];
+            ks[it] = a.ksc[base + j];
+            vs[it] = a.vsc[base + j];
+        }
+    }
+    const int pos = a.d_pos ? *a.d_pos : a.pos;
+    if (pos < 0 || pos >= a.max_seq) return;  // uniform: nothing to append or attend
+    const int T = pos + 1;
+    if (j0 >= T) return;  // uniform
+    const int nj = min(kAttnChunk, T - j0);
+    float cs = 1.0f, sn = 0.0f;
+    if (act) {
+        cs = kv.cos_t[(int64_t)pos * half + lane];
+        sn = kv.sin_t[(int64_t)pos * half + lane];
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const int idx = tid + it * nthr;
+        if (idx < nvec) {
+            const int j = idx / vpr, e0 = (idx - j * vpr) * 16;
+            const uint32_t kw[4] = {kvv[it].x, kvv[it].y, kvv[it].z, kvv[it].w};
+            const uint32_t vw[4] = {vvv[it].x, vvv[it].y, vvv[it].z, vvv[it].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float4 kf, vf;
+                kf.x = __fmul_rn(__fsub_rn((float)(kw[q] & 255u), 128.0f), ks[it]);
+                kf.y = __fmul_rn(__fsub_rn((float)((kw[q] >> 8) & 255u), 128.0f), ks[it]);
+                kf.z = __fmul_rn(__fsub_rn((float)((kw[q] >> 16) & 255u), 128.0f), ks[it]);
+                kf.w = __fmul_rn(__fsub_rn((float)(kw[q] >> 24), 128.0f), ks[it]);
+                vf.x = __fmul_rn(__fsub_rn((float)(vw[q] & 255u), 128.0f), vs[it]);
+                vf.y = __fmul_rn(__fsub_rn((float)((vw[q] >> 8) & 255u), 128.0f), vs[it]);
+                vf.z = __fmul_rn(__fsub_rn((float)((vw[q] >> 16) & 255u), 128.0f), vs[it]);
+                vf.w = __fmul_rn(__fsub_rn((float)(vw[q] >> 24), 128.0f), vs[it]);
+                *(float4*)&s_k[j][e0 + 4 * q] = kf;
+                *(float4*)&s_v[j][e0 + 4 * q] = vf;
+            }
+        }
+    }
+    // RoPE of this wave's query head (attention.rs:67-83)
+    if (act) {
+        s_q[wave][lane] = __fsub_rn(__fmul_rn(q1, cs), __fmul_rn(q2, sn));
+        s_q[wave][lane + half] = __fadd_rn(__fmul_rn(q1, sn), __fmul_rn(q2, cs));
+    }
+    const bool owner = pos - j0 < kAttnChunk;  // uniform: this chunk holds the new row
+    __syncthreads();
+    if (owner && wave < 2) {
+        // wave 0: RoPE + Q8 of k;  wave 1 (or wave 0 again when rep == 1): Q8 of v
+        for (int which = wave; which < 2; which += (rep == 1 ? 1 : 2)) {
+            float x1 = which == 0 ? k1 : v1, x2 = which == 0 ? k2 : v2;
+            if (which == 0 && act) {
+                const float o1 = __fsub_rn(__fmul_rn(x1, cs), __fmul_rn(x2, sn));
+                const float o2 = __fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, cs));
+                x1 = o1;
+                x2 = o2;
+            }
+            const uint32_t am =
+                wave_max_dpp(max(__float_as_uint(x1) & 0x7FFFFFFFu, __float_as_uint(x2) & 0x7FFFFFFFu));
+            const float sc = __fdiv_rn(__uint_as_float(am), 127.0f);
+            const int64_t row = (int64_t)g * a.max_seq + pos;
+            uint8_t* cache = (which == 0 ? kv.kc_w : kv.vc_w) + row * hd;
+            float* srow = which == 0 ? &s_k[pos - j0][0] : &s_v[pos - j0][0];
+            if (act) {
+                const uint32_t c1 = sat_u8(__fadd_rn(__builtin_roundf(__fdiv_rn(x1, sc)), 128.0f));
+                const uint32_t c2 = sat_u8(__fadd_rn(__builtin_roundf(__fdiv_rn(x2, sc)), 128.0f));
+                cache[lane] = (uint8_t)c1;
+                cache[lane + half] = (uint8_t)c2;
+                srow[lane] = __fmul_rn(__fsub_rn((float)c1, 128.0f), sc);
+                srow[lane + half] = __fmul_rn(__fsub_rn((float)c2, 128.0f), sc);
+            }
+            if (lane == 0) (which == 0 ? kv.ksc_w : kv.vsc_w)[row] = sc;
+        }
+    }
+    __syncthreads();
+    float* part = a.part + ((int64_t)h * a.cmax + c) * (hd + 2);
+    attn_chunk_query<HD>(s_k, s_v, s_q[wave], s_p[wave], nj, hd, a.scal, lane, part);
+}
+
 // grid (m, nh), block 64: y[d] = (sum_c w_c o_c[d]) / (sum_c w_c l_c),
-// w_c = exp(m_c - max_c m_c), sums sequential over the chunks.
+// w_c = exp(m_c - max_c m_c), both sums sequential over the chunks.  Lane c
+// holds chunk c's (m_c, l_c); the value loads of up to 16 chunks are all in
+// flight before the sums.
 __global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a)
 {
     const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-    const int hd = a.hd;
+    const int hd = a.hd, st = hd + 2;
+    const float* part = a.part + ((int64_t)i * a.nh + h) * a.cmax * st;
+    const int d0 = lane, d1 = lane + 64;
+    const bool h0 = d0 < hd, h1 = d1 < hd;
+    // loads that do not need the position: the first 64 chunks' (m, l) and the
+    // first 16 chunks' values (slots past the used chunks hold stale data, unused)
+    constexpr int kPre = 16;
+    float p0[kPre], p1[kPre];
+#pragma unroll
+    for (int c = 0; c < kPre; ++c) {
+        p0[c] = (c < a.cmax && h0) ? part[c * st + 2 + d0] : 0.0f;
+        p1[c] = (c < a.cmax && h1) ? part[c * st + 2 + d1] : 0.0f;
+    }
+    const float m_pre = lane < a.cmax ? part[lane * st] : 0.0f;
+    const float l_pre = lane < a.cmax ? part[lane * st + 1] : 0.0f;
     const int pos0 = a.d_pos ? *a.d_pos : a.pos;
-    const int T = min(pos0 + i + 1, a.max_seq);
+    const int T = pos0 + i + 1;
     float* y = a.out + ((int64_t)i * a.nh + h) * hd;
-    if (T <= 0) {
-        for (int d = lane; d < hd; d += 64) y[d] = __builtin_nanf("");
+    if (T <= 0 || T > a.max_seq) {  // a device position outside the cache: no result
+        if (h0) y[d0] = __builtin_nanf("");
+        if (h1) y[d1] = __builtin_nanf("");
         return;
     }
     const int C = (T + kAttnChunk - 1) / kAttnChunk;
-    const float* part = a.part + ((int64_t)i * a.nh + h) * a.cmax * (hd + 2);
     float M = -__builtin_inff();
-    for (int c = 0; c < C; ++c) M = fmaxf(M, part[c * (hd + 2)]);
-    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
-    const int d0 = lane, d1 = lane + 64;
-    for (int c = 0; c < C; ++c) {
-        const float* pc = part + c * (hd + 2);
-        const float w = btl_expf(__fsub_rn(pc[0], M));
-        L = __fadd_rn(L, __fmul_rn(w, pc[1]));
-        if (d0 < hd) O0 = __fadd_rn(O0, __fmul_rn(w, pc[2 + d0]));
-        if (d1 < hd) O1 = __fadd_rn(O1, __fmul_rn(w, pc[2 + d1]));
+    for (int c0 = 0; c0 < C; c0 += 64) {
+        const int cc = c0 + lane;
+        const float mv = c0 == 0 ? m_pre : (cc < C ? part[cc * st] : 0.0f);
+        M = fmaxf(M, wave_max_f32(cc < C ? mv : -__builtin_inff()));
     }
-    if (d0 < hd) y[d0] = __fdiv_rn(O0, L);
-    if (d1 < hd) y[d1] = __fdiv_rn(O1, L);
+    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+    for (int c0 = 0; c0 < C; c0 += 64) {
+        const int cc = c0 + lane;
+        const float mv = c0 == 0 ? m_pre : (cc < C ? part[cc * st] : 0.0f);
+        const float lv = c0 == 0 ? l_pre : (cc < C ? part[cc * st + 1] : 0.0f);
+        const float w = cc < C ? btl_expf(__fsub_rn(mv, M)) : 0.0f;
+        const float l = cc < C ? lv : 0.0f;
+        const int n = min(64, C - c0);
+        int u = 0;
+        if (c0 == 0) {
+#pragma unroll
+            for (int q = 0; q < kPre; ++q) {
+                if (q < n) {
+                    const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), q));
+                    const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), q));
+                    L = __fadd_rn(L, __fmul_rn(wu, lu));
+                    O0 = __fadd_rn(O0, __fmul_rn(wu, p0[q]));
+                    O1 = __fadd_rn(O1, __fmul_rn(wu, p1[q]));
+                }
+            }
+            u = min(n, kPre);
+        }
+        for (; u < n; ++u) {
+            const int c = c0 + u;
+            const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+            const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), u));
+            L = __fadd_rn(L, __fmul_rn(wu, lu));
+            const float v0 = h0 ? part[c * st + 2 + d0] : 0.0f;
+            const float v1 = h1 ? part[c * st + 2 + d1] : 0.0f;
+            O0 = __fadd_rn(O0, __fmul_rn(wu, v0));
+            O1 = __fadd_rn(O1, __fmul_rn(wu, v1));
+        }
+    }
+    if (h0) y[d0] = __fdiv_rn(O0, L);
+    if (h1) y[d1] = __fdiv_rn(O1, L);
+}
+
+hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t st)
+{
+    const int rep = a.nh / a.nkv;
+    if (a.m != 1 || a.hd < 16 || a.hd > kAttnMaxHd || (a.hd & 15) || a.nkv < 1 || a.nh % a.nkv != 0 ||
+        rep > kAttnMaxRep || a.cmax < 1)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)a.nkv, (unsigned)a.cmax), block((unsigned)(64 * rep));
+    if (a.hd == 128) hipLaunchKernelGGL(k_attn_dec1<128>, grid, block, 0, st, a, kv);
+    else if (a.hd == 64) hipLaunchKernelGGL(k_attn_dec1<64>, grid, block, 0, st, a, kv);
+    else hipLaunchKernelGGL(k_attn_dec1<0>, grid, block, 0, st, a, kv);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_combine, dim3(1u, (unsigned)a.nh), dim3(64), 0, st, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st)
@@ -226,7 +495,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st)
         a.cmax < 1)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)a.nkv, (unsigned)a.cmax, (unsigned)((a.m + a.qb - 1) / a.qb));
-    hipLaunchKernelGGL(k_attn_part, grid, dim3((unsigned)(64 * rep)), 0, st, a);
+    const dim3 block((unsigned)(64 * rep));
+    if (a.hd == 128) hipLaunchKernelGGL(k_attn_part<128>, grid, block, 0, st, a);
+    else if (a.hd == 64) hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, a);
+    else hipLaunchKernelGGL(k_attn_part<0>, grid, block, 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)a.m, (unsigned)a.nh), dim3(64), 0, st, a);

@@ -62,6 +62,13 @@ int check_pos(int64_t pos, int64_t m, const int32_t* d_pos, const btl_kv_q8_t* c
 // few enough that the grid still covers the chip
 int attn_qb(int64_t m) { return m <= 1 ? 1 : (m <= 64 ? 4 : 16); }
 
+// workspace: [rotated q, m * n_heads * head_dim f32 (btl_rope_append_attention
+// with m > 1)] [chunk partials, m * n_heads * cmax * (head_dim + 2) f32]
+size_t qrot_bytes(int64_t m, int64_t n_heads, const btl_kv_q8_t* cache)
+{
+    return (size_t)((m * n_heads * cache->head_dim * 4 + 255) / 256 * 256);
+}
+
 }  // namespace
 
 extern "C" {
@@ -122,7 +129,7 @@ size_t btl_attention_workspace_bytes(int64_t m, int64_t n_heads, const btl_kv_q8
 {
     if (!cache || m < 0 || n_heads < 0 || cache->max_seq < 1) return 0;
     const int64_t cmax = (cache->max_seq + kChunk - 1) / kChunk;
-    return (size_t)(m * n_heads * cmax * (cache->head_dim + 2) * 4);
+    return qrot_bytes(m, n_heads, cache) + (size_t)(m * n_heads * cmax * (cache->head_dim + 2) * 4);
 }
 
 int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t* cache, int64_t pos,
@@ -136,9 +143,10 @@ int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t*
     if (!q || !out) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
     int dev;
     if ((rc = btl::host::device(&dev))) return rc;
-    void* part = nullptr;
-    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &part)))
+    void* wsp = nullptr;
+    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &wsp)))
         return rc;
+    void* part = (uint8_t*)wsp + qrot_bytes(m, n_heads, cache);
     btl::AttnArgs a{};
     a.q = q;
     a.kc = cache->k;
@@ -158,6 +166,74 @@ int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t*
     a.part = (float*)part;
     a.out = out;
     hipError_t e = btl::launch_attention(a, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "attention kernel launch");
+    return BTL_OK;
+}
+
+int btl_rope_append_attention(const float* q, const float* k, const float* v, int64_t m, int64_t n_heads,
+                              const btl_kv_q8_t* cache, int64_t pos, const int32_t* d_pos, const float* rope_cos,
+                              const float* rope_sin, float* out, void* ws, size_t ws_bytes, void* stream)
+{
+    int rc;
+    if ((rc = check_cache(cache, n_heads))) return rc;
+    if (m < 0 || m > (1 << 20)) return fail_msg(BTL_ERR_SHAPE, "token count out of range");
+    if ((rc = check_pos(pos, m, d_pos, cache))) return rc;
+    if (m == 0) return BTL_OK;
+    if (!q || !k || !v || !out || !rope_cos || !rope_sin) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    int dev;
+    if ((rc = btl::host::device(&dev))) return rc;
+    void* wsp = nullptr;
+    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &wsp)))
+        return rc;
+    float* qrot = (float*)wsp;
+    btl::AttnArgs a{};
+    a.kc = cache->k;
+    a.vc = cache->v;
+    a.ksc = cache->k_scale;
+    a.vsc = cache->v_scale;
+    a.d_pos = d_pos;
+    a.pos = (int)pos;
+    a.m = (int)m;
+    a.nh = (int)n_heads;
+    a.nkv = (int)cache->n_kv_heads;
+    a.hd = (int)cache->head_dim;
+    a.max_seq = (int)cache->max_seq;
+    a.cmax = (int)((cache->max_seq + kChunk - 1) / kChunk);
+    a.qb = attn_qb(m);
+    a.scal = (float)(1.0 / std::sqrt((double)cache->head_dim));
+    a.part = (float*)((uint8_t*)wsp + qrot_bytes(m, n_heads, cache));
+    a.out = out;
+    hipError_t e;
+    if (m == 1 && cache->head_dim % 16 == 0) {
+        // one decode token: RoPE, append and attention in one kernel, then the merge
+        btl::DecKv kv{q, k, v, rope_cos, rope_sin, cache->k, cache->v, cache->k_scale, cache->v_scale};
+        a.q = q;
+        e = btl::launch_attention_dec1(a, kv, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_error(e, "decode attention kernel launch");
+        return BTL_OK;
+    }
+    btl::KvArgs r{};
+    r.q = q;
+    r.k = k;
+    r.v = v;
+    r.q_out = qrot;
+    r.kc = cache->k;
+    r.vc = cache->v;
+    r.ksc = cache->k_scale;
+    r.vsc = cache->v_scale;
+    r.cos_t = rope_cos;
+    r.sin_t = rope_sin;
+    r.d_pos = d_pos;
+    r.pos = (int)pos;
+    r.m = (int)m;
+    r.nh = (int)n_heads;
+    r.nkv = (int)cache->n_kv_heads;
+    r.hd = (int)cache->head_dim;
+    r.max_seq = (int)cache->max_seq;
+    e = btl::launch_rope_kv_q8(r, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "rope / kv append kernel launch");
+    a.q = qrot;
+    e = btl::launch_attention(a, (hipStream_t)stream);
     if (e != hipSuccess) return hip_error(e, "attention kernel launch");
     return BTL_OK;
 }

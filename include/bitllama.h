@@ -95,6 +95,21 @@ int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t*
                   const int32_t* d_pos, float* out, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The attention core of BitAttention::forward between the q/k/v projections and
+ * o_proj (attention.rs:165-219): RoPE of q and k, QuantizedKVCache::append of
+ * k and v, attention -- btl_rope_kv_append then btl_attention, same results
+ * bit for bit.  q [m, n_heads * head_dim], k, v [m, n_kv * head_dim] raw
+ * projection outputs (not modified), out [m, n_heads * head_dim].  For one
+ * token (m == 1, head_dim % 16 == 0) the RoPE, the append and the attention
+ * partials run in one kernel.  ws: btl_attention_workspace_bytes (it covers
+ * the rotated queries too).  A device position outside the cache gives NaN
+ * outputs and no append.
+ */
+int btl_rope_append_attention(const float* q, const float* k, const float* v, int64_t m, int64_t n_heads,
+                              const btl_kv_q8_t* cache, int64_t pos, const int32_t* d_pos, const float* rope_cos,
+                              const float* rope_sin, float* out, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Embedding::forward (llama.rs:208): out[t] = (f32) table[ids[t]] for
  * t < m.  table [vocab, dim] of dtype (BTL_F32 / BTL_BF16), ids device int32.
  * An id outside [0, vocab) gives a zero row.
@@ -113,14 +128,17 @@ int btl_greedy_next(const float* logits, int64_t n, int32_t* next_id, int32_t* d
 
 /*
  * Residual connection fused ahead of RMSNorm and a BitLinear group
- * (block.rs:122-123,137 then the next norm): h += delta (f32, in place), then
- * btl_rmsnorm_linear_group on h.  delta == NULL: plain RMSNorm of h (h not
- * written).  h, delta [m, k] f32, g [k] f32.  k % 64 == 0, 64 <= k <= 65536;
- * h, delta and g 16-byte aligned.
+ * (block.rs:122-123,137 then the next norm): s = h + delta (f32), stored to
+ * h_out when h_out != NULL (h_out may be h itself, or a buffer that does not
+ * overlap it), then btl_rmsnorm_linear_group on s.  delta == NULL: plain
+ * RMSNorm of h, h_out not written.  h, delta, h_out [m, k] f32, g [k] f32.
+ * k % 64 == 0, 64 <= k <= 65536; h, delta, h_out and g 16-byte aligned.
+ * For one token row (decode) with h_out not aliasing h, the add and the norm
+ * run inside the contraction kernel's prologue (one launch).
  */
-int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, float* h,
-                                 const float* delta, const float* g, float eps, int64_t m, int64_t k, int ydtype,
-                                 void* ws, size_t ws_bytes, void* stream);
+int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, int count, const float* h,
+                                 const float* delta, float* h_out, const float* g, float eps, int64_t m, int64_t k,
+                                 int ydtype, void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -160,6 +160,66 @@ def test_attention_device_position():
         assert_same(out[0], orc.attn_decode(q[0], kq, ks, vq, vs, nh, p + 1), "pos %d" % p)
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(4, 2, 64), (32, 8, 128), (4, 4, 128), (8, 1, 16)])
+@pytest.mark.parametrize("pos,dpos", [(0, False), (63, True), (64, False), (130, True), (255, False)])
+def test_rope_append_attention_one_token(nh, nkv, hd, pos, dpos):
+    # m = 1: RoPE, the Q8 append and the attention in one kernel; same bits as
+    # btl_rope_kv_append + btl_attention and as the oracle
+    print("rope_append_attention", nh, nkv, hd, pos, dpos, flush=True)
+    S = 256
+    rng = np.random.default_rng(pos * 7 + hd + nh)
+    q = rng.standard_normal((1, nh * hd)).astype(np.float32)
+    k = (rng.standard_normal((1, nkv * hd)) * 2).astype(np.float32)
+    v = rng.standard_normal((1, nkv * hd)).astype(np.float32)
+    cos, sin, dc, ds = rope_dev(500000.0, hd, S)
+    cache = Cache(nkv, S, hd)
+    _fill_cache(cache, S, seed=pos + 1)
+    kq0, ks0, vq0, vs0 = cache.host()
+    qt, kt, vt = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
+    out = torch.full((1, nh * hd), 3.0, device=DEV)
+    d_pos = torch.tensor([pos], dtype=torch.int32, device=DEV) if dpos else None
+    bl.check(bl.lib.btl_rope_append_attention(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), 1, nh, ctypes.byref(cache.c),
+                                              0 if dpos else pos, d_pos.data_ptr() if dpos else None, dc.data_ptr(),
+                                              ds.data_ptr(), out.data_ptr(), None, 0, stream()))
+    assert_same(qt, q, "q not modified")
+    kq, ks, vq, vs = cache.host()
+    ekq, eks = orc.q8_quant(orc.rope_apply(k[0].reshape(nkv, hd), cos[pos], sin[pos]))
+    evq, evs = orc.q8_quant(v[0].reshape(nkv, hd))
+    assert np.array_equal(kq[:, pos], ekq) and np.array_equal(vq[:, pos], evq)
+    assert_same(ks[:, pos], eks, "k scale")
+    assert_same(vs[:, pos], evs, "v scale")
+    other = [r for r in range(S) if r != pos]
+    assert np.array_equal(kq[:, other], kq0[:, other]) and np.array_equal(vs[:, other], vs0[:, other])
+    qr = orc.rope_apply(q[0].reshape(nh, hd), cos[pos], sin[pos]).reshape(-1)
+    assert_same(out[0], orc.attn_decode(qr, kq, ks, vq, vs, nh, pos + 1), "attention")
+
+
+@pytest.mark.parametrize("m,pos", [(2, 0), (17, 40), (70, 60)])
+def test_rope_append_attention_many_tokens(m, pos):
+    nh, nkv, hd, S = 8, 2, 128, 200
+    rng = np.random.default_rng(m + pos)
+    q = rng.standard_normal((m, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((m, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((m, nkv * hd)).astype(np.float32)
+    cos, sin, dc, ds = rope_dev(10000.0, hd, S)
+    a, b = Cache(nkv, S, hd), Cache(nkv, S, hd)
+    _fill_cache(a, S, seed=3)
+    _fill_cache(b, S, seed=3)
+    qt, kt, vt = (torch.from_numpy(x).to(DEV) for x in (q, k, v))
+    out = torch.empty((m, nh * hd), device=DEV)
+    bl.check(bl.lib.btl_rope_append_attention(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), m, nh, ctypes.byref(a.c),
+                                              pos, None, dc.data_ptr(), ds.data_ptr(), out.data_ptr(), None, 0,
+                                              stream()))
+    qr = torch.empty_like(qt)
+    bl.check(bl.lib.btl_rope_kv_append(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), m, nh, ctypes.byref(b.c), pos,
+                                       None, dc.data_ptr(), ds.data_ptr(), qr.data_ptr(), stream()))
+    out2 = torch.empty_like(out)
+    bl.check(bl.lib.btl_attention(qr.data_ptr(), m, nh, ctypes.byref(b.c), pos, None, out2.data_ptr(), None, 0,
+                                  stream()))
+    assert torch.equal(a.k, b.k) and torch.equal(a.vs, b.vs)
+    assert_same(out, out2.cpu().numpy(), "two-call path")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_embedding(dtype):
     vocab, dim = 1000, 320
@@ -197,34 +257,68 @@ def test_greedy_next():
     assert log.cpu().tolist() == [-1, -1, -1, -1, -1, 3, 3, 3]  # log[8] is outside: not written
 
 
-@pytest.mark.parametrize("m,k", [(1, 256), (3, 4096), (70, 512)])
-def test_add_rmsnorm_linear_group(m, k):
+@pytest.mark.parametrize("m,k,ns", [(1, 256, (96, 40)), (1, 4096, (96, 40)), (1, 4096, (8192, 96)),
+                                    (3, 4096, (96, 40)), (70, 512, (96, 40))])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_add_rmsnorm_linear_group(m, k, ns, inplace):
+    # (1, 4096, (8192, 96)): 518 row blocks, over the limit for the fused decode prologue
+    print("add_rmsnorm", m, k, ns, inplace, flush=True)
     rng = np.random.default_rng(m + k)
     h = rng.standard_normal((m, k)).astype(np.float32)
     d = rng.standard_normal((m, k)).astype(np.float32)
     g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
     layers = []
-    for i, n in enumerate((96, 40)):
+    for i, n in enumerate(ns):
         wb, sw = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
         layers.append((bl.PackedTensor(torch.from_numpy(wb).to(DEV), sw, (n, k), DEV), wb, sw, n))
     ht, dt, gt = (torch.from_numpy(a).to(DEV) for a in (h, d, g))
+    ho = ht if inplace else torch.full_like(ht, 5.0)
     outs = [torch.empty((m, n), device=DEV) for (_, _, _, n) in layers]
     cs = [L[0].as_c() for L in layers]
     arr = (ctypes.POINTER(bl.BtlPacked) * 2)(*[ctypes.pointer(c) for c in cs])
     ys = (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs])
-    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 2, ht.data_ptr(), dt.data_ptr(), gt.data_ptr(), 1e-5, m,
-                                                 k, bl.BTL_F32, None, 0, stream()))
+    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 2, ht.data_ptr(), dt.data_ptr(), ho.data_ptr(),
+                                                 gt.data_ptr(), 1e-5, m, k, bl.BTL_F32, None, 0, stream()))
     hs = (h + d).astype(np.float32)
-    assert_same(ht, hs, "residual")
+    assert_same(ho, hs, "residual")
+    if not inplace:
+        assert_same(ht, h, "input untouched")
     xn = orc.rmsnorm(hs, g, 1e-5)
     for o, (_, wb, sw, n) in zip(outs, layers):
         assert_same(o, orc.forward_i8(xn, wb, n, sw)[0], "layer")
-    # delta = NULL: RMSNorm of h only, h untouched
+    # delta = NULL: RMSNorm of h only, nothing written
     h2 = torch.from_numpy(h).to(DEV)
-    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 2, h2.data_ptr(), None, gt.data_ptr(), 1e-5, m, k,
+    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 2, h2.data_ptr(), None, None, gt.data_ptr(), 1e-5, m, k,
                                                  bl.BTL_F32, None, 0, stream()))
     assert_same(h2, h, "h untouched")
-    assert_same(outs[0], orc.forward_i8(orc.rmsnorm(h, g, 1e-5), layers[0][1], 96, layers[0][2])[0], "plain")
+    assert_same(outs[0], orc.forward_i8(orc.rmsnorm(h, g, 1e-5), layers[0][1], ns[0], layers[0][2])[0], "plain")
+
+
+@pytest.mark.parametrize("k", [512, 4096, 14336])
+def test_swiglu_group_one_token_fused(k):
+    # m = 1, f32: the SwiGLU runs inside the decode kernel's prologue
+    rng = np.random.default_rng(k)
+    gte = (rng.standard_normal((1, k)) * 3).astype(np.float32)
+    up = rng.standard_normal((1, k)).astype(np.float32)
+    n = 200
+    wb, sw = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), sw, (n, k), DEV)
+    y = bl.swiglu_linear_group([pt], torch.from_numpy(gte).to(DEV), torch.from_numpy(up).to(DEV))[0]
+    assert_same(y, orc.forward_i8(orc.swiglu(gte, up), wb, n, sw)[0], "swiglu fused")
+
+
+def test_add_rmsnorm_rejects_partial_overlap():
+    k = 256
+    h = torch.zeros((2, k), device=DEV)
+    pt = bl.PackedTensor(torch.zeros((16 * k // 4,), dtype=torch.uint8, device=DEV), 1.0, (16, k), DEV)
+    c = pt.as_c()
+    arr = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(c))
+    y = torch.empty((2, 16), device=DEV)
+    ys = (ctypes.c_void_p * 1)(y.data_ptr())
+    g = torch.ones(k, device=DEV)
+    st = bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 1, h.data_ptr(), h.data_ptr(), h[1].data_ptr(), g.data_ptr(),
+                                             1e-5, 2, k, bl.BTL_F32, None, 0, stream())
+    assert st == bl.BTL_ERR_LAYOUT
 
 
 # --- the decoder end to end ----------------------------------------------------
