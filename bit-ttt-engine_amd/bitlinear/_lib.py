@@ -35,7 +35,8 @@ EXPORTS = (
     # include/bitllama.h
     "btl_rope_table", "btl_rope_kv_append", "btl_attention_workspace_bytes", "btl_attention",
     "btl_rope_append_attention",
-    "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm_linear_group",
+    "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm_linear_group", "btl_add_rmsnorm_swiglu",
+    "btl_add_rmsnorm_swiglu_workspace_bytes",
 )
 
 
@@ -97,6 +98,8 @@ def _load():
         "btl_greedy_next": (i32, [vp, i64, vp, vp, vp, i64, vp]),
         "btl_add_rmsnorm_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, vp, vp, f32, i64, i64, i32, vp,
                                                sz, vp]),
+        "btl_add_rmsnorm_swiglu": (i32, [P(BtlPacked), P(BtlPacked), vp, vp, vp, vp, f32, i64, i64, vp, vp, sz, vp]),
+        "btl_add_rmsnorm_swiglu_workspace_bytes": (sz, [i64, i64, i64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

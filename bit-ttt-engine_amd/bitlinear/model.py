@@ -14,14 +14,15 @@ Mapping of the block onto the C ABI (one row of activations per token, f32 betwe
   RoPE(q, k); cache.append(k, v);
   attn = softmax(q k^T / sqrt(d)) v                      btl_rope_append_attention
   o = BitLinear_o(attn)                                  btl_linear_group
-  x' = x + o; gate, up = BitLinear(RMSNorm2(x'))         btl_add_rmsnorm_linear_group
-  mlp_out = BitLinear_down(silu(gate) * up)              btl_swiglu_linear_group
+  x' = x + o; hs = silu(W1 RMSNorm2(x')) * W3 RMSNorm2(x')  btl_add_rmsnorm_swiglu
+  mlp_out = BitLinear_down(hs)                           btl_linear_group
 and after the last block logits = lm_head(RMSNorm_f(x' + mlp_out)) in one more
 btl_add_rmsnorm_linear_group.  The residual stream alternates between two
 buffers (each add writes the other one), so for a one-token step the add +
-norm and the SwiGLU can run inside the contraction kernel's prologue (the
-library does so for launches of up to 512 workgroups).  Every linear is a
-BitLinear (W1.58-A8), the lm_head included.
+norm can run inside the contraction kernel's prologue (the library does so for
+launches of up to 512 workgroups), and the gate/up kernel writes silu(gate) * up
+from its epilogue.  Every linear is a BitLinear (W1.58-A8), the lm_head
+included.
 
 Deliberate differences from the reference, all on the host side:
   * the prompt is prefilled as one batch of rows (the reference feeds it token by
@@ -118,8 +119,7 @@ class BitLlamaHip:
         self.v = torch.zeros((M, c.n_kv_heads * c.head_dim), **f32)
         self.attn = torch.zeros((M, c.n_heads * c.head_dim), **f32)
         self.o = torch.zeros((M, c.hidden), **f32)
-        self.gate = torch.zeros((M, c.intermediate), **f32)
-        self.up = torch.zeros((M, c.intermediate), **f32)
+        self.hs = torch.zeros((M, c.intermediate), **f32)  # silu(gate) * up
         self.down = torch.zeros((M, c.hidden), **f32)
         self.logits = torch.zeros((1, c.vocab), **f32)
         self.ids = torch.zeros((M,), dtype=torch.int32, device=self.dev)
@@ -139,14 +139,14 @@ class BitLlamaHip:
         for L in weights["layers"]:
             qkv_c, qkv = _arr([L["q"], L["k"], L["v"]])
             o_c, o = _arr([L["o"]])
-            gu_c, gu = _arr([L["gate"], L["up"]])
+            gate_c, up_c = L["gate"].as_c(), L["up"].as_c()
             d_c, d = _arr([L["down"]])
-            self._layers.append(dict(keep=(qkv_c, o_c, gu_c, d_c), qkv=qkv, o=o, gu=gu, down=d,
+            self._layers.append(dict(keep=(qkv_c, o_c, d_c), qkv=qkv, o=o, down=d,
+                                     gate=ctypes.byref(gate_c), up=ctypes.byref(up_c), gate_c=gate_c, up_c=up_c,
                                      n1=L["norm1"].data_ptr(), n2=L["norm2"].data_ptr()))
         self._head_c, self._head = _arr([weights["lm_head"]])
         self._y_qkv = _ptrs([self.q, self.k, self.v])
         self._y_o = _ptrs([self.o])
-        self._y_gu = _ptrs([self.gate, self.up])
         self._y_down = _ptrs([self.down])
         self._y_logits = _ptrs([self.logits])
         self.pos = 0
@@ -180,11 +180,11 @@ class BitLlamaHip:
                                                 self.rope_sin.data_ptr(), self.attn.data_ptr(), None, 0, st))
             check(lib.btl_linear_group(L["o"], self._y_o, 1, self.attn.data_ptr(), BTL_F32, m,
                                        c.n_heads * c.head_dim, BTL_F32, None, 0, st))
-            check(lib.btl_add_rmsnorm_linear_group(L["gu"], self._y_gu, 2, cur.data_ptr(), self.o.data_ptr(),
-                                                   nxt.data_ptr(), L["n2"], c.eps, m, hid, BTL_F32, None, 0, st))
+            check(lib.btl_add_rmsnorm_swiglu(L["gate"], L["up"], cur.data_ptr(), self.o.data_ptr(), nxt.data_ptr(),
+                                             L["n2"], c.eps, m, hid, self.hs.data_ptr(), None, 0, st))
             cur, nxt = nxt, cur
-            check(lib.btl_swiglu_linear_group(L["down"], self._y_down, 1, self.gate.data_ptr(), self.up.data_ptr(),
-                                              BTL_F32, m, c.intermediate, BTL_F32, None, 0, st))
+            check(lib.btl_linear_group(L["down"], self._y_down, 1, self.hs.data_ptr(), BTL_F32, m, c.intermediate,
+                                       BTL_F32, None, 0, st))
         last = m - 1
         check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, cur[last].data_ptr(),
                                                self.down[last].data_ptr(), None, self.w["norm_f"].data_ptr(), c.eps,

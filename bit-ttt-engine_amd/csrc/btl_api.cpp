@@ -268,8 +268,11 @@ struct Xform {
 // With a transform (xf), the transform + quantisation runs first into the
 // workspace on every route (k % 64 == 0 and aligned inputs are checked by the
 // caller) and the decode kernel reads the operand-order rows.
+// swiglu_out (decode route only; the caller checks it): two layers of equal n,
+// silu(y0) * y1 written by the decode kernel's epilogue, y[i] may be NULL.
 int run_i8(const Layer* layers, int count, const void* x, int xkind, const float* xs, int64_t m,
-           int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st, const Xform* xf = nullptr)
+           int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st, const Xform* xf = nullptr,
+           float* swiglu_out = nullptr)
 {
     int dev;
     int rc = current_device(&dev);
@@ -315,6 +318,10 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     int rbw = 1;
     const int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k, &rbw) : 0;
     const bool dec = wv > 0;
+    if (swiglu_out) {
+        if (!dec || wv > 8) return fail(BTL_ERR_ARG, "SwiGLU epilogue needs the decode route");
+        rbw = 2;  // workgroup w: row block w of gate and of up
+    }
     const bool bat = !dec && m <= env_int("BTL_GEMV_BAT_MAX_M", 32) && m <= 64 && env_int("BTL_GEMV_BAT", 1) != 0;
     int split_steps = 0, splits = 1;
     if (!dec)
@@ -395,6 +402,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             a.eps = xf->eps;
             a.hout = xf->hout;
         }
+        a.swiglu_out = swiglu_out;
         e = btl::launch_gemv_dec(a, pre ? (int)btl::XK_I8O : xkind, xform, st);
         if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
         return BTL_OK;
@@ -734,6 +742,61 @@ int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, i
     const Xform xf{delta ? btl::XF_ADD_RMSNORM : btl::XF_RMSNORM, delta, g, eps, delta ? h_out : nullptr};
     return run_i8(ls, count, h, btl::XK_F32, nullptr, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws,
                   ws_bytes, (hipStream_t)stream, &xf);
+}
+
+int btl_add_rmsnorm_swiglu(const btl_packed_t* w_gate, const btl_packed_t* w_up, const float* h,
+                           const float* delta, float* h_out, const float* g, float eps, int64_t m, int64_t k,
+                           float* out, void* ws, size_t ws_bytes, void* stream)
+{
+    const btl_packed_t* w[2] = {w_gate, w_up};
+    void* ydummy[2] = {out, out};
+    Layer ls[2];
+    int rc;
+    if ((rc = check_group(w, ydummy, 2, m, k, BTL_F32, ls))) return rc;
+    if (w_gate->n != w_up->n)
+        return fail(BTL_ERR_SHAPE, "gate and up have %lld and %lld rows", (long long)w_gate->n, (long long)w_up->n);
+    if ((rc = check_fused_shape(k, 65536, "fused residual + RMSNorm"))) return rc;
+    const int64_t n = w_gate->n;
+    if (m == 0 || n == 0) return BTL_OK;
+    if (!h || !g || !out) return fail(BTL_ERR_LAYOUT, "null residual, norm weight or output");
+    if (!aligned16(h) || !aligned16(g) || (delta && !aligned16(delta)) || (delta && h_out && !aligned16(h_out)))
+        return fail(BTL_ERR_LAYOUT, "h, delta, h_out and g must be 16-byte aligned");
+    if (delta && h_out && h_out != h) {
+        const uintptr_t a0 = (uintptr_t)h, a1 = (uintptr_t)h_out, nb = (uintptr_t)(m * k * 4);
+        if (a0 < a1 + nb && a1 < a0 + nb) return fail(BTL_ERR_LAYOUT, "h_out overlaps h without being h");
+    }
+    if (m > INT32_MAX / 2 || n * m > ((int64_t)1 << 40)) return fail(BTL_ERR_SHAPE, "dimension too large");
+    const Xform xf{delta ? btl::XF_ADD_RMSNORM : btl::XF_RMSNORM, delta, g, eps, delta ? h_out : nullptr};
+    int rbw = 1;
+    const bool dec = env_int("BTL_GEMV_DEC", 1) != 0 && dec_waves(m, k, &rbw) > 0 && dec_waves(m, k, &rbw) <= 8;
+    const hipStream_t st = (hipStream_t)stream;
+    if (dec) {
+        // the decode kernel writes silu(gate) * up from its epilogue
+        ls[0].y = nullptr;
+        ls[1].y = nullptr;
+        return run_i8(ls, 2, h, btl::XK_F32, nullptr, m, k, btl::YK_F32, ws, ws_bytes, st, &xf, out);
+    }
+    // many rows: gate and up into workspace scratch, then the elementwise SwiGLU
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    const size_t inner = btl_workspace_bytes(m, 2 * n, k, BTL_ACT_I8);
+    const size_t ybytes = align_up((size_t)(m * n * 4), 256);
+    void* wsp = nullptr;
+    if ((rc = get_ws(dev, ws, ws_bytes, inner + 2 * ybytes, &wsp))) return rc;
+    float* yg = (float*)((uint8_t*)wsp + inner);
+    float* yu = (float*)((uint8_t*)wsp + inner + ybytes);
+    ls[0].y = yg;
+    ls[1].y = yu;
+    if ((rc = run_i8(ls, 2, h, btl::XK_F32, nullptr, m, k, btl::YK_F32, wsp, inner, st, &xf))) return rc;
+    hipError_t e = btl::launch_swiglu_f32(yg, yu, m * n, out, st);
+    if (e != hipSuccess) return hip_fail(e, "swiglu kernel launch");
+    return BTL_OK;
+}
+
+size_t btl_add_rmsnorm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k)
+{
+    if (m < 0 || n < 0 || k < 0) return 0;
+    return btl_workspace_bytes(m, 2 * n, k, BTL_ACT_I8) + 2 * align_up((size_t)(m * n * 4), 256);
 }
 
 int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* gate,

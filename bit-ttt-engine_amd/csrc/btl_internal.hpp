@@ -48,6 +48,10 @@ struct GemvArgs {
     const float* g;
     float eps;
     float* hout;
+    // SwiGLU epilogue (swiglu.rs:29-35): layers 0 (gate) and 1 (up) of equal n,
+    // tiles == 2; workgroup w computes row block w of both and writes
+    // silu(gate) * up to swiglu_out [m, n] f32 (the layers' y may be NULL)
+    float* swiglu_out;
 };
 
 // Decode (k_gemv_dec): parts * tiles <= 16, parts * kpart >= k, kpart <= 2048,
@@ -180,6 +184,9 @@ struct DecKv {
     float* vsc_w;
 };
 hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t st);
+
+// out[i] = silu(g[i]) * u[i], silu(v) = v / (1 + exp(-v)) (swiglu.rs:29-35), f32
+hipError_t launch_swiglu_f32(const float* g, const float* u, int64_t n, float* out, hipStream_t st);
 
 hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
                         float* out, hipStream_t st);

@@ -257,7 +257,7 @@ struct DecXf {
     static constexpr int kGroups = XF == XF_NONE ? kDecGroups : (XF == XF_SWIGLU ? 2 : 1);
 };
 
-template <int XK, int ST, int MT, int XF>
+template <int XK, int ST, int MT, int XF, bool PAIR>
 __global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArgs a)
 {
     const int WV = a.parts, RB = a.tiles;  // NW = WV * RB <= 16 waves
@@ -270,7 +270,12 @@ __global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArg
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rbi = wave / WV, part = wave - rbi * WV;
-    const int rbg = blockIdx.x * RB + rbi;  // past rb_total: no rows (zero loads, no stores)
+    // PAIR (SwiGLU epilogue): rbi 0 is gate's row block w, rbi 1 up's.  A
+    // template parameter, so the plain launch's first weight address needs no
+    // extra kernel-argument load.
+    constexpr bool paired = PAIR;
+    const int rbg = paired ? (rbi == 0 ? 0 : a.p[1].rb_begin) + (int)blockIdx.x
+                           : (int)blockIdx.x * RB + rbi;  // past rb_total: no rows (zero loads, no stores)
     const int mt = MT == 1 ? 1 : min(MT, a.m);
 
     const uint8_t* W = a.p[0].w;
@@ -485,14 +490,45 @@ __global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArg
     if (WV > 1) {
         if (part > 0) s_red[wave][lane] = res;
         __syncthreads();
-        if (part > 0) return;
-        for (int p = 1; p < WV; ++p) res += s_red[wave + p][lane];
+        if (part > 0 && !paired) return;
+        if (part == 0)
+            for (int p = 1; p < WV; ++p) res += s_red[wave + p][lane];
     }
     const float sx = MT == 1 ? s_l : __shfl(s_l, mcol < mt ? mcol : 0, 64);
-    if (!m_ok) return;
     const float c = __fmul_rn(sx, SW);
     const bool ybf = a.ykind == YK_BF16;
     const int nb = row0 + 4 * (lane >> 4);
+    if (paired) {
+        // gate's part-0 wave hands its outputs to up's through LDS (every wave
+        // reaches the barrier), which writes silu(gate) * up
+        float* s_gate = (float*)s_red;  // [16 rows][4 token columns], free after the K-part sum
+        __syncthreads();
+        if (part == 0 && rbi == 0 && m_ok) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) s_gate[(nb - row0 + v) * 4 + mcol] = __fmul_rn((float)res[v], c);
+        }
+        __syncthreads();
+        if (part != 0 || !m_ok) return;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int n = nb + v;
+            if (n < N) {
+                const int64_t o = (int64_t)mcol * N + n;
+                const float yv = __fmul_rn((float)res[v], c);
+                if (Y) {
+                    if (ybf) ((uint16_t*)Y)[o] = f32_to_bf16(yv);
+                    else ((float*)Y)[o] = yv;
+                }
+                if (ACC) ACC[o] = res[v];
+                if (rbi == 1) {
+                    const float gv = s_gate[(nb - row0 + v) * 4 + mcol];
+                    a.swiglu_out[o] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, btl_expf(-gv))), yv);
+                }
+            }
+        }
+        return;
+    }
+    if (!m_ok) return;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int n = nb + v;
@@ -513,6 +549,9 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
     if (wv < 1 || rb < 1 || wv * rb > 16 || st_need > 8 || a.m < 1 || a.m > 4 ||
         (int64_t)wv * a.kpart < a.k || (int64_t)a.m * (a.k >> 4) > (int64_t)kDecGroups * wv * rb * 64)
         return hipErrorInvalidValue;
+    if (a.swiglu_out && (a.nprob != 2 || a.p[0].n != a.p[1].n || rb != 2 || a.p[1].rb_begin != (a.p[0].n + 15) / 16 ||
+                         a.rb_total != 2 * a.p[1].rb_begin))
+        return hipErrorInvalidValue;
     if (xform != XF_NONE &&
         (xkind != XK_F32 || a.m != 1 || wv * rb > 8 || !a.x2 == (xform == XF_ADD_RMSNORM || xform == XF_SWIGLU) ||
          ((xform == XF_RMSNORM || xform == XF_ADD_RMSNORM) && (!a.g || (a.k >> 4) > wv * rb * 64)) ||
@@ -522,24 +561,38 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
     const size_t lds = (size_t)a.m * (size_t)(a.k + 16);
     const bool st4 = st_need <= 4;
     const bool mt1 = a.m == 1;
-#define BTL_DEC_XF(XFV)                                                                               \
-    if (xform == XFV) {                                                                               \
-        if (st4) hipLaunchKernelGGL((k_gemv_dec<XK_F32, 4, 1, XFV>), grid, block, lds, s, a);         \
-        else hipLaunchKernelGGL((k_gemv_dec<XK_F32, 8, 1, XFV>), grid, block, lds, s, a);             \
-        return hipGetLastError();                                                                     \
+    const bool pr = a.swiglu_out != nullptr;
+#define BTL_DEC_XF(XFV)                                                                                     \
+    if (xform == XFV) {                                                                                     \
+        if (pr) {                                                                                           \
+            if (st4) hipLaunchKernelGGL((k_gemv_dec<XK_F32, 4, 1, XFV, true>), grid, block, lds, s, a);     \
+            else hipLaunchKernelGGL((k_gemv_dec<XK_F32, 8, 1, XFV, true>), grid, block, lds, s, a);         \
+        } else {                                                                                            \
+            if (st4) hipLaunchKernelGGL((k_gemv_dec<XK_F32, 4, 1, XFV, false>), grid, block, lds, s, a);    \
+            else hipLaunchKernelGGL((k_gemv_dec<XK_F32, 8, 1, XFV, false>), grid, block, lds, s, a);        \
+        }                                                                                                   \
+        return hipGetLastError();                                                                           \
     }
     BTL_DEC_XF(XF_RMSNORM) BTL_DEC_XF(XF_ADD_RMSNORM) BTL_DEC_XF(XF_SWIGLU)
 #undef BTL_DEC_XF
-#define BTL_DEC_CASE(XKV)                                                                             \
-    if (xkind == XKV) {                                                                               \
-        if (st4 && mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 1, XF_NONE>), grid, block, lds, s, a); \
-        else if (st4) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 4, XF_NONE>), grid, block, lds, s, a);   \
-        else if (mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 1, XF_NONE>), grid, block, lds, s, a);   \
-        else hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 4, XF_NONE>), grid, block, lds, s, a);            \
-        return hipGetLastError();                                                                     \
+#define BTL_DEC_MT(XKV, PRV)                                                                                    \
+    if (st4 && mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 1, XF_NONE, PRV>), grid, block, lds, s, a);          \
+    else if (st4) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 4, XF_NONE, PRV>), grid, block, lds, s, a);            \
+    else if (mt1) hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 1, XF_NONE, PRV>), grid, block, lds, s, a);            \
+    else hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 4, XF_NONE, PRV>), grid, block, lds, s, a);
+    if (pr) {  // the SwiGLU epilogue's inputs: f32 tokens or the operand-order int8 of a separate transform
+        if (xkind == XK_F32) { BTL_DEC_MT(XK_F32, true) return hipGetLastError(); }
+        if (xkind == XK_I8O) { BTL_DEC_MT(XK_I8O, true) return hipGetLastError(); }
+        return hipErrorInvalidValue;
+    }
+#define BTL_DEC_CASE(XKV)                     \
+    if (xkind == XKV) {                       \
+        BTL_DEC_MT(XKV, false)                \
+        return hipGetLastError();             \
     }
     BTL_DEC_CASE(XK_BF16) BTL_DEC_CASE(XK_F32) BTL_DEC_CASE(XK_I8) BTL_DEC_CASE(XK_I8O)
 #undef BTL_DEC_CASE
+#undef BTL_DEC_MT
     return hipErrorInvalidValue;
 }
 

@@ -23,6 +23,8 @@
 // the CPU oracle (oracle/bitllama_oracle.c) restates the same operations.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "btl_device.hpp"
 #include "btl_internal.hpp"
 
@@ -502,6 +504,26 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st)
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)a.m, (unsigned)a.nh), dim3(64), 0, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_swiglu_f32: silu(g) * u elementwise (swiglu.rs:29-35), candle's silu
+// v / (1 + exp(-v)) with btl_expf; the route for many token rows
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_swiglu_f32(const float* g, const float* u, int64_t n, float* out)
+{
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float v = g[i];
+        out[i] = __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, btl_expf(-v))), u[i]);
+    }
+}
+
+hipError_t launch_swiglu_f32(const float* g, const float* u, int64_t n, float* out, hipStream_t st)
+{
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_swiglu_f32, dim3((unsigned)blocks), dim3(256), 0, st, g, u, n, out);
     return hipGetLastError();
 }
 

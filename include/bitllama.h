@@ -140,6 +140,21 @@ int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, i
                                  const float* delta, float* h_out, const float* g, float eps, int64_t m, int64_t k,
                                  int ydtype, void* ws, size_t ws_bytes, void* stream);
 
+/*
+ * The gate/up half of SwiGLU::forward (swiglu.rs:29-35) after the residual add
+ * and RMSNorm of btl_add_rmsnorm_linear_group: out = silu(xn W1^T) * (xn W3^T),
+ * xn = RMSNorm(h + delta) * g, silu(v) = v / (1 + exp(-v)), out [m, n] f32 --
+ * the input of the down projection.  w_gate, w_up: [n, k] packed, equal n.
+ * Same bits as btl_add_rmsnorm_linear_group into two f32 outputs followed by
+ * the elementwise SwiGLU; for up to 4 rows the decode kernel computes the pair
+ * and writes silu(gate) * up from its epilogue (no gate / up tensors).
+ * ws: btl_add_rmsnorm_swiglu_workspace_bytes (or NULL: the library's).
+ */
+int btl_add_rmsnorm_swiglu(const btl_packed_t* w_gate, const btl_packed_t* w_up, const float* h,
+                           const float* delta, float* h_out, const float* g, float eps, int64_t m, int64_t k,
+                           float* out, void* ws, size_t ws_bytes, void* stream);
+size_t btl_add_rmsnorm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
 #ifdef __cplusplus
 }
 #endif

@@ -294,6 +294,36 @@ def test_add_rmsnorm_linear_group(m, k, ns, inplace):
     assert_same(outs[0], orc.forward_i8(orc.rmsnorm(h, g, 1e-5), layers[0][1], ns[0], layers[0][2])[0], "plain")
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 256, 512), (1, 4096, 14336), (2, 512, 96), (4, 4096, 1000),
+                                   (9, 512, 256), (70, 256, 512)])
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_add_rmsnorm_swiglu(m, k, n, with_delta):
+    # decode rows (m <= 4): the gate/up kernel writes silu(gate) * up from its epilogue;
+    # (1, 4096, 14336) takes the separate norm kernel (1792 row blocks), the small ones fuse it
+    print("add_rmsnorm_swiglu", m, k, n, with_delta, flush=True)
+    rng = np.random.default_rng(m * 31 + k + n)
+    h = rng.standard_normal((m, k)).astype(np.float32)
+    d = rng.standard_normal((m, k)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    wg, sg = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    wu, su = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    pg = bl.PackedTensor(torch.from_numpy(wg).to(DEV), sg, (n, k), DEV)
+    pu = bl.PackedTensor(torch.from_numpy(wu).to(DEV), su, (n, k), DEV)
+    ht, dt, gt = (torch.from_numpy(a).to(DEV) for a in (h, d, g))
+    ho = torch.zeros_like(ht)
+    out = torch.full((m, n), 9.0, device=DEV)
+    cg, cu = pg.as_c(), pu.as_c()
+    bl.check(bl.lib.btl_add_rmsnorm_swiglu(ctypes.byref(cg), ctypes.byref(cu), ht.data_ptr(),
+                                           dt.data_ptr() if with_delta else None, ho.data_ptr() if with_delta else None,
+                                           gt.data_ptr(), 1e-5, m, k, out.data_ptr(), None, 0, stream()))
+    hs = (h + d).astype(np.float32) if with_delta else h
+    if with_delta:
+        assert_same(ho, hs, "residual")
+    xn = orc.rmsnorm(hs, g, 1e-5)
+    e = orc.swiglu(orc.forward_i8(xn, wg, n, sg)[0], orc.forward_i8(xn, wu, n, su)[0])
+    assert_same(out, e, "swiglu")
+
+
 @pytest.mark.parametrize("k", [512, 4096, 14336])
 def test_swiglu_group_one_token_fused(k):
     # m = 1, f32: the SwiGLU runs inside the decode kernel's prologue
