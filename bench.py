@@ -275,6 +275,8 @@ def run_decode(args):
         result["pack"] = run_pack(gen, dev)
     if args.e2e:
         result["e2e"] = run_e2e(layers, gen, dev, args)
+    if args.adaptive:
+        result["adaptive"] = run_adaptive(gen, dev, args)
     if args.cpu_baseline:
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         host = []
@@ -485,6 +487,69 @@ def run_e2e(layers, gen, dev, args):
             "first_tokens": [int(t) for t in toks[:8]]}
 
 
+def run_adaptive(gen, dev, args):
+    """The multi-base adaptive format (AdaptiveBitLinear, adaptive_linear.rs) with the
+    reference converter's default of 3 bases (convert_llama_v2.py --n-bases 3), on the
+    Llama-3-8B MLP gate shape 4096 -> 14336: 32 distinct layers of interleaved bytes
+    (44 MB each, random codes, ~1/3 zeros), split once on the device
+    (btl_adaptive_split), then W1.58-A8 btl_adaptive_linear at M=1 (the 32 calls
+    back to back in a HIP graph) and at M=2048.  Algorithmic bytes at M=1: the 3
+    bases' packed bytes + x (bf16) + y (bf16)."""
+    nb, n, k = 3, INTER, HIDDEN
+    layers = []
+    for _ in range(LAYERS):
+        codes = torch.randint(0, 3, (n * (k // 4) * nb, 4), generator=gen, device=dev, dtype=torch.uint8)
+        packed = (codes[:, 0] | (codes[:, 1] << 2) | (codes[:, 2] << 4) | (codes[:, 3] << 6)).contiguous()
+        del codes
+        scales = [0.02, 0.007, 0.0025]
+        layers.append(bl.AdaptiveBitLinear.load(k, n, packed, scales))
+        del packed
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    x1 = synth_act(1, k, gen, dev)
+    y1 = torch.empty((1, n), **bf)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(L, x, y, st):
+        if L._c is None:
+            L.forward(x)  # binds the C arrays
+        bl.check(bl.lib.btl_adaptive_linear(L._c[1], nb, x.data_ptr(), bl.BTL_BF16, x.shape[0], k, y.data_ptr(),
+                                            bl.BTL_BF16, None, 0, st))
+    for L in layers:
+        call(L, x1, y1, stream)
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            s2 = torch.cuda.current_stream().cuda_stream
+            for L in layers:
+                call(L, x1, y1, s2)
+    torch.cuda.synchronize()
+    g.replay()
+    reps = 10
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us1 = 1000.0 * e0.elapsed_time(e1) / (reps * LAYERS)
+    b1 = nb * n * k // 4 + k * 2 + n * 2
+    M = args.prefill_m
+    xm = synth_act(M, k, gen, dev)
+    ym = torch.empty((M, n), **bf)
+    usm = time_launches(lambda st: call(layers[0], xm, ym, st), 10, cap)
+    ops = 2.0 * M * n * k * nb
+    print("bench: adaptive nb=3 decode %.2f us, prefill %.1f us" % (us1, usm), file=sys.stderr, flush=True)
+    return {"workload": "multi-base adaptive format, 3 bases, 4096 -> 14336 (Llama-3-8B gate), W1.58-A8, bf16 in/out; "
+                        "split once on the device, then btl_adaptive_linear (one grouped launch over the bases + "
+                        "the ordered base sum)",
+            "decode_m1_us": round(us1, 2), "decode_bytes": b1, "decode_GB_s": round(b1 / us1 / 1e3, 1),
+            "decode_frac_hbm": round(b1 / us1 / 1e3 / HBM_PEAK_GBS, 3),
+            "prefill_m": M, "prefill_us": round(usm, 2), "prefill_TOPS": round(ops / usm / 1e6, 1),
+            "prefill_frac_int8": round(ops / usm / 1e6 / INT8_PEAK_TOPS, 3)}
+
+
 def run_pack(gen, dev):
     """PackedTensor::pack on the device (btl_pack_device) of one f32 weight of the
     MLP up shape 14336 x 4096: the load-time quantisation a checkpoint loader
@@ -560,6 +625,8 @@ def main():
                     help="counter-run mode: --steps launches of one workload and a 256 MiB copy; no JSON")
     ap.add_argument("--no-e2e", dest="e2e", action="store_false",
                     help="skip the cfg5 end-to-end decoder section of the JSON line")
+    ap.add_argument("--no-adaptive", dest="adaptive", action="store_false",
+                    help="skip the multi-base adaptive-format section of the JSON line")
     ap.add_argument("--e2e-prompt", type=int, default=512)
     ap.add_argument("--e2e-tokens", type=int, default=256)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)

@@ -21,3 +21,4 @@ from .layer import (  # noqa: F401
     BitLinear, BitLinearHip, Workspace, linear_group, linear_i8, linear_i8_op, quantize_act,
     quantize_act_op, rmsnorm_linear_group, swiglu_linear_group,
 )
+from .adaptive import AdaptiveBitLinear, reconstruct_dense, split_bases  # noqa: F401,E402

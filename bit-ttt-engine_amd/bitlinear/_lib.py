@@ -32,6 +32,7 @@ EXPORTS = (
     "btl_linear_i8", "btl_linear_group", "btl_quantize_act_op", "btl_linear_i8_op",
     "btl_rmsnorm_linear_group", "btl_swiglu_linear_group",
     "btl_workspace_bytes", "btl_workspace_clear",
+    "btl_adaptive_split", "btl_adaptive_reconstruct", "btl_adaptive_linear", "btl_adaptive_workspace_bytes",
     # include/bitllama.h
     "btl_rope_table", "btl_rope_kv_append", "btl_attention_workspace_bytes", "btl_attention",
     "btl_rope_append_attention",
@@ -89,6 +90,10 @@ def _load():
         "btl_swiglu_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, i32, i64, i64, i32, vp, sz, vp]),
         "btl_workspace_bytes": (sz, [i64, i64, i64, i32]),
         "btl_workspace_clear": (i32, [vp, sz, vp]),
+        "btl_adaptive_split": (i32, [vp, i64, i64, i32, P(vp), vp]),
+        "btl_adaptive_reconstruct": (i32, [vp, P(f32), i32, i64, i64, vp, vp]),
+        "btl_adaptive_linear": (i32, [P(P(BtlPacked)), i32, vp, i32, i64, i64, vp, i32, vp, sz, vp]),
+        "btl_adaptive_workspace_bytes": (sz, [i64, i64, i64, i32]),
         "btl_rope_table": (i32, [ctypes.c_double, i64, i64, vp, vp]),
         "btl_rope_kv_append": (i32, [vp, vp, vp, i64, i64, P(BtlKvQ8), i64, vp, vp, vp, vp, vp]),
         "btl_attention_workspace_bytes": (sz, [i64, i64, P(BtlKvQ8)]),

@@ -799,6 +799,101 @@ size_t btl_add_rmsnorm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k)
     return btl_workspace_bytes(m, 2 * n, k, BTL_ACT_I8) + 2 * align_up((size_t)(m * n * 4), 256);
 }
 
+int btl_adaptive_split(const uint8_t* packed, int64_t n, int64_t k, int nb, uint8_t* const* out, void* stream)
+{
+    if (nb < 1 || nb > btl::kMaxBases) return fail(BTL_ERR_ARG, "number of bases %d not in 1..%d", nb, btl::kMaxBases);
+    if (n < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    if (k % 4 != 0) return fail(BTL_ERR_SHAPE, "in_features %lld is not a multiple of 4", (long long)k);
+    if (n * (k / 4) == 0) return BTL_OK;
+    if (!packed || !out) return fail(BTL_ERR_LAYOUT, "null pointer");
+    btl::AdaptiveOut o;
+    memset(&o, 0, sizeof(o));
+    for (int b = 0; b < nb; ++b) {
+        if (!out[b] || ((uintptr_t)out[b] & 3u)) return fail(BTL_ERR_LAYOUT, "base %d output null or not 4-byte aligned", b);
+        o.p[b] = out[b];
+    }
+    int dev, rc;
+    if ((rc = current_device(&dev))) return rc;
+    hipError_t e = btl::launch_adaptive_split(packed, n, k, nb, o, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "adaptive split kernel launch");
+    return BTL_OK;
+}
+
+int btl_adaptive_reconstruct(const uint8_t* packed, const float* scales, int nb, int64_t n, int64_t k, float* out,
+                             void* stream)
+{
+    if (nb < 1 || nb > btl::kMaxBases) return fail(BTL_ERR_ARG, "number of bases %d not in 1..%d", nb, btl::kMaxBases);
+    if (n < 0 || k < 0) return fail(BTL_ERR_SHAPE, "negative size");
+    if (k % 4 != 0) return fail(BTL_ERR_SHAPE, "in_features %lld is not a multiple of 4", (long long)k);
+    if (n * k == 0) return BTL_OK;
+    if (!packed || !scales || !out) return fail(BTL_ERR_LAYOUT, "null pointer");
+    if (!aligned16(out)) return fail(BTL_ERR_LAYOUT, "out must be 16-byte aligned");
+    btl::AdaptiveScales sc;
+    memset(&sc, 0, sizeof(sc));
+    for (int b = 0; b < nb; ++b) sc.s[b] = scales[b];
+    int dev, rc;
+    if ((rc = current_device(&dev))) return rc;
+    hipError_t e = btl::launch_adaptive_reconstruct(packed, n, k, nb, sc, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "adaptive reconstruct kernel launch");
+    return BTL_OK;
+}
+
+size_t btl_adaptive_workspace_bytes(int64_t m, int64_t n, int64_t k, int nb)
+{
+    if (m < 0 || n < 0 || k < 0 || nb < 1 || nb > btl::kMaxBases) return 0;
+    const int chunk = nb < btl::kMaxGroup ? nb : btl::kMaxGroup;
+    return btl_workspace_bytes(m, chunk * n, k, BTL_ACT_I8) + (size_t)nb * align_up((size_t)(m * n * 4), 256);
+}
+
+int btl_adaptive_linear(const btl_packed_t* const* bases, int nb, const void* x, int xdtype, int64_t m, int64_t k,
+                        void* y, int ydtype, void* ws, size_t ws_bytes, void* stream)
+{
+    if (nb < 1 || nb > btl::kMaxBases) return fail(BTL_ERR_ARG, "number of bases %d not in 1..%d", nb, btl::kMaxBases);
+    if (!bases) return fail(BTL_ERR_ARG, "null base array");
+    int rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_dtype(ydtype, "output"))) return rc;
+    for (int b = 0; b < nb; ++b) {
+        if ((rc = check_packed(bases[b], m, k))) return rc;
+        if (bases[b]->n != bases[0]->n)
+            return fail(BTL_ERR_SHAPE, "base %d has %lld rows, base 0 %lld", b, (long long)bases[b]->n,
+                        (long long)bases[0]->n);
+    }
+    const int64_t n = bases[0]->n;
+    if (m == 0 || n == 0) return BTL_OK;
+    if (!x || !y) return fail(BTL_ERR_LAYOUT, "null input or output");
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    const int chunk = nb < btl::kMaxGroup ? nb : btl::kMaxGroup;
+    const size_t inner = btl_workspace_bytes(m, chunk * n, k, BTL_ACT_I8);
+    const size_t ybytes = align_up((size_t)(m * n * 4), 256);
+    void* wsp = nullptr;
+    if ((rc = get_ws(dev, ws, ws_bytes, inner + (size_t)nb * ybytes, &wsp))) return rc;
+    const hipStream_t st = (hipStream_t)stream;
+    btl::AdaptiveSum sum;
+    memset(&sum, 0, sizeof(sum));
+    // every base's f32 output y_b = (float)acc_b * (s_x * s_b), up to kMaxGroup bases per launch
+    for (int b0 = 0; b0 < nb; b0 += btl::kMaxGroup) {
+        const int cnt = nb - b0 < btl::kMaxGroup ? nb - b0 : btl::kMaxGroup;
+        Layer ls[btl::kMaxGroup];
+        for (int i = 0; i < cnt; ++i) {
+            float* yb = (float*)((uint8_t*)wsp + inner + (size_t)(b0 + i) * ybytes);
+            ls[i] = Layer{bases[b0 + i], yb, nullptr};
+            sum.ys[b0 + i] = yb;
+        }
+        if ((rc = run_i8(ls, cnt, x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k, btl::YK_F32, wsp,
+                         inner, st)))
+            return rc;
+    }
+    // y = y_0 + y_1 + ... in base order
+    sum.nb = nb;
+    sum.count = m * n;
+    sum.y = y;
+    sum.ykind = ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32;
+    hipError_t e = btl::launch_base_sum(sum, st);
+    if (e != hipSuccess) return hip_fail(e, "base sum kernel launch");
+    return BTL_OK;
+}
+
 int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int count, const void* gate,
                             const void* up, int xdtype, int64_t m, int64_t k, int ydtype, void* ws,
                             size_t ws_bytes, void* stream)

@@ -188,6 +188,28 @@ hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t
 // out[i] = silu(g[i]) * u[i], silu(v) = v / (1 + exp(-v)) (swiglu.rs:29-35), f32
 hipError_t launch_swiglu_f32(const float* g, const float* u, int64_t n, float* out, hipStream_t st);
 
+// Multi-base adaptive format (adaptive_linear.rs): at most kMaxBases bases (the
+// reference's loader tries 1..=8, adaptive_linear.rs:56).
+constexpr int kMaxBases = 8;
+struct AdaptiveOut {
+    uint8_t* p[kMaxBases];  // base b's PackedTensor bytes [n, k/4]
+};
+struct AdaptiveScales {
+    float s[kMaxBases];
+};
+struct AdaptiveSum {
+    const float* ys[kMaxBases];  // per-base outputs [count] f32
+    int nb;
+    int64_t count;
+    void* y;
+    int ykind;
+};
+hipError_t launch_adaptive_split(const uint8_t* packed, int64_t n, int64_t k, int nb, const AdaptiveOut& out,
+                                 hipStream_t st);
+hipError_t launch_adaptive_reconstruct(const uint8_t* packed, int64_t n, int64_t k, int nb, const AdaptiveScales& sc,
+                                       float* out, hipStream_t st);
+hipError_t launch_base_sum(const AdaptiveSum& a, hipStream_t st);
+
 hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
                         float* out, hipStream_t st);
 hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,

@@ -528,6 +528,105 @@ hipError_t launch_swiglu_f32(const float* g, const float* u, int64_t n, float* o
 }
 
 // ---------------------------------------------------------------------------
+// Multi-base adaptive format (AdaptiveBitLinear, adaptive_linear.rs:51-160)
+// ---------------------------------------------------------------------------
+// The reference's weight_packed [n, k/4, nb] interleaves the bases per column
+// pack (byte (r, cp, b) at (r * k/4 + cp) * nb + b, convert_llama_v2.py:111-151).
+// k_adaptive_split copies base b's bytes into a PackedTensor array [n, k/4]
+// (same 2-bit codes and bit positions), so every base runs through the
+// BitLinear kernels; one thread per 4 column packs of one row.
+__global__ __launch_bounds__(256) void k_adaptive_split(const uint8_t* packed, int64_t total, int nb,
+                                                        AdaptiveOut out)
+{
+    // byte f of base b is packed[f * nb + b] over the flattened [n * k/4] index;
+    // unit u = 4 consecutive f (one 32-bit store per base), the last < 4 by bytes
+    const int64_t units = total >> 2;
+    for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u <= units; u += (int64_t)gridDim.x * 256) {
+        const uint8_t* src = packed + u * 4 * nb;
+        if (u < units) {
+            for (int b = 0; b < nb; ++b) {
+                const uint32_t v = (uint32_t)src[b] | ((uint32_t)src[nb + b] << 8) |
+                                   ((uint32_t)src[2 * nb + b] << 16) | ((uint32_t)src[3 * nb + b] << 24);
+                ((uint32_t*)out.p[b])[u] = v;
+            }
+        } else {
+            for (int64_t f = 4 * u; f < total; ++f)
+                for (int b = 0; b < nb; ++b) out.p[b][f] = packed[f * nb + b];
+        }
+    }
+}
+
+hipError_t launch_adaptive_split(const uint8_t* packed, int64_t n, int64_t k, int nb, const AdaptiveOut& out,
+                                 hipStream_t st)
+{
+    const int64_t total = n * (k / 4);
+    if (total <= 0) return hipSuccess;
+    if (nb < 1 || nb > kMaxBases) return hipErrorInvalidValue;
+    const int64_t blocks = std::min<int64_t>(((total >> 2) + 256) / 256, 8192);
+    hipLaunchKernelGGL(k_adaptive_split, dim3((unsigned)blocks), dim3(256), 0, st, packed, total, nb, out);
+    return hipGetLastError();
+}
+
+// AdaptiveBitLinear::load's dense reconstruction (adaptive_linear.rs:86-117):
+// w[r][4cp + j] = ((0 + t_0 s_0) + t_1 s_1) + ..., bases in order, f32.
+__global__ __launch_bounds__(256) void k_adaptive_reconstruct(const uint8_t* packed, int64_t cps, int nb,
+                                                              AdaptiveScales sc, float* out)
+{
+    for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < cps; u += (int64_t)gridDim.x * 256) {
+        float w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int b = 0; b < nb; ++b) {
+            const uint32_t byte = packed[u * nb + b];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t c = (byte >> (2 * j)) & 3u;
+                const float v = c == 1u ? 1.0f : (c == 2u ? -1.0f : 0.0f);
+                w[j] = __fadd_rn(w[j], __fmul_rn(v, sc.s[b]));
+            }
+        }
+        ((float4*)out)[u] = make_float4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+hipError_t launch_adaptive_reconstruct(const uint8_t* packed, int64_t n, int64_t k, int nb, const AdaptiveScales& sc,
+                                       float* out, hipStream_t st)
+{
+    const int64_t cps = n * (k / 4);
+    if (cps <= 0) return hipSuccess;
+    if (nb < 1 || nb > kMaxBases) return hipErrorInvalidValue;
+    const int64_t blocks = std::min<int64_t>((cps + 255) / 256, 8192);
+    hipLaunchKernelGGL(k_adaptive_reconstruct, dim3((unsigned)blocks), dim3(256), 0, st, packed, cps, nb, sc, out);
+    return hipGetLastError();
+}
+
+// y = ys[0] + ys[1] + ... (f32, in base order), stored f32 or bf16
+__device__ __forceinline__ uint16_t bf16_rne(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__global__ __launch_bounds__(256) void k_base_sum(AdaptiveSum a)
+{
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < a.count; i += (int64_t)gridDim.x * 256) {
+        float v = a.ys[0][i];
+        for (int b = 1; b < a.nb; ++b) v = __fadd_rn(v, a.ys[b][i]);
+        if (a.ykind == YK_BF16) ((uint16_t*)a.y)[i] = bf16_rne(v);
+        else ((float*)a.y)[i] = v;
+    }
+}
+
+hipError_t launch_base_sum(const AdaptiveSum& a, hipStream_t st)
+{
+    if (a.count <= 0) return hipSuccess;
+    if (a.nb < 1 || a.nb > kMaxBases) return hipErrorInvalidValue;
+    const int64_t blocks = std::min<int64_t>((a.count + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_base_sum, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // k_embed: candle_nn::Embedding::forward (llama.rs:208) -> f32 rows
 // ---------------------------------------------------------------------------
 // grid (m), block 256.  An id outside [0, vocab) gives a zero row (the

@@ -225,6 +225,34 @@ int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int co
                             size_t ws_bytes, void* stream);
 
 /*
+ * Multi-base adaptive format: AdaptiveBitLinear (layers/adaptive_linear.rs:51-160).
+ * The reference stores weight_packed [n, k/4, nb] u8 -- byte (r, c, b) holds the
+ * codes of base b for columns 4c..4c+3, bits and codes as PackedTensor
+ * (tools/conversion/convert_llama_v2.py:111-151) -- and scales [nb] f32, and
+ * reconstructs dense f32 weights at load time (adaptive_linear.rs:86-117).
+ * nb in 1..8 (the loader's range, adaptive_linear.rs:56); k % 4 == 0.
+ *
+ * btl_adaptive_split: load-time repack of the interleaved bytes (device) into
+ *   nb PackedTensor byte arrays out[b] [n, k/4] (device, 4-byte aligned), so each
+ *   base is an ordinary btl_packed_t {out[b], n, k, scales[b]}.  For nb == 1 the
+ *   bytes are unchanged.
+ * btl_adaptive_reconstruct: the reference's dense weights on the device,
+ *   out[r][4c + j] = ((0 + t_0 s_0) + t_1 s_1) + ... (f32, bases in order), for
+ *   callers that want its fp32 matmul semantics.  scales: host array [nb].
+ * btl_adaptive_linear: W1.58-A8 over the split bases (build-defined; no
+ *   reference counterpart): the activations quantised once per launch as
+ *   btl_linear, acc_b exact per base, y = (float)acc_0 (s_x s_0) + (float)acc_1
+ *   (s_x s_1) + ... in base order.  bases: nb btl_packed_t of equal shape.
+ *   ws: btl_adaptive_workspace_bytes (or NULL: the library's).
+ */
+int btl_adaptive_split(const uint8_t* packed, int64_t n, int64_t k, int nb, uint8_t* const* out, void* stream);
+int btl_adaptive_reconstruct(const uint8_t* packed, const float* scales, int nb, int64_t n, int64_t k, float* out,
+                             void* stream);
+int btl_adaptive_linear(const btl_packed_t* const* bases, int nb, const void* x, int xdtype, int64_t m, int64_t k,
+                        void* y, int ydtype, void* ws, size_t ws_bytes, void* stream);
+size_t btl_adaptive_workspace_bytes(int64_t m, int64_t n, int64_t k, int nb);
+
+/*
  * Workspace bytes needed by btl_linear / btl_linear_i8 / btl_linear_group (and
  * the fused RMSNorm / SwiGLU groups) for this shape and mode (for btl_linear_group pass n = sum of the layers' n):
  * scratch for the quantised activations.  Its contents between calls do not

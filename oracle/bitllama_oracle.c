@@ -36,6 +36,11 @@
  *                    pins the result against a float64 softmax-attention.
  *   orc_argmax       the greedy pick of Llama::stream_completion (llama.rs:509-515):
  *                    Iterator::max_by(partial_cmp) returns the LAST maximum
+ *   orc_adaptive_reconstruct  AdaptiveBitLinear::load (adaptive_linear.rs:86-117): the
+ *                    dense f32 weights of the multi-base format, bases added in order
+ *   orc_adaptive_split        the interleaved [n, k/4, nb] bytes -> nb PackedTensor arrays
+ *   orc_adaptive_forward_i8   W1.58-A8 over the bases (build-defined; the reference runs
+ *                    a dense f32 matmul of the reconstruction, adaptive_linear.rs:131-160)
  */
 #include <math.h>
 #include <stdint.h>
@@ -161,4 +166,74 @@ int64_t orc_argmax(const float* x, int64_t n)
     for (int64_t i = 1; i < n; ++i)
         if (!(x[i] < x[best])) best = i;  /* max_by keeps the later of equal elements */
     return best;
+}
+
+/* ------------------------------------------------------------------ */
+/* Multi-base adaptive format (AdaptiveBitLinear, adaptive_linear.rs)  */
+/* ------------------------------------------------------------------ */
+/* weight_packed [n, k/4, nb] u8 (adaptive_linear.rs:60, producer
+ * convert_llama_v2.py:111-151): byte (row, cp, b) holds the 2-bit codes of
+ * base b for columns 4cp..4cp+3 at bits 2j; scales [nb] f32. */
+
+static float orc_lut(int code) { return code == 1 ? 1.0f : (code == 2 ? -1.0f : 0.0f); }
+
+/* AdaptiveBitLinear::load's dense reconstruction (adaptive_linear.rs:86-117):
+ * per row, bases in order, row_w[4cp + j] += LUT[byte][j] * scale[b]. */
+void orc_adaptive_reconstruct(const uint8_t* packed, const float* scales, int64_t nb, int64_t n, int64_t k, float* out)
+{
+    const int64_t kp = k / 4;
+    for (int64_t r = 0; r < n; ++r) {
+        float* w = out + r * k;
+        for (int64_t c = 0; c < k; ++c) w[c] = 0.0f;
+        for (int64_t b = 0; b < nb; ++b) {
+            const float s = scales[b];
+            for (int64_t cp = 0; cp < kp; ++cp) {
+                const uint8_t byte = packed[r * kp * nb + cp * nb + b];
+                for (int j = 0; j < 4; ++j) w[cp * 4 + j] += orc_lut((byte >> (2 * j)) & 3) * s;
+            }
+        }
+    }
+}
+
+/* The interleaved bytes -> nb standard PackedTensor byte arrays [n, k/4] each. */
+void orc_adaptive_split(const uint8_t* packed, int64_t nb, int64_t n, int64_t k, uint8_t* out)
+{
+    const int64_t kp = k / 4;
+    for (int64_t b = 0; b < nb; ++b)
+        for (int64_t r = 0; r < n; ++r)
+            for (int64_t cp = 0; cp < kp; ++cp) out[b * n * kp + r * kp + cp] = packed[r * kp * nb + cp * nb + b];
+}
+
+void orc_quantize_act(const float* x, int64_t m, int64_t k, int8_t* q, float* s);
+void orc_contract_i8(const int8_t* q, int64_t m, int64_t k, const uint8_t* w, int64_t n, int32_t* acc);
+
+/* W1.58-A8 multi-base forward (build-defined): the activations quantised as
+ * for BitLinear, acc_b = sum_k q * t_b exact per base, and
+ * y = (float)acc_0 * (s_x * s_0) + (float)acc_1 * (s_x * s_1) + ... in base order. */
+int orc_adaptive_forward_i8(const float* x, int64_t m, int64_t k, const uint8_t* packed, const float* scales,
+                            int64_t nb, int64_t n, float* y)
+{
+    const int64_t kp = k / 4;
+    int8_t* q = (int8_t*)malloc((size_t)(m * k) + 1);
+    float* sx = (float*)malloc(sizeof(float) * (size_t)(m + 1));
+    int32_t* acc = (int32_t*)malloc(sizeof(int32_t) * (size_t)(m * n + 1));
+    uint8_t* split = (uint8_t*)malloc((size_t)(nb * n * kp) + 1);
+    if (!q || !sx || !acc || !split) return 1;
+    orc_quantize_act(x, m, k, q, sx);
+    orc_adaptive_split(packed, nb, n, k, split);
+    for (int64_t b = 0; b < nb; ++b) {
+        orc_contract_i8(q, m, k, split + b * n * kp, n, acc);
+        for (int64_t i = 0; i < m; ++i) {
+            const float c = sx[i] * scales[b];
+            for (int64_t j = 0; j < n; ++j) {
+                const float v = (float)acc[i * n + j] * c;
+                y[i * n + j] = b == 0 ? v : y[i * n + j] + v;
+            }
+        }
+    }
+    free(q);
+    free(sx);
+    free(acc);
+    free(split);
+    return 0;
 }

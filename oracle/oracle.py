@@ -46,6 +46,9 @@ def _load():
         "orc_q8_dequant": (None, [vp, i64, f32, vp]),
         "orc_attn_decode": (None, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp]),
         "orc_argmax": (i64, [vp, i64]),
+        "orc_adaptive_reconstruct": (None, [vp, vp, i64, i64, i64, vp]),
+        "orc_adaptive_split": (None, [vp, i64, i64, i64, vp]),
+        "orc_adaptive_forward_i8": (i32, [vp, i64, i64, vp, vp, i64, i64, vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -268,3 +271,35 @@ def argmax(x):
     """Greedy pick of stream_completion (llama.rs:509-515): the last maximum."""
     x = _f32(x).reshape(-1)
     return int(lib.orc_argmax(_p(x), x.size))
+
+
+# ---------------------------------------------------------------------------
+# multi-base adaptive format (adaptive_linear.rs)
+# ---------------------------------------------------------------------------
+def adaptive_reconstruct(packed, scales, n, k):
+    """AdaptiveBitLinear::load's dense f32 weights [n, k] (adaptive_linear.rs:86-117)."""
+    packed = np.ascontiguousarray(packed, np.uint8).reshape(-1)
+    scales = _f32(scales).reshape(-1)
+    out = np.zeros((n, k), dtype=np.float32)
+    lib.orc_adaptive_reconstruct(_p(packed), _p(scales), scales.size, n, k, _p(out))
+    return out
+
+
+def adaptive_split(packed, nb, n, k):
+    """[n, k/4, nb] interleaved bytes -> [nb, n * k/4] PackedTensor byte arrays."""
+    packed = np.ascontiguousarray(packed, np.uint8).reshape(-1)
+    out = np.zeros((nb, n * (k // 4)), dtype=np.uint8)
+    lib.orc_adaptive_split(_p(packed), nb, n, k, _p(out))
+    return out
+
+
+def adaptive_forward_i8(x, packed, scales, n):
+    """W1.58-A8 multi-base forward: y = sum_b (float)acc_b * (s_x * s_b) in base order."""
+    x = _f32(x)
+    m, k = x.shape
+    scales = _f32(scales).reshape(-1)
+    y = np.zeros((m, n), dtype=np.float32)
+    rc = lib.orc_adaptive_forward_i8(_p(x), m, k, _p(np.ascontiguousarray(packed, np.uint8).reshape(-1)), _p(scales),
+                                     scales.size, n, _p(y))
+    assert rc == 0
+    return y

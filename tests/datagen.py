@@ -40,3 +40,31 @@ def ternary(data, numel):
     b = np.asarray(data, np.uint8)
     codes = np.stack([(b >> (2 * i)) & 3 for i in range(4)], axis=1).reshape(-1)[:numel]
     return ((codes & 1).astype(np.int8) - (codes >> 1).astype(np.int8)).astype(np.int8)
+
+
+def rvq_bases(w, nb):
+    """The reference converter's residual ternary decomposition (quantize_adaptive_basis,
+    tools/conversion/convert_llama_v2.py:28-72), restated in numpy to produce test
+    weights of the multi-base format: scale = mean|R| (1.0 below 1e-9), t =
+    clamp(round_half_even(R / scale), -1, 1), R -= t * scale.  -> (t [nb, n, k] int8,
+    scales [nb] float32)."""
+    r = np.asarray(w, np.float32).copy()
+    ts, ss = [], []
+    for _ in range(nb):
+        s = np.float32(np.abs(r, dtype=np.float32).mean(dtype=np.float64))
+        if s < 1e-9:
+            s = np.float32(1.0)
+        t = np.clip(np.round(r / s), -1, 1).astype(np.int8)
+        r = (r - t.astype(np.float32) * s).astype(np.float32)
+        ts.append(t)
+        ss.append(s)
+    return np.stack(ts), np.array(ss, np.float32)
+
+
+def pack_interleaved_2bit(t):
+    """pack_2bit (convert_llama_v2.py:111-151): ternary [nb, n, k] -> [n, k/4, nb] bytes,
+    codes (v + 3) % 3 (-1 -> 2), column 4c + j at bits 2j."""
+    nb, n, k = t.shape
+    codes = ((t.astype(np.int16) + 3) % 3).astype(np.uint8)       # [nb, n, k]
+    c = codes.transpose(1, 2, 0).reshape(n, k // 4, 4, nb)          # [n, k/4, 4, nb]
+    return np.ascontiguousarray(c[:, :, 0] | (c[:, :, 1] << 2) | (c[:, :, 2] << 4) | (c[:, :, 3] << 6), np.uint8)
