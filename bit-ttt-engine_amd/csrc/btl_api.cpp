@@ -316,8 +316,33 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     // measured on MI355X: the GEMM is faster from m = 64, Llama-3-8B MLP
     // shapes) and GEMM: K split over workgroups when the output has few tiles.
     int rbw = 1;
-    const int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k, &rbw) : 0;
+    int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k, &rbw) : 0;
     const bool dec = wv > 0;
+    // One token row, k a multiple of 64 up to 16384: the row-contiguous form
+    // (whole weight rows per wave, 1 KB per load instruction, no K parts).
+    // Measured on MI355X for k >= 4096 (Llama-3-8B decode shapes).
+    const int rowc = dec && m == 1 && k % 64 == 0 && k >= env_int("BTL_DEC_ROW_MIN_K", 4096) && k <= 16384 &&
+                             env_int("BTL_DEC_ROW", 1) != 0
+                         ? (k <= 4096 ? 1 : (k <= 8192 ? 2 : 4))
+                         : 0;
+    if (rowc) {
+        // rows per wave: 4 (2 for k > 8192), so 4 KB (8 KB) of loads per wave
+        // in workgroups of one row block (measured on MI355X against 8 and 16
+        // rows per wave and 2..7 row blocks per workgroup); BTL_DEC_ROW_RPW /
+        // BTL_DEC_ROW_RB override them (tuning; launches with a fused
+        // transform keep the default)
+        int rpw = btl::dec_row_st(rowc) / rowc;
+        rbw = 1;
+        const int rpw_env = env_int("BTL_DEC_ROW_RPW", 0), rb_env = env_int("BTL_DEC_ROW_RB", 0);
+        if (!xf && (rpw_env == 1 || rpw_env == 2 || rpw_env == 4 || rpw_env == 8 || rpw_env == 16)) {
+            rpw = rpw_env;
+            while (rowc * rpw > 16) rpw >>= 1;
+            while (rowc * rpw < 4) rpw <<= 1;
+            rbw = 16 / rpw >= 4 ? 1 : rpw / 4;
+        }
+        wv = 16 / rpw;
+        if (!xf && rb_env >= 1 && rb_env * wv <= 16 && rb_env * wv >= 4) rbw = rb_env;
+    }
     if (swiglu_out) {
         if (!dec || wv > 8) return fail(BTL_ERR_ARG, "SwiGLU epilogue needs the decode route");
         rbw = 2;  // workgroup w: row block w of gate and of up
@@ -403,6 +428,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             a.hout = xf->hout;
         }
         a.swiglu_out = swiglu_out;
+        a.rowc = rowc;
         e = btl::launch_gemv_dec(a, pre ? (int)btl::XK_I8O : xkind, xform, st);
         if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
         return BTL_OK;

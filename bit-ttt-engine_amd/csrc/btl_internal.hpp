@@ -52,7 +52,16 @@ struct GemvArgs {
     // tiles == 2; workgroup w computes row block w of both and writes
     // silu(gate) * up to swiglu_out [m, n] f32 (the layers' y may be NULL)
     float* swiglu_out;
+    // row-contiguous form (m == 1, k % 64 == 0): 0 = K parts; 1, 2, 4 = whole
+    // rows of up to that many 4096-weight chunks, 16 / parts rows per wave
+    // (parts in {1, 2, 4, 8}, chunks * 16 / parts loads of 1 KB per wave in
+    // {4, 8, 16}; kpart unused)
+    int rowc;
 };
+
+// Loads per wave of the row-contiguous form by default: 4 rows of 1 KB (one
+// chunk), 4 rows of 2 KB (two), 2 rows of up to 4 KB (four).
+constexpr int dec_row_st(int rowc) { return rowc == 1 ? 4 : 8; }
 
 // Decode (k_gemv_dec): parts * tiles <= 16, parts * kpart >= k, kpart <= 2048,
 // a.m <= 4, a.m * k / 16 <= kDecGroups * 64 * parts * tiles.

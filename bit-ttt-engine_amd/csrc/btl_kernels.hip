@@ -257,14 +257,34 @@ struct DecXf {
     static constexpr int kGroups = XF == XF_NONE ? kDecGroups : (XF == XF_SWIGLU ? 2 : 1);
 };
 
-template <int XK, int ST, int MT, int XF, bool PAIR>
-__global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArgs a)
+// Threads per workgroup a decode instantiation is compiled for: up to 16
+// waves (128 registers per lane); 8 with a fused transform or 16 loads per
+// wave in flight (256 registers per lane).
+constexpr int dec_threads(int st, int xf, int ni)
 {
-    const int WV = a.parts, RB = a.tiles;  // NW = WV * RB <= 16 waves
+    return xf != XF_NONE ? 512 : (ni > 0 && st > 8 ? 512 : 1024);
+}
+
+template <int XK, int ST, int MT, int XF, bool PAIR, int NI = 0>
+__global__ __launch_bounds__(dec_threads(ST, XF, NI)) void k_gemv_dec(GemvArgs a)
+{
+    // NI > 0: the row-contiguous form (one token row, k <= NI * 4096).  Wave
+    // `part` of a row block owns RPW = ST / NI whole rows, part + WV * rho
+    // (rows interleaved over the waves, measured faster than consecutive
+    // rows); its load t reads 1 KB of its row t / NI (chunk t % NI, lane l:
+    // bytes 16l..16l+15), so one
+    // load instruction covers 8 full 128-byte lines.  The activation operand
+    // of MFMA word h is the 16 quantised values at k = 4096c + 64l + 16h, the
+    // same for every row: the 16x16 product's diagonal D[i][i] sums lanes i,
+    // i+16, i+32, i+48 of the row, and the row's dot product is the trace.
+    // No K parts, so no cross-wave reduction.
+    static_assert(NI == 0 || (MT == 1 && ST % NI == 0), "row-contiguous form: one token row");
+    constexpr int RPW = NI > 0 ? ST / NI : 1;
+    const int WV = NI > 0 ? 16 / RPW : a.parts, RB = a.tiles;  // NW = WV * RB <= 16 waves
     const int NW = WV * RB, NT = NW * 64;
     extern __shared__ __align__(16) uint8_t sq[];  // [mt][k + 16], operand order
     __shared__ uint32_t s_amax[16][MT];
-    __shared__ v4i s_red[16][64];
+    __shared__ v4i s_red[NI > 0 ? 1 : 16][64];  // K-part sums; the row-contiguous form stages gate outputs only
     __shared__ float s_ss[16];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -304,7 +324,9 @@ __global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArg
     constexpr bool PREQ = DecX<XK>::kPreq;
     const int gpr = K >> 4;  // groups per token row
     const int ng = mt * gpr;
-    constexpr int DG = DecXf<XF>::kGroups;
+    // the row-contiguous form launches at least 256 threads: NI groups per
+    // thread cover k <= NI * 4096
+    constexpr int DG = NI > 0 && XF == XF_NONE ? NI : DecXf<XF>::kGroups;
     int gm_[DG], gc_[DG];
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(mt * K * ES));
     uint4 xv[DG][NV];
@@ -336,11 +358,21 @@ __global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArg
     const int row0 = (rbg - RB0) * 16;
     const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, N - row0)));
     const int rb_bytes = K >> 2;
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(W + (int64_t)row0 * rb_bytes, (uint32_t)(rows * rb_bytes));
     uint4 buf[ST];
+    if (NI > 0) {
+        // rows row0 + part * RPW + [0, RPW) of this row block, chunks past the row read zeros
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(W + (int64_t)row0 * rb_bytes, (uint32_t)(rows * rb_bytes));
 #pragma unroll
-    for (int j = 0; j < ST; ++j)
-        buf[j] = bload(wr, j * kStepWeights + kq * 64 < len ? r * rb_bytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
+        for (int j = 0; j < ST; ++j) {
+            const int rho = j / (NI > 0 ? NI : 1), c = j - rho * (NI > 0 ? NI : 1);
+            buf[j] = bload(wr, c * 1024 + 16 * lane < rb_bytes ? (part + WV * rho) * rb_bytes + c * 1024 + 16 * lane : kOOB);
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(W + (int64_t)row0 * rb_bytes, (uint32_t)(rows * rb_bytes));
+#pragma unroll
+        for (int j = 0; j < ST; ++j)
+            buf[j] = bload(wr, j * kStepWeights + kq * 64 < len ? r * rb_bytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
+    }
 
     // 3. absmax of each token row over the workgroup; lane m then holds the
     //    quantisation parameters of token row m
@@ -464,6 +496,69 @@ __global__ __launch_bounds__(XF == XF_NONE ? 1024 : 512) void k_gemv_dec(GemvArg
     }
     __syncthreads();
 
+    if constexpr (NI > 0) {
+        // 5. row-contiguous contraction, row by row (one accumulator, the
+        //    rows interleave in the schedule); 6. the trace of each
+        //    row's product: lane l holds D[4(l/16) + v][l % 16], so D[i][i] is
+        //    register l % 4 of lane l when (l / 4) % 4 == l / 16 (lanes 0-3,
+        //    20-23, 40-43, 60-63); exact int32 sums.  Lanes past the row's end
+        //    read the activation at k = 0 (their weights are zero).
+        const bool diag = ((lane >> 2) & 3) == (lane >> 4);
+        int sv = 0;
+#pragma unroll
+        for (int rho = 0; rho < RPW; ++rho) {
+            v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < NI; ++c) {
+                const int ko = c * 4096 + 64 * lane;
+                const uint8_t* bj = sq + (ko < K ? ko : 0);
+                const v4i b0 = *(const v4i*)(bj + 0);
+                const v4i b1 = *(const v4i*)(bj + 16);
+                const v4i b2 = *(const v4i*)(bj + 32);
+                const v4i b3 = *(const v4i*)(bj + 48);
+                const uint4 cur = buf[rho * NI + c];
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc, 0, 0, 0);
+            }
+            const v4i t = acc;
+            int d = (lane & 2) ? ((lane & 1) ? t.w : t.z) : ((lane & 1) ? t.y : t.x);
+            d = diag ? d : 0;
+            d += __builtin_amdgcn_update_dpp(d, d, 0xB1, 0xF, 0xF, false);  // quad [1,0,3,2]
+            d += __builtin_amdgcn_update_dpp(d, d, 0x4E, 0xF, 0xF, false);  // quad [2,3,0,1]
+            const int s = __builtin_amdgcn_readlane(d, 0) + __builtin_amdgcn_readlane(d, 20) +
+                          __builtin_amdgcn_readlane(d, 40) + __builtin_amdgcn_readlane(d, 60);
+            sv = lane == rho ? s : sv;
+        }
+        // lane rho stores row row0 + part + WV * rho
+        const int n = row0 + part + WV * lane;
+        const bool own = lane < RPW && n < N;
+        const float yv = __fmul_rn((float)sv, __fmul_rn(s_l, SW));
+        if (paired) {
+            // gate's wave hands its outputs to the up wave of the same rows
+            float* s_gate = (float*)s_red;
+            if (rbi == 0 && own) s_gate[part + WV * lane] = yv;
+            __syncthreads();
+            if (!own) return;
+            if (Y) {
+                if (a.ykind == YK_BF16) ((uint16_t*)Y)[n] = f32_to_bf16(yv);
+                else ((float*)Y)[n] = yv;
+            }
+            if (ACC) ACC[n] = sv;
+            if (rbi == 1) {
+                const float gv = s_gate[part + WV * lane];
+                a.swiglu_out[n] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, btl_expf(-gv))), yv);
+            }
+            return;
+        }
+        if (!own) return;
+        if (a.ykind == YK_BF16) ((uint16_t*)Y)[n] = f32_to_bf16(yv);
+        else ((float*)Y)[n] = yv;
+        if (ACC) ACC[n] = sv;
+        return;
+    }
+
     // 5. contraction.  B lanes of token columns >= mt read row 0: those
     //    columns of D are never stored.
     const int mcol = lane & 15;
@@ -546,8 +641,8 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
 {
     const int wv = a.parts, rb = a.tiles;
     const int st_need = (a.kpart + kStepWeights - 1) / kStepWeights;
-    if (wv < 1 || rb < 1 || wv * rb > 16 || st_need > 8 || a.m < 1 || a.m > 4 ||
-        (int64_t)wv * a.kpart < a.k || (int64_t)a.m * (a.k >> 4) > (int64_t)kDecGroups * wv * rb * 64)
+    if (wv < 1 || rb < 1 || wv * rb > 16 || (a.rowc == 0 && (st_need > 8 || (int64_t)wv * a.kpart < a.k)) ||
+        a.m < 1 || a.m > 4 || (int64_t)a.m * (a.k >> 4) > (int64_t)kDecGroups * wv * rb * 64)
         return hipErrorInvalidValue;
     if (a.swiglu_out && (a.nprob != 2 || a.p[0].n != a.p[1].n || rb != 2 || a.p[1].rb_begin != (a.p[0].n + 15) / 16 ||
                          a.rb_total != 2 * a.p[1].rb_begin))
@@ -559,9 +654,50 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.rb_total + rb - 1) / rb)), block((unsigned)(wv * rb * 64));
     const size_t lds = (size_t)a.m * (size_t)(a.k + 16);
+    const bool pr = a.swiglu_out != nullptr;
+    if (a.rowc != 0) {
+        // (chunks, waves per row block) -> loads per wave ST = chunks * 16 / waves
+        const int ni = a.rowc;
+        const int st = wv > 0 ? ni * 16 / wv : 0;
+        if ((ni != 1 && ni != 2 && ni != 4) || a.m != 1 || a.k % 64 != 0 || a.k > ni * 4096 || 16 % wv != 0 ||
+            (st != 4 && st != 8 && st != 16) || wv * rb * 64 > dec_threads(st, xform, ni) || wv * rb < 4 ||
+            (xform != XF_NONE && st != dec_row_st(ni)))
+            return hipErrorInvalidValue;
+#define BTL_ROW_ST(XKV, XFV, PRV, NIV)                                                                     \
+    if (st == 4) hipLaunchKernelGGL((k_gemv_dec<XKV, 4, 1, XFV, PRV, NIV>), grid, block, lds, s, a);       \
+    else if (st == 8) hipLaunchKernelGGL((k_gemv_dec<XKV, 8, 1, XFV, PRV, NIV>), grid, block, lds, s, a);  \
+    else hipLaunchKernelGGL((k_gemv_dec<XKV, 16, 1, XFV, PRV, NIV>), grid, block, lds, s, a);
+#define BTL_ROW_NI(XKV, XFV, PRV)             \
+    if (ni == 1) { BTL_ROW_ST(XKV, XFV, PRV, 1) } \
+    else if (ni == 2) { BTL_ROW_ST(XKV, XFV, PRV, 2) } \
+    else { BTL_ROW_ST(XKV, XFV, PRV, 4) }
+        if (xform != XF_NONE) {  // the default rows per wave only
+#define BTL_ROW_XF(XFV)                                                                                      \
+    if (ni == 1) hipLaunchKernelGGL((k_gemv_dec<XK_F32, 4, 1, XFV, false, 1>), grid, block, lds, s, a);      \
+    else if (ni == 2) hipLaunchKernelGGL((k_gemv_dec<XK_F32, 8, 1, XFV, false, 2>), grid, block, lds, s, a); \
+    else hipLaunchKernelGGL((k_gemv_dec<XK_F32, 8, 1, XFV, false, 4>), grid, block, lds, s, a);
+            if (pr) return hipErrorInvalidValue;
+            if (xform == XF_RMSNORM) { BTL_ROW_XF(XF_RMSNORM) }
+            else if (xform == XF_ADD_RMSNORM) { BTL_ROW_XF(XF_ADD_RMSNORM) }
+            else { BTL_ROW_XF(XF_SWIGLU) }
+#undef BTL_ROW_XF
+            return hipGetLastError();
+        }
+        if (pr) {
+            if (xkind == XK_F32) { BTL_ROW_NI(XK_F32, XF_NONE, true) return hipGetLastError(); }
+            if (xkind == XK_I8O) { BTL_ROW_NI(XK_I8O, XF_NONE, true) return hipGetLastError(); }
+            return hipErrorInvalidValue;
+        }
+        if (xkind == XK_BF16) { BTL_ROW_NI(XK_BF16, XF_NONE, false) return hipGetLastError(); }
+        if (xkind == XK_F32) { BTL_ROW_NI(XK_F32, XF_NONE, false) return hipGetLastError(); }
+        if (xkind == XK_I8) { BTL_ROW_NI(XK_I8, XF_NONE, false) return hipGetLastError(); }
+        if (xkind == XK_I8O) { BTL_ROW_NI(XK_I8O, XF_NONE, false) return hipGetLastError(); }
+#undef BTL_ROW_NI
+#undef BTL_ROW_ST
+        return hipErrorInvalidValue;
+    }
     const bool st4 = st_need <= 4;
     const bool mt1 = a.m == 1;
-    const bool pr = a.swiglu_out != nullptr;
 #define BTL_DEC_XF(XFV)                                                                                     \
     if (xform == XFV) {                                                                                     \
         if (pr) {                                                                                           \

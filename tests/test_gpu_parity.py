@@ -126,16 +126,92 @@ def test_decode_k_parts_are_exact(parts, k, m, monkeypatch):
     # a decode workgroup: 4 / parts row blocks (when parts divides 4), each
     # split into `parts` K parts summed through LDS; n = 330 leaves a partial
     # row block and a workgroup with row blocks past the end.  Shapes whose
-    # tokens do not fit the prologue take the batched route instead.
+    # tokens do not fit the prologue take the batched route instead.  One
+    # token row takes the K-part form here only with the row-contiguous form
+    # switched off.
     n = 330
     x = activations(m, k, seed=11)
     pt, wb, sw = make_layer(n, k, seed=12)
     monkeypatch.setenv("BTL_GEMV_DEC_PARTS", parts)
+    monkeypatch.setenv("BTL_DEC_ROW", "0")
     acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
     assert np.array_equal(acc.cpu().numpy(), accr)
     assert_f32_identical(y, yr)
+
+
+# One token row, k % 64 == 0 and 4096 <= k <= 16384: the row-contiguous decode
+# form (whole rows per wave, 1 KB per load, the row's dot product as the trace
+# of a 16x16 MFMA product).  k covers one chunk, two chunks with a 64-byte
+# second one (only lane 0 loads), two full chunks, three of four chunks, three
+# and a half (Llama-3-8B down) and four; n = 330 leaves rows past the end of
+# the last row block.  rpw / rb override rows per wave and row blocks per
+# workgroup (the tuning knobs); every variant must give the oracle's bits and
+# those of the K-part form.
+ROW_CASES = [(4096, None, None), (4096, "8", None), (4096, "16", None), (4096, None, "2"),
+             (4160, None, None), (8192, None, None), (8192, "8", None), (12288, None, None),
+             (14336, None, None), (14336, "4", None), (16384, None, None), (2048, None, None)]
+
+
+@pytest.mark.parametrize("k,rpw,rb", ROW_CASES)
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_decode_row_form_exact(k, rpw, rb, xdt, monkeypatch):
+    print("row form", k, rpw, rb, xdt, flush=True)
+    n = 330
+    x = activations(1, k, seed=k + 5)
+    pt, wb, sw = make_layer(n, k, seed=k + 6)
+    xt = to_dev(x, xdt)
+    monkeypatch.setenv("BTL_DEC_ROW_MIN_K", "2048")
+    if rpw:
+        monkeypatch.setenv("BTL_DEC_ROW_RPW", rpw)
+    if rb:
+        monkeypatch.setenv("BTL_DEC_ROW_RB", rb)
+    acc = torch.empty((1, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert_f32_identical(y, yr)
+    monkeypatch.setenv("BTL_DEC_ROW", "0")
+    acc2 = torch.empty((1, n), dtype=torch.int32, device=DEV)
+    y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
+    assert torch.equal(acc, acc2) and torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("case", ["zero", "inf", "nan", "tiny", "outliers"])
+def test_decode_row_form_special_rows(case):
+    # the one-token quantiser's special rows through the row-contiguous form
+    k, n = 4096, 96
+    x = activations(1, k, seed=21)
+    if case == "zero":
+        x[:] = 0.0
+    elif case == "inf":
+        x[0, 17] = -np.inf
+    elif case == "nan":
+        x[0, 4000] = np.nan
+    elif case == "tiny":
+        x *= np.float32(1e-35)
+    else:
+        x[0, ::97] = np.float32(3.0e4)
+    pt, wb, sw = make_layer(n, k, seed=22)
+    acc = torch.empty((1, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert_f32_identical(y, yr)
+
+
+def test_decode_row_form_group_of_ragged_layers():
+    # three layers of one launch whose row counts are not multiples of 16
+    k = 4096
+    x = activations(1, k, seed=31)
+    ns = (100, 37, 250)
+    layers = [make_layer(n, k, seed=32 + n) for n in ns]
+    xt = to_dev(x, torch.bfloat16)
+    ys = bl.linear_group([l[0] for l in layers], xt, out_dtype=torch.float32)
+    for n, (pt, wb, sw), y in zip(ns, layers, ys):
+        yr, _, _, _ = orc.forward_i8(host_x(xt), wb, n, sw)
+        assert_f32_identical(y, yr)
 
 
 # batched decode / small prefill: k_gemv_bat (m <= 64) and the GEMM, both with
