@@ -525,8 +525,8 @@ __global__ __launch_bounds__(dec_threads(ST, XF, NI)) void k_gemv_dec(GemvArgs a
             const v4i t = acc;
             int d = (lane & 2) ? ((lane & 1) ? t.w : t.z) : ((lane & 1) ? t.y : t.x);
             d = diag ? d : 0;
-            d += __builtin_amdgcn_update_dpp(d, d, 0xB1, 0xF, 0xF, false);  // quad [1,0,3,2]
-            d += __builtin_amdgcn_update_dpp(d, d, 0x4E, 0xF, 0xF, false);  // quad [2,3,0,1]
+            d += __builtin_amdgcn_update_dpp(0, d, 0xB1, 0xF, 0xF, true);  // quad [1,0,3,2], one v_add_u32_dpp
+            d += __builtin_amdgcn_update_dpp(0, d, 0x4E, 0xF, 0xF, true);  // quad [2,3,0,1]
             const int s = __builtin_amdgcn_readlane(d, 0) + __builtin_amdgcn_readlane(d, 20) +
                           __builtin_amdgcn_readlane(d, 40) + __builtin_amdgcn_readlane(d, 60);
             sv = lane == rho ? s : sv;
