@@ -96,6 +96,7 @@ struct GemmArgs {
 };
 
 constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for
+constexpr int kGemmWideMinTiles = 512;  // 256-row GEMM tiles from this many workgroups on
 // K splits for an (m, ncols, k) GEMM: enough workgroups to cover the chip when
 // the output has few tiles (small m); 1 when it already has kGemmSplitTarget.
 int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps);

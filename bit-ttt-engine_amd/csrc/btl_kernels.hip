@@ -9,7 +9,7 @@
 //   k_gemv_dec<XK,YK,WV>  the decode case (1..4 token rows): one 16-row tile
 //                     per workgroup, WV waves split K, activations quantised
 //                     per wave from registers loaded ahead of the weights.
-//   k_gemm_i8         prefill GEMM (many token rows): int8 MFMA on 128x128
+//   k_gemm_i8         prefill GEMM (many token rows): int8 MFMA on 128x128 or 128x256
 //                     tiles fed by direct global->LDS copies, the packed
 //                     weight tile unpacked per wave; k_quant_op quantises the
 //                     tokens ahead of it in operand order (k_op_order
@@ -24,6 +24,7 @@
 // Compiled with -ffp-contract=off: every fp32 operation below is rounded as
 // written (the oracle restates the same operations in C).
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 
 #include "btl_device.hpp"
 #include "btl_internal.hpp"
@@ -1039,28 +1040,31 @@ hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, h
 // ---------------------------------------------------------------------------
 // k_gemm_i8: prefill GEMM, int8 activations x packed ternary weights
 // ---------------------------------------------------------------------------
-// Workgroup tile 128 (tokens) x 128 (output rows), K steps of 128; 4 waves in
-// a 2x2 grid, wave tile 64 x 64 = 4 x 4 blocks of v_mfma_i32_16x16x64_i8 with
-// the activations as A and the weights as B (D[m][n]).
+// Workgroup tile 128 (tokens) x TN (output rows, 128 or 256), K steps of 128;
+// 4 waves, each a 64 x 64 (TN = 128: 2 x 2 waves) or 128 x 64 (TN = 256: 1 x 4
+// waves) block of v_mfma_i32_16x16x64_i8 with the activations as A and the
+// weights as B (D[m][n]).  The wider tile halves the unpack VALU per MFMA (a
+// wave's 4 unpacked weight words feed 8 token blocks instead of 4; the VALU
+// issue, 4 cycles per wave instruction, otherwise rivals the 16 cycles of an
+// MFMA) and the activation re-reads from L2 (one per 256 output rows).  A 2 x 2
+// layout of 64 x 128 wave tiles (less LDS traffic, same VALU as 64 x 64) and a
+// third LDS stage (occupancy 2 instead of 3-4) measured slower.
 //
 // Global memory is copied straight into LDS by buffer_load_dwordx4 ... lds
 // (each lane's 16 bytes land at M0 + 16 * lane), so no register staging sits
-// between HBM/L2 and the matrix cores.  Two LDS stages of 20 KB: the copies of
-// step s+1 are issued right after the barrier that opens step s and have the
-// whole of step s to land.  One barrier per step; 40 KB of LDS and ~110 VGPRs
-// leave room for 3-4 workgroups per CU.
+// between HBM/L2 and the matrix cores.  Two LDS stages (20 or 24 KB): the
+// copies of step s+1 are issued right after the barrier that opens step s and
+// have the whole of step s to land.  One barrier per step.
 //
 // Stage layout (the lane -> global mapping of the copies produces it):
 //   A [half j (k 64j..64j+63)][row 0..127][64 B]: 16-byte slot s of row r
 //     holds k group s ^ ((r >> 1) & 3), so the MFMA-operand reads (16 rows x
 //     4 slots per instruction) hit every bank once;
-//   B [half j][column 0..127][16 B]: the packed word kq of a column at byte
+//   B [half j][column 0..TN-1][16 B]: the packed word kq of a column at byte
 //     4 kq, so a read of 16 columns x 4 words covers the 64 banks once.
 // Each wave unpacks the 4 weight words of its 64 columns per half step.
 constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 128;
 constexpr int kGemmABytes = kGemmBM * kGemmBK;      // 16 KB
-constexpr int kGemmBBytes = kGemmBN * kGemmBK / 4;  // 4 KB
-constexpr int kGemmStage = kGemmABytes + kGemmBBytes;
 constexpr int kGemmACh = kGemmABytes / 1024 / 4;    // A copies (1 KB) per wave per step
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -1079,13 +1083,22 @@ constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4
 // s_waitcnt vmcnt(0): every global load (and LDS copy) of this wave has landed.
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); }
 
+template <int TN, int WGN>
 __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
 {
-    __shared__ __align__(1024) uint8_t lds[2 * kGemmStage];
+    static_assert(TN == 128 || TN == 256, "tile of 128 or 256 output rows");
+    static_assert(WGN == 2 || WGN == 4, "2 x 2 or 1 x 4 waves");
+    constexpr int WGM = 4 / WGN;               // waves along the tokens
+    constexpr int TMB = kGemmBM / 16 / WGM;    // 16-token blocks per wave
+    constexpr int TNB = TN / 16 / WGN;         // 16-row weight blocks per wave
+    constexpr int BBytes = TN * kGemmBK / 4;
+    constexpr int Stage = kGemmABytes + BBytes;
+    constexpr int BCh = BBytes / 1024 / 4;  // B copies (1 KB) per wave per step
+    __shared__ __align__(1024) uint8_t lds[2 * Stage];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     // consecutive workgroups go to consecutive XCDs: with tm = bid % tiles_m
     // each XCD keeps re-reading the same activation row tiles from its L2
     const int tiles_m = (a.m + kGemmBM - 1) / kGemmBM;
@@ -1098,9 +1111,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
     for (int i = 1; i < kMaxGroup; ++i)
         if (i < a.nl && tn >= a.L[i].tile0) Lw = a.L[i];
     tn -= Lw.tile0;
-    const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
+    const int m0 = tm * kGemmBM, n0 = tn * TN;
     const int K = a.k, N = Lw.n;
-    const int rows_a = min(kGemmBM, a.m - m0), rows_b = min(kGemmBN, N - n0);
+    const int rows_a = min(kGemmBM, a.m - m0), rows_b = min(TN, N - n0);
     const int split = blockIdx.y;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.q + (int64_t)m0 * K, (uint32_t)(rows_a * K));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(Lw.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
@@ -1117,65 +1130,82 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
         const int grp = (lane & 3) ^ ((row >> 1) & 3);
         aoff[i] = row * K + j * 64 + grp * 16;
     }
-    // B: wave w fills half w / 2, columns 64 (w % 2) + lane
-    const int boff = ((wave & 1) * 64 + lane) * (K >> 2) + (wave >> 1) * 16;
+    // B chunk c = 64 columns x 16 B of half j: columns 64 (c % (TN / 64)) + lane
+    int boff[BCh];
+#pragma unroll
+    for (int i = 0; i < BCh; ++i) {
+        const int c = wave * BCh + i;
+        boff[i] = ((c % (TN / 64)) * 64 + lane) * (K >> 2) + (c / (TN / 64)) * 16;
+    }
 
     auto issue = [&](int st, int stage) {
         const int ko = st * kGemmBK;
-        uint8_t* base = lds + stage * kGemmStage;
+        uint8_t* base = lds + stage * Stage;
 #pragma unroll
         for (int i = 0; i < kGemmACh; ++i) copy_to_lds(ra, base + (wave * kGemmACh + i) * 1024, aoff[i] + ko);
-        copy_to_lds(rb, base + kGemmABytes + wave * 1024, boff + (ko >> 2));
+#pragma unroll
+        for (int i = 0; i < BCh; ++i) copy_to_lds(rb, base + kGemmABytes + (wave * BCh + i) * 1024, boff[i] + (ko >> 2));
     };
 
-    v4i acc[4][4];
+    v4i acc[TMB][TNB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < TMB; ++b)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[b][c] = v4i{0, 0, 0, 0};
+        for (int c = 0; c < TNB; ++c) acc[b][c] = v4i{0, 0, 0, 0};
 
     const int r16 = lane & 15, kq = lane >> 4;
-    // row = 64 wm + 16 b + r16, so (row >> 1) & 3 == (r16 >> 1) & 3
-    const int aread = (wm * 64 + r16) * 64 + ((kq ^ ((r16 >> 1) & 3)) * 16);
-    const int bread = kGemmABytes + (wn * 64 + r16) * 16 + kq * 4;
+    // row = wm TMB 16 + 16 b + r16, so (row >> 1) & 3 == (r16 >> 1) & 3
+    const int aread = (wm * TMB * 16 + r16) * 64 + ((kq ^ ((r16 >> 1) & 3)) * 16);
+    const int bread = kGemmABytes + (wn * TNB * 16 + r16) * 16 + kq * 4;
     auto compute_half = [&](const uint8_t* base, int j) {
-        v4i bop[4];
+        v4i bop[TNB];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) bop[c] = unpack16(*(const uint32_t*)(base + bread + j * 2048 + c * 256));
+        for (int c = 0; c < TNB; ++c) bop[c] = unpack16(*(const uint32_t*)(base + bread + j * (TN * 16) + c * 256));
         const uint8_t* ab = base + j * (kGemmBM * 64) + aread;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < TMB; ++b) {
             const v4i aop = *(const v4i*)(ab + b * 1024);
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
+            for (int c = 0; c < TNB; ++c)
                 acc[b][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop[c], acc[b][c], 0, 0, 0);
         }
     };
 
+    // every step but the last has both halves, and the loop body no branch
+    // (one basic block: the scheduler can overlap a half's unpack with the
+    // other half's MFMAs)
     if (st_begin < st_end) issue(st_begin, 0);
-    for (int st = st_begin; st < st_end; ++st) {
+    int st = st_begin;
+    for (; st + 1 < st_end; ++st) {
         const int stage = (st - st_begin) & 1;
         wait_loads();     // this wave's copies of step st are in LDS
         __syncthreads();  // ... every wave's; and the other stage is no longer read
-        if (st + 1 < st_end) issue(st + 1, stage ^ 1);
-        const uint8_t* base = lds + stage * kGemmStage;
+        issue(st + 1, stage ^ 1);
+        const uint8_t* base = lds + stage * Stage;
         compute_half(base, 0);
-        if (st * kGemmBK + 64 < K) compute_half(base, 1);  // k % 128 == 64: last step is half
+        compute_half(base, 1);
+    }
+    if (st < st_end) {
+        wait_loads();
+        __syncthreads();
+        const uint8_t* base = lds + ((st - st_begin) & 1) * Stage;
+        compute_half(base, 0);
+        if (st * kGemmBK + 64 < K) compute_half(base, 1);  // k % 128 == 64: the last step is half
     }
 
     if (a.splits > 1) {
         // exact int32 partial sums; k_gemm_reduce adds the splits
         const int ncols = a.L[a.nl - 1].col0 + a.L[a.nl - 1].n;
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < TMB; ++b)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int m = m0 + wm * 64 + b * 16 + 4 * kq + v;
+                const int m = m0 + wm * TMB * 16 + b * 16 + 4 * kq + v;
                 if (m < a.m) {
                     int32_t* prow = a.part + ((int64_t)split * a.m + m) * ncols + Lw.col0;
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        const int n = n0 + wn * 64 + c * 16 + r16;
+                    for (int c = 0; c < TNB; ++c) {
+                        const int n = n0 + wn * TNB * 16 + c * 16 + r16;
                         if (n < N) prow[n] = acc[b][c][v];
                     }
                 }
@@ -1183,18 +1213,61 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
         return;
     }
 
-    // epilogue: y = (float)acc * (s_x[m] * s_w)
+    // epilogue: y = (float)acc * (s_x[m] * s_w).  A whole tile (the common
+    // case) takes the short path: one row address per token row, no bounds
+    // checks, the output kind tested once.
     const bool ybf = a.ykind == YK_BF16;
+    if (m0 + kGemmBM <= a.m && n0 + TN <= N) {
+        const int nb = n0 + wn * TNB * 16 + r16;
+        float cmv[TMB][4];  // every token scale load in flight before the first use
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+        for (int b = 0; b < TMB; ++b)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) cmv[b][v] = a.sx[m0 + wm * TMB * 16 + b * 16 + 4 * kq + v];
+        const int64_t rb0 = (int64_t)(m0 + wm * TMB * 16 + 4 * kq) * N + nb;
+        if (ybf) {
+#pragma unroll
+            for (int b = 0; b < TMB; ++b)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float cm = __fmul_rn(cmv[b][v], Lw.sw);
+                    uint16_t* yr = (uint16_t*)Lw.y + rb0 + (int64_t)(b * 16 + v) * N;
+#pragma unroll
+                    for (int c = 0; c < TNB; ++c) yr[c * 16] = f32_to_bf16(__fmul_rn((float)acc[b][c][v], cm));
+                }
+        } else {
+#pragma unroll
+            for (int b = 0; b < TMB; ++b)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float cm = __fmul_rn(cmv[b][v], Lw.sw);
+                    float* yr = (float*)Lw.y + rb0 + (int64_t)(b * 16 + v) * N;
+#pragma unroll
+                    for (int c = 0; c < TNB; ++c) yr[c * 16] = __fmul_rn((float)acc[b][c][v], cm);
+                }
+        }
+        if (Lw.acc_out) {
+#pragma unroll
+            for (int b = 0; b < TMB; ++b)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    int32_t* ar = Lw.acc_out + rb0 + (int64_t)(b * 16 + v) * N;
+#pragma unroll
+                    for (int c = 0; c < TNB; ++c) ar[c * 16] = acc[b][c][v];
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int b = 0; b < TMB; ++b) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int m = m0 + wm * 64 + b * 16 + 4 * kq + v;
+            const int m = m0 + wm * TMB * 16 + b * 16 + 4 * kq + v;
             if (m < a.m) {
                 const float cm = __fmul_rn(a.sx[m], Lw.sw);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const int n = n0 + wn * 64 + c * 16 + r16;
+                for (int c = 0; c < TNB; ++c) {
+                    const int n = n0 + wn * TNB * 16 + c * 16 + r16;
                     if (n < N) {
                         const int64_t o = (int64_t)m * N + n;
                         const float yv = __fmul_rn((float)acc[b][c][v], cm);
@@ -1245,6 +1318,8 @@ int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps)
     const int64_t steps = (k + kGemmBK - 1) / kGemmBK;
     const int64_t tiles = (m + kGemmBM - 1) / kGemmBM * tiles_n;
     int64_t s = tiles >= kGemmSplitTarget || tiles <= 0 ? 1 : (kGemmSplitTarget + tiles - 1) / tiles;
+    const char* ev = getenv("BTL_GEMM_MAX_SPLITS");  // tuning / tests: 1 turns split-K off
+    if (ev && *ev && atoll(ev) >= 1 && s > atoll(ev)) s = atoll(ev);
     if (s > steps / 2) s = steps / 2;  // at least two K steps per split
     if (s < 1) s = 1;
     const int64_t per = (steps + s - 1) / s;
@@ -1254,23 +1329,33 @@ int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps)
 
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
 {
-    // tile0 / col0 of every layer are filled in here from the layers' n
+    // Tiles of 256 output rows when there is no K split and they still give
+    // every CU two workgroups at once (measured on MI355X, Llama-3-8B prefill
+    // shapes); else 128.  tile0 / col0 of every layer are filled in here.
     GemmArgs g = a;
+    const int64_t tiles_m = (g.m + kGemmBM - 1) / kGemmBM;
+    int64_t tn256 = 0;
+    for (int l = 0; l < g.nl; ++l) tn256 += (g.L[l].n + 255) / 256;
+    const char* ev = getenv("BTL_GEMM_WIDE_MIN_TILES");
+    const int64_t wide_min = ev && *ev ? atoll(ev) : kGemmWideMinTiles;
+    const int TN = g.splits <= 1 && tiles_m * tn256 >= wide_min ? 256 : 128;
     int64_t tn = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
         g.L[l].tile0 = (int)tn;
         g.L[l].col0 = (int)cols;
-        tn += (g.L[l].n + kGemmBN - 1) / kGemmBN;
+        tn += (g.L[l].n + TN - 1) / TN;
         cols += g.L[l].n;
     }
-    const int64_t tiles = (int64_t)((g.m + kGemmBM - 1) / kGemmBM) * tn;
+    const int64_t tiles = tiles_m * tn;
     if (tiles <= 0) return hipSuccess;
     if (tiles > INT32_MAX || g.nl < 1 || g.nl > kMaxGroup || cols > INT32_MAX) return hipErrorInvalidValue;
     if (g.splits < 1) g.splits = 1;
     if (g.splits == 1) g.split_steps = (g.k + kGemmBK - 1) / kGemmBK;
     if (g.splits > 1 && (!g.part || g.split_steps < 1 || (int64_t)g.splits * g.m * cols > INT32_MAX))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gemm_i8, dim3((unsigned)tiles, (unsigned)g.splits), dim3(256), 0, s, g);
+    const dim3 grid((unsigned)tiles, (unsigned)g.splits);
+    if (TN == 256) hipLaunchKernelGGL((k_gemm_i8<256, 4>), grid, dim3(256), 0, s, g);
+    else hipLaunchKernelGGL((k_gemm_i8<128, 2>), grid, dim3(256), 0, s, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || g.splits == 1) return e;
     const int64_t outs = (int64_t)g.m * cols;

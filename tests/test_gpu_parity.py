@@ -432,6 +432,48 @@ def test_gemm_matches_oracle(m, k, n, xdt, ydt):
         assert_bf16_matches(y, yr)
 
 
+# Tiles of 256 output rows (1 x 4 waves of 128 x 64; chosen for launches of
+# >= 512 such workgroups, forced here) and the whole-tile epilogue of both tile
+# widths: ragged m / n / k (a half last K step), exact multiples, a group of
+# layers whose tiles start mid-way through the launch.
+WIDE_SHAPES = [(300, 1088, 257), (129, 4096, 1000), (256, 512, 512), (384, 1024, 768), (128, 192, 256),
+               (131, 14336, 64)]
+
+
+@pytest.mark.parametrize("wide", [True, False])
+@pytest.mark.parametrize("m,k,n", WIDE_SHAPES)
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
+def test_gemm_tile_widths_match_oracle(m, k, n, xdt, ydt, wide, monkeypatch):
+    print("gemm tiles", m, k, n, xdt, ydt, wide, flush=True)
+    monkeypatch.setenv("BTL_GEMM_MAX_SPLITS", "1")
+    monkeypatch.setenv("BTL_GEMM_WIDE_MIN_TILES", "1" if wide else "1000000000")
+    x = activations(m, k, seed=m + k * 5 + n)
+    x[min(7, m - 1)] = 0.0
+    pt, wb, sw = make_layer(n, k, seed=n * 11 + k)
+    xt = to_dev(x, xdt)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, out_dtype=ydt, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    if ydt == torch.float32:
+        assert_f32_identical(y, yr)
+    else:
+        assert_bf16_matches(y, yr)
+
+
+def test_gemm_wide_tiles_group_of_layers(monkeypatch):
+    monkeypatch.setenv("BTL_GEMM_MAX_SPLITS", "1")
+    monkeypatch.setenv("BTL_GEMM_WIDE_MIN_TILES", "1")
+    m, k, ns = 256, 1024, (300, 512, 70)
+    x = activations(m, k, seed=77)
+    layers = [make_layer(n, k, seed=78 + n) for n in ns]
+    xt = to_dev(x, torch.bfloat16)
+    ys = bl.linear_group([l[0] for l in layers], xt, out_dtype=torch.float32)
+    for n, (pt, wb, sw), y in zip(ns, layers, ys):
+        yr, _, _, _ = orc.forward_i8(host_x(xt), wb, n, sw)
+        assert_f32_identical(y, yr)
+
+
 @pytest.mark.parametrize("m,k,n", [(200, 512, 96), (130, 1088, 200)])
 def test_gemm_prequantized_natural_layout(m, k, n):
     # btl_linear_i8 hands the GEMM natural-order int8 rows
