@@ -249,6 +249,32 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
     return w;
 }
 
+// Compute waves per workgroup of the row-group decode form: the count in
+// [1, 16 - quantising waves] that minimises the compute waves of the busiest CU
+// when the workgroups spread evenly over the CUs (ties: the larger workgroup,
+// which quantises the token fewer times).  Llama-3-8B on 256 CUs: gate|up 14
+// (two workgroups per CU), q|k|v 6, o 4, down 8 (one each).  BTL_DEC_RQ_WPC
+// overrides it (tuning).
+int rq_waves_per_group(int64_t rb_total, int64_t k, int cus)
+{
+    const int rows = k <= 4096 ? 4 : 2;
+    const int64_t waves = rb_total * (16 / rows);
+    const int hi = 16 - btl::rq_quant_waves((int)k);
+    const int forced = env_int("BTL_DEC_RQ_WPC", 0);
+    if (forced >= 1 && forced <= hi) return forced;
+    if (cus < 1) cus = 1;
+    int best = 1;
+    int64_t best_cost = -1;
+    for (int w = 1; w <= hi; ++w) {
+        const int64_t cost = ceil_div(ceil_div(waves, w), cus) * w;
+        if (best_cost < 0 || cost <= best_cost) {
+            best = w;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
 // Activation transform fused ahead of the quantisation (btl_rmsnorm_linear_group,
 // btl_swiglu_linear_group).
 struct Xform {
@@ -370,6 +396,12 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
                       wv * rbw <= 8 && k / 16 <= (int64_t)(xf->kind == btl::XF_SWIGLU ? 2 : 1) * wv * rbw * 64 &&
                       !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
 
+    // One token row with no transform in the prologue and no SwiGLU epilogue:
+    // the row-group form (R whole rows per wave, one accumulator, workgroups of
+    // up to 16 waves of which only the first few quantise the token).
+    const bool rq = dec && m == 1 && !fuse && !swiglu_out && k % 64 == 0 && k <= 16384 &&
+                    k >= env_int("BTL_DEC_RQ_MIN_K", 1024) && env_int("BTL_DEC_RQ", 1) != 0;
+
     // operand-order quantisation into the workspace (all routes but plain decode)
     const bool pre = (xf && !fuse) || !dec;
     const int8_t* q = nullptr;
@@ -429,6 +461,12 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         }
         a.swiglu_out = swiglu_out;
         a.rowc = rowc;
+        if (rq) {
+            a.parts = rq_waves_per_group(rb, k, g_dev[dev].cus);
+            e = btl::launch_gemv_rq(a, pre ? (int)btl::XK_I8O : xkind, st);
+            if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
+            return BTL_OK;
+        }
         e = btl::launch_gemv_dec(a, pre ? (int)btl::XK_I8O : xkind, xform, st);
         if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
         return BTL_OK;

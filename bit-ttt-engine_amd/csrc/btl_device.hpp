@@ -13,6 +13,9 @@ namespace btl {
 // and an out-of-range offset reads zeros without a branch, so the compiler can
 // count the loads in flight exactly (s_waitcnt vmcnt(N) per step).
 constexpr int kOOB = 0x7FFFFFF0;  // offset outside every descriptor range
+// cache policy of a load read once (weights): the non-temporal bit (nt) of
+// the gfx950 buffer instructions
+constexpr int kCachePolicyNT = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
 {

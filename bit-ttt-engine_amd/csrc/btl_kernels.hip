@@ -734,6 +734,228 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
 }
 
 // ---------------------------------------------------------------------------
+// k_gemv_rq: one-token decode, row-group form
+// ---------------------------------------------------------------------------
+// A workgroup is nqw quantising waves followed by wpc compute waves.
+//
+// Compute wave c owns R consecutive weight rows (R = 4, or 2 for k > 4096).
+// Its load t, lane l = 16 g + i, reads 16 bytes of row i / (16 / R) at byte
+// t * (1024 / R) + 16 s, slice s = (16 / R) g + i % (16 / R): one load
+// instruction covers R rows x 1024 / R contiguous bytes (eight whole 128-byte
+// lines), non-temporal (the weights are read once).  MFMA word h of the lane
+// takes the 16 quantised activations at k = 4 (t * 1024 / R + 16 s) + 16 h as
+// B.  In the 16x16 product D[i][j] = sum_g A[i][g] B[g][j] (lane 16 g + i
+// holds A row i and B column i of k block g), D[i][i] pairs every lane's
+// weights with its own activations; the 16 / R diagonal entries of row rho sit
+// in register v of lanes 20 rho + v (R = 4), or of lanes 40 rho + v and
+// 40 rho + 20 + v (R = 2), so one accumulator over all loads and three DPP
+// adds give every row's exact int32 dot product.
+//
+// The quantising waves (two 16-element groups of the token per thread) load
+// the token, exchange the absmax through an LDS atomic max and quantise into
+// the shared LDS row in operand order; the compute waves issue their weight
+// loads at once and wait for the quantised row on an LDS counter, not on a
+// barrier, so no wave waits for another wave's loads to issue (the memory
+// queue of a CU back-pressures the issue of later loads for microseconds).
+// Every wait is bounded by kRqSpinMax polls.
+constexpr int kRqDG = 2;               // token groups per quantising thread
+constexpr int kRqSpinMax = 1 << 22;    // bound of every LDS poll (~0.1 s)
+
+template <int R>
+struct RqShape {
+    static constexpr int kSub = 16 / R;      // lanes of one row in a 16-lane group
+    static constexpr int kBytes = 1024 / R;  // bytes of a row per load instruction
+};
+
+__device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target)
+{
+    for (int it = 0; it < kRqSpinMax; ++it) {
+        if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int XK, int R, int ST>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8 : 4))) void k_gemv_rq(GemvArgs a)
+{
+    constexpr int SUB = RqShape<R>::kSub, RB = RqShape<R>::kBytes, DG = kRqDG;
+    constexpr int NV = DecX<XK>::kVec;
+    constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);
+    constexpr bool PREQ = DecX<XK>::kPreq;
+    extern __shared__ __align__(16) uint8_t sq[];  // [k + 16], operand order
+    __shared__ uint32_t s_sync[2];                 // absmax bits, arrivals
+    __shared__ float s_scale;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = a.k;
+    const int gpr = K >> 4;                               // 16-element groups of the token row
+    const int nqw = rq_quant_waves(K);
+    const int nq = nqw * 64;
+    const uint32_t done = PREQ ? (uint32_t)nqw : 2u * (uint32_t)nqw;
+
+    // 1. the quantising waves' token groups, issued before anything else
+    uint4 xv[DG][NV];
+    if (wave < nqw) {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(K * ES));
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi) {
+            const int g = tid + nq * gi;
+#pragma unroll
+            for (int h = 0; h < NV; ++h) xv[gi][h] = bload(xr, g < gpr ? 16 * g * ES + 16 * h : kOOB);
+        }
+    }
+    if (tid == 0) {
+        s_sync[0] = 0u;
+        s_sync[1] = 0u;
+    }
+    __syncthreads();  // the counters are set before any wave uses them
+
+    if (wave < nqw) {
+        // 2. quantise (or copy a pre-quantised row) into LDS; count arrivals
+        float rm = 0.0f;
+        if (!PREQ) {
+            uint32_t am = 0;
+#pragma unroll
+            for (int gi = 0; gi < DG; ++gi) am = max(am, group_absmax<XK>(xv[gi]));
+            const uint32_t v = wave_max_dpp(am);
+            if (lane == 0) {
+                __hip_atomic_fetch_max(&s_sync[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            rq_wait(&s_sync[1], (uint32_t)nqw);
+            const QParams qp = qparams(__hip_atomic_load(&s_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            rm = qp.ok ? qp.r : 0.0f;
+            if (tid == 0) s_scale = qp.s;
+        }
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi) {
+            const int g = tid + nq * gi;
+            uint4 qv = group_quant<XK>(xv[gi], rm);
+            if (!PREQ && rm == 0.0f) qv = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
+            if (g < gpr) *(uint4*)(sq + 16 * g) = qv;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return;
+    }
+
+    // 3. this compute wave's rows: R-row group q of the launch, in 16-row block q / SUB
+    const int q = (int)blockIdx.x * a.parts + (wave - nqw);
+    const int rbg = q / SUB;
+    const uint8_t* W = a.p[0].w;
+    void* Y = a.p[0].y;
+    int32_t* ACC = a.p[0].acc_out;
+    float SW = a.p[0].sw;
+    int N = a.p[0].n;
+    int RB0 = a.p[0].rb_begin;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i) {
+        if (i < a.nprob && rbg >= a.p[i].rb_begin) {
+            W = a.p[i].w; Y = a.p[i].y; ACC = a.p[i].acc_out;
+            SW = a.p[i].sw; N = a.p[i].n; RB0 = a.p[i].rb_begin;
+        }
+    }
+    const int row0 = (rbg - RB0) * 16 + (q - rbg * SUB) * R;  // past rb_total: no rows
+    const int rows = __builtin_amdgcn_readfirstlane(rbg < a.rb_total ? max(0, min(R, N - row0)) : 0);
+    const int rowb = K >> 2;
+    const int gq = lane >> 4, il = lane & 15;
+    const int rho = il / SUB, sl = SUB * gq + (il - rho * SUB);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(W + (int64_t)max(row0, 0) * rowb, (uint32_t)(rows * rowb));
+    uint4 buf[ST];
+#pragma unroll
+    for (int t = 0; t < ST; ++t) {
+        const int b = t * RB + 16 * sl;
+        buf[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               wr, b < rowb ? rho * rowb + b : kOOB, 0, kCachePolicyNT));
+    }
+    rq_wait(&s_sync[1], done);
+    const float s_l = PREQ ? a.xs[0] : s_scale;
+
+    // 4. one accumulator over every load; slices past the row read the
+    //    activations at k = 0 (their weights are zero)
+    v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < ST; ++t) {
+        const int ko = 4 * (t * RB + 16 * sl);
+        const uint8_t* bj = sq + (ko < K ? ko : 0);
+        const v4i b0 = *(const v4i*)(bj + 0);
+        const v4i b1 = *(const v4i*)(bj + 16);
+        const v4i b2 = *(const v4i*)(bj + 32);
+        const v4i b3 = *(const v4i*)(bj + 48);
+        const uint4 cur = buf[t];
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc, 0, 0, 0);
+    }
+
+    // 5. quad position 0 gathers register v of quad lane v (quad_perm
+    //    broadcasts of lanes 1, 2, 3): lanes 20 rho (R = 4) hold row rho; for
+    //    R = 2 lanes 40 rho add their half from lane 40 rho + 20
+    int d = acc[0] + __builtin_amdgcn_update_dpp(0, acc[1], 0x55, 0xF, 0xF, true);
+    d += __builtin_amdgcn_update_dpp(0, acc[2], 0xAA, 0xF, 0xF, true);
+    d += __builtin_amdgcn_update_dpp(0, acc[3], 0xFF, 0xF, 0xF, true);
+    int r;
+    bool own;
+    if (R == 4) {
+        r = lane / 20;
+        own = lane - 20 * r == 0;
+    } else {
+        d += __shfl_down(d, 20, 64);
+        r = lane / 40;
+        own = lane - 40 * r == 0;
+    }
+    if (!own || r >= rows) return;
+    const int n = row0 + r;
+    const float yv = __fmul_rn((float)d, __fmul_rn(s_l, SW));
+    if (a.ykind == YK_BF16) ((uint16_t*)Y)[n] = f32_to_bf16(yv);
+    else ((float*)Y)[n] = yv;
+    if (ACC) ACC[n] = d;
+}
+
+// Loads per compute wave: ceil(k * R / 4096); R = 4 for k <= 4096 (ST 1..4),
+// R = 2 above (ST 3..8, k <= 16384).  Workgroup: rq_quant_waves(k) + a.parts
+// waves, at most 16.
+hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, hipStream_t s)
+{
+    const int R = a.k <= 4096 ? 4 : 2;
+    const int st = (int)(((int64_t)a.k * R + 4095) / 4096);
+    const int nqw = rq_quant_waves(a.k);
+    if (a.m != 1 || a.k % 64 != 0 || a.k < 64 || a.k > 16384 || a.parts < 1 || nqw + a.parts > 16 ||
+        a.rb_total < 1 || (xkind != XK_F32 && xkind != XK_BF16 && xkind != XK_I8 && xkind != XK_I8O))
+        return hipErrorInvalidValue;
+    const int64_t waves = (int64_t)a.rb_total * (16 / R);
+    const dim3 grid((unsigned)((waves + a.parts - 1) / a.parts)), block((unsigned)((nqw + a.parts) * 64));
+    const size_t lds = (size_t)a.k + 16;
+#define BTL_RQ_XK(RV, STV)                                                                                       \
+    if (xkind == XK_BF16) hipLaunchKernelGGL((k_gemv_rq<XK_BF16, RV, STV>), grid, block, lds, s, a);          \
+    else if (xkind == XK_F32) hipLaunchKernelGGL((k_gemv_rq<XK_F32, RV, STV>), grid, block, lds, s, a);       \
+    else if (xkind == XK_I8) hipLaunchKernelGGL((k_gemv_rq<XK_I8, RV, STV>), grid, block, lds, s, a);         \
+    else hipLaunchKernelGGL((k_gemv_rq<XK_I8O, RV, STV>), grid, block, lds, s, a);
+    if (R == 4) {
+        switch (st) {
+        case 1: { BTL_RQ_XK(4, 1) break; }
+        case 2: { BTL_RQ_XK(4, 2) break; }
+        case 3: { BTL_RQ_XK(4, 3) break; }
+        default: { BTL_RQ_XK(4, 4) break; }
+        }
+    } else {
+        switch (st) {
+        case 3: { BTL_RQ_XK(2, 3) break; }
+        case 4: { BTL_RQ_XK(2, 4) break; }
+        case 5: { BTL_RQ_XK(2, 5) break; }
+        case 6: { BTL_RQ_XK(2, 6) break; }
+        case 7: { BTL_RQ_XK(2, 7) break; }
+        default: { BTL_RQ_XK(2, 8) break; }
+        }
+    }
+#undef BTL_RQ_XK
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // k_quant_op: per-token quantisation into MFMA operand order (prefill)
 // ---------------------------------------------------------------------------
 // One workgroup per token row; the arithmetic of k_quant_act, but every group

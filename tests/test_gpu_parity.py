@@ -134,6 +134,7 @@ def test_decode_k_parts_are_exact(parts, k, m, monkeypatch):
     pt, wb, sw = make_layer(n, k, seed=12)
     monkeypatch.setenv("BTL_GEMV_DEC_PARTS", parts)
     monkeypatch.setenv("BTL_DEC_ROW", "0")
+    monkeypatch.setenv("BTL_DEC_RQ", "0")
     acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
@@ -162,6 +163,7 @@ def test_decode_row_form_exact(k, rpw, rb, xdt, monkeypatch):
     x = activations(1, k, seed=k + 5)
     pt, wb, sw = make_layer(n, k, seed=k + 6)
     xt = to_dev(x, xdt)
+    monkeypatch.setenv("BTL_DEC_RQ", "0")
     monkeypatch.setenv("BTL_DEC_ROW_MIN_K", "2048")
     if rpw:
         monkeypatch.setenv("BTL_DEC_ROW_RPW", rpw)
@@ -178,9 +180,13 @@ def test_decode_row_form_exact(k, rpw, rb, xdt, monkeypatch):
     assert torch.equal(acc, acc2) and torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("form", ["rq", "row"])
 @pytest.mark.parametrize("case", ["zero", "inf", "nan", "tiny", "outliers"])
-def test_decode_row_form_special_rows(case):
-    # the one-token quantiser's special rows through the row-contiguous form
+def test_decode_row_form_special_rows(case, form, monkeypatch):
+    # the one-token quantiser's special rows through the row-group form and
+    # the row-contiguous form
+    if form == "row":
+        monkeypatch.setenv("BTL_DEC_RQ", "0")
     k, n = 4096, 96
     x = activations(1, k, seed=21)
     if case == "zero":
@@ -201,9 +207,12 @@ def test_decode_row_form_special_rows(case):
     assert_f32_identical(y, yr)
 
 
-def test_decode_row_form_group_of_ragged_layers():
+@pytest.mark.parametrize("form", ["rq", "row"])
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_decode_row_form_group_of_ragged_layers(k, form, monkeypatch):
     # three layers of one launch whose row counts are not multiples of 16
-    k = 4096
+    if form == "row":
+        monkeypatch.setenv("BTL_DEC_RQ", "0")
     x = activations(1, k, seed=31)
     ns = (100, 37, 250)
     layers = [make_layer(n, k, seed=32 + n) for n in ns]
@@ -212,6 +221,75 @@ def test_decode_row_form_group_of_ragged_layers():
     for n, (pt, wb, sw), y in zip(ns, layers, ys):
         yr, _, _, _ = orc.forward_i8(host_x(xt), wb, n, sw)
         assert_f32_identical(y, yr)
+
+
+# One token row, no transform: the row-group form (R = 4 rows per wave for
+# k <= 4096, else 2; one load instruction covers R rows x 1024 / R bytes; the
+# rows' dot products are diagonal sums of one MFMA accumulator; only the first
+# waves of a workgroup quantise).  k covers partial last slices (1088, 4160,
+# 5120), every loads-per-wave count (1024..4096 -> 1..4, 6144..16384 -> 3..8)
+# and k below 1024 (one partial slice); wpc overrides the compute waves per
+# workgroup (1 up to 16 minus the quantising waves).  n = 330 leaves a partial row
+# block and waves past the end.  Every case must give the oracle's bits and
+# those of the K-part form.
+RQ_CASES = [(4096, None), (4096, "1"), (4096, "5"), (4096, "14"), (1024, None), (2048, None),
+            (3072, None), (1088, None), (64, None), (960, "1"), (4160, None), (5120, None),
+            (6144, None), (8192, None), (10240, None), (12288, None), (14336, None), (14336, "7"),
+            (14336, "9"), (16384, None)]
+
+
+@pytest.mark.parametrize("k,wpc", RQ_CASES)
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_decode_row_group_form_exact(k, wpc, xdt, monkeypatch):
+    print("row-group form", k, wpc, xdt, flush=True)
+    n = 330
+    x = activations(1, k, seed=k + 7)
+    pt, wb, sw = make_layer(n, k, seed=k + 8)
+    xt = to_dev(x, xdt)
+    monkeypatch.setenv("BTL_DEC_RQ_MIN_K", "64")
+    if wpc:
+        monkeypatch.setenv("BTL_DEC_RQ_WPC", wpc)
+    acc = torch.empty((1, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert_f32_identical(y, yr)
+    yb = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.bfloat16)
+    assert_bf16_matches(yb, yr)
+    monkeypatch.setenv("BTL_DEC_RQ", "0")
+    monkeypatch.setenv("BTL_DEC_ROW", "0")
+    acc2 = torch.empty((1, n), dtype=torch.int32, device=DEV)
+    y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
+    assert torch.equal(acc, acc2) and torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_decode_row_group_form_prequantized(k, monkeypatch):
+    # int8 inputs through the row-group form: natural order (btl_linear_i8)
+    # and operand order (an RMSNorm group whose transform runs as its own
+    # launch), against the fused quantisation, the GEMM on the same operand-
+    # order rows and the transform fused into the K-part decode kernel
+    n = 200
+    g = torch.from_numpy(np.random.default_rng(k).uniform(0.5, 1.5, k).astype(np.float32)).to(DEV)
+    xf = to_dev(activations(1, k, seed=k + 11), torch.float32)
+    pn, _, _ = make_layer(n, k, seed=k + 12)
+    yf = bl.rmsnorm_linear_group([pn], xf, g, 1e-5, out_dtype=torch.float32)[0]
+    monkeypatch.setenv("BTL_FUSE_DEC", "0")
+    yu = bl.rmsnorm_linear_group([pn], xf, g, 1e-5, out_dtype=torch.float32)[0]
+    assert torch.equal(yf, yu)
+    x = to_dev(activations(1, k, seed=k + 9), torch.bfloat16)
+    pt, wb, sw = make_layer(n, k, seed=k + 10)
+    acc0 = torch.empty((1, n), dtype=torch.int32, device=DEV)
+    y0 = bl.BitLinearHip.forward(x, pt, out_dtype=torch.float32, acc_out=acc0)
+    q, s = bl.quantize_act(x)
+    acc1 = torch.empty_like(acc0)
+    y1 = bl.linear_i8(q, s, pt, acc_out=acc1)
+    qo, so = bl.quantize_act_op(x)
+    y2 = bl.linear_i8_op(qo, so, [pt])[0]
+    assert torch.equal(acc0, acc1) and torch.equal(y0, y1) and torch.equal(y0, y2)
+    yr, _, _, accr = orc.forward_i8(host_x(x), wb, n, sw)
+    assert np.array_equal(acc0.cpu().numpy(), accr)
+    assert_f32_identical(y0, yr)
 
 
 # batched decode / small prefill: k_gemv_bat (m <= 64) and the GEMM, both with
