@@ -258,11 +258,11 @@ def run_decode(args):
                    "bytes_per_step": step_bytes,
                    "step_GB_s": round(step_bytes / ms / 1e6, 1),
                    "step_frac_hbm": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 3)},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_dec<XK_BF16> gate|up 4096->2x14336 (W1.58-A8)",
+        "roofline": {"bound": "hbm", "kernel": "k_gemv_rq<XK_BF16, 4, 4> gate|up 4096->2x14336 (W1.58-A8)",
                      "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": dom["frac_hbm"],
-                     "traffic": profiled_traffic("k_gemv_dec_gate_up_decode_traffic.md"),
-                     "traffic_source": "profiles/k_gemv_dec_gate_up_decode_traffic.md (FETCH_SIZE x copy-calibrated "
+                     "traffic": profiled_traffic("k_gemv_rq_gate_up_decode_traffic.md"),
+                     "traffic_source": "profiles/k_gemv_rq_gate_up_decode_traffic.md (FETCH_SIZE x copy-calibrated "
                                        "factor + WRITE_SIZE, bytes per launch)",
                      "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"]},
         "kernels": kern,
@@ -591,7 +591,7 @@ def run_probe(args):
         x = synth_act(1, HIDDEN, gen, dev)
         outs = [torch.empty((1, INTER), dtype=torch.bfloat16, device=dev) for _ in range(2)]
         call = Call([gate, up], x, outs)
-        what = "btl_linear_group gate|up, M=1, 4096 -> 2 x 14336, bf16 (k_gemv_dec)"
+        what = "btl_linear_group gate|up, M=1, 4096 -> 2 x 14336, bf16 (k_gemv_rq)"
     else:
         x = synth_act(args.prefill_m, HIDDEN, gen, dev)
         q, s = bl.quantize_act_op(x)

@@ -1305,17 +1305,18 @@ constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4
 // s_waitcnt vmcnt(0): every global load (and LDS copy) of this wave has landed.
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); }
 
-template <int TN, int WGN>
-__global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
+template <int TN, int WGN, int NW = 4>
+__global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
 {
     static_assert(TN == 128 || TN == 256, "tile of 128 or 256 output rows");
-    static_assert(WGN == 2 || WGN == 4, "2 x 2 or 1 x 4 waves");
-    constexpr int WGM = 4 / WGN;               // waves along the tokens
+    static_assert(NW == 4 && (WGN == 2 || WGN == 4), "2 x 2 or 1 x 4 waves");
+    constexpr int WGM = NW / WGN;              // waves along the tokens
     constexpr int TMB = kGemmBM / 16 / WGM;    // 16-token blocks per wave
     constexpr int TNB = TN / 16 / WGN;         // 16-row weight blocks per wave
     constexpr int BBytes = TN * kGemmBK / 4;
     constexpr int Stage = kGemmABytes + BBytes;
-    constexpr int BCh = BBytes / 1024 / 4;  // B copies (1 KB) per wave per step
+    constexpr int ACh = kGemmABytes / 1024 / NW;  // A copies (1 KB) per wave per step
+    constexpr int BCh = BBytes / 1024 / NW;       // B copies (1 KB) per wave per step
     __shared__ __align__(1024) uint8_t lds[2 * Stage];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1344,10 +1345,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
 
     // source offsets (relative to the step's first k) of this wave's copies:
     // A chunk c = 16 rows x 64 B of half j; lane -> (row, slot) as laid out above
-    int aoff[kGemmACh];
+    int aoff[ACh];
 #pragma unroll
-    for (int i = 0; i < kGemmACh; ++i) {
-        const int c = wave * kGemmACh + i;
+    for (int i = 0; i < ACh; ++i) {
+        const int c = wave * ACh + i;
         const int j = c / (kGemmBM / 16), row = (c % (kGemmBM / 16)) * 16 + (lane >> 2);
         const int grp = (lane & 3) ^ ((row >> 1) & 3);
         aoff[i] = row * K + j * 64 + grp * 16;
@@ -1364,7 +1365,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_i8(GemmArgs a)
         const int ko = st * kGemmBK;
         uint8_t* base = lds + stage * Stage;
 #pragma unroll
-        for (int i = 0; i < kGemmACh; ++i) copy_to_lds(ra, base + (wave * kGemmACh + i) * 1024, aoff[i] + ko);
+        for (int i = 0; i < ACh; ++i) copy_to_lds(ra, base + (wave * ACh + i) * 1024, aoff[i] + ko);
 #pragma unroll
         for (int i = 0; i < BCh; ++i) copy_to_lds(rb, base + kGemmABytes + (wave * BCh + i) * 1024, boff[i] + (ko >> 2));
     };

@@ -518,13 +518,14 @@ WIDE_SHAPES = [(300, 1088, 257), (129, 4096, 1000), (256, 512, 512), (384, 1024,
                (131, 14336, 64)]
 
 
-@pytest.mark.parametrize("wide", [True, False])
+@pytest.mark.parametrize("tile", ["wide", "narrow"])
 @pytest.mark.parametrize("m,k,n", WIDE_SHAPES)
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
-def test_gemm_tile_widths_match_oracle(m, k, n, xdt, ydt, wide, monkeypatch):
-    print("gemm tiles", m, k, n, xdt, ydt, wide, flush=True)
+def test_gemm_tile_widths_match_oracle(m, k, n, xdt, ydt, tile, monkeypatch):
+    # narrow: 128-row tiles of 2 x 2 waves (64 x 64 each)
+    print("gemm tiles", m, k, n, xdt, ydt, tile, flush=True)
     monkeypatch.setenv("BTL_GEMM_MAX_SPLITS", "1")
-    monkeypatch.setenv("BTL_GEMM_WIDE_MIN_TILES", "1" if wide else "1000000000")
+    monkeypatch.setenv("BTL_GEMM_WIDE_MIN_TILES", "1" if tile == "wide" else "1000000000")
     x = activations(m, k, seed=m + k * 5 + n)
     x[min(7, m - 1)] = 0.0
     pt, wb, sw = make_layer(n, k, seed=n * 11 + k)
