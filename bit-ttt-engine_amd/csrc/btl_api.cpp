@@ -253,19 +253,22 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
 // [1, 16 - quantising waves] that minimises the compute waves of the busiest CU
 // when the workgroups spread evenly over the CUs (ties: the larger workgroup,
 // which quantises the token fewer times).  Llama-3-8B on 256 CUs: gate|up 14
-// (two workgroups per CU), q|k|v 6, o 4, down 8 (one each).  BTL_DEC_RQ_WPC
-// overrides it (tuning).
-int rq_waves_per_group(int64_t rb_total, int64_t k, int cus)
+// (two workgroups per CU), q|k|v 6, o 4, down 8 (one each).  With the SwiGLU
+// pairing (pair_n = the rows of gate and of up) the count is even: half the
+// waves take gate's rows, half the same rows of up.  BTL_DEC_RQ_WPC overrides
+// it (tuning).
+int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n)
 {
     const int rows = k <= 4096 ? 4 : 2;
-    const int64_t waves = rb_total * (16 / rows);
+    const int64_t waves = pair_n ? 2 * ceil_div(pair_n, rows) : rb_total * (16 / rows);
     const int hi = 16 - btl::rq_quant_waves((int)k);
+    const int step = pair_n ? 2 : 1;
     const int forced = env_int("BTL_DEC_RQ_WPC", 0);
-    if (forced >= 1 && forced <= hi) return forced;
+    if (forced >= step && forced <= hi && forced % step == 0) return forced;
     if (cus < 1) cus = 1;
-    int best = 1;
+    int best = step;
     int64_t best_cost = -1;
-    for (int w = 1; w <= hi; ++w) {
+    for (int w = step; w <= hi; w += step) {
         const int64_t cost = ceil_div(ceil_div(waves, w), cus) * w;
         if (best_cost < 0 || cost <= best_cost) {
             best = w;
@@ -396,11 +399,13 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
                       wv * rbw <= 8 && k / 16 <= (int64_t)(xf->kind == btl::XF_SWIGLU ? 2 : 1) * wv * rbw * 64 &&
                       !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
 
-    // One token row with no transform in the prologue and no SwiGLU epilogue:
-    // the row-group form (R whole rows per wave, one accumulator, workgroups of
-    // up to 16 waves of which only the first few quantise the token).
-    const bool rq = dec && m == 1 && !fuse && !swiglu_out && k % 64 == 0 && k <= 16384 &&
-                    k >= env_int("BTL_DEC_RQ_MIN_K", 1024) && env_int("BTL_DEC_RQ", 1) != 0;
+    // One token row with no transform in the prologue: the row-group form (R
+    // whole rows per wave, one accumulator, workgroups of up to 16 waves of
+    // which only the first few quantise the token), with the SwiGLU pairing for
+    // tokens transformed by a launch of their own.
+    const bool rq = dec && m == 1 && !fuse && k % 64 == 0 && k <= 16384 &&
+                    k >= env_int("BTL_DEC_RQ_MIN_K", 1024) && env_int("BTL_DEC_RQ", 1) != 0 &&
+                    (!swiglu_out || (xf && !fuse));
 
     // operand-order quantisation into the workspace (all routes but plain decode)
     const bool pre = (xf && !fuse) || !dec;
@@ -462,7 +467,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.swiglu_out = swiglu_out;
         a.rowc = rowc;
         if (rq) {
-            a.parts = rq_waves_per_group(rb, k, g_dev[dev].cus);
+            a.parts = rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0);
             e = btl::launch_gemv_rq(a, pre ? (int)btl::XK_I8O : xkind, st);
             if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
             return BTL_OK;

@@ -776,7 +776,7 @@ __device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target)
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <int XK, int R, int ST>
+template <int XK, int R, int ST, bool PAIR = false>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8 : 4))) void k_gemv_rq(GemvArgs a)
 {
     constexpr int SUB = RqShape<R>::kSub, RB = RqShape<R>::kBytes, DG = kRqDG;
@@ -784,8 +784,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8
     constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);
     constexpr bool PREQ = DecX<XK>::kPreq;
     extern __shared__ __align__(16) uint8_t sq[];  // [k + 16], operand order
-    __shared__ uint32_t s_sync[2];                 // absmax bits, arrivals
+    __shared__ uint32_t s_sync[3];                 // absmax bits, quantiser arrivals, gate arrivals
     __shared__ float s_scale;
+    __shared__ float s_gate[PAIR ? 8 * R : 1];     // PAIR: gate outputs of the workgroup's rows
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -809,6 +810,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8
     if (tid == 0) {
         s_sync[0] = 0u;
         s_sync[1] = 0u;
+        s_sync[2] = 0u;
     }
     __syncthreads();  // the counters are set before any wave uses them
 
@@ -841,24 +843,40 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8
         return;
     }
 
-    // 3. this compute wave's rows: R-row group q of the launch, in 16-row block q / SUB
-    const int q = (int)blockIdx.x * a.parts + (wave - nqw);
-    const int rbg = q / SUB;
+    // 3. this compute wave's rows.  Plain: R-row group q of the launch, in
+    //    16-row block q / SUB of its layer.  PAIR: the first half of the
+    //    compute waves take gate's row groups cw of the workgroup's span, the
+    //    second half the same rows of up.
+    const int cw = wave - nqw;
     const uint8_t* W = a.p[0].w;
     void* Y = a.p[0].y;
     int32_t* ACC = a.p[0].acc_out;
     float SW = a.p[0].sw;
     int N = a.p[0].n;
-    int RB0 = a.p[0].rb_begin;
-#pragma unroll
-    for (int i = 1; i < kMaxGroup; ++i) {
-        if (i < a.nprob && rbg >= a.p[i].rb_begin) {
-            W = a.p[i].w; Y = a.p[i].y; ACC = a.p[i].acc_out;
-            SW = a.p[i].sw; N = a.p[i].n; RB0 = a.p[i].rb_begin;
+    int row0, rows;
+    const int half = a.parts >> 1;
+    const bool isup = PAIR && cw >= half;
+    const int cp = isup ? cw - half : cw;  // PAIR: row group of the workgroup's span
+    if (PAIR) {
+        if (isup) {
+            W = a.p[1].w; Y = a.p[1].y; ACC = a.p[1].acc_out; SW = a.p[1].sw;
         }
+        row0 = ((int)blockIdx.x * half + cp) * R;
+        rows = __builtin_amdgcn_readfirstlane(max(0, min(R, N - row0)));
+    } else {
+        const int q = (int)blockIdx.x * a.parts + cw;
+        const int rbg = q / SUB;
+        int RB0 = a.p[0].rb_begin;
+#pragma unroll
+        for (int i = 1; i < kMaxGroup; ++i) {
+            if (i < a.nprob && rbg >= a.p[i].rb_begin) {
+                W = a.p[i].w; Y = a.p[i].y; ACC = a.p[i].acc_out;
+                SW = a.p[i].sw; N = a.p[i].n; RB0 = a.p[i].rb_begin;
+            }
+        }
+        row0 = (rbg - RB0) * 16 + (q - rbg * SUB) * R;  // past rb_total: no rows
+        rows = __builtin_amdgcn_readfirstlane(rbg < a.rb_total ? max(0, min(R, N - row0)) : 0);
     }
-    const int row0 = (rbg - RB0) * 16 + (q - rbg * SUB) * R;  // past rb_total: no rows
-    const int rows = __builtin_amdgcn_readfirstlane(rbg < a.rb_total ? max(0, min(R, N - row0)) : 0);
     const int rowb = K >> 2;
     const int gq = lane >> 4, il = lane & 15;
     const int rho = il / SUB, sl = SUB * gq + (il - rho * SUB);
@@ -907,9 +925,32 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8
         r = lane / 40;
         own = lane - 40 * r == 0;
     }
-    if (!own || r >= rows) return;
     const int n = row0 + r;
     const float yv = __fmul_rn((float)d, __fmul_rn(s_l, SW));
+    if (PAIR) {
+        // 6. gate's waves leave their outputs in LDS; up's waves wait for every
+        //    gate wave of the workgroup and write silu(gate) * up
+        if (!isup) {
+            if (own && r < rows) s_gate[cp * R + r] = yv;
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the LDS writes are done
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            if (lane == 0) __hip_atomic_fetch_add(&s_sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else {
+            rq_wait(&s_sync[2], (uint32_t)half);
+        }
+        if (!own || r >= rows) return;
+        if (Y) {
+            if (a.ykind == YK_BF16) ((uint16_t*)Y)[n] = f32_to_bf16(yv);
+            else ((float*)Y)[n] = yv;
+        }
+        if (ACC) ACC[n] = d;
+        if (isup) {
+            const float gv = s_gate[cp * R + r];
+            a.swiglu_out[n] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, btl_expf(-gv))), yv);
+        }
+        return;
+    }
+    if (!own || r >= rows) return;
     if (a.ykind == YK_BF16) ((uint16_t*)Y)[n] = f32_to_bf16(yv);
     else ((float*)Y)[n] = yv;
     if (ACC) ACC[n] = d;
@@ -923,14 +964,21 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, hipStream_t s)
     const int R = a.k <= 4096 ? 4 : 2;
     const int st = (int)(((int64_t)a.k * R + 4095) / 4096);
     const int nqw = rq_quant_waves(a.k);
+    const bool pair = a.swiglu_out != nullptr;
     if (a.m != 1 || a.k % 64 != 0 || a.k < 64 || a.k > 16384 || a.parts < 1 || nqw + a.parts > 16 ||
         a.rb_total < 1 || (xkind != XK_F32 && xkind != XK_BF16 && xkind != XK_I8 && xkind != XK_I8O))
         return hipErrorInvalidValue;
-    const int64_t waves = (int64_t)a.rb_total * (16 / R);
-    const dim3 grid((unsigned)((waves + a.parts - 1) / a.parts)), block((unsigned)((nqw + a.parts) * 64));
+    // SwiGLU pairing: gate and up of equal n, an even number of compute waves,
+    // operand-order int8 tokens (a transform ran ahead of the launch)
+    if (pair && (a.nprob != 2 || a.p[0].n != a.p[1].n || (a.parts & 1) || xkind != XK_I8O))
+        return hipErrorInvalidValue;
+    const int64_t groups = pair ? ((int64_t)a.p[0].n + R - 1) / R : (int64_t)a.rb_total * (16 / R);
+    const int64_t per = pair ? a.parts / 2 : a.parts;
+    const dim3 grid((unsigned)((groups + per - 1) / per)), block((unsigned)((nqw + a.parts) * 64));
     const size_t lds = (size_t)a.k + 16;
 #define BTL_RQ_XK(RV, STV)                                                                                       \
-    if (xkind == XK_BF16) hipLaunchKernelGGL((k_gemv_rq<XK_BF16, RV, STV>), grid, block, lds, s, a);          \
+    if (pair) hipLaunchKernelGGL((k_gemv_rq<XK_I8O, RV, STV, true>), grid, block, lds, s, a);                   \
+    else if (xkind == XK_BF16) hipLaunchKernelGGL((k_gemv_rq<XK_BF16, RV, STV>), grid, block, lds, s, a);   \
     else if (xkind == XK_F32) hipLaunchKernelGGL((k_gemv_rq<XK_F32, RV, STV>), grid, block, lds, s, a);       \
     else if (xkind == XK_I8) hipLaunchKernelGGL((k_gemv_rq<XK_I8, RV, STV>), grid, block, lds, s, a);         \
     else hipLaunchKernelGGL((k_gemv_rq<XK_I8O, RV, STV>), grid, block, lds, s, a);

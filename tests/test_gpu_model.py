@@ -294,13 +294,18 @@ def test_add_rmsnorm_linear_group(m, k, ns, inplace):
     assert_same(outs[0], orc.forward_i8(orc.rmsnorm(h, g, 1e-5), layers[0][1], ns[0], layers[0][2])[0], "plain")
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 256, 512), (1, 4096, 14336), (2, 512, 96), (4, 4096, 1000),
-                                   (9, 512, 256), (70, 256, 512)])
+@pytest.mark.parametrize("m,k,n,fuse", [(1, 256, 512, "1"), (1, 4096, 14336, "1"), (2, 512, 96, "1"),
+                                        (4, 4096, 1000, "1"), (9, 512, 256, "1"), (70, 256, 512, "1"),
+                                        (1, 4096, 1000, "0"), (1, 14336, 300, "0"), (1, 2048, 7, "0")])
 @pytest.mark.parametrize("with_delta", [False, True])
-def test_add_rmsnorm_swiglu(m, k, n, with_delta):
+def test_add_rmsnorm_swiglu(m, k, n, fuse, with_delta, monkeypatch):
     # decode rows (m <= 4): the gate/up kernel writes silu(gate) * up from its epilogue;
-    # (1, 4096, 14336) takes the separate norm kernel (1792 row blocks), the small ones fuse it
-    print("add_rmsnorm_swiglu", m, k, n, with_delta, flush=True)
+    # (1, 4096, 14336) takes the separate norm kernel (1792 row blocks) and the
+    # row-group decode form's pairing of gate and up waves, the small ones fuse
+    # the norm into the decode kernel; fuse "0" forces the separate norm kernel
+    # (row-group pairing with ragged n: rows past the end of a workgroup's span)
+    print("add_rmsnorm_swiglu", m, k, n, fuse, with_delta, flush=True)
+    monkeypatch.setenv("BTL_FUSE_DEC", fuse)
     rng = np.random.default_rng(m * 31 + k + n)
     h = rng.standard_normal((m, k)).astype(np.float32)
     d = rng.standard_normal((m, k)).astype(np.float32)
