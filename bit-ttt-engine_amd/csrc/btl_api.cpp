@@ -257,11 +257,11 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
 // pairing (pair_n = the rows of gate and of up) the count is even: half the
 // waves take gate's rows, half the same rows of up.  BTL_DEC_RQ_WPC overrides
 // it (tuning).
-int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n)
+int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n, bool xform)
 {
     const int rows = k <= 4096 ? 4 : 2;
     const int64_t waves = pair_n ? 2 * ceil_div(pair_n, rows) : rb_total * (16 / rows);
-    const int hi = 16 - btl::rq_quant_waves((int)k);
+    const int hi = 16 - btl::rq_quant_waves((int)k, xform);
     const int step = pair_n ? 2 : 1;
     const int forced = env_int("BTL_DEC_RQ_WPC", 0);
     if (forced >= step && forced <= hi && forced % step == 0) return forced;
@@ -394,21 +394,31 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     constexpr int64_t kFuseMaxWg = 512;
     int64_t dec_rb = 0;
     for (int i = 0; i < count; ++i) dec_rb += ceil_div(layers[i].w->n, 16);
-    const bool fuse = dec && xf && m == 1 && xkind == btl::XK_F32 && env_int("BTL_FUSE_DEC", 1) != 0 &&
-                      ceil_div(dec_rb, rbw) <= env_int("BTL_FUSE_MAX_WG", (int)kFuseMaxWg) &&
-                      wv * rbw <= 8 && k / 16 <= (int64_t)(xf->kind == btl::XF_SWIGLU ? 2 : 1) * wv * rbw * 64 &&
-                      !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
+    const int64_t fuse_max_wg = env_int("BTL_FUSE_MAX_WG", (int)kFuseMaxWg);
+    const bool xf_ok = xf && m == 1 && xkind == btl::XK_F32 && env_int("BTL_FUSE_DEC", 1) != 0 &&
+                       !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
 
-    // One token row with no transform in the prologue: the row-group form (R
-    // whole rows per wave, one accumulator, workgroups of up to 16 waves of
-    // which only the first few quantise the token), with the SwiGLU pairing for
-    // tokens transformed by a launch of their own.
-    const bool rq = dec && m == 1 && !fuse && k % 64 == 0 && k <= 16384 &&
-                    k >= env_int("BTL_DEC_RQ_MIN_K", 1024) && env_int("BTL_DEC_RQ", 1) != 0 &&
-                    (!swiglu_out || (xf && !fuse));
+    // One token row: the row-group form (R whole rows per wave, one
+    // accumulator, workgroups of up to 16 waves of which only the first few
+    // quantise the token).  Its quantising waves also apply a transform (k <=
+    // 4096, no SwiGLU epilogue, at most kFuseMaxWg workgroups: each repeats
+    // it); the SwiGLU pairing takes tokens transformed by a launch of their own.
+    const bool rq_on = dec && m == 1 && k % 64 == 0 && k <= 16384 && k >= env_int("BTL_DEC_RQ_MIN_K", 1024) &&
+                       env_int("BTL_DEC_RQ", 1) != 0;
+    bool rqx = false;
+    int rqx_wpc = 0;
+    if (rq_on && xf_ok && !swiglu_out && k <= 4096) {
+        rqx_wpc = rq_waves_per_group(dec_rb, k, g_dev[dev].cus, 0, true);
+        rqx = ceil_div(dec_rb * 4, rqx_wpc) <= fuse_max_wg;
+    }
+    // Otherwise the K-part / row-contiguous decode kernel applies a transform in
+    // its own prologue for launches of at most kFuseMaxWg workgroups.
+    const bool fuse = !rqx && dec && xf_ok && ceil_div(dec_rb, rbw) <= fuse_max_wg && wv * rbw <= 8 &&
+                      k / 16 <= (int64_t)(xf->kind == btl::XF_SWIGLU ? 2 : 1) * wv * rbw * 64;
+    const bool rq = rq_on && !fuse && (!swiglu_out || (xf && !rqx));
 
     // operand-order quantisation into the workspace (all routes but plain decode)
-    const bool pre = (xf && !fuse) || !dec;
+    const bool pre = (xf && !fuse && !rqx) || !dec;
     const int8_t* q = nullptr;
     const float* sxp = xs;
     void* ws = nullptr;
@@ -457,7 +467,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.kpart = (int)kpart;
         a.ykind = ykind;
         int xform = btl::XF_NONE;
-        if (fuse) {
+        if (fuse || rqx) {
             xform = xf->kind;
             a.x2 = (const float*)xf->x2;
             a.g = xf->g;
@@ -467,8 +477,8 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.swiglu_out = swiglu_out;
         a.rowc = rowc;
         if (rq) {
-            a.parts = rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0);
-            e = btl::launch_gemv_rq(a, pre ? (int)btl::XK_I8O : xkind, st);
+            a.parts = rqx ? rqx_wpc : rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0, false);
+            e = btl::launch_gemv_rq(a, pre ? (int)btl::XK_I8O : xkind, rqx ? xform : (int)btl::XF_NONE, st);
             if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
             return BTL_OK;
         }

@@ -68,13 +68,18 @@ constexpr int dec_row_st(int rowc) { return rowc == 1 ? 4 : 8; }
 constexpr int kDecGroups = 4;  // 16-element token groups per thread in the prologue
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t s);
 
-// One-token decode, row-group form (k_gemv_rq): m == 1, k % 64 == 0, k <= 16384,
-// no transform, no SwiGLU epilogue.  R = 4 rows per compute wave for k <= 4096,
-// else 2.  A workgroup is rq_quant_waves(k) quantising waves (two 16-element
-// token groups per thread) and a.parts compute waves, at most 16 in all;
-// a.tiles and a.kpart unused.
-constexpr int rq_quant_waves(int k) { return ((k / 16 + 1) / 2 + 63) / 64; }
-hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, hipStream_t s);
+// One-token decode, row-group form (k_gemv_rq): m == 1, k % 64 == 0, k <= 16384.
+// R = 4 rows per compute wave for k <= 4096, else 2.  A workgroup is
+// rq_quant_waves(k, xform) quantising waves (two 16-element token groups per
+// thread, one with a transform) and a.parts compute waves, at most 16 in all;
+// a.tiles and a.kpart unused.  The SwiGLU epilogue (a.swiglu_out) takes
+// operand-order int8 tokens and an even a.parts; a transform (xform, the
+// fields of the decode kernel's) takes f32 tokens and k <= 4096.
+constexpr int rq_quant_waves(int k, bool xform = false)
+{
+    return xform ? (k / 16 + 63) / 64 : ((k / 16 + 1) / 2 + 63) / 64;
+}
+hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s);
 
 // Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op or
 // k_op_order), k % 64 == 0, k < 2^24, 16-byte aligned q and w.  Up to

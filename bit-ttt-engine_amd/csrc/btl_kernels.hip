@@ -213,14 +213,12 @@ __device__ __forceinline__ uint32_t group_absmax(const uint4* v)
 // 16 f32 values -> operand-order int8 word quadruple (finite row, r = 127/a)
 __device__ __forceinline__ uint4 group_quant_f(const float* f, float r)
 {
-    int q[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) q[i] = quant_fast(f[i], r);
+    // one output word at a time (fewer live registers)
     uint4 o;
-    o.x = pack4(q[0], q[4], q[8], q[12]);
-    o.y = pack4(q[1], q[5], q[9], q[13]);
-    o.z = pack4(q[2], q[6], q[10], q[14]);
-    o.w = pack4(q[3], q[7], q[11], q[15]);
+    o.x = pack4(quant_fast(f[0], r), quant_fast(f[4], r), quant_fast(f[8], r), quant_fast(f[12], r));
+    o.y = pack4(quant_fast(f[1], r), quant_fast(f[5], r), quant_fast(f[9], r), quant_fast(f[13], r));
+    o.z = pack4(quant_fast(f[2], r), quant_fast(f[6], r), quant_fast(f[10], r), quant_fast(f[14], r));
+    o.w = pack4(quant_fast(f[3], r), quant_fast(f[7], r), quant_fast(f[11], r), quant_fast(f[15], r));
     return o;
 }
 
@@ -776,10 +774,134 @@ __device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target)
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <int XK, int R, int ST, bool PAIR = false>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8 : 4))) void k_gemv_rq(GemvArgs a)
+// The quantising waves of k_gemv_rq, f32 / bf16 / int8 tokens: the absmax
+// over the quantising waves (LDS atomic max, arrivals counted in s_sync[1]),
+// then each thread's DG groups in operand order into sq; pre-quantised rows
+// are only copied.  Ends with this wave's last arrival.
+template <int XK, int DG>
+__device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], int K, int gpr, int nqw, int nq, int tid,
+                                            int lane, uint8_t* sq, uint32_t* s_sync, float* s_scale)
 {
-    constexpr int SUB = RqShape<R>::kSub, RB = RqShape<R>::kBytes, DG = kRqDG;
+    constexpr bool PREQ = DecX<XK>::kPreq;
+    float rm = 0.0f;
+    if (!PREQ) {
+        uint32_t am = 0;
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi) am = max(am, group_absmax<XK>(xv[gi]));
+        const uint32_t v = wave_max_dpp(am);
+        if (lane == 0) {
+            __hip_atomic_fetch_max(&s_sync[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        rq_wait(&s_sync[1], (uint32_t)nqw);
+        const QParams qp = qparams(__hip_atomic_load(&s_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        rm = qp.ok ? qp.r : 0.0f;
+        if (tid == 0) *s_scale = qp.s;
+    }
+#pragma unroll
+    for (int gi = 0; gi < DG; ++gi) {
+        const int g = tid + nq * gi;
+        uint4 qv = group_quant<XK>(xv[gi], rm);
+        if (!PREQ && rm == 0.0f) qv = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
+        if (g < gpr) *(uint4*)(sq + 16 * g) = qv;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The quantising waves of k_gemv_rq with a transform (f32 tokens, one group
+// per thread): the transform of k_xform_quant on this workgroup's copy of the
+// row.  Thread t holds elements [16 t, 16 t + 16) (zeros past k), so the sum of
+// squares is the pairwise tree in index order (in-thread, the lanes' xor
+// butterfly, then the waves zero-padded to 16); XF_ADD_RMSNORM's summed row
+// goes to a.hout from workgroup 0.  Then the absmax and the quantisation as in
+// rq_quantise.  PH arrivals per wave in s_sync[1].
+template <int XF>
+__device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv, const uint4* x2v, int K, int gpr,
+                                             int nqw, uint32_t PH, int tid, int lane, int wave, uint8_t* sq,
+                                             uint32_t* s_sync, float* s_scale, float* s_ss)
+{
+    constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;
+    constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;
+    float fv[16];
+    widen16<XK_F32>(xv, fv);
+    if (X2) {
+        float u[16];
+        widen16<XK_F32>(x2v, u);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float v = fv[e];
+            fv[e] = XF == XF_SWIGLU ? __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, btl_expf(-v))), u[e]) : __fadd_rn(v, u[e]);
+        }
+        if (XF == XF_ADD_RMSNORM && a.hout && blockIdx.x == 0 && tid < gpr) {
+            float4* hp = (float4*)(a.hout + 16 * tid);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) hp[h] = make_float4(fv[4 * h], fv[4 * h + 1], fv[4 * h + 2], fv[4 * h + 3]);
+        }
+    }
+    if (XN) {
+        float t[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = __fmul_rn(fv[e], fv[e]);
+#pragma unroll
+        for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+            for (int i = 0; i < len / 2; ++i) t[i] = __fadd_rn(t[2 * i], t[2 * i + 1]);
+        const float ws = wave_pairwise_sum(t[0]);
+        if (lane == 0) {
+            s_ss[wave] = ws;
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the sum is in LDS
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        uint4 gv[4];  // the norm weight, loaded only now (fewer live registers)
+        {
+            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
+#pragma unroll
+            for (int h = 0; h < 4; ++h) gv[h] = bload(gr, tid < gpr ? 64 * tid + 16 * h : kOOB);
+        }
+        rq_wait(&s_sync[1], (uint32_t)nqw);
+        float p[16];
+#pragma unroll
+        for (int w = 0; w < 16; ++w) p[w] = w < nqw ? s_ss[w] : 0.0f;
+#pragma unroll
+        for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+            for (int i = 0; i < len / 2; ++i) p[i] = __fadd_rn(p[2 * i], p[2 * i + 1]);
+        const float inv_k = (float)(1.0 / (double)K);
+        const float d = sqrt_rn(__fadd_rn(__fmul_rn(p[0], inv_k), a.eps));
+        float gf[16];
+        widen16<XK_F32>(gv, gf);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) fv[e] = __fmul_rn(__fdiv_rn(fv[e], d), gf[e]);
+    }
+    uint32_t am = 0;
+    if (tid < gpr)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) am = max(am, __float_as_uint(fv[e]) & 0x7FFFFFFFu);
+    const uint32_t v = wave_max_dpp(am);
+    if (lane == 0) {
+        __hip_atomic_fetch_max(&s_sync[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    rq_wait(&s_sync[1], (PH - 1u) * (uint32_t)nqw);
+    const QParams qp = qparams(__hip_atomic_load(&s_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    const float rm = qp.ok ? qp.r : 0.0f;
+    if (tid == 0) *s_scale = qp.s;
+    const uint4 qv = rm != 0.0f ? group_quant_f(fv, rm) : uint4{0u, 0u, 0u, 0u};
+    if (tid < gpr) *(uint4*)(sq + 16 * tid) = qv;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int XK, int R, int ST, bool PAIR = false, int XF = XF_NONE>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 && XF == XF_NONE ? 8 : 4))) void
+k_gemv_rq(GemvArgs a)
+{
+    static_assert(XF == XF_NONE || (XK == XK_F32 && R == 4 && !PAIR), "transforms: f32 tokens, k <= 4096");
+    constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;   // a norm over the row
+    constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;    // a second input row
+    constexpr int SUB = RqShape<R>::kSub, RB = RqShape<R>::kBytes, DG = XF != XF_NONE ? 1 : kRqDG;
     constexpr int NV = DecX<XK>::kVec;
     constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);
     constexpr bool PREQ = DecX<XK>::kPreq;
@@ -787,18 +909,25 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8
     __shared__ uint32_t s_sync[3];                 // absmax bits, quantiser arrivals, gate arrivals
     __shared__ float s_scale;
     __shared__ float s_gate[PAIR ? 8 * R : 1];     // PAIR: gate outputs of the workgroup's rows
+    __shared__ float s_ss[XN ? 16 : 1];            // the norm's per-wave sums of squares
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.k;
     const int gpr = K >> 4;                               // 16-element groups of the token row
-    const int nqw = rq_quant_waves(K);
+    const int nqw = rq_quant_waves(K, XF != XF_NONE);
     const int nq = nqw * 64;
-    const uint32_t done = PREQ ? (uint32_t)nqw : 2u * (uint32_t)nqw;
+    // arrivals per quantising wave: the norm's sum (XN), the absmax (unless
+    // pre-quantised), the quantised row
+    constexpr uint32_t PH = PREQ ? 1u : (XN ? 3u : 2u);
+    const uint32_t done = PH * (uint32_t)nqw;
 
-    // 1. the quantising waves' token groups, issued before anything else
-    uint4 xv[DG][NV];
+    // The quantising waves and the compute waves take separate paths; each
+    // meets the one barrier (after which the counters are set) once.
     if (wave < nqw) {
+        // 1. the token groups (and the transform's second row), issued first
+        uint4 xv[DG][NV];
+        uint4 x2v[X2 ? 4 : 1];
         const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(K * ES));
 #pragma unroll
         for (int gi = 0; gi < DG; ++gi) {
@@ -806,42 +935,24 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8
 #pragma unroll
             for (int h = 0; h < NV; ++h) xv[gi][h] = bload(xr, g < gpr ? 16 * g * ES + 16 * h : kOOB);
         }
-    }
-    if (tid == 0) {
-        s_sync[0] = 0u;
-        s_sync[1] = 0u;
-        s_sync[2] = 0u;
-    }
-    __syncthreads();  // the counters are set before any wave uses them
-
-    if (wave < nqw) {
-        // 2. quantise (or copy a pre-quantised row) into LDS; count arrivals
-        float rm = 0.0f;
-        if (!PREQ) {
-            uint32_t am = 0;
+        if (X2) {
+            const __amdgpu_buffer_rsrc_t x2r = make_rsrc(a.x2, (uint32_t)(K * 4));
 #pragma unroll
-            for (int gi = 0; gi < DG; ++gi) am = max(am, group_absmax<XK>(xv[gi]));
-            const uint32_t v = wave_max_dpp(am);
-            if (lane == 0) {
-                __hip_atomic_fetch_max(&s_sync[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            }
-            rq_wait(&s_sync[1], (uint32_t)nqw);
-            const QParams qp = qparams(__hip_atomic_load(&s_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-            rm = qp.ok ? qp.r : 0.0f;
-            if (tid == 0) s_scale = qp.s;
+            for (int h = 0; h < 4; ++h) x2v[h] = bload(x2r, tid < gpr ? 64 * tid + 16 * h : kOOB);
         }
-#pragma unroll
-        for (int gi = 0; gi < DG; ++gi) {
-            const int g = tid + nq * gi;
-            uint4 qv = group_quant<XK>(xv[gi], rm);
-            if (!PREQ && rm == 0.0f) qv = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
-            if (g < gpr) *(uint4*)(sq + 16 * g) = qv;
+        if (tid == 0) {
+            s_sync[0] = 0u;
+            s_sync[1] = 0u;
+            s_sync[2] = 0u;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __syncthreads();
+        if (XF != XF_NONE)
+            rq_transform<XF>(a, xv[0], x2v, K, gpr, nqw, PH, tid, lane, wave, sq, s_sync, &s_scale, s_ss);
+        else
+            rq_quantise<XK, DG>(xv, K, gpr, nqw, nq, tid, lane, sq, s_sync, &s_scale);
         return;
     }
+    __syncthreads();
 
     // 3. this compute wave's rows.  Plain: R-row group q of the launch, in
     //    16-row block q / SUB of its layer.  PAIR: the first half of the
@@ -959,15 +1070,38 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 ? 8
 // Loads per compute wave: ceil(k * R / 4096); R = 4 for k <= 4096 (ST 1..4),
 // R = 2 above (ST 3..8, k <= 16384).  Workgroup: rq_quant_waves(k) + a.parts
 // waves, at most 16.
-hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, hipStream_t s)
+hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s)
 {
     const int R = a.k <= 4096 ? 4 : 2;
     const int st = (int)(((int64_t)a.k * R + 4095) / 4096);
-    const int nqw = rq_quant_waves(a.k);
+    const int nqw = rq_quant_waves(a.k, xform != XF_NONE);
     const bool pair = a.swiglu_out != nullptr;
     if (a.m != 1 || a.k % 64 != 0 || a.k < 64 || a.k > 16384 || a.parts < 1 || nqw + a.parts > 16 ||
         a.rb_total < 1 || (xkind != XK_F32 && xkind != XK_BF16 && xkind != XK_I8 && xkind != XK_I8O))
         return hipErrorInvalidValue;
+    if (xform != XF_NONE) {
+        // a transform in the quantising waves: f32 tokens, k <= 4096, the inputs
+        // it reads; the summed residual (XF_ADD_RMSNORM) goes to another buffer
+        if (xkind != XK_F32 || R != 4 || pair || !a.x2 == (xform == XF_ADD_RMSNORM || xform == XF_SWIGLU) ||
+            ((xform == XF_RMSNORM || xform == XF_ADD_RMSNORM) && !a.g) || (a.hout && (const void*)a.hout == a.x))
+            return hipErrorInvalidValue;
+        const dim3 grid((unsigned)(((int64_t)a.rb_total * 4 + a.parts - 1) / a.parts)),
+            block((unsigned)((nqw + a.parts) * 64));
+        const size_t lds = (size_t)a.k + 16;
+#define BTL_RQ_XF(STV)                                                                                        \
+    if (xform == XF_RMSNORM) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_RMSNORM>), grid, block, lds, s, a); \
+    else if (xform == XF_ADD_RMSNORM)                                                                           \
+        hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_ADD_RMSNORM>), grid, block, lds, s, a);         \
+    else hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_SWIGLU>), grid, block, lds, s, a);
+        switch (st) {
+        case 1: { BTL_RQ_XF(1) break; }
+        case 2: { BTL_RQ_XF(2) break; }
+        case 3: { BTL_RQ_XF(3) break; }
+        default: { BTL_RQ_XF(4) break; }
+        }
+#undef BTL_RQ_XF
+        return hipGetLastError();
+    }
     // SwiGLU pairing: gate and up of equal n, an even number of compute waves,
     // operand-order int8 tokens (a transform ran ahead of the launch)
     if (pair && (a.nprob != 2 || a.p[0].n != a.p[1].n || (a.parts & 1) || xkind != XK_I8O))

@@ -342,6 +342,43 @@ def test_swiglu_group_one_token_fused(k):
     assert_same(y, orc.forward_i8(orc.swiglu(gte, up), wb, n, sw)[0], "swiglu fused")
 
 
+@pytest.mark.parametrize("form", ["rq", "dec"])
+@pytest.mark.parametrize("kind", ["rmsnorm", "add_rmsnorm", "swiglu"])
+@pytest.mark.parametrize("k", [1024, 1088, 2048, 3008, 4096])
+def test_one_token_transforms_both_forms(k, kind, form, monkeypatch):
+    # m = 1, f32, k <= 4096: the transform runs in the row-group form's
+    # quantising waves (rq) or in the decode kernel's prologue (dec); both
+    # must give the oracle's bits.  n = 150 leaves a partial row group.
+    print("one-token transform", k, kind, form, flush=True)
+    if form == "dec":
+        monkeypatch.setenv("BTL_DEC_RQ", "0")
+    rng = np.random.default_rng(k * 3 + len(kind))
+    x = (rng.standard_normal((1, k)) * 2).astype(np.float32)
+    x2 = rng.standard_normal((1, k)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    n = 150
+    wb, sw = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), sw, (n, k), DEV)
+    xt, x2t, gt = (torch.from_numpy(a).to(DEV) for a in (x, x2, g))
+    if kind == "swiglu":
+        y = bl.swiglu_linear_group([pt], xt, x2t)[0]
+        assert_same(y, orc.forward_i8(orc.swiglu(x, x2), wb, n, sw)[0], "swiglu")
+        return
+    out = torch.empty((1, n), device=DEV)
+    c = pt.as_c()
+    arr = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(c))
+    ys = (ctypes.c_void_p * 1)(out.data_ptr())
+    ho = torch.full_like(xt, 5.0)
+    add = kind == "add_rmsnorm"
+    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 1, xt.data_ptr(), x2t.data_ptr() if add else None,
+                                                 ho.data_ptr() if add else None, gt.data_ptr(), 1e-5, 1, k,
+                                                 bl.BTL_F32, None, 0, stream()))
+    hs = (x + x2).astype(np.float32) if add else x
+    if add:
+        assert_same(ho, hs, "residual")
+    assert_same(out, orc.forward_i8(orc.rmsnorm(hs, g, 1e-5), wb, n, sw)[0], kind)
+
+
 def test_add_rmsnorm_rejects_partial_overlap():
     k = 256
     h = torch.zeros((2, k), device=DEV)
