@@ -257,11 +257,11 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
 // pairing (pair_n = the rows of gate and of up) the count is even: half the
 // waves take gate's rows, half the same rows of up.  BTL_DEC_RQ_WPC overrides
 // it (tuning).
-int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n, bool xform)
+int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n, bool xform, int m)
 {
     const int rows = k <= 4096 ? 4 : 2;
     const int64_t waves = pair_n ? 2 * ceil_div(pair_n, rows) : rb_total * (16 / rows);
-    const int hi = 16 - btl::rq_quant_waves((int)k, xform);
+    const int hi = 16 - btl::rq_quant_waves((int)k, xform ? 1 : 2, m);
     const int step = pair_n ? 2 : 1;
     const int forced = env_int("BTL_DEC_RQ_WPC", 0);
     if (forced >= step && forced <= hi && forced % step == 0) return forced;
@@ -345,7 +345,12 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     // measured on MI355X: the GEMM is faster from m = 64, Llama-3-8B MLP
     // shapes) and GEMM: K split over workgroups when the output has few tiles.
     int rbw = 1;
-    int wv = env_int("BTL_GEMV_DEC", 1) != 0 ? dec_waves(m, k, &rbw) : 0;
+    // Plain launches of 3..4 token rows take the batched route (measured on
+    // MI355X, Llama-3-8B MLP at m = 4: 24.8 against 29.2 us per layer through
+    // the decode kernel); a transform or the SwiGLU epilogue keeps the decode
+    // kernel.  BTL_GEMV_DEC_MAX_M overrides the limit (tuning, tests).
+    const int dec_max_m = xf || swiglu_out ? 4 : env_int("BTL_GEMV_DEC_MAX_M", 2);
+    int wv = env_int("BTL_GEMV_DEC", 1) != 0 && m <= dec_max_m ? dec_waves(m, k, &rbw) : 0;
     const bool dec = wv > 0;
     // One token row, k a multiple of 64 up to 16384: the row-contiguous form
     // (whole weight rows per wave, 1 KB per load instruction, no K parts).
@@ -398,17 +403,19 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     const bool xf_ok = xf && m == 1 && xkind == btl::XK_F32 && env_int("BTL_FUSE_DEC", 1) != 0 &&
                        !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
 
-    // One token row: the row-group form (R whole rows per wave, one
-    // accumulator, workgroups of up to 16 waves of which only the first few
-    // quantise the token).  Its quantising waves also apply a transform (k <=
+    // One token row (two for k <= 4096; measured on MI355X, Llama-3-8B MLP: the
+    // K-part form is faster from three rows on, where the quantising waves
+    // take half of every workgroup): the row-group form (R whole rows per
+    // wave, one accumulator per token row, workgroups of up to 16 waves of
+    // which only the first few quantise the tokens).  Its quantising waves also apply a transform (k <=
     // 4096, no SwiGLU epilogue, at most kFuseMaxWg workgroups: each repeats
     // it); the SwiGLU pairing takes tokens transformed by a launch of their own.
-    const bool rq_on = dec && m == 1 && k % 64 == 0 && k <= 16384 && k >= env_int("BTL_DEC_RQ_MIN_K", 1024) &&
-                       env_int("BTL_DEC_RQ", 1) != 0;
+    const bool rq_on = dec && k % 64 == 0 && k >= env_int("BTL_DEC_RQ_MIN_K", 1024) && env_int("BTL_DEC_RQ", 1) != 0 &&
+                       ((m == 1 && k <= 16384) || (m == 2 && k <= 4096 && !xf && !swiglu_out));
     bool rqx = false;
     int rqx_wpc = 0;
     if (rq_on && xf_ok && !swiglu_out && k <= 4096) {
-        rqx_wpc = rq_waves_per_group(dec_rb, k, g_dev[dev].cus, 0, true);
+        rqx_wpc = rq_waves_per_group(dec_rb, k, g_dev[dev].cus, 0, true, 1);
         rqx = ceil_div(dec_rb * 4, rqx_wpc) <= fuse_max_wg;
     }
     // Otherwise the K-part / row-contiguous decode kernel applies a transform in
@@ -477,7 +484,15 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.swiglu_out = swiglu_out;
         a.rowc = rowc;
         if (rq) {
-            a.parts = rqx ? rqx_wpc : rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0, false);
+            a.parts = rqx ? rqx_wpc
+                          : rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0, false, (int)m);
+            // one token group per quantising thread when the workgroup has room
+            // for the quantising waves that takes (one token row, k <= 4096): a
+            // shorter prologue for the launches of few compute waves
+            a.tiles = rqx || (m == 1 && k <= 4096 && !swiglu_out && btl::rq_quant_waves((int)k, 1) + a.parts <= 16 &&
+                              env_int("BTL_DEC_RQ_DG", 0) != 2)
+                          ? 1
+                          : 2;
             e = btl::launch_gemv_rq(a, pre ? (int)btl::XK_I8O : xkind, rqx ? xform : (int)btl::XF_NONE, st);
             if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
             return BTL_OK;

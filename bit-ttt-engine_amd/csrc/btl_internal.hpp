@@ -68,17 +68,15 @@ constexpr int dec_row_st(int rowc) { return rowc == 1 ? 4 : 8; }
 constexpr int kDecGroups = 4;  // 16-element token groups per thread in the prologue
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t s);
 
-// One-token decode, row-group form (k_gemv_rq): m == 1, k % 64 == 0, k <= 16384.
+// Decode, row-group form (k_gemv_rq): m == 1, k % 64 == 0, k <= 16384, or m == 2
+// token rows with k <= 4096 (no transform, no SwiGLU epilogue, dg = 2).
 // R = 4 rows per compute wave for k <= 4096, else 2.  A workgroup is
-// rq_quant_waves(k, xform) quantising waves (two 16-element token groups per
-// thread, one with a transform) and a.parts compute waves, at most 16 in all;
-// a.tiles and a.kpart unused.  The SwiGLU epilogue (a.swiglu_out) takes
-// operand-order int8 tokens and an even a.parts; a transform (xform, the
-// fields of the decode kernel's) takes f32 tokens and k <= 4096.
-constexpr int rq_quant_waves(int k, bool xform = false)
-{
-    return xform ? (k / 16 + 63) / 64 : ((k / 16 + 1) / 2 + 63) / 64;
-}
+// rq_quant_waves(k, dg) quantising waves, dg = a.tiles 16-element token groups
+// per thread (1 for k <= 4096 only, else 2), and a.parts compute waves, at most
+// 16 in all; a.kpart unused.  The SwiGLU epilogue (a.swiglu_out) takes
+// operand-order int8 tokens, dg = 2 and an even a.parts; a transform (xform,
+// the fields of the decode kernel's) takes f32 tokens, k <= 4096 and dg = 1.
+constexpr int rq_quant_waves(int k, int dg, int m = 1) { return ((m * (k / 16) + dg - 1) / dg + 63) / 64; }
 hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s);
 
 // Prefill GEMM (k_gemm_i8): q is [m, k] int8 in operand order (k_quant_op or

@@ -756,7 +756,6 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
 // barrier, so no wave waits for another wave's loads to issue (the memory
 // queue of a CU back-pressures the issue of later loads for microseconds).
 // Every wait is bounded by kRqSpinMax polls.
-constexpr int kRqDG = 2;               // token groups per quantising thread
 constexpr int kRqSpinMax = 1 << 22;    // bound of every LDS poll (~0.1 s)
 
 template <int R>
@@ -774,36 +773,61 @@ __device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target)
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// The quantising waves of k_gemv_rq, f32 / bf16 / int8 tokens: the absmax
-// over the quantising waves (LDS atomic max, arrivals counted in s_sync[1]),
-// then each thread's DG groups in operand order into sq; pre-quantised rows
-// are only copied.  Ends with this wave's last arrival.
-template <int XK, int DG>
-__device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], int K, int gpr, int nqw, int nq, int tid,
-                                            int lane, uint8_t* sq, uint32_t* s_sync, float* s_scale)
+// The quantising waves of k_gemv_rq, f32 / bf16 / int8 tokens: thread t
+// holds groups t + nq gi of the MT x gpr groups of the token rows (row g /
+// gpr).  The absmax of every row over the quantising waves (LDS atomic max per
+// row, arrivals counted in s_sync[1]), then the groups in operand order into
+// sq (row stride k + 16); pre-quantised rows are only copied.  Ends with this
+// wave's last arrival.
+template <int XK, int DG, int MT>
+__device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], int K, int gpr, int mt, int nqw,
+                                            int nq, int tid, int lane, uint8_t* sq, uint32_t* s_sync,
+                                            uint32_t* s_amax, float* s_scale)
 {
     constexpr bool PREQ = DecX<XK>::kPreq;
-    float rm = 0.0f;
-    if (!PREQ) {
-        uint32_t am = 0;
+    const int ng = mt * gpr;
+    float rm[DG];
 #pragma unroll
-        for (int gi = 0; gi < DG; ++gi) am = max(am, group_absmax<XK>(xv[gi]));
-        const uint32_t v = wave_max_dpp(am);
-        if (lane == 0) {
-            __hip_atomic_fetch_max(&s_sync[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int gi = 0; gi < DG; ++gi) rm[gi] = 0.0f;
+    if (!PREQ) {
+        uint32_t am[MT];
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm) am[mm] = 0u;
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi) {
+            const int g = tid + nq * gi;
+            const uint32_t v = g < ng ? group_absmax<XK>(xv[gi]) : 0u;
+            const int row = MT == 1 ? 0 : g / gpr;
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm) am[mm] = (MT == 1 || mm == row) ? max(am[mm], v) : am[mm];
         }
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm) {
+            if (mm < mt) {
+                const uint32_t v = wave_max_dpp(am[mm]);
+                if (lane == 0) __hip_atomic_fetch_max(&s_amax[mm], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+        if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         rq_wait(&s_sync[1], (uint32_t)nqw);
-        const QParams qp = qparams(__hip_atomic_load(&s_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-        rm = qp.ok ? qp.r : 0.0f;
-        if (tid == 0) *s_scale = qp.s;
+        // lane mm holds row mm's parameters
+        const QParams qp = qparams(
+            __hip_atomic_load(&s_amax[MT == 1 ? 0 : min(lane, mt - 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        const float rl = qp.ok ? qp.r : 0.0f;
+        if (tid < mt) s_scale[tid] = qp.s;
+#pragma unroll
+        for (int gi = 0; gi < DG; ++gi) {
+            const int g = tid + nq * gi;
+            rm[gi] = MT == 1 ? rl : __shfl(rl, min(g / gpr, mt - 1), 64);
+        }
     }
 #pragma unroll
     for (int gi = 0; gi < DG; ++gi) {
         const int g = tid + nq * gi;
-        uint4 qv = group_quant<XK>(xv[gi], rm);
-        if (!PREQ && rm == 0.0f) qv = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
-        if (g < gpr) *(uint4*)(sq + 16 * g) = qv;
+        uint4 qv = group_quant<XK>(xv[gi], rm[gi]);
+        if (!PREQ && rm[gi] == 0.0f) qv = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
+        const int row = MT == 1 ? 0 : g / gpr;
+        if (g < ng) *(uint4*)(sq + row * (K + 16) + 16 * (g - row * gpr)) = qv;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -819,7 +843,7 @@ __device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], i
 template <int XF>
 __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv, const uint4* x2v, int K, int gpr,
                                              int nqw, uint32_t PH, int tid, int lane, int wave, uint8_t* sq,
-                                             uint32_t* s_sync, float* s_scale, float* s_ss)
+                                             uint32_t* s_sync, uint32_t* s_amax, float* s_scale, float* s_ss)
 {
     constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;
     constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;
@@ -881,41 +905,46 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv,
         for (int e = 0; e < 16; ++e) am = max(am, __float_as_uint(fv[e]) & 0x7FFFFFFFu);
     const uint32_t v = wave_max_dpp(am);
     if (lane == 0) {
-        __hip_atomic_fetch_max(&s_sync[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_fetch_max(&s_amax[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     rq_wait(&s_sync[1], (PH - 1u) * (uint32_t)nqw);
-    const QParams qp = qparams(__hip_atomic_load(&s_sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    const QParams qp = qparams(__hip_atomic_load(&s_amax[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     const float rm = qp.ok ? qp.r : 0.0f;
-    if (tid == 0) *s_scale = qp.s;
+    if (tid == 0) s_scale[0] = qp.s;
     const uint4 qv = rm != 0.0f ? group_quant_f(fv, rm) : uint4{0u, 0u, 0u, 0u};
     if (tid < gpr) *(uint4*)(sq + 16 * tid) = qv;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-template <int XK, int R, int ST, bool PAIR = false, int XF = XF_NONE>
+template <int XK, int R, int ST, bool PAIR = false, int XF = XF_NONE, int DG = 2, int MT = 1>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 && XF == XF_NONE ? 8 : 4))) void
 k_gemv_rq(GemvArgs a)
 {
-    static_assert(XF == XF_NONE || (XK == XK_F32 && R == 4 && !PAIR), "transforms: f32 tokens, k <= 4096");
+    static_assert(XF == XF_NONE || (XK == XK_F32 && R == 4 && !PAIR && DG == 1 && MT == 1),
+                  "transforms: one f32 token row, k <= 4096");
+    static_assert(DG == 1 || DG == 2, "one or two token groups per quantising thread");
+    static_assert(MT == 1 || (MT == 2 && R == 4 && !PAIR), "two token rows: k <= 4096, no SwiGLU epilogue");
     constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;   // a norm over the row
     constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;    // a second input row
-    constexpr int SUB = RqShape<R>::kSub, RB = RqShape<R>::kBytes, DG = XF != XF_NONE ? 1 : kRqDG;
+    constexpr int SUB = RqShape<R>::kSub, RB = RqShape<R>::kBytes;
     constexpr int NV = DecX<XK>::kVec;
     constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);
     constexpr bool PREQ = DecX<XK>::kPreq;
-    extern __shared__ __align__(16) uint8_t sq[];  // [k + 16], operand order
-    __shared__ uint32_t s_sync[3];                 // absmax bits, quantiser arrivals, gate arrivals
-    __shared__ float s_scale;
+    extern __shared__ __align__(16) uint8_t sq[];  // [MT][k + 16], operand order
+    __shared__ uint32_t s_sync[3];                 // (unused), quantiser arrivals, gate arrivals
+    __shared__ uint32_t s_amax[MT];                // absmax bits of each token row
+    __shared__ float s_scale[MT];
     __shared__ float s_gate[PAIR ? 8 * R : 1];     // PAIR: gate outputs of the workgroup's rows
     __shared__ float s_ss[XN ? 16 : 1];            // the norm's per-wave sums of squares
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = a.k;
-    const int gpr = K >> 4;                               // 16-element groups of the token row
-    const int nqw = rq_quant_waves(K, XF != XF_NONE);
+    const int gpr = K >> 4;                               // 16-element groups of a token row
+    const int mt = MT == 1 ? 1 : a.m;
+    const int nqw = rq_quant_waves(K, DG, mt);
     const int nq = nqw * 64;
     // arrivals per quantising wave: the norm's sum (XN), the absmax (unless
     // pre-quantised), the quantised row
@@ -928,28 +957,25 @@ k_gemv_rq(GemvArgs a)
         // 1. the token groups (and the transform's second row), issued first
         uint4 xv[DG][NV];
         uint4 x2v[X2 ? 4 : 1];
-        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(K * ES));
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(mt * K * ES));
 #pragma unroll
         for (int gi = 0; gi < DG; ++gi) {
             const int g = tid + nq * gi;
 #pragma unroll
-            for (int h = 0; h < NV; ++h) xv[gi][h] = bload(xr, g < gpr ? 16 * g * ES + 16 * h : kOOB);
+            for (int h = 0; h < NV; ++h) xv[gi][h] = bload(xr, g < mt * gpr ? 16 * g * ES + 16 * h : kOOB);
         }
         if (X2) {
             const __amdgpu_buffer_rsrc_t x2r = make_rsrc(a.x2, (uint32_t)(K * 4));
 #pragma unroll
             for (int h = 0; h < 4; ++h) x2v[h] = bload(x2r, tid < gpr ? 64 * tid + 16 * h : kOOB);
         }
-        if (tid == 0) {
-            s_sync[0] = 0u;
-            s_sync[1] = 0u;
-            s_sync[2] = 0u;
-        }
+        if (tid < 3) s_sync[tid] = 0u;
+        if (tid < MT) s_amax[tid] = 0u;
         __syncthreads();
         if (XF != XF_NONE)
-            rq_transform<XF>(a, xv[0], x2v, K, gpr, nqw, PH, tid, lane, wave, sq, s_sync, &s_scale, s_ss);
+            rq_transform<XF>(a, xv[0], x2v, K, gpr, nqw, PH, tid, lane, wave, sq, s_sync, s_amax, s_scale, s_ss);
         else
-            rq_quantise<XK, DG>(xv, K, gpr, nqw, nq, tid, lane, sq, s_sync, &s_scale);
+            rq_quantise<XK, DG, MT>(xv, K, gpr, mt, nqw, nq, tid, lane, sq, s_sync, s_amax, s_scale);
         return;
     }
     __syncthreads();
@@ -1000,42 +1026,61 @@ k_gemv_rq(GemvArgs a)
                                                wr, b < rowb ? rho * rowb + b : kOOB, 0, kCachePolicyNT));
     }
     rq_wait(&s_sync[1], done);
-    const float s_l = PREQ ? a.xs[0] : s_scale;
 
-    // 4. one accumulator over every load; slices past the row read the
-    //    activations at k = 0 (their weights are zero)
-    v4i acc = v4i{0, 0, 0, 0};
+    // 4. one accumulator per token row over every load; slices past the row
+    //    read the activations at k = 0 (their weights are zero), token rows
+    //    past m read row 0 (never stored)
+    v4i acc[MT];
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) acc[mm] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int t = 0; t < ST; ++t) {
         const int ko = 4 * (t * RB + 16 * sl);
-        const uint8_t* bj = sq + (ko < K ? ko : 0);
-        const v4i b0 = *(const v4i*)(bj + 0);
-        const v4i b1 = *(const v4i*)(bj + 16);
-        const v4i b2 = *(const v4i*)(bj + 32);
-        const v4i b3 = *(const v4i*)(bj + 48);
         const uint4 cur = buf[t];
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc, 0, 0, 0);
+        const uint32_t wv[4] = {cur.x, cur.y, cur.z, cur.w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const v4i aw = unpack16(wv[h]);
+#pragma unroll
+            for (int mm = 0; mm < MT; ++mm) {
+                const uint8_t* bj = sq + (mm < mt ? mm : 0) * (K + 16) + (ko < K ? ko : 0);
+                acc[mm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aw, *(const v4i*)(bj + 16 * h), acc[mm], 0, 0, 0);
+            }
+        }
     }
 
     // 5. quad position 0 gathers register v of quad lane v (quad_perm
     //    broadcasts of lanes 1, 2, 3): lanes 20 rho (R = 4) hold row rho; for
     //    R = 2 lanes 40 rho add their half from lane 40 rho + 20
-    int d = acc[0] + __builtin_amdgcn_update_dpp(0, acc[1], 0x55, 0xF, 0xF, true);
-    d += __builtin_amdgcn_update_dpp(0, acc[2], 0xAA, 0xF, 0xF, true);
-    d += __builtin_amdgcn_update_dpp(0, acc[3], 0xFF, 0xF, 0xF, true);
-    int r;
-    bool own;
-    if (R == 4) {
-        r = lane / 20;
-        own = lane - 20 * r == 0;
-    } else {
-        d += __shfl_down(d, 20, 64);
-        r = lane / 40;
-        own = lane - 40 * r == 0;
+    int dm[MT];
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+        int d = acc[mm][0] + __builtin_amdgcn_update_dpp(0, acc[mm][1], 0x55, 0xF, 0xF, true);
+        d += __builtin_amdgcn_update_dpp(0, acc[mm][2], 0xAA, 0xF, 0xF, true);
+        d += __builtin_amdgcn_update_dpp(0, acc[mm][3], 0xFF, 0xF, 0xF, true);
+        if (R == 2) d += __shfl_down(d, 20, 64);
+        dm[mm] = d;
     }
+    const int r = R == 4 ? lane / 20 : lane / 40;
+    const bool own = lane - (R == 4 ? 20 : 40) * r == 0;
+    if (MT > 1) {
+        if (!own || r >= rows) return;
+        const int n = row0 + r;
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm) {
+            if (mm < mt) {
+                const float s_x = PREQ ? a.xs[mm] : s_scale[mm];
+                const float yv = __fmul_rn((float)dm[mm], __fmul_rn(s_x, SW));
+                const int64_t o = (int64_t)mm * N + n;
+                if (a.ykind == YK_BF16) ((uint16_t*)Y)[o] = f32_to_bf16(yv);
+                else ((float*)Y)[o] = yv;
+                if (ACC) ACC[o] = dm[mm];
+            }
+        }
+        return;
+    }
+    const int d = dm[0];
+    const float s_l = PREQ ? a.xs[0] : s_scale[0];
     const int n = row0 + r;
     const float yv = __fmul_rn((float)d, __fmul_rn(s_l, SW));
     if (PAIR) {
@@ -1074,10 +1119,14 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
 {
     const int R = a.k <= 4096 ? 4 : 2;
     const int st = (int)(((int64_t)a.k * R + 4095) / 4096);
-    const int nqw = rq_quant_waves(a.k, xform != XF_NONE);
+    const int dg = a.tiles;
+    const int nqw = rq_quant_waves(a.k, dg, a.m);
     const bool pair = a.swiglu_out != nullptr;
-    if (a.m != 1 || a.k % 64 != 0 || a.k < 64 || a.k > 16384 || a.parts < 1 || nqw + a.parts > 16 ||
-        a.rb_total < 1 || (xkind != XK_F32 && xkind != XK_BF16 && xkind != XK_I8 && xkind != XK_I8O))
+    if ((dg != 1 && dg != 2) || (dg == 1 && (R != 4 || pair)) || (xform != XF_NONE && dg != 1))
+        return hipErrorInvalidValue;
+    if (a.m < 1 || a.m > 2 || (a.m > 1 && (R != 4 || pair || xform != XF_NONE || dg != 2)) || a.k % 64 != 0 ||
+        a.k < 64 || a.k > 16384 || a.parts < 1 || nqw + a.parts > 16 || a.rb_total < 1 ||
+        (xkind != XK_F32 && xkind != XK_BF16 && xkind != XK_I8 && xkind != XK_I8O))
         return hipErrorInvalidValue;
     if (xform != XF_NONE) {
         // a transform in the quantising waves: f32 tokens, k <= 4096, the inputs
@@ -1089,10 +1138,10 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
             block((unsigned)((nqw + a.parts) * 64));
         const size_t lds = (size_t)a.k + 16;
 #define BTL_RQ_XF(STV)                                                                                        \
-    if (xform == XF_RMSNORM) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_RMSNORM>), grid, block, lds, s, a); \
+    if (xform == XF_RMSNORM) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_RMSNORM, 1>), grid, block, lds, s, a); \
     else if (xform == XF_ADD_RMSNORM)                                                                           \
-        hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_ADD_RMSNORM>), grid, block, lds, s, a);         \
-    else hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_SWIGLU>), grid, block, lds, s, a);
+        hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_ADD_RMSNORM, 1>), grid, block, lds, s, a);      \
+    else hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_SWIGLU, 1>), grid, block, lds, s, a);
         switch (st) {
         case 1: { BTL_RQ_XF(1) break; }
         case 2: { BTL_RQ_XF(2) break; }
@@ -1109,13 +1158,18 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
     const int64_t groups = pair ? ((int64_t)a.p[0].n + R - 1) / R : (int64_t)a.rb_total * (16 / R);
     const int64_t per = pair ? a.parts / 2 : a.parts;
     const dim3 grid((unsigned)((groups + per - 1) / per)), block((unsigned)((nqw + a.parts) * 64));
-    const size_t lds = (size_t)a.k + 16;
+    const int mt = a.m;
+    const size_t lds = (size_t)mt * (a.k + 16);
+#define BTL_RQ_DG(XKV, RV, STV)                                                                                    \
+    if (RV == 4 && mt == 2) hipLaunchKernelGGL((k_gemv_rq<XKV, 4, STV, false, XF_NONE, 2, 2>), grid, block, lds, s, a); \
+    else if (RV == 4 && dg == 1) hipLaunchKernelGGL((k_gemv_rq<XKV, RV, STV, false, XF_NONE, 1>), grid, block, lds, s, a); \
+    else hipLaunchKernelGGL((k_gemv_rq<XKV, RV, STV>), grid, block, lds, s, a);
 #define BTL_RQ_XK(RV, STV)                                                                                       \
     if (pair) hipLaunchKernelGGL((k_gemv_rq<XK_I8O, RV, STV, true>), grid, block, lds, s, a);                   \
-    else if (xkind == XK_BF16) hipLaunchKernelGGL((k_gemv_rq<XK_BF16, RV, STV>), grid, block, lds, s, a);   \
-    else if (xkind == XK_F32) hipLaunchKernelGGL((k_gemv_rq<XK_F32, RV, STV>), grid, block, lds, s, a);       \
-    else if (xkind == XK_I8) hipLaunchKernelGGL((k_gemv_rq<XK_I8, RV, STV>), grid, block, lds, s, a);         \
-    else hipLaunchKernelGGL((k_gemv_rq<XK_I8O, RV, STV>), grid, block, lds, s, a);
+    else if (xkind == XK_BF16) { BTL_RQ_DG(XK_BF16, RV, STV) }                                                  \
+    else if (xkind == XK_F32) { BTL_RQ_DG(XK_F32, RV, STV) }                                                    \
+    else if (xkind == XK_I8) { BTL_RQ_DG(XK_I8, RV, STV) }                                                      \
+    else { BTL_RQ_DG(XK_I8O, RV, STV) }
     if (R == 4) {
         switch (st) {
         case 1: { BTL_RQ_XK(4, 1) break; }
@@ -1134,6 +1188,7 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
         }
     }
 #undef BTL_RQ_XK
+#undef BTL_RQ_DG
     return hipGetLastError();
 }
 

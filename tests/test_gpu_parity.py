@@ -135,6 +135,7 @@ def test_decode_k_parts_are_exact(parts, k, m, monkeypatch):
     monkeypatch.setenv("BTL_GEMV_DEC_PARTS", parts)
     monkeypatch.setenv("BTL_DEC_ROW", "0")
     monkeypatch.setenv("BTL_DEC_RQ", "0")
+    monkeypatch.setenv("BTL_GEMV_DEC_MAX_M", "4")
     acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
@@ -238,15 +239,20 @@ RQ_CASES = [(4096, None), (4096, "1"), (4096, "5"), (4096, "14"), (1024, None), 
             (14336, "9"), (16384, None)]
 
 
+@pytest.mark.parametrize("dg", ["auto", "2"])
 @pytest.mark.parametrize("k,wpc", RQ_CASES)
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
-def test_decode_row_group_form_exact(k, wpc, xdt, monkeypatch):
-    print("row-group form", k, wpc, xdt, flush=True)
+def test_decode_row_group_form_exact(k, wpc, xdt, dg, monkeypatch):
+    # dg "2": two token groups per quantising thread even where the launch
+    # would take one (k <= 4096 and room in the workgroup)
+    print("row-group form", k, wpc, xdt, dg, flush=True)
     n = 330
     x = activations(1, k, seed=k + 7)
     pt, wb, sw = make_layer(n, k, seed=k + 8)
     xt = to_dev(x, xdt)
     monkeypatch.setenv("BTL_DEC_RQ_MIN_K", "64")
+    if dg == "2":
+        monkeypatch.setenv("BTL_DEC_RQ_DG", "2")
     if wpc:
         monkeypatch.setenv("BTL_DEC_RQ_WPC", wpc)
     acc = torch.empty((1, n), dtype=torch.int32, device=DEV)
@@ -259,6 +265,38 @@ def test_decode_row_group_form_exact(k, wpc, xdt, monkeypatch):
     monkeypatch.setenv("BTL_DEC_RQ", "0")
     monkeypatch.setenv("BTL_DEC_ROW", "0")
     acc2 = torch.empty((1, n), dtype=torch.int32, device=DEV)
+    y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
+    assert torch.equal(acc, acc2) and torch.equal(y, y2)
+
+
+# Two token rows, k <= 4096: the row-group form with one accumulator per token
+# row (every unpacked weight word feeds each row's MFMA) and a per-row absmax
+# over the quantising waves; three and four rows take the batched route.  Every
+# route gives the oracle's bits and those of the K-part form.
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("k", [1024, 1088, 2048, 3072, 4096])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_decode_row_group_form_token_rows(m, k, xdt, monkeypatch):
+    print("row-group form, token rows", m, k, xdt, flush=True)
+    n = 330
+    x = activations(m, k, seed=m * 100 + k)
+    x[m - 1, 3] = np.float32(-25.0)
+    if m == 3:
+        x[1] = 0.0  # a zero row among others
+    pt, wb, sw = make_layer(n, k, seed=k + m)
+    xt = to_dev(x, xdt)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert_f32_identical(y, yr)
+    q, s = bl.quantize_act(xt)
+    acc1 = torch.empty_like(acc)
+    y1 = bl.linear_i8(q, s, pt, acc_out=acc1)
+    assert torch.equal(acc, acc1) and torch.equal(y, y1)
+    monkeypatch.setenv("BTL_DEC_RQ", "0")
+    monkeypatch.setenv("BTL_GEMV_DEC_MAX_M", "4")
+    acc2 = torch.empty_like(acc)
     y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
     assert torch.equal(acc, acc2) and torch.equal(y, y2)
 
