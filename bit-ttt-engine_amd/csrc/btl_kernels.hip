@@ -841,7 +841,8 @@ __device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], i
 // goes to a.hout from workgroup 0.  Then the absmax and the quantisation as in
 // rq_quantise.  PH arrivals per wave in s_sync[1].
 template <int XF>
-__device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv, const uint4* x2v, int K, int gpr,
+__device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv, const uint4* x2v, const uint4* gv,
+                                             int K, int gpr,
                                              int nqw, uint32_t PH, int tid, int lane, int wave, uint8_t* sq,
                                              uint32_t* s_sync, uint32_t* s_amax, float* s_scale, float* s_ss)
 {
@@ -877,12 +878,6 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv,
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the sum is in LDS
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-        uint4 gv[4];  // the norm weight, loaded only now (fewer live registers)
-        {
-            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
-#pragma unroll
-            for (int h = 0; h < 4; ++h) gv[h] = bload(gr, tid < gpr ? 64 * tid + 16 * h : kOOB);
         }
         rq_wait(&s_sync[1], (uint32_t)nqw);
         float p[16];
@@ -969,11 +964,17 @@ k_gemv_rq(GemvArgs a)
 #pragma unroll
             for (int h = 0; h < 4; ++h) x2v[h] = bload(x2r, tid < gpr ? 64 * tid + 16 * h : kOOB);
         }
+        uint4 gv[XN ? 4 : 1];  // the norm weight
+        if (XN) {
+            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
+#pragma unroll
+            for (int h = 0; h < 4; ++h) gv[h] = bload(gr, tid < gpr ? 64 * tid + 16 * h : kOOB);
+        }
         if (tid < 3) s_sync[tid] = 0u;
         if (tid < MT) s_amax[tid] = 0u;
         __syncthreads();
         if (XF != XF_NONE)
-            rq_transform<XF>(a, xv[0], x2v, K, gpr, nqw, PH, tid, lane, wave, sq, s_sync, s_amax, s_scale, s_ss);
+            rq_transform<XF>(a, xv[0], x2v, gv, K, gpr, nqw, PH, tid, lane, wave, sq, s_sync, s_amax, s_scale, s_ss);
         else
             rq_quantise<XK, DG, MT>(xv, K, gpr, mt, nqw, nq, tid, lane, sq, s_sync, s_amax, s_scale);
         return;
@@ -1319,6 +1320,20 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
     constexpr int NV = XK == XK_F32 ? 4 : 2;
     constexpr int ES = XK == XK_F32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc((const uint8_t*)x + row * k * ES, (uint32_t)(k * ES));
+    // G <= 2 (k <= 32768): every input's loads in flight at once (x, the
+    // residual delta, the norm weight); G = 4 loads the latter two where they
+    // are used (the registers of all three would spill)
+    constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;
+    constexpr bool PRE = G <= 2;
+    const __amdgpu_buffer_rsrc_t dr = make_rsrc((const uint8_t*)x2 + row * k * 4, (uint32_t)(k * 4));
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(g, (uint32_t)(k * 4));
+    uint4 dv[PRE && XF == XF_ADD_RMSNORM ? G : 1][4];
+    uint4 gw[PRE && XN ? G : 1][4];
+    auto load_row4 = [&](__amdgpu_buffer_rsrc_t r, uint4* out, int gi) {
+        const int gg = tid * G + gi;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) out[h] = bload(r, (gg < groups ? gg * 64 : kOOB) + 16 * h);
+    };
     float f[G][16];
     {
         uint4 v[G][NV];
@@ -1328,6 +1343,13 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
             const int off = gg < groups ? gg * 16 * ES : kOOB;
 #pragma unroll
             for (int h = 0; h < NV; ++h) v[gi][h] = bload(xr, off + 16 * h);
+        }
+        if (PRE) {
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                if (XF == XF_ADD_RMSNORM) load_row4(dr, dv[gi], gi);
+                if (XN) load_row4(gr, gw[gi], gi);
+            }
         }
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) widen16<XK>(v[gi], f[gi]);
@@ -1356,17 +1378,18 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
     }
     if (XF == XF_ADD_RMSNORM) {
         // residual connection (block.rs:122,137: residual + mixed_out), f32 + f32
-        const __amdgpu_buffer_rsrc_t dr = make_rsrc((const uint8_t*)x2 + row * k * 4, (uint32_t)(k * 4));
         float* hr = hout ? hout + row * k : nullptr;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             const int gg = tid * G + gi;
-            const int off = gg < groups ? gg * 64 : kOOB;
-            uint4 v[4];
-#pragma unroll
-            for (int h = 0; h < 4; ++h) v[h] = bload(dr, off + 16 * h);
             float u[16];
-            widen16<XK_F32>(v, u);
+            if constexpr (PRE) {
+                widen16<XK_F32>(dv[gi], u);
+            } else {
+                uint4 dl[4];
+                load_row4(dr, dl, gi);
+                widen16<XK_F32>(dl, u);
+            }
 #pragma unroll
             for (int e = 0; e < 16; ++e) f[gi][e] = __fadd_rn(f[gi][e], u[e]);
             if (hr && gg < groups) {
@@ -1405,15 +1428,19 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
         for (int gi = 0; gi < G; ++gi) {
             const int gg = tid * G + gi;
             if (gg < groups) {
-                const float4* gp = (const float4*)(g + gg * 16);
+                float gf[16];
+                if constexpr (PRE) {
+                    widen16<XK_F32>(gw[gi], gf);
+                } else {
+                    const float4* gp = (const float4*)(g + gg * 16);
 #pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    const float4 gv = gp[h];
-                    f[gi][4 * h + 0] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 0], d), gv.x);
-                    f[gi][4 * h + 1] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 1], d), gv.y);
-                    f[gi][4 * h + 2] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 2], d), gv.z);
-                    f[gi][4 * h + 3] = __fmul_rn(__fdiv_rn(f[gi][4 * h + 3], d), gv.w);
+                    for (int h = 0; h < 4; ++h) {
+                        const float4 gq = gp[h];
+                        gf[4 * h] = gq.x; gf[4 * h + 1] = gq.y; gf[4 * h + 2] = gq.z; gf[4 * h + 3] = gq.w;
+                    }
                 }
+#pragma unroll
+                for (int e = 0; e < 16; ++e) f[gi][e] = __fmul_rn(__fdiv_rn(f[gi][e], d), gf[e]);
             }
         }
     }
