@@ -273,6 +273,8 @@ def run_decode(args):
         result["batched_decode"] = run_sweep(layers, gen, dev, args)
     if args.pack:
         result["pack"] = run_pack(gen, dev)
+    if args.cfg1:
+        result["cfg1"] = run_cfg1(gen, dev, args)
     if args.e2e:
         result["e2e"] = run_e2e(layers, gen, dev, args)
     if args.adaptive:
@@ -552,6 +554,75 @@ def run_adaptive(gen, dev, args):
             "prefill_frac_int8": round(ops / usm / 1e6 / INT8_PEAK_TOPS, 3)}
 
 
+def run_cfg1(gen, dev, args):
+    """cfg1 (the reference's own CPU-runnable case): one
+    BitLinear forward, K=2048 -> N=5632, M=1, f32 N(0,1) in, f32 out, in both
+    arithmetic modes -- BTL_ACT_F32_REF (the reference's fp32 semantics and
+    summation order) and W1.58-A8.  16 distinct weight copies replayed back to
+    back in a HIP graph (us per call); the reference's CPU algorithm (cpu.rs,
+    restated with AVX2 intrinsics and a thread pool) on the same shape beside it.
+    A parity configuration: launch-latency-bound, its roofline fraction is
+    reported, not targeted."""
+    import ctypes
+    n, k, copies = 5632, 2048, 16
+    ws = [synth_packed(n, k, gen, dev) for _ in range(copies)]
+    x = torch.randn((1, k), generator=gen, device=dev, dtype=torch.float32)
+    y = torch.empty((1, n), dtype=torch.float32, device=dev)
+    cs = [w.as_c() for w in ws]
+    out = {"workload": "cfg1: one BitLinear 2048 -> 5632, M=1, f32 in/out, 16 distinct weight copies "
+                       "back to back in a HIP graph",
+           "algorithmic_bytes": n * k // 4 + k * 4 + n * 4 + 4}
+    b = out["algorithmic_bytes"]
+    for mode_name, mode in (("f32_ref", bl.BTL_ACT_F32_REF), ("i8", bl.BTL_ACT_I8)):
+        def one(stream, c):
+            bl.check(bl.lib.btl_linear(ctypes.byref(c), x.data_ptr(), bl.BTL_F32, 1, k, y.data_ptr(), bl.BTL_F32,
+                                       mode, None, None, 0, stream))
+        st = torch.cuda.current_stream().cuda_stream
+        for c in cs:
+            one(st, c)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        with torch.cuda.stream(cap):
+            with torch.cuda.graph(g, stream=cap):
+                s2 = torch.cuda.current_stream().cuda_stream
+                for c in cs:
+                    one(s2, c)
+        torch.cuda.synchronize()
+        g.replay()
+        reps = 20
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / (reps * copies)
+        out[mode_name] = {"us": round(us, 2), "GB_s": round(b / us / 1e3, 1),
+                          "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+    print("bench: cfg1 f32_ref %.2f us, i8 %.2f us" % (out["f32_ref"]["us"], out["i8"]["us"]), file=sys.stderr,
+          flush=True)
+    if args.cpu_baseline:
+        from oracle import oracle as orc
+        threads = max(1, min(16, os.cpu_count() or 1))
+        xh = x.cpu().numpy()
+        wb, sw = ws[0].data.cpu().numpy(), ws[0].scale
+        orc.forward_f32_avx2(xh, wb, n, sw, threads=threads)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.forward_f32_avx2(xh, wb, n, sw, threads=threads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= 2.0 and reps >= 10:
+                break
+        cus = 1e6 * el / reps
+        out["cpu_baseline"] = {"us": round(cus, 2), "GB_s": round(b / cus / 1e3, 2), "cores": threads,
+                               "kind": "port", "sample": "%d calls of the cfg1 shape on one weight copy, "
+                                                         "%.1f s" % (reps, el)}
+    return out
+
+
 def run_pack(gen, dev):
     """PackedTensor::pack on the device (btl_pack_device) of one f32 weight of the
     MLP up shape 14336 x 4096: the load-time quantisation a checkpoint loader
@@ -627,6 +698,8 @@ def main():
                     help="counter-run mode: --steps launches of one workload and a 256 MiB copy; no JSON")
     ap.add_argument("--no-e2e", dest="e2e", action="store_false",
                     help="skip the cfg5 end-to-end decoder section of the JSON line")
+    ap.add_argument("--no-cfg1", dest="cfg1", action="store_false",
+                    help="skip the cfg1 section (one 2048 -> 5632 forward in both modes, CPU beside it)")
     ap.add_argument("--no-adaptive", dest="adaptive", action="store_false",
                     help="skip the multi-base adaptive-format section of the JSON line")
     ap.add_argument("--e2e-prompt", type=int, default=512)
