@@ -2112,11 +2112,78 @@ __global__ __launch_bounds__(256) void k_ref_f32(const void* x, int64_t m, int64
     store_y<YK>(y, out, __fmul_rn(sum, scale));
 }
 
+// The same contraction for k % 64 == 0, k <= 16384 and 16-byte aligned rows:
+// grid (ceil(n / 32), m), 32 outputs of one token row per workgroup, 8 lanes
+// each.  The row is staged once in LDS lane-major (sx[b][j] = x[8 j + b], rows
+// padded by 4 floats: the lanes' 16-byte reads hit distinct banks), so lane b
+// reads its inputs 8 at a time; each weight row is read 16 bytes (64 weights)
+// per load, the 8 lanes of an output sharing the address.  Lane b's code of
+// weight 8 j' + b, j' = 8 q + e, sits at bit 16 (e % 2) + 2 b of word e / 2 of
+// the q-th 16 bytes.  The FMA order per lane (increasing j') and the lane sum
+// are those of k_ref_f32 (no tail: 32 divides k).
+template <int XK, int YK>
+__global__ __launch_bounds__(256) void k_ref_f32_lds(const void* x, int64_t k, const uint8_t* w, int64_t n,
+                                                     float scale, void* y)
+{
+    extern __shared__ __align__(16) float sxl[];
+    const int K = (int)k, S = (K >> 3) + 4;
+    const int64_t row = blockIdx.y;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < K; i += 256) sxl[(i & 7) * S + (i >> 3)] = load_x<XK>(x, row * k + i);
+    __syncthreads();
+    const int64_t col = (int64_t)blockIdx.x * 32 + (tid >> 3);
+    const int b = tid & 7;
+    const bool active = col < n;
+    const uint4* wr = (const uint4*)(w + (active ? col : 0) * (k >> 2));
+    const float* xb = sxl + b * S;
+    float acc = 0.0f;
+    // 8 steps unrolled (k % 512 == 0 for the Llama shapes): their weight loads
+    // are in flight together
+#pragma unroll 8
+    for (int q = 0; q < (K >> 6); ++q) {
+        const uint4 wv = wr[q];
+        const float4 x0 = *(const float4*)(xb + 8 * q);
+        const float4 x1 = *(const float4*)(xb + 8 * q + 4);
+        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t code = (wd[e >> 1] >> (16 * (e & 1) + 2 * b)) & 3u;
+            const float coeff = (float)((int)(code & 1u) - (int)(code >> 1));
+            acc = __builtin_fmaf(xs[e], coeff, acc);
+        }
+    }
+    float lanes[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) lanes[i] = __shfl(acc, i, 8);
+    if (!active || b != 0) return;
+    float r = -0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r = __fadd_rn(r, lanes[i]);
+    const float sum = __fadd_rn(0.0f, r);
+    store_y<YK>(y, row * n + col, __fmul_rn(sum, scale));
+}
+
 hipError_t launch_ref_f32(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* w,
                           int64_t n, float scale, void* y, int ykind, hipStream_t st)
 {
     const int64_t threads = m * n * 8;
     if (threads <= 0) return hipSuccess;
+    if (k % 64 == 0 && k <= 16384 && ((uintptr_t)w & 15u) == 0 && m <= 65535 && (n + 31) / 32 <= INT32_MAX) {
+        const dim3 grid((unsigned)((n + 31) / 32), (unsigned)m);
+        const size_t lds = (size_t)8 * ((k >> 3) + 4) * 4;
+#define BTL_REF_LDS(XKV, YKV)                                                                               \
+        if (xkind == XKV && ykind == YKV) {                                                                 \
+            hipLaunchKernelGGL((k_ref_f32_lds<XKV, YKV>), grid, dim3(256), lds, st, x, k, w, n, scale, y); \
+            return hipGetLastError();                                                                       \
+        }
+        BTL_REF_LDS(XK_F32, YK_F32)
+        BTL_REF_LDS(XK_F32, YK_BF16)
+        BTL_REF_LDS(XK_BF16, YK_F32)
+        BTL_REF_LDS(XK_BF16, YK_BF16)
+#undef BTL_REF_LDS
+        return hipErrorInvalidValue;
+    }
     dim3 grid((unsigned)((threads + 255) / 256));
 #define BTL_REF_CASE(XKV, YKV)                                                                  \
     if (xkind == XKV && ykind == YKV) {                                                         \

@@ -485,6 +485,29 @@ def test_linear_f32_ref_order_cases():
     assert_f32_identical(y, orc.forward_f32(x, wb, 2, 1.0))
 
 
+# k % 64 == 0 and k <= 16384: the LDS-staged form of the reference-order kernel
+# (inputs lane-major in LDS, 16-byte weight loads).  Inputs spanning 40 binades
+# make every sum order-sensitive, so a lane or step mismatch shows; codes 3
+# appear; m > 1 reads each token row's staging; bf16 in and out; k = 16448 takes
+# the general form.
+@pytest.mark.parametrize("m,k,n", [(1, 64, 40), (3, 192, 33), (2, 4096, 70), (1, 16384, 24), (2, 16448, 9)])
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
+def test_linear_f32_ref_staged_form(m, k, n, xdt, ydt):
+    print("f32 ref staged", m, k, n, xdt, ydt, flush=True)
+    rng = np.random.default_rng(m * 7 + k + n)
+    x = (rng.standard_normal((m, k)) * np.exp2(rng.integers(-20, 20, (m, k)))).astype(np.float32)
+    wb = random_codes(n, k, seed=k + n, p3=0.1)
+    sw = np.float32(0.0173)
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), float(sw), (n, k), DEV)
+    xt = to_dev(x, xdt)
+    y = bl.BitLinearHip.forward(xt, pt, mode="f32_ref", out_dtype=ydt)
+    yr = orc.forward_f32(host_x(xt), wb, n, sw)
+    if ydt == torch.float32:
+        assert_f32_identical(y, yr)
+    else:
+        assert_bf16_matches(y, yr)
+
+
 def test_linear_f32_ref_reference_bench_input():
     # bench_cpu_kernel.rs:33,47,50 at a reduced N: y[n] = 0.5 * sum_k t[n,k]
     k, n = 8192, 512
