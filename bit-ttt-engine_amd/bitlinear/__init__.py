@@ -18,7 +18,7 @@ from ._lib import (  # noqa: F401
 )
 from .packed import PackedTensor  # noqa: F401
 from .layer import (  # noqa: F401
-    BitLinear, BitLinearHip, Workspace, linear_group, linear_i8, linear_i8_op, quantize_act,
+    BitLinear, BitLinearHip, Workspace, linear_group, linear_i8, linear_i8_op, linear_residual, quantize_act,
     quantize_act_op, rmsnorm_linear_group, swiglu_linear_group,
 )
 from .adaptive import AdaptiveBitLinear, reconstruct_dense, split_bases  # noqa: F401,E402

@@ -37,7 +37,7 @@ EXPORTS = (
     "btl_rope_table", "btl_rope_kv_append", "btl_attention_workspace_bytes", "btl_attention",
     "btl_rope_append_attention",
     "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm_linear_group", "btl_add_rmsnorm_swiglu",
-    "btl_add_rmsnorm_swiglu_workspace_bytes",
+    "btl_add_rmsnorm_swiglu_workspace_bytes", "btl_linear_residual",
 )
 
 
@@ -105,6 +105,7 @@ def _load():
                                                sz, vp]),
         "btl_add_rmsnorm_swiglu": (i32, [P(BtlPacked), P(BtlPacked), vp, vp, vp, vp, f32, i64, i64, vp, vp, sz, vp]),
         "btl_add_rmsnorm_swiglu_workspace_bytes": (sz, [i64, i64, i64]),
+        "btl_linear_residual": (i32, [P(BtlPacked), vp, i32, i64, i64, vp, vp, vp, sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -200,6 +200,25 @@ def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None):
     return outputs
 
 
+def linear_residual(weight, x, resid, out=None, workspace=None):
+    """btl_linear_residual: resid + x W^T (the residual connection after a
+    BitLinear, block.rs:119,131), f32 out; `out` must not overlap `resid`."""
+    _on_gpu(x, "input")
+    _on_gpu(resid, "residual")
+    m, k = x.shape
+    n = weight.dims2()[0]
+    if resid.dtype != torch.float32 or tuple(resid.shape) != (m, n):
+        raise BitLinearError(BTL_ERR_LAYOUT, "residual must be float32 [%d, %d]" % (m, n))
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    c = weight.as_c()
+    wsp, wsn = _ws_args(workspace)
+    check(lib.btl_linear_residual(ctypes.byref(c), x.data_ptr() if x.numel() else None, _dtype_code(x, "input"), m,
+                                  k, resid.data_ptr() if resid.numel() else None,
+                                  out.data_ptr() if out.numel() else None, wsp, wsn, _stream(x.device)))
+    return out
+
+
 class BitLinear:
     """1.58-bit linear layer (layers/bit_linear.rs:12-21)."""
 

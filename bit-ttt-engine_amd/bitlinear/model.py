@@ -18,9 +18,10 @@ Mapping of the block onto the C ABI (one row of activations per token, f32 betwe
   mlp_out = BitLinear_down(hs)                           btl_linear_group
 and after the last block logits = lm_head(RMSNorm_f(x' + mlp_out)) in one more
 btl_add_rmsnorm_linear_group.  The residual stream alternates between two
-buffers (each add writes the other one), so for a one-token step the add +
-norm can run inside the contraction kernel's prologue (the library does so for
-launches of up to 512 workgroups), and the gate/up kernel writes silu(gate) * up
+buffers (each add writes the other one).  A one-token step moves the two adds
+into the epilogues of o and down (x' = x + o and x + mlp_out through
+btl_linear_residual), so the kernels of q|k|v and gate|up apply only the
+RMSNorm, in their quantising waves; the gate/up kernel writes silu(gate) * up
 from its epilogue.  Every linear is a BitLinear (W1.58-A8), the lm_head
 included.
 
@@ -141,7 +142,8 @@ class BitLlamaHip:
             o_c, o = _arr([L["o"]])
             gate_c, up_c = L["gate"].as_c(), L["up"].as_c()
             d_c, d = _arr([L["down"]])
-            self._layers.append(dict(keep=(qkv_c, o_c, d_c), qkv=qkv, o=o, down=d,
+            self._layers.append(dict(keep=(qkv_c, o_c, d_c), qkv=qkv, o=o, down=d, o_w=ctypes.byref(o_c[0]),
+                                     down_w=ctypes.byref(d_c[0]),
                                      gate=ctypes.byref(gate_c), up=ctypes.byref(up_c), gate_c=gate_c, up_c=up_c,
                                      n1=L["norm1"].data_ptr(), n2=L["norm2"].data_ptr()))
         self._head_c, self._head = _arr([weights["lm_head"]])
@@ -165,10 +167,15 @@ class BitLlamaHip:
         hid = c.hidden
         check(lib.btl_embedding(self.w["embed"].data_ptr(), self.emb_dtype, c.vocab, hid, ids.data_ptr(), m,
                                 self.h.data_ptr(), st))
-        cur, nxt = self.h, self.h2  # each add writes the other buffer (lets a one-token step fuse it)
+        cur, nxt = self.h, self.h2  # each add writes the other buffer
+        # One token: the residual adds run in the epilogues of the o and down
+        # projections (btl_linear_residual), so the norms ahead of q|k|v and
+        # gate|up are plain RMSNorms inside those launches.  More rows: the add
+        # is fused into the next norm's transform instead.  Same bits.
+        one = m == 1
         for li, L in enumerate(self._layers):
             cache = self.caches[li].c
-            if li > 0:
+            if li > 0 and not one:
                 check(lib.btl_add_rmsnorm_linear_group(L["qkv"], self._y_qkv, 3, cur.data_ptr(), self.down.data_ptr(),
                                                        nxt.data_ptr(), L["n1"], c.eps, m, hid, BTL_F32, None, 0, st))
                 cur, nxt = nxt, cur
@@ -178,6 +185,16 @@ class BitLlamaHip:
             check(lib.btl_rope_append_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), m,
                                                 c.n_heads, ctypes.byref(cache), pos, dp, self.rope_cos.data_ptr(),
                                                 self.rope_sin.data_ptr(), self.attn.data_ptr(), None, 0, st))
+            if one:
+                check(lib.btl_linear_residual(L["o_w"], self.attn.data_ptr(), BTL_F32, m, c.n_heads * c.head_dim,
+                                              cur.data_ptr(), nxt.data_ptr(), None, 0, st))
+                cur, nxt = nxt, cur
+                check(lib.btl_add_rmsnorm_swiglu(L["gate"], L["up"], cur.data_ptr(), None, None, L["n2"], c.eps, m,
+                                                 hid, self.hs.data_ptr(), None, 0, st))
+                check(lib.btl_linear_residual(L["down_w"], self.hs.data_ptr(), BTL_F32, m, c.intermediate,
+                                              cur.data_ptr(), nxt.data_ptr(), None, 0, st))
+                cur, nxt = nxt, cur
+                continue
             check(lib.btl_linear_group(L["o"], self._y_o, 1, self.attn.data_ptr(), BTL_F32, m,
                                        c.n_heads * c.head_dim, BTL_F32, None, 0, st))
             check(lib.btl_add_rmsnorm_swiglu(L["gate"], L["up"], cur.data_ptr(), self.o.data_ptr(), nxt.data_ptr(),
@@ -186,9 +203,9 @@ class BitLlamaHip:
             check(lib.btl_linear_group(L["down"], self._y_down, 1, self.hs.data_ptr(), BTL_F32, m, c.intermediate,
                                        BTL_F32, None, 0, st))
         last = m - 1
-        check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, cur[last].data_ptr(),
-                                               self.down[last].data_ptr(), None, self.w["norm_f"].data_ptr(), c.eps,
-                                               1, hid, BTL_F32, None, 0, st))
+        delta = None if one else self.down[last].data_ptr()
+        check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, cur[last].data_ptr(), delta, None,
+                                               self.w["norm_f"].data_ptr(), c.eps, 1, hid, BTL_F32, None, 0, st))
 
     def reset(self):
         """Llama::reset_state / BitLlama::reset_kv_cache (llama.rs:179-186, 460-468)."""

@@ -288,6 +288,15 @@ struct Xform {
     float* hout;     // XF_ADD_RMSNORM: the summed residual stream (may alias x)
 };
 
+// y += resid for a launch whose kernel did not add it (f32, one layer, y and
+// resid not overlapping: checked by the entry point)
+int add_resid(const Layer& l, const float* resid, int64_t m, hipStream_t st)
+{
+    hipError_t e = btl::launch_add_f32((float*)l.y, resid, m * l.w->n, st);
+    if (e != hipSuccess) return hip_fail(e, "residual add kernel launch");
+    return BTL_OK;
+}
+
 // W1.58-A8 contraction of `count` layers sharing one input.
 //   any k % 4 == 0 / any alignment .... quantise into scratch, k_generic_i8
 //   m <= 4 (decode) ................... k_gemv_dec, quantisation fused
@@ -301,7 +310,7 @@ struct Xform {
 // silu(y0) * y1 written by the decode kernel's epilogue, y[i] may be NULL.
 int run_i8(const Layer* layers, int count, const void* x, int xkind, const float* xs, int64_t m,
            int64_t k, int ykind, void* ws_user, size_t ws_bytes, hipStream_t st, const Xform* xf = nullptr,
-           float* swiglu_out = nullptr)
+           float* swiglu_out = nullptr, const float* resid = nullptr)
 {
     int dev;
     int rc = current_device(&dev);
@@ -337,7 +346,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
                                        layers[i].y, ykind, layers[i].acc, st);
             if (e != hipSuccess) return hip_fail(e, "generic int8 kernel launch");
         }
-        return BTL_OK;
+        return resid ? add_resid(layers[0], resid, m, st) : BTL_OK;
     }
 
     // Route.  Decode (1..4 token rows): RB row blocks of 16 rows per
@@ -414,15 +423,17 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
                        ((m == 1 && k <= 16384) || (m == 2 && k <= 4096 && !xf && !swiglu_out));
     bool rqx = false;
     int rqx_wpc = 0;
-    if (rq_on && xf_ok && !swiglu_out && k <= 4096) {
-        rqx_wpc = rq_waves_per_group(dec_rb, k, g_dev[dev].cus, 0, true, 1);
-        rqx = ceil_div(dec_rb * 4, rqx_wpc) <= fuse_max_wg;
+    if (rq_on && xf_ok && k <= 4096 && (!swiglu_out || xf->kind == btl::XF_RMSNORM)) {
+        // with the SwiGLU pairing (RMSNorm only): two groups per quantising thread
+        const int64_t pn = swiglu_out ? layers[0].w->n : 0;
+        rqx_wpc = rq_waves_per_group(dec_rb, k, g_dev[dev].cus, pn, !swiglu_out, 1);
+        rqx = (swiglu_out ? ceil_div(ceil_div(pn, 4), rqx_wpc / 2) : ceil_div(dec_rb * 4, rqx_wpc)) <= fuse_max_wg;
     }
     // Otherwise the K-part / row-contiguous decode kernel applies a transform in
     // its own prologue for launches of at most kFuseMaxWg workgroups.
     const bool fuse = !rqx && dec && xf_ok && ceil_div(dec_rb, rbw) <= fuse_max_wg && wv * rbw <= 8 &&
                       k / 16 <= (int64_t)(xf->kind == btl::XF_SWIGLU ? 2 : 1) * wv * rbw * 64;
-    const bool rq = rq_on && !fuse && (!swiglu_out || (xf && !rqx));
+    const bool rq = rq_on && !fuse && (!swiglu_out || xf);
 
     // operand-order quantisation into the workspace (all routes but plain decode)
     const bool pre = (xf && !fuse && !rqx) || !dec;
@@ -489,22 +500,25 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             // one token group per quantising thread when the workgroup has room
             // for the quantising waves that takes (one token row, k <= 4096): a
             // shorter prologue for the launches of few compute waves
-            a.tiles = rqx || (m == 1 && k <= 4096 && !swiglu_out && btl::rq_quant_waves((int)k, 1) + a.parts <= 16 &&
-                              env_int("BTL_DEC_RQ_DG", 0) != 2)
+            a.tiles = (rqx && !swiglu_out) ||
+                              (!rqx && m == 1 && k <= 4096 && !swiglu_out &&
+                               btl::rq_quant_waves((int)k, 1) + a.parts <= 16 && env_int("BTL_DEC_RQ_DG", 0) != 2)
                           ? 1
                           : 2;
+            a.resid = count == 1 ? resid : nullptr;
             e = btl::launch_gemv_rq(a, pre ? (int)btl::XK_I8O : xkind, rqx ? xform : (int)btl::XF_NONE, st);
             if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
+            if (resid && !a.resid) return add_resid(layers[0], resid, m, st);
             return BTL_OK;
         }
         e = btl::launch_gemv_dec(a, pre ? (int)btl::XK_I8O : xkind, xform, st);
         if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
-        return BTL_OK;
+        return resid ? add_resid(layers[0], resid, m, st) : BTL_OK;
     }
     e = launch_gemm(layers, count, q, sxp, m, k, ykind, splits, split_steps,
                     splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr, bat, st);
     if (e != hipSuccess) return hip_fail(e, bat ? "batched gemv kernel launch" : "gemm kernel launch");
-    return BTL_OK;
+    return resid ? add_resid(layers[0], resid, m, st) : BTL_OK;
 }
 
 // Shared validation of the fused entry points; fills `ls`.
@@ -836,6 +850,26 @@ int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, i
     const Xform xf{delta ? btl::XF_ADD_RMSNORM : btl::XF_RMSNORM, delta, g, eps, delta ? h_out : nullptr};
     return run_i8(ls, count, h, btl::XK_F32, nullptr, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws,
                   ws_bytes, (hipStream_t)stream, &xf);
+}
+
+int btl_linear_residual(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int64_t k, const float* resid,
+                        float* y, void* ws, size_t ws_bytes, void* stream)
+{
+    int rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_packed(w, m, k))) return rc;
+    const int64_t n = w->n;
+    if (m == 0 || n == 0) return BTL_OK;
+    if (k > 0 && (!x || !resid || !y)) return fail(BTL_ERR_LAYOUT, "null input, residual or output");
+    if (k == 0) return fail(BTL_ERR_SHAPE, "in_features must be positive");
+    {
+        const uintptr_t a0 = (uintptr_t)resid, a1 = (uintptr_t)y, nb = (uintptr_t)(m * n * 4);
+        if (a0 < a1 + nb && a1 < a0 + nb) return fail(BTL_ERR_LAYOUT, "y overlaps resid");
+        const uintptr_t ax = (uintptr_t)x, xb = (uintptr_t)(m * k * (xdtype == BTL_BF16 ? 2 : 4));
+        if (ax < a1 + nb && a1 < ax + xb) return fail(BTL_ERR_LAYOUT, "y overlaps the input");
+    }
+    Layer l{w, y, nullptr};
+    return run_i8(&l, 1, x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, nullptr, m, k, btl::YK_F32, ws, ws_bytes,
+                  (hipStream_t)stream, nullptr, nullptr, resid);
 }
 
 int btl_add_rmsnorm_swiglu(const btl_packed_t* w_gate, const btl_packed_t* w_up, const float* h,

@@ -52,6 +52,9 @@ struct GemvArgs {
     // tiles == 2; workgroup w computes row block w of both and writes
     // silu(gate) * up to swiglu_out [m, n] f32 (the layers' y may be NULL)
     float* swiglu_out;
+    // residual stream added to the f32 output (the row-group form, one layer):
+    // y = resid + (float)acc * (s_x * s_w); y may be resid
+    const float* resid;
     // row-contiguous form (m == 1, k % 64 == 0): 0 = K parts; 1, 2, 4 = whole
     // rows of up to that many 4096-weight chunks, 16 / parts rows per wave
     // (parts in {1, 2, 4, 8}, chunks * 16 / parts loads of 1 KB per wave in
@@ -208,6 +211,8 @@ hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t
 
 // out[i] = silu(g[i]) * u[i], silu(v) = v / (1 + exp(-v)) (swiglu.rs:29-35), f32
 hipError_t launch_swiglu_f32(const float* g, const float* u, int64_t n, float* out, hipStream_t st);
+// y[i] = fadd(y[i], r[i]) for i < n (the residual add after a contraction)
+hipError_t launch_add_f32(float* y, const float* r, int64_t n, hipStream_t st);
 
 // Multi-base adaptive format (adaptive_linear.rs): at most kMaxBases bases (the
 // reference's loader tries 1..=8, adaptive_linear.rs:56).

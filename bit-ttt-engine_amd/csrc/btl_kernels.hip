@@ -833,71 +833,114 @@ __device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], i
     if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// The quantising waves of k_gemv_rq with a transform (f32 tokens, one group
-// per thread): the transform of k_xform_quant on this workgroup's copy of the
-// row.  Thread t holds elements [16 t, 16 t + 16) (zeros past k), so the sum of
-// squares is the pairwise tree in index order (in-thread, the lanes' xor
-// butterfly, then the waves zero-padded to 16); XF_ADD_RMSNORM's summed row
-// goes to a.hout from workgroup 0.  Then the absmax and the quantisation as in
-// rq_quantise.  PH arrivals per wave in s_sync[1].
-template <int XF>
-__device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv, const uint4* x2v, const uint4* gv,
-                                             int K, int gpr,
-                                             int nqw, uint32_t PH, int tid, int lane, int wave, uint8_t* sq,
-                                             uint32_t* s_sync, uint32_t* s_amax, float* s_scale, float* s_ss)
+// The quantising waves of k_gemv_rq with a transform (f32 tokens, DG groups
+// per thread: thread t holds groups t + nq gi): the transform of k_xform_quant
+// on this workgroup's copy of the row.  Wave w's groups of slot gi are the 64
+// consecutive groups of 1024-element block gi nqw + w (zeros past k), so the
+// sum of squares is the pairwise tree in index order: in-thread, the lanes'
+// xor butterfly, then the blocks zero-padded to 16 (per-block sums exchanged in
+// LDS).  XF_ADD_RMSNORM's summed row goes to a.hout from workgroup 0.  Then the
+// absmax and the quantisation as in rq_quantise.  PH arrivals per wave in
+// s_sync[1].
+template <int XF, int DG>
+__device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv)[4], const uint4 (*x2v)[4],
+                                             const uint4 (*gv)[4], int K, int gpr, int nqw, int nq, uint32_t PH,
+                                             int tid, int lane, int wave, uint8_t* sq, uint32_t* s_sync,
+                                             uint32_t* s_amax, float* s_scale, float* s_ss)
 {
     constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;
     constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;
-    float fv[16];
-    widen16<XK_F32>(xv, fv);
-    if (X2) {
-        float u[16];
-        widen16<XK_F32>(x2v, u);
+    // Two groups per thread (RMSNorm only): the token row and the norm weight
+    // would need all 64 registers at once, so the row waits in LDS (uint4 h of
+    // group gi of thread t at sxs[(4 gi + h) nq + t], after the operand row)
+    // while the weight loads, issued once the row is in, are in flight.
+    constexpr bool GL = XN && DG == 2;
+    uint4* const sxs = (uint4*)(sq + K + 16);
+    float fv[DG][16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float v = fv[e];
-            fv[e] = XF == XF_SWIGLU ? __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, btl_expf(-v))), u[e]) : __fadd_rn(v, u[e]);
-        }
-        if (XF == XF_ADD_RMSNORM && a.hout && blockIdx.x == 0 && tid < gpr) {
-            float4* hp = (float4*)(a.hout + 16 * tid);
+    for (int gi = 0; gi < DG; ++gi) {
+        const int g = tid + nq * gi;
+        widen16<XK_F32>(xv[gi], fv[gi]);
+        if (X2) {
+            float u[16];
+            widen16<XK_F32>(x2v[gi], u);
 #pragma unroll
-            for (int h = 0; h < 4; ++h) hp[h] = make_float4(fv[4 * h], fv[4 * h + 1], fv[4 * h + 2], fv[4 * h + 3]);
+            for (int e = 0; e < 16; ++e) {
+                const float v = fv[gi][e];
+                fv[gi][e] = XF == XF_SWIGLU ? __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, btl_expf(-v))), u[e])
+                                            : __fadd_rn(v, u[e]);
+            }
+            if (XF == XF_ADD_RMSNORM && a.hout && blockIdx.x == 0 && g < gpr) {
+                float4* hp = (float4*)(a.hout + 16 * g);
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    hp[h] = make_float4(fv[gi][4 * h], fv[gi][4 * h + 1], fv[gi][4 * h + 2], fv[gi][4 * h + 3]);
+            }
         }
     }
     if (XN) {
-        float t[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) t[e] = __fmul_rn(fv[e], fv[e]);
+        for (int gi = 0; gi < DG; ++gi) {
+            float t[16];
 #pragma unroll
-        for (int len = 16; len > 1; len >>= 1)
+            for (int e = 0; e < 16; ++e) t[e] = __fmul_rn(fv[gi][e], fv[gi][e]);
 #pragma unroll
-            for (int i = 0; i < len / 2; ++i) t[i] = __fadd_rn(t[2 * i], t[2 * i + 1]);
-        const float ws = wave_pairwise_sum(t[0]);
+            for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+                for (int i = 0; i < len / 2; ++i) t[i] = __fadd_rn(t[2 * i], t[2 * i + 1]);
+            const float ws = wave_pairwise_sum(t[0]);
+            if (lane == 0) s_ss[gi * nqw + wave] = ws;
+        }
+        uint4 gl[GL ? DG : 1][4];
+        if constexpr (GL) {
+#pragma unroll
+            for (int gi = 0; gi < DG; ++gi)
+#pragma unroll
+                for (int h = 0; h < 4; ++h) sxs[(4 * gi + h) * nq + tid] = xv[gi][h];
+            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
+#pragma unroll
+            for (int gi = 0; gi < DG; ++gi) {
+                const int g = tid + nq * gi;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) gl[gi][h] = bload(gr, g < gpr ? 64 * g + 16 * h : kOOB);
+            }
+        }
         if (lane == 0) {
-            s_ss[wave] = ws;
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the sum is in LDS
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the sums are in LDS
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         rq_wait(&s_sync[1], (uint32_t)nqw);
+        const int nblk = DG * nqw;
         float p[16];
 #pragma unroll
-        for (int w = 0; w < 16; ++w) p[w] = w < nqw ? s_ss[w] : 0.0f;
+        for (int w = 0; w < 16; ++w) p[w] = w < nblk ? s_ss[w] : 0.0f;
 #pragma unroll
         for (int len = 16; len > 1; len >>= 1)
 #pragma unroll
             for (int i = 0; i < len / 2; ++i) p[i] = __fadd_rn(p[2 * i], p[2 * i + 1]);
         const float inv_k = (float)(1.0 / (double)K);
         const float d = sqrt_rn(__fadd_rn(__fmul_rn(p[0], inv_k), a.eps));
-        float gf[16];
-        widen16<XK_F32>(gv, gf);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) fv[e] = __fmul_rn(__fdiv_rn(fv[e], d), gf[e]);
+        for (int gi = 0; gi < DG; ++gi) {
+            float gf[16];
+            widen16<XK_F32>(GL ? gl[gi] : gv[gi], gf);
+            if constexpr (GL) {
+                uint4 xl[4];
+#pragma unroll
+                for (int h = 0; h < 4; ++h) xl[h] = sxs[(4 * gi + h) * nq + tid];
+                widen16<XK_F32>(xl, fv[gi]);
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) fv[gi][e] = __fmul_rn(__fdiv_rn(fv[gi][e], d), gf[e]);
+        }
     }
     uint32_t am = 0;
-    if (tid < gpr)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) am = max(am, __float_as_uint(fv[e]) & 0x7FFFFFFFu);
+    for (int gi = 0; gi < DG; ++gi)
+        if (tid + nq * gi < gpr)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) am = max(am, __float_as_uint(fv[gi][e]) & 0x7FFFFFFFu);
     const uint32_t v = wave_max_dpp(am);
     if (lane == 0) {
         __hip_atomic_fetch_max(&s_amax[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -907,18 +950,22 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4* xv,
     const QParams qp = qparams(__hip_atomic_load(&s_amax[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     const float rm = qp.ok ? qp.r : 0.0f;
     if (tid == 0) s_scale[0] = qp.s;
-    const uint4 qv = rm != 0.0f ? group_quant_f(fv, rm) : uint4{0u, 0u, 0u, 0u};
-    if (tid < gpr) *(uint4*)(sq + 16 * tid) = qv;
+#pragma unroll
+    for (int gi = 0; gi < DG; ++gi) {
+        const int g = tid + nq * gi;
+        const uint4 qv = rm != 0.0f ? group_quant_f(fv[gi], rm) : uint4{0u, 0u, 0u, 0u};
+        if (g < gpr) *(uint4*)(sq + 16 * g) = qv;
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 template <int XK, int R, int ST, bool PAIR = false, int XF = XF_NONE, int DG = 2, int MT = 1>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(R == 4 && XF == XF_NONE ? 8 : 4))) void
-k_gemv_rq(GemvArgs a)
+__global__ __launch_bounds__(1024)
+__attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) void k_gemv_rq(GemvArgs a)
 {
-    static_assert(XF == XF_NONE || (XK == XK_F32 && R == 4 && !PAIR && DG == 1 && MT == 1),
-                  "transforms: one f32 token row, k <= 4096");
+    static_assert(XF == XF_NONE || (XK == XK_F32 && R == 4 && MT == 1 && (PAIR ? XF == XF_RMSNORM && DG == 2 : DG == 1)),
+                  "transforms: one f32 token row, k <= 4096; with the SwiGLU pairing RMSNorm only");
     static_assert(DG == 1 || DG == 2, "one or two token groups per quantising thread");
     static_assert(MT == 1 || (MT == 2 && R == 4 && !PAIR), "two token rows: k <= 4096, no SwiGLU epilogue");
     constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;   // a norm over the row
@@ -951,7 +998,7 @@ k_gemv_rq(GemvArgs a)
     if (wave < nqw) {
         // 1. the token groups (and the transform's second row), issued first
         uint4 xv[DG][NV];
-        uint4 x2v[X2 ? 4 : 1];
+        uint4 x2v[X2 ? DG : 1][4];
         const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)(mt * K * ES));
 #pragma unroll
         for (int gi = 0; gi < DG; ++gi) {
@@ -959,22 +1006,27 @@ k_gemv_rq(GemvArgs a)
 #pragma unroll
             for (int h = 0; h < NV; ++h) xv[gi][h] = bload(xr, g < mt * gpr ? 16 * g * ES + 16 * h : kOOB);
         }
-        if (X2) {
-            const __amdgpu_buffer_rsrc_t x2r = make_rsrc(a.x2, (uint32_t)(K * 4));
+        uint4 gv[XN ? DG : 1][4];  // the norm weight (two groups per thread: loaded later)
 #pragma unroll
-            for (int h = 0; h < 4; ++h) x2v[h] = bload(x2r, tid < gpr ? 64 * tid + 16 * h : kOOB);
-        }
-        uint4 gv[XN ? 4 : 1];  // the norm weight
-        if (XN) {
-            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
+        for (int gi = 0; gi < (XF != XF_NONE && !(XN && DG == 2) ? DG : 0); ++gi) {
+            const int g = tid + nq * gi;
+            if (X2) {
+                const __amdgpu_buffer_rsrc_t x2r = make_rsrc(a.x2, (uint32_t)(K * 4));
 #pragma unroll
-            for (int h = 0; h < 4; ++h) gv[h] = bload(gr, tid < gpr ? 64 * tid + 16 * h : kOOB);
+                for (int h = 0; h < 4; ++h) x2v[X2 ? gi : 0][h] = bload(x2r, g < gpr ? 64 * g + 16 * h : kOOB);
+            }
+            if (XN) {
+                const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
+#pragma unroll
+                for (int h = 0; h < 4; ++h) gv[XN ? gi : 0][h] = bload(gr, g < gpr ? 64 * g + 16 * h : kOOB);
+            }
         }
         if (tid < 3) s_sync[tid] = 0u;
         if (tid < MT) s_amax[tid] = 0u;
         __syncthreads();
-        if (XF != XF_NONE)
-            rq_transform<XF>(a, xv[0], x2v, gv, K, gpr, nqw, PH, tid, lane, wave, sq, s_sync, s_amax, s_scale, s_ss);
+        if constexpr (XF != XF_NONE)
+            rq_transform<XF, DG>(a, xv, x2v, gv, K, gpr, nqw, nq, PH, tid, lane, wave, sq, s_sync, s_amax, s_scale,
+                                 s_ss);
         else
             rq_quantise<XK, DG, MT>(xv, K, gpr, mt, nqw, nq, tid, lane, sq, s_sync, s_amax, s_scale);
         return;
@@ -1074,7 +1126,7 @@ k_gemv_rq(GemvArgs a)
                 const float yv = __fmul_rn((float)dm[mm], __fmul_rn(s_x, SW));
                 const int64_t o = (int64_t)mm * N + n;
                 if (a.ykind == YK_BF16) ((uint16_t*)Y)[o] = f32_to_bf16(yv);
-                else ((float*)Y)[o] = yv;
+                else ((float*)Y)[o] = a.resid ? __fadd_rn(a.resid[o], yv) : yv;
                 if (ACC) ACC[o] = dm[mm];
             }
         }
@@ -1109,7 +1161,7 @@ k_gemv_rq(GemvArgs a)
     }
     if (!own || r >= rows) return;
     if (a.ykind == YK_BF16) ((uint16_t*)Y)[n] = f32_to_bf16(yv);
-    else ((float*)Y)[n] = yv;
+    else ((float*)Y)[n] = a.resid ? __fadd_rn(a.resid[n], yv) : yv;  // the residual add of block.rs:119,131
     if (ACC) ACC[n] = d;
 }
 
@@ -1123,23 +1175,29 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
     const int dg = a.tiles;
     const int nqw = rq_quant_waves(a.k, dg, a.m);
     const bool pair = a.swiglu_out != nullptr;
-    if ((dg != 1 && dg != 2) || (dg == 1 && (R != 4 || pair)) || (xform != XF_NONE && dg != 1))
+    if ((dg != 1 && dg != 2) || (dg == 1 && (R != 4 || pair)) || (xform != XF_NONE && dg != (pair ? 2 : 1)))
         return hipErrorInvalidValue;
     if (a.m < 1 || a.m > 2 || (a.m > 1 && (R != 4 || pair || xform != XF_NONE || dg != 2)) || a.k % 64 != 0 ||
         a.k < 64 || a.k > 16384 || a.parts < 1 || nqw + a.parts > 16 || a.rb_total < 1 ||
         (xkind != XK_F32 && xkind != XK_BF16 && xkind != XK_I8 && xkind != XK_I8O))
         return hipErrorInvalidValue;
+    if (a.resid && (a.ykind != YK_F32 || pair || a.nprob != 1)) return hipErrorInvalidValue;
     if (xform != XF_NONE) {
         // a transform in the quantising waves: f32 tokens, k <= 4096, the inputs
-        // it reads; the summed residual (XF_ADD_RMSNORM) goes to another buffer
-        if (xkind != XK_F32 || R != 4 || pair || !a.x2 == (xform == XF_ADD_RMSNORM || xform == XF_SWIGLU) ||
+        // it reads; the summed residual (XF_ADD_RMSNORM) goes to another buffer;
+        // with the SwiGLU pairing RMSNorm only, two groups per thread
+        if (xkind != XK_F32 || R != 4 || (pair && (xform != XF_RMSNORM || dg != 2)) || (!pair && dg != 1) ||
+            !a.x2 == (xform == XF_ADD_RMSNORM || xform == XF_SWIGLU) ||
             ((xform == XF_RMSNORM || xform == XF_ADD_RMSNORM) && !a.g) || (a.hout && (const void*)a.hout == a.x))
             return hipErrorInvalidValue;
-        const dim3 grid((unsigned)(((int64_t)a.rb_total * 4 + a.parts - 1) / a.parts)),
-            block((unsigned)((nqw + a.parts) * 64));
-        const size_t lds = (size_t)a.k + 16;
+        const int64_t groups = pair ? ((int64_t)a.p[0].n + 3) / 4 : (int64_t)a.rb_total * 4;
+        const int64_t per = pair ? a.parts / 2 : a.parts;
+        const dim3 grid((unsigned)((groups + per - 1) / per)), block((unsigned)((nqw + a.parts) * 64));
+        // the operand row; with the pairing also the staged f32 row (64 B per group)
+        const size_t lds = (size_t)a.k + 16 + (pair ? (size_t)dg * 64 * nqw * 64 : 0);
 #define BTL_RQ_XF(STV)                                                                                        \
-    if (xform == XF_RMSNORM) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_RMSNORM, 1>), grid, block, lds, s, a); \
+    if (pair) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, true, XF_RMSNORM, 2>), grid, block, lds, s, a);       \
+    else if (xform == XF_RMSNORM) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_RMSNORM, 1>), grid, block, lds, s, a); \
     else if (xform == XF_ADD_RMSNORM)                                                                           \
         hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_ADD_RMSNORM, 1>), grid, block, lds, s, a);      \
     else hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_SWIGLU, 1>), grid, block, lds, s, a);
@@ -1377,7 +1435,7 @@ __global__ __launch_bounds__(1024) void k_xform_quant(const void* x, const void*
         }
     }
     if (XF == XF_ADD_RMSNORM) {
-        // residual connection (block.rs:122,137: residual + mixed_out), f32 + f32
+        // residual connection (block.rs:119,131: residual + mixed_out), f32 + f32
         float* hr = hout ? hout + row * k : nullptr;
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {

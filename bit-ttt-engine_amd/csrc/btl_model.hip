@@ -508,6 +508,23 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st)
 }
 
 // ---------------------------------------------------------------------------
+// k_add_f32: y += r elementwise (the residual add after a contraction of many
+// token rows; IEEE addition commutes, so the bits are those of r + y)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_add_f32(float* y, const float* r, int64_t n)
+{
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) y[i] = __fadd_rn(y[i], r[i]);
+}
+
+hipError_t launch_add_f32(float* y, const float* r, int64_t n, hipStream_t st)
+{
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_add_f32, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st, y, r, n);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // k_swiglu_f32: silu(g) * u elementwise (swiglu.rs:29-35), candle's silu
 // v / (1 + exp(-v)) with btl_expf; the route for many token rows
 // ---------------------------------------------------------------------------

@@ -141,6 +141,22 @@ int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, i
                                  int ydtype, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * A BitLinear with the residual connection after it (block.rs:119,131:
+ * residual + mixed_out): y = resid + x W^T, the W1.58-A8 product as
+ * btl_linear's then one f32 add per element.  x [m, k] f32 or bf16 (xdtype),
+ * resid and y [m, n] f32; y must overlap neither resid nor x.  On the decode
+ * kernel of whole weight rows (one token row with k % 64 == 0 and
+ * 1024 <= k <= 16384, two with k <= 4096) the add runs in its epilogue (one
+ * launch), otherwise in an elementwise launch after the product.  It lets the
+ * decoder drop the add from the next residual + RMSNorm:
+ * btl_add_rmsnorm_linear_group / btl_add_rmsnorm_swiglu on y with delta = NULL
+ * give the same bits.  ws: as btl_linear (or NULL).
+ * No reference function of its own: the residual add of BitLlamaBlock::forward.
+ */
+int btl_linear_residual(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int64_t k, const float* resid,
+                        float* y, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * The gate/up half of SwiGLU::forward (swiglu.rs:29-35) after the residual add
  * and RMSNorm of btl_add_rmsnorm_linear_group: out = silu(xn W1^T) * (xn W3^T),
  * xn = RMSNorm(h + delta) * g, silu(v) = v / (1 + exp(-v)), out [m, n] f32 --

@@ -296,14 +296,17 @@ def test_add_rmsnorm_linear_group(m, k, ns, inplace):
 
 @pytest.mark.parametrize("m,k,n,fuse", [(1, 256, 512, "1"), (1, 4096, 14336, "1"), (2, 512, 96, "1"),
                                         (4, 4096, 1000, "1"), (9, 512, 256, "1"), (70, 256, 512, "1"),
-                                        (1, 4096, 1000, "0"), (1, 14336, 300, "0"), (1, 2048, 7, "0")])
+                                        (1, 4096, 1000, "0"), (1, 14336, 300, "0"), (1, 2048, 7, "0"),
+                                        (1, 1024, 300, "1"), (1, 3008, 150, "1"), (1, 2048, 4001, "1")])
 @pytest.mark.parametrize("with_delta", [False, True])
 def test_add_rmsnorm_swiglu(m, k, n, fuse, with_delta, monkeypatch):
-    # decode rows (m <= 4): the gate/up kernel writes silu(gate) * up from its epilogue;
-    # (1, 4096, 14336) takes the separate norm kernel (1792 row blocks) and the
-    # row-group decode form's pairing of gate and up waves, the small ones fuse
-    # the norm into the decode kernel; fuse "0" forces the separate norm kernel
-    # (row-group pairing with ragged n: rows past the end of a workgroup's span)
+    # decode rows (m <= 4): the gate/up kernel writes silu(gate) * up from its epilogue.
+    # One row, 1024 <= k <= 4096: without delta the RMSNorm runs in the quantising
+    # waves of the row-group form's gate/up pairing (two token groups per thread,
+    # the row staged in LDS; k = 3008 leaves half-empty groups and a zero block);
+    # with delta a separate one-workgroup transform runs first.  fuse "0" forces
+    # the separate norm kernel (row-group pairing with ragged n: rows past the end
+    # of a workgroup's span)
     print("add_rmsnorm_swiglu", m, k, n, fuse, with_delta, flush=True)
     monkeypatch.setenv("BTL_FUSE_DEC", fuse)
     rng = np.random.default_rng(m * 31 + k + n)
@@ -377,6 +380,43 @@ def test_one_token_transforms_both_forms(k, kind, form, monkeypatch):
     if add:
         assert_same(ho, hs, "residual")
     assert_same(out, orc.forward_i8(orc.rmsnorm(hs, g, 1e-5), wb, n, sw)[0], kind)
+
+
+@pytest.mark.parametrize("m,k,n,xdt", [(1, 4096, 4096, "f32"), (1, 14336, 4096, "f32"), (1, 4096, 1000, "f32"),
+                                        (1, 1024, 150, "bf16"), (1, 512, 96, "f32"), (1, 1000, 40, "f32"),
+                                        (2, 4096, 300, "f32"), (2, 2048, 200, "bf16"), (3, 1024, 100, "f32"),
+                                        (70, 512, 200, "f32")])
+def test_linear_residual(m, k, n, xdt):
+    # y = resid + x W^T.  One row, 1024 <= k <= 16384 (and two rows, k <= 4096):
+    # the add runs in the row-group decode kernel's epilogue; k < 1024, k % 64 != 0,
+    # three rows and the GEMM add in a launch after the product.
+    print("linear_residual", m, k, n, xdt, flush=True)
+    rng = np.random.default_rng(m * 7 + k + n)
+    x = (rng.standard_normal((m, k)) * 2).astype(np.float32)
+    if xdt == "bf16":
+        xt = torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+        x = xt.float().cpu().numpy()
+    else:
+        xt = torch.from_numpy(x).to(DEV)
+    r = rng.standard_normal((m, n)).astype(np.float32)
+    wb, sw = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), sw, (n, k), DEV)
+    rt = torch.from_numpy(r).to(DEV)
+    y = bl.linear_residual(pt, xt, rt)
+    assert_same(rt, r, "residual untouched")
+    assert_same(y, (r + orc.forward_i8(x, wb, n, sw)[0]).astype(np.float32), "resid + x W^T")
+
+
+def test_linear_residual_rejects_overlap():
+    k, n = 1024, 64
+    pt = bl.PackedTensor(torch.zeros((n * k // 4,), dtype=torch.uint8, device=DEV), 1.0, (n, k), DEV)
+    c = pt.as_c()
+    x = torch.zeros((1, k), device=DEV)
+    r = torch.zeros((1, 2 * n), device=DEV)
+    for y, xx in ((r[:, 1:], x), (x[:, :n], x)):  # y over resid; y over the input
+        st = bl.lib.btl_linear_residual(ctypes.byref(c), xx.data_ptr(), bl.BTL_F32, 1, k, r[:, :n].data_ptr(),
+                                        y.data_ptr(), None, 0, stream())
+        assert st == bl.BTL_ERR_LAYOUT
 
 
 def test_add_rmsnorm_rejects_partial_overlap():
