@@ -1078,6 +1078,12 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
         buf[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                wr, b < rowb ? rho * rowb + b : kOOB, 0, kCachePolicyNT));
     }
+    const int r = R == 4 ? lane / 20 : lane / 40;
+    const bool own = lane - (R == 4 ? 20 : 40) * r == 0;
+    float rres[MT];
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm)
+        rres[mm] = a.resid && own && r < rows && mm < mt ? a.resid[(int64_t)mm * N + row0 + r] : 0.0f;
     rq_wait(&s_sync[1], done);
 
     // 4. one accumulator per token row over every load; slices past the row
@@ -1114,8 +1120,6 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
         if (R == 2) d += __shfl_down(d, 20, 64);
         dm[mm] = d;
     }
-    const int r = R == 4 ? lane / 20 : lane / 40;
-    const bool own = lane - (R == 4 ? 20 : 40) * r == 0;
     if (MT > 1) {
         if (!own || r >= rows) return;
         const int n = row0 + r;
@@ -1126,7 +1130,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
                 const float yv = __fmul_rn((float)dm[mm], __fmul_rn(s_x, SW));
                 const int64_t o = (int64_t)mm * N + n;
                 if (a.ykind == YK_BF16) ((uint16_t*)Y)[o] = f32_to_bf16(yv);
-                else ((float*)Y)[o] = a.resid ? __fadd_rn(a.resid[o], yv) : yv;
+                else ((float*)Y)[o] = a.resid ? __fadd_rn(rres[mm], yv) : yv;
                 if (ACC) ACC[o] = dm[mm];
             }
         }
@@ -1161,7 +1165,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
     }
     if (!own || r >= rows) return;
     if (a.ykind == YK_BF16) ((uint16_t*)Y)[n] = f32_to_bf16(yv);
-    else ((float*)Y)[n] = a.resid ? __fadd_rn(a.resid[n], yv) : yv;  // the residual add of block.rs:119,131
+    else ((float*)Y)[n] = a.resid ? __fadd_rn(rres[0], yv) : yv;  // the residual add of block.rs:119,131
     if (ACC) ACC[n] = d;
 }
 

@@ -419,6 +419,48 @@ def test_linear_residual_rejects_overlap():
         assert st == bl.BTL_ERR_LAYOUT
 
 
+@pytest.mark.parametrize("case", ["tiny", "huge"])
+@pytest.mark.parametrize("k", [2048, 4096])
+def test_one_token_rmsnorm_special_values(k, case):
+    # RMSNorm in the quantising waves of one token row with values at the
+    # edges of f32: zeros of both signs, a subnormal, 2^-100 and a group of
+    # zeros ("tiny"); one 2^62 entry that dominates the mean square ("huge").
+    # Both the gate/up pairing (two token groups per thread) and a plain
+    # launch (one group) must give the oracle's bits.
+    print("rmsnorm special values", k, case, flush=True)
+    rng = np.random.default_rng(k + len(case))
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    if case == "tiny":
+        x[0, 5] = 0.0
+        x[0, 40] = -0.0
+        x[0, 100] = np.float32(1e-40)   # subnormal
+        x[0, 333] = np.float32(2.0 ** -100)
+        x[0, 17 * 16:18 * 16] = 0.0     # a group of zeros
+        x[0, 700] = np.float32(2.0 ** -60)  # the bottom of the range
+    else:
+        x[0, 9] = np.float32(2.0 ** 62)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    xn = orc.rmsnorm(x, g, 1e-5)
+    xt, gt = torch.from_numpy(x).to(DEV), torch.from_numpy(g).to(DEV)
+    n = 300
+    wg, sg = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    wu, su = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    pg = bl.PackedTensor(torch.from_numpy(wg).to(DEV), sg, (n, k), DEV)
+    pu = bl.PackedTensor(torch.from_numpy(wu).to(DEV), su, (n, k), DEV)
+    out = torch.full((1, n), 9.0, device=DEV)
+    cg, cu = pg.as_c(), pu.as_c()
+    bl.check(bl.lib.btl_add_rmsnorm_swiglu(ctypes.byref(cg), ctypes.byref(cu), xt.data_ptr(), None, None,
+                                           gt.data_ptr(), 1e-5, 1, k, out.data_ptr(), None, 0, stream()))
+    e = orc.swiglu(orc.forward_i8(xn, wg, n, sg)[0], orc.forward_i8(xn, wu, n, su)[0])
+    assert_same(out, e, "gate/up pairing")
+    y = torch.empty((1, n), device=DEV)
+    arr = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(cg))
+    ys = (ctypes.c_void_p * 1)(y.data_ptr())
+    bl.check(bl.lib.btl_add_rmsnorm_linear_group(arr, ys, 1, xt.data_ptr(), None, None, gt.data_ptr(), 1e-5, 1, k,
+                                                 bl.BTL_F32, None, 0, stream()))
+    assert_same(y, orc.forward_i8(xn, wg, n, sg)[0], "one group per thread")
+
+
 def test_add_rmsnorm_rejects_partial_overlap():
     k = 256
     h = torch.zeros((2, k), device=DEV)
