@@ -112,6 +112,23 @@ def test_validation_errors_before_device_work():
     assert bl.lib.btl_linear_group(None, None, 5, 16, 0, 1, 8, 0, None, 0, None) == bl.BTL_ERR_ARG
 
 
+def test_linear_residual_validation():
+    # btl_linear_residual checks its arguments before any device work
+    f = bl.lib.btl_linear_residual
+    w = _packed(8, 64, data=16)
+    assert f(ctypes.byref(w), 4096, 9, 1, 64, 8192, 12288, None, 0, None) == bl.BTL_ERR_DTYPE
+    assert f(ctypes.byref(w), 4096, bl.BTL_F32, 1, 32, 8192, 12288, None, 0, None) == bl.BTL_ERR_SHAPE
+    assert f(None, 4096, bl.BTL_F32, 1, 64, 8192, 12288, None, 0, None) == bl.BTL_ERR_ARG
+    assert f(ctypes.byref(w), None, bl.BTL_F32, 1, 64, 8192, 12288, None, 0, None) == bl.BTL_ERR_LAYOUT
+    assert f(ctypes.byref(w), 4096, bl.BTL_F32, 1, 64, None, 12288, None, 0, None) == bl.BTL_ERR_LAYOUT
+    # y overlapping the residual (8 rows of f32 from 8192) or the input (64 f32 from 4096)
+    assert f(ctypes.byref(w), 4096, bl.BTL_F32, 1, 64, 8192, 8196, None, 0, None) == bl.BTL_ERR_LAYOUT
+    assert f(ctypes.byref(w), 4096, bl.BTL_F32, 1, 64, 8192, 4160, None, 0, None) == bl.BTL_ERR_LAYOUT
+    # empty problems are no-ops
+    assert f(ctypes.byref(w), 4096, bl.BTL_F32, 0, 64, 8192, 12288, None, 0, None) == bl.BTL_OK
+    assert f(ctypes.byref(_packed(0, 64)), 4096, bl.BTL_F32, 1, 64, 8192, 12288, None, 0, None) == bl.BTL_OK
+
+
 def test_operand_order_entry_validation():
     w = _packed(64, 128, data=16)
     arr = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(w))
