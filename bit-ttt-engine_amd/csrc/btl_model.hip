@@ -699,12 +699,27 @@ __global__ __launch_bounds__(1024) void k_greedy(const float* x, int n, int32_t*
     const int tid = threadIdx.x;
     uint64_t best = 0;
     const int n4 = n >> 2;
-    for (int i = tid; i < n4; i += 1024) {
-        const float4 v = ((const float4*)x)[i];
-        best = max(best, greedy_key(v.x, 4 * i));
-        best = max(best, greedy_key(v.y, 4 * i + 1));
-        best = max(best, greedy_key(v.z, 4 * i + 2));
-        best = max(best, greedy_key(v.w, 4 * i + 3));
+    // 16 independent loads in flight per thread (the logits come mostly from
+    // other XCDs' writes: one dependent load per step made this latency-bound);
+    // the key order is total, so the visiting order does not change the pick
+    constexpr int kU = 16;
+    for (int i0 = tid; i0 < n4; i0 += 1024 * kU) {
+        float4 v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int i = i0 + 1024 * u;
+            v[u] = i < n4 ? ((const float4*)x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int i = i0 + 1024 * u;
+            if (i < n4) {
+                best = max(best, greedy_key(v[u].x, 4 * i));
+                best = max(best, greedy_key(v[u].y, 4 * i + 1));
+                best = max(best, greedy_key(v[u].z, 4 * i + 2));
+                best = max(best, greedy_key(v[u].w, 4 * i + 3));
+            }
+        }
     }
     for (int i = 4 * n4 + tid; i < n; i += 1024) best = max(best, greedy_key(x[i], i));
 #pragma unroll
