@@ -850,10 +850,11 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
 {
     constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;
     constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;
-    // Two groups per thread (RMSNorm only): the token row and the norm weight
-    // would need all 64 registers at once, so the row waits in LDS (uint4 h of
-    // group gi of thread t at sxs[(4 gi + h) nq + t], after the operand row)
-    // while the weight loads, issued once the row is in, are in flight.
+    // Two groups per thread (RMSNorm only, the SwiGLU pairing): the token row
+    // and the norm weight would need all 64 registers at once, so after the
+    // sum of squares the row waits in LDS (uint4 h of group gi of thread t at
+    // sxs[(4 gi + h) nq + t], after the operand row) while the norm-weight
+    // loads, issued then, are in flight.
     constexpr bool GL = XN && DG == 2;
     uint4* const sxs = (uint4*)(sq + K + 16);
     float fv[DG][16];
