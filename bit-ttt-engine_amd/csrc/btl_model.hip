@@ -656,13 +656,26 @@ __global__ __launch_bounds__(256) void k_embed(const void* table, int64_t vocab,
     const int64_t id = ids[t];
     const bool ok = id >= 0 && id < vocab;
     float* y = out + (int64_t)t * dim;
-    for (int d = threadIdx.x; d < dim; d += 256) {
-        float v = 0.0f;
-        if (ok) {
-            if (XK == XK_BF16) v = __uint_as_float((uint32_t)((const uint16_t*)table)[id * dim + d] << 16);
-            else v = ((const float*)table)[id * dim + d];
+    // all of a pass's loads in flight before its stores (a store between two
+    // loads would order them: one round trip per element otherwise)
+    constexpr int kU = 16;
+    for (int d0 = threadIdx.x; d0 < dim; d0 += 256 * kU) {
+        float v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int d = d0 + 256 * u;
+            v[u] = 0.0f;
+            if (ok && d < dim) {
+                if (XK == XK_BF16) v[u] = __uint_as_float((uint32_t)((const uint16_t*)table)[id * dim + d] << 16);
+                else v[u] = ((const float*)table)[id * dim + d];
+            }
         }
-        y[d] = v;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int d = d0 + 256 * u;
+            if (d < dim) y[d] = v[u];
+        }
     }
 }
 
