@@ -17,6 +17,7 @@ BTL_ERR_DEVICE = 4
 BTL_ERR_HIP = 5
 BTL_ERR_ARG = 6
 BTL_ERR_WORKSPACE = 7
+BTL_ERR_FAULT = 8
 
 BTL_F32 = 0
 BTL_BF16 = 1
@@ -26,7 +27,8 @@ BTL_ACT_I8 = 1
 
 # Every symbol include/bitlinear.h declares.
 EXPORTS = (
-    "btl_version", "btl_last_error", "btl_status_string", "btl_init", "btl_packed_bytes",
+    "btl_version", "btl_last_error", "btl_status_string", "btl_init", "btl_set_tuning", "btl_get_tuning",
+    "btl_check_faults", "btl_packed_bytes",
     "btl_pack_host", "btl_unpack_host", "btl_pack_device", "btl_pack_workspace_bytes", "btl_unpack_device",
     "btl_quantize_act", "btl_linear",
     "btl_linear_i8", "btl_linear_group", "btl_quantize_act_op", "btl_linear_i8_op",
@@ -73,6 +75,9 @@ def _load():
         "btl_last_error": (ctypes.c_char_p, []),
         "btl_status_string": (ctypes.c_char_p, [i32]),
         "btl_init": (i32, [i32]),
+        "btl_set_tuning": (i32, [ctypes.c_char_p, i32]),
+        "btl_get_tuning": (i32, [ctypes.c_char_p, P(i32)]),
+        "btl_check_faults": (i32, [vp]),
         "btl_packed_bytes": (i64, [i64, i64]),
         "btl_pack_host": (i32, [vp, i64, i64, vp, P(f32)]),
         "btl_unpack_host": (i32, [vp, i64, i64, f32, vp]),
@@ -115,6 +120,44 @@ def _load():
 
 
 lib = _load()
+
+
+def get_tuning(name):
+    """Current value of a routing / tuning knob (btl_get_tuning)."""
+    v = ctypes.c_int()
+    check(lib.btl_get_tuning(name.encode(), ctypes.byref(v)))
+    return v.value
+
+
+def set_tuning(name, value):
+    """Set a routing / tuning knob (btl_set_tuning); returns the previous value."""
+    old = get_tuning(name)
+    check(lib.btl_set_tuning(name.encode(), int(value)))
+    return old
+
+
+class tuning:
+    """Context manager: knobs set for the body, restored afterwards.
+    with tuning(BTL_DEC_RQ=0, BTL_DEC_ROW=0): ..."""
+
+    def __init__(self, **knobs):
+        self.knobs = knobs
+        self.saved = {}
+
+    def __enter__(self):
+        for k, v in self.knobs.items():
+            self.saved[k] = set_tuning(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        for k, v in self.saved.items():
+            set_tuning(k, v)
+        return False
+
+
+def check_faults(stream=None):
+    """btl_check_faults: synchronise the stream and raise if a kernel's bounded wait gave up."""
+    check(lib.btl_check_faults(stream))
 
 
 def check(status):

@@ -2,6 +2,7 @@
 import ctypes
 import warnings
 
+import numpy as np
 import torch
 
 from ._lib import (
@@ -242,7 +243,9 @@ class BitLinear:
     def forward(self, x, mode="i8"):
         """bit_linear.rs:52-119: flatten rank > 2 to [B*T, K], run the packed kernel,
         reshape back.  Without packed params this is the reference's STE training
-        path (x @ round(W/mean|W|).clamp(-1,1)^T, no scale; bit_linear.rs:98-118)."""
+        path (bit_linear.rs:98-118): a dense matmul with ste_weight(W), no scale --
+        the reference's path for layers that were never packed, not a fallback of
+        the packed kernel (a packed layer always runs the HIP library)."""
         orig = None
         inp = x
         if x.dim() > 2:
@@ -255,7 +258,36 @@ class BitLinear:
                 return y.reshape(orig)
             return y
         warnings.warn("BitLinear: no packed params, using the STE training path", stacklevel=2)
-        w = self.weight
-        v = w / w.abs().mean()
-        w_q = (torch.sign(v) * torch.floor(v.abs() + 0.5)).clamp(-1.0, 1.0)  # f32::round, half away
-        return x.to(torch.float32) @ w_q.t()
+        return matmul_robust(x.to(torch.float32), ste_weight(self.weight).t())
+
+
+def ste_weight(w):
+    """The straight-through weight of BitLinear's training path (bit_linear.rs:101-110):
+        scale   = mean_all(|w|)                       (no epsilon here, unlike pack)
+        w_s     = w / scale   -> candle's Tensor / f64 = affine(1/scale, 0):
+                  w * (f32)(1 / (f64)scale) + 0
+        w_q     = round(w_s).clamp(-1, 1)             (f32::round: half away from zero)
+        w_ste   = (w_q - w_s).detach() + w_s          (f32 ops; differs from w_q by rounding)
+    Gradients flow to w through w_s (d w_ste / d w = 1 / scale).  The mean is taken in
+    float64 and rounded once; candle's own f32 reduction order is not vendored, so its
+    last ulp is not pinned."""
+    w = w.to(torch.float32)
+    s = float(np.float32(w.detach().abs().double().mean().item())) if w.numel() else float("nan")
+    inv = float(np.float32(1.0 / s)) if s != 0.0 else float("inf")
+    w_s = w * inv + 0.0
+    a = w_s.detach().abs().double()
+    w_q = (torch.sign(w_s.detach()) * torch.floor(a + 0.5).to(torch.float32)).clamp(-1.0, 1.0)
+    return (w_q - w_s).detach() + w_s
+
+
+def matmul_robust(lhs, rhs):
+    """TensorExt::matmul_robust (layers.rs:28-59): rhs moved to lhs's device, rank 1
+    lhs as one row, rank > 2 flattened to [B*T, K] and reshaped back."""
+    lhs = lhs.contiguous()
+    rhs = rhs.contiguous().to(lhs.device)
+    if lhs.dim() == 1:
+        return (lhs.unsqueeze(0) @ rhs).squeeze(0)
+    if lhs.dim() == 2:
+        return lhs @ rhs
+    out = lhs.reshape(-1, lhs.shape[-1]) @ rhs
+    return out.reshape(*lhs.shape[:-1], out.shape[1])

@@ -151,6 +151,20 @@ class BitLlamaHip:
         self._y_o = _ptrs([self.o])
         self._y_down = _ptrs([self.down])
         self._y_logits = _ptrs([self.logits])
+        # the model's own workspace, sized for every call it makes, so captured
+        # steps never depend on the library's shared workspace
+        I8 = 1
+        kvd, qd = c.n_kv_heads * c.head_dim, c.n_heads * c.head_dim
+        need = max(lib.btl_workspace_bytes(M, qd + 2 * kvd, c.hidden, I8),
+                   lib.btl_workspace_bytes(M, c.hidden, qd, I8),
+                   lib.btl_add_rmsnorm_swiglu_workspace_bytes(M, c.intermediate, c.hidden),
+                   lib.btl_workspace_bytes(M, c.hidden, c.intermediate, I8),
+                   lib.btl_workspace_bytes(1, c.vocab, c.hidden, I8),
+                   lib.btl_attention_workspace_bytes(M, c.n_heads, ctypes.byref(self.caches[0].c)))
+        self.ws = torch.empty((need + 256,), dtype=torch.uint8, device=self.dev)
+        base = self.ws.data_ptr()
+        self._ws = ctypes.c_void_p((base + 255) // 256 * 256)
+        self._ws_n = need
         self.pos = 0
         self.graph = None
 
@@ -163,6 +177,7 @@ class BitLlamaHip:
         positions pos.. (or *d_pos.. when d_pos is a device tensor); leaves the last
         row's logits in self.logits."""
         c, st = self.cfg, self._stream()
+        ws, wn = self._ws, self._ws_n
         dp = ctypes.c_void_p(d_pos.data_ptr()) if d_pos is not None else None
         hid = c.hidden
         check(lib.btl_embedding(self.w["embed"].data_ptr(), self.emb_dtype, c.vocab, hid, ids.data_ptr(), m,
@@ -177,35 +192,35 @@ class BitLlamaHip:
             cache = self.caches[li].c
             if li > 0 and not one:
                 check(lib.btl_add_rmsnorm_linear_group(L["qkv"], self._y_qkv, 3, cur.data_ptr(), self.down.data_ptr(),
-                                                       nxt.data_ptr(), L["n1"], c.eps, m, hid, BTL_F32, None, 0, st))
+                                                       nxt.data_ptr(), L["n1"], c.eps, m, hid, BTL_F32, ws, wn, st))
                 cur, nxt = nxt, cur
             else:
                 check(lib.btl_add_rmsnorm_linear_group(L["qkv"], self._y_qkv, 3, cur.data_ptr(), None, None, L["n1"],
-                                                       c.eps, m, hid, BTL_F32, None, 0, st))
+                                                       c.eps, m, hid, BTL_F32, ws, wn, st))
             check(lib.btl_rope_append_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), m,
                                                 c.n_heads, ctypes.byref(cache), pos, dp, self.rope_cos.data_ptr(),
-                                                self.rope_sin.data_ptr(), self.attn.data_ptr(), None, 0, st))
+                                                self.rope_sin.data_ptr(), self.attn.data_ptr(), ws, wn, st))
             if one:
                 check(lib.btl_linear_residual(L["o_w"], self.attn.data_ptr(), BTL_F32, m, c.n_heads * c.head_dim,
-                                              cur.data_ptr(), nxt.data_ptr(), None, 0, st))
+                                              cur.data_ptr(), nxt.data_ptr(), ws, wn, st))
                 cur, nxt = nxt, cur
                 check(lib.btl_add_rmsnorm_swiglu(L["gate"], L["up"], cur.data_ptr(), None, None, L["n2"], c.eps, m,
-                                                 hid, self.hs.data_ptr(), None, 0, st))
+                                                 hid, self.hs.data_ptr(), ws, wn, st))
                 check(lib.btl_linear_residual(L["down_w"], self.hs.data_ptr(), BTL_F32, m, c.intermediate,
-                                              cur.data_ptr(), nxt.data_ptr(), None, 0, st))
+                                              cur.data_ptr(), nxt.data_ptr(), ws, wn, st))
                 cur, nxt = nxt, cur
                 continue
             check(lib.btl_linear_group(L["o"], self._y_o, 1, self.attn.data_ptr(), BTL_F32, m,
-                                       c.n_heads * c.head_dim, BTL_F32, None, 0, st))
+                                       c.n_heads * c.head_dim, BTL_F32, ws, wn, st))
             check(lib.btl_add_rmsnorm_swiglu(L["gate"], L["up"], cur.data_ptr(), self.o.data_ptr(), nxt.data_ptr(),
-                                             L["n2"], c.eps, m, hid, self.hs.data_ptr(), None, 0, st))
+                                             L["n2"], c.eps, m, hid, self.hs.data_ptr(), ws, wn, st))
             cur, nxt = nxt, cur
             check(lib.btl_linear_group(L["down"], self._y_down, 1, self.hs.data_ptr(), BTL_F32, m, c.intermediate,
-                                       BTL_F32, None, 0, st))
+                                       BTL_F32, ws, wn, st))
         last = m - 1
         delta = None if one else self.down[last].data_ptr()
         check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, cur[last].data_ptr(), delta, None,
-                                               self.w["norm_f"].data_ptr(), c.eps, 1, hid, BTL_F32, None, 0, st))
+                                               self.w["norm_f"].data_ptr(), c.eps, 1, hid, BTL_F32, ws, wn, st))
 
     def reset(self):
         """Llama::reset_state / BitLlama::reset_kv_cache (llama.rs:179-186, 460-468)."""
@@ -255,8 +270,9 @@ class BitLlamaHip:
                                   self.d_pos.data_ptr(), self.log.data_ptr(), self.log.numel(), self._stream()))
 
     def capture_decode(self):
-        """Capture one device-position decode step in a HIP graph.  The library
-        workspace must already be large enough (any earlier forward sizes it)."""
+        """Capture one device-position decode step in a HIP graph.  Every call of the
+        step uses the model's own workspace (sized at construction), so later calls
+        of any size elsewhere cannot move memory the graph uses."""
         torch.cuda.synchronize(self.dev)
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(self.dev)
@@ -277,7 +293,8 @@ class BitLlamaHip:
         """n greedy steps on the device, no host synchronisation in between; the
         tokens accumulate in self.log."""
         if self.pos + n > self.cfg.max_seq:
-            raise ValueError("%d steps from position %d overflow the cache of %d rows" % (n, self.pos, self.cfg.max_seq))
+            raise ValueError("%d steps from position %d overflow the cache of %d rows"
+                             % (n, self.pos, self.cfg.max_seq))
         for _ in range(n):
             if use_graph and self.graph is not None:
                 self.graph.replay()

@@ -9,6 +9,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -16,6 +17,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "btl_host.hpp"
 #include "btl_internal.hpp"
@@ -49,6 +51,9 @@ struct DeviceState {
     std::string arch;
     void* ws = nullptr;  // library-owned workspace
     size_t ws_bytes = 0;
+    // workspaces replaced by a larger one; never freed, because a HIP graph
+    // captured while one was current still reads and writes it on replay
+    std::vector<void*> retired;
 };
 
 std::mutex g_mu;
@@ -84,12 +89,43 @@ int current_device(int* dev)
     return probe_device(*dev);
 }
 
-int env_int(const char* name, int dflt)
+// The knobs of btl::Knob: names, built-in defaults, current values.
+struct KnobDef {
+    const char* name;
+    int dflt;
+};
+constexpr KnobDef kKnobs[btl::KN_COUNT] = {
+    {"BTL_GEMV_DEC_PARTS", 0}, {"BTL_DEC_RQ_WPC", 0},     {"BTL_GEMV_DEC_MAX_M", 2},
+    {"BTL_GEMV_DEC", 1},       {"BTL_DEC_ROW_MIN_K", 4096}, {"BTL_DEC_ROW", 1},
+    {"BTL_DEC_ROW_RPW", 0},    {"BTL_DEC_ROW_RB", 0},     {"BTL_GEMV_BAT_MAX_M", 32},
+    {"BTL_GEMV_BAT", 1},       {"BTL_FUSE_MAX_WG", 512},  {"BTL_FUSE_DEC", 1},
+    {"BTL_DEC_RQ_MIN_K", 1024}, {"BTL_DEC_RQ", 1},        {"BTL_DEC_RQ_DG", 0},
+    {"BTL_GEMM_MAX_SPLITS", 0}, {"BTL_GEMM_WIDE_MIN_TILES", btl::kGemmWideMinTiles},
+    {"BTL_WAIT_SPIN", 1 << 22},
+};
+std::atomic<int> g_knob[btl::KN_COUNT];
+std::once_flag g_knob_once;
+
+// the environment, read once per process
+void knobs_init()
 {
-    const char* v = getenv(name);
-    if (!v || !*v) return dflt;
-    return atoi(v);
+    std::call_once(g_knob_once, [] {
+        for (int i = 0; i < btl::KN_COUNT; ++i) {
+            const char* v = getenv(kKnobs[i].name);
+            g_knob[i].store(v && *v ? atoi(v) : kKnobs[i].dflt, std::memory_order_relaxed);
+        }
+    });
 }
+
+int knob_index(const char* name)
+{
+    if (!name) return -1;
+    for (int i = 0; i < btl::KN_COUNT; ++i)
+        if (!strcmp(name, kKnobs[i].name) || !strcmp(name, kKnobs[i].name + 4)) return i;
+    return -1;
+}
+
+inline int env_int(btl::Knob k) { return btl::knob(k); }
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -114,30 +150,32 @@ WsLayout ws_layout(int64_t m, int64_t k, size_t part_bytes)
     return l;
 }
 
-// Library-owned per-device workspace, grown on demand.
-int library_ws(int dev, size_t need, void** out)
+// Library-owned per-device workspace, grown on demand (at least doubling).  A
+// replaced workspace is retired, not freed: graphs captured while it was current
+// keep valid memory (the retired total stays below the current size).  It
+// cannot grow while `st` is being captured (the new buffer would not be the one
+// the graph's later calls expect, and allocation during capture is not
+// ordered with the captured work): the call fails with BTL_ERR_WORKSPACE.
+int library_ws(int dev, size_t need, void** out, hipStream_t st)
 {
     std::lock_guard<std::mutex> lock(g_mu);
     DeviceState& d = g_dev[dev];
     if (d.ws_bytes < need) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(BTL_ERR_WORKSPACE,
+                        "the library workspace of device %d holds %zu bytes and this call needs %zu: it cannot "
+                        "grow while the stream is being captured (make the largest call once before capture, "
+                        "or pass a workspace of btl_workspace_bytes)",
+                        dev, d.ws_bytes, need);
         size_t bytes = align_up(need, (size_t)1 << 20);
-        hipError_t e;
-        if (d.ws) {
-            e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize (workspace growth)");
-            (void)hipFree(d.ws);
-            d.ws = nullptr;
-            d.ws_bytes = 0;
-        }
+        if (bytes < 2 * d.ws_bytes) bytes = 2 * d.ws_bytes;
         void* p = nullptr;
         e = hipMalloc(&p, bytes);
         if (e != hipSuccess) return hip_fail(e, "hipMalloc (workspace)");
-        e = hipMemset(p, 0, bytes);
-        if (e == hipSuccess) e = hipDeviceSynchronize();
-        if (e != hipSuccess) {
-            (void)hipFree(p);
-            return hip_fail(e, "hipMemset (workspace)");
-        }
+        if (d.ws) d.retired.push_back(d.ws);
         d.ws = p;
         d.ws_bytes = bytes;
     }
@@ -145,9 +183,9 @@ int library_ws(int dev, size_t need, void** out)
     return BTL_OK;
 }
 
-int get_ws(int dev, void* ws, size_t ws_bytes, size_t need, void** out)
+int get_ws(int dev, void* ws, size_t ws_bytes, size_t need, void** out, hipStream_t st)
 {
-    if (!ws) return library_ws(dev, need, out);
+    if (!ws) return library_ws(dev, need, out, st);
     if (ws_bytes < need)
         return fail(BTL_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu needed", ws_bytes,
                     need);
@@ -239,7 +277,7 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
     if (m < 1 || m > 4 || k <= 0) return 0;
     int w = (int)ceil_div(k, 1024);
     if (w > 8) w = (int)ceil_div(k, 2048);
-    const int forced = env_int("BTL_GEMV_DEC_PARTS", 0);
+    const int forced = env_int(btl::KN_GEMV_DEC_PARTS);
     if (forced >= 1 && forced <= 16) w = forced;
     const int rb = (w == 1 || w == 2 || w == 4) ? 4 / w : 1;
     const int64_t kp = ceil_div(ceil_div(k, w), btl::kStepWeights) * btl::kStepWeights;
@@ -263,7 +301,7 @@ int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n, boo
     const int64_t waves = pair_n ? 2 * ceil_div(pair_n, rows) : rb_total * (16 / rows);
     const int hi = 16 - btl::rq_quant_waves((int)k, xform ? 1 : 2, m);
     const int step = pair_n ? 2 : 1;
-    const int forced = env_int("BTL_DEC_RQ_WPC", 0);
+    const int forced = env_int(btl::KN_DEC_RQ_WPC);
     if (forced >= step && forced <= hi && forced % step == 0) return forced;
     if (cus < 1) cus = 1;
     int best = step;
@@ -331,7 +369,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         const bool scratch = xkind != btl::XK_I8;
         const WsLayout L = ws_layout(m, k, 0);
         void* ws = nullptr;
-        if (scratch && (rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
+        if (scratch && (rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws, st))) return rc;
         const int8_t* q = (const int8_t*)x;
         const float* s = xs;
         if (scratch) {
@@ -358,14 +396,14 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     // MI355X, Llama-3-8B MLP at m = 4: 24.8 against 29.2 us per layer through
     // the decode kernel); a transform or the SwiGLU epilogue keeps the decode
     // kernel.  BTL_GEMV_DEC_MAX_M overrides the limit (tuning, tests).
-    const int dec_max_m = xf || swiglu_out ? 4 : env_int("BTL_GEMV_DEC_MAX_M", 2);
-    int wv = env_int("BTL_GEMV_DEC", 1) != 0 && m <= dec_max_m ? dec_waves(m, k, &rbw) : 0;
+    const int dec_max_m = xf || swiglu_out ? 4 : env_int(btl::KN_GEMV_DEC_MAX_M);
+    int wv = env_int(btl::KN_GEMV_DEC) != 0 && m <= dec_max_m ? dec_waves(m, k, &rbw) : 0;
     const bool dec = wv > 0;
     // One token row, k a multiple of 64 up to 16384: the row-contiguous form
     // (whole weight rows per wave, 1 KB per load instruction, no K parts).
     // Measured on MI355X for k >= 4096 (Llama-3-8B decode shapes).
-    const int rowc = dec && m == 1 && k % 64 == 0 && k >= env_int("BTL_DEC_ROW_MIN_K", 4096) && k <= 16384 &&
-                             env_int("BTL_DEC_ROW", 1) != 0
+    const int rowc = dec && m == 1 && k % 64 == 0 && k >= env_int(btl::KN_DEC_ROW_MIN_K) && k <= 16384 &&
+                             env_int(btl::KN_DEC_ROW) != 0
                          ? (k <= 4096 ? 1 : (k <= 8192 ? 2 : 4))
                          : 0;
     if (rowc) {
@@ -376,7 +414,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         // transform keep the default)
         int rpw = btl::dec_row_st(rowc) / rowc;
         rbw = 1;
-        const int rpw_env = env_int("BTL_DEC_ROW_RPW", 0), rb_env = env_int("BTL_DEC_ROW_RB", 0);
+        const int rpw_env = env_int(btl::KN_DEC_ROW_RPW), rb_env = env_int(btl::KN_DEC_ROW_RB);
         if (!xf && (rpw_env == 1 || rpw_env == 2 || rpw_env == 4 || rpw_env == 8 || rpw_env == 16)) {
             rpw = rpw_env;
             while (rowc * rpw > 16) rpw >>= 1;
@@ -390,7 +428,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         if (!dec || wv > 8) return fail(BTL_ERR_ARG, "SwiGLU epilogue needs the decode route");
         rbw = 2;  // workgroup w: row block w of gate and of up
     }
-    const bool bat = !dec && m <= env_int("BTL_GEMV_BAT_MAX_M", 32) && m <= 64 && env_int("BTL_GEMV_BAT", 1) != 0;
+    const bool bat = !dec && m <= env_int(btl::KN_GEMV_BAT_MAX_M) && m <= 64 && env_int(btl::KN_GEMV_BAT) != 0;
     int split_steps = 0, splits = 1;
     if (!dec)
         splits = bat ? btl::gemv_bat_split(m, gemv_row_blocks(layers, count), k, &split_steps)
@@ -401,15 +439,14 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     // for f32 input, when the row fits the workgroup for the norm's pairwise
     // sum, and (residual add) when the summed stream goes to another buffer.
     // Every workgroup repeats the transform, so it pays only for launches of
-    // at most kFuseMaxWg workgroups (measured on MI355X, Llama-3-8B shapes:
+    // at most KN_FUSE_MAX_WG workgroups (measured on MI355X, Llama-3-8B shapes:
     // q|k|v with 384 and down with 256 gain ~2 us; gate|up with 1792 and the
     // 128256-row head lose 2-20 us against the separate one-workgroup
     // transform kernel).
-    constexpr int64_t kFuseMaxWg = 512;
     int64_t dec_rb = 0;
     for (int i = 0; i < count; ++i) dec_rb += ceil_div(layers[i].w->n, 16);
-    const int64_t fuse_max_wg = env_int("BTL_FUSE_MAX_WG", (int)kFuseMaxWg);
-    const bool xf_ok = xf && m == 1 && xkind == btl::XK_F32 && env_int("BTL_FUSE_DEC", 1) != 0 &&
+    const int64_t fuse_max_wg = env_int(btl::KN_FUSE_MAX_WG);
+    const bool xf_ok = xf && m == 1 && xkind == btl::XK_F32 && env_int(btl::KN_FUSE_DEC) != 0 &&
                        !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
 
     // One token row (two for k <= 4096; measured on MI355X, Llama-3-8B MLP: the
@@ -417,9 +454,9 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     // take half of every workgroup): the row-group form (R whole rows per
     // wave, one accumulator per token row, workgroups of up to 16 waves of
     // which only the first few quantise the tokens).  Its quantising waves also apply a transform (k <=
-    // 4096, no SwiGLU epilogue, at most kFuseMaxWg workgroups: each repeats
+    // 4096, no SwiGLU epilogue, at most KN_FUSE_MAX_WG workgroups: each repeats
     // it); the SwiGLU pairing takes tokens transformed by a launch of their own.
-    const bool rq_on = dec && k % 64 == 0 && k >= env_int("BTL_DEC_RQ_MIN_K", 1024) && env_int("BTL_DEC_RQ", 1) != 0 &&
+    const bool rq_on = dec && k % 64 == 0 && k >= env_int(btl::KN_DEC_RQ_MIN_K) && env_int(btl::KN_DEC_RQ) != 0 &&
                        ((m == 1 && k <= 16384) || (m == 2 && k <= 4096 && !xf && !swiglu_out));
     bool rqx = false;
     int rqx_wpc = 0;
@@ -430,7 +467,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         rqx = (swiglu_out ? ceil_div(ceil_div(pn, 4), rqx_wpc / 2) : ceil_div(dec_rb * 4, rqx_wpc)) <= fuse_max_wg;
     }
     // Otherwise the K-part / row-contiguous decode kernel applies a transform in
-    // its own prologue for launches of at most kFuseMaxWg workgroups.
+    // its own prologue for launches of at most KN_FUSE_MAX_WG workgroups.
     const bool fuse = !rqx && dec && xf_ok && ceil_div(dec_rb, rbw) <= fuse_max_wg && wv * rbw <= 8 &&
                       k / 16 <= (int64_t)(xf->kind == btl::XF_SWIGLU ? 2 : 1) * wv * rbw * 64;
     const bool rq = rq_on && !fuse && (!swiglu_out || xf);
@@ -442,7 +479,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     void* ws = nullptr;
     WsLayout L = ws_layout(m, k, splits > 1 ? (size_t)splits * m * nsum * 4 : 0);
     if (pre) {
-        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws))) return rc;
+        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws, st))) return rc;
         q = (const int8_t*)ws + L.q_off;
         if (xf) {
             sxp = (const float*)((uint8_t*)ws + L.s_off);
@@ -494,6 +531,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         }
         a.swiglu_out = swiglu_out;
         a.rowc = rowc;
+        a.spin = env_int(btl::KN_WAIT_SPIN);
         if (rq) {
             a.parts = rqx ? rqx_wpc
                           : rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0, false, (int)m);
@@ -502,7 +540,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
             // shorter prologue for the launches of few compute waves
             a.tiles = (rqx && !swiglu_out) ||
                               (!rqx && m == 1 && k <= 4096 && !swiglu_out &&
-                               btl::rq_quant_waves((int)k, 1) + a.parts <= 16 && env_int("BTL_DEC_RQ_DG", 0) != 2)
+                               btl::rq_quant_waves((int)k, 1) + a.parts <= 16 && env_int(btl::KN_DEC_RQ_DG) != 2)
                           ? 1
                           : 2;
             a.resid = count == 1 ? resid : nullptr;
@@ -583,12 +621,50 @@ const char* btl_status_string(int status)
     case BTL_ERR_HIP: return "BTL_ERR_HIP";
     case BTL_ERR_ARG: return "BTL_ERR_ARG";
     case BTL_ERR_WORKSPACE: return "BTL_ERR_WORKSPACE";
+    case BTL_ERR_FAULT: return "BTL_ERR_FAULT";
     default: return "BTL_ERR_UNKNOWN";
     }
 }
 
+int btl_set_tuning(const char* name, int value)
+{
+    knobs_init();
+    const int i = knob_index(name);
+    if (i < 0) return fail(BTL_ERR_ARG, "unknown tuning knob '%s'", name ? name : "(null)");
+    g_knob[i].store(value, std::memory_order_relaxed);
+    return BTL_OK;
+}
+
+int btl_get_tuning(const char* name, int* value)
+{
+    knobs_init();
+    const int i = knob_index(name);
+    if (i < 0) return fail(BTL_ERR_ARG, "unknown tuning knob '%s'", name ? name : "(null)");
+    if (!value) return fail(BTL_ERR_ARG, "null pointer");
+    *value = g_knob[i].load(std::memory_order_relaxed);
+    return BTL_OK;
+}
+
+int btl_check_faults(void* stream)
+{
+    int dev;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    uint32_t bits = 0;
+    hipError_t e = btl::read_clear_faults(&bits, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "reading the device fault word");
+    if (bits)
+        return fail(BTL_ERR_FAULT,
+                    "a bounded wait inside a kernel gave up on device %d (fault bits 0x%x: %s%s); the outputs of "
+                    "the calls since the last check are not valid",
+                    dev, bits, (bits & btl::kFaultRqWait) ? "decode workgroup token row" : "",
+                    (bits & btl::kFaultStream) ? " decode stream stage" : "");
+    return BTL_OK;
+}
+
 int btl_init(int device)
 {
+    knobs_init();
     int count = 0;
     hipError_t e = hipGetDeviceCount(&count);
     if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
@@ -668,7 +744,7 @@ int btl_pack_device(const float* w, int64_t n, int64_t k, uint8_t* out, float* s
         return e == hipSuccess ? BTL_OK : hip_fail(e, "scale copy");
     }
     void* wsp = nullptr;
-    if ((rc = get_ws(dev, ws, ws_bytes, btl_pack_workspace_bytes(n, k), &wsp))) return rc;
+    if ((rc = get_ws(dev, ws, ws_bytes, btl_pack_workspace_bytes(n, k), &wsp, (hipStream_t)stream))) return rc;
     e = btl::launch_pack(w, numel, out, scale, (double*)wsp, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "pack kernel launch");
     return BTL_OK;
@@ -896,7 +972,7 @@ int btl_add_rmsnorm_swiglu(const btl_packed_t* w_gate, const btl_packed_t* w_up,
     if (m > INT32_MAX / 2 || n * m > ((int64_t)1 << 40)) return fail(BTL_ERR_SHAPE, "dimension too large");
     const Xform xf{delta ? btl::XF_ADD_RMSNORM : btl::XF_RMSNORM, delta, g, eps, delta ? h_out : nullptr};
     int rbw = 1;
-    const bool dec = env_int("BTL_GEMV_DEC", 1) != 0 && dec_waves(m, k, &rbw) > 0 && dec_waves(m, k, &rbw) <= 8;
+    const bool dec = env_int(btl::KN_GEMV_DEC) != 0 && dec_waves(m, k, &rbw) > 0 && dec_waves(m, k, &rbw) <= 8;
     const hipStream_t st = (hipStream_t)stream;
     if (dec) {
         // the decode kernel writes silu(gate) * up from its epilogue
@@ -910,7 +986,7 @@ int btl_add_rmsnorm_swiglu(const btl_packed_t* w_gate, const btl_packed_t* w_up,
     const size_t inner = btl_workspace_bytes(m, 2 * n, k, BTL_ACT_I8);
     const size_t ybytes = align_up((size_t)(m * n * 4), 256);
     void* wsp = nullptr;
-    if ((rc = get_ws(dev, ws, ws_bytes, inner + 2 * ybytes, &wsp))) return rc;
+    if ((rc = get_ws(dev, ws, ws_bytes, inner + 2 * ybytes, &wsp, st))) return rc;
     float* yg = (float*)((uint8_t*)wsp + inner);
     float* yu = (float*)((uint8_t*)wsp + inner + ybytes);
     ls[0].y = yg;
@@ -995,8 +1071,8 @@ int btl_adaptive_linear(const btl_packed_t* const* bases, int nb, const void* x,
     const size_t inner = btl_workspace_bytes(m, chunk * n, k, BTL_ACT_I8);
     const size_t ybytes = align_up((size_t)(m * n * 4), 256);
     void* wsp = nullptr;
-    if ((rc = get_ws(dev, ws, ws_bytes, inner + (size_t)nb * ybytes, &wsp))) return rc;
     const hipStream_t st = (hipStream_t)stream;
+    if ((rc = get_ws(dev, ws, ws_bytes, inner + (size_t)nb * ybytes, &wsp, st))) return rc;
     btl::AdaptiveSum sum;
     memset(&sum, 0, sizeof(sum));
     // every base's f32 output y_b = (float)acc_b * (s_x * s_b), up to kMaxGroup bases per launch
@@ -1075,9 +1151,15 @@ namespace host {
 int fail_msg(int code, const char* msg) { return fail(code, "%s", msg); }
 int hip_error(hipError_t e, const char* what) { return hip_fail(e, what); }
 int device(int* dev) { return current_device(dev); }
-int workspace(int dev, void* ws, size_t ws_bytes, size_t need, void** out)
+int workspace(int dev, void* ws, size_t ws_bytes, size_t need, void** out, hipStream_t st)
 {
-    return get_ws(dev, ws, ws_bytes, need, out);
+    return get_ws(dev, ws, ws_bytes, need, out, st);
 }
 }  // namespace host
+
+int knob(Knob k)
+{
+    knobs_init();
+    return g_knob[k].load(std::memory_order_relaxed);
+}
 }  // namespace btl

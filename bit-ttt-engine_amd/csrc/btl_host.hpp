@@ -15,6 +15,6 @@ int hip_error(hipError_t e, const char* what);
 int device(int* dev);
 // The caller's workspace when ws != NULL (checked against `need`), else the
 // library's per-device workspace grown to `need` bytes.
-int workspace(int dev, void* ws, size_t ws_bytes, size_t need, void** out);
+int workspace(int dev, void* ws, size_t ws_bytes, size_t need, void** out, hipStream_t st);
 }  // namespace host
 }  // namespace btl

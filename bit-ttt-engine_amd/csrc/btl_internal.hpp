@@ -8,6 +8,43 @@
 
 namespace btl {
 
+// Routing and tuning knobs.  Each starts from the environment variable of its
+// name ("BTL_" + the enumerator's suffix) when set, read once at the first
+// library call, else from its built-in default; afterwards only
+// btl_set_tuning changes it, so the process environment cannot re-route calls.
+enum Knob {
+    KN_GEMV_DEC_PARTS,       // force the K parts of the decode kernel (1..16; 0 = measured rule)
+    KN_DEC_RQ_WPC,           // force the compute waves of the row-group decode form (0 = rule)
+    KN_GEMV_DEC_MAX_M,       // plain launches of up to this many rows take the decode kernel (2)
+    KN_GEMV_DEC,             // 0 turns the decode kernel off (1)
+    KN_DEC_ROW_MIN_K,        // row-contiguous decode form from this k on (4096)
+    KN_DEC_ROW,              // 0 turns the row-contiguous form off (1)
+    KN_DEC_ROW_RPW,          // force rows per wave of the row-contiguous form (0 = rule)
+    KN_DEC_ROW_RB,           // force row blocks per workgroup of the row-contiguous form (0 = rule)
+    KN_GEMV_BAT_MAX_M,       // batched decode up to this many rows (32)
+    KN_GEMV_BAT,             // 0 turns the batched decode kernel off (1)
+    KN_FUSE_MAX_WG,          // fuse transforms into decode launches of at most this many workgroups (512)
+    KN_FUSE_DEC,             // 0 turns transform fusion into the decode kernels off (1)
+    KN_DEC_RQ_MIN_K,         // row-group decode form from this k on (1024)
+    KN_DEC_RQ,               // 0 turns the row-group decode form off (1)
+    KN_DEC_RQ_DG,            // 2 forces two token groups per quantising thread (0 = rule)
+    KN_GEMM_MAX_SPLITS,      // cap on the K splits of the GEMM (0 = none; 1 turns split-K off)
+    KN_GEMM_WIDE_MIN_TILES,  // 256-row GEMM tiles from this many workgroups on (512)
+    KN_WAIT_SPIN,            // polls before a kernel's internal wait gives up (2^22; the only
+                             // knob that can change results: a wait that gives up leaves
+                             // invalid outputs and sets the device fault word)
+    KN_COUNT
+};
+int knob(Knob k);
+
+// Device fault word: bits set by a kernel whose bounded wait gave up (the
+// outputs of that launch are then not valid); btl_check_faults reads and
+// clears it.
+constexpr uint32_t kFaultRqWait = 1u;  // k_gemv_rq: a compute wave's wait for the token row
+constexpr uint32_t kFaultStream = 2u;  // the decode stream: a stage's wait for its input
+// the fault bits of every kernel source, read after the stream's work, then cleared
+hipError_t read_clear_faults(uint32_t* bits, hipStream_t st);
+
 constexpr int kMaxGroup = 4;       // layers per grouped launch (q|k|v, w1|w3)
 constexpr int kStepWeights = 256;  // weights of one row consumed per wave-load (64 B)
 
@@ -55,6 +92,9 @@ struct GemvArgs {
     // residual stream added to the f32 output (the row-group form, one layer):
     // y = resid + (float)acc * (s_x * s_w); y may be resid
     const float* resid;
+    // bound (polls) of the row-group form's LDS waits; one that gives up sets
+    // kFaultRqWait
+    int spin;
     // row-contiguous form (m == 1, k % 64 == 0): 0 = K parts; 1, 2, 4 = whole
     // rows of up to that many 4096-weight chunks, 16 / parts rows per wave
     // (parts in {1, 2, 4, 8}, chunks * 16 / parts loads of 1 KB per wave in

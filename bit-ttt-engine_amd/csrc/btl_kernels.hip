@@ -755,8 +755,8 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
 // loads at once and wait for the quantised row on an LDS counter, not on a
 // barrier, so no wave waits for another wave's loads to issue (the memory
 // queue of a CU back-pressures the issue of later loads for microseconds).
-// Every wait is bounded by kRqSpinMax polls.
-constexpr int kRqSpinMax = 1 << 22;    // bound of every LDS poll (~0.1 s)
+// Every wait is bounded by a.spin polls (BTL_WAIT_SPIN, 2^22 by default, ~0.1 s);
+// a wait that gives up sets kFaultRqWait in the device fault word.
 
 template <int R>
 struct RqShape {
@@ -764,12 +764,18 @@ struct RqShape {
     static constexpr int kBytes = 1024 / R;  // bytes of a row per load instruction
 };
 
-__device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target)
+// Fault bits of this source's kernels (kFault*), read and cleared by the host.
+__device__ uint32_t g_faults;
+
+__device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target, int spin)
 {
-    for (int it = 0; it < kRqSpinMax; ++it) {
+    int it = 0;
+    for (; it < spin; ++it) {
         if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
         __builtin_amdgcn_s_sleep(1);
     }
+    // gave up: the row in LDS is incomplete and this launch's outputs are not valid
+    if (it >= spin) __hip_atomic_fetch_or(&g_faults, kFaultRqWait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
@@ -782,7 +788,7 @@ __device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target)
 template <int XK, int DG, int MT>
 __device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], int K, int gpr, int mt, int nqw,
                                             int nq, int tid, int lane, uint8_t* sq, uint32_t* s_sync,
-                                            uint32_t* s_amax, float* s_scale)
+                                            uint32_t* s_amax, float* s_scale, int spin)
 {
     constexpr bool PREQ = DecX<XK>::kPreq;
     const int ng = mt * gpr;
@@ -809,7 +815,7 @@ __device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], i
             }
         }
         if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        rq_wait(&s_sync[1], (uint32_t)nqw);
+        rq_wait(&s_sync[1], (uint32_t)nqw, spin);
         // lane mm holds row mm's parameters
         const QParams qp = qparams(
             __hip_atomic_load(&s_amax[MT == 1 ? 0 : min(lane, mt - 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
@@ -911,7 +917,7 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        rq_wait(&s_sync[1], (uint32_t)nqw);
+        rq_wait(&s_sync[1], (uint32_t)nqw, a.spin);
         const int nblk = DG * nqw;
         float p[16];
 #pragma unroll
@@ -947,7 +953,7 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
         __hip_atomic_fetch_max(&s_amax[0], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-    rq_wait(&s_sync[1], (PH - 1u) * (uint32_t)nqw);
+    rq_wait(&s_sync[1], (PH - 1u) * (uint32_t)nqw, a.spin);
     const QParams qp = qparams(__hip_atomic_load(&s_amax[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     const float rm = qp.ok ? qp.r : 0.0f;
     if (tid == 0) s_scale[0] = qp.s;
@@ -1029,7 +1035,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
             rq_transform<XF, DG>(a, xv, x2v, gv, K, gpr, nqw, nq, PH, tid, lane, wave, sq, s_sync, s_amax, s_scale,
                                  s_ss);
         else
-            rq_quantise<XK, DG, MT>(xv, K, gpr, mt, nqw, nq, tid, lane, sq, s_sync, s_amax, s_scale);
+            rq_quantise<XK, DG, MT>(xv, K, gpr, mt, nqw, nq, tid, lane, sq, s_sync, s_amax, s_scale, a.spin);
         return;
     }
     __syncthreads();
@@ -1085,7 +1091,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm)
         rres[mm] = a.resid && own && r < rows && mm < mt ? a.resid[(int64_t)mm * N + row0 + r] : 0.0f;
-    rq_wait(&s_sync[1], done);
+    rq_wait(&s_sync[1], done, a.spin);
 
     // 4. one accumulator per token row over every load; slices past the row
     //    read the activations at k = 0 (their weights are zero), token rows
@@ -1150,7 +1156,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             if (lane == 0) __hip_atomic_fetch_add(&s_sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         } else {
-            rq_wait(&s_sync[2], (uint32_t)half);
+            rq_wait(&s_sync[2], (uint32_t)half, a.spin);
         }
         if (!own || r >= rows) return;
         if (Y) {
@@ -1868,8 +1874,8 @@ int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps)
     const int64_t steps = (k + kGemmBK - 1) / kGemmBK;
     const int64_t tiles = (m + kGemmBM - 1) / kGemmBM * tiles_n;
     int64_t s = tiles >= kGemmSplitTarget || tiles <= 0 ? 1 : (kGemmSplitTarget + tiles - 1) / tiles;
-    const char* ev = getenv("BTL_GEMM_MAX_SPLITS");  // tuning / tests: 1 turns split-K off
-    if (ev && *ev && atoll(ev) >= 1 && s > atoll(ev)) s = atoll(ev);
+    const int cap = knob(KN_GEMM_MAX_SPLITS);  // tuning / tests: 1 turns split-K off
+    if (cap >= 1 && s > cap) s = cap;
     if (s > steps / 2) s = steps / 2;  // at least two K steps per split
     if (s < 1) s = 1;
     const int64_t per = (steps + s - 1) / s;
@@ -1886,8 +1892,7 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     const int64_t tiles_m = (g.m + kGemmBM - 1) / kGemmBM;
     int64_t tn256 = 0;
     for (int l = 0; l < g.nl; ++l) tn256 += (g.L[l].n + 255) / 256;
-    const char* ev = getenv("BTL_GEMM_WIDE_MIN_TILES");
-    const int64_t wide_min = ev && *ev ? atoll(ev) : kGemmWideMinTiles;
+    const int64_t wide_min = knob(KN_GEMM_WIDE_MIN_TILES);
     const int TN = g.splits <= 1 && tiles_m * tn256 >= wide_min ? 256 : 128;
     int64_t tn = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
@@ -2478,6 +2483,23 @@ __global__ __launch_bounds__(256) void k_fill_zero(uint8_t* p, size_t bytes)
     } else {
         for (size_t j = i; j < bytes; ++j) p[j] = 0;
     }
+}
+
+hipError_t read_clear_faults_kernels(uint32_t* bits, hipStream_t st)
+{
+    hipError_t e = hipMemcpyFromSymbolAsync(bits, HIP_SYMBOL(g_faults), sizeof(uint32_t), 0, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess || !*bits) return e;
+    static const uint32_t zero = 0;
+    e = hipMemcpyToSymbolAsync(HIP_SYMBOL(g_faults), &zero, sizeof(uint32_t), 0, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e;
+}
+
+hipError_t read_clear_faults(uint32_t* bits, hipStream_t st)
+{
+    *bits = 0;
+    return read_clear_faults_kernels(bits, st);
 }
 
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t st)

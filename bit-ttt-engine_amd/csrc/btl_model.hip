@@ -53,6 +53,13 @@ __device__ __forceinline__ uint32_t sat_u8(float r)
     return (uint32_t)r;
 }
 
+// kv_cache.rs:101 `max_val / 127.0`: candle's Tensor / f64 is affine(1/127, 0), a multiply
+// by the f32-rounded reciprocal plus zero, not a division
+__device__ __forceinline__ float q8_scale(float amax)
+{
+    return __fadd_rn(__fmul_rn(amax, (float)(1.0 / 127.0)), 0.0f);
+}
+
 // ---------------------------------------------------------------------------
 // k_rope_kv_q8
 // ---------------------------------------------------------------------------
@@ -95,9 +102,9 @@ __global__ __launch_bounds__(64) void k_rope_kv_q8(KvArgs a)
         }
         return;
     }
-    // quantize_q8 (kv_cache.rs:95-119): s = max|x| / 127, code = u8(round(x / s) + 128)
+    // quantize_q8 (kv_cache.rs:95-119): s = max|x| * (f32)(1/127), code = u8(round(x / s) + 128)
     const uint32_t am = wave_max_dpp(max(__float_as_uint(x1) & 0x7FFFFFFFu, __float_as_uint(x2) & 0x7FFFFFFFu));
-    const float s = __fdiv_rn(__uint_as_float(am), 127.0f);
+    const float s = q8_scale(__uint_as_float(am));
     const int64_t row = (int64_t)head * a.max_seq + pos;
     uint8_t* cache = (kind == 1 ? a.kc : a.vc) + row * hd;
     if (act) {
@@ -379,7 +386,7 @@ __global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
             }
             const uint32_t am =
                 wave_max_dpp(max(__float_as_uint(x1) & 0x7FFFFFFFu, __float_as_uint(x2) & 0x7FFFFFFFu));
-            const float sc = __fdiv_rn(__uint_as_float(am), 127.0f);
+            const float sc = q8_scale(__uint_as_float(am));
             const int64_t row = (int64_t)g * a.max_seq + pos;
             uint8_t* cache = (which == 0 ? kv.kc_w : kv.vc_w) + row * hd;
             float* srow = which == 0 ? &s_k[pos - j0][0] : &s_v[pos - j0][0];

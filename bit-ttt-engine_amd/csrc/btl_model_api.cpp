@@ -80,7 +80,12 @@ int btl_rope_table(double theta, int64_t head_dim, int64_t max_seq, float* cos_o
     if (max_seq && (!cos_out || !sin_out)) return fail_msg(BTL_ERR_ARG, "null output");
     const int64_t half = head_dim / 2;
     std::vector<float> inv((size_t)half);
-    for (int64_t i = 0; i < half; ++i) inv[(size_t)i] = (float)(1.0 / std::pow(theta, (double)(2 * i) / (double)head_dim));
+    // attention.rs:19 `1.0 / (theta.powf(2i / hd)) as f32`: the cast binds first, so the
+    // f64 power is rounded to f32 and the reciprocal is an f32 division
+    for (int64_t i = 0; i < half; ++i) {
+        const float pw = (float)std::pow(theta, (double)(2 * i) / (double)head_dim);
+        inv[(size_t)i] = 1.0f / pw;
+    }
     for (int64_t p = 0; p < max_seq; ++p)
         for (int64_t i = 0; i < half; ++i) {
             const float f = (float)p * inv[(size_t)i];
@@ -144,7 +149,8 @@ int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t*
     int dev;
     if ((rc = btl::host::device(&dev))) return rc;
     void* wsp = nullptr;
-    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &wsp)))
+    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &wsp,
+                                   (hipStream_t)stream)))
         return rc;
     void* part = (uint8_t*)wsp + qrot_bytes(m, n_heads, cache);
     btl::AttnArgs a{};
@@ -183,7 +189,8 @@ int btl_rope_append_attention(const float* q, const float* k, const float* v, in
     int dev;
     if ((rc = btl::host::device(&dev))) return rc;
     void* wsp = nullptr;
-    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &wsp)))
+    if ((rc = btl::host::workspace(dev, ws, ws_bytes, btl_attention_workspace_bytes(m, n_heads, cache), &wsp,
+                                   (hipStream_t)stream)))
         return rc;
     float* qrot = (float*)wsp;
     btl::AttnArgs a{};

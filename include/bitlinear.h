@@ -26,8 +26,12 @@
  *    device function is asynchronous with respect to the host and stream ordered.
  *  - Nothing here allocates or frees caller memory.  Functions that take a
  *    workspace accept ws == NULL, in which case the library uses a per-device
- *    workspace it owns (allocated and grown with hipMalloc; calls that share
- *    it must be ordered on one stream).
+ *    workspace it owns (allocated with hipMalloc and grown by at least
+ *    doubling; a replaced workspace is kept until the process ends, so HIP
+ *    graphs captured earlier stay valid; it cannot grow while the call's
+ *    stream is being captured -- BTL_ERR_WORKSPACE -- so make the largest call
+ *    once before capturing, or pass a workspace).  Calls that share the
+ *    library's workspace must be ordered on one stream.
  *  - Functions are reentrant: no per-call global state besides that workspace
  *    and the per-thread error message.
  */
@@ -51,7 +55,9 @@ extern "C" {
 #define BTL_ERR_DEVICE 4    /* no usable gfx950 device / pointer not on the device */
 #define BTL_ERR_HIP 5       /* a HIP runtime call failed */
 #define BTL_ERR_ARG 6       /* any other invalid argument */
-#define BTL_ERR_WORKSPACE 7 /* caller workspace smaller than btl_workspace_bytes() */
+#define BTL_ERR_WORKSPACE 7 /* caller workspace smaller than btl_workspace_bytes(), or the
+                               library's cannot grow during stream capture */
+#define BTL_ERR_FAULT 8     /* btl_check_faults: a kernel's bounded wait gave up */
 
 /* Element types of activations and outputs. */
 #define BTL_F32 0
@@ -92,6 +98,38 @@ const char* btl_status_string(int status);
  * Idempotent and thread-safe; every device function also initialises lazily.
  */
 int btl_init(int device);
+
+/*
+ * Routing and tuning knobs (no reference counterpart: the reference has one
+ * kernel per device).  Each knob starts from the environment variable of its
+ * name when set -- read once, at the first library call -- else from a
+ * measured default; afterwards only btl_set_tuning changes it, so the
+ * environment of a running process cannot re-route calls.  Names are
+ * "BTL_GEMV_DEC_PARTS", "BTL_DEC_RQ_WPC", "BTL_GEMV_DEC_MAX_M", "BTL_GEMV_DEC",
+ * "BTL_DEC_ROW_MIN_K", "BTL_DEC_ROW", "BTL_DEC_ROW_RPW", "BTL_DEC_ROW_RB",
+ * "BTL_GEMV_BAT_MAX_M", "BTL_GEMV_BAT", "BTL_FUSE_MAX_WG", "BTL_FUSE_DEC",
+ * "BTL_DEC_RQ_MIN_K", "BTL_DEC_RQ", "BTL_DEC_RQ_DG", "BTL_GEMM_MAX_SPLITS",
+ * "BTL_GEMM_WIDE_MIN_TILES", "BTL_WAIT_SPIN" (the "BTL_" prefix may be left
+ * out).  Every route gives the same bits; knobs only choose among kernels and
+ * launch shapes -- except BTL_WAIT_SPIN, the number of polls after which a
+ * kernel's internal wait gives up (2^22 by default; lowering it to force that
+ * path is for tests: btl_check_faults then reports it).
+ * Unknown names: BTL_ERR_ARG.  Process-wide; not ordered with calls already
+ * issued on other threads.
+ */
+int btl_set_tuning(const char* name, int value);
+int btl_get_tuning(const char* name, int* value);
+
+/*
+ * Synchronise `stream`, then read and clear the current device's fault word:
+ * bits set by kernels whose bounded internal waits gave up (a wave of the
+ * one-token decode kernel waiting for its workgroup's quantised token row, a
+ * stage of the decode stream waiting for its input).  Such a launch has
+ * finished but its outputs are not valid.  Returns BTL_ERR_FAULT with a
+ * message naming the waits when any bit was set, else BTL_OK.  No reference
+ * counterpart (the reference's kernels do not wait on each other).
+ */
+int btl_check_faults(void* stream);
 
 /* Number of packed bytes for an [n, k] weight: ceil(n*k/4) (packing.rs:36,71). */
 int64_t btl_packed_bytes(int64_t n, int64_t k);

@@ -10,12 +10,15 @@
  * Restated from (paths inside imonoonoko/Bit-TTT-Engine, crate crates/rust_engine):
  *
  *   orc_rope_table   src/layers/attention.rs:15-42 (RotaryEmbedding::new):
- *                    inv_freq in f64 rounded to f32, freq = (f32)p * inv_freq,
+ *                    inv_freq = 1.0f / (f32)theta^(2i/hd) (the f64 power rounded
+ *                    to f32, then an f32 division: `as` binds before `/` at :19),
+ *                    freq = (f32)p * inv_freq,
  *                    cos / sin in f32 (cosf / sinf, the libm Rust's f32::cos
  *                    calls on Linux)
  *   orc_rope_apply   src/layers/attention.rs:46-87 (RotaryEmbedding::apply):
  *                    [x1*cos - x2*sin, x1*sin + x2*cos], every op rounded
- *   orc_q8_quant     src/layers/kv_cache.rs:95-119 (quantize_q8): s = max|x|/127,
+ *   orc_q8_quant     src/layers/kv_cache.rs:95-119 (quantize_q8): s = max|x| *
+ *                    (f32)(1/127) + 0 (candle's Tensor / f64 is an affine multiply),
  *                    code = u8(round(x / s) + 128) with Rust's saturating
  *                    `as u8` (NaN -> 0)
  *   orc_q8_dequant   src/layers/kv_cache.rs:122-128 (dequantize_q8):
@@ -54,7 +57,12 @@ void orc_rope_table(double theta, int64_t hd, int64_t max_seq, float* cos_t, flo
 {
     const int64_t half = hd / 2;
     float* inv = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
-    for (int64_t i = 0; i < half; ++i) inv[i] = (float)(1.0 / pow(theta, (double)(2 * i) / (double)hd));
+    /* attention.rs:19: `1.0 / (theta.powf(..)) as f32` rounds the power to f32 first,
+     * then divides in f32 */
+    for (int64_t i = 0; i < half; ++i) {
+        const float pw = (float)pow(theta, (double)(2 * i) / (double)hd);
+        inv[i] = 1.0f / pw;
+    }
     for (int64_t p = 0; p < max_seq; ++p)
         for (int64_t i = 0; i < half; ++i) {
             const float f = (float)p * inv[i];
@@ -90,7 +98,9 @@ void orc_q8_quant(const float* x, int64_t hd, uint8_t* q, float* s_out)
         const float a = fabsf(x[d]);
         if (a > amax) amax = a;
     }
-    const float s = amax / 127.0f;
+    /* kv_cache.rs:101 `max_val / 127.0` is candle's Tensor / f64 = affine(1/127, 0):
+     * x * (f32)(1/127) + 0 -- a multiply by the rounded reciprocal, not a division */
+    const float s = amax * (float)(1.0 / 127.0) + 0.0f;
     for (int64_t d = 0; d < hd; ++d) q[d] = sat_u8(roundf(x[d] / s) + 128.0f);
     *s_out = s;
 }

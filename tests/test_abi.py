@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -67,6 +68,47 @@ def test_unpack_host_matches_oracle():
     out = np.zeros(1023, np.float32)
     bl.check(bl.lib.btl_unpack_host(data.ctypes.data, 3, 341, ctypes.c_float(0.37), out.ctypes.data))
     assert np.array_equal(out, orc.unpack(data, 1023, np.float32(0.37)))
+
+
+def test_rope_table_host_matches_oracle():
+    # btl_rope_table is host code: the same table as the oracle, bit for bit, at the Llama-3
+    # theta over cfg5's positions (attention.rs:15-42)
+    S, hd = 769, 128
+    c = np.zeros((S, hd // 2), np.float32)
+    s = np.zeros_like(c)
+    bl.check(bl.lib.btl_rope_table(500000.0, hd, S, c.ctypes.data, s.ctypes.data))
+    oc, osn = orc.rope_table(500000.0, hd, S)
+    assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), osn.view(np.uint32))
+
+
+def test_tuning_knobs_set_get_and_unknown():
+    old = bl.get_tuning("BTL_GEMV_BAT_MAX_M")
+    try:
+        assert bl.set_tuning("GEMV_BAT_MAX_M", 7) == old  # the prefix may be left out
+        assert bl.get_tuning("BTL_GEMV_BAT_MAX_M") == 7
+        with bl.tuning(BTL_GEMV_BAT_MAX_M=3, BTL_DEC_RQ=0):
+            assert bl.get_tuning("BTL_GEMV_BAT_MAX_M") == 3 and bl.get_tuning("BTL_DEC_RQ") == 0
+        assert bl.get_tuning("BTL_GEMV_BAT_MAX_M") == 7
+    finally:
+        bl.set_tuning("BTL_GEMV_BAT_MAX_M", old)
+    v = ctypes.c_int()
+    assert bl.lib.btl_get_tuning(b"BTL_NO_SUCH_KNOB", ctypes.byref(v)) == bl.BTL_ERR_ARG
+    assert b"unknown tuning knob" in bl.lib.btl_last_error()
+    assert bl.lib.btl_set_tuning(None, 1) == bl.BTL_ERR_ARG
+
+
+def test_tuning_reads_the_environment_once():
+    # the environment at the first library call sets a knob; later changes to the
+    # process environment do not re-route calls
+    code = ("import os, bitlinear as bl; a = bl.get_tuning('BTL_GEMV_BAT_MAX_M'); "
+            "os.environ['BTL_GEMV_BAT_MAX_M'] = '5'; b = bl.get_tuning('BTL_GEMV_BAT_MAX_M'); "
+            "c = bl.get_tuning('BTL_DEC_ROW_MIN_K'); print(a, b, c)")
+    path = os.pathsep.join([ROOT, os.path.join(ROOT, "bit-ttt-engine_amd")])
+    env = dict(os.environ, BTL_GEMV_BAT_MAX_M="9", PYTHONPATH=path)
+    env.pop("BTL_DEC_ROW_MIN_K", None)
+    out = subprocess.run([sys.executable, "-c", code], env=env, stdout=subprocess.PIPE, text=True, check=True).stdout
+    assert out.split() == ["9", "9", "4096"]
 
 
 def test_workspace_bytes():

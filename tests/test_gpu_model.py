@@ -299,7 +299,7 @@ def test_add_rmsnorm_linear_group(m, k, ns, inplace):
                                         (1, 4096, 1000, "0"), (1, 14336, 300, "0"), (1, 2048, 7, "0"),
                                         (1, 1024, 300, "1"), (1, 3008, 150, "1"), (1, 2048, 4001, "1")])
 @pytest.mark.parametrize("with_delta", [False, True])
-def test_add_rmsnorm_swiglu(m, k, n, fuse, with_delta, monkeypatch):
+def test_add_rmsnorm_swiglu(m, k, n, fuse, with_delta, tune):
     # decode rows (m <= 4): the gate/up kernel writes silu(gate) * up from its epilogue.
     # One row, 1024 <= k <= 4096: without delta the RMSNorm runs in the quantising
     # waves of the row-group form's gate/up pairing (two token groups per thread,
@@ -308,7 +308,7 @@ def test_add_rmsnorm_swiglu(m, k, n, fuse, with_delta, monkeypatch):
     # the separate norm kernel (row-group pairing with ragged n: rows past the end
     # of a workgroup's span)
     print("add_rmsnorm_swiglu", m, k, n, fuse, with_delta, flush=True)
-    monkeypatch.setenv("BTL_FUSE_DEC", fuse)
+    tune("BTL_FUSE_DEC", fuse)
     rng = np.random.default_rng(m * 31 + k + n)
     h = rng.standard_normal((m, k)).astype(np.float32)
     d = rng.standard_normal((m, k)).astype(np.float32)
@@ -348,13 +348,13 @@ def test_swiglu_group_one_token_fused(k):
 @pytest.mark.parametrize("form", ["rq", "dec"])
 @pytest.mark.parametrize("kind", ["rmsnorm", "add_rmsnorm", "swiglu"])
 @pytest.mark.parametrize("k", [1024, 1088, 2048, 3008, 4096])
-def test_one_token_transforms_both_forms(k, kind, form, monkeypatch):
+def test_one_token_transforms_both_forms(k, kind, form, tune):
     # m = 1, f32, k <= 4096: the transform runs in the row-group form's
     # quantising waves (rq) or in the decode kernel's prologue (dec); both
     # must give the oracle's bits.  n = 150 leaves a partial row group.
     print("one-token transform", k, kind, form, flush=True)
     if form == "dec":
-        monkeypatch.setenv("BTL_DEC_RQ", "0")
+        tune("BTL_DEC_RQ", "0")
     rng = np.random.default_rng(k * 3 + len(kind))
     x = (rng.standard_normal((1, k)) * 2).astype(np.float32)
     x2 = rng.standard_normal((1, k)).astype(np.float32)

@@ -122,7 +122,7 @@ def test_linear_i8_special_rows():
 @pytest.mark.parametrize("k,parts", [(4096, "2"), (4096, "3"), (4096, "4"), (4096, "16"), (1024, "1"),
                                      (1024, "4"), (320, "1"), (14336, "7"), (14336, "8"), (14336, "14")])
 @pytest.mark.parametrize("m", [1, 2, 4])
-def test_decode_k_parts_are_exact(parts, k, m, monkeypatch):
+def test_decode_k_parts_are_exact(parts, k, m, tune):
     # a decode workgroup: 4 / parts row blocks (when parts divides 4), each
     # split into `parts` K parts summed through LDS; n = 330 leaves a partial
     # row block and a workgroup with row blocks past the end.  Shapes whose
@@ -132,10 +132,10 @@ def test_decode_k_parts_are_exact(parts, k, m, monkeypatch):
     n = 330
     x = activations(m, k, seed=11)
     pt, wb, sw = make_layer(n, k, seed=12)
-    monkeypatch.setenv("BTL_GEMV_DEC_PARTS", parts)
-    monkeypatch.setenv("BTL_DEC_ROW", "0")
-    monkeypatch.setenv("BTL_DEC_RQ", "0")
-    monkeypatch.setenv("BTL_GEMV_DEC_MAX_M", "4")
+    tune("BTL_GEMV_DEC_PARTS", parts)
+    tune("BTL_DEC_ROW", "0")
+    tune("BTL_DEC_RQ", "0")
+    tune("BTL_GEMV_DEC_MAX_M", "4")
     acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(x, wb, n, sw)
@@ -158,24 +158,24 @@ ROW_CASES = [(4096, None, None), (4096, "8", None), (4096, "16", None), (4096, N
 
 @pytest.mark.parametrize("k,rpw,rb", ROW_CASES)
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
-def test_decode_row_form_exact(k, rpw, rb, xdt, monkeypatch):
+def test_decode_row_form_exact(k, rpw, rb, xdt, tune):
     print("row form", k, rpw, rb, xdt, flush=True)
     n = 330
     x = activations(1, k, seed=k + 5)
     pt, wb, sw = make_layer(n, k, seed=k + 6)
     xt = to_dev(x, xdt)
-    monkeypatch.setenv("BTL_DEC_RQ", "0")
-    monkeypatch.setenv("BTL_DEC_ROW_MIN_K", "2048")
+    tune("BTL_DEC_RQ", "0")
+    tune("BTL_DEC_ROW_MIN_K", "2048")
     if rpw:
-        monkeypatch.setenv("BTL_DEC_ROW_RPW", rpw)
+        tune("BTL_DEC_ROW_RPW", rpw)
     if rb:
-        monkeypatch.setenv("BTL_DEC_ROW_RB", rb)
+        tune("BTL_DEC_ROW_RB", rb)
     acc = torch.empty((1, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
     assert np.array_equal(acc.cpu().numpy(), accr)
     assert_f32_identical(y, yr)
-    monkeypatch.setenv("BTL_DEC_ROW", "0")
+    tune("BTL_DEC_ROW", "0")
     acc2 = torch.empty((1, n), dtype=torch.int32, device=DEV)
     y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
     assert torch.equal(acc, acc2) and torch.equal(y, y2)
@@ -183,11 +183,11 @@ def test_decode_row_form_exact(k, rpw, rb, xdt, monkeypatch):
 
 @pytest.mark.parametrize("form", ["rq", "row"])
 @pytest.mark.parametrize("case", ["zero", "inf", "nan", "tiny", "outliers"])
-def test_decode_row_form_special_rows(case, form, monkeypatch):
+def test_decode_row_form_special_rows(case, form, tune):
     # the one-token quantiser's special rows through the row-group form and
     # the row-contiguous form
     if form == "row":
-        monkeypatch.setenv("BTL_DEC_RQ", "0")
+        tune("BTL_DEC_RQ", "0")
     k, n = 4096, 96
     x = activations(1, k, seed=21)
     if case == "zero":
@@ -210,10 +210,10 @@ def test_decode_row_form_special_rows(case, form, monkeypatch):
 
 @pytest.mark.parametrize("form", ["rq", "row"])
 @pytest.mark.parametrize("k", [4096, 14336])
-def test_decode_row_form_group_of_ragged_layers(k, form, monkeypatch):
+def test_decode_row_form_group_of_ragged_layers(k, form, tune):
     # three layers of one launch whose row counts are not multiples of 16
     if form == "row":
-        monkeypatch.setenv("BTL_DEC_RQ", "0")
+        tune("BTL_DEC_RQ", "0")
     x = activations(1, k, seed=31)
     ns = (100, 37, 250)
     layers = [make_layer(n, k, seed=32 + n) for n in ns]
@@ -242,7 +242,7 @@ RQ_CASES = [(4096, None), (4096, "1"), (4096, "5"), (4096, "14"), (1024, None), 
 @pytest.mark.parametrize("dg", ["auto", "2"])
 @pytest.mark.parametrize("k,wpc", RQ_CASES)
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
-def test_decode_row_group_form_exact(k, wpc, xdt, dg, monkeypatch):
+def test_decode_row_group_form_exact(k, wpc, xdt, dg, tune):
     # dg "2": two token groups per quantising thread even where the launch
     # would take one (k <= 4096 and room in the workgroup)
     print("row-group form", k, wpc, xdt, dg, flush=True)
@@ -250,11 +250,11 @@ def test_decode_row_group_form_exact(k, wpc, xdt, dg, monkeypatch):
     x = activations(1, k, seed=k + 7)
     pt, wb, sw = make_layer(n, k, seed=k + 8)
     xt = to_dev(x, xdt)
-    monkeypatch.setenv("BTL_DEC_RQ_MIN_K", "64")
+    tune("BTL_DEC_RQ_MIN_K", "64")
     if dg == "2":
-        monkeypatch.setenv("BTL_DEC_RQ_DG", "2")
+        tune("BTL_DEC_RQ_DG", "2")
     if wpc:
-        monkeypatch.setenv("BTL_DEC_RQ_WPC", wpc)
+        tune("BTL_DEC_RQ_WPC", wpc)
     acc = torch.empty((1, n), dtype=torch.int32, device=DEV)
     y = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc)
     yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
@@ -262,8 +262,8 @@ def test_decode_row_group_form_exact(k, wpc, xdt, dg, monkeypatch):
     assert_f32_identical(y, yr)
     yb = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.bfloat16)
     assert_bf16_matches(yb, yr)
-    monkeypatch.setenv("BTL_DEC_RQ", "0")
-    monkeypatch.setenv("BTL_DEC_ROW", "0")
+    tune("BTL_DEC_RQ", "0")
+    tune("BTL_DEC_ROW", "0")
     acc2 = torch.empty((1, n), dtype=torch.int32, device=DEV)
     y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
     assert torch.equal(acc, acc2) and torch.equal(y, y2)
@@ -276,7 +276,7 @@ def test_decode_row_group_form_exact(k, wpc, xdt, dg, monkeypatch):
 @pytest.mark.parametrize("m", [2, 3, 4])
 @pytest.mark.parametrize("k", [1024, 1088, 2048, 3072, 4096])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
-def test_decode_row_group_form_token_rows(m, k, xdt, monkeypatch):
+def test_decode_row_group_form_token_rows(m, k, xdt, tune):
     print("row-group form, token rows", m, k, xdt, flush=True)
     n = 330
     x = activations(m, k, seed=m * 100 + k)
@@ -294,15 +294,15 @@ def test_decode_row_group_form_token_rows(m, k, xdt, monkeypatch):
     acc1 = torch.empty_like(acc)
     y1 = bl.linear_i8(q, s, pt, acc_out=acc1)
     assert torch.equal(acc, acc1) and torch.equal(y, y1)
-    monkeypatch.setenv("BTL_DEC_RQ", "0")
-    monkeypatch.setenv("BTL_GEMV_DEC_MAX_M", "4")
+    tune("BTL_DEC_RQ", "0")
+    tune("BTL_GEMV_DEC_MAX_M", "4")
     acc2 = torch.empty_like(acc)
     y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
     assert torch.equal(acc, acc2) and torch.equal(y, y2)
 
 
 @pytest.mark.parametrize("k", [4096, 14336])
-def test_decode_row_group_form_prequantized(k, monkeypatch):
+def test_decode_row_group_form_prequantized(k, tune):
     # int8 inputs through the row-group form: natural order (btl_linear_i8)
     # and operand order (an RMSNorm group whose transform runs as its own
     # launch), against the fused quantisation, the GEMM on the same operand-
@@ -312,7 +312,7 @@ def test_decode_row_group_form_prequantized(k, monkeypatch):
     xf = to_dev(activations(1, k, seed=k + 11), torch.float32)
     pn, _, _ = make_layer(n, k, seed=k + 12)
     yf = bl.rmsnorm_linear_group([pn], xf, g, 1e-5, out_dtype=torch.float32)[0]
-    monkeypatch.setenv("BTL_FUSE_DEC", "0")
+    tune("BTL_FUSE_DEC", "0")
     yu = bl.rmsnorm_linear_group([pn], xf, g, 1e-5, out_dtype=torch.float32)[0]
     assert torch.equal(yf, yu)
     x = to_dev(activations(1, k, seed=k + 9), torch.bfloat16)
@@ -341,12 +341,12 @@ SPLIT_SHAPES = [(16, 14336, 256), (5, 4096, 300), (64, 1088, 1000), (2, 14336, 1
 @pytest.mark.parametrize("route", ["bat", "gemm"])
 @pytest.mark.parametrize("m,k,n", SPLIT_SHAPES)
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
-def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, monkeypatch):
+def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, tune):
     print("split-k", route, m, k, n, xdt, ydt, flush=True)
     if route == "gemm":
-        monkeypatch.setenv("BTL_GEMV_BAT", "0")
+        tune("BTL_GEMV_BAT", "0")
     else:
-        monkeypatch.setenv("BTL_GEMV_BAT_MAX_M", "64")  # the 33..64-row blocks too
+        tune("BTL_GEMV_BAT_MAX_M", "64")  # the 33..64-row blocks too
     x = activations(m, k, seed=m * 5 + k + n)
     pt, wb, sw = make_layer(n, k, seed=n * 3 + k)
     xt = to_dev(x, xdt)
@@ -582,11 +582,11 @@ WIDE_SHAPES = [(300, 1088, 257), (129, 4096, 1000), (256, 512, 512), (384, 1024,
 @pytest.mark.parametrize("tile", ["wide", "narrow"])
 @pytest.mark.parametrize("m,k,n", WIDE_SHAPES)
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
-def test_gemm_tile_widths_match_oracle(m, k, n, xdt, ydt, tile, monkeypatch):
+def test_gemm_tile_widths_match_oracle(m, k, n, xdt, ydt, tile, tune):
     # narrow: 128-row tiles of 2 x 2 waves (64 x 64 each)
     print("gemm tiles", m, k, n, xdt, ydt, tile, flush=True)
-    monkeypatch.setenv("BTL_GEMM_MAX_SPLITS", "1")
-    monkeypatch.setenv("BTL_GEMM_WIDE_MIN_TILES", "1" if tile == "wide" else "1000000000")
+    tune("BTL_GEMM_MAX_SPLITS", "1")
+    tune("BTL_GEMM_WIDE_MIN_TILES", "1" if tile == "wide" else "1000000000")
     x = activations(m, k, seed=m + k * 5 + n)
     x[min(7, m - 1)] = 0.0
     pt, wb, sw = make_layer(n, k, seed=n * 11 + k)
@@ -601,9 +601,9 @@ def test_gemm_tile_widths_match_oracle(m, k, n, xdt, ydt, tile, monkeypatch):
         assert_bf16_matches(y, yr)
 
 
-def test_gemm_wide_tiles_group_of_layers(monkeypatch):
-    monkeypatch.setenv("BTL_GEMM_MAX_SPLITS", "1")
-    monkeypatch.setenv("BTL_GEMM_WIDE_MIN_TILES", "1")
+def test_gemm_wide_tiles_group_of_layers(tune):
+    tune("BTL_GEMM_MAX_SPLITS", "1")
+    tune("BTL_GEMM_WIDE_MIN_TILES", "1")
     m, k, ns = 256, 1024, (300, 512, 70)
     x = activations(m, k, seed=77)
     layers = [make_layer(n, k, seed=78 + n) for n in ns]
@@ -795,6 +795,77 @@ def test_fused_with_caller_workspace_and_graph_replays():
         graph.replay()
         torch.cuda.synchronize()
         assert_f32_identical(out[0], yr)
+
+
+def test_library_workspace_growth_keeps_captured_graph_valid():
+    # a call on the library's own workspace (ws = NULL) captured in a HIP graph, then
+    # calls that need a larger library workspace: it is replaced and the old one
+    # retired (never freed), so every replay, with eager work between the replays,
+    # still gives the oracle's bits.  Growth while capturing fails cleanly.
+    print("workspace growth under capture", flush=True)
+    m, k, n = 6, 4096, 512
+    x = activations(m, k, seed=31)
+    pt, wb, sw = make_layer(n, k, seed=32)
+    xt = to_dev(x, torch.float32)
+    out = [torch.empty((m, n), dtype=torch.float32, device=DEV)]
+    bl.linear_group([pt], xt, outputs=out)
+    torch.cuda.synchronize()
+    yr, _, _, _ = orc.forward_i8(x, wb, n, sw)
+    assert_f32_identical(out[0], yr)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            bl.linear_group([pt], xt, outputs=out)
+    for i, (mb, kb, nb) in enumerate([(1024, 4096, 64), (2048, 8192, 64)]):
+        xb = activations(mb, kb, seed=40 + i)
+        pb, wbb, swb = make_layer(nb, kb, seed=50 + i)
+        yb = bl.BitLinearHip.forward(to_dev(xb, torch.float32), pb)
+        out[0].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_f32_identical(out[0], yr)
+        ybr, _, _, _ = orc.forward_i8(xb, wbb, nb, swb)
+        assert_f32_identical(yb, ybr)
+    big = torch.zeros((4096, 16384), dtype=torch.float32, device=DEV)
+    pbig, _, _ = make_layer(64, 16384, seed=60)
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(bl.BitLinearError) as ei:
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g2, stream=s):
+                bl.BitLinearHip.forward(big, pbig)
+    assert ei.value.status == bl.BTL_ERR_WORKSPACE
+    torch.cuda.synchronize()
+    bl.check_faults()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert_f32_identical(out[0], yr)
+
+
+def test_wait_that_gives_up_is_reported(tune):
+    # the one-token decode kernel's LDS waits bounded by BTL_WAIT_SPIN polls: with a
+    # bound of 0 every wait gives up at once (the kernel still finishes, its output is
+    # not valid) and btl_check_faults reports it; the default bound gives the exact
+    # result and a clean check
+    print("wait bound fault word", flush=True)
+    k, n = 4096, 1024
+    x = activations(1, k, seed=70)
+    pt, wb, sw = make_layer(n, k, seed=71)
+    xt = to_dev(x, torch.float32)
+    bl.check_faults()
+    tune("BTL_WAIT_SPIN", 0)
+    bl.BitLinearHip.forward(xt, pt)
+    with pytest.raises(bl.BitLinearError) as ei:
+        bl.check_faults()
+    assert ei.value.status == bl.BTL_ERR_FAULT
+    assert "token row" in str(ei.value)
+    bl.check_faults()  # cleared by the read
+    tune("BTL_WAIT_SPIN", 1 << 22)
+    y = bl.BitLinearHip.forward(xt, pt)
+    bl.check_faults()
+    yr, _, _, _ = orc.forward_i8(x, wb, n, sw)
+    assert_f32_identical(y, yr)
 
 
 # --- PackedTensor::pack on the device ---------------------------------------------

@@ -3,14 +3,20 @@ before the GPU decoder is checked against it.
 
 What pins each function (reference = imonoonoko/Bit-TTT-Engine, crates/rust_engine):
   orc_rope_table    float64 closed form of RotaryEmbedding::new (attention.rs:15-42):
-                    inv_freq rounded to f32 once, freq = (f32)p * inv_freq exactly, cos/sin
+                    inv_freq = 1.0f / (f32)theta^(2i/hd) (attention.rs:19: the cast binds
+                    before the division, so the power is rounded to f32 and the reciprocal
+                    is an f32 division; the reading that rounds 1/theta^e once in f64
+                    differs at 18 of the 64 Llama-3 frequencies and is rejected below),
+                    freq = (f32)p * inv_freq exactly, cos/sin
                     within 1 ulp of the float64 values (glibc cosf/sinf, which Rust's
                     f32::cos/sin call on Linux); the Llama-3 theta 500000.
   orc_rope_apply    float64 rotation (relative 1e-6), norm preservation, position 0 is
                     the identity, the half-split pairing (i, i + hd/2) of attention.rs:67-72
                     (an interleaved (2i, 2i+1) pairing fails).
   orc_q8_quant /    kv_cache.rs:95-128 closed form: the max element -> code 255 or 1, codes
-  orc_q8_dequant    in [1, 255], |dequant - x| <= s/2, s = max|x|/127; the round-half-away
+  orc_q8_dequant    in [1, 255], |dequant - x| <= s/2, s = max|x| * (f32)(1/127) (candle's
+                    Tensor / f64 is affine(1/rhs, 0), kv_cache.rs:101; rows where the IEEE
+                    quotient max|x|/127 differs by an ulp are planted); the round-half-away
                     tie; a zero row (0/0 -> NaN -> code 0 by Rust's saturating cast,
                     dequantised to 0).
   orc_attn_decode   float64 softmax attention over the dequantised cache with the GQA map
@@ -38,12 +44,40 @@ def _ulp_diff(a, b):
     return np.abs(a - b)
 
 
+def ref_inv_freq(theta, hd):
+    """attention.rs:19 `1.0 / (theta.powf((2 * i) as f64 / head_dim as f64)) as f32`: the f64
+    power cast to f32, then 1.0f32 / that (numpy float32 division is IEEE)."""
+    return np.array([np.float32(1.0) / np.float32(theta ** ((2 * i) / hd)) for i in range(hd // 2)], np.float32)
+
+
+def _table64(inv, S):
+    freq = (np.arange(S, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    return (np.cos(freq.astype(np.float64)).astype(np.float32), np.sin(freq.astype(np.float64)).astype(np.float32))
+
+
+def test_rope_inv_freq_rounds_the_power_first():
+    # theta 500000, hd 128 (Llama-3), i = 2: fl32(1 / fl32(p)) != fl32(1 / p)
+    theta, hd, S = 500000.0, 128, 769
+    p = theta ** (4 / 128)
+    assert np.float32(1.0) / np.float32(p) != np.float32(1.0 / p)
+    wrong = np.array([np.float32(1.0 / theta ** ((2 * i) / hd)) for i in range(hd // 2)], np.float32)
+    right = ref_inv_freq(theta, hd)
+    assert (wrong != right).sum() == 18
+    c, s = orc.rope_table(theta, hd, S)
+    rc, rs = _table64(right, S)
+    wc, ws = _table64(wrong, S)
+    assert np.all(_ulp_diff(c, rc) <= 1) and np.all(_ulp_diff(s, rs) <= 1)
+    # the double-rounded reading moves the table by far more than an ulp at most positions
+    bad = (_ulp_diff(c, wc) > 1) | (_ulp_diff(s, ws) > 1)
+    assert bad.any(axis=1).sum() > S // 2
+
+
 @pytest.mark.parametrize("theta,hd", [(500000.0, 128), (10000.0, 64), (10000.0, 2)])
 def test_rope_table_closed_form(theta, hd):
     S = 300
     c, s = orc.rope_table(theta, hd, S)
     half = hd // 2
-    inv = np.array([np.float32(1.0 / theta ** (2 * i / hd)) for i in range(half)], np.float32)
+    inv = ref_inv_freq(theta, hd)
     freq = (np.arange(S, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
     assert np.all(_ulp_diff(c, np.cos(freq.astype(np.float64)).astype(np.float32)) <= 1)
     assert np.all(_ulp_diff(s, np.sin(freq.astype(np.float64)).astype(np.float32)) <= 1)
@@ -79,7 +113,7 @@ def test_q8_quant_closed_form():
     x = rng.standard_normal((50, 128)).astype(np.float32)
     q, s = orc.q8_quant(x)
     amax = np.abs(x).max(1)
-    assert np.array_equal(s, (amax / np.float32(127)).astype(np.float32))
+    assert np.array_equal(s, (amax * np.float32(1.0 / 127.0)).astype(np.float32))
     assert q.min() >= 1 and q.max() <= 255
     idx = np.abs(x).argmax(1)
     top = q[np.arange(50), idx]
@@ -90,6 +124,24 @@ def test_q8_quant_closed_form():
     r = x / s[:, None]
     exp_codes = (np.sign(r) * np.floor(np.abs(r) + 0.5) + 128).astype(np.uint8)
     assert np.array_equal(q, exp_codes)
+
+
+def test_q8_scale_is_candle_affine_multiply():
+    # kv_cache.rs:101: candle's `tensor / 127.0` multiplies by (f32)(1/127); pick row maxima
+    # where the IEEE quotient amax / 127 is one ulp away from that product
+    rng = np.random.default_rng(11)
+    cand = np.abs(rng.standard_normal(20000)).astype(np.float32) + np.float32(0.01)
+    div = (cand / np.float32(127)).astype(np.float32)
+    mul = (cand * np.float32(1.0 / 127.0)).astype(np.float32)
+    amax = cand[div != mul][:16]
+    assert amax.size == 16
+    x = rng.uniform(-1, 1, (16, 64)).astype(np.float32) * amax[:, None]
+    x[np.arange(16), rng.integers(0, 64, 16)] = amax
+    q, s = orc.q8_quant(x)
+    assert np.array_equal(s, (amax * np.float32(1.0 / 127.0)).astype(np.float32))
+    assert np.all(s != (amax / np.float32(127)).astype(np.float32))
+    r = x / s[:, None]
+    assert np.array_equal(q, (np.sign(r) * np.floor(np.abs(r) + 0.5) + 128).astype(np.uint8))
 
 
 def test_q8_quant_tie_and_zero_row():
