@@ -30,7 +30,7 @@ EXPORTS = (
     "btl_version", "btl_last_error", "btl_status_string", "btl_init", "btl_set_tuning", "btl_get_tuning",
     "btl_check_faults", "btl_packed_bytes",
     "btl_pack_host", "btl_unpack_host", "btl_pack_device", "btl_pack_workspace_bytes", "btl_unpack_device",
-    "btl_quantize_act", "btl_linear",
+    "btl_quantize_act", "btl_linear", "btl_linear_noalloc",
     "btl_linear_i8", "btl_linear_group", "btl_quantize_act_op", "btl_linear_i8_op",
     "btl_rmsnorm_linear_group", "btl_swiglu_linear_group",
     "btl_workspace_bytes", "btl_workspace_clear",
@@ -86,6 +86,7 @@ def _load():
         "btl_pack_workspace_bytes": (sz, [i64, i64]),
         "btl_quantize_act": (i32, [vp, i32, i64, i64, vp, vp, vp]),
         "btl_linear": (i32, [P(BtlPacked), vp, i32, i64, i64, vp, i32, i32, vp, vp, sz, vp]),
+        "btl_linear_noalloc": (i32, [P(BtlPacked), vp, i32, i64, i64, vp, i32, i32, vp, vp]),
         "btl_linear_i8": (i32, [P(BtlPacked), vp, vp, i64, i64, vp, i32, vp, vp, sz, vp]),
         "btl_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, i32, i64, i64, i32, vp, sz, vp]),
         "btl_quantize_act_op": (i32, [vp, i32, i64, i64, vp, vp, vp]),

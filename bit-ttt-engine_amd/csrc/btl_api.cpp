@@ -669,7 +669,13 @@ int btl_init(int device)
     hipError_t e = hipGetDeviceCount(&count);
     if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
     if (device < 0 || device >= count) return fail(BTL_ERR_DEVICE, "device %d not present (%d devices)", device, count);
-    return probe_device(device);
+    int rc = probe_device(device);
+    if (rc) return rc;
+    // the device address of btl_linear_noalloc's scratch array, taken once per device
+    void* scratch = nullptr;
+    e = btl::scratch_address(device, &scratch);
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress (scratch)");
+    return BTL_OK;
 }
 
 int64_t btl_packed_bytes(int64_t n, int64_t k)
@@ -806,6 +812,30 @@ int btl_linear(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int6
     }
     Layer l = {w, y, acc_out};
     return run_i8(&l, 1, x, xk, nullptr, m, k, yk, ws, ws_bytes, st);
+}
+
+int btl_linear_noalloc(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int64_t k, void* y,
+                       int ydtype, int mode, int32_t* acc_out, void* stream)
+{
+    int rc = check_packed(w, m, k);
+    if (rc) return rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_dtype(ydtype, "output"))) return rc;
+    if (mode == BTL_ACT_I8 && m > 0 && w->n > 0) {
+        const size_t need = btl_workspace_bytes(m, w->n, k, BTL_ACT_I8);
+        if (need > btl::kScratchBytes)
+            return fail(BTL_ERR_WORKSPACE,
+                        "btl_linear_noalloc: [%lld, %lld] x [%lld, %lld] needs %zu bytes of scratch; its fixed "
+                        "device array holds %zu (use btl_linear with a workspace)",
+                        (long long)m, (long long)k, (long long)w->n, (long long)k, need, btl::kScratchBytes);
+        int dev;
+        if ((rc = current_device(&dev))) return rc;
+        void* scratch = nullptr;
+        const hipError_t e = btl::scratch_address(dev, &scratch);
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress (scratch)");
+        return btl_linear(w, x, xdtype, m, k, y, ydtype, mode, acc_out, scratch, btl::kScratchBytes, stream);
+    }
+    // the reference-order mode and empty calls use no scratch
+    return btl_linear(w, x, xdtype, m, k, y, ydtype, mode, acc_out, nullptr, 0, stream);
 }
 
 int btl_linear_i8(const btl_packed_t* w, const int8_t* xq, const float* xscale, int64_t m, int64_t k,

@@ -45,6 +45,12 @@ constexpr uint32_t kFaultStream = 2u;  // the decode stream: a stage's wait for 
 // the fault bits of every kernel source, read after the stream's work, then cleared
 hipError_t read_clear_faults(uint32_t* bits, hipStream_t st);
 
+// btl_linear_noalloc: its scratch is a static device array of this many bytes
+// (btl_noalloc.hip); scratch_address gives its device address on `dev`, taken
+// once per device with hipGetSymbolAddress.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+hipError_t scratch_address(int dev, void** out);
+
 constexpr int kMaxGroup = 4;       // layers per grouped launch (q|k|v, w1|w3)
 constexpr int kStepWeights = 256;  // weights of one row consumed per wave-load (64 B)
 

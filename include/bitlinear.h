@@ -191,6 +191,22 @@ int btl_linear(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int6
                int ydtype, int mode, int32_t* acc_out, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * btl_linear without a workspace and without any allocation: no counterpart in
+ * the reference.  For callers that cannot allocate device memory -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  The
+ * scratch of BTL_ACT_I8 (quantised activations, split-K partial sums) lives in a
+ * static device array of 32 MiB per device (held until the process ends; its
+ * address is taken in btl_init or at the first call on a device); a shape whose
+ * btl_workspace_bytes(m, n, k, BTL_ACT_I8) exceeds it fails with
+ * BTL_ERR_WORKSPACE before any device work.  Results are those of btl_linear,
+ * bit for bit.  Every call on one device shares that array and the kernels do
+ * not need it cleared; calls that overlap on one device (different streams or
+ * threads) race on it and must be ordered by the caller.
+ */
+int btl_linear_noalloc(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int64_t k, void* y,
+                       int ydtype, int mode, int32_t* acc_out, void* stream);
+
+/*
  * Same contraction for pre-quantised activations (as produced by
  * btl_quantize_act, or fused into a producer kernel): xq [m, k] int8,
  * xscale [m] f32.  y = (float)acc * (xscale[row] * w->scale).
