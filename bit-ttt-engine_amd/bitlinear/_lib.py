@@ -40,6 +40,7 @@ EXPORTS = (
     "btl_rope_append_attention",
     "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm_linear_group", "btl_add_rmsnorm_swiglu",
     "btl_add_rmsnorm_swiglu_workspace_bytes", "btl_linear_residual",
+    "btl_stream_create", "btl_stream_stage_words", "btl_stream_run", "btl_stream_destroy",
 )
 
 
@@ -54,6 +55,11 @@ class BtlKvQ8(ctypes.Structure):
     _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("k_scale", ctypes.c_void_p),
                 ("v_scale", ctypes.c_void_p), ("n_kv_heads", ctypes.c_int64), ("max_seq", ctypes.c_int64),
                 ("head_dim", ctypes.c_int64)]
+
+
+class BtlStreamLayer(ctypes.Structure):
+    """btl_stream_layer_t: the seven packed projections of one decoder layer."""
+    _fields_ = [(nm, BtlPacked) for nm in ("q", "k", "v", "o", "gate", "up", "down")]
 
 
 class BitLinearError(RuntimeError):
@@ -112,6 +118,10 @@ def _load():
         "btl_add_rmsnorm_swiglu": (i32, [P(BtlPacked), P(BtlPacked), vp, vp, vp, vp, f32, i64, i64, vp, vp, sz, vp]),
         "btl_add_rmsnorm_swiglu_workspace_bytes": (sz, [i64, i64, i64]),
         "btl_linear_residual": (i32, [P(BtlPacked), vp, i32, i64, i64, vp, vp, vp, sz, vp]),
+        "btl_stream_create": (i32, [P(BtlStreamLayer), i32, P(vp)]),
+        "btl_stream_stage_words": (sz, [vp]),
+        "btl_stream_run": (i32, [vp, vp, vp, vp, vp]),
+        "btl_stream_destroy": (i32, [vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -32,8 +32,8 @@ HIP_FLAGS = [
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
              "-I" + os.path.join(ROCM, "include")]
 
-KERNEL_SOURCES = ["btl_kernels.hip", "btl_model.hip", "btl_noalloc.hip"]
-HOST_SOURCES = ["btl_api.cpp", "btl_model_api.cpp"]
+KERNEL_SOURCES = ["btl_kernels.hip", "btl_model.hip", "btl_noalloc.hip", "btl_stream.hip"]
+HOST_SOURCES = ["btl_api.cpp", "btl_model_api.cpp", "btl_stream_api.cpp"]
 
 
 def _run(cmd, verbose):

@@ -282,6 +282,30 @@ hipError_t launch_adaptive_reconstruct(const uint8_t* packed, int64_t n, int64_t
                                        float* out, hipStream_t st);
 hipError_t launch_base_sum(const AdaptiveSum& a, hipStream_t st);
 
+// The decode stream (btl_stream.hip): the one-token projections of nl layers
+// (q|k|v, o, gate|up with SwiGLU, down) in one persistent launch of nwg
+// workgroups (one per CU, all resident), bf16 between the stages.
+struct StreamLayer {
+    const uint8_t* w[7];  // packed q, k, v, o, gate, up, down
+    float sw[7];
+};
+struct StreamArgs {
+    const StreamLayer* layers;  // [nl], device
+    int nl, H, I, nq, nk, nv;   // nq == H; every n a multiple of 4
+    int nwg, kmax;              // workgroups; max(H, I)
+    const uint16_t* x0;         // bf16 [H] input of layer 0
+    uint16_t* y;                // bf16 [H] output of the last layer
+    uint32_t* tbuf;             // tagged transport words, nl * (nq + nk + nv + 2 H + I)
+    uint64_t* flags;            // [8][nwg] stage flags (sequence | absmax << 32)
+    uint32_t* epoch;            // launch epoch (device; starts at 1)
+    uint16_t* dbg;              // optional plain bf16 copies of every stage output (tbuf layout)
+    int64_t budget_ticks;       // time budget of the waits (s_memrealtime ticks, 100 MHz)
+};
+size_t stream_lds_bytes(int kmax);
+hipError_t launch_dec_stream(const StreamArgs& a, hipStream_t s);
+// kFaultStream bits of the stream kernel, read then cleared
+hipError_t stream_faults(uint32_t* bits, hipStream_t st);
+
 hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
                         float* out, hipStream_t st);
 hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,

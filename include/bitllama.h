@@ -171,6 +171,44 @@ int btl_add_rmsnorm_swiglu(const btl_packed_t* w_gate, const btl_packed_t* w_up,
                            float* out, void* ws, size_t ws_bytes, void* stream);
 size_t btl_add_rmsnorm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
+/*
+ * The decode stream: the one-token projections of every layer of a Llama block
+ * stack in ONE persistent launch.  No single reference counterpart: it replaces
+ * the sequence of BitLinear::forward calls (layers/bit_linear.rs:52-119) that
+ * one decoder step issues per layer in dependency order -- q|k|v
+ * (attention.rs:159-162), o_proj, w1|w3 and w2 (swiglu.rs:29-35) from
+ * BitLlamaBlock::forward (model/block.rs:90-138) -- with the launch boundaries
+ * between them replaced by a device-side handoff.  Per layer l:
+ *   [q|k|v] = W1.58-A8(q, k, v; x_l);  o = W1.58-A8(o; q);
+ *   h = silu(W1.58-A8(gate; o)) * W1.58-A8(up; o);  x_{l+1} = W1.58-A8(down; h)
+ * every output rounded to bf16; each contraction bit-identical to btl_linear
+ * on the bf16 input, silu as btl_add_rmsnorm_swiglu.  (Attention, norms and
+ * residual adds are not part of this chain: it is the decoder's projection
+ * chain, what a one-token step streams from HBM.)
+ *
+ * btl_stream_create: checks the shapes (q: [H, H], k/v: [nk/nv, H], o: [H, H],
+ *   gate/up: [I, H], down: [H, I]; H a multiple of 64 up to 4096, I a multiple
+ *   of 64 up to 14336, every layer alike, packed data 16-byte aligned; at most
+ *   6 / 4 / 14 / 8 row groups of q|k|v / o / gate|up / down per CU) and
+ *   allocates the plan's device buffers (layer table, handoff words, flags).
+ * btl_stream_run: x bf16 [H] (device, 16-byte aligned) -> y bf16 [H]; stage_out
+ *   NULL, or a bf16 buffer of btl_stream_stage_words(plan) elements that
+ *   receives every stage's output (per layer: [q|k|v], o, h, down).  The launch
+ *   takes every CU (one workgroup each, all resident): nothing else may run on
+ *   the device meanwhile.  Its waits are bounded in time (BTL_WAIT_SPIN); a
+ *   wait that gives up is reported by btl_check_faults.  Runs on one plan must
+ *   be ordered on one stream.
+ * btl_stream_destroy: synchronises the device and frees the plan.
+ */
+typedef struct btl_stream_layer {
+    btl_packed_t q, k, v, o, gate, up, down;
+} btl_stream_layer_t;
+
+int btl_stream_create(const btl_stream_layer_t* layers, int n_layers, void** plan);
+size_t btl_stream_stage_words(const void* plan);
+int btl_stream_run(void* plan, const void* x, void* y, void* stage_out, void* stream);
+int btl_stream_destroy(void* plan);
+
 #ifdef __cplusplus
 }
 #endif

@@ -111,6 +111,28 @@ def test_tuning_reads_the_environment_once():
     assert out.split() == ["9", "9", "4096"]
 
 
+def test_stream_create_rejects_bad_shapes():
+    # shape checks of btl_stream_create run before any device work
+    def layer(H, I, nkv, q_rows=None):
+        L = bl.BtlStreamLayer()
+        dims = {"q": (q_rows or H, H), "k": (nkv, H), "v": (nkv, H), "o": (H, q_rows or H), "gate": (I, H),
+                "up": (I, H), "down": (H, I)}
+        for nm, (n, k) in dims.items():
+            setattr(L, nm, bl.BtlPacked(256, n, k, 1.0))
+        return L
+    h = ctypes.c_void_p()
+    for L, frag in ((layer(4160, 512, 64), b"hidden"), (layer(256, 520, 64), b"intermediate"),
+                    (layer(256, 512, 64, q_rows=512), b"o reads q"), (layer(256, 16384, 64), b"intermediate")):
+        arr = (bl.BtlStreamLayer * 1)(L)
+        assert bl.lib.btl_stream_create(arr, 1, ctypes.byref(h)) == bl.BTL_ERR_SHAPE
+        assert frag in bl.lib.btl_last_error()
+    arr = (bl.BtlStreamLayer * 2)(layer(256, 512, 64), layer(256, 1024, 64))
+    assert bl.lib.btl_stream_create(arr, 2, ctypes.byref(h)) == bl.BTL_ERR_SHAPE
+    assert bl.lib.btl_stream_create(arr, 0, ctypes.byref(h)) == bl.BTL_ERR_ARG
+    assert bl.lib.btl_stream_stage_words(None) == 0
+    assert bl.lib.btl_stream_destroy(None) == bl.BTL_OK
+
+
 def test_workspace_bytes():
     assert bl.lib.btl_workspace_bytes(1, 4096, 4096, bl.BTL_ACT_F32_REF) == 0
     a = bl.lib.btl_workspace_bytes(1, 4096, 4096, bl.BTL_ACT_I8)
