@@ -90,10 +90,7 @@ struct Clock {
     __device__ __forceinline__ bool expired()
     {
         if (abort) return true;
-        if (now_ticks() > deadline) {
-            abort = true;
-            __hip_atomic_fetch_or(&g_stream_faults, kFaultStream, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (now_ticks() > deadline) abort = true;  // reported once, when the wave ends
         return abort;
     }
 };
@@ -274,214 +271,176 @@ __device__ __forceinline__ int own_row(int lane, bool* own)
     return r;
 }
 
+constexpr int kSOut = 64;  // outputs of one stage a workgroup computes at most (gate|up: 14 x 4)
+
 struct Shared {
-    uint32_t ready;        // operand rows posted (each control wave adds 1 per stage)
-    uint32_t done[2];      // compute waves done with the stage (by parity)
-    uint32_t amax[2];      // |output| max of this workgroup's rows (by parity), f32 bits
-    float scale[2];        // s_x of the operand row (by parity)
+    uint32_t ready;            // operand rows posted (each control wave adds 1 per stage)
+    uint32_t cdone;            // compute-wave arrivals (one per participating wave per stage)
+    float scale[2];            // s_x of the operand row (by stage parity)
+    float out[kSOut];          // this workgroup's outputs of the current stage (f32, before rounding)
     uint32_t ctl_amax[kSCtl];  // first stage: the control waves' absmax of x0
     uint32_t ctl_arrive;
-    uint32_t ctl_copy;     // control waves whose input copies are in LDS (one per wave per stage)
+    uint32_t ctl_copy;         // control waves whose input copies are in LDS (one per wave per stage)
 };
-
-// A compute wave's end of stage s: fold its outputs' absmax into the
-// workgroup's, count itself done; the last of the stage's waves resets the
-// parity slots and publishes the flag replicas.
-__device__ __forceinline__ void stage_done(const StreamArgs& a, Shared& sh, int s, int nparticipants, uint32_t amax,
-                                           uint32_t seq, int lane)
-{
-    const int p = s & 1;
-    const uint32_t m = wave_max_dpp(amax);
-    uint32_t old = 0;
-    if (lane == 0) {
-        __hip_atomic_fetch_max(&sh.amax[p], m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        old = __hip_atomic_fetch_add(&sh.done[p], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
-    if (old + 1u != (uint32_t)nparticipants) return;
-    uint32_t wg_amax = 0;
-    if (lane == 0) {
-        wg_amax = __hip_atomic_load(&sh.amax[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        sh.amax[p] = 0u;
-        sh.done[p] = 0u;
-    }
-    wg_amax = (uint32_t)__builtin_amdgcn_readfirstlane((int)wg_amax);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane < kSReplicas)
-        __hip_atomic_store(a.flags + (size_t)lane * a.nwg + blockIdx.x, ((uint64_t)wg_amax << 32) | seq,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 __device__ __forceinline__ uint32_t tag_of(uint32_t epoch) { return epoch & 0xFFFFu; }
 
-// store one output (bf16-rounded) as a tagged word, plain copies where asked
-__device__ __forceinline__ void put_out(const StreamArgs& a, int out_off, int n, float v, uint32_t tag, bool last)
-{
-    const uint16_t b = f32_to_bf16(v);
-    __hip_atomic_store(a.tbuf + out_off + n, ((uint32_t)b << 16) | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (a.dbg) a.dbg[out_off + n] = b;
-    if (last) a.y[n] = b;
-}
-
-// |bf16 value| as f32 bits (the absmax the next stage quantises with)
-__device__ __forceinline__ uint32_t abs_bits(float v) { return ((uint32_t)f32_to_bf16(v) << 16) & 0x7FFFFFFFu; }
-
 // A compute wave's group in one slot: which layer matrix (w index), the first
-// row in that matrix and in the stage output, rows, K.  Layer-independent.
+// row in that matrix, rows (0: none) and K.  Layer-independent.
 struct Slot {
-    int wi;      // index into StreamLayer::w / sw
-    int lrow0;   // first row in the matrix
-    int orow0;   // first row in the stage's output
-    int rows;    // 0: no group
+    int wi;
+    int lrow0;
+    int rows;
     int K;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const StreamLayer* layers, int l, const Slot& sl)
+// The layer table through the constant address space: read with scalar loads
+// (lgkmcnt).  A vector load of it (the compiler's choice for a plain pointer,
+// since the kernel also stores to global memory) would count in vmcnt, and
+// waiting for it would wait for every weight load issued before it.
+typedef const __attribute__((address_space(4))) StreamLayer* LayerTab;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(LayerTab layers, int l, const Slot& sl)
 {
+    // every field wave-uniform (readfirstlane): a descriptor in VGPRs turns each
+    // load into a waterfall loop
     const int rowb = sl.K >> 2;
-    return make_rsrc(layers[l].w[sl.wi] + (int64_t)sl.lrow0 * rowb, (uint32_t)(sl.rows * rowb));
+    const uint64_t base = (uint64_t)(layers[l].w[sl.wi] + (int64_t)sl.lrow0 * rowb);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
+    const uint32_t nb = (uint32_t)__builtin_amdgcn_readfirstlane(sl.rows * rowb);
+    return make_rsrc((const void*)(((uint64_t)hi << 32) | lo), nb);
 }
 
+// The slot's loads for layer l, issued whether or not the wave owns a group
+// (rows == 0: every offset is out of range, nothing is read): the compute
+// waves issue no other vector memory instructions, so the order of their
+// loads is the same on every path and the compiler's in-order wait counts
+// (s_waitcnt vmcnt(N) before each use) stay exact across the layer loop.
 template <int R, int ST>
-__device__ __forceinline__ void slot_issue(uint4* buf, const StreamLayer* layers, int l, const Slot& sl, int lane)
+__device__ __forceinline__ void slot_issue(uint4* buf, LayerTab layers, int l, const Slot& sl, int lane)
 {
     GroupW g;
     g.rs = slot_rsrc(layers, l, sl);
     g.rows = sl.rows;
     issue_loads<R, ST>(buf, g, sl.K, lane);
+    __builtin_amdgcn_sched_barrier(0);  // the slots' loads stay in the order they are issued
+}
+
+// a compute wave's end of stage s: its outputs are in sh.out; count it
+__device__ __forceinline__ void compute_arrive(Shared& sh, int lane)
+{
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the outputs are in LDS
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) __hip_atomic_fetch_add(&sh.cdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Compute wave c.  ROLE: 0 = QKV + O + GU (c 0..3), 1 = QKV + GU (c 4..5),
-// 2 = D + GU (c 6..13).
+// 2 = D + GU (c 6..13).  Local output index of group g in a stage: g * R + r.
 template <int ROLE, int RD, int STD>
-__device__ void compute_wave(const StreamArgs& a, Shared& sh, const uint8_t* rows_lds, int c, int lane, uint32_t epoch,
-                             Clock& clk)
+__device__ void compute_wave(const StreamArgs& a, Shared& sh, const uint8_t* rows_lds, int c, int lane, Clock& clk)
 {
     constexpr bool HQ = ROLE <= 1, HO = ROLE == 0, HD = ROLE == 2;
     const int w = blockIdx.x;
-    const uint32_t tag = tag_of(epoch);
     const int kmax_row = a.kmax + 16;
     const int H = a.H, I = a.I, nqkv = a.nq + a.nk + a.nv;
     const GroupPos pq = group_pos(nqkv / 4, a.nwg, w);
     const GroupPos po = group_pos(H / 4, a.nwg, w);
     const GroupPos pg = group_pos(I / 4, a.nwg, w);
     const GroupPos pd = group_pos(H / RD, a.nwg, w);
-    const int npq = min(pq.ng, kSQkvWaves), npo = min(po.ng, kSOWaves), npg = min(pg.ng, kSComp),
-              npd = min(pd.ng, kSComp - kSDWave0);
 
     Slot sq_, so_, sg_, sd_;
-    sq_.rows = so_.rows = sg_.rows = sd_.rows = 0;
+    sq_.wi = 0; sq_.lrow0 = 0; sq_.rows = 0; sq_.K = H;
+    so_.wi = 3; so_.lrow0 = 0; so_.rows = 0; so_.K = a.nq;
+    sg_.wi = 4; sg_.lrow0 = 0; sg_.rows = 0; sg_.K = H;
+    sd_.wi = 6; sd_.lrow0 = 0; sd_.rows = 0; sd_.K = I;
     if (HQ && c < pq.ng) {
         const int r0 = (pq.g0 + c) * 4;  // row in [q | k | v]
         const int li = r0 < a.nq ? 0 : (r0 < a.nq + a.nk ? 1 : 2);
         sq_.wi = li;
         sq_.lrow0 = li == 0 ? r0 : (li == 1 ? r0 - a.nq : r0 - a.nq - a.nk);
-        sq_.orow0 = r0;
         sq_.rows = min(4, (li == 0 ? a.nq : (li == 1 ? a.nk : a.nv)) - sq_.lrow0);
-        sq_.K = H;
     }
     if (HO && c < po.ng) {
-        so_.wi = 3;
-        so_.lrow0 = so_.orow0 = (po.g0 + c) * 4;
+        so_.lrow0 = (po.g0 + c) * 4;
         so_.rows = min(4, H - so_.lrow0);
-        so_.K = a.nq;
     }
     if (c < pg.ng) {
-        sg_.wi = 4;
-        sg_.lrow0 = sg_.orow0 = (pg.g0 + c) * 4;
+        sg_.lrow0 = (pg.g0 + c) * 4;
         sg_.rows = min(4, I - sg_.lrow0);
-        sg_.K = H;
     }
     if (HD && c - kSDWave0 < pd.ng) {
-        sd_.wi = 6;
-        sd_.lrow0 = sd_.orow0 = (pd.g0 + c - kSDWave0) * RD;
+        sd_.lrow0 = (pd.g0 + c - kSDWave0) * RD;
         sd_.rows = min(RD, H - sd_.lrow0);
-        sd_.K = I;
     }
     Slot su_ = sg_;
     su_.wi = 5;
 
     uint4 bq[HQ ? 4 : 1], bo[HO ? 4 : 1], bg[8], bd[HD ? STD : 1];
-    const StreamLayer* layers = a.layers;
-    if (HQ && sq_.rows) slot_issue<4, 4>(bq, layers, 0, sq_, lane);
-    if (HO && so_.rows) slot_issue<4, 4>(bo, layers, 0, so_, lane);
-    if (sg_.rows) {
-        slot_issue<4, 4>(bg, layers, 0, sg_, lane);
-        slot_issue<4, 4>(bg + 4, layers, 0, su_, lane);
-    }
-    if (HD && sd_.rows) slot_issue<RD, STD>(bd, layers, 0, sd_, lane);
+    const LayerTab layers = (LayerTab)a.layers;
+    // layer 0, in the slot order the loop re-issues them
+    if (HQ) slot_issue<4, 4>(bq, layers, 0, sq_, lane);
+    if (HO) slot_issue<4, 4>(bo, layers, 0, so_, lane);
+    slot_issue<4, 4>(bg, layers, 0, sg_, lane);
+    slot_issue<4, 4>(bg + 4, layers, 0, su_, lane);
+    if (HD) slot_issue<RD, STD>(bd, layers, 0, sd_, lane);
 
     bool own4, own_d;
     const int r4 = own_row<4>(lane, &own4);
     const int rdd = own_row<RD>(lane, &own_d);
 
     for (int l = 0; l < a.nl; ++l) {
-        const bool more = l + 1 < a.nl;
-        const int ob = l * (nqkv + H + I + H);  // this layer's output words
-        // ---- QKV
-        if (HQ && sq_.rows) {
+        const int ln = l + 1 < a.nl ? l + 1 : l;  // the last layer re-reads its own weights (never used)
+        if (HQ) {
             const int s = 4 * l;
-            lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
-            const int d = group_dot<4, 4>(bq, rows_lds + (s & 1) * kmax_row, H, lane);
-            uint32_t am = 0;
-            if (own4 && r4 < sq_.rows) {
-                const float y = __fmul_rn((float)d, __fmul_rn(sh.scale[s & 1], layers[l].sw[sq_.wi]));
-                put_out(a, ob, sq_.orow0 + r4, y, tag, false);
-                // the next stage (o) reads q only: k and v rows stay out of the absmax
-                am = sq_.orow0 + r4 < a.nq ? abs_bits(y) : 0u;
+            if (sq_.rows) {
+                lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
+                const int d = group_dot<4, 4>(bq, rows_lds + (s & 1) * kmax_row, H, lane);
+                if (own4 && r4 < sq_.rows)
+                    sh.out[c * 4 + r4] = __fmul_rn((float)d, __fmul_rn(sh.scale[s & 1], layers[l].sw[sq_.wi]));
+                compute_arrive(sh, lane);
             }
-            stage_done(a, sh, s, npq, am, (epoch << 10) + (uint32_t)s + 1u, lane);
-            if (more) slot_issue<4, 4>(bq, layers, l + 1, sq_, lane);
+            slot_issue<4, 4>(bq, layers, ln, sq_, lane);
         }
-        // ---- O
-        if (HO && so_.rows) {
+        if (HO) {
             const int s = 4 * l + 1;
-            lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
-            const int d = group_dot<4, 4>(bo, rows_lds + (s & 1) * kmax_row, a.nq, lane);
-            uint32_t am = 0;
-            if (own4 && r4 < so_.rows) {
-                const float y = __fmul_rn((float)d, __fmul_rn(sh.scale[s & 1], layers[l].sw[3]));
-                put_out(a, ob + nqkv, so_.orow0 + r4, y, tag, false);
-                am = abs_bits(y);
+            if (so_.rows) {
+                lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
+                const int d = group_dot<4, 4>(bo, rows_lds + (s & 1) * kmax_row, a.nq, lane);
+                if (own4 && r4 < so_.rows)
+                    sh.out[c * 4 + r4] = __fmul_rn((float)d, __fmul_rn(sh.scale[s & 1], layers[l].sw[3]));
+                compute_arrive(sh, lane);
             }
-            stage_done(a, sh, s, npo, am, (epoch << 10) + (uint32_t)s + 1u, lane);
-            if (more) slot_issue<4, 4>(bo, layers, l + 1, so_, lane);
+            slot_issue<4, 4>(bo, layers, ln, so_, lane);
         }
-        // ---- GU: silu(gate) * up
-        if (sg_.rows) {
+        {
             const int s = 4 * l + 2;
-            lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
-            const uint8_t* sq = rows_lds + (s & 1) * kmax_row;
-            int dg, du;
-            group_dot_pair(bg, bg + 4, sq, H, lane, &dg, &du);
-            uint32_t am = 0;
-            if (own4 && r4 < sg_.rows) {
-                const float sx = sh.scale[s & 1];
-                const float yg = __fmul_rn((float)dg, __fmul_rn(sx, layers[l].sw[4]));
-                const float yu = __fmul_rn((float)du, __fmul_rn(sx, layers[l].sw[5]));
-                const float hv = __fmul_rn(__fdiv_rn(yg, __fadd_rn(1.0f, btl_expf(-yg))), yu);
-                put_out(a, ob + nqkv + H, sg_.orow0 + r4, hv, tag, false);
-                am = abs_bits(hv);
+            if (sg_.rows) {
+                lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
+                int dg, du;
+                group_dot_pair(bg, bg + 4, rows_lds + (s & 1) * kmax_row, H, lane, &dg, &du);
+                if (own4 && r4 < sg_.rows) {
+                    const float sx = sh.scale[s & 1];
+                    const float yg = __fmul_rn((float)dg, __fmul_rn(sx, layers[l].sw[4]));
+                    const float yu = __fmul_rn((float)du, __fmul_rn(sx, layers[l].sw[5]));
+                    sh.out[c * 4 + r4] = __fmul_rn(__fdiv_rn(yg, __fadd_rn(1.0f, btl_expf(-yg))), yu);
+                }
+                compute_arrive(sh, lane);
             }
-            stage_done(a, sh, s, npg, am, (epoch << 10) + (uint32_t)s + 1u, lane);
-            if (more) {
-                slot_issue<4, 4>(bg, layers, l + 1, sg_, lane);
-                slot_issue<4, 4>(bg + 4, layers, l + 1, su_, lane);
-            }
+            slot_issue<4, 4>(bg, layers, ln, sg_, lane);
+            slot_issue<4, 4>(bg + 4, layers, ln, su_, lane);
         }
-        // ---- D
-        if (HD && sd_.rows) {
+        if (HD) {
             const int s = 4 * l + 3;
-            lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
-            const int d = group_dot<RD, STD>(bd, rows_lds + (s & 1) * kmax_row, I, lane);
-            uint32_t am = 0;
-            if (own_d && rdd < sd_.rows) {
-                const float y = __fmul_rn((float)d, __fmul_rn(sh.scale[s & 1], layers[l].sw[6]));
-                put_out(a, ob + nqkv + H + I, sd_.orow0 + rdd, y, tag, !more);
-                am = abs_bits(y);
+            if (sd_.rows) {
+                lds_wait(&sh.ready, 2u * (uint32_t)(s + 1), clk);
+                const int d = group_dot<RD, STD>(bd, rows_lds + (s & 1) * kmax_row, I, lane);
+                if (own_d && rdd < sd_.rows)
+                    sh.out[(c - kSDWave0) * RD + rdd] =
+                        __fmul_rn((float)d, __fmul_rn(sh.scale[s & 1], layers[l].sw[6]));
+                compute_arrive(sh, lane);
             }
-            stage_done(a, sh, s, npd, am, (epoch << 10) + (uint32_t)s + 1u, lane);
-            if (more) slot_issue<RD, STD>(bd, layers, l + 1, sd_, lane);
+            slot_issue<RD, STD>(bd, layers, ln, sd_, lane);
         }
     }
 }
@@ -495,6 +454,29 @@ __device__ __forceinline__ void quant_group_to(uint8_t* sq, int g, const float* 
     *(uint4*)(sq + 16 * g) = qp.ok ? group_quant_f(f, qp.r) : uint4{0u, 0u, 0u, 0u};
 }
 
+// Control wave 0 after the compute waves of stage s are done: the workgroup's
+// outputs (n local rows from output row o0) as tagged bf16 words, plain copies
+// where asked, then the flag replicas with the absmax of the rows the next
+// stage reads (rows below amax_rows of the stage's output).
+__device__ __forceinline__ void publish(const StreamArgs& a, Shared& sh, int out_off, int o0, int n, int amax_rows,
+                                        bool last, uint32_t epoch, uint32_t seq, int lane)
+{
+    uint32_t am = 0;
+    if (lane < n) {
+        const uint16_t b = f32_to_bf16(sh.out[lane]);
+        const int row = o0 + lane;
+        __hip_atomic_store(a.tbuf + out_off + row, ((uint32_t)b << 16) | tag_of(epoch), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        if (a.dbg) a.dbg[out_off + row] = b;
+        if (last) a.y[row] = b;
+        if (row < amax_rows) am = ((uint32_t)b << 16) & 0x7FFFFFFFu;
+    }
+    am = wave_max_dpp(am);
+    if (lane < kSReplicas)
+        __hip_atomic_store(a.flags + (size_t)lane * a.nwg + blockIdx.x, ((uint64_t)am << 32) | seq, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds, uint8_t* stage_lds, int cw, int lane,
                              uint32_t epoch, Clock& clk, int rd)
 {
@@ -505,11 +487,12 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
     const int kmax_row = a.kmax + 16;
     const int S = 4 * a.nl;
     const int rep = w % kSReplicas;
-    int nslot[4];
-    nslot[0] = min(group_pos(stage_groups(a, 0, rd), a.nwg, w).ng, kSQkvWaves);
-    nslot[1] = min(group_pos(stage_groups(a, 1, rd), a.nwg, w).ng, kSOWaves);
-    nslot[2] = min(group_pos(stage_groups(a, 2, rd), a.nwg, w).ng, kSComp);
-    nslot[3] = min(group_pos(stage_groups(a, 3, rd), a.nwg, w).ng, kSComp - kSDWave0);
+    const int nqkv = a.nq + a.nk + a.nv;
+    // this workgroup's groups per slot, their first output rows and counts
+    const GroupPos gp[4] = {group_pos(nqkv / 4, a.nwg, w), group_pos(a.H / 4, a.nwg, w),
+                            group_pos(a.I / 4, a.nwg, w), group_pos(a.H / rd, a.nwg, w)};
+    const int gr[4] = {4, 4, 4, rd};
+    uint32_t cum = 0;  // compute-wave arrivals expected through the current stage
     const __amdgpu_buffer_rsrc_t fr = make_rsrc(a.flags + (size_t)rep * a.nwg, (uint32_t)(a.nwg * 8));
     for (int s = 0; s < S; ++s) {
         const int l = s >> 2, j = s & 3;
@@ -552,8 +535,10 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
                 const uint4 f0 = ld_sc1(fr, lane * 32), f1 = ld_sc1(fr, lane * 32 + 16);
                 const int i0 = 4 * lane;
                 // sequence numbers compared modulo 2^32 (stale ones are at most a launch old)
-                bool ok = (i0 >= a.nwg || (int32_t)(f0.x - want) >= 0) && (i0 + 1 >= a.nwg || (int32_t)(f0.z - want) >= 0) &&
-                          (i0 + 2 >= a.nwg || (int32_t)(f1.x - want) >= 0) && (i0 + 3 >= a.nwg || (int32_t)(f1.z - want) >= 0);
+                const bool ok = (i0 >= a.nwg || (int32_t)(f0.x - want) >= 0) &&
+                                (i0 + 1 >= a.nwg || (int32_t)(f0.z - want) >= 0) &&
+                                (i0 + 2 >= a.nwg || (int32_t)(f1.x - want) >= 0) &&
+                                (i0 + 3 >= a.nwg || (int32_t)(f1.z - want) >= 0);
                 if (__all(ok)) {
                     uint32_t m = 0;
                     if (i0 < a.nwg) m = max(m, f0.y);
@@ -566,12 +551,13 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
                 if (clk.expired()) break;
             }
             qp = qparams(gam);
-            // 2. the tagged input into LDS: this wave's 1 KB chunks
+            // 2. the tagged input into LDS: this wave's 1 KB copies, then wait for the other's
             const __amdgpu_buffer_rsrc_t ir = make_rsrc(a.tbuf + io.in_off, (uint32_t)(K * 4));
             const int nch = (K * 4 + 1023) >> 10;
             for (int ch = cw; ch < nch; ch += kSCtl)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ir, (__attribute__((address_space(3))) void*)(stage_lds + ch * 1024),
-                                                         16, ch * 1024 + 16 * lane, 0, 0, 16);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ir, (__attribute__((address_space(3))) void*)(stage_lds + ch * 1024), 16, ch * 1024 + 16 * lane, 0,
+                    0, 16);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies are in LDS
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             if (lane == 0) __hip_atomic_fetch_add(&sh.ctl_copy, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -586,11 +572,11 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
 #pragma unroll
                 for (int e = 0; e < 16; ++e) ok = ok && (u[e] & 0xFFFFu) == tag;
                 if (!ok) {
-                    const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.tbuf + io.in_off + 16 * g, 64u);
+                    const __amdgpu_buffer_rsrc_t gr_ = make_rsrc(a.tbuf + io.in_off + 16 * g, 64u);
                     for (;;) {
                         asm volatile("" ::: "memory");
 #pragma unroll
-                        for (int h = 0; h < 4; ++h) v[h] = ld_sc1(gr, 16 * h);
+                        for (int h = 0; h < 4; ++h) v[h] = ld_sc1(gr_, 16 * h);
                         ok = true;
 #pragma unroll
                         for (int e = 0; e < 16; ++e) ok = ok && (u[e] & 0xFFFFu) == tag;
@@ -608,12 +594,17 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the row is in LDS
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         if (lane == 0) __hip_atomic_fetch_add(&sh.ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        // 5. a workgroup without rows in this stage publishes its flag itself
+        // 5. wave 0: once this stage's compute waves are done, publish the outputs
+        //    (q|k|v: the absmax of q only, the rows o reads)
+        const int cap = j == 0 ? kSQkvWaves : (j == 1 ? kSOWaves : (j == 2 ? kSComp : kSComp - kSDWave0));
+        const int np = min(gp[j].ng, cap);
+        cum += (uint32_t)np;
         if (cw == 0) {
-            const int ng = j == 0 ? nslot[0] : (j == 1 ? nslot[1] : (j == 2 ? nslot[2] : nslot[3]));
-            if (ng == 0 && lane < kSReplicas)
-                __hip_atomic_store(a.flags + (size_t)lane * a.nwg + w, (uint64_t)((epoch << 10) + (uint32_t)s + 1u),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lds_wait(&sh.cdone, cum, clk);
+            publish(a, sh, io.out_off, gp[j].g0 * gr[j], np * gr[j] < io.n_out - gp[j].g0 * gr[j]
+                                                               ? np * gr[j]
+                                                               : io.n_out - gp[j].g0 * gr[j],
+                    j == 0 ? a.nq : io.n_out, j == 3 && l + 1 == a.nl, epoch, (epoch << 10) + (uint32_t)s + 1u, lane);
         }
     }
 }
@@ -621,14 +612,13 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
 template <int RD, int STD>
 __global__ __launch_bounds__(1024, 1) void k_dec_stream(StreamArgs a)
 {
-    extern __shared__ __align__(16) uint8_t lds[];  // [2][kmax + 16] operand rows, then [kmax * 4] staging
+    extern __shared__ __align__(16) uint8_t lds[];  // [2][kmax + 16] operand rows, then the staging copy
     __shared__ Shared sh;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (tid == 0) {
         sh.ready = 0u;
-        sh.done[0] = sh.done[1] = 0u;
-        sh.amax[0] = sh.amax[1] = 0u;
+        sh.cdone = 0u;
         sh.ctl_arrive = 0u;
         sh.ctl_copy = 0u;
     }
@@ -640,18 +630,18 @@ __global__ __launch_bounds__(1024, 1) void k_dec_stream(StreamArgs a)
     uint8_t* stage_lds = lds + 2 * (a.kmax + 16);
     if (wave < kSCtl) {
         control_wave(a, sh, rows_lds, stage_lds, wave, lane, epoch, clk, RD);
-        // workgroup 0 ends the launch's epoch after its last stage
-        if (blockIdx.x == 0 && wave == 0 && lane == 0) {
-            // every compute wave of this workgroup has read the epoch (they
-            // read it before the barrier above)
+        // workgroup 0 ends the launch's epoch after its last stage (every
+        // workgroup read the epoch before producing the outputs it consumed)
+        if (blockIdx.x == 0 && wave == 0 && lane == 0)
             __hip_atomic_store(a.epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        return;
+    } else {
+        const int c = wave - kSCtl;
+        if (c < kSOWaves) compute_wave<0, RD, STD>(a, sh, rows_lds, c, lane, clk);
+        else if (c < kSQkvWaves) compute_wave<1, RD, STD>(a, sh, rows_lds, c, lane, clk);
+        else compute_wave<2, RD, STD>(a, sh, rows_lds, c, lane, clk);
     }
-    const int c = wave - kSCtl;
-    if (c < kSOWaves) compute_wave<0, RD, STD>(a, sh, rows_lds, c, lane, epoch, clk);
-    else if (c < kSQkvWaves) compute_wave<1, RD, STD>(a, sh, rows_lds, c, lane, epoch, clk);
-    else compute_wave<2, RD, STD>(a, sh, rows_lds, c, lane, epoch, clk);
+    if (clk.abort && lane == 0)
+        __hip_atomic_fetch_or(&g_stream_faults, kFaultStream, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
