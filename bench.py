@@ -485,10 +485,10 @@ def run_e2e(layers, gen, dev, args):
             "decode_tok_s": round(1000.0 / dec_ms, 1), "decode_ms_per_token": round(dec_ms, 4),
             "decode_bytes_per_token": int(step_bytes),
             "decode_frac_hbm": round(step_bytes / dec_ms / 1e6 / HBM_PEAK_GBS, 3),
-            # embedding; per layer q|k|v (norm in the quantising waves), attention, chunk
-            # merge, o (+ residual), gate|up (norm; SwiGLU epilogue), down (+ residual);
-            # final norm, lm_head, pick
-            "launches_per_token": 1 + LAYERS * 6 + 3,
+            # embedding; per layer q|k|v (norm in the quantising waves), attention (RoPE,
+            # append, chunks and their merge), o (+ residual), gate|up (norm; SwiGLU
+            # epilogue), down (+ residual); final norm, lm_head, pick
+            "launches_per_token": 1 + LAYERS * 5 + 3,
             "first_tokens": [int(t) for t in toks[:8]]}
 
 

@@ -101,7 +101,7 @@ constexpr KnobDef kKnobs[btl::KN_COUNT] = {
     {"BTL_GEMV_BAT", 1},       {"BTL_FUSE_MAX_WG", 512},  {"BTL_FUSE_DEC", 1},
     {"BTL_DEC_RQ_MIN_K", 1024}, {"BTL_DEC_RQ", 1},        {"BTL_DEC_RQ_DG", 0},
     {"BTL_GEMM_MAX_SPLITS", 0}, {"BTL_GEMM_WIDE_MIN_TILES", btl::kGemmWideMinTiles},
-    {"BTL_WAIT_SPIN", 1 << 22},
+    {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1},
 };
 std::atomic<int> g_knob[btl::KN_COUNT];
 std::once_flag g_knob_once;

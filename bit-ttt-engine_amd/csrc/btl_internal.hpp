@@ -33,6 +33,7 @@ enum Knob {
     KN_WAIT_SPIN,            // polls before a kernel's internal wait gives up (2^22; the only
                              // knob that can change results: a wait that gives up leaves
                              // invalid outputs and sets the device fault word)
+    KN_ATTN_MERGE,           // 0: one-token attention merges its chunks in a second launch (1)
     KN_COUNT
 };
 int knob(Knob k);
@@ -238,7 +239,11 @@ struct AttnArgs {
     float scal;            // (f32)(1 / sqrt(hd))
     float* part;
     float* out;
+    uint32_t* ctr;         // one-token attention: the per-KV-head merge counters (attn_counters), or NULL
 };
+constexpr int kAttnMaxCtr = 64;  // KV heads the one-launch decode attention counts
+// the device's merge counters (the current device must be `dev`)
+hipError_t attn_counters(int dev, uint32_t** out);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 // One decode token: RoPE of q and of the new k, the Q8 append of k / v and the
 // attention chunk partials in one kernel, then the merge (m == 1, hd % 16 == 0).

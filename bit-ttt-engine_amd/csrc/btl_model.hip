@@ -23,6 +23,8 @@
 // the CPU oracle (oracle/bitllama_oracle.c) restates the same operations.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <algorithm>
 
 #include "btl_device.hpp"
@@ -144,7 +146,16 @@ constexpr int kAttnKs = kAttnMaxHd + 4;  // LDS key row stride (floats): 16-byte
 //   o_c[d] = sum_j p_j * vd[j][d], sequential over j                (lanes: d, d + 64)
 // and (m_c, l_c, o_c) to part.  Called by every thread of the workgroup (it
 // holds a barrier); sq / sp are this wave's rows of s_q / s_p.
-template <int HD>
+// a partial-sum store: plain, or coherent at agent scope (sc1, written through
+// to memory) when another workgroup merges it in the same launch
+template <bool SC1>
+__device__ __forceinline__ void put_part(float* p, float v)
+{
+    if (SC1) __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+
+template <int HD, bool SC1 = false>
 __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], const float (*s_v)[kAttnMaxHd],
                                                  const float* sq, float* sp, int nj, int hd_rt, float scal, int lane,
                                                  float* part)
@@ -196,11 +207,11 @@ __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], co
         o0 = __fadd_rn(o0, __fmul_rn(pj, s_v[j][c0]));
         o1 = __fadd_rn(o1, __fmul_rn(pj, s_v[j][c1]));
     }
-    if (h0) part[2 + d0] = o0;
-    if (h1) part[2 + d1] = o1;
+    if (h0) put_part<SC1>(&part[2 + d0], o0);
+    if (h1) put_part<SC1>(&part[2 + d1], o1);
     if (lane == 0) {
-        part[0] = mc;
-        part[1] = lc;
+        put_part<SC1>(&part[0], mc);
+        put_part<SC1>(&part[1], lc);
     }
 }
 
@@ -298,7 +309,64 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
 // dequantised row (the reference attends over the dequantised cache, new row
 // included: kv_cache.rs:82-86).  Loads that do not depend on the position (the
 // raw q / k / v rows and the chunk's cache rows) are issued before it arrives.
-template <int HD>
+// Chunk merge of one (query, head) by one wave (k_attn_combine's arithmetic):
+//   M = max_c m_c, w_c = exp(m_c - M), L = sum_c w_c l_c, O_d = sum_c w_c o_c[d]
+//   (both sums sequential over the chunks), y_d = O_d / L.
+// part: the head's cmax chunk slots of hd + 2 floats; C chunks used.  SC1: the
+// slots were written by other workgroups of this launch (coherent loads).
+template <bool SC1>
+__device__ __forceinline__ float ld_part(const float* p)
+{
+    if (SC1) return __uint_as_float(__hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    return *p;
+}
+
+template <bool SC1>
+__device__ __forceinline__ void attn_merge_head(const float* part, int st, int C, int hd, int lane, float* y)
+{
+    const int d0 = lane, d1 = lane + 64;
+    const bool h0 = d0 < hd, h1 = d1 < hd;
+    float M = -__builtin_inff();
+    for (int c0 = 0; c0 < C; c0 += 64) {
+        const int cc = c0 + lane;
+        M = fmaxf(M, wave_max_f32(cc < C ? ld_part<SC1>(&part[cc * st]) : -__builtin_inff()));
+    }
+    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+    for (int c0 = 0; c0 < C; c0 += 64) {
+        const int cc = c0 + lane;
+        const float w = cc < C ? btl_expf(__fsub_rn(ld_part<SC1>(&part[cc * st]), M)) : 0.0f;
+        const float l = cc < C ? ld_part<SC1>(&part[cc * st + 1]) : 0.0f;
+        const int n = min(64, C - c0);
+        constexpr int kB = 8;  // chunks whose values are in flight together
+        for (int u0 = 0; u0 < n; u0 += kB) {
+            float v0[kB], v1[kB];
+#pragma unroll
+            for (int q = 0; q < kB; ++q) {
+                const int c = c0 + u0 + q;
+                v0[q] = (u0 + q < n && h0) ? ld_part<SC1>(&part[c * st + 2 + d0]) : 0.0f;
+                v1[q] = (u0 + q < n && h1) ? ld_part<SC1>(&part[c * st + 2 + d1]) : 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < kB; ++q) {
+                if (u0 + q < n) {
+                    const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u0 + q));
+                    const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), u0 + q));
+                    L = __fadd_rn(L, __fmul_rn(wu, lu));
+                    O0 = __fadd_rn(O0, __fmul_rn(wu, v0[q]));
+                    O1 = __fadd_rn(O1, __fmul_rn(wu, v1[q]));
+                }
+            }
+        }
+    }
+    if (h0) y[d0] = __fdiv_rn(O0, L);
+    if (h1) y[d1] = __fdiv_rn(O1, L);
+}
+
+// MERGE: the chunk partials go out with coherent stores, the workgroups of a
+// KV head count themselves on an agent-scope counter, and the last one merges
+// every query head of the KV head (the counter is left at zero for the next
+// launch): no second launch.
+template <int HD, bool MERGE = false>
 __global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
 {
     __shared__ __align__(16) float s_k[kAttnChunk][kAttnKs];
@@ -335,7 +403,14 @@ __global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
         }
     }
     const int pos = a.d_pos ? *a.d_pos : a.pos;
-    if (pos < 0 || pos >= a.max_seq) return;  // uniform: nothing to append or attend
+    if (pos < 0 || pos >= a.max_seq) {  // uniform: nothing to append or attend, no result
+        if (MERGE && c == 0) {
+            float* y = a.out + (int64_t)h * hd;
+            if (lane < hd) y[lane] = __builtin_nanf("");
+            if (lane + 64 < hd) y[lane + 64] = __builtin_nanf("");
+        }
+        return;
+    }
     const int T = pos + 1;
     if (j0 >= T) return;  // uniform
     const int nj = min(kAttnChunk, T - j0);
@@ -403,7 +478,23 @@ __global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
     }
     __syncthreads();
     float* part = a.part + ((int64_t)h * a.cmax + c) * (hd + 2);
-    attn_chunk_query<HD>(s_k, s_v, s_q[wave], s_p[wave], nj, hd, a.scal, lane, part);
+    attn_chunk_query<HD, MERGE>(s_k, s_v, s_q[wave], s_p[wave], nj, hd, a.scal, lane, part);
+    if (MERGE) {
+        __shared__ uint32_t s_last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are stored
+        __syncthreads();
+        if (tid == 0) {
+            const int C = (T + kAttnChunk - 1) / kAttnChunk;  // workgroups of this KV head with keys
+            const uint32_t old = __hip_atomic_fetch_add(a.ctr + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = old + 1u == (uint32_t)C;
+            if (last) __hip_atomic_store(a.ctr + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        const int C = (T + kAttnChunk - 1) / kAttnChunk;
+        attn_merge_head<true>(a.part + (int64_t)h * a.cmax * (hd + 2), hd + 2, C, hd, lane, a.out + (int64_t)h * hd);
+    }
 }
 
 // grid (m, nh), block 64: y[d] = (sum_c w_c o_c[d]) / (sum_c w_c l_c),
@@ -487,6 +578,13 @@ hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t
         rep > kAttnMaxRep || a.cmax < 1)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)a.nkv, (unsigned)a.cmax), block((unsigned)(64 * rep));
+    if (a.ctr) {
+        if (a.nkv > kAttnMaxCtr) return hipErrorInvalidValue;
+        if (a.hd == 128) hipLaunchKernelGGL((k_attn_dec1<128, true>), grid, block, 0, st, a, kv);
+        else if (a.hd == 64) hipLaunchKernelGGL((k_attn_dec1<64, true>), grid, block, 0, st, a, kv);
+        else hipLaunchKernelGGL((k_attn_dec1<0, true>), grid, block, 0, st, a, kv);
+        return hipGetLastError();
+    }
     if (a.hd == 128) hipLaunchKernelGGL(k_attn_dec1<128>, grid, block, 0, st, a, kv);
     else if (a.hd == 64) hipLaunchKernelGGL(k_attn_dec1<64>, grid, block, 0, st, a, kv);
     else hipLaunchKernelGGL(k_attn_dec1<0>, grid, block, 0, st, a, kv);
@@ -494,6 +592,27 @@ hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3(1u, (unsigned)a.nh), dim3(64), 0, st, a);
     return hipGetLastError();
+}
+
+// The merge counters of the one-launch decode attention: kAttnMaxCtr words per
+// device, zero at load and left at zero by every launch (the last workgroup of
+// a KV head resets its word).  Calls that overlap on one device share them.
+static __device__ uint32_t g_attn_ctr[kAttnMaxCtr];
+
+hipError_t attn_counters(int dev, uint32_t** out)
+{
+    static std::atomic<uint32_t*> ptr[64];
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    uint32_t* p = ptr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        void* q = nullptr;
+        hipError_t e = hipGetSymbolAddress(&q, HIP_SYMBOL(g_attn_ctr));
+        if (e != hipSuccess) return e;
+        p = (uint32_t*)q;
+        ptr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return hipSuccess;
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st)

@@ -100,10 +100,13 @@ int btl_attention(const float* q, int64_t m, int64_t n_heads, const btl_kv_q8_t*
  * k and v, attention -- btl_rope_kv_append then btl_attention, same results
  * bit for bit.  q [m, n_heads * head_dim], k, v [m, n_kv * head_dim] raw
  * projection outputs (not modified), out [m, n_heads * head_dim].  For one
- * token (m == 1, head_dim % 16 == 0) the RoPE, the append and the attention
- * partials run in one kernel.  ws: btl_attention_workspace_bytes (it covers
- * the rotated queries too).  A device position outside the cache gives NaN
- * outputs and no append.
+ * token (m == 1, head_dim % 16 == 0) the RoPE, the append, the attention and
+ * the merge of its key chunks run in one launch (n_kv <= 64; the last
+ * workgroup of a KV head merges, counted on per-device counters that every
+ * launch leaves at zero, so such calls on one device must not overlap in
+ * time -- order them on one stream, as the workspace already asks).
+ * ws: btl_attention_workspace_bytes (it covers the rotated queries too).  A
+ * device position outside the cache gives NaN outputs and no append.
  */
 int btl_rope_append_attention(const float* q, const float* k, const float* v, int64_t m, int64_t n_heads,
                               const btl_kv_q8_t* cache, int64_t pos, const int32_t* d_pos, const float* rope_cos,

@@ -160,12 +160,15 @@ def test_attention_device_position():
         assert_same(out[0], orc.attn_decode(q[0], kq, ks, vq, vs, nh, p + 1), "pos %d" % p)
 
 
+@pytest.mark.parametrize("merge", [1, 0])
 @pytest.mark.parametrize("nh,nkv,hd", [(4, 2, 64), (32, 8, 128), (4, 4, 128), (8, 1, 16)])
 @pytest.mark.parametrize("pos,dpos", [(0, False), (63, True), (64, False), (130, True), (255, False)])
-def test_rope_append_attention_one_token(nh, nkv, hd, pos, dpos):
-    # m = 1: RoPE, the Q8 append and the attention in one kernel; same bits as
+def test_rope_append_attention_one_token(nh, nkv, hd, pos, dpos, merge, tune):
+    # m = 1: RoPE, the Q8 append and the attention in one kernel, the chunk
+    # merge in the same launch (merge=1) or a second one; same bits as
     # btl_rope_kv_append + btl_attention and as the oracle
-    print("rope_append_attention", nh, nkv, hd, pos, dpos, flush=True)
+    print("rope_append_attention", nh, nkv, hd, pos, dpos, merge, flush=True)
+    tune("BTL_ATTN_MERGE", merge)
     S = 256
     rng = np.random.default_rng(pos * 7 + hd + nh)
     q = rng.standard_normal((1, nh * hd)).astype(np.float32)
@@ -192,6 +195,46 @@ def test_rope_append_attention_one_token(nh, nkv, hd, pos, dpos):
     assert np.array_equal(kq[:, other], kq0[:, other]) and np.array_equal(vs[:, other], vs0[:, other])
     qr = orc.rope_apply(q[0].reshape(nh, hd), cos[pos], sin[pos]).reshape(-1)
     assert_same(out[0], orc.attn_decode(qr, kq, ks, vq, vs, nh, pos + 1), "attention")
+
+
+@pytest.mark.parametrize("pos", [4095, 8190])
+def test_rope_append_attention_one_token_long_cache(pos, tune):
+    # more than 64 key chunks (the merge walks them in several 64-chunk passes),
+    # Llama-3-8B head layout; then repeated calls (the merge counters must be
+    # back at zero after each launch) and a device position outside the cache
+    nh, nkv, hd, S = 32, 8, 128, 8192
+    print("rope_append_attention long", pos, flush=True)
+    rng = np.random.default_rng(pos)
+    q = rng.standard_normal((1, nh * hd)).astype(np.float32)
+    k = rng.standard_normal((1, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((1, nkv * hd)).astype(np.float32)
+    cos, sin, dc, ds = rope_dev(500000.0, hd, S)
+    cache = Cache(nkv, S, hd)
+    _fill_cache(cache, S, seed=pos)
+    qt, kt, vt = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
+    d_pos = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    outs = []
+    for merge in (1, 1, 0, 1):
+        tune("BTL_ATTN_MERGE", merge)
+        out = torch.full((1, nh * hd), 3.0, device=DEV)
+        bl.check(bl.lib.btl_rope_append_attention(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), 1, nh,
+                                                  ctypes.byref(cache.c), 0, d_pos.data_ptr(), dc.data_ptr(),
+                                                  ds.data_ptr(), out.data_ptr(), None, 0, stream()))
+        outs.append(out.cpu().numpy())
+    kq, ks, vq, vs = cache.host()
+    qr = orc.rope_apply(q[0].reshape(nh, hd), cos[pos], sin[pos]).reshape(-1)
+    ref = orc.attn_decode(qr, kq, ks, vq, vs, nh, pos + 1)
+    for i, o in enumerate(outs):
+        assert_same(o[0], ref, "call %d" % i)
+    tune("BTL_ATTN_MERGE", 1)
+    bad = torch.tensor([S], dtype=torch.int32, device=DEV)
+    out = torch.full((1, nh * hd), 3.0, device=DEV)
+    bl.check(bl.lib.btl_rope_append_attention(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), 1, nh,
+                                              ctypes.byref(cache.c), 0, bad.data_ptr(), dc.data_ptr(),
+                                              ds.data_ptr(), out.data_ptr(), None, 0, stream()))
+    assert torch.isnan(out).all(), "a device position outside the cache gives NaN"
+    kq2, ks2, _, _ = cache.host()
+    assert np.array_equal(kq2, kq) and np.array_equal(ks2, ks), "no append"
 
 
 @pytest.mark.parametrize("m,pos", [(2, 0), (17, 40), (70, 60)])
