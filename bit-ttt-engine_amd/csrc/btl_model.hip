@@ -16,7 +16,8 @@
 //                    (max, sum, weighted values) per query and head.
 //   k_attn_combine   merges the chunk partials of each (query, head).
 //   k_embed          token ids -> f32 rows of the embedding table.
-//   k_greedy         argmax over the logits (last maximum wins), next id and
+//   k_greedy         argmax over the logits (last maximum wins; workgroups fold
+//                    into one device word), next id and
 //                    position bookkeeping for a device-resident decode loop.
 //
 // Compiled with -ffp-contract=off: every f32 operation is rounded as written and
@@ -299,6 +300,86 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
     }
 }
 
+// a partial-sum load: plain, or coherent at agent scope (sc1) when other
+// workgroups of the same launch wrote it
+template <bool SC1>
+__device__ __forceinline__ float ld_part(const float* p)
+{
+    if (SC1) return __uint_as_float(__hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    return *p;
+}
+
+// The chunk merge of one (query, head) by one wave, k_attn_combine's
+// arithmetic: y[d] = (sum_c w_c o_c[d]) / (sum_c w_c l_c), w_c = exp(m_c -
+// max_c m_c), both sums sequential over the chunks.  part: the head's chunk
+// slots of st = hd + 2 floats.  Before the chunk count is known (cfun(): C,
+// or <= 0 for no result -> NaN), the (m, l) of the first 64 slots below cpre
+// and the values of the first 16 are loaded, all in flight together.  SC1: the
+// slots were written by other workgroups of this launch (coherent loads).
+template <bool SC1, typename CF>
+__device__ __forceinline__ void attn_merge_head(const float* part, int st, int cpre, int hd, int lane, float* y,
+                                                CF cfun)
+{
+    const int d0 = lane, d1 = lane + 64;
+    const bool h0 = d0 < hd, h1 = d1 < hd;
+    constexpr int kPre = 16;
+    float p0[kPre], p1[kPre];
+#pragma unroll
+    for (int c = 0; c < kPre; ++c) {
+        p0[c] = (c < cpre && h0) ? ld_part<SC1>(&part[c * st + 2 + d0]) : 0.0f;
+        p1[c] = (c < cpre && h1) ? ld_part<SC1>(&part[c * st + 2 + d1]) : 0.0f;
+    }
+    const float m_pre = lane < cpre ? ld_part<SC1>(&part[lane * st]) : 0.0f;
+    const float l_pre = lane < cpre ? ld_part<SC1>(&part[lane * st + 1]) : 0.0f;
+    const int C = cfun();
+    if (C <= 0) {
+        if (h0) y[d0] = __builtin_nanf("");
+        if (h1) y[d1] = __builtin_nanf("");
+        return;
+    }
+    float M = -__builtin_inff();
+    for (int c0 = 0; c0 < C; c0 += 64) {
+        const int cc = c0 + lane;
+        const float mv = c0 == 0 ? m_pre : (cc < C ? ld_part<SC1>(&part[cc * st]) : 0.0f);
+        M = fmaxf(M, wave_max_f32(cc < C ? mv : -__builtin_inff()));
+    }
+    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+    for (int c0 = 0; c0 < C; c0 += 64) {
+        const int cc = c0 + lane;
+        const float mv = c0 == 0 ? m_pre : (cc < C ? ld_part<SC1>(&part[cc * st]) : 0.0f);
+        const float lv = c0 == 0 ? l_pre : (cc < C ? ld_part<SC1>(&part[cc * st + 1]) : 0.0f);
+        const float w = cc < C ? btl_expf(__fsub_rn(mv, M)) : 0.0f;
+        const float l = cc < C ? lv : 0.0f;
+        const int n = min(64, C - c0);
+        int u = 0;
+        if (c0 == 0) {
+#pragma unroll
+            for (int q = 0; q < kPre; ++q) {
+                if (q < n) {
+                    const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), q));
+                    const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), q));
+                    L = __fadd_rn(L, __fmul_rn(wu, lu));
+                    O0 = __fadd_rn(O0, __fmul_rn(wu, p0[q]));
+                    O1 = __fadd_rn(O1, __fmul_rn(wu, p1[q]));
+                }
+            }
+            u = min(n, kPre);
+        }
+        for (; u < n; ++u) {
+            const int c = c0 + u;
+            const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+            const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), u));
+            L = __fadd_rn(L, __fmul_rn(wu, lu));
+            const float v0 = h0 ? ld_part<SC1>(&part[c * st + 2 + d0]) : 0.0f;
+            const float v1 = h1 ? ld_part<SC1>(&part[c * st + 2 + d1]) : 0.0f;
+            O0 = __fadd_rn(O0, __fmul_rn(wu, v0));
+            O1 = __fadd_rn(O1, __fmul_rn(wu, v1));
+        }
+    }
+    if (h0) y[d0] = __fdiv_rn(O0, L);
+    if (h1) y[d1] = __fdiv_rn(O1, L);
+}
+
 // ---------------------------------------------------------------------------
 // k_attn_dec1: one decode token -- RoPE, the Q8 append and the chunk partials
 // ---------------------------------------------------------------------------
@@ -309,59 +390,6 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
 // dequantised row (the reference attends over the dequantised cache, new row
 // included: kv_cache.rs:82-86).  Loads that do not depend on the position (the
 // raw q / k / v rows and the chunk's cache rows) are issued before it arrives.
-// Chunk merge of one (query, head) by one wave (k_attn_combine's arithmetic):
-//   M = max_c m_c, w_c = exp(m_c - M), L = sum_c w_c l_c, O_d = sum_c w_c o_c[d]
-//   (both sums sequential over the chunks), y_d = O_d / L.
-// part: the head's cmax chunk slots of hd + 2 floats; C chunks used.  SC1: the
-// slots were written by other workgroups of this launch (coherent loads).
-template <bool SC1>
-__device__ __forceinline__ float ld_part(const float* p)
-{
-    if (SC1) return __uint_as_float(__hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    return *p;
-}
-
-template <bool SC1>
-__device__ __forceinline__ void attn_merge_head(const float* part, int st, int C, int hd, int lane, float* y)
-{
-    const int d0 = lane, d1 = lane + 64;
-    const bool h0 = d0 < hd, h1 = d1 < hd;
-    float M = -__builtin_inff();
-    for (int c0 = 0; c0 < C; c0 += 64) {
-        const int cc = c0 + lane;
-        M = fmaxf(M, wave_max_f32(cc < C ? ld_part<SC1>(&part[cc * st]) : -__builtin_inff()));
-    }
-    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
-    for (int c0 = 0; c0 < C; c0 += 64) {
-        const int cc = c0 + lane;
-        const float w = cc < C ? btl_expf(__fsub_rn(ld_part<SC1>(&part[cc * st]), M)) : 0.0f;
-        const float l = cc < C ? ld_part<SC1>(&part[cc * st + 1]) : 0.0f;
-        const int n = min(64, C - c0);
-        constexpr int kB = 8;  // chunks whose values are in flight together
-        for (int u0 = 0; u0 < n; u0 += kB) {
-            float v0[kB], v1[kB];
-#pragma unroll
-            for (int q = 0; q < kB; ++q) {
-                const int c = c0 + u0 + q;
-                v0[q] = (u0 + q < n && h0) ? ld_part<SC1>(&part[c * st + 2 + d0]) : 0.0f;
-                v1[q] = (u0 + q < n && h1) ? ld_part<SC1>(&part[c * st + 2 + d1]) : 0.0f;
-            }
-#pragma unroll
-            for (int q = 0; q < kB; ++q) {
-                if (u0 + q < n) {
-                    const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u0 + q));
-                    const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), u0 + q));
-                    L = __fadd_rn(L, __fmul_rn(wu, lu));
-                    O0 = __fadd_rn(O0, __fmul_rn(wu, v0[q]));
-                    O1 = __fadd_rn(O1, __fmul_rn(wu, v1[q]));
-                }
-            }
-        }
-    }
-    if (h0) y[d0] = __fdiv_rn(O0, L);
-    if (h1) y[d1] = __fdiv_rn(O1, L);
-}
-
 // MERGE: the chunk partials go out with coherent stores, the workgroups of a
 // KV head count themselves on an agent-scope counter, and the last one merges
 // every query head of the KV head (the counter is left at zero for the next
@@ -493,7 +521,8 @@ __global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
         __syncthreads();
         if (!s_last) return;
         const int C = (T + kAttnChunk - 1) / kAttnChunk;
-        attn_merge_head<true>(a.part + (int64_t)h * a.cmax * (hd + 2), hd + 2, C, hd, lane, a.out + (int64_t)h * hd);
+        attn_merge_head<true>(a.part + (int64_t)h * a.cmax * (hd + 2), hd + 2, C, hd, lane, a.out + (int64_t)h * hd,
+                              [C]() { return C; });
     }
 }
 
@@ -506,69 +535,12 @@ __global__ __launch_bounds__(64) void k_attn_combine(AttnArgs a)
     const int i = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int hd = a.hd, st = hd + 2;
     const float* part = a.part + ((int64_t)i * a.nh + h) * a.cmax * st;
-    const int d0 = lane, d1 = lane + 64;
-    const bool h0 = d0 < hd, h1 = d1 < hd;
-    // loads that do not need the position: the first 64 chunks' (m, l) and the
-    // first 16 chunks' values (slots past the used chunks hold stale data, unused)
-    constexpr int kPre = 16;
-    float p0[kPre], p1[kPre];
-#pragma unroll
-    for (int c = 0; c < kPre; ++c) {
-        p0[c] = (c < a.cmax && h0) ? part[c * st + 2 + d0] : 0.0f;
-        p1[c] = (c < a.cmax && h1) ? part[c * st + 2 + d1] : 0.0f;
-    }
-    const float m_pre = lane < a.cmax ? part[lane * st] : 0.0f;
-    const float l_pre = lane < a.cmax ? part[lane * st + 1] : 0.0f;
-    const int pos0 = a.d_pos ? *a.d_pos : a.pos;
-    const int T = pos0 + i + 1;
     float* y = a.out + ((int64_t)i * a.nh + h) * hd;
-    if (T <= 0 || T > a.max_seq) {  // a device position outside the cache: no result
-        if (h0) y[d0] = __builtin_nanf("");
-        if (h1) y[d1] = __builtin_nanf("");
-        return;
-    }
-    const int C = (T + kAttnChunk - 1) / kAttnChunk;
-    float M = -__builtin_inff();
-    for (int c0 = 0; c0 < C; c0 += 64) {
-        const int cc = c0 + lane;
-        const float mv = c0 == 0 ? m_pre : (cc < C ? part[cc * st] : 0.0f);
-        M = fmaxf(M, wave_max_f32(cc < C ? mv : -__builtin_inff()));
-    }
-    float L = 0.0f, O0 = 0.0f, O1 = 0.0f;
-    for (int c0 = 0; c0 < C; c0 += 64) {
-        const int cc = c0 + lane;
-        const float mv = c0 == 0 ? m_pre : (cc < C ? part[cc * st] : 0.0f);
-        const float lv = c0 == 0 ? l_pre : (cc < C ? part[cc * st + 1] : 0.0f);
-        const float w = cc < C ? btl_expf(__fsub_rn(mv, M)) : 0.0f;
-        const float l = cc < C ? lv : 0.0f;
-        const int n = min(64, C - c0);
-        int u = 0;
-        if (c0 == 0) {
-#pragma unroll
-            for (int q = 0; q < kPre; ++q) {
-                if (q < n) {
-                    const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), q));
-                    const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), q));
-                    L = __fadd_rn(L, __fmul_rn(wu, lu));
-                    O0 = __fadd_rn(O0, __fmul_rn(wu, p0[q]));
-                    O1 = __fadd_rn(O1, __fmul_rn(wu, p1[q]));
-                }
-            }
-            u = min(n, kPre);
-        }
-        for (; u < n; ++u) {
-            const int c = c0 + u;
-            const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
-            const float lu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), u));
-            L = __fadd_rn(L, __fmul_rn(wu, lu));
-            const float v0 = h0 ? part[c * st + 2 + d0] : 0.0f;
-            const float v1 = h1 ? part[c * st + 2 + d1] : 0.0f;
-            O0 = __fadd_rn(O0, __fmul_rn(wu, v0));
-            O1 = __fadd_rn(O1, __fmul_rn(wu, v1));
-        }
-    }
-    if (h0) y[d0] = __fdiv_rn(O0, L);
-    if (h1) y[d1] = __fdiv_rn(O1, L);
+    attn_merge_head<false>(part, st, a.cmax, hd, lane, y, [&]() {
+        const int T = (a.d_pos ? *a.d_pos : a.pos) + i + 1;
+        // a device position outside the cache: no result
+        return T <= 0 || T > a.max_seq ? 0 : (T + kAttnChunk - 1) / kAttnChunk;
+    });
 }
 
 hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t st)
@@ -772,57 +744,80 @@ hipError_t launch_base_sum(const AdaptiveSum& a, hipStream_t st)
 // ---------------------------------------------------------------------------
 // k_embed: candle_nn::Embedding::forward (llama.rs:208) -> f32 rows
 // ---------------------------------------------------------------------------
-// grid (m), block 256.  An id outside [0, vocab) gives a zero row (the
-// reference's index_select would fail; ids from k_greedy are always in range).
+// grid (m, ceil(dim / 1024)), block 256: workgroup (t, b) copies elements
+// [1024 b, 1024 b + 1024) of row t, four per thread (vec: one 16-byte load of
+// an f32 row or one 8-byte load of a bf16 row and one 16-byte store -- dim % 4
+// == 0 and the pointers aligned for it; else four element loads, all in flight
+// before the stores).  An id outside [0, vocab)
+// gives a zero row (the reference's index_select would fail; ids from the
+// greedy pick are always in range).
 template <int XK>
 __global__ __launch_bounds__(256) void k_embed(const void* table, int64_t vocab, int dim, const int32_t* ids,
-                                               float* out)
+                                               float* out, bool vec)
 {
     const int t = blockIdx.x;
+    const int d = blockIdx.y * 1024 + 4 * threadIdx.x;
+    if (d >= dim) return;
     const int64_t id = ids[t];
     const bool ok = id >= 0 && id < vocab;
     float* y = out + (int64_t)t * dim;
-    // all of a pass's loads in flight before its stores (a store between two
-    // loads would order them: one round trip per element otherwise)
-    constexpr int kU = 16;
-    for (int d0 = threadIdx.x; d0 < dim; d0 += 256 * kU) {
-        float v[kU];
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int d = d0 + 256 * u;
-            v[u] = 0.0f;
-            if (ok && d < dim) {
-                if (XK == XK_BF16) v[u] = __uint_as_float((uint32_t)((const uint16_t*)table)[id * dim + d] << 16);
-                else v[u] = ((const float*)table)[id * dim + d];
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (vec) {
+        if (ok) {
+            if (XK == XK_BF16) {
+                const uint2 u = *(const uint2*)((const uint16_t*)table + id * dim + d);
+                v[0] = __uint_as_float(u.x << 16);
+                v[1] = __uint_as_float(u.x & 0xFFFF0000u);
+                v[2] = __uint_as_float(u.y << 16);
+                v[3] = __uint_as_float(u.y & 0xFFFF0000u);
+            } else {
+                const float4 f = *(const float4*)((const float*)table + id * dim + d);
+                v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
             }
         }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        *(float4*)(y + d) = make_float4(v[0], v[1], v[2], v[3]);
+        return;
+    }
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int d = d0 + 256 * u;
-            if (d < dim) y[d] = v[u];
+    for (int u = 0; u < 4; ++u) {
+        if (ok && d + u < dim) {
+            if (XK == XK_BF16) v[u] = __uint_as_float((uint32_t)((const uint16_t*)table)[id * dim + d + u] << 16);
+            else v[u] = ((const float*)table)[id * dim + d + u];
         }
     }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (d + u < dim) y[d + u] = v[u];
 }
 
 hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim, const int32_t* ids, int64_t m,
                         float* out, hipStream_t st)
 {
     if (m <= 0) return hipSuccess;
-    if (xkind == XK_BF16) hipLaunchKernelGGL(k_embed<XK_BF16>, dim3((unsigned)m), dim3(256), 0, st, table, vocab, (int)dim, ids, out);
-    else hipLaunchKernelGGL(k_embed<XK_F32>, dim3((unsigned)m), dim3(256), 0, st, table, vocab, (int)dim, ids, out);
+    if (m > INT32_MAX || dim < 1 || dim > INT32_MAX - 1024) return hipErrorInvalidValue;
+    const uintptr_t ta = xkind == XK_BF16 ? 7u : 15u;
+    const bool vec = dim % 4 == 0 && ((uintptr_t)table & ta) == 0 && ((uintptr_t)out & 15u) == 0;
+    const dim3 grid((unsigned)m, (unsigned)((dim + 1023) / 1024));
+    if (xkind == XK_BF16)
+        hipLaunchKernelGGL(k_embed<XK_BF16>, grid, dim3(256), 0, st, table, vocab, (int)dim, ids, out, vec);
+    else hipLaunchKernelGGL(k_embed<XK_F32>, grid, dim3(256), 0, st, table, vocab, (int)dim, ids, out, vec);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // k_greedy: the greedy pick of stream_completion (llama.rs:509-515)
 // ---------------------------------------------------------------------------
-// One workgroup of 1024 threads.  Each value maps to a key that orders floats
-// totally (-0 taken as +0; NaN above +inf: the reference's partial_cmp would
-// panic there); (key, index) pairs compare lexicographically, so equal maxima
-// resolve to the largest index, as Iterator::max_by does.  Thread 0 writes the
-// id; with d_pos it also stores it at log[*d_pos + 1] (the sequence position
-// the token will take) and advances *d_pos.
+// Each value maps to a key that orders floats totally (-0 taken as +0; NaN
+// above +inf: the reference's partial_cmp would panic there); (key, index)
+// pairs compare lexicographically as one 64-bit word, so equal maxima resolve
+// to the largest index, as Iterator::max_by does.  The maximum of a set of
+// words does not depend on the order they are visited in, so the workgroups
+// fold their maxima into one device word with an atomic max; the last
+// workgroup to arrive (device counter) takes the word, writes the id -- with
+// d_pos also log[*d_pos + 1] (the sequence position the token will take) --
+// advances *d_pos, and leaves the word and the counter at zero for the next
+// launch.
 __device__ __forceinline__ uint64_t greedy_key(float f, uint32_t idx)
 {
     uint32_t u = __float_as_uint(f);
@@ -831,27 +826,34 @@ __device__ __forceinline__ uint64_t greedy_key(float f, uint32_t idx)
     return ((uint64_t)u << 32) | idx;
 }
 
-__global__ __launch_bounds__(1024) void k_greedy(const float* x, int n, int32_t* next_id, int32_t* d_pos,
-                                                 int32_t* log, int log_len)
+struct GreedyState {
+    uint64_t best;   // the running maximum word of the launch
+    uint32_t count;  // workgroups done
+};
+static __device__ GreedyState g_greedy;
+
+constexpr int kGreedyU = 4;       // float4 loads in flight per thread
+constexpr int kGreedyMaxWg = 256;
+
+// grid G, block 256: workgroup b reads the float4s b * 256 + tid + G * 256 * u
+__global__ __launch_bounds__(256) void k_greedy(const float* x, int n, int32_t* next_id, int32_t* d_pos,
+                                                int32_t* log, int log_len, GreedyState* gs)
 {
-    __shared__ uint64_t s_best[16];
+    __shared__ uint64_t s_best[4];
     const int tid = threadIdx.x;
-    uint64_t best = 0;
+    const int G = gridDim.x;
     const int n4 = n >> 2;
-    // 16 independent loads in flight per thread (the logits come mostly from
-    // other XCDs' writes: one dependent load per step made this latency-bound);
-    // the key order is total, so the visiting order does not change the pick
-    constexpr int kU = 16;
-    for (int i0 = tid; i0 < n4; i0 += 1024 * kU) {
-        float4 v[kU];
+    uint64_t best = 0;
+    for (int i0 = blockIdx.x * 256 + tid; i0 < n4; i0 += G * 256 * kGreedyU) {
+        float4 v[kGreedyU];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int i = i0 + 1024 * u;
+        for (int u = 0; u < kGreedyU; ++u) {
+            const int i = i0 + G * 256 * u;
             v[u] = i < n4 ? ((const float4*)x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const int i = i0 + 1024 * u;
+        for (int u = 0; u < kGreedyU; ++u) {
+            const int i = i0 + G * 256 * u;
             if (i < n4) {
                 best = max(best, greedy_key(v[u].x, 4 * i));
                 best = max(best, greedy_key(v[u].y, 4 * i + 1));
@@ -860,7 +862,8 @@ __global__ __launch_bounds__(1024) void k_greedy(const float* x, int n, int32_t*
             }
         }
     }
-    for (int i = 4 * n4 + tid; i < n; i += 1024) best = max(best, greedy_key(x[i], i));
+    if (blockIdx.x == 0)
+        for (int i = 4 * n4 + tid; i < n; i += 256) best = max(best, greedy_key(x[i], i));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)best, off, 64);
@@ -869,24 +872,43 @@ __global__ __launch_bounds__(1024) void k_greedy(const float* x, int n, int32_t*
     }
     if ((tid & 63) == 0) s_best[tid >> 6] = best;
     __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < 16; ++w) best = max(best, s_best[w]);
-        const int32_t id = (int32_t)(uint32_t)best;
-        next_id[0] = id;
-        if (d_pos) {
-            const int32_t p = *d_pos;
-            if (log && p + 1 >= 0 && p + 1 < log_len) log[p + 1] = id;
-            *d_pos = p + 1;
-        }
+    if (tid != 0) return;
+    for (int w = 1; w < 4; ++w) best = max(best, s_best[w]);
+    __hip_atomic_fetch_max(&gs->best, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the maximum is folded in before the arrival counts
+    const uint32_t old = __hip_atomic_fetch_add(&gs->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old + 1u != (uint32_t)G) return;
+    const uint64_t win = __hip_atomic_exchange(&gs->best, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&gs->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int32_t id = (int32_t)(uint32_t)win;
+    next_id[0] = id;
+    if (d_pos) {
+        const int32_t p = *d_pos;
+        if (log && p + 1 >= 0 && p + 1 < log_len) log[p + 1] = id;
+        *d_pos = p + 1;
     }
 }
 
 hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log, int64_t log_len,
                          hipStream_t st)
 {
+    static std::atomic<GreedyState*> ptr[64];
     if (n <= 0 || n > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_greedy, dim3(1), dim3(1024), 0, st, x, (int)n, next_id, d_pos, log,
-                       (int)(log_len > INT32_MAX ? INT32_MAX : log_len));
+    int dev;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    GreedyState* gs = ptr[dev].load(std::memory_order_acquire);
+    if (!gs) {
+        void* q = nullptr;
+        if ((e = hipGetSymbolAddress(&q, HIP_SYMBOL(g_greedy))) != hipSuccess) return e;
+        gs = (GreedyState*)q;
+        ptr[dev].store(gs, std::memory_order_release);
+    }
+    const int64_t n4 = n >> 2;
+    const int G = (int)std::min<int64_t>(kGreedyMaxWg, std::max<int64_t>(1, (n4 + 256 * kGreedyU - 1) / (256 * kGreedyU)));
+    hipLaunchKernelGGL(k_greedy, dim3((unsigned)G), dim3(256), 0, st, x, (int)n, next_id, d_pos, log,
+                       (int)(log_len > INT32_MAX ? INT32_MAX : log_len), gs);
     return hipGetLastError();
 }
 

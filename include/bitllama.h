@@ -124,7 +124,10 @@ int btl_embedding(const void* table, int dtype, int64_t vocab, int64_t dim, cons
  * Greedy pick (llama.rs:509-515): next_id[0] = argmax(logits[0..n)), the last
  * index among equal maxima (Iterator::max_by).  With d_pos != NULL, also
  * log[*d_pos + 1] = id when it is inside log[0..log_len), then *d_pos += 1:
- * one decode step's bookkeeping on the device.  logits 16-byte aligned.
+ * one decode step's bookkeeping on the device.  logits 16-byte aligned.  The
+ * workgroups of the launch meet in a per-device word that every launch leaves
+ * at zero: calls on one device must not overlap in time (order them on one
+ * stream).
  */
 int btl_greedy_next(const float* logits, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,
                     int64_t log_len, void* stream);

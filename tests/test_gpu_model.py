@@ -264,16 +264,23 @@ def test_rope_append_attention_many_tokens(m, pos):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_embedding(dtype):
-    vocab, dim = 1000, 320
+@pytest.mark.parametrize("dim,off", [(320, 0), (4096, 0), (4100, 0), (322, 0), (4096, 1), (5, 0)])
+def test_embedding(dtype, dim, off):
+    # whole-row copies: 16-byte (f32) / 8-byte (bf16) loads when dim % 4 == 0 and
+    # the pointers allow it, element loads otherwise (off: an output view one
+    # float past an aligned start); several 1024-element blocks per row
+    vocab = 1000
     table = torch.randn((vocab, dim), device=DEV).to(dtype)
     ids = torch.tensor([5, 999, 0, -1, 1000, 5], dtype=torch.int32, device=DEV)
-    out = torch.full((6, dim), 7.0, device=DEV)
+    buf = torch.full((6 * dim + off,), 7.0, device=DEV)
+    out = buf[off:].view(6, dim)
     bl.check(bl.lib.btl_embedding(table.data_ptr(), bl.BTL_BF16 if dtype == torch.bfloat16 else bl.BTL_F32, vocab,
                                   dim, ids.data_ptr(), 6, out.data_ptr(), stream()))
     t = table.float()
     exp = torch.stack([t[5], t[999], t[0], torch.zeros(dim, device=DEV), torch.zeros(dim, device=DEV), t[5]])
     assert torch.equal(out, exp)
+    if off:
+        assert float(buf[0]) == 7.0
 
 
 def test_greedy_next():
@@ -284,6 +291,18 @@ def test_greedy_next():
     big[77777] = big[1234] = 9.0  # tie: the later index wins
     cases.append(big)
     cases.append(rng.standard_normal(1001).astype(np.float32))  # tail of n % 4
+    cases += [np.array([2.0], np.float32), np.array([1.0, 3.0, 3.0], np.float32)]
+    sp = rng.standard_normal(128256).astype(np.float32)
+    sp[[3, 128255]] = np.inf  # equal infinities: the later one
+    cases.append(sp)
+    # many workgroups, several passes each; the maximum in the last element's
+    # workgroup and a tie far apart
+    huge = rng.standard_normal(10_000_003).astype(np.float32)
+    huge[[17, 10_000_002]] = 50.0
+    cases.append(huge)
+    neg = -np.abs(rng.standard_normal(50_001)).astype(np.float32) - 1.0
+    neg[49_999] = -0.5
+    cases.append(neg)
     for x in cases:
         xt = torch.from_numpy(x).to(DEV)
         nid = torch.full((1,), -5, dtype=torch.int32, device=DEV)
