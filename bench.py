@@ -423,30 +423,10 @@ def run_sweep(layers, gen, dev, args):
             "rows": rows}
 
 
-def run_e2e(layers, gen, dev, args):
-    """cfg5: the end-to-end ternary decoder (bitlinear.model.BitLlamaHip) with
-    Llama-3-8B shapes on the same 32 layers of packed weights, plus seeded norm
-    weights, an f32 embedding table and a ternary lm_head (vocab 128256): a
-    prompt of 512 uniform random ids prefilled in one batch, then 256 greedy
-    decode steps at batch 1, each a HIP-graph replay of one step with the
-    position and next id on the device (no host synchronisation between steps).
-    Timed separately: the prefill (HIP events around it) and the decode steps
-    after the first (events around the replays)."""
-    from bitlinear.model import BitLlamaHip, LlamaConfig
-    prompt_len, gen_len = args.e2e_prompt, args.e2e_tokens
-    cfg = LlamaConfig.llama3_8b(max_seq=prompt_len + gen_len + 1)
-
-    def norm():
-        return (1.0 + 0.1 * torch.randn((HIDDEN,), generator=gen, device=dev)).contiguous()
-
-    w = torch.randn((cfg.vocab, HIDDEN), generator=gen, device=dev) * 0.02
-    head = bl.PackedTensor.pack_device(w)
-    del w
-    weights = {"embed": torch.randn((cfg.vocab, HIDDEN), generator=gen, device=dev), "norm_f": norm(),
-               "lm_head": head,
-               "layers": [dict(L, norm1=norm(), norm2=norm()) for L in layers]}
-    model = BitLlamaHip(cfg, weights, dev, max_rows=prompt_len)
-    prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=gen, device=dev).cpu().numpy()
+def _e2e_run(model, prompt, gen_len):
+    """Prefill (timed with HIP events), the first greedy pick, one eager decode
+    step, capture, then gen_len - 2 graph replays (timed).  -> (prefill ms,
+    decode ms per token, the generated ids)."""
     model.reset()
     model.prefill(prompt)  # warm-up (sizes the library workspace)
     torch.cuda.synchronize()
@@ -468,28 +448,96 @@ def run_e2e(layers, gen, dev, args):
     e1.record()
     torch.cuda.synchronize()
     dec_ms = e0.elapsed_time(e1) / (gen_len - 2)
-    toks = model.log[start:start + gen_len].cpu().numpy()
-    print("bench: e2e prefill %d tokens %.2f ms, decode %.3f ms/token" % (prompt_len, prefill_ms, dec_ms),
-          file=sys.stderr, flush=True)
+    return prefill_ms, dec_ms, model.log[start:start + gen_len].cpu().numpy()
+
+
+def _dense_head_kernel(w, code, dev, reps=20):
+    """btl_dense_linear alone at M=1 (the lm_head GEMV): launches over the same
+    weights back to back on one stream (each reads far more than the caches hold);
+    us per launch and the HBM fraction of its bytes."""
+    x = torch.randn((1, w.shape[1]), device=dev)
+    y = torch.empty((1, w.shape[0]), device=dev)
+
+    def fn(stream):
+        for _ in range(reps):
+            bl.check(bl.lib.btl_dense_linear(w.data_ptr(), code, w.shape[0], w.shape[1], x.data_ptr(), 1,
+                                             y.data_ptr(), stream))
+
+    us = time_launches(fn, 5, torch.cuda.Stream()) / reps
+    nbytes = w.numel() * w.element_size() + x.numel() * 4 + y.numel() * 4
+    return {"us": round(us, 2), "bytes": int(nbytes), "GB_s": round(nbytes / us / 1e3, 1),
+            "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 3)}
+
+
+def run_e2e(layers, gen, dev, args):
+    """cfg5: the end-to-end decoder (bitlinear.model.BitLlamaHip) with Llama-3-8B
+    shapes on the same 32 layers of packed weights, plus seeded norm weights and an
+    f32 embedding table (vocab 128256): a prompt of 512 uniform random ids
+    prefilled in one batch, then 256 greedy decode steps at batch 1, each a
+    HIP-graph replay of one step with the position and next id on the device (no
+    host synchronisation between steps).  Timed separately: the prefill (HIP
+    events around it) and the decode steps after the first (events around the
+    replays).  Three heads: a ternary BitLinear lm_head (the headline), and the
+    reference's dense lm_head (llama.rs:129-141) with f32 weights -- as the
+    reference holds them -- and with bf16 weights."""
+    from bitlinear.model import BitLlamaHip, LlamaConfig
+    prompt_len, gen_len = args.e2e_prompt, args.e2e_tokens
+    cfg = LlamaConfig.llama3_8b(max_seq=prompt_len + gen_len + 1)
+
+    def norm():
+        return (1.0 + 0.1 * torch.randn((HIDDEN,), generator=gen, device=dev)).contiguous()
+
+    w = torch.randn((cfg.vocab, HIDDEN), generator=gen, device=dev) * 0.02
+    head = bl.PackedTensor.pack_device(w)
+    weights = {"embed": torch.randn((cfg.vocab, HIDDEN), generator=gen, device=dev), "norm_f": norm(),
+               "lm_head": head,
+               "layers": [dict(L, norm1=norm(), norm2=norm()) for L in layers]}
+    prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=gen, device=dev).cpu().numpy()
     # per-step bytes: the 32 layers' packed weights + lm_head + the Q8 KV rows read at the mean context
     wbytes = sum(L[nm].data.numel() for L in layers for nm in ("q", "k", "v", "o", "gate", "up", "down"))
     mean_ctx = prompt_len + gen_len / 2
     kv_bytes = LAYERS * 2 * cfg.n_kv_heads * mean_ctx * (cfg.head_dim + 4)
-    step_bytes = wbytes + head.data.numel() + kv_bytes
+
+    def summary(prefill_ms, dec_ms, head_bytes):
+        step_bytes = wbytes + head_bytes + kv_bytes
+        return {"prefill_tok_s": round(prompt_len / prefill_ms * 1000.0, 1), "prefill_ms": round(prefill_ms, 3),
+                "decode_tok_s": round(1000.0 / dec_ms, 1), "decode_ms_per_token": round(dec_ms, 4),
+                "decode_bytes_per_token": int(step_bytes),
+                "decode_frac_hbm": round(step_bytes / dec_ms / 1e6 / HBM_PEAK_GBS, 3)}
+
+    model = BitLlamaHip(cfg, weights, dev, max_rows=prompt_len)
+    prefill_ms, dec_ms, toks = _e2e_run(model, prompt, gen_len)
     del model
-    return {"workload": "cfg5: Llama-3-8B-shaped ternary decoder, 32 layers, hidden 4096, 32/8 heads x 128, "
-                        "intermediate 14336, vocab 128256, every linear BitLinear W1.58-A8 (lm_head too), Q8 KV "
-                        "cache; %d-token uniform random prompt prefilled in one batch, %d greedy tokens at batch 1 "
-                        "(HIP-graph step, device-side position)" % (prompt_len, gen_len),
-            "prefill_tok_s": round(prompt_len / prefill_ms * 1000.0, 1), "prefill_ms": round(prefill_ms, 3),
-            "decode_tok_s": round(1000.0 / dec_ms, 1), "decode_ms_per_token": round(dec_ms, 4),
-            "decode_bytes_per_token": int(step_bytes),
-            "decode_frac_hbm": round(step_bytes / dec_ms / 1e6 / HBM_PEAK_GBS, 3),
-            # embedding; per layer q|k|v (norm in the quantising waves), attention (RoPE,
-            # append, chunks and their merge), o (+ residual), gate|up (norm; SwiGLU
-            # epilogue), down (+ residual); final norm, lm_head, pick
-            "launches_per_token": 1 + LAYERS * 5 + 3,
-            "first_tokens": [int(t) for t in toks[:8]]}
+    print("bench: e2e prefill %d tokens %.2f ms, decode %.3f ms/token" % (prompt_len, prefill_ms, dec_ms),
+          file=sys.stderr, flush=True)
+    out = {"workload": "cfg5: Llama-3-8B-shaped ternary decoder, 32 layers, hidden 4096, 32/8 heads x 128, "
+                       "intermediate 14336, vocab 128256, every linear BitLinear W1.58-A8 (lm_head too), Q8 KV "
+                       "cache; %d-token uniform random prompt prefilled in one batch, %d greedy tokens at batch 1 "
+                       "(HIP-graph step, device-side position)" % (prompt_len, gen_len)}
+    out.update(summary(prefill_ms, dec_ms, head.data.numel()))
+    # embedding; per layer q|k|v (norm in the quantising waves), attention (RoPE,
+    # append, chunks and their merge), o (+ residual), gate|up (norm; SwiGLU
+    # epilogue), down (+ residual); final norm, lm_head, pick
+    out["launches_per_token"] = 1 + LAYERS * 5 + 3
+    out["first_tokens"] = [int(t) for t in toks[:8]]
+    dense = {"workload": "the same decoder with the reference's dense lm_head (candle_nn::Linear, "
+                         "llama.rs:129-141): final RMSNorm to f32 (btl_add_rmsnorm), then btl_dense_linear "
+                         "(f32 sums) over f32 weights (as the reference holds them) or bf16 weights"}
+    for name, dt, code in (("f32", torch.float32, bl.BTL_F32), ("bf16", torch.bfloat16, bl.BTL_BF16)):
+        dw = w.to(dt).contiguous()
+        weights["lm_head"] = dw
+        model = BitLlamaHip(cfg, weights, dev, max_rows=prompt_len)
+        p_ms, d_ms, _ = _e2e_run(model, prompt, gen_len)
+        del model
+        dense[name] = summary(p_ms, d_ms, dw.numel() * dw.element_size())
+        dense[name]["lm_head_kernel"] = _dense_head_kernel(dw, code, dev)
+        print("bench: e2e dense %s head: decode %.3f ms/token, head kernel %.1f us" %
+              (name, d_ms, dense[name]["lm_head_kernel"]["us"]), file=sys.stderr, flush=True)
+        del dw
+    weights["lm_head"] = head
+    del w
+    out["dense_head"] = dense
+    return out
 
 
 def run_adaptive(gen, dev, args):

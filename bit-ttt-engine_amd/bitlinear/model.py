@@ -22,8 +22,10 @@ buffers (each add writes the other one).  A one-token step moves the two adds
 into the epilogues of o and down (x' = x + o and x + mlp_out through
 btl_linear_residual), so the kernels of q|k|v and gate|up apply only the
 RMSNorm, in their quantising waves; the gate/up kernel writes silu(gate) * up
-from its epilogue.  Every linear is a BitLinear (W1.58-A8), the lm_head
-included.
+from its epilogue.  Every linear of the blocks is a BitLinear (W1.58-A8); the
+lm_head is either a BitLinear too (one launch with the final norm) or, as in the
+reference, a dense linear (llama.rs:129-141: btl_add_rmsnorm, then
+btl_dense_linear over f32 or bf16 weights).
 
 Deliberate differences from the reference, all on the host side:
   * the prompt is prefilled as one batch of rows (the reference feeds it token by
@@ -100,7 +102,9 @@ class BitLlamaHip:
 
     weights: dict with
       "embed" [vocab, hidden] float32 or bfloat16 (GPU),
-      "norm_f" [hidden] float32, "lm_head" PackedTensor [vocab, hidden],
+      "norm_f" [hidden] float32, "lm_head" PackedTensor [vocab, hidden] (ternary, a
+      BitLinear) or a dense float32 / bfloat16 tensor [vocab, hidden] (the
+      reference's candle_nn::Linear, llama.rs:129-141),
       "layers": list of dicts {"norm1", "norm2": [hidden] f32,
                                "q", "k", "v", "o", "gate", "up", "down": PackedTensor}.
     """
@@ -146,7 +150,16 @@ class BitLlamaHip:
                                      down_w=ctypes.byref(d_c[0]),
                                      gate=ctypes.byref(gate_c), up=ctypes.byref(up_c), gate_c=gate_c, up_c=up_c,
                                      n1=L["norm1"].data_ptr(), n2=L["norm2"].data_ptr()))
-        self._head_c, self._head = _arr([weights["lm_head"]])
+        head = weights["lm_head"]
+        self.dense_head = isinstance(head, torch.Tensor)
+        if self.dense_head:
+            if head.dtype not in (torch.float32, torch.bfloat16) or tuple(head.shape) != (c.vocab, c.hidden) \
+                    or not head.is_contiguous():
+                raise ValueError("dense lm_head: a contiguous float32 / bfloat16 [vocab, hidden] tensor")
+            self._head_dt = BTL_BF16 if head.dtype == torch.bfloat16 else BTL_F32
+            self.xf = torch.zeros((1, c.hidden), **f32)  # RMSNorm_f of the last row
+        else:
+            self._head_c, self._head = _arr([head])
         self._y_qkv = _ptrs([self.q, self.k, self.v])
         self._y_o = _ptrs([self.o])
         self._y_down = _ptrs([self.down])
@@ -219,6 +232,13 @@ class BitLlamaHip:
                                        BTL_F32, ws, wn, st))
         last = m - 1
         delta = None if one else self.down[last].data_ptr()
+        if self.dense_head:
+            # RMSNorm_f into f32, then the dense linear (llama.rs:255-265)
+            check(lib.btl_add_rmsnorm(cur[last].data_ptr(), delta, None, self.w["norm_f"].data_ptr(), c.eps, 1, hid,
+                                      self.xf.data_ptr(), st))
+            check(lib.btl_dense_linear(self.w["lm_head"].data_ptr(), self._head_dt, c.vocab, hid, self.xf.data_ptr(),
+                                       1, self.logits.data_ptr(), st))
+            return
         check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, cur[last].data_ptr(), delta, None,
                                                self.w["norm_f"].data_ptr(), c.eps, 1, hid, BTL_F32, ws, wn, st))
 

@@ -315,5 +315,9 @@ hipError_t launch_embed(const void* table, int xkind, int64_t vocab, int64_t dim
                         float* out, hipStream_t st);
 hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,
                          int64_t log_len, hipStream_t st);
+hipError_t launch_rmsnorm_f32(const float* h, const float* delta, float* h_out, const float* g, float eps, int64_t m,
+                              int64_t k, float* y, hipStream_t st);
+hipError_t launch_dense_gemv(const void* w, int wkind, int64_t n, int64_t k, const float* x, int64_t m, float* y,
+                             hipStream_t st);
 
 }  // namespace btl

@@ -16,6 +16,8 @@
 //                    (max, sum, weighted values) per query and head.
 //   k_attn_combine   merges the chunk partials of each (query, head).
 //   k_embed          token ids -> f32 rows of the embedding table.
+//   k_rmsnorm_f32    RMSNorm of f32 rows (+ a residual) into f32 rows.
+//   k_dense_gemv     a dense f32 / bf16 linear (the reference's lm_head), f32 sums.
 //   k_greedy         argmax over the logits (last maximum wins; workgroups fold
 //                    into one device word), next id and
 //                    position bookkeeping for a device-resident decode loop.
@@ -909,6 +911,192 @@ hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d
     const int G = (int)std::min<int64_t>(kGreedyMaxWg, std::max<int64_t>(1, (n4 + 256 * kGreedyU - 1) / (256 * kGreedyU)));
     hipLaunchKernelGGL(k_greedy, dim3((unsigned)G), dim3(256), 0, st, x, (int)n, next_id, d_pos, log,
                        (int)(log_len > INT32_MAX ? INT32_MAX : log_len), gs);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_rmsnorm_f32: RMSNorm::forward (rms_norm.rs:33-56) into f32 rows
+// ---------------------------------------------------------------------------
+// grid (m), block 256.  s = h (+ delta); the sum of s*s is the pairwise tree
+// over the row in index order (zero-padded): thread t folds the 16 elements of
+// group b * 256 + t (pairwise), the lanes' xor butterfly the 64 groups of a
+// wave, then ((w0 + w1) + (w2 + w3)) the 256 groups of block b, and thread 0
+// the blocks pairwise.  d = sqrt(sum * (f32)(1/k) + eps); y = (s / d) * g;
+// h_out = s (written in the second pass, so h_out may be h).  k % 64 == 0.
+__device__ __forceinline__ void rms_load16(const float* h, const float* delta, int k, int64_t e0, float* v)
+{
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (e0 + 4 * q < k) {
+            a = *(const float4*)(h + e0 + 4 * q);
+            if (delta) {
+                const float4 b = *(const float4*)(delta + e0 + 4 * q);
+                a = make_float4(__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w));
+            }
+        }
+        v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
+    }
+}
+
+constexpr int kRmsMaxBlocks = 16;  // k <= 16 * 4096
+
+__global__ __launch_bounds__(256) void k_rmsnorm_f32(const float* h, const float* delta, float* h_out, const float* g,
+                                                     float eps, int k, float* y)
+{
+    __shared__ float s_w[4];
+    __shared__ float s_blk[kRmsMaxBlocks];
+    __shared__ float s_d;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t row = (int64_t)blockIdx.x * k;
+    h += row;
+    if (delta) delta += row;
+    y += row;
+    if (h_out) h_out += row;
+    const int nblk = (k + 4095) / 4096;
+    for (int b = 0; b < nblk; ++b) {
+        float v[16];
+        rms_load16(h, delta, k, (int64_t)(b * 256 + tid) * 16, v);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = __fmul_rn(v[e], v[e]);
+#pragma unroll
+        for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+            for (int i = 0; i < len / 2; ++i) v[i] = __fadd_rn(v[2 * i], v[2 * i + 1]);
+        const float ws = wave_pairwise_sum(v[0]);
+        if (lane == 0) s_w[wave] = ws;
+        __syncthreads();
+        if (tid == 0) s_blk[b] = __fadd_rn(__fadd_rn(s_w[0], s_w[1]), __fadd_rn(s_w[2], s_w[3]));
+        __syncthreads();
+    }
+    if (tid == 0) {
+        float p[kRmsMaxBlocks];
+#pragma unroll
+        for (int b = 0; b < kRmsMaxBlocks; ++b) p[b] = b < nblk ? s_blk[b] : 0.0f;
+#pragma unroll
+        for (int len = kRmsMaxBlocks; len > 1; len >>= 1)
+#pragma unroll
+            for (int i = 0; i < len / 2; ++i) p[i] = __fadd_rn(p[2 * i], p[2 * i + 1]);
+        const float inv_k = (float)(1.0 / (double)k);
+        s_d = sqrt_rn(__fadd_rn(__fmul_rn(p[0], inv_k), eps));
+    }
+    __syncthreads();
+    const float d = s_d;
+    for (int b = 0; b < nblk; ++b) {
+        const int64_t e0 = (int64_t)(b * 256 + tid) * 16;
+        if (e0 >= k) break;
+        float v[16];
+        rms_load16(h, delta, k, e0, v);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 gv = *(const float4*)(g + e0 + 4 * q);
+            if (h_out) *(float4*)(h_out + e0 + 4 * q) = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            *(float4*)(y + e0 + 4 * q) =
+                make_float4(__fmul_rn(__fdiv_rn(v[4 * q], d), gv.x), __fmul_rn(__fdiv_rn(v[4 * q + 1], d), gv.y),
+                            __fmul_rn(__fdiv_rn(v[4 * q + 2], d), gv.z), __fmul_rn(__fdiv_rn(v[4 * q + 3], d), gv.w));
+        }
+    }
+}
+
+hipError_t launch_rmsnorm_f32(const float* h, const float* delta, float* h_out, const float* g, float eps, int64_t m,
+                              int64_t k, float* y, hipStream_t st)
+{
+    if (m < 1 || m > INT32_MAX || k < 64 || k % 64 || k > 4096 * kRmsMaxBlocks) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rmsnorm_f32, dim3((unsigned)m), dim3(256), 0, st, h, delta, h_out, g, eps, (int)k, y);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// k_dense_gemv: candle_nn::Linear::forward without a bias (the dense lm_head,
+// llama.rs:129-141), f32 sums in a fixed order
+// ---------------------------------------------------------------------------
+// grid (G, m), block 256: wave gw = 4 blockIdx.x + wave computes rows j = gw,
+// gw + 4G, ... of token row blockIdx.y.  Lane l takes the 4-element chunks
+// c = l, l + 64, ... of the row and folds each chunk's elements in order into
+// acc = fma(x, w, acc); six butterfly steps (xor 32 .. 1) add the lanes.  KX >
+// 0: k == 256 KX and the lane's x chunks stay in registers (one weight load per
+// chunk, all KX in flight); KX == 0: any k % 4 == 0, eight chunks of w and x
+// in flight at a time.  Weights are read once: non-temporal loads.
+typedef uint32_t dense_u2 __attribute__((ext_vector_type(2)));
+typedef float dense_f4 __attribute__((ext_vector_type(4)));
+
+template <int WK>
+__device__ __forceinline__ float4 dense_w4(const void* w, int64_t off)
+{
+    if (WK == XK_BF16) {
+        const dense_u2 u = __builtin_nontemporal_load((const dense_u2*)((const uint16_t*)w + off));
+        return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u), __uint_as_float(u.y << 16),
+                           __uint_as_float(u.y & 0xFFFF0000u));
+    }
+    const dense_f4 f = __builtin_nontemporal_load((const dense_f4*)((const float*)w + off));
+    return make_float4(f.x, f.y, f.z, f.w);
+}
+
+__device__ __forceinline__ float fma4(float4 x, float4 w, float acc)
+{
+    acc = __fmaf_rn(x.x, w.x, acc);
+    acc = __fmaf_rn(x.y, w.y, acc);
+    acc = __fmaf_rn(x.z, w.z, acc);
+    return __fmaf_rn(x.w, w.w, acc);
+}
+
+template <int WK, int KX>
+__global__ __launch_bounds__(256) void k_dense_gemv(const void* w, int64_t n, int k, const float* x, float* y)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float4* xr = (const float4*)(x + (int64_t)blockIdx.y * k);
+    float* yr = y + (int64_t)blockIdx.y * n;
+    const int nc = k >> 2;
+    const int64_t stride = (int64_t)gridDim.x * 4;
+    float4 xv[KX > 0 ? KX : 1];
+#pragma unroll
+    for (int u = 0; u < KX; ++u) xv[u] = xr[lane + 64 * u];
+    for (int64_t j = (int64_t)blockIdx.x * 4 + wave; j < n; j += stride) {
+        const int64_t base = j * k;
+        float acc = 0.0f;
+        if (KX > 0) {
+            float4 wv[KX > 0 ? KX : 1];
+#pragma unroll
+            for (int u = 0; u < KX; ++u) wv[u] = dense_w4<WK>(w, base + 4 * (lane + 64 * u));
+#pragma unroll
+            for (int u = 0; u < KX; ++u) acc = fma4(xv[u], wv[u], acc);
+        } else {
+            constexpr int kU = 8;
+            for (int c0 = lane; c0 < nc; c0 += 64 * kU) {
+                float4 wv[kU], xq[kU];
+#pragma unroll
+                for (int u = 0; u < kU; ++u) {
+                    const int c = c0 + 64 * u;
+                    wv[u] = c < nc ? dense_w4<WK>(w, base + 4 * c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    xq[u] = c < nc ? xr[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+#pragma unroll
+                for (int u = 0; u < kU; ++u)
+                    if (c0 + 64 * u < nc) acc = fma4(xq[u], wv[u], acc);
+            }
+        }
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, s, 64));
+        if (lane == 0) yr[j] = acc;
+    }
+}
+
+hipError_t launch_dense_gemv(const void* w, int wkind, int64_t n, int64_t k, const float* x, int64_t m, float* y,
+                             hipStream_t st)
+{
+    if (n < 1 || m < 1 || m > 65535 || k < 4 || k % 4 || k > INT32_MAX / 2) return hipErrorInvalidValue;
+    const unsigned G = (unsigned)std::min<int64_t>((n + 3) / 4, 1024);
+    const dim3 grid(G, (unsigned)m), block(256);
+    const bool xr = k == 4096;
+#define BTL_DENSE(WKV)                                                                                   \
+    if (xr) hipLaunchKernelGGL((k_dense_gemv<WKV, 16>), grid, block, 0, st, w, n, (int)k, x, y);        \
+    else hipLaunchKernelGGL((k_dense_gemv<WKV, 0>), grid, block, 0, st, w, n, (int)k, x, y);
+    if (wkind == XK_BF16) {
+        BTL_DENSE(XK_BF16)
+    } else {
+        BTL_DENSE(XK_F32)
+    }
+#undef BTL_DENSE
     return hipGetLastError();
 }
 

@@ -280,4 +280,50 @@ int btl_greedy_next(const float* logits, int64_t n, int32_t* next_id, int32_t* d
     return BTL_OK;
 }
 
+int btl_add_rmsnorm(const float* h, const float* delta, float* h_out, const float* g, float eps, int64_t m, int64_t k,
+                    float* y, void* stream)
+{
+    if (m < 0 || m > INT32_MAX) return fail_msg(BTL_ERR_SHAPE, "row count out of range");
+    if (k < 64 || k % 64 || k > 65536) return failf(BTL_ERR_SHAPE, "k = %lld: need a multiple of 64 in [64, 65536]", (long long)k);
+    if (m == 0) return BTL_OK;
+    if (!h || !g || !y) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    if (!aligned16(h) || !aligned16(g) || !aligned16(y) || (delta && !aligned16(delta)) || (h_out && !aligned16(h_out)))
+        return fail_msg(BTL_ERR_LAYOUT, "h, delta, h_out, g and y must be 16-byte aligned");
+    const size_t rows = (size_t)m * (size_t)k * 4, row = (size_t)k * 4;
+    auto overlap = [](const void* a, size_t na, const void* b, size_t nb) {
+        return a && b && (const uint8_t*)a < (const uint8_t*)b + nb && (const uint8_t*)b < (const uint8_t*)a + na;
+    };
+    if (overlap(y, rows, h, rows) || overlap(y, rows, delta, rows) || overlap(y, rows, h_out, rows) ||
+        overlap(y, rows, g, row))
+        return fail_msg(BTL_ERR_LAYOUT, "y overlaps an input or h_out");
+    if (h_out && h_out != h && (overlap(h_out, rows, h, rows) || overlap(h_out, rows, delta, rows) ||
+                                overlap(h_out, rows, g, row)))
+        return fail_msg(BTL_ERR_LAYOUT, "h_out must be h itself or not overlap h, delta and g");
+    int dev;
+    int rc = btl::host::device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_rmsnorm_f32(h, delta, h_out, g, eps, m, k, y, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "rmsnorm kernel launch");
+    return BTL_OK;
+}
+
+int btl_dense_linear(const void* w, int wdtype, int64_t n, int64_t k, const float* x, int64_t m, float* y,
+                     void* stream)
+{
+    if (wdtype != BTL_F32 && wdtype != BTL_BF16) return failf(BTL_ERR_DTYPE, "weight dtype %d is not BTL_F32/BTL_BF16", wdtype);
+    if (n < 0 || m < 0 || m > 65535 || n > ((int64_t)1 << 40)) return fail_msg(BTL_ERR_SHAPE, "size out of range");
+    if (k < 4 || k % 4 || k > (1 << 28)) return failf(BTL_ERR_SHAPE, "k = %lld: need a positive multiple of 4", (long long)k);
+    if (m == 0 || n == 0) return BTL_OK;
+    if (!w || !x || !y) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    if (!aligned16(x) || ((uintptr_t)w & (wdtype == BTL_F32 ? 15u : 7u)))
+        return fail_msg(BTL_ERR_LAYOUT, "x must be 16-byte aligned, w 16-byte (f32) or 8-byte (bf16) aligned");
+    int dev;
+    int rc = btl::host::device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_dense_gemv(w, wdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, n, k, x, m, y,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "dense linear kernel launch");
+    return BTL_OK;
+}
+
 }  // extern "C"

@@ -13,6 +13,8 @@
  *                                            src/layers/attention.rs:149-224
  *   BitLlamaBlock::forward residual + norm2  src/model/block.rs:122-137
  *   BitLlama::forward_one embedding          src/model/llama.rs:208
+ *   RMSNorm::forward (final norm)            src/layers/rms_norm.rs:33-56
+ *   lm_head (dense candle_nn::Linear)        src/model/llama.rs:129-141, 255-265
  *   Llama::stream_completion greedy pick     src/model/llama.rs:509-515
  *
  * Conventions are those of bitlinear.h: int status (BTL_OK / BTL_ERR_*),
@@ -131,6 +133,29 @@ int btl_embedding(const void* table, int dtype, int64_t vocab, int64_t dim, cons
  */
 int btl_greedy_next(const float* logits, int64_t n, int32_t* next_id, int32_t* d_pos, int32_t* log,
                     int64_t log_len, void* stream);
+
+/*
+ * RMSNorm::forward (rms_norm.rs:33-56) into f32 rows: s = h + delta (delta may
+ * be NULL), y = s / sqrt(sum(s * s) * (f32)(1/k) + eps) * g, the sum a pairwise
+ * tree over the row in index order; h_out = s when h_out != NULL (h_out may be
+ * h itself).  h, delta, h_out, y [m, k] f32, g [k] f32, all 16-byte aligned;
+ * k % 64 == 0, 64 <= k <= 65536; y overlaps none of the others.  The input of a
+ * dense lm_head (btl_dense_linear).
+ */
+int btl_add_rmsnorm(const float* h, const float* delta, float* h_out, const float* g, float eps, int64_t m, int64_t k,
+                    float* y, void* stream);
+
+/*
+ * candle_nn::Linear::forward without a bias -- the reference's lm_head, a dense
+ * linear (llama.rs:129-141): y[m, n] = x[m, k] . w[n, k]^T in f32, w of dtype
+ * BTL_F32 (the reference's) or BTL_BF16 (widened exactly).  Fixed order: lane l
+ * of 64 folds the 4-element chunks l, l + 64, ... of a row into fma partial
+ * sums, then a butterfly over the lanes (oracle/bitllama_oracle.c restates it).
+ * k % 4 == 0; x 16-byte aligned, w 16-byte (f32) or 8-byte (bf16) aligned;
+ * m <= 65535.
+ */
+int btl_dense_linear(const void* w, int wdtype, int64_t n, int64_t k, const float* x, int64_t m, float* y,
+                     void* stream);
 
 /*
  * Residual connection fused ahead of RMSNorm and a BitLinear group

@@ -37,6 +37,9 @@
  *                      O[d] = sum_c w_c * o_c[d] (sequential over c), y = O / L.
  *                    exp is orc_expf (bitlinear_oracle.c).  tests/test_model_oracle.py
  *                    pins the result against a float64 softmax-attention.
+ *   orc_dense_linear candle_nn::Linear::forward without a bias (the dense lm_head of
+ *                    llama.rs:129-141) in f32 with the GPU kernel's fixed order
+ *                    (64 lane partial sums of fmas, then a butterfly; see below)
  *   orc_argmax       the greedy pick of Llama::stream_completion (llama.rs:509-515):
  *                    Iterator::max_by(partial_cmp) returns the LAST maximum
  *   orc_adaptive_reconstruct  AdaptiveBitLinear::load (adaptive_linear.rs:86-117): the
@@ -246,4 +249,45 @@ int orc_adaptive_forward_i8(const float* x, int64_t m, int64_t k, const uint8_t*
     free(acc);
     free(split);
     return 0;
+}
+
+/* candle_nn::Linear::forward without a bias (the lm_head, llama.rs:129-141):
+ * y[i][j] = sum_t x[i][t] * w[j][t] in f32, w f32 or bf16 (widened exactly).
+ * The reference's sum runs in candle's gemm order (not vendored); this fixes
+ * the order of the GPU kernel so the two agree bit for bit: 64 lanes, lane l
+ * takes the 4-element chunks c = l, l + 64, l + 128, ... (c < k / 4) and folds
+ * each chunk's elements in order into acc = fma(x, w, acc); then six butterfly
+ * steps acc_l = acc_l + acc_(l xor s), s = 32, 16, 8, 4, 2, 1 (every lane ends
+ * with the same value).  k % 4 == 0. */
+void orc_dense_linear(const float* x, int64_t m, int64_t k, const void* w, int wbf16, int64_t n, float* y)
+{
+    const int64_t nc = k / 4;
+    for (int64_t i = 0; i < m; ++i) {
+        const float* xr = x + i * k;
+        for (int64_t j = 0; j < n; ++j) {
+            float acc[64], nxt[64];
+            for (int l = 0; l < 64; ++l) {
+                float a = 0.0f;
+                for (int64_t c = l; c < nc; c += 64) {
+                    for (int e = 0; e < 4; ++e) {
+                        const int64_t t = 4 * c + e;
+                        float wv;
+                        if (wbf16) {
+                            const uint32_t u = (uint32_t)((const uint16_t*)w)[j * k + t] << 16;
+                            memcpy(&wv, &u, 4);
+                        } else {
+                            wv = ((const float*)w)[j * k + t];
+                        }
+                        a = fmaf(xr[t], wv, a);
+                    }
+                }
+                acc[l] = a;
+            }
+            for (int s = 32; s >= 1; s >>= 1) {
+                for (int l = 0; l < 64; ++l) nxt[l] = acc[l] + acc[l ^ s];
+                memcpy(acc, nxt, sizeof(acc));
+            }
+            y[i * n + j] = acc[0];
+        }
+    }
 }

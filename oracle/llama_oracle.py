@@ -23,7 +23,9 @@ class OracleLlama:
     """cfg: an object with hidden, n_layers, n_heads, n_kv_heads, head_dim,
     intermediate, vocab, rope_theta, max_seq, eps.  w: host weights
       embed [vocab, hidden] f32, norm_f [hidden] f32,
-      lm_head (bytes, scale), layers: [{norm1, norm2, q, k, v, o, gate, up, down}]
+      lm_head (bytes, scale) -- or a dense [vocab, hidden] f32 array / uint16 array
+      of bf16 bits (the reference's candle_nn::Linear), layers: [{norm1, norm2, q,
+      k, v, o, gate, up, down}]
     with the linears as (packed bytes uint8, scale) pairs."""
 
     def __init__(self, cfg, w):
@@ -64,7 +66,12 @@ class OracleLlama:
             u = self._lin(xn2, L["up"], c.intermediate)
             d = self._lin(orc.swiglu(g, u), L["down"], c.hidden)
             h = (h + d).astype(np.float32)
-        logits = self._lin(orc.rmsnorm(h, w["norm_f"], c.eps), w["lm_head"], c.vocab)[0]
+        xf = orc.rmsnorm(h, w["norm_f"], c.eps)
+        head = w["lm_head"]
+        if isinstance(head, np.ndarray):  # dense f32 / bf16-bits [vocab, hidden] (llama.rs:129-141)
+            logits = orc.dense_linear(xf, head)[0]
+        else:
+            logits = self._lin(xf, head, c.vocab)[0]
         self.pos += 1
         return logits
 

@@ -46,6 +46,7 @@ def _load():
         "orc_q8_dequant": (None, [vp, i64, f32, vp]),
         "orc_attn_decode": (None, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp]),
         "orc_argmax": (i64, [vp, i64]),
+        "orc_dense_linear": (None, [vp, i64, i64, vp, i32, i64, vp]),
         "orc_adaptive_reconstruct": (None, [vp, vp, i64, i64, i64, vp]),
         "orc_adaptive_split": (None, [vp, i64, i64, i64, vp]),
         "orc_adaptive_forward_i8": (i32, [vp, i64, i64, vp, vp, i64, i64, vp]),
@@ -265,6 +266,21 @@ def attn_decode(q, kq, ks, vq, vs, n_heads, T):
     out = np.zeros((n_heads * hd,), dtype=np.float32)
     lib.orc_attn_decode(_p(q), _p(kq), _p(ks), _p(vq), _p(vs), n_heads, nkv, hd, max_seq, T, _p(out))
     return out
+
+
+def dense_linear(x, w):
+    """candle_nn::Linear::forward without a bias (the dense lm_head, llama.rs:129-141)
+    in the GPU kernel's fixed order.  x [m, k] f32; w [n, k] f32, or uint16 holding
+    bf16 bits.  -> y [m, n] f32."""
+    x = _f32(x)
+    m, k = x.shape
+    bf = w.dtype == np.uint16
+    w = np.ascontiguousarray(w, np.uint16 if bf else np.float32)
+    n = w.shape[0]
+    assert w.shape[1] == k and k % 4 == 0
+    y = np.zeros((m, n), dtype=np.float32)
+    lib.orc_dense_linear(_p(x), m, k, _p(w), int(bf), n, _p(y))
+    return y
 
 
 def argmax(x):

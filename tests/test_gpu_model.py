@@ -615,3 +615,174 @@ def test_decoder_generate_matches_oracle(use_graph):
         torch.cuda.synchronize()
         again = gm.generate(prompt, 24, use_graph=True)
         assert np.array_equal(again, exp)
+
+
+class Llama3Wide(TinyCfg):
+    # Llama-3-8B's widths (hidden 4096, 32 / 8 heads of 128, intermediate 14336,
+    # vocab 128256, theta 500000), two layers
+    hidden, n_layers, n_heads, n_kv_heads, head_dim = 4096, 2, 32, 8, 128
+    intermediate, vocab, rope_theta, max_seq, eps = 14336, 128256, 500000.0, 256, 1e-5
+
+
+def _random_codes(rng, n, k):
+    # packed ternary rows of valid codes (00 -> 0, 01 -> +1, 10 -> -1; the
+    # unused 11 folded to 00) and a scale, as PackedTensor holds them
+    b = rng.integers(0, 256, n * k // 4, dtype=np.uint8)
+    m = b & (b >> 1) & 0x55
+    b &= ~(m | (m << 1)).astype(np.uint8)
+    return b, float(rng.uniform(0.005, 0.02))
+
+
+class _RowsOnDevice:
+    # the oracle's view of a device embedding table: the rows it asks for
+    def __init__(self, t):
+        self.t = t
+
+    def __getitem__(self, i):
+        return self.t[int(i)].float().cpu().numpy()
+
+
+def test_decoder_llama3_width_matches_oracle():
+    # full Llama-3-8B widths, two layers: five tokens one at a time (logits bit
+    # for bit each step, then the KV caches), then a greedy continuation from a
+    # two-token prefill (the batched path) replayed from a HIP graph
+    cfg = Llama3Wide()
+    rng = np.random.default_rng(11)
+    kvd, qd = cfg.n_kv_heads * cfg.head_dim, cfg.n_heads * cfg.head_dim
+
+    def norm(n):
+        return (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+
+    layers = [{"norm1": norm(cfg.hidden), "norm2": norm(cfg.hidden),
+               "q": _random_codes(rng, qd, cfg.hidden), "k": _random_codes(rng, kvd, cfg.hidden),
+               "v": _random_codes(rng, kvd, cfg.hidden), "o": _random_codes(rng, cfg.hidden, qd),
+               "gate": _random_codes(rng, cfg.intermediate, cfg.hidden),
+               "up": _random_codes(rng, cfg.intermediate, cfg.hidden),
+               "down": _random_codes(rng, cfg.hidden, cfg.intermediate)} for _ in range(cfg.n_layers)]
+    g = torch.Generator(device=DEV)
+    g.manual_seed(5)
+    embed = torch.randn((cfg.vocab, cfg.hidden), device=DEV, generator=g)
+    w = {"embed": _RowsOnDevice(embed), "norm_f": norm(cfg.hidden),
+         "lm_head": _random_codes(rng, cfg.vocab, cfg.hidden), "layers": layers}
+
+    def lin(pk, n, k):
+        return bl.PackedTensor(torch.from_numpy(pk[0]).to(DEV), pk[1], (n, k), DEV)
+
+    gl = [{"norm1": torch.from_numpy(L["norm1"]).to(DEV), "norm2": torch.from_numpy(L["norm2"]).to(DEV),
+           "q": lin(L["q"], qd, cfg.hidden), "k": lin(L["k"], kvd, cfg.hidden), "v": lin(L["v"], kvd, cfg.hidden),
+           "o": lin(L["o"], cfg.hidden, qd), "gate": lin(L["gate"], cfg.intermediate, cfg.hidden),
+           "up": lin(L["up"], cfg.intermediate, cfg.hidden), "down": lin(L["down"], cfg.hidden, cfg.intermediate)}
+          for L in layers]
+    gw = {"embed": embed, "norm_f": torch.from_numpy(w["norm_f"]).to(DEV),
+          "lm_head": lin(w["lm_head"], cfg.vocab, cfg.hidden), "layers": gl}
+    gm = BitLlamaHip(cfg, gw, DEV, max_rows=16)
+    om = OracleLlama(cfg, w)
+    toks = [int(t) for t in rng.integers(0, cfg.vocab, 5)]
+    for i, t in enumerate(toks):
+        print("llama3-width forward_one", i, flush=True)
+        assert_same(gm.forward_one(t), om.forward_one(t), "step %d logits" % i)
+    for li in range(cfg.n_layers):
+        c = gm.caches[li]
+        assert np.array_equal(c.k.cpu().numpy()[:, :5], om.caches[li]["kq"][:, :5])
+        assert np.array_equal(c.v.cpu().numpy()[:, :5], om.caches[li]["vq"][:, :5])
+        assert_same(c.k_scale.cpu().numpy()[:, :5], om.caches[li]["ks"][:, :5], "k scales")
+    print("llama3-width generate", flush=True)
+    gm2 = BitLlamaHip(cfg, gw, DEV, max_rows=16)
+    got = gm2.generate(toks[:2], 3, use_graph=True)
+    exp = OracleLlama(cfg, w).generate(toks[:2], 3)
+    assert np.array_equal(got, exp), (got, exp)
+
+
+@pytest.mark.parametrize("m,k", [(1, 64), (1, 4096), (3, 4160), (2, 65536)])
+@pytest.mark.parametrize("mode", ["plain", "delta", "delta_out", "inplace"])
+def test_add_rmsnorm_rows(m, k, mode):
+    # RMSNorm into f32 rows, the sum of squares a pairwise tree over the row
+    print("add_rmsnorm", m, k, mode, flush=True)
+    rng = np.random.default_rng(k + m)
+    h = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    d = rng.standard_normal((m, k)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    ht, dt, gt = (torch.from_numpy(a).to(DEV) for a in (h, d, g))
+    y = torch.full((m, k), 5.0, device=DEV)
+    ho = torch.full((m, k), 5.0, device=DEV)
+    delta = dt.data_ptr() if mode != "plain" else None
+    hout = {"plain": None, "delta": None, "delta_out": ho.data_ptr(), "inplace": ht.data_ptr()}[mode]
+    bl.check(bl.lib.btl_add_rmsnorm(ht.data_ptr(), delta, hout, gt.data_ptr(), 1e-5, m, k, y.data_ptr(), stream()))
+    s = h + d if mode != "plain" else h
+    assert_same(y, orc.rmsnorm(s, g, 1e-5), "rmsnorm rows")
+    if mode == "delta_out":
+        assert_same(ho, s, "h_out")
+    if mode == "inplace":
+        assert_same(ht, s, "h in place")
+
+
+def test_add_rmsnorm_rejects_overlap():
+    h = torch.zeros((2, 256), device=DEV)
+    g = torch.ones(256, device=DEV)
+    assert bl.lib.btl_add_rmsnorm(h.data_ptr(), None, None, g.data_ptr(), 1e-5, 2, 256, h.data_ptr(),
+                                  stream()) == bl.BTL_ERR_LAYOUT
+    assert bl.lib.btl_add_rmsnorm(h.data_ptr(), None, None, g.data_ptr(), 1e-5, 2, 100, h.data_ptr(),
+                                  stream()) == bl.BTL_ERR_SHAPE
+
+
+@pytest.mark.parametrize("n,k,m,dt", [(1000, 4096, 1, "f32"), (1000, 4096, 2, "bf16"), (333, 520, 3, "f32"),
+                                      (77, 4100, 1, "bf16"), (128256, 4096, 1, "f32")])
+def test_dense_linear(n, k, m, dt):
+    # the dense lm_head: f32 sums in the fixed lane order (registers for k = 4096,
+    # the generic chunk loop otherwise), bit for bit with the oracle
+    print("dense_linear", n, k, m, dt, flush=True)
+    rng = np.random.default_rng(n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if dt == "bf16":
+        wt = torch.from_numpy(w).to(DEV).to(torch.bfloat16)
+        wh = wt.view(torch.int16).cpu().numpy().view(np.uint16)
+        code = bl.BTL_BF16
+    else:
+        wt = torch.from_numpy(w).to(DEV)
+        wh = w
+        code = bl.BTL_F32
+    xt = torch.from_numpy(x).to(DEV)
+    y = torch.full((m, n), 9.0, device=DEV)
+    bl.check(bl.lib.btl_dense_linear(wt.data_ptr(), code, n, k, xt.data_ptr(), m, y.data_ptr(), stream()))
+    exp = orc.dense_linear(x, wh)
+    assert_same(y, exp, "dense linear")
+    ref = x.astype(np.float64) @ (wt.float().cpu().numpy().astype(np.float64)).T
+    assert np.abs(y.cpu().numpy() - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+
+
+def test_decoder_dense_head_matches_oracle():
+    # the reference's dense lm_head (f32 and bf16 weights) after the ternary blocks
+    cfg = TinyA()
+    w = tiny_weights(cfg, seed=8)
+    rng = np.random.default_rng(4)
+    for dt in (torch.float32, torch.bfloat16):
+        head = torch.from_numpy((rng.standard_normal((cfg.vocab, cfg.hidden)) * 0.05).astype(np.float32)).to(DEV)
+        head = head.to(dt).contiguous()
+        gm = gpu_model(cfg, w)
+        gm.w["lm_head"] = head
+        gm2 = BitLlamaHip(cfg, dict(gm.w), DEV)
+        wo = dict(w)
+        wo["lm_head"] = head.cpu().numpy() if dt == torch.float32 else head.view(torch.int16).cpu().numpy().view(np.uint16)
+        om = OracleLlama(cfg, wo)
+        for i, t in enumerate(rng.integers(0, cfg.vocab, 6)):
+            assert_same(gm2.forward_one(int(t)), om.forward_one(int(t)), "%s step %d" % (dt, i))
+        got = BitLlamaHip(cfg, dict(gm.w), DEV).generate([3, 9, 27], 8, use_graph=True)
+        exp = OracleLlama(cfg, wo).generate([3, 9, 27], 8)
+        assert np.array_equal(got, exp), (dt, got, exp)
+
+
+def test_dense_linear_order_cases():
+    # rows where only the fixed lane order keeps the small term (see the oracle
+    # tests): the kernel must agree with it
+    k, B, t = 512, 2.0 ** 25, 2.0 ** -30
+    w = np.zeros((3, k), np.float32)
+    w[0, [0, 256, 4]] = [B, -B, t]
+    w[1, [0, 128, 4]] = [B, -B, t]
+    w[2, [0, 1, 2]] = [B, t, -B]
+    x = np.ones((1, k), np.float32)
+    y = torch.zeros((1, 3), device=DEV)
+    wt, xt = torch.from_numpy(w).to(DEV), torch.from_numpy(x).to(DEV)
+    bl.check(bl.lib.btl_dense_linear(wt.data_ptr(), bl.BTL_F32, 3, k, xt.data_ptr(), 1, y.data_ptr(), stream()))
+    assert y.cpu().numpy()[0].tolist() == [t, t, 0.0]
+    assert_same(y, orc.dense_linear(x, w), "order cases")

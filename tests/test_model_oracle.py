@@ -26,6 +26,13 @@ What pins each function (reference = imonoonoko/Bit-TTT-Engine, crates/rust_engi
                     The reference's own summation order (candle gemm) is not vendored:
                     its last ulps are parity unpinned (tolerance above).
   orc_argmax        Iterator::max_by semantics: the last of equal maxima.
+  orc_dense_linear  candle_nn::Linear::forward (the dense lm_head, llama.rs:129-141):
+                    exact integer-valued products and sums (no dropped term, no
+                    transposed operand: rectangular w with distinct rows), float64
+                    matmul within 1e-5 relative, bf16 weights = their exact f32
+                    widening, and the order itself: a row whose lane-0 partial sum
+                    absorbs a small term only in the fixed order.  The reference's
+                    gemm order is not vendored: its last ulps are parity unpinned.
   OracleLlama       composition only; pinned by the functions above and by
                     test_oracle.py (BitLinear, RMSNorm, SwiGLU); checked here for the
                     causal invariant that token t's logits do not depend on later tokens.
@@ -252,3 +259,44 @@ def test_oracle_llama_is_causal_and_deterministic():
     g2 = OracleLlama(cfg, w).generate(prompt, 5)
     assert np.array_equal(g1, g2) and g1.shape == (5,)
     assert np.all((g1 >= 0) & (g1 < cfg.vocab))
+
+
+def test_dense_linear_exact_small_integers():
+    # products and partial sums are small integers: every order gives the exact dot
+    rng = np.random.default_rng(3)
+    for m, n, k in [(1, 1, 4), (2, 5, 12), (3, 7, 520)]:
+        x = rng.integers(-8, 9, (m, k)).astype(np.float32)
+        w = rng.integers(-8, 9, (n, k)).astype(np.float32)
+        y = orc.dense_linear(x, w)
+        assert np.array_equal(y, (x.astype(np.int64) @ w.astype(np.int64).T).astype(np.float32))
+
+
+def test_dense_linear_float64_and_bf16_widening():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 4096)).astype(np.float32)
+    w = (rng.standard_normal((33, 4096)) * 0.02).astype(np.float32)
+    y = orc.dense_linear(x, w)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    bits = (w.view(np.uint32) >> 16).astype(np.uint16)  # truncated to bf16 bits
+    wide = (bits.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(orc.dense_linear(x, bits), orc.dense_linear(x, wide))
+
+
+def test_dense_linear_lane_order():
+    # B = 2^25 absorbs t = 2^-30 (t is far below half an ulp of B).  k = 512: lane 0
+    # holds chunks 0 and 64 (elements 0-3, 256-259), lane 1 chunk 1 (elements 4-7),
+    # lane 32 chunk 32 (elements 128-131).  A fold over k in index order gives
+    # (B + t) - B = 0 in both cases below; the fixed order keeps t.
+    k, B, t = 512, 2.0 ** 25, 2.0 ** -30
+    x = np.ones((1, k), np.float32)
+    # chunk-to-lane map: B and -B meet inside lane 0, t sits in lane 1
+    w = np.zeros((1, k), np.float32)
+    w[0, 0], w[0, 256], w[0, 4] = B, -B, t
+    assert orc.dense_linear(x, w)[0, 0] == np.float32(t)
+    # butterfly, xor 32 first: lane 0 (B) meets lane 32 (-B) before lane 1 (t)
+    w = np.zeros((1, k), np.float32)
+    w[0, 0], w[0, 128], w[0, 4] = B, -B, t
+    assert orc.dense_linear(x, w)[0, 0] == np.float32(t)
+    # and the fold that the order replaces loses it
+    assert np.float32(np.float32(np.float32(B) + np.float32(t)) - np.float32(B)) == 0.0
