@@ -68,7 +68,7 @@ class Call:
     """A pre-bound C-ABI call (pointers resolved once, so graph capture and timing
     loops pay no Python argument handling)."""
 
-    def __init__(self, layers, x, outs):
+    def __init__(self, layers, x, outs, mode=None):
         import ctypes
         self.cs = [l.as_c() for l in layers]
         self.n = len(layers)
@@ -76,12 +76,15 @@ class Call:
         self.ys = (ctypes.c_void_p * self.n)(*[o.data_ptr() for o in outs])
         self.x = x
         self.m, self.k = x.shape
+        self.xdt = bl.BTL_BF16 if x.dtype == torch.bfloat16 else bl.BTL_F32
+        self.ydt = bl.BTL_BF16 if outs[0].dtype == torch.bfloat16 else bl.BTL_F32
+        self.mode = bl.BTL_ACT_I8 if mode is None else mode
         self.bytes = sum(l.data.numel() for l in layers) + x.numel() * x.element_size() + sum(
             o.numel() * o.element_size() for o in outs)
 
     def __call__(self, stream):
-        bl.check(bl.lib.btl_linear_group(self.arr, self.ys, self.n, self.x.data_ptr(), bl.BTL_BF16,
-                                         self.m, self.k, bl.BTL_BF16, None, 0, stream))
+        bl.check(bl.lib.btl_linear_group_mode(self.arr, self.ys, self.n, self.x.data_ptr(), self.xdt,
+                                              self.m, self.k, self.ydt, self.mode, None, 0, stream))
 
 
 class OpCall:
@@ -244,6 +247,7 @@ def run_decode(args):
         b = calls[name][0].bytes
         kern[name] = {"us": round(us, 2), "bytes": b, "GB_s": round(b / us / 1e3, 1),
                       "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+    f32_ref = run_decode_f32_ref(layers, gen, dev, args)
     dom = kern["gate_up"]
     result = {
         "metric": METRIC, "value": round(1000.0 / ms, 2), "unit": "tok/s", "n_gpus": 1,
@@ -266,6 +270,7 @@ def run_decode(args):
                                        "factor + WRITE_SIZE, bytes per launch)",
                      "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"]},
         "kernels": kern,
+        "f32_ref": f32_ref,
     }
     if args.prefill:
         result["prefill"] = run_prefill(layers, gen, dev, args)
@@ -289,6 +294,63 @@ def run_decode(args):
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
+
+
+def _graph_us(fns, reps, cap):
+    """us per replay of one HIP graph holding fns (each fn(stream)) in order."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            s = torch.cuda.current_stream().cuda_stream
+            for fn in fns:
+                fn(s)
+    torch.cuda.synchronize()
+    g.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return 1000.0 * e0.elapsed_time(e1) / reps
+
+
+def run_decode_f32_ref(layers, gen, dev, args):
+    """The cfg2 step in the reference's own arithmetic (BTL_ACT_F32_REF: cpu.rs's
+    fp32 semantics and 8-lane summation order, bit for bit), f32 in and out as the
+    reference's BitLinearCpu takes them: q|k|v and gate|up through
+    btl_linear_group_mode, o and down single, 32 layers in one HIP graph."""
+    f32 = dict(dtype=torch.float32, device=dev)
+    calls = {"qkv": [], "o": [], "gate_up": [], "down": []}
+    for L in layers:
+        xq, xo, xg, xd = (torch.randn((1, k), generator=gen, **f32) for k in (HIDDEN, HIDDEN, HIDDEN, INTER))
+        calls["qkv"].append(Call([L["q"], L["k"], L["v"]], xq,
+                                 [torch.empty((1, HIDDEN), **f32), torch.empty((1, KV), **f32),
+                                  torch.empty((1, KV), **f32)], mode=bl.BTL_ACT_F32_REF))
+        calls["o"].append(Call([L["o"]], xo, [torch.empty((1, HIDDEN), **f32)], mode=bl.BTL_ACT_F32_REF))
+        calls["gate_up"].append(Call([L["gate"], L["up"]], xg,
+                                     [torch.empty((1, INTER), **f32), torch.empty((1, INTER), **f32)],
+                                     mode=bl.BTL_ACT_F32_REF))
+        calls["down"].append(Call([L["down"]], xd, [torch.empty((1, HIDDEN), **f32)], mode=bl.BTL_ACT_F32_REF))
+    order = [calls[c][l] for l in range(LAYERS) for c in ("qkv", "o", "gate_up", "down")]
+    step_bytes = sum(c.bytes for c in order)
+    cap = torch.cuda.Stream()
+    for c in order:
+        c(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    us = _graph_us(order, 10, cap)
+    kern = {}
+    for name in ("qkv", "o", "gate_up", "down"):
+        kus = _graph_us(calls[name], 10, cap) / LAYERS
+        b = calls[name][0].bytes
+        kern[name] = {"us": round(kus, 2), "bytes": b, "GB_s": round(b / kus / 1e3, 1),
+                      "frac_hbm": round(b / kus / 1e3 / HBM_PEAK_GBS, 3)}
+    print("bench: cfg2 in f32_ref mode %.4f ms/step" % (us / 1000.0), file=sys.stderr, flush=True)
+    return {"workload": "cfg2 in the reference's arithmetic (BTL_ACT_F32_REF, cpu.rs order bit for bit): "
+                        "M=1, 32 layers x {q|k|v grouped, o, gate|up grouped, down}, f32 in/out, HIP graph",
+            "ms_per_step": round(us / 1000.0, 4), "tok_s": round(1e6 / us, 1), "bytes_per_step": step_bytes,
+            "step_GB_s": round(step_bytes / us / 1e3, 1),
+            "step_frac_hbm": round(step_bytes / us / 1e3 / HBM_PEAK_GBS, 3), "kernels": kern}
 
 
 def run_prefill(layers, gen, dev, args):
@@ -371,6 +433,7 @@ def run_prefill(layers, gen, dev, args):
                                        "the L2s; the 8 XCDs each fetch the weights once)",
                      "algorithmic_ops": dom["ops"], "avg_us": dom["us"]},
         "kernels": kern,
+        "f32_ref": f32_ref,
     }
 
 

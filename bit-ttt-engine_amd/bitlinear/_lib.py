@@ -31,14 +31,15 @@ EXPORTS = (
     "btl_check_faults", "btl_packed_bytes",
     "btl_pack_host", "btl_unpack_host", "btl_pack_device", "btl_pack_workspace_bytes", "btl_unpack_device",
     "btl_quantize_act", "btl_linear", "btl_linear_noalloc",
-    "btl_linear_i8", "btl_linear_group", "btl_quantize_act_op", "btl_linear_i8_op",
+    "btl_linear_i8", "btl_linear_group", "btl_linear_group_mode", "btl_quantize_act_op", "btl_linear_i8_op",
     "btl_rmsnorm_linear_group", "btl_swiglu_linear_group",
     "btl_workspace_bytes", "btl_workspace_clear",
     "btl_adaptive_split", "btl_adaptive_reconstruct", "btl_adaptive_linear", "btl_adaptive_workspace_bytes",
     # include/bitllama.h
     "btl_rope_table", "btl_rope_kv_append", "btl_attention_workspace_bytes", "btl_attention",
     "btl_rope_append_attention",
-    "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm", "btl_dense_linear", "btl_add_rmsnorm_linear_group", "btl_add_rmsnorm_swiglu",
+    "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm", "btl_dense_linear",
+    "btl_add_rmsnorm_linear_group", "btl_add_rmsnorm_swiglu",
     "btl_add_rmsnorm_swiglu_workspace_bytes", "btl_linear_residual",
     "btl_stream_create", "btl_stream_stage_words", "btl_stream_run", "btl_stream_destroy",
 )
@@ -95,6 +96,7 @@ def _load():
         "btl_linear_noalloc": (i32, [P(BtlPacked), vp, i32, i64, i64, vp, i32, i32, vp, vp]),
         "btl_linear_i8": (i32, [P(BtlPacked), vp, vp, i64, i64, vp, i32, vp, vp, sz, vp]),
         "btl_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, i32, i64, i64, i32, vp, sz, vp]),
+        "btl_linear_group_mode": (i32, [P(P(BtlPacked)), P(vp), i32, vp, i32, i64, i64, i32, i32, vp, sz, vp]),
         "btl_quantize_act_op": (i32, [vp, i32, i64, i64, vp, vp, vp]),
         "btl_linear_i8_op": (i32, [P(P(BtlPacked)), P(vp), P(vp), i32, vp, vp, i64, i64, i32, vp]),
         "btl_rmsnorm_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, i32, vp, f32, i64, i64, i32, vp, sz,

@@ -185,8 +185,11 @@ def swiglu_linear_group(weights, gate, up, out_dtype=None, workspace=None, outpu
     return outputs
 
 
-def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None):
-    """Several layers reading the same input in one launch (q|k|v, w1|w3)."""
+def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None, mode="i8"):
+    """Several layers reading the same input in one launch (q|k|v, w1|w3), in
+    W1.58-A8 (mode "i8") or the reference's fp32 order (mode "f32_ref")."""
+    if mode not in _MODES:
+        raise BitLinearError(BTL_ERR_DTYPE, "unknown mode %r" % (mode,))
     _on_gpu(x, "input")
     m, k = x.shape
     out_dtype = out_dtype or x.dtype
@@ -196,8 +199,8 @@ def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None):
     arr = (ctypes.POINTER(BtlPacked) * len(cs))(*[ctypes.pointer(c) for c in cs])
     ys = (ctypes.c_void_p * len(cs))(*[o.data_ptr() for o in outputs])
     wsp, wsn = _ws_args(workspace)
-    check(lib.btl_linear_group(arr, ys, len(cs), x.data_ptr(), _dtype_code(x, "input"), m, k,
-                               _dtype_code(outputs[0], "output"), wsp, wsn, _stream(x.device)))
+    check(lib.btl_linear_group_mode(arr, ys, len(cs), x.data_ptr(), _dtype_code(x, "input"), m, k,
+                                    _dtype_code(outputs[0], "output"), _MODES[mode], wsp, wsn, _stream(x.device)))
     return outputs
 
 

@@ -869,6 +869,40 @@ int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, co
                   ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32, ws, ws_bytes, (hipStream_t)stream);
 }
 
+int btl_linear_group_mode(const btl_packed_t* const* w, void* const* y, int count, const void* x, int xdtype,
+                          int64_t m, int64_t k, int ydtype, int mode, void* ws, size_t ws_bytes, void* stream)
+{
+    if (mode == BTL_ACT_I8) return btl_linear_group(w, y, count, x, xdtype, m, k, ydtype, ws, ws_bytes, stream);
+    if (mode != BTL_ACT_F32_REF) return fail(BTL_ERR_DTYPE, "unknown mode %d", mode);
+    if (count < 1 || count > btl::kMaxGroup) return fail(BTL_ERR_ARG, "count %d not in 1..%d", count, btl::kMaxGroup);
+    if (!w || !y) return fail(BTL_ERR_ARG, "null layer array");
+    int rc;
+    if ((rc = check_dtype(xdtype, "input")) || (rc = check_dtype(ydtype, "output"))) return rc;
+    const uint8_t* wd[btl::kMaxGroup];
+    int64_t n[btl::kMaxGroup];
+    float sc[btl::kMaxGroup];
+    void* yy[btl::kMaxGroup];
+    int64_t nsum = 0;
+    for (int i = 0; i < count; ++i) {
+        if ((rc = check_packed(w[i], m, k))) return rc;
+        if (!y[i] && m > 0 && w[i]->n > 0) return fail(BTL_ERR_LAYOUT, "null output %d", i);
+        wd[i] = w[i]->data;
+        n[i] = w[i]->n;
+        sc[i] = w[i]->scale;
+        yy[i] = y[i];
+        nsum += w[i]->n;
+    }
+    if (m == 0 || nsum == 0) return BTL_OK;
+    if (k > 0 && !x) return fail(BTL_ERR_LAYOUT, "null input");
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    const hipError_t e = btl::launch_ref_f32_group(x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, m, k, wd, n, sc,
+                                                   yy, count, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32,
+                                                   (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "reference-order kernel launch");
+    return BTL_OK;
+}
+
 int btl_quantize_act_op(const void* x, int xdtype, int64_t m, int64_t k, int8_t* xq, float* xscale,
                         void* stream)
 {

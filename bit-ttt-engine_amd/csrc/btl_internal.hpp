@@ -186,6 +186,19 @@ hipError_t launch_quant_act(const void* x, int xkind, int64_t m, int64_t k, int8
 
 hipError_t launch_ref_f32(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* w,
                           int64_t n, float scale, void* y, int ykind, hipStream_t st);
+// several layers over the same x (count <= kMaxGroup): one launch when the
+// LDS form applies, else one launch per layer
+struct RefGroup {
+    const uint8_t* w[kMaxGroup];
+    void* y[kMaxGroup];
+    float scale[kMaxGroup];
+    int64_t n[kMaxGroup];
+    int wg_begin[kMaxGroup + 1];  // 32-output workgroups of each layer
+    int count;
+};
+hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* const* w,
+                                const int64_t* n, const float* scale, void* const* y, int count, int ykind,
+                                hipStream_t st);
 
 hipError_t launch_generic_i8(const int8_t* q, const float* xs, int64_t m, int64_t k,
                              const uint8_t* w, int64_t n, float sw, void* y, int ykind,

@@ -1984,17 +1984,27 @@ __global__ __launch_bounds__(256) void k_ref_f32(const void* x, int64_t m, int64
 // weight 8 j' + b, j' = 8 q + e, sits at bit 16 (e % 2) + 2 b of word e / 2 of
 // the q-th 16 bytes.  The FMA order per lane (increasing j') and the lane sum
 // are those of k_ref_f32 (no tail: 32 divides k).
+//
+// Grouped (several layers reading the same x, btl_linear_group_mode): the
+// workgroups of layer i are [g.wg_begin[i], g.wg_begin[i + 1]) of the grid's x.
 template <int XK, int YK>
-__global__ __launch_bounds__(256) void k_ref_f32_lds(const void* x, int64_t k, const uint8_t* w, int64_t n,
-                                                     float scale, void* y)
+__global__ __launch_bounds__(256) void k_ref_f32_lds(const void* x, int64_t k, RefGroup g)
 {
     extern __shared__ __align__(16) float sxl[];
     const int K = (int)k, S = (K >> 3) + 4;
     const int64_t row = blockIdx.y;
     const int tid = threadIdx.x;
+    int li = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i)
+        if (i < g.count && (int)blockIdx.x >= g.wg_begin[i]) li = i;
+    const uint8_t* w = g.w[li];
+    const int64_t n = g.n[li];
+    const float scale = g.scale[li];
+    void* y = g.y[li];
     for (int i = tid; i < K; i += 256) sxl[(i & 7) * S + (i >> 3)] = load_x<XK>(x, row * k + i);
     __syncthreads();
-    const int64_t col = (int64_t)blockIdx.x * 32 + (tid >> 3);
+    const int64_t col = (int64_t)((int)blockIdx.x - g.wg_begin[li]) * 32 + (tid >> 3);
     const int b = tid & 7;
     const bool active = col < n;
     const uint4* wr = (const uint4*)(w + (active ? col : 0) * (k >> 2));
@@ -2027,26 +2037,59 @@ __global__ __launch_bounds__(256) void k_ref_f32_lds(const void* x, int64_t k, c
     store_y<YK>(y, row * n + col, __fmul_rn(sum, scale));
 }
 
+hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* const* w,
+                                const int64_t* n, const float* scale, void* const* y, int count, int ykind,
+                                hipStream_t st)
+{
+    if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
+    bool lds_ok = k % 64 == 0 && k <= 16384 && m <= 65535;
+    int64_t wgs = 0;
+    for (int i = 0; i < count; ++i) {
+        lds_ok = lds_ok && ((uintptr_t)w[i] & 15u) == 0;
+        wgs += (n[i] + 31) / 32;
+    }
+    if (m <= 0 || wgs == 0) return hipSuccess;
+    if (!lds_ok || wgs > INT32_MAX) {
+        for (int i = 0; i < count; ++i) {
+            const hipError_t e = launch_ref_f32(x, xkind, m, k, w[i], n[i], scale[i], y[i], ykind, st);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    RefGroup g{};
+    g.count = count;
+    int b = 0;
+    for (int i = 0; i < count; ++i) {
+        g.w[i] = w[i];
+        g.y[i] = y[i];
+        g.scale[i] = scale[i];
+        g.n[i] = n[i];
+        g.wg_begin[i] = b;
+        b += (int)((n[i] + 31) / 32);
+    }
+    g.wg_begin[count] = b;
+    const dim3 grid((unsigned)b, (unsigned)m);
+    const size_t lds = (size_t)8 * ((k >> 3) + 4) * 4;
+#define BTL_REF_LDS(XKV, YKV)                                                                   \
+    if (xkind == XKV && ykind == YKV) {                                                         \
+        hipLaunchKernelGGL((k_ref_f32_lds<XKV, YKV>), grid, dim3(256), lds, st, x, k, g);      \
+        return hipGetLastError();                                                               \
+    }
+    BTL_REF_LDS(XK_F32, YK_F32)
+    BTL_REF_LDS(XK_F32, YK_BF16)
+    BTL_REF_LDS(XK_BF16, YK_F32)
+    BTL_REF_LDS(XK_BF16, YK_BF16)
+#undef BTL_REF_LDS
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_ref_f32(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* w,
                           int64_t n, float scale, void* y, int ykind, hipStream_t st)
 {
     const int64_t threads = m * n * 8;
     if (threads <= 0) return hipSuccess;
-    if (k % 64 == 0 && k <= 16384 && ((uintptr_t)w & 15u) == 0 && m <= 65535 && (n + 31) / 32 <= INT32_MAX) {
-        const dim3 grid((unsigned)((n + 31) / 32), (unsigned)m);
-        const size_t lds = (size_t)8 * ((k >> 3) + 4) * 4;
-#define BTL_REF_LDS(XKV, YKV)                                                                               \
-        if (xkind == XKV && ykind == YKV) {                                                                 \
-            hipLaunchKernelGGL((k_ref_f32_lds<XKV, YKV>), grid, dim3(256), lds, st, x, k, w, n, scale, y); \
-            return hipGetLastError();                                                                       \
-        }
-        BTL_REF_LDS(XK_F32, YK_F32)
-        BTL_REF_LDS(XK_F32, YK_BF16)
-        BTL_REF_LDS(XK_BF16, YK_F32)
-        BTL_REF_LDS(XK_BF16, YK_BF16)
-#undef BTL_REF_LDS
-        return hipErrorInvalidValue;
-    }
+    if (k % 64 == 0 && k <= 16384 && ((uintptr_t)w & 15u) == 0 && m <= 65535 && (n + 31) / 32 <= INT32_MAX)
+        return launch_ref_f32_group(x, xkind, m, k, &w, &n, &scale, &y, 1, ykind, st);
     dim3 grid((unsigned)((threads + 255) / 256));
 #define BTL_REF_CASE(XKV, YKV)                                                                  \
     if (xkind == XKV && ykind == YKV) {                                                         \

@@ -226,6 +226,17 @@ int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, co
                      void* stream);
 
 /*
+ * btl_linear_group in either arithmetic mode: BTL_ACT_I8 is btl_linear_group;
+ * BTL_ACT_F32_REF runs every layer in the reference's own fp32 semantics and
+ * summation order (BitLinearCpu::forward, cpu.rs:17-127; the results of
+ * btl_linear with that mode, bit for bit), all layers in one launch when k % 64
+ * == 0, k <= 16384 and the weights are 16-byte aligned.  ws is unused in that
+ * mode.  count in 1..4.
+ */
+int btl_linear_group_mode(const btl_packed_t* const* w, void* const* y, int count, const void* x, int xdtype,
+                          int64_t m, int64_t k, int ydtype, int mode, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Operand-order activations for prefill (many token rows).  No reference
  * counterpart: the reference quantises nothing on this path.  The prefill GEMM
  * reads every 16-element group of k in the order its unpacked weights take,

@@ -894,3 +894,23 @@ def test_pack_device_clamps_and_zeros():
     assert torch.equal(dev.data.cpu(), host.data) and dev.scale == host.scale
     wb, sw = orc.pack(w)
     assert np.array_equal(host.data.numpy(), wb)
+
+
+# btl_linear_group_mode in the reference's fp32 order: the layers of one launch
+# (and the per-layer fallback for k % 64 != 0) bit for bit with the oracle
+@pytest.mark.parametrize("m,k,ns,xdt", [(1, 4096, (4096, 1024, 1024), torch.float32),
+                                        (1, 4096, (14336, 14336), torch.bfloat16),
+                                        (3, 512, (96, 40, 33, 7), torch.float32), (2, 100, (17, 9), torch.float32)])
+def test_group_f32_ref_bitexact(m, k, ns, xdt):
+    print("group f32_ref", m, k, ns, flush=True)
+    rng = np.random.default_rng(m + k + len(ns))
+    x = (rng.standard_normal((m, k)) * np.exp2(rng.integers(-10, 10, (m, k)))).astype(np.float32)
+    xt = to_dev(x, xdt)
+    layers = []
+    for i, n in enumerate(ns):
+        wb = random_codes(n, k, seed=31 * i + n, p3=0.1)
+        layers.append((bl.PackedTensor(torch.from_numpy(wb).to(DEV), 0.01 * (i + 1), (n, k), DEV), wb))
+    outs = bl.linear_group([l[0] for l in layers], xt, out_dtype=torch.float32, mode="f32_ref")
+    for (pt, wb), y in zip(layers, outs):
+        assert_f32_identical(y, orc.forward_f32(host_x(xt), wb, pt.shape[0], np.float32(pt.scale)))
+        assert torch.equal(y, bl.BitLinearHip.forward(xt, pt, mode="f32_ref", out_dtype=torch.float32))
