@@ -597,6 +597,20 @@ def run_e2e(layers, gen, dev, args):
         print("bench: e2e dense %s head: decode %.3f ms/token, head kernel %.1f us" %
               (name, d_ms, dense[name]["lm_head_kernel"]["us"]), file=sys.stderr, flush=True)
         del dw
+    # the decoder in the reference's own arithmetic: fp32 BitLinears (cpu.rs order,
+    # BTL_ACT_F32_REF) and the dense f32 lm_head -- what the reference computes on a CPU
+    dw = w.contiguous()
+    weights["lm_head"] = dw
+    model = BitLlamaHip(cfg, weights, dev, max_rows=prompt_len, mode="f32_ref")
+    ref_tokens = min(gen_len, 64)
+    p_ms, d_ms, _ = _e2e_run(model, prompt, ref_tokens)
+    del model, dw
+    out["reference_arithmetic"] = dict(
+        summary(p_ms, d_ms, cfg.vocab * HIDDEN * 4),
+        workload="the same decoder with every BitLinear in the reference's fp32 order (mode f32_ref, "
+                 "BitLinearCpu::forward bit for bit) and the dense f32 lm_head: the reference's own CPU "
+                 "arithmetic; %d greedy tokens" % ref_tokens)
+    print("bench: e2e in the reference's arithmetic: decode %.3f ms/token" % d_ms, file=sys.stderr, flush=True)
     weights["lm_head"] = head
     del w
     out["dense_head"] = dense

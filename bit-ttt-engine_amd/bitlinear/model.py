@@ -41,7 +41,7 @@ import ctypes
 import numpy as np
 import torch
 
-from ._lib import BTL_F32, BTL_BF16, BtlKvQ8, BtlPacked, check, lib
+from ._lib import BTL_ACT_F32_REF, BTL_F32, BTL_BF16, BtlKvQ8, BtlPacked, check, lib
 from .packed import PackedTensor
 
 RMS_NORM_EPS = 1e-5  # block.rs:10
@@ -100,6 +100,11 @@ def _ptrs(ts):
 class BitLlamaHip:
     """BitLlama with attention blocks (ModelArch::Llama), all linears packed ternary.
 
+    mode "i8" runs every BitLinear in W1.58-A8 with the fused decode kernels;
+    mode "f32_ref" runs them in the reference's own fp32 arithmetic
+    (BitLinearCpu::forward, cpu.rs:17-127, bit for bit) -- with a dense f32
+    lm_head this is the decoder the reference runs on a CPU.
+
     weights: dict with
       "embed" [vocab, hidden] float32 or bfloat16 (GPU),
       "norm_f" [hidden] float32, "lm_head" PackedTensor [vocab, hidden] (ternary, a
@@ -109,7 +114,10 @@ class BitLlamaHip:
                                "q", "k", "v", "o", "gate", "up", "down": PackedTensor}.
     """
 
-    def __init__(self, cfg, weights, device="cuda", max_rows=512):
+    def __init__(self, cfg, weights, device="cuda", max_rows=512, mode="i8"):
+        if mode not in ("i8", "f32_ref"):
+            raise ValueError("mode is 'i8' (W1.58-A8) or 'f32_ref' (the reference's fp32 BitLinear)")
+        self.mode = mode
         self.cfg = cfg
         self.dev = torch.device(device)
         self.w = weights
@@ -126,6 +134,10 @@ class BitLlamaHip:
         self.o = torch.zeros((M, c.hidden), **f32)
         self.hs = torch.zeros((M, c.intermediate), **f32)  # silu(gate) * up
         self.down = torch.zeros((M, c.hidden), **f32)
+        if mode == "f32_ref":
+            self.xn = torch.zeros((M, c.hidden), **f32)         # the normed rows
+            self.gate = torch.zeros((M, c.intermediate), **f32)
+            self.up = torch.zeros((M, c.intermediate), **f32)
         self.logits = torch.zeros((1, c.vocab), **f32)
         self.ids = torch.zeros((M,), dtype=torch.int32, device=self.dev)
         self.next_id = torch.zeros((1,), dtype=torch.int32, device=self.dev)
@@ -146,7 +158,9 @@ class BitLlamaHip:
             o_c, o = _arr([L["o"]])
             gate_c, up_c = L["gate"].as_c(), L["up"].as_c()
             d_c, d = _arr([L["down"]])
-            self._layers.append(dict(keep=(qkv_c, o_c, d_c), qkv=qkv, o=o, down=d, o_w=ctypes.byref(o_c[0]),
+            gu_c, gu = _arr([L["gate"], L["up"]])
+            self._layers.append(dict(keep=(qkv_c, o_c, d_c, gu_c), qkv=qkv, o=o, down=d, gu=gu,
+                                     o_w=ctypes.byref(o_c[0]),
                                      down_w=ctypes.byref(d_c[0]),
                                      gate=ctypes.byref(gate_c), up=ctypes.byref(up_c), gate_c=gate_c, up_c=up_c,
                                      n1=L["norm1"].data_ptr(), n2=L["norm2"].data_ptr()))
@@ -164,6 +178,8 @@ class BitLlamaHip:
         self._y_o = _ptrs([self.o])
         self._y_down = _ptrs([self.down])
         self._y_logits = _ptrs([self.logits])
+        if mode == "f32_ref":
+            self._y_gu = _ptrs([self.gate, self.up])
         # the model's own workspace, sized for every call it makes, so captured
         # steps never depend on the library's shared workspace
         I8 = 1
@@ -195,6 +211,9 @@ class BitLlamaHip:
         hid = c.hidden
         check(lib.btl_embedding(self.w["embed"].data_ptr(), self.emb_dtype, c.vocab, hid, ids.data_ptr(), m,
                                 self.h.data_ptr(), st))
+        if self.mode == "f32_ref":
+            self._run_ref(m, pos, dp, st)
+            return
         cur, nxt = self.h, self.h2  # each add writes the other buffer
         # One token: the residual adds run in the epilogues of the o and down
         # projections (btl_linear_residual), so the norms ahead of q|k|v and
@@ -241,6 +260,49 @@ class BitLlamaHip:
             return
         check(lib.btl_add_rmsnorm_linear_group(self._head, self._y_logits, 1, cur[last].data_ptr(), delta, None,
                                                self.w["norm_f"].data_ptr(), c.eps, 1, hid, BTL_F32, ws, wn, st))
+
+    def _run_ref(self, m, pos, dp, st):
+        """The blocks and the head in the reference's own arithmetic: every BitLinear
+        as BitLinearCpu::forward (btl_linear_group_mode, BTL_ACT_F32_REF), the
+        residual adds and norms through btl_add_rmsnorm (the add of a block's output
+        is done by the next norm), SwiGLU's activation through btl_swiglu."""
+        c = self.cfg
+        hid, qd = c.hidden, c.n_heads * c.head_dim
+        F, R = BTL_F32, BTL_ACT_F32_REF
+        cur, nxt = self.h, self.h2
+        delta = None  # the block output still to be added to cur
+        for li, L in enumerate(self._layers):
+            if delta is None:
+                check(lib.btl_add_rmsnorm(cur.data_ptr(), None, None, L["n1"], c.eps, m, hid, self.xn.data_ptr(), st))
+            else:
+                check(lib.btl_add_rmsnorm(cur.data_ptr(), delta.data_ptr(), nxt.data_ptr(), L["n1"], c.eps, m, hid,
+                                          self.xn.data_ptr(), st))
+                cur, nxt = nxt, cur
+            check(lib.btl_linear_group_mode(L["qkv"], self._y_qkv, 3, self.xn.data_ptr(), F, m, hid, F, R, None, 0,
+                                            st))
+            check(lib.btl_rope_append_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), m,
+                                                c.n_heads, ctypes.byref(self.caches[li].c), pos, dp,
+                                                self.rope_cos.data_ptr(), self.rope_sin.data_ptr(),
+                                                self.attn.data_ptr(), self._ws, self._ws_n, st))
+            check(lib.btl_linear_group_mode(L["o"], self._y_o, 1, self.attn.data_ptr(), F, m, qd, F, R, None, 0, st))
+            check(lib.btl_add_rmsnorm(cur.data_ptr(), self.o.data_ptr(), nxt.data_ptr(), L["n2"], c.eps, m, hid,
+                                      self.xn.data_ptr(), st))
+            cur, nxt = nxt, cur
+            check(lib.btl_linear_group_mode(L["gu"], self._y_gu, 2, self.xn.data_ptr(), F, m, hid, F, R, None, 0, st))
+            check(lib.btl_swiglu(self.gate.data_ptr(), self.up.data_ptr(), m * c.intermediate, self.hs.data_ptr(), st))
+            check(lib.btl_linear_group_mode(L["down"], self._y_down, 1, self.hs.data_ptr(), F, m, c.intermediate, F,
+                                            R, None, 0, st))
+            delta = self.down
+        last = m - 1
+        xf = self.xf if self.dense_head else self.xn
+        check(lib.btl_add_rmsnorm(cur[last].data_ptr(), self.down[last].data_ptr(), None,
+                                  self.w["norm_f"].data_ptr(), c.eps, 1, hid, xf.data_ptr(), st))
+        if self.dense_head:
+            check(lib.btl_dense_linear(self.w["lm_head"].data_ptr(), self._head_dt, c.vocab, hid, xf.data_ptr(), 1,
+                                       self.logits.data_ptr(), st))
+        else:
+            check(lib.btl_linear_group_mode(self._head, self._y_logits, 1, xf.data_ptr(), F, 1, hid, F, R, None, 0,
+                                            st))
 
     def reset(self):
         """Llama::reset_state / BitLlama::reset_kv_cache (llama.rs:179-186, 460-468)."""

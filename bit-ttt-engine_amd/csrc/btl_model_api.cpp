@@ -307,6 +307,19 @@ int btl_add_rmsnorm(const float* h, const float* delta, float* h_out, const floa
     return BTL_OK;
 }
 
+int btl_swiglu(const float* gate, const float* up, int64_t count, float* out, void* stream)
+{
+    if (count < 0) return fail_msg(BTL_ERR_SHAPE, "negative count");
+    if (count == 0) return BTL_OK;
+    if (!gate || !up || !out) return fail_msg(BTL_ERR_LAYOUT, "null pointer");
+    int dev;
+    int rc = btl::host::device(&dev);
+    if (rc) return rc;
+    hipError_t e = btl::launch_swiglu_f32(gate, up, count, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "swiglu kernel launch");
+    return BTL_OK;
+}
+
 int btl_dense_linear(const void* w, int wdtype, int64_t n, int64_t k, const float* x, int64_t m, float* y,
                      void* stream)
 {

@@ -146,6 +146,15 @@ int btl_add_rmsnorm(const float* h, const float* delta, float* h_out, const floa
                     float* y, void* stream);
 
 /*
+ * SwiGLU's activation (swiglu.rs:29-35): out[i] = silu(gate[i]) * up[i], silu
+ * as candle's v / (1 + exp(-v)), every operation rounded to f32 (exp by a
+ * Cody-Waite reduction and a degree-7 Taylor polynomial, each step rounded;
+ * oracle/bitlinear_oracle.c restates it).
+ * count elements of f32; out may be gate or up.
+ */
+int btl_swiglu(const float* gate, const float* up, int64_t count, float* out, void* stream);
+
+/*
  * candle_nn::Linear::forward without a bias -- the reference's lm_head, a dense
  * linear (llama.rs:129-141): y[m, n] = x[m, k] . w[n, k]^T in f32, w of dtype
  * BTL_F32 (the reference's) or BTL_BF16 (widened exactly).  Fixed order: lane l

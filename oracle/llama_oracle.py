@@ -26,10 +26,13 @@ class OracleLlama:
       lm_head (bytes, scale) -- or a dense [vocab, hidden] f32 array / uint16 array
       of bf16 bits (the reference's candle_nn::Linear), layers: [{norm1, norm2, q,
       k, v, o, gate, up, down}]
-    with the linears as (packed bytes uint8, scale) pairs."""
+    with the linears as (packed bytes uint8, scale) pairs.  mode "i8": every
+    BitLinear in W1.58-A8; "f32_ref": in the reference's own fp32 arithmetic
+    (BitLinearCpu, cpu.rs:17-127), the decoder the reference runs on a CPU."""
 
-    def __init__(self, cfg, w):
-        self.cfg, self.w = cfg, w
+    def __init__(self, cfg, w, mode="i8"):
+        assert mode in ("i8", "f32_ref")
+        self.cfg, self.w, self.mode = cfg, w, mode
         c = cfg
         self.cos, self.sin = orc.rope_table(c.rope_theta, c.head_dim, c.max_seq)
         self.caches = [dict(kq=np.zeros((c.n_kv_heads, c.max_seq, c.head_dim), np.uint8),
@@ -39,6 +42,8 @@ class OracleLlama:
         self.pos = 0
 
     def _lin(self, x, pk, n):
+        if self.mode == "f32_ref":  # BitLinearCpu::forward's fp32 order (cpu.rs:17-127)
+            return orc.forward_f32(x, pk[0], n, np.float32(pk[1]))
         return orc.forward_i8(x, pk[0], n, pk[1])[0]
 
     def forward_one(self, token):

@@ -786,3 +786,42 @@ def test_dense_linear_order_cases():
     bl.check(bl.lib.btl_dense_linear(wt.data_ptr(), bl.BTL_F32, 3, k, xt.data_ptr(), 1, y.data_ptr(), stream()))
     assert y.cpu().numpy()[0].tolist() == [t, t, 0.0]
     assert_same(y, orc.dense_linear(x, w), "order cases")
+
+
+@pytest.mark.parametrize("cfg_cls", [TinyA, Tiny2])
+def test_decoder_f32_ref_matches_oracle(cfg_cls):
+    # every BitLinear in the reference's own fp32 order (BTL_ACT_F32_REF): token by
+    # token against the oracle in that mode, a batched prefill equal to it, and a
+    # graph-replayed greedy continuation
+    cfg = cfg_cls()
+    w = tiny_weights(cfg, seed=12)
+    gm = gpu_model(cfg, w)
+    ref = BitLlamaHip(cfg, dict(gm.w), DEV, mode="f32_ref")
+    om = OracleLlama(cfg, w, mode="f32_ref")
+    toks = np.random.default_rng(13).integers(0, cfg.vocab, 40)
+    for i, t in enumerate(toks):
+        print("f32_ref forward_one", i, flush=True)
+        assert_same(ref.forward_one(int(t)), om.forward_one(int(t)), "step %d logits" % i)
+    b = BitLlamaHip(cfg, dict(gm.w), DEV, mode="f32_ref", max_rows=16)
+    assert_same(b.prefill(toks), ref.logits[0].cpu().numpy(), "prefill in batches of 16")
+    for li in range(cfg.n_layers):
+        assert torch.equal(b.caches[li].k, ref.caches[li].k) and torch.equal(b.caches[li].v_scale, ref.caches[li].v_scale)
+    got = BitLlamaHip(cfg, dict(gm.w), DEV, mode="f32_ref").generate(toks[:5], 10, use_graph=True)
+    exp = OracleLlama(cfg, w, mode="f32_ref").generate(toks[:5], 10)
+    assert np.array_equal(got, exp), (got, exp)
+
+
+def test_decoder_reference_arithmetic_with_dense_head():
+    # the decoder as the reference runs it on a CPU: fp32 BitLinears and a dense
+    # f32 lm_head
+    cfg = TinyA()
+    w = tiny_weights(cfg, seed=14)
+    gm = gpu_model(cfg, w)
+    head = (np.random.default_rng(5).standard_normal((cfg.vocab, cfg.hidden)) * 0.05).astype(np.float32)
+    gw = dict(gm.w)
+    gw["lm_head"] = torch.from_numpy(head).to(DEV)
+    wo = dict(w)
+    wo["lm_head"] = head
+    got = BitLlamaHip(cfg, gw, DEV, mode="f32_ref").generate([7, 1, 99, 5], 12, use_graph=True)
+    exp = OracleLlama(cfg, wo, mode="f32_ref").generate([7, 1, 99, 5], 12)
+    assert np.array_equal(got, exp), (got, exp)
