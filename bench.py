@@ -280,6 +280,7 @@ def run_decode(args):
         result["pack"] = run_pack(gen, dev)
     if args.cfg1:
         result["cfg1"] = run_cfg1(gen, dev, args)
+    result["anchor"] = run_anchor(dev, args)
     if args.e2e:
         result["e2e"] = run_e2e(layers, gen, dev, args)
     if args.adaptive:
@@ -433,7 +434,6 @@ def run_prefill(layers, gen, dev, args):
                                        "the L2s; the 8 XCDs each fetch the weights once)",
                      "algorithmic_ops": dom["ops"], "avg_us": dom["us"]},
         "kernels": kern,
-        "f32_ref": f32_ref,
     }
 
 
@@ -746,6 +746,63 @@ def run_cfg1(gen, dev, args):
         out["cpu_baseline"] = {"us": round(cus, 2), "GB_s": round(b / cus / 1e3, 2), "cores": threads,
                                "kind": "port", "sample": "%d calls of the cfg1 shape on one weight copy, "
                                                          "%.1f s" % (reps, el)}
+    return out
+
+
+def run_anchor(dev, args):
+    """The reference's own kernel benchmark (bench_cpu_kernel.rs:12-91): one
+    BitLinear M=1, K=N=8192, x = 0.5, packed bytes i % 255, scale 1; 10 warm-up
+    calls, then the mean of 100 timed calls; GOps/s = M*N*K/t and GB/s =
+    (4MK + NK/4 + 4MN)/t, the reference's formulas.  On the GPU in both
+    arithmetic modes (f32 in/out), and the reference's CPU algorithm (cpu.rs
+    restated with AVX2 intrinsics) on the host cores."""
+    import ctypes
+    m, k, n = 1, 8192, 8192
+    wb = (np.arange(n * k // 4) % 255).astype(np.uint8)
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(dev), 1.0, (n, k), dev)
+    c = pt.as_c()
+    x = torch.full((m, k), 0.5, device=dev)
+    y = torch.empty((m, n), device=dev)
+    nbytes = 4 * m * k + n * k // 4 + 4 * m * n
+    ops = m * n * k
+
+    def rates(sec):
+        return {"ms": round(sec * 1e3, 4), "GOps_s": round(ops / sec / 1e9, 2), "GB_s": round(nbytes / sec / 1e9, 2)}
+
+    out = {"workload": "bench_cpu_kernel.rs: M=1, K=N=8192, x=0.5, weight bytes i % 255, scale 1; 10 warm-ups, "
+                       "mean of 100 calls; GOps/s = M*N*K/t, GB/s = (4MK + NK/4 + 4MN)/t"}
+    for name, mode in (("gpu_f32_ref", bl.BTL_ACT_F32_REF), ("gpu_i8", bl.BTL_ACT_I8)):
+        def call(stream):
+            bl.check(bl.lib.btl_linear(ctypes.byref(c), x.data_ptr(), bl.BTL_F32, m, k, y.data_ptr(), bl.BTL_F32,
+                                       mode, None, None, 0, stream))
+        st = torch.cuda.current_stream()
+        for _ in range(10):
+            call(st.cuda_stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(100):
+            call(st.cuda_stream)
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = rates(e0.elapsed_time(e1) / 1e3 / 100)
+        out[name]["frac_hbm"] = round(nbytes / (e0.elapsed_time(e1) / 1e3 / 100) / 1e9 / HBM_PEAK_GBS, 4)
+    if args.cpu_baseline:
+        from oracle import oracle as orc
+        threads = max(1, min(16, os.cpu_count() or 1))
+        xh = np.full((m, k), 0.5, np.float32)
+        for _ in range(10):
+            orc.forward_f32_avx2(xh, wb, n, 1.0, threads=threads)
+        t0 = time.perf_counter()
+        for _ in range(100):
+            orc.forward_f32_avx2(xh, wb, n, 1.0, threads=threads)
+        out["cpu"] = dict(rates((time.perf_counter() - t0) / 100), cores=threads, kind="port",
+                          nproc=os.cpu_count() or 0,
+                          sample="cpu.rs restated in C with AVX2+FMA intrinsics, %d threads (the box's CPU share; "
+                                 "the reference's rayon pool would take nproc)" % threads)
+    print("bench: anchor (M=1, K=N=8192): gpu f32_ref %.4f ms, gpu i8 %.4f ms%s" %
+          (out["gpu_f32_ref"]["ms"], out["gpu_i8"]["ms"],
+           ", cpu %.3f ms" % out["cpu"]["ms"] if "cpu" in out else ""), file=sys.stderr, flush=True)
     return out
 
 
