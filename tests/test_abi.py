@@ -30,6 +30,41 @@ def test_header_declares_python_exports():
     assert header_functions() == sorted(bl.EXPORTS)
 
 
+CRATE = os.path.join(ROOT, "bit-ttt-engine_amd", "crates", "bitlinear-hip-sys", "src", "lib.rs")
+
+
+def _c_prototypes():
+    text = "".join(open(h).read() for h in HEADERS)
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(btl_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_ffi_crate_mirrors_the_headers():
+    # the Rust FFI crate (bitlinear-hip-sys, source only: no cargo in this image)
+    # declares every function of include/*.h with the same arity, every struct
+    # with the same fields and every BTL_ constant with the same value
+    rs = open(CRATE).read()
+    decls = {m.group(1): m.group(2) for m in re.finditer(r"pub fn (btl_[a-z0-9_]+)\(([^)]*)\)", rs, flags=re.S)}
+    protos = _c_prototypes()
+    assert sorted(protos) == sorted(header_functions())
+    assert sorted(decls) == sorted(protos), set(decls) ^ set(protos)
+    for name, n in protos.items():
+        args = decls[name].strip()
+        assert (0 if not args else args.count(":")) == n, name
+    text = "".join(open(h).read() for h in HEADERS)
+    for name, val in re.findall(r"#define\s+(BTL_[A-Z0-9_]+)\s+(-?\d+)", text):
+        assert re.search(r"pub const %s: c_int = %s;" % (name, val), rs), name
+    for body, tname in re.findall(r"typedef struct \w+ \{(.*?)\}\s*(\w+);", text, flags=re.S):
+        fields = re.findall(r"(\w+)\s*(?:,|;)", re.sub(r"//.*", "", body))
+        m = re.search(r"pub struct %s \{(.*?)\}" % tname, rs, flags=re.S)
+        assert m, tname
+        assert re.findall(r"pub (\w+):", m.group(1)) == fields, tname
+
+
 def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", bl.LIB_PATH], stdout=subprocess.PIPE, text=True,
                          check=True).stdout
