@@ -101,7 +101,7 @@ constexpr KnobDef kKnobs[btl::KN_COUNT] = {
     {"BTL_GEMV_BAT", 1},       {"BTL_FUSE_MAX_WG", 512},  {"BTL_FUSE_DEC", 1},
     {"BTL_DEC_RQ_MIN_K", 1024}, {"BTL_DEC_RQ", 1},        {"BTL_DEC_RQ_DG", 0},
     {"BTL_GEMM_MAX_SPLITS", 0}, {"BTL_GEMM_WIDE_MIN_TILES", btl::kGemmWideMinTiles},
-    {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1},
+    {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1}, {"BTL_SPLIT_MERGE", 1},
 };
 std::atomic<int> g_knob[btl::KN_COUNT];
 std::once_flag g_knob_once;
@@ -225,10 +225,11 @@ struct Layer {
 
 // One k_gemm_i8 (or, bat, k_gemv_bat) launch over the layers of a group
 // (operand-order q); with splits > 1, the partial sums go to `part` and a
-// reduce kernel follows.
+// reduce kernel follows -- or, k_gemv_bat with merge counters `ctr`, the last
+// split of each row block adds them in the same launch.
 hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const float* sx, int64_t m,
                        int64_t k, int ykind, int splits, int split_steps, int32_t* part, bool bat,
-                       hipStream_t st)
+                       hipStream_t st, uint32_t* ctr)
 {
     btl::GemmArgs g;
     memset(&g, 0, sizeof(g));
@@ -240,6 +241,7 @@ hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const fl
     g.splits = splits;
     g.split_steps = split_steps;
     g.part = part;
+    g.ctr = ctr;
     for (int i = 0; i < count; ++i) {
         if (layers[i].w->n == 0) continue;
         btl::GemmLayer& L = g.L[g.nl++];
@@ -553,8 +555,17 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");
         return resid ? add_resid(layers[0], resid, m, st) : BTL_OK;
     }
+    // batched decode: the K splits merged in the launch (counters of this
+    // workspace) up to 16 token rows -- measured on MI355X, Llama-3-8B MLP: 1-2 us
+    // per layer faster at m = 4..16, 4 us slower at m = 32, where one workgroup
+    // per row block adds 2048 outputs' partials and gate|up splits too
+    uint32_t* ctr = nullptr;
+    if (bat && splits > 1 && m <= 16 && env_int(btl::KN_SPLIT_MERGE) != 0 && splits <= btl::kMergeMaxSplits &&
+        gemv_row_blocks(layers, count) <= btl::kSplitCounters) {
+        if ((e = btl::split_counters(dev, ws, &ctr)) != hipSuccess) return hip_fail(e, "split-K merge counters");
+    }
     e = launch_gemm(layers, count, q, sxp, m, k, ykind, splits, split_steps,
-                    splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr, bat, st);
+                    splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr, bat, st, ctr);
     if (e != hipSuccess) return hip_fail(e, bat ? "batched gemv kernel launch" : "gemm kernel launch");
     return resid ? add_resid(layers[0], resid, m, st) : BTL_OK;
 }
@@ -950,7 +961,7 @@ int btl_linear_i8_op(const btl_packed_t* const* w, void* const* y, int32_t* cons
     int dev;
     if ((rc = current_device(&dev))) return rc;
     hipError_t e = launch_gemm(ls, count, xq, xscale, m, k, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32,
-                               1, 0, nullptr, false, (hipStream_t)stream);
+                               1, 0, nullptr, false, (hipStream_t)stream, nullptr);
     if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
     return BTL_OK;
 }

@@ -34,6 +34,7 @@ enum Knob {
                              // knob that can change results: a wait that gives up leaves
                              // invalid outputs and sets the device fault word)
     KN_ATTN_MERGE,           // 0: one-token attention merges its chunks in a second launch (1)
+    KN_SPLIT_MERGE,          // 0: the batched decode adds its K splits in a reduce launch (1: in the launch)
     KN_COUNT
 };
 int knob(Knob k);
@@ -154,6 +155,7 @@ struct GemmArgs {
     // adds them and applies the epilogue.  splits == 1: part unused.
     int splits, split_steps;
     int32_t* part;
+    uint32_t* ctr;     // k_gemv_bat: merge counters (split_counters) -- splits merged in the launch; NULL: reduce launch
 };
 
 constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for
@@ -169,6 +171,15 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s);
 // ceil(n / 64) over the layers.
 int gemv_bat_split(int64_t m, int64_t row_blocks, int64_t k, int* steps);
 hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s);
+
+// The split-K merge of k_gemv_bat inside the launch: a slot of kSplitCounters
+// per workspace (calls that share a workspace are ordered by the caller, so
+// they may share counters), one counter per row block; the current device
+// must be `dev`.
+constexpr int kSplitCounters = 2048;
+constexpr int kSplitSlots = 128;
+constexpr int kMergeMaxSplits = 16;  // K ranges of >= 1024 weights, k <= 16384
+hipError_t split_counters(int dev, const void* ws_key, uint32_t** out);
 // natural-order int8 rows -> operand order (k % 16 == 0, 16-byte aligned)
 hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, hipStream_t st);
 hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,

@@ -24,6 +24,8 @@
 // Compiled with -ffp-contract=off: every fp32 operation below is rounded as
 // written (the oracle restates the same operations in C).
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 #include <stdlib.h>
 
 #include "btl_device.hpp"
@@ -1728,7 +1730,22 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
 // ks bytes of token t with 16-byte slot s stored at slot s ^ (t & 15): the 16
 // lanes of a quarter-wave read 16 different token rows at one k without bank
 // conflicts.  One split: the epilogue stores y; several: exact int32 partial
-// sums for k_gemm_reduce.
+// sums, added by k_gemm_reduce -- or, with a.ctr (one counter per row block,
+// left at zero by every launch), stored coherently (sc1) and added by the last
+// split of the row block to arrive, which applies the epilogue: no second
+// launch.
+constexpr int kSc1 = 16;  // buffer / global cache policy: coherent at agent scope
+
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int ST, int MTB>
 __global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
 {
@@ -1799,21 +1816,71 @@ __global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
 
     // 5. D lane l element v: weight row 4 (l >> 4) + v, token column l & 15
     const int nb = row0 + 4 * kq;
+    const bool ybf = a.ykind == YK_BF16;
     if (a.splits > 1) {
         const int ncols = a.L[a.nl - 1].col0 + a.L[a.nl - 1].n;
+        const bool merge = a.ctr != nullptr;
 #pragma unroll
         for (int tb = 0; tb < MTB; ++tb) {
             const int t = tb * 16 + (lane & 15);
             if (t < M) {
                 int32_t* prow = a.part + ((int64_t)split * M + t) * ncols + Lw.col0;
 #pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    if (nb + v < N) prow[nb + v] = acc[tb][v];
+                for (int v = 0; v < 4; ++v) {
+                    if (nb + v < N) {
+                        if (merge) st_agent((uint32_t*)prow + nb + v, (uint32_t)acc[tb][v]);
+                        else prow[nb + v] = acc[tb][v];
+                    }
+                }
+            }
+        }
+        if (!merge) return;  // k_gemm_reduce adds them
+        // the last split of this row block adds every split's partials (exact
+        // int32: any order) and applies the epilogue; its counter goes back to zero
+        __shared__ uint32_t s_last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are stored
+        __syncthreads();
+        const int rbg = (int)blockIdx.x;
+        if (tid == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(a.ctr + rbg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = old + 1u == (uint32_t)a.splits;
+            if (last) __hip_atomic_fetch_sub(a.ctr + rbg, (uint32_t)a.splits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        const int rbase = rb * 64;
+        const int64_t sstride = (int64_t)M * ncols;
+        // four outputs per thread at a time, every split's load in flight
+        for (int o0 = tid; o0 < M * 64; o0 += 4 * 256) {
+            uint32_t pv[4][kMergeMaxSplits];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int o = o0 + 256 * u;
+                const int t = min(o >> 6, M - 1), n = rbase + (o & 63);
+                const bool ok = o < M * 64 && n < N;
+                const uint32_t* p = (const uint32_t*)a.part + (int64_t)t * ncols + Lw.col0 + (ok ? n : 0);
+#pragma unroll
+                for (int sp = 0; sp < kMergeMaxSplits; ++sp)
+                    pv[u][sp] = ok && sp < a.splits ? ld_agent(p + sp * sstride) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int o = o0 + 256 * u;
+                const int t = o >> 6, n = rbase + (o & 63);
+                if (o >= M * 64 || n >= N) continue;
+                int32_t sum = 0;
+#pragma unroll
+                for (int sp = 0; sp < kMergeMaxSplits; ++sp) sum += (int32_t)pv[u][sp];
+                const float yv = __fmul_rn((float)sum, __fmul_rn(a.sx[t], Lw.sw));
+                const int64_t oi = (int64_t)t * N + n;
+                if (ybf) ((uint16_t*)Lw.y)[oi] = f32_to_bf16(yv);
+                else ((float*)Lw.y)[oi] = yv;
+                if (Lw.acc_out) Lw.acc_out[oi] = sum;
             }
         }
         return;
     }
-    const bool ybf = a.ykind == YK_BF16;
 #pragma unroll
     for (int tb = 0; tb < MTB; ++tb) {
         const int t = tb * 16 + (lane & 15);
@@ -1861,6 +1928,7 @@ hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s)
     const int st = g.split_steps;
     if (g.m > 64 || g.nl < 1 || g.nl > kMaxGroup || (st != 4 && st != 8 && st != 16) ||
         (int64_t)mr * st * kStepWeights > 65536 || rbs > INT32_MAX ||
+        (g.ctr && (rbs > kSplitCounters || g.splits > kMergeMaxSplits)) ||
         g.splits != (g.k + st * kStepWeights - 1) / (st * kStepWeights) || (g.splits > 1 && !g.part))
         return hipErrorInvalidValue;
     const size_t lds = (size_t)mr * st * kStepWeights;
@@ -1873,11 +1941,42 @@ hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s)
     BTL_BAT(16, 1) BTL_BAT(16, 2) BTL_BAT(16, 4) return hipErrorInvalidValue;
 #undef BTL_BAT
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || g.splits == 1) return e;
+    if (e != hipSuccess || g.splits == 1 || g.ctr) return e;
     const int64_t outs = (int64_t)g.m * cols;
     const int64_t blocks = (outs + 255) / 256;
     hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, s, g, (int)cols);
     return hipGetLastError();
+}
+
+static __device__ uint32_t g_split_ctr[kSplitSlots * kSplitCounters];
+
+hipError_t split_counters(int dev, const void* ws_key, uint32_t** out)
+{
+    struct Slots {
+        std::mutex mu;
+        uint32_t* base = nullptr;
+        const void* key[kSplitSlots] = {};
+        int next = 0;
+    };
+    static Slots slots[64];
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    Slots& S = slots[dev];
+    std::lock_guard<std::mutex> lk(S.mu);
+    if (!S.base) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_split_ctr));
+        if (e != hipSuccess) return e;
+        S.base = (uint32_t*)p;
+    }
+    int i = 0;
+    while (i < kSplitSlots && S.key[i] != ws_key) ++i;
+    if (i == kSplitSlots) {  // a new workspace: the next slot in turn
+        i = S.next;
+        S.next = (S.next + 1) % kSplitSlots;
+        S.key[i] = ws_key;
+    }
+    *out = S.base + (size_t)i * kSplitCounters;
+    return hipSuccess;
 }
 
 // ---------------------------------------------------------------------------

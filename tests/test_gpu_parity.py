@@ -338,15 +338,18 @@ SPLIT_SHAPES = [(16, 14336, 256), (5, 4096, 300), (64, 1088, 1000), (2, 14336, 1
                 (128, 2048, 130), (33, 256, 64), (20, 192, 70), (48, 8192, 200)]
 
 
-@pytest.mark.parametrize("route", ["bat", "gemm"])
+@pytest.mark.parametrize("route", ["merge", "bat", "gemm"])
 @pytest.mark.parametrize("m,k,n", SPLIT_SHAPES)
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
 def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, tune):
+    # merge: the batched kernel adding its K splits in the launch; bat: the same
+    # contraction with a reduce launch after it
     print("split-k", route, m, k, n, xdt, ydt, flush=True)
     if route == "gemm":
         tune("BTL_GEMV_BAT", "0")
     else:
         tune("BTL_GEMV_BAT_MAX_M", "64")  # the 33..64-row blocks too
+        tune("BTL_SPLIT_MERGE", 1 if route == "merge" else 0)
     x = activations(m, k, seed=m * 5 + k + n)
     pt, wb, sw = make_layer(n, k, seed=n * 3 + k)
     xt = to_dev(x, xdt)
@@ -914,3 +917,31 @@ def test_group_f32_ref_bitexact(m, k, ns, xdt):
     for (pt, wb), y in zip(layers, outs):
         assert_f32_identical(y, orc.forward_f32(host_x(xt), wb, pt.shape[0], np.float32(pt.scale)))
         assert torch.equal(y, bl.BitLinearHip.forward(xt, pt, mode="f32_ref", out_dtype=torch.float32))
+
+
+def test_batched_merge_counters_and_graph_replays(tune):
+    # the in-launch split merge keeps its counters per workspace and every launch
+    # leaves them at zero: calls of different m and K splits on one workspace, then
+    # a captured call replayed with eager calls in between, all bit for bit
+    print("split merge counters / graph", flush=True)
+    tune("BTL_GEMV_BAT_MAX_M", "64")
+    tune("BTL_SPLIT_MERGE", 1)
+    k, n = 14336, 384
+    pt, wb, sw = make_layer(n, k, seed=90)
+    ws = bl.Workspace(64, n, k, device=DEV)
+    xs = {m: to_dev(activations(m, k, seed=91 + m), torch.bfloat16) for m in (3, 16, 40, 64)}
+    ref = {m: orc.forward_i8(host_x(x), wb, n, sw)[0] for m, x in xs.items()}
+    for m in (3, 16, 40, 64, 16, 3):
+        assert_f32_identical(bl.BitLinearHip.forward(xs[m], pt, out_dtype=torch.float32, workspace=ws), ref[m])
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            y = bl.BitLinearHip.forward(xs[16], pt, out_dtype=torch.float32, workspace=ws)
+    torch.cuda.synchronize()
+    for i in range(3):
+        y.fill_(-1.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert_f32_identical(y, ref[16])
+        assert_f32_identical(bl.BitLinearHip.forward(xs[40], pt, out_dtype=torch.float32, workspace=ws), ref[40])
