@@ -123,6 +123,30 @@ def time_launches(fn, reps, stream_obj):
     return 1000.0 * e0.elapsed_time(e1) / reps
 
 
+def profiled_trace_us(name):
+    """The kernel-trace mean duration (us) of the roofline launch recorded in
+    profiles/<name> (line "trace_mean_us_gate_up: X"); None if absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("trace_mean_us_gate_up:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def _trace_frac(trace_us, work, peak, unit_div):
+    """trace_avg_us / achieved_trace / frac_trace of a roofline launch from its
+    kernel-trace mean: work (bytes or ops) / trace_us / unit_div against peak."""
+    if not trace_us:
+        return {"trace_avg_us": None, "frac_trace": None}
+    ach = work / trace_us / unit_div
+    return {"trace_avg_us": trace_us, "achieved_trace": round(ach, 1), "frac_trace": round(ach / peak, 3),
+            "trace_source": "kernel-trace mean of the committed rocprofv3 summary"}
+
+
 def profiled_traffic(name):
     """HBM bytes per launch measured by the FETCH_SIZE / WRITE_SIZE counter runs
     summarised in profiles/<name> (see the commands there); None if absent."""
@@ -268,7 +292,10 @@ def run_decode(args):
                      "traffic": profiled_traffic("k_gemv_rq_gate_up_decode_traffic.md"),
                      "traffic_source": "profiles/k_gemv_rq_gate_up_decode_traffic.md (FETCH_SIZE x copy-calibrated "
                                        "factor + WRITE_SIZE, bytes per launch)",
-                     "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"]},
+                     "algorithmic_bytes": dom["bytes"], "avg_us": dom["us"],
+                     # the same launch's kernel-trace mean (rocprofv3, no launch gap) from the committed summary
+                     **_trace_frac(profiled_trace_us("k_gemv_rq_decode_llama3-8b_m1.md"), dom["bytes"], HBM_PEAK_GBS,
+                                   1e3)},
         "kernels": kern,
         "f32_ref": f32_ref,
     }
@@ -432,7 +459,9 @@ def run_prefill(layers, gen, dev, args):
                      "traffic": profiled_traffic("k_gemm_i8_gate_up_prefill_traffic.md"),
                      "traffic_source": "profiles/k_gemm_i8_gate_up_prefill_traffic.md (bytes per launch crossing "
                                        "the L2s; the 8 XCDs each fetch the weights once)",
-                     "algorithmic_ops": dom["ops"], "avg_us": dom["us"]},
+                     "algorithmic_ops": dom["ops"], "avg_us": dom["us"],
+                     **_trace_frac(profiled_trace_us("k_gemm_i8_prefill_llama3-8b_m2048.md"), dom["ops"],
+                                   INT8_PEAK_TOPS, 1e6)},
         "kernels": kern,
     }
 
