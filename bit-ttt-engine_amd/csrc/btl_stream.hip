@@ -30,12 +30,13 @@
 // MFMA trace trick, exact int32), then y = (float)acc * (s_x * s_w).
 //
 // Handoff (cross-workgroup, agent scope, no grid barrier):
-//  - outputs are stored as tagged 32-bit words (bf16 << 16 | epoch tag) with
-//    sc1 stores, no wait for their completion;
-//  - the last compute wave of the workgroup to finish a stage publishes a
-//    64-bit flag (launch sequence number | absmax of the workgroup's outputs
-//    that the next stage reads: q only, of q|k|v)
-//    in 8 replicas (one per XCD, fewer pollers per line);
+//  - the compute waves leave a stage's outputs in LDS (they issue no global
+//    memory operation but their weight loads, so the compiler's in-order wait
+//    counts stay exact); control wave 0, once they are done, stores them as
+//    tagged 32-bit words (bf16 << 16 | epoch tag) with sc1 stores, no wait for
+//    their completion, and publishes a 64-bit flag (launch sequence number |
+//    absmax of the workgroup's outputs that the next stage reads: q only, of
+//    q|k|v) in 8 replicas (one per XCD, fewer pollers per line);
 //  - the control waves of every workgroup poll their replica (2 KB), take the
 //    global absmax from the flags (so the quantisation needs no pass of its
 //    own), copy the tagged input into LDS (buffer_load ... lds, sc1), re-read
