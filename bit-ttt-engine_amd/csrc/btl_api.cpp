@@ -102,6 +102,7 @@ constexpr KnobDef kKnobs[btl::KN_COUNT] = {
     {"BTL_DEC_RQ_MIN_K", 1024}, {"BTL_DEC_RQ", 1},        {"BTL_DEC_RQ_DG", 0},
     {"BTL_GEMM_MAX_SPLITS", 0}, {"BTL_GEMM_WIDE_MIN_TILES", btl::kGemmWideMinTiles},
     {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1}, {"BTL_SPLIT_MERGE", 1},
+    {"BTL_SPLIT_MERGE_MAX_M", 16}, {"BTL_GEMV_BAT_NW", 0}, {"BTL_GEMV_BAT_KS", 0},
 };
 std::atomic<int> g_knob[btl::KN_COUNT];
 std::once_flag g_knob_once;
@@ -229,7 +230,7 @@ struct Layer {
 // split of each row block adds them in the same launch.
 hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const float* sx, int64_t m,
                        int64_t k, int ykind, int splits, int split_steps, int32_t* part, bool bat,
-                       hipStream_t st, uint32_t* ctr)
+                       hipStream_t st, uint32_t* ctr, int bat_nw = 4)
 {
     btl::GemmArgs g;
     memset(&g, 0, sizeof(g));
@@ -242,6 +243,7 @@ hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const fl
     g.split_steps = split_steps;
     g.part = part;
     g.ctr = ctr;
+    g.bat_nw = bat_nw;
     for (int i = 0; i < count; ++i) {
         if (layers[i].w->n == 0) continue;
         btl::GemmLayer& L = g.L[g.nl++];
@@ -262,10 +264,18 @@ int64_t gemm_tiles_n(const Layer* layers, int count)
     return t;
 }
 
-int64_t gemv_row_blocks(const Layer* layers, int count)
+int64_t rows_of(const Layer* layers, int count)
 {
     int64_t t = 0;
-    for (int i = 0; i < count; ++i) t += ceil_div(layers[i].w->n, 64);
+    for (int i = 0; i < count; ++i) t += layers[i].w->n;
+    return t;
+}
+
+// row blocks of 16 nw rows over the layers of a batched-decode launch
+int64_t gemv_row_blocks(const Layer* layers, int count, int nw)
+{
+    int64_t t = 0;
+    for (int i = 0; i < count; ++i) t += ceil_div(layers[i].w->n, 16 * nw);
     return t;
 }
 
@@ -432,9 +442,14 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     }
     const bool bat = !dec && m <= env_int(btl::KN_GEMV_BAT_MAX_M) && m <= 64 && env_int(btl::KN_GEMV_BAT) != 0;
     int split_steps = 0, splits = 1;
-    if (!dec)
-        splits = bat ? btl::gemv_bat_split(m, gemv_row_blocks(layers, count), k, &split_steps)
-                     : btl::gemm_splits(m, gemm_tiles_n(layers, count), k, &split_steps);
+    btl::BatPlan bp{4, 0, 1};
+    if (bat) {
+        bp = btl::gemv_bat_plan(m, rows_of(layers, count), k);
+        splits = bp.splits;
+        split_steps = bp.steps;
+    } else if (!dec) {
+        splits = btl::gemm_splits(m, gemm_tiles_n(layers, count), k, &split_steps);
+    }
 
     // One-token decode with a transform: the decode kernel applies it in its own
     // prologue (every workgroup on its copy of the row), no separate launch --
@@ -560,12 +575,12 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     // per layer faster at m = 4..16, 4 us slower at m = 32, where one workgroup
     // per row block adds 2048 outputs' partials and gate|up splits too
     uint32_t* ctr = nullptr;
-    if (bat && splits > 1 && m <= 16 && env_int(btl::KN_SPLIT_MERGE) != 0 && splits <= btl::kMergeMaxSplits &&
-        gemv_row_blocks(layers, count) <= btl::kSplitCounters) {
+    if (bat && splits > 1 && m <= env_int(btl::KN_SPLIT_MERGE_MAX_M) && env_int(btl::KN_SPLIT_MERGE) != 0 &&
+        splits <= btl::kMergeMaxSplits && gemv_row_blocks(layers, count, bp.nw) <= btl::kSplitCounters) {
         if ((e = btl::split_counters(dev, ws, &ctr)) != hipSuccess) return hip_fail(e, "split-K merge counters");
     }
     e = launch_gemm(layers, count, q, sxp, m, k, ykind, splits, split_steps,
-                    splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr, bat, st, ctr);
+                    splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr, bat, st, ctr, bp.nw);
     if (e != hipSuccess) return hip_fail(e, bat ? "batched gemv kernel launch" : "gemm kernel launch");
     return resid ? add_resid(layers[0], resid, m, st) : BTL_OK;
 }
@@ -1198,7 +1213,7 @@ size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)
     // splits only fall as tiles are added, so this bounds them
     int splits = btl::gemm_splits(m, ceil_div(n, 128), k, nullptr);
     if (m <= 64) {  // any BTL_GEMV_BAT_MAX_M
-        const int sb = btl::gemv_bat_split(m, ceil_div(n, 64), k, nullptr);
+        const int sb = btl::gemv_bat_plan(m, n, k).splits;
         splits = sb > splits ? sb : splits;
     }
     return ws_layout(m, k, splits > 1 ? (size_t)splits * m * n * 4 : 0).total;

@@ -35,6 +35,9 @@ enum Knob {
                              // invalid outputs and sets the device fault word)
     KN_ATTN_MERGE,           // 0: one-token attention merges its chunks in a second launch (1)
     KN_SPLIT_MERGE,          // 0: the batched decode adds its K splits in a reduce launch (1: in the launch)
+    KN_SPLIT_MERGE_MAX_M,    // ... up to this many token rows (16)
+    KN_GEMV_BAT_NW,          // force the waves per workgroup of the batched decode kernel (1..16; 0 = rule)
+    KN_GEMV_BAT_KS,          // force its K range (1024, 2048, 4096 weights; 0 = rule)
     KN_COUNT
 };
 int knob(Knob k);
@@ -156,6 +159,7 @@ struct GemmArgs {
     int splits, split_steps;
     int32_t* part;
     uint32_t* ctr;     // k_gemv_bat: merge counters (split_counters) -- splits merged in the launch; NULL: reduce launch
+    int bat_nw;        // k_gemv_bat: waves per workgroup (4, 8, 16), a row block of 16 bat_nw rows
 };
 
 constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for
@@ -166,10 +170,13 @@ int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps);
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s);
 
 // Batched decode (k_gemv_bat): the GemmArgs of a GEMM with m <= 64, k % 64
-// == 0; split_steps = 4, 8 or 16 steps of 256 weights per K split and splits
-// = ceil(k / (256 split_steps)) from gemv_bat_split; row_blocks = sum of
-// ceil(n / 64) over the layers.
-int gemv_bat_split(int64_t m, int64_t row_blocks, int64_t k, int* steps);
+// == 0; bat_nw, split_steps (4, 8 or 16 steps of 256 weights per K split)
+// and splits = ceil(k / (256 split_steps)) from gemv_bat_plan (rows = the
+// output rows of the launch's layers).
+struct BatPlan {
+    int nw, steps, splits;
+};
+BatPlan gemv_bat_plan(int64_t m, int64_t rows, int64_t k);
 hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s);
 
 // The split-K merge of k_gemv_bat inside the launch: a slot of kSplitCounters

@@ -1721,8 +1721,10 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
 // register budget does not hold the part)
 // ---------------------------------------------------------------------------
 // Weight-stationary like k_gemv_dec, with the tokens pre-quantised in operand
-// order (k_quant_op).  Workgroup: 4 waves x one 16-row weight tile = 64 rows,
-// over one K range of 256 ST weights (grid.y = K splits).  Each wave first
+// order (k_quant_op).  Workgroup: NW waves x one 16-row weight tile = 16 NW
+// rows (a row block), over one K range of 256 ST weights (grid.y = K splits):
+// the token bytes a workgroup copies per weight byte fall as 4 m / (16 NW).
+// Each wave first
 // copies its share of the token rows of that range into LDS (direct
 // global->LDS copies), then puts all ST of its weight loads in flight, so the
 // copies wait only for themselves.  The tokens are the B operand: MTB blocks of
@@ -1746,9 +1748,11 @@ __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v)
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int ST, int MTB>
-__global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
+template <int ST, int MTB, int NW>
+__global__ __launch_bounds__(NW ? NW * 64 : 1024) void k_gemv_bat(GemmArgs a)
 {
+    const int nw = NW ? NW : a.bat_nw;  // NW = 0: the waves of a.bat_nw
+    const int RBW = 16 * nw;            // rows of a row block
     extern __shared__ __align__(1024) uint8_t sx_lds[];  // [16 MTB][ks], swizzled slots
     constexpr int KS = ST * kStepWeights;                 // weights of the K range
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1768,44 +1772,67 @@ __global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
     //    slots past k read zeros or the next row: their weights are zero
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.q, (uint32_t)(M * K));
     constexpr int CPR = KS / 1024;  // copies per token row
-    for (int c = wave; c < M * CPR; c += 4) {
+    for (int c = wave; c < M * CPR; c += nw) {
         const int t = c / CPR, slot = (c - t * CPR) * 64 + lane;
         const int src = slot ^ (t & 15);
         copy_to_lds(xr, sx_lds + c * 1024, t * K + kb + src * 16);
     }
     __asm__ volatile("" ::: "memory");  // the copies stay ahead of the weight loads
 
-    // 2. every weight load of this wave in flight: lane (r, kq) holds row r,
-    //    k in [kb + 256 j + 64 kq, +64) of step j
-    const int r = lane & 15, kq = lane >> 4;
-    const int row0 = rb * 64 + wave * 16;
+    // 2. every weight load of this wave in flight, non-temporal, in pairs: load
+    //    2p + h gives lane l row 8 h + (l & 7), bytes [128 p + 16 (l >> 3), +16)
+    //    of the K range -- 8 rows x 128 contiguous bytes per instruction (16
+    //    rows x 64 bytes would split every 128-byte line over two instructions;
+    //    measured on MI355X, a 29 MB tile stream: 6.1 against 7.1 us)
+    const int kq = lane >> 4;
+    const int row0 = rb * RBW + wave * 16;
     // (uniform; readfirstlane keeps the clamp, and so the descriptor, scalar)
     const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, N - row0)));
     const int rbytes = K >> 2;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(Lw.w + (int64_t)row0 * rbytes, (uint32_t)(rows * rbytes));
+    static_assert(ST % 2 == 0, "loads come in pairs");
     uint4 buf[ST];
 #pragma unroll
-    for (int j = 0; j < ST; ++j)
-        buf[j] = bload(wr, j * kStepWeights + kq * 64 < len ? r * rbytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
+    for (int j = 0; j < ST; ++j) {
+        const int kw = (j >> 1) * 512 + (lane >> 3) * 64;  // first weight of the lane's 16 bytes
+        const int off = (8 * (j & 1) + (lane & 7)) * rbytes + (kb >> 2) + (kw >> 2);
+        buf[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, kw < len ? off : kOOB, 0,
+                                                                                 kCachePolicyNT));
+    }
     __builtin_amdgcn_sched_barrier(0);  // all ST loads issue before any of them is consumed
 
     // 3. the copies (issued first) have landed once at most ST loads are outstanding
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(ST));
     __syncthreads();
 
-    // 4. contraction: A = 16 weight rows, B = 16 token columns per block
+    // 4. contraction: A = 16 weight rows (lane l: row l & 15), B = 16 token
+    //    columns per block.  Pair p: lane l (b = bit 3 of l) holds its own row
+    //    in load 2p + b, 16-byte chunk 2 kq + b of the 128 bytes; the chunk
+    //    2 kq + 1 - b of that row sits in the other load at lane l ^ 8 (a DPP
+    //    row rotation by 8).  Word w of chunk c is token slot 32 p + 4 c + w.
     v4i acc[MTB];
 #pragma unroll
     for (int tb = 0; tb < MTB; ++tb) acc[tb] = v4i{0, 0, 0, 0};
     const int tsw = lane & 15;  // (t & 15) of this lane's token row
+    const bool hi = (lane & 8) != 0;
     const uint8_t* brow = sx_lds + (lane & 15) * KS;
 #pragma unroll
-    for (int j = 0; j < ST; ++j) {
-        const uint32_t wd[4] = {buf[j].x, buf[j].y, buf[j].z, buf[j].w};
+    for (int p = 0; p < ST / 2; ++p) {
+        const uint32_t X[4] = {buf[2 * p].x, buf[2 * p].y, buf[2 * p].z, buf[2 * p].w};
+        const uint32_t Y[4] = {buf[2 * p + 1].x, buf[2 * p + 1].y, buf[2 * p + 1].z, buf[2 * p + 1].w};
+        uint32_t wd[8];  // chunk 2 kq (words 0..3), chunk 2 kq + 1 (words 4..7)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
+            const uint32_t own = hi ? Y[w] : X[w];
+            const uint32_t give = hi ? X[w] : Y[w];
+            const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)give, 0x128, 0xF, 0xF, false);  // row_ror:8
+            wd[w] = hi ? got : own;
+            wd[4 + w] = hi ? own : got;
+        }
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
             const v4i av = unpack16(wd[w]);
-            const int slot = (16 * j + 4 * kq + w) ^ tsw;
+            const int slot = (32 * p + 8 * kq + w) ^ tsw;
 #pragma unroll
             for (int tb = 0; tb < MTB; ++tb) {
                 const v4i bv = *(const v4i*)(brow + tb * 16 * KS + slot * 16);
@@ -1849,16 +1876,16 @@ __global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
         }
         __syncthreads();
         if (!s_last) return;
-        const int rbase = rb * 64;
+        const int rbase = rb * RBW;
         const int64_t sstride = (int64_t)M * ncols;
         // four outputs per thread at a time, every split's load in flight
-        for (int o0 = tid; o0 < M * 64; o0 += 4 * 256) {
+        for (int o0 = tid; o0 < M * RBW; o0 += 4 * nw * 64) {
             uint32_t pv[4][kMergeMaxSplits];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int o = o0 + 256 * u;
-                const int t = min(o >> 6, M - 1), n = rbase + (o & 63);
-                const bool ok = o < M * 64 && n < N;
+                const int o = o0 + nw * 64 * u;
+                const int t = min(o / RBW, M - 1), n = rbase + o % RBW;
+                const bool ok = o < M * RBW && n < N;
                 const uint32_t* p = (const uint32_t*)a.part + (int64_t)t * ncols + Lw.col0 + (ok ? n : 0);
 #pragma unroll
                 for (int sp = 0; sp < kMergeMaxSplits; ++sp)
@@ -1866,9 +1893,9 @@ __global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int o = o0 + 256 * u;
-                const int t = o >> 6, n = rbase + (o & 63);
-                if (o >= M * 64 || n >= N) continue;
+                const int o = o0 + nw * 64 * u;
+                const int t = o / RBW, n = rbase + o % RBW;
+                if (o >= M * RBW || n >= N) continue;
                 int32_t sum = 0;
 #pragma unroll
                 for (int sp = 0; sp < kMergeMaxSplits; ++sp) sum += (int32_t)pv[u][sp];
@@ -1901,25 +1928,47 @@ __global__ __launch_bounds__(256) void k_gemv_bat(GemmArgs a)
     }
 }
 
-int gemv_bat_split(int64_t m, int64_t row_blocks, int64_t k, int* steps)
+BatPlan gemv_bat_plan(int64_t m, int64_t rows, int64_t k)
 {
     // LDS holds the token rows of whole 16-row blocks (16, 32 or 64 rows) x ks
-    // bytes (<= 64 KB); ks shrinks from 4096 until the launch has ~448 workgroups
+    // bytes (<= 64 KB); ks shrinks from 4096 until the launch has ~448
+    // workgroups.  4 waves per workgroup; above 16 token rows 8 when that keeps
+    // the K range (measured on MI355X, Llama-3-8B MLP at m = 32: gate|up 23.9
+    // against 25.9 us; down keeps 4 waves, with 8 its K range would halve).
+    // BTL_GEMV_BAT_NW / BTL_GEMV_BAT_KS force the waves per workgroup (1..16)
+    // and the K range (1024, 2048, 4096; tuning).
     const int64_t mr = m <= 16 ? 16 : m <= 32 ? 32 : 64;
-    int64_t ks = 4096;
-    while (ks > 1024 && (mr * ks > 65536 || row_blocks * ((k + ks - 1) / ks) < 448)) ks >>= 1;
-    if (steps) *steps = (int)(ks / kStepWeights);
-    return (int)((k + ks - 1) / ks);
+    auto range = [&](int nw) {
+        const int64_t blocks = (rows + 16 * nw - 1) / (16 * nw);
+        int64_t ks = 4096;
+        while (ks > 1024 && (mr * ks > 65536 || blocks * ((k + ks - 1) / ks) < 448)) ks >>= 1;
+        return ks;
+    };
+    BatPlan p;
+    p.nw = 4;
+    int64_t ks = range(4);
+    if (m > 16 && range(8) == ks) p.nw = 8;
+    const int fnw = knob(KN_GEMV_BAT_NW);
+    if (fnw >= 1 && fnw <= 16) {
+        p.nw = fnw;
+        ks = range(fnw);
+    }
+    const int fks = knob(KN_GEMV_BAT_KS);
+    if ((fks == 1024 || fks == 2048 || fks == 4096) && mr * fks <= 65536) ks = fks;
+    p.steps = (int)(ks / kStepWeights);
+    p.splits = (int)((k + ks - 1) / ks);
+    return p;
 }
 
 hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s)
 {
     GemmArgs g = a;
+    const int nw = g.bat_nw, rbw = 16 * nw;
     int64_t rbs = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
         g.L[l].tile0 = (int)rbs;
         g.L[l].col0 = (int)cols;
-        rbs += (g.L[l].n + 63) / 64;
+        rbs += (g.L[l].n + rbw - 1) / rbw;
         cols += g.L[l].n;
     }
     if (rbs <= 0 || g.m <= 0) return hipSuccess;
@@ -1927,18 +1976,21 @@ hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s)
     const int mr = mtb == 3 ? 64 : 16 * mtb;  // token rows the LDS tile spans (MTB = 1, 2, 4)
     const int st = g.split_steps;
     if (g.m > 64 || g.nl < 1 || g.nl > kMaxGroup || (st != 4 && st != 8 && st != 16) ||
-        (int64_t)mr * st * kStepWeights > 65536 || rbs > INT32_MAX ||
+        nw < 1 || nw > 16 || (int64_t)mr * st * kStepWeights > 65536 || rbs > INT32_MAX ||
         (g.ctr && (rbs > kSplitCounters || g.splits > kMergeMaxSplits)) ||
         g.splits != (g.k + st * kStepWeights - 1) / (st * kStepWeights) || (g.splits > 1 && !g.part))
         return hipErrorInvalidValue;
     const size_t lds = (size_t)mr * st * kStepWeights;
     const dim3 grid((unsigned)rbs, (unsigned)g.splits);
-#define BTL_BAT(STV, MTV)                                                                    \
-    if (st == STV && (mtb == MTV || (MTV == 4 && mtb == 3))) {                               \
-        hipLaunchKernelGGL((k_gemv_bat<STV, MTV>), grid, dim3(256), lds, s, g);              \
+#define BTL_BAT(STV, MTV, NWV)                                                                   \
+    if (st == STV && (NWV == 0 || nw == NWV) && (mtb == MTV || (MTV == 4 && mtb == 3))) {        \
+        hipLaunchKernelGGL((k_gemv_bat<STV, MTV, NWV>), grid, dim3(nw * 64), lds, s, g);         \
     } else
-    BTL_BAT(4, 1) BTL_BAT(4, 2) BTL_BAT(4, 4) BTL_BAT(8, 1) BTL_BAT(8, 2) BTL_BAT(8, 4)
-    BTL_BAT(16, 1) BTL_BAT(16, 2) BTL_BAT(16, 4) return hipErrorInvalidValue;
+#define BTL_BAT_NW(NWV) \
+    BTL_BAT(4, 1, NWV) BTL_BAT(4, 2, NWV) BTL_BAT(4, 4, NWV) BTL_BAT(8, 1, NWV) BTL_BAT(8, 2, NWV) \
+    BTL_BAT(8, 4, NWV) BTL_BAT(16, 1, NWV) BTL_BAT(16, 2, NWV) BTL_BAT(16, 4, NWV)
+    BTL_BAT_NW(4) BTL_BAT_NW(8) BTL_BAT_NW(16) BTL_BAT_NW(0) return hipErrorInvalidValue;
+#undef BTL_BAT_NW
 #undef BTL_BAT
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || g.splits == 1 || g.ctr) return e;
