@@ -149,8 +149,11 @@ __global__ __launch_bounds__(dec_threads(ST, XF, NI)) void k_gemv_dec(GemvArgs a
         }
     }
 
-    // 2. every weight load of this wave in flight
-    const int r = lane & 15, kq = lane >> 4;
+    // 2. every weight load of this wave in flight.  K-part form: non-temporal
+    //    pairs as in k_gemv_bat (load 2p + h: lane l reads row 8 h + (l & 7),
+    //    bytes [128 p + 16 (l >> 3), +16) of the part; 8 rows x 128 bytes per
+    //    instruction)
+    const int kq = lane >> 4;
     const int row0 = (rbg - RB0) * 16;
     const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, N - row0)));
     const int rb_bytes = K >> 2;
@@ -164,10 +167,15 @@ __global__ __launch_bounds__(dec_threads(ST, XF, NI)) void k_gemv_dec(GemvArgs a
             buf[j] = bload(wr, c * 1024 + 16 * lane < rb_bytes ? (part + WV * rho) * rb_bytes + c * 1024 + 16 * lane : kOOB);
         }
     } else {
+        static_assert(NI > 0 || ST % 2 == 0, "loads come in pairs");
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(W + (int64_t)row0 * rb_bytes, (uint32_t)(rows * rb_bytes));
 #pragma unroll
-        for (int j = 0; j < ST; ++j)
-            buf[j] = bload(wr, j * kStepWeights + kq * 64 < len ? r * rb_bytes + (kb >> 2) + kq * 16 + j * 64 : kOOB);
+        for (int j = 0; j < ST; ++j) {
+            const int kw = (j >> 1) * 512 + (lane >> 3) * 64;  // first weight of the lane's 16 bytes
+            const int off = (8 * (j & 1) + (lane & 7)) * rb_bytes + (kb >> 2) + (kw >> 2);
+            buf[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, kw < len ? off : kOOB, 0,
+                                                                                     kCachePolicyNT));
+        }
     }
 
     // 3. absmax of each token row over the workgroup; lane m then holds the
@@ -355,25 +363,35 @@ __global__ __launch_bounds__(dec_threads(ST, XF, NI)) void k_gemv_dec(GemvArgs a
         return;
     }
 
-    // 5. contraction.  B lanes of token columns >= mt read row 0: those
-    //    columns of D are never stored.
+    // 5. contraction: lane l holds row l & 15 after the pair exchange of
+    //    k_gemv_bat (chunk 2 kq + b from load 2p + b, chunk 2 kq + 1 - b from
+    //    lane l ^ 8 of the other load, b = bit 3 of l); word w of the 32 bytes
+    //    takes the 16 activations at k = kb + 512 p + 128 kq + 16 w.  B lanes of
+    //    token columns >= mt read row 0: those columns of D are never stored.
     const int mcol = lane & 15;
     const bool m_ok = mcol < mt;
-    const uint8_t* bq = sq + (m_ok ? mcol : 0) * lp + kb + kq * 64;
+    const bool hi = (lane & 8) != 0;
+    const uint8_t* bq = sq + (m_ok ? mcol : 0) * lp + kb + kq * 128;
     v4i acc[2];
     acc[0] = acc[1] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < ST; ++j) {
-        const uint8_t* bj = bq + j * kStepWeights;
-        const v4i b0 = *(const v4i*)(bj + 0);
-        const v4i b1 = *(const v4i*)(bj + 16);
-        const v4i b2 = *(const v4i*)(bj + 32);
-        const v4i b3 = *(const v4i*)(bj + 48);
-        const uint4 cur = buf[j];
-        acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.x), b0, acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.y), b1, acc[1], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.z), b2, acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(cur.w), b3, acc[1], 0, 0, 0);
+    for (int p = 0; p < ST / 2; ++p) {
+        const uint8_t* bj = bq + p * 512;
+        const uint32_t X[4] = {buf[2 * p].x, buf[2 * p].y, buf[2 * p].z, buf[2 * p].w};
+        const uint32_t Y[4] = {buf[2 * p + 1].x, buf[2 * p + 1].y, buf[2 * p + 1].z, buf[2 * p + 1].w};
+        uint32_t wd[8];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t own = hi ? Y[w] : X[w];
+            const uint32_t give = hi ? X[w] : Y[w];
+            const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)give, 0x128, 0xF, 0xF, false);  // row_ror:8
+            wd[w] = hi ? got : own;
+            wd[4 + w] = hi ? own : got;
+        }
+#pragma unroll
+        for (int w = 0; w < 8; ++w)
+            acc[w & 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(unpack16(wd[w]), *(const v4i*)(bj + 16 * w), acc[w & 1],
+                                                              0, 0, 0);
     }
     v4i res = acc[0] + acc[1];
 
@@ -449,7 +467,10 @@ hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t 
          (xform == XF_SWIGLU && (a.k >> 4) > 2 * wv * rb * 64) || (a.hout && (const void*)a.hout == a.x)))
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.rb_total + rb - 1) / rb)), block((unsigned)(wv * rb * 64));
-    const size_t lds = (size_t)a.m * (size_t)(a.k + 16);
+    // the token rows, plus what the last K part reads past the last row (its
+    // weights there are zero) when the parts overrun k
+    const size_t lds = (size_t)a.m * (size_t)(a.k + 16) +
+                       (a.rowc == 0 && (int64_t)wv * a.kpart > a.k ? (size_t)((int64_t)wv * a.kpart - a.k) : 0);
     const bool pr = a.swiglu_out != nullptr;
     if (a.rowc != 0) {
         // (chunks, waves per row block) -> loads per wave ST = chunks * 16 / waves
