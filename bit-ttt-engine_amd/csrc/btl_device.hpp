@@ -27,6 +27,22 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, int off)
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane, global (descriptor r, byte offset voff) -> LDS lds + 16 * lane.
+// Offsets outside the descriptor range read as zero.
+__device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int voff)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 layout: vmcnt bits
+// 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// s_waitcnt vmcnt(0): every global load (and LDS copy) of this wave has landed.
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); }
+
 // Max of a u32 over the wave, via DPP (quad perms, row rotations, row
 // broadcasts); the result is read from lane 63.  The DPP source reads 0 (the
 // identity of the max) where a lane is masked, which lets the compiler fold

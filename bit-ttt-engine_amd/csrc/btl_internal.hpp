@@ -38,6 +38,7 @@ enum Knob {
     KN_SPLIT_MERGE_MAX_M,    // ... up to this many token rows (16)
     KN_GEMV_BAT_NW,          // force the waves per workgroup of the batched decode kernel (1..16; 0 = rule)
     KN_GEMV_BAT_KS,          // force its K range (1024, 2048, 4096 weights; 0 = rule)
+    KN_GEMM_TILE,            // force the prefill GEMM tile (1: 128 rows, 2: 256 rows; 0 = rule)
     KN_COUNT
 };
 int knob(Knob k);

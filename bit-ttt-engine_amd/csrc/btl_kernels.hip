@@ -675,12 +675,12 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
     constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;
     constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;
     // Two groups per thread (RMSNorm only, the SwiGLU pairing): the token row
-    // and the norm weight would need all 64 registers at once, so after the
-    // sum of squares the row waits in LDS (uint4 h of group gi of thread t at
-    // sxs[(4 gi + h) nq + t], after the operand row) while the norm-weight
-    // loads, issued then, are in flight.
+    // and the norm weight would need all 64 registers at once, so the norm
+    // weight was copied into LDS (sg, after the operand row) by the kernel's
+    // first instructions, ahead of every weight load of the workgroup, and is
+    // read from there group by group.
     constexpr bool GL = XN && DG == 2;
-    uint4* const sxs = (uint4*)(sq + K + 16);
+    const uint4* const sg = (const uint4*)(sq + K + 16);
     float fv[DG][16];
 #pragma unroll
     for (int gi = 0; gi < DG; ++gi) {
@@ -716,20 +716,10 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
             const float ws = wave_pairwise_sum(t[0]);
             if (lane == 0) s_ss[gi * nqw + wave] = ws;
         }
-        uint4 gl[GL ? DG : 1][4];
-        if constexpr (GL) {
-#pragma unroll
-            for (int gi = 0; gi < DG; ++gi)
-#pragma unroll
-                for (int h = 0; h < 4; ++h) sxs[(4 * gi + h) * nq + tid] = xv[gi][h];
-            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
-#pragma unroll
-            for (int gi = 0; gi < DG; ++gi) {
-                const int g = tid + nq * gi;
-#pragma unroll
-                for (int h = 0; h < 4; ++h) gl[gi][h] = bload(gr, g < gpr ? 64 * g + 16 * h : kOOB);
-            }
-        }
+        // GL: this wave's copies of the norm weight are in LDS (its only
+        // outstanding vector-memory operations); every quantising wave's are
+        // once the arrivals below are complete
+        if constexpr (GL) wait_loads();
         if (lane == 0) {
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the sums are in LDS
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -749,12 +739,14 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
 #pragma unroll
         for (int gi = 0; gi < DG; ++gi) {
             float gf[16];
-            widen16<XK_F32>(GL ? gl[gi] : gv[gi], gf);
             if constexpr (GL) {
-                uint4 xl[4];
+                const int g = min(tid + nq * gi, gpr - 1);  // past k: any group (never stored)
+                uint4 gl[4];
 #pragma unroll
-                for (int h = 0; h < 4; ++h) xl[h] = sxs[(4 * gi + h) * nq + tid];
-                widen16<XK_F32>(xl, fv[gi]);
+                for (int h = 0; h < 4; ++h) gl[h] = sg[4 * g + h];
+                widen16<XK_F32>(gl, gf);
+            } else {
+                widen16<XK_F32>(gv[gi], gf);
             }
 #pragma unroll
             for (int e = 0; e < 16; ++e) fv[gi][e] = __fmul_rn(__fdiv_rn(fv[gi][e], d), gf[e]);
@@ -831,7 +823,13 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
 #pragma unroll
             for (int h = 0; h < NV; ++h) xv[gi][h] = bload(xr, g < mt * gpr ? 16 * g * ES + 16 * h : kOOB);
         }
-        uint4 gv[XN ? DG : 1][4];  // the norm weight (two groups per thread: loaded later)
+        uint4 gv[XN ? DG : 1][4];  // the norm weight (two groups per thread: copied into LDS)
+        if constexpr (XN && DG == 2) {
+            // 1 KB copies of the norm weight into LDS after the operand row,
+            // spread over the quantising waves (zeros past k)
+            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
+            for (int c = wave; c < (K * 4 + 1023) / 1024; c += nqw) copy_to_lds(gr, sq + K + 16 + c * 1024, c * 1024 + 16 * lane);
+        }
 #pragma unroll
         for (int gi = 0; gi < (XF != XF_NONE && !(XN && DG == 2) ? DG : 0); ++gi) {
             const int g = tid + nq * gi;
@@ -1022,8 +1020,8 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
         const int64_t groups = pair ? ((int64_t)a.p[0].n + 3) / 4 : (int64_t)a.rb_total * 4;
         const int64_t per = pair ? a.parts / 2 : a.parts;
         const dim3 grid((unsigned)((groups + per - 1) / per)), block((unsigned)((nqw + a.parts) * 64));
-        // the operand row; with the pairing also the staged f32 row (64 B per group)
-        const size_t lds = (size_t)a.k + 16 + (pair ? (size_t)dg * 64 * nqw * 64 : 0);
+        // the operand row; with the pairing also the norm weight (f32, whole 1 KB copies)
+        const size_t lds = (size_t)a.k + 16 + (pair ? ((size_t)a.k * 4 + 1023) / 1024 * 1024 : 0);
 #define BTL_RQ_XF(STV)                                                                                        \
     if (pair) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, true, XF_RMSNORM, 2>), grid, block, lds, s, a);       \
     else if (xform == XF_RMSNORM) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_RMSNORM, 1>), grid, block, lds, s, a); \
@@ -1440,22 +1438,6 @@ constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 128;
 constexpr int kGemmABytes = kGemmBM * kGemmBK;      // 16 KB
 constexpr int kGemmACh = kGemmABytes / 1024 / 4;    // A copies (1 KB) per wave per step
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// 16 bytes per lane, global (descriptor r, byte offset voff) -> LDS lds + 16 * lane.
-// Offsets outside the descriptor range read as zero.
-__device__ __forceinline__ void copy_to_lds(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int voff)
-{
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
-}
-
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 layout: vmcnt bits
-// 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-
-// s_waitcnt vmcnt(0): every global load (and LDS copy) of this wave has landed.
-__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); }
-
 template <int TN, int WGN, int NW = 4>
 __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
 {
@@ -1711,7 +1693,13 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     int64_t tn256 = 0;
     for (int l = 0; l < g.nl; ++l) tn256 += (g.L[l].n + 255) / 256;
     const int64_t wide_min = knob(KN_GEMM_WIDE_MIN_TILES);
-    const int TN = g.splits <= 1 && tiles_m * tn256 >= wide_min ? 256 : 128;
+    int TN = g.splits <= 1 && tiles_m * tn256 >= wide_min ? 256 : 128;
+    // BTL_GEMM_TILE forces the tile (tuning): 1 = 128 rows (2 x 2 waves), 2 =
+    // 256 rows (1 x 4 waves).  (A 256-row tile of 2 x 4 waves, each 64 x 64,
+    // measured slower for every Llama-3-8B prefill shape: gate|up 227 against
+    // 195 us.)
+    const int ftile = knob(KN_GEMM_TILE);
+    if (ftile == 1 || ftile == 2) TN = ftile == 1 ? 128 : 256;
     int64_t tn = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
         g.L[l].tile0 = (int)tn;
