@@ -365,10 +365,10 @@ def test_add_rmsnorm_swiglu(m, k, n, fuse, with_delta, tune):
     # decode rows (m <= 4): the gate/up kernel writes silu(gate) * up from its epilogue.
     # One row, 1024 <= k <= 4096: without delta the RMSNorm runs in the quantising
     # waves of the row-group form's gate/up pairing (two token groups per thread,
-    # the row staged in LDS; k = 3008 leaves half-empty groups and a zero block);
-    # with delta a separate one-workgroup transform runs first.  fuse "0" forces
-    # the separate norm kernel (row-group pairing with ragged n: rows past the end
-    # of a workgroup's span)
+    # the norm weight copied into LDS at the start; k = 3008 leaves half-empty
+    # groups and a zero block); with delta a separate one-workgroup transform runs
+    # first.  fuse "0" forces the separate norm kernel (row-group pairing with
+    # ragged n: rows past the end of a workgroup's span)
     print("add_rmsnorm_swiglu", m, k, n, fuse, with_delta, flush=True)
     tune("BTL_FUSE_DEC", fuse)
     rng = np.random.default_rng(m * 31 + k + n)
