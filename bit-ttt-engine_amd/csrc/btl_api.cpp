@@ -103,7 +103,7 @@ constexpr KnobDef kKnobs[btl::KN_COUNT] = {
     {"BTL_GEMM_MAX_SPLITS", 0}, {"BTL_GEMM_WIDE_MIN_TILES", btl::kGemmWideMinTiles},
     {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1}, {"BTL_SPLIT_MERGE", 1},
     {"BTL_SPLIT_MERGE_MAX_M", 16}, {"BTL_GEMV_BAT_NW", 0}, {"BTL_GEMV_BAT_KS", 0},
-    {"BTL_GEMM_TILE", 0},
+    {"BTL_GEMM_TILE", 0}, {"BTL_GEMM_TM64", 1}, {"BTL_GEMM_TM64_STAGES", 0},
 };
 std::atomic<int> g_knob[btl::KN_COUNT];
 std::once_flag g_knob_once;
@@ -441,7 +441,14 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         if (!dec || wv > 8) return fail(BTL_ERR_ARG, "SwiGLU epilogue needs the decode route");
         rbw = 2;  // workgroup w: row block w of gate and of up
     }
-    const bool bat = !dec && m <= env_int(btl::KN_GEMV_BAT_MAX_M) && m <= 64 && env_int(btl::KN_GEMV_BAT) != 0;
+    // Batched decode up to KN_GEMV_BAT_MAX_M rows -- but from 21 rows on, a
+    // layer group wide enough for the unsplit 64-token GEMM takes that
+    // (measured on MI355X, Llama-3-8B gate|up: m = 20 19.6 against 20.8 us, m =
+    // 24 21.3 against 20.8, m = 32 23.3 against 21.0)
+    const bool gemm_wide = m > 20 && m <= 64 && gemm_tiles_n(layers, count) >= btl::kGemmSmallMUnsplit &&
+                           env_int(btl::KN_GEMM_TM64) != 0;
+    const bool bat = !dec && !gemm_wide && m <= env_int(btl::KN_GEMV_BAT_MAX_M) && m <= 64 &&
+                     env_int(btl::KN_GEMV_BAT) != 0;
     int split_steps = 0, splits = 1;
     btl::BatPlan bp{4, 0, 1};
     if (bat) {

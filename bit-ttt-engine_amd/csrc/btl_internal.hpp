@@ -39,6 +39,8 @@ enum Knob {
     KN_GEMV_BAT_NW,          // force the waves per workgroup of the batched decode kernel (1..16; 0 = rule)
     KN_GEMV_BAT_KS,          // force its K range (1024, 2048, 4096 weights; 0 = rule)
     KN_GEMM_TILE,            // force the prefill GEMM tile (1: 128 rows, 2: 256 rows; 0 = rule)
+    KN_GEMM_TM64,            // 0: the GEMM keeps 128-token tiles for m <= 64 (1: 64-token tiles)
+    KN_GEMM_TM64_STAGES,     // force the LDS stages of the 64-token tiles (2 or 4; 0 = rule)
     KN_COUNT
 };
 int knob(Knob k);
@@ -164,6 +166,10 @@ struct GemmArgs {
 };
 
 constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for
+// up to 64 token rows, a GEMM of at least this many 128-row tiles runs unsplit
+// (64-token tiles, 4 LDS stages; measured on MI355X, Llama-3-8B gate|up at
+// m = 24..64: 19-21 us against 31 split three ways)
+constexpr int kGemmSmallMUnsplit = 192;
 constexpr int kGemmWideMinTiles = 512;  // 256-row GEMM tiles from this many workgroups on
 // K splits for an (m, ncols, k) GEMM: enough workgroups to cover the chip when
 // the output has few tiles (small m); 1 when it already has kGemmSplitTarget.

@@ -1438,30 +1438,31 @@ hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, h
 //   B [half j][column 0..TN-1][16 B]: the packed word kq of a column at byte
 //     4 kq, so a read of 16 columns x 4 words covers the 64 banks once.
 // Each wave unpacks the 4 weight words of its 64 columns per half step.
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 128;
-constexpr int kGemmABytes = kGemmBM * kGemmBK;      // 16 KB
-constexpr int kGemmACh = kGemmABytes / 1024 / 4;    // A copies (1 KB) per wave per step
+constexpr int kGemmBM = 128, kGemmBK = 128;  // token rows of the prefill tile, K step
 
-template <int TN, int WGN, int NW = 4>
+template <int TN, int WGN, int NW = 4, int TM = 128, int NS = 2>
 __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
 {
+    static_assert(TM == 128 || TM == 64, "token tile of 128 or 64 rows");
+    static_assert(NS >= 2 && NS <= 8, "2 to 8 LDS stages");
+    constexpr int ABytes = TM * kGemmBK;
     static_assert(TN == 128 || TN == 256, "tile of 128 or 256 output rows");
     static_assert(NW == 4 && (WGN == 2 || WGN == 4), "2 x 2 or 1 x 4 waves");
     constexpr int WGM = NW / WGN;              // waves along the tokens
-    constexpr int TMB = kGemmBM / 16 / WGM;    // 16-token blocks per wave
+    constexpr int TMB = TM / 16 / WGM;         // 16-token blocks per wave
     constexpr int TNB = TN / 16 / WGN;         // 16-row weight blocks per wave
     constexpr int BBytes = TN * kGemmBK / 4;
-    constexpr int Stage = kGemmABytes + BBytes;
-    constexpr int ACh = kGemmABytes / 1024 / NW;  // A copies (1 KB) per wave per step
+    constexpr int Stage = ABytes + BBytes;
+    constexpr int ACh = ABytes / 1024 / NW;  // A copies (1 KB) per wave per step
     constexpr int BCh = BBytes / 1024 / NW;       // B copies (1 KB) per wave per step
-    __shared__ __align__(1024) uint8_t lds[2 * Stage];
+    __shared__ __align__(1024) uint8_t lds[NS * Stage];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     // consecutive workgroups go to consecutive XCDs: with tm = bid % tiles_m
     // each XCD keeps re-reading the same activation row tiles from its L2
-    const int tiles_m = (a.m + kGemmBM - 1) / kGemmBM;
+    const int tiles_m = (a.m + TM - 1) / TM;
     const int tm = blockIdx.x % tiles_m;
     int tn = blockIdx.x / tiles_m;
     // the layers of a group share the activations: output tiles are numbered
@@ -1471,9 +1472,9 @@ __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
     for (int i = 1; i < kMaxGroup; ++i)
         if (i < a.nl && tn >= a.L[i].tile0) Lw = a.L[i];
     tn -= Lw.tile0;
-    const int m0 = tm * kGemmBM, n0 = tn * TN;
+    const int m0 = tm * TM, n0 = tn * TN;
     const int K = a.k, N = Lw.n;
-    const int rows_a = min(kGemmBM, a.m - m0), rows_b = min(TN, N - n0);
+    const int rows_a = min(TM, a.m - m0), rows_b = min(TN, N - n0);
     const int split = blockIdx.y;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.q + (int64_t)m0 * K, (uint32_t)(rows_a * K));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(Lw.w + (int64_t)n0 * (K >> 2), (uint32_t)(rows_b * (K >> 2)));
@@ -1486,7 +1487,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
 #pragma unroll
     for (int i = 0; i < ACh; ++i) {
         const int c = wave * ACh + i;
-        const int j = c / (kGemmBM / 16), row = (c % (kGemmBM / 16)) * 16 + (lane >> 2);
+        const int j = c / (TM / 16), row = (c % (TM / 16)) * 16 + (lane >> 2);
         const int grp = (lane & 3) ^ ((row >> 1) & 3);
         aoff[i] = row * K + j * 64 + grp * 16;
     }
@@ -1504,7 +1505,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
 #pragma unroll
         for (int i = 0; i < ACh; ++i) copy_to_lds(ra, base + (wave * ACh + i) * 1024, aoff[i] + ko);
 #pragma unroll
-        for (int i = 0; i < BCh; ++i) copy_to_lds(rb, base + kGemmABytes + (wave * BCh + i) * 1024, boff[i] + (ko >> 2));
+        for (int i = 0; i < BCh; ++i) copy_to_lds(rb, base + ABytes + (wave * BCh + i) * 1024, boff[i] + (ko >> 2));
     };
 
     v4i acc[TMB][TNB];
@@ -1516,12 +1517,12 @@ __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
     const int r16 = lane & 15, kq = lane >> 4;
     // row = wm TMB 16 + 16 b + r16, so (row >> 1) & 3 == (r16 >> 1) & 3
     const int aread = (wm * TMB * 16 + r16) * 64 + ((kq ^ ((r16 >> 1) & 3)) * 16);
-    const int bread = kGemmABytes + (wn * TNB * 16 + r16) * 16 + kq * 4;
+    const int bread = ABytes + (wn * TNB * 16 + r16) * 16 + kq * 4;
     auto compute_half = [&](const uint8_t* base, int j) {
         v4i bop[TNB];
 #pragma unroll
         for (int c = 0; c < TNB; ++c) bop[c] = unpack16(*(const uint32_t*)(base + bread + j * (TN * 16) + c * 256));
-        const uint8_t* ab = base + j * (kGemmBM * 64) + aread;
+        const uint8_t* ab = base + j * (TM * 64) + aread;
 #pragma unroll
         for (int b = 0; b < TMB; ++b) {
             const v4i aop = *(const v4i*)(ab + b * 1024);
@@ -1534,23 +1535,61 @@ __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
     // every step but the last has both halves, and the loop body no branch
     // (one basic block: the scheduler can overlap a half's unpack with the
     // other half's MFMAs)
-    if (st_begin < st_end) issue(st_begin, 0);
-    int st = st_begin;
-    for (; st + 1 < st_end; ++st) {
-        const int stage = (st - st_begin) & 1;
-        wait_loads();     // this wave's copies of step st are in LDS
-        __syncthreads();  // ... every wave's; and the other stage is no longer read
-        issue(st + 1, stage ^ 1);
-        const uint8_t* base = lds + stage * Stage;
-        compute_half(base, 0);
-        compute_half(base, 1);
-    }
-    if (st < st_end) {
-        wait_loads();
-        __syncthreads();
-        const uint8_t* base = lds + ((st - st_begin) & 1) * Stage;
-        compute_half(base, 0);
-        if (st * kGemmBK + 64 < K) compute_half(base, 1);  // k % 128 == 64: the last step is half
+    if constexpr (NS == 2) {
+        if (st_begin < st_end) issue(st_begin, 0);
+        int st = st_begin;
+        for (; st + 1 < st_end; ++st) {
+            const int stage = (st - st_begin) & 1;
+            wait_loads();     // this wave's copies of step st are in LDS
+            __syncthreads();  // ... every wave's; and the other stage is no longer read
+            issue(st + 1, stage ^ 1);
+            const uint8_t* base = lds + stage * Stage;
+            compute_half(base, 0);
+            compute_half(base, 1);
+        }
+        if (st < st_end) {
+            wait_loads();
+            __syncthreads();
+            const uint8_t* base = lds + ((st - st_begin) & 1) * Stage;
+            compute_half(base, 0);
+            if (st * kGemmBK + 64 < K) compute_half(base, 1);  // k % 128 == 64: the last step is half
+        }
+    } else {
+        // NS stages (few workgroups per CU: more of the copies' latency to hide):
+        // the copies of NS - 1 steps in flight; at step st those of st + 1 ..
+        // st + NS - 2 may still be outstanding, (NS - 2) (ACh + BCh) per wave
+        constexpr int CPS = ACh + BCh;
+        for (int i = 0; i < NS - 1; ++i)
+            if (st_begin + i < st_end) issue(st_begin + i, i);
+        int st = st_begin;
+        // NS steps per iteration, so every stage index is a constant (the
+        // compiler then sees which copies each LDS read depends on)
+        for (; st + 2 * NS - 2 < st_end; st += NS) {
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                // a barrier without the workgroup fence of __syncthreads (whose
+                // release waits for every outstanding copy, vmcnt(0)); the empty
+                // asm statements keep the compiler from moving LDS accesses
+                // across it
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * CPS));
+                __asm__ volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();  // every wave's copies of step st + i; stage i - 1 is no longer read
+                __asm__ volatile("" ::: "memory");
+                issue(st + i + NS - 1, (i + NS - 1) % NS);
+                const uint8_t* base = lds + i * Stage;
+                compute_half(base, 0);
+                compute_half(base, 1);
+            }
+        }
+        for (; st < st_end; ++st) {  // the last steps
+            const int rel = st - st_begin;
+            wait_loads();
+            __syncthreads();
+            if (st + NS - 1 < st_end) issue(st + NS - 1, (rel + NS - 1) % NS);
+            const uint8_t* base = lds + (rel % NS) * Stage;
+            compute_half(base, 0);
+            if (st + 1 < st_end || st * kGemmBK + 64 < K) compute_half(base, 1);
+        }
     }
 
     if (a.splits > 1) {
@@ -1577,7 +1616,7 @@ __global__ __launch_bounds__(NW * 64, 2) void k_gemm_i8(GemmArgs a)
     // case) takes the short path: one row address per token row, no bounds
     // checks, the output kind tested once.
     const bool ybf = a.ykind == YK_BF16;
-    if (m0 + kGemmBM <= a.m && n0 + TN <= N) {
+    if (m0 + TM <= a.m && n0 + TN <= N) {
         const int nb = n0 + wn * TNB * 16 + r16;
         float cmv[TMB][4];  // every token scale load in flight before the first use
 #pragma unroll
@@ -1676,6 +1715,11 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(GemmArgs a, int ncols)
 int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps)
 {
     const int64_t steps = (k + kGemmBK - 1) / kGemmBK;
+    if (m <= 64 && tiles_n >= kGemmSmallMUnsplit && knob(KN_GEMM_TM64) != 0) {
+        // 64-token tiles that already cover most CUs: no split, no partials
+        if (split_steps) *split_steps = (int)steps;
+        return 1;
+    }
     const int64_t tiles = (m + kGemmBM - 1) / kGemmBM * tiles_n;
     int64_t s = tiles >= kGemmSplitTarget || tiles <= 0 ? 1 : (kGemmSplitTarget + tiles - 1) / tiles;
     const int cap = knob(KN_GEMM_MAX_SPLITS);  // tuning / tests: 1 turns split-K off
@@ -1704,6 +1748,12 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     // 195 us.)
     const int ftile = knob(KN_GEMM_TILE);
     if (ftile == 1 || ftile == 2) TN = ftile == 1 ? 128 : 256;
+    // up to 64 token rows: tiles of 64 tokens (a 128-row tile would be half
+    // zero-filled, its MFMAs and LDS reads half wasted), 256 rows wide when
+    // split (measured on MI355X, Llama-3-8B down at m = 24..64); BTL_GEMM_TM64
+    // = 0 keeps 128
+    const bool tm64 = g.m <= 64 && knob(KN_GEMM_TM64) != 0;
+    if (tm64 && g.splits > 1 && ftile != 1) TN = 256;
     int64_t tn = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
         g.L[l].tile0 = (int)tn;
@@ -1719,7 +1769,16 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     if (g.splits > 1 && (!g.part || g.split_steps < 1 || (int64_t)g.splits * g.m * cols > INT32_MAX))
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)tiles, (unsigned)g.splits);
-    if (TN == 256) hipLaunchKernelGGL((k_gemm_i8<256, 4>), grid, dim3(256), 0, s, g);
+    // 64-token tiles: unsplit, 4 LDS stages (one workgroup per CU has the
+    // copies' latency to hide); split, 2 (a split's few K steps would run
+    // mostly in the stages' tail); BTL_GEMM_TM64_STAGES = 2 or 4 forces it
+    const int fns = knob(KN_GEMM_TM64_STAGES);
+    const int ns = fns == 2 || fns == 4 ? fns : (g.splits > 1 ? 2 : 4);
+    if (TN == 256 && tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64, 4>), grid, dim3(256), 0, s, g);
+    else if (TN == 256 && tm64) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64>), grid, dim3(256), 0, s, g);
+    else if (TN == 256) hipLaunchKernelGGL((k_gemm_i8<256, 4>), grid, dim3(256), 0, s, g);
+    else if (tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64, 4>), grid, dim3(256), 0, s, g);
+    else if (tm64) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64>), grid, dim3(256), 0, s, g);
     else hipLaunchKernelGGL((k_gemm_i8<128, 2>), grid, dim3(256), 0, s, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || g.splits == 1) return e;

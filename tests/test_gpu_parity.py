@@ -363,6 +363,58 @@ def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, tune):
         assert_bf16_matches(y, yr)
 
 
+# 21..64 token rows on a layer group of at least 192 tiles of 128 rows: the
+# GEMM's 64-token tiles, unsplit, 4 LDS stages (steady loop of 4 steps + tail).
+# k = 1088: 9 steps, the last one half; k = 4096: 32 steps; n ragged.  Checked
+# bit for bit against the 128-token tiles (BTL_GEMM_TM64 = 0, the prefill
+# kernel the oracle tests pin) and, on the smaller shape, against the oracle.
+@pytest.mark.parametrize("m,k,ns", [(24, 1088, (24576 + 70,)), (64, 4096, (14336, 14336)), (40, 2048, (12288, 12288 + 130))])
+def test_small_m_gemm_unsplit_stages(m, k, ns, tune):
+    print("small-m gemm", m, k, ns, flush=True)
+    x = to_dev(activations(m, k, seed=m + k), torch.bfloat16)
+    layers = [make_layer(n, k, seed=n + 7 * i) for i, n in enumerate(ns)]
+
+    def run():
+        if len(ns) == 1:  # one layer: the int32 sums too
+            acc = torch.empty((m, ns[0]), dtype=torch.int32, device=DEV)
+            return [bl.BitLinearHip.forward(x, layers[0][0], out_dtype=torch.float32, acc_out=acc)], [acc]
+        return bl.linear_group([l[0] for l in layers], x, out_dtype=torch.float32), []
+
+    got, accs = run()
+    tune("BTL_GEMM_TM64", 0)
+    ref, accs0 = run()
+    for y, y0 in zip(got, ref):
+        assert torch.equal(y, y0)
+    for a, a0 in zip(accs, accs0):
+        assert torch.equal(a, a0)
+    if len(ns) == 1:
+        pt, wb, sw = layers[0]
+        yr, _, _, accr = orc.forward_i8(host_x(x), wb, ns[0], sw)
+        assert np.array_equal(accs[0].cpu().numpy(), accr)
+        assert_f32_identical(got[0], yr)
+
+
+# the 64-token tiles with a K split: 256-row tiles (2 stages by the rule, 4
+# forced), and the 128-row tile forced; every form against the 128-token tiles
+@pytest.mark.parametrize("m,k,n", [(48, 14336, 4096), (64, 1088, 1000), (33, 8192, 200)])
+@pytest.mark.parametrize("stages,tile", [(0, 0), (4, 0), (2, 1), (4, 1)])
+def test_small_m_gemm_split_forms(m, k, n, stages, tile, tune):
+    print("small-m gemm split", m, k, n, stages, tile, flush=True)
+    tune("BTL_GEMV_BAT", 0)
+    x = to_dev(activations(m, k, seed=3 * m + k), torch.bfloat16)
+    pt, wb, sw = make_layer(n, k, seed=n + k)
+    tune("BTL_GEMM_TM64", 0)
+    acc0 = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y0 = bl.BitLinearHip.forward(x, pt, out_dtype=torch.float32, acc_out=acc0)
+    tune("BTL_GEMM_TM64", 1)
+    tune("BTL_GEMM_TM64_STAGES", stages)
+    tune("BTL_GEMM_TILE", tile)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(x, pt, out_dtype=torch.float32, acc_out=acc)
+    assert torch.equal(acc, acc0)
+    assert torch.equal(y, y0)
+
+
 @pytest.mark.parametrize("m,k,ns", [(20, 2048, (100, 64, 64)), (7, 14336, (300, 64)), (64, 4096, (1000, 200, 200))])
 def test_split_k_group_with_exact_caller_workspace(m, k, ns):
     # a group's layers share one split-K launch; btl_workspace_bytes(m, sum n, k)
