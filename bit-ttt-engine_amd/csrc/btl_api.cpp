@@ -103,7 +103,7 @@ constexpr KnobDef kKnobs[btl::KN_COUNT] = {
     {"BTL_GEMM_MAX_SPLITS", 0}, {"BTL_GEMM_WIDE_MIN_TILES", btl::kGemmWideMinTiles},
     {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1}, {"BTL_SPLIT_MERGE", 1},
     {"BTL_SPLIT_MERGE_MAX_M", 16}, {"BTL_GEMV_BAT_NW", 0}, {"BTL_GEMV_BAT_KS", 0},
-    {"BTL_GEMM_TILE", 0}, {"BTL_GEMM_TM64", 1}, {"BTL_GEMM_TM64_STAGES", 0},
+    {"BTL_GEMM_TILE", 0}, {"BTL_GEMM_TM64", 1}, {"BTL_GEMM_TM64_STAGES", 0}, {"BTL_GEMM_STAGES", 0},
 };
 std::atomic<int> g_knob[btl::KN_COUNT];
 std::once_flag g_knob_once;
@@ -245,6 +245,8 @@ hipError_t launch_gemm(const Layer* layers, int count, const int8_t* q, const fl
     g.part = part;
     g.ctr = ctr;
     g.bat_nw = bat_nw;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices) g.cus = g_dev[dev].cus;
     for (int i = 0; i < count; ++i) {
         if (layers[i].w->n == 0) continue;
         btl::GemmLayer& L = g.L[g.nl++];

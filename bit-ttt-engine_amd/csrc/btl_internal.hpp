@@ -41,6 +41,7 @@ enum Knob {
     KN_GEMM_TILE,            // force the prefill GEMM tile (1: 128 rows, 2: 256 rows; 0 = rule)
     KN_GEMM_TM64,            // 0: the GEMM keeps 128-token tiles for m <= 64 (1: 64-token tiles)
     KN_GEMM_TM64_STAGES,     // force the LDS stages of the 64-token tiles (2 or 4; 0 = rule)
+    KN_GEMM_STAGES,          // force the LDS stages of the 128-token tiles (2 or 3; 0 = rule)
     KN_COUNT
 };
 int knob(Knob k);
@@ -163,6 +164,7 @@ struct GemmArgs {
     int32_t* part;
     uint32_t* ctr;     // k_gemv_bat: merge counters (split_counters) -- splits merged in the launch; NULL: reduce launch
     int bat_nw;        // k_gemv_bat: waves per workgroup (4, 8, 16), a row block of 16 bat_nw rows
+    int cus;           // compute units of the device (0: unknown), for the GEMM's stage count
 };
 
 constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for

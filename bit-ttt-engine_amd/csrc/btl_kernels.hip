@@ -1774,10 +1774,19 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     // mostly in the stages' tail); BTL_GEMM_TM64_STAGES = 2 or 4 forces it
     const int fns = knob(KN_GEMM_TM64_STAGES);
     const int ns = fns == 2 || fns == 4 ? fns : (g.splits > 1 ? 2 : 4);
+    // 128-token tiles: 3 LDS stages when every workgroup is resident at two per
+    // CU (3 stages fit two, 2 stages three): measured on MI355X, Llama-3-8B
+    // M = 2048, o 37.5 -> 36.5 and down 116.2 -> 111.5 us with 3 (512
+    // workgroups); q|k|v (768) 48.9 -> 51.6 and gate|up (1792) 194.6 -> 200.2 keep 2
+    const int fps = knob(KN_GEMM_STAGES);
+    const int64_t wgs = tiles * g.splits;
+    const int pns = fps == 2 || fps == 3 ? fps : (g.cus > 0 && wgs <= 2 * g.cus ? 3 : 2);
     if (TN == 256 && tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64, 4>), grid, dim3(256), 0, s, g);
     else if (TN == 256 && tm64) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64>), grid, dim3(256), 0, s, g);
+    else if (TN == 256 && pns == 3) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 128, 3>), grid, dim3(256), 0, s, g);
     else if (TN == 256) hipLaunchKernelGGL((k_gemm_i8<256, 4>), grid, dim3(256), 0, s, g);
     else if (tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64, 4>), grid, dim3(256), 0, s, g);
+    else if (!tm64 && pns == 3) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 128, 3>), grid, dim3(256), 0, s, g);
     else if (tm64) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64>), grid, dim3(256), 0, s, g);
     else hipLaunchKernelGGL((k_gemm_i8<128, 2>), grid, dim3(256), 0, s, g);
     hipError_t e = hipGetLastError();
