@@ -1754,6 +1754,11 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     // = 0 keeps 128
     const bool tm64 = g.m <= 64 && knob(KN_GEMM_TM64) != 0;
     if (tm64 && g.splits > 1 && ftile != 1) TN = 256;
+    // a long K whose 256-row tiles give at most one workgroup per CU: 256 rows
+    // and 4 LDS stages (the pipeline's fill amortised over many steps; measured
+    // on MI355X, Llama-3-8B down at M = 2048: 112.2 -> 105.3 us)
+    const bool deep = !tm64 && g.splits <= 1 && ftile == 0 && g.cus > 0 && tiles_m * tn256 <= g.cus && g.k >= 8192;
+    if (deep) TN = 256;
     int64_t tn = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
         g.L[l].tile0 = (int)tn;
@@ -1780,9 +1785,12 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     // workgroups); q|k|v (768) 48.9 -> 51.6 and gate|up (1792) 194.6 -> 200.2 keep 2
     const int fps = knob(KN_GEMM_STAGES);
     const int64_t wgs = tiles * g.splits;
-    const int pns = fps == 2 || fps == 3 ? fps : (g.cus > 0 && wgs <= 2 * g.cus ? 3 : 2);
+    const int pns = fps == 2 || fps == 3 || (fps == 4 && TN == 256) ? fps
+                    : deep                                         ? 4
+                    : (g.cus > 0 && wgs <= 2 * g.cus ? 3 : 2);
     if (TN == 256 && tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64, 4>), grid, dim3(256), 0, s, g);
     else if (TN == 256 && tm64) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64>), grid, dim3(256), 0, s, g);
+    else if (TN == 256 && pns == 4) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 128, 4>), grid, dim3(256), 0, s, g);
     else if (TN == 256 && pns == 3) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 128, 3>), grid, dim3(256), 0, s, g);
     else if (TN == 256) hipLaunchKernelGGL((k_gemm_i8<256, 4>), grid, dim3(256), 0, s, g);
     else if (tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64, 4>), grid, dim3(256), 0, s, g);

@@ -415,21 +415,24 @@ def test_small_m_gemm_split_forms(m, k, n, stages, tile, tune):
     assert torch.equal(y, y0)
 
 
-# the prefill GEMM (128-token tiles) with 2 and 3 LDS stages: k = 1088 (9 steps,
-# the last one half: two unrolled rounds of 3 and a tail of 3), k = 4096; ragged m
-# and n; one split launch (m = 130 x 300 rows has few tiles)
-@pytest.mark.parametrize("m,k,n", [(256, 1088, 1000), (130, 4096, 300), (300, 2048, 2560)])
+# the prefill GEMM (128-token tiles) with 2 and 3 LDS stages, and 256-row tiles
+# with 4: k = 1088 (9 steps, the last one half: unrolled rounds and a tail),
+# k = 4096, k = 8256 (64.5 steps); ragged m and n; one split launch (m = 130 x 300
+# rows has few tiles)
+@pytest.mark.parametrize("m,k,n", [(256, 1088, 1000), (130, 4096, 300), (300, 2048, 2560), (200, 8256, 700)])
 def test_prefill_gemm_stages(m, k, n, tune):
     print("prefill gemm stages", m, k, n, flush=True)
     x = to_dev(activations(m, k, seed=m * 7 + k), torch.bfloat16)
     pt, wb, sw = make_layer(n, k, seed=n + 2 * k)
     ys, accs = [], []
-    for stages in (2, 3):
+    for tile, stages in ((0, 2), (0, 3), (2, 4)):
+        tune("BTL_GEMM_TILE", tile)
         tune("BTL_GEMM_STAGES", stages)
         acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
         ys.append(bl.BitLinearHip.forward(x, pt, out_dtype=torch.float32, acc_out=acc))
         accs.append(acc)
-    assert torch.equal(accs[0], accs[1]) and torch.equal(ys[0], ys[1])
+    for a, y in zip(accs[1:], ys[1:]):
+        assert torch.equal(accs[0], a) and torch.equal(ys[0], y)
     yr, _, _, accr = orc.forward_i8(host_x(x), wb, n, sw)
     assert np.array_equal(accs[1].cpu().numpy(), accr)
     assert_f32_identical(ys[1], yr)
