@@ -850,7 +850,17 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
         }
         if (tid < 3) s_sync[tid] = 0u;
         if (tid < MT) s_amax[tid] = 0u;
-        __syncthreads();
+        // the counters' initialisation is in LDS; no wait for this wave's loads
+        // and copies (__syncthreads' release would wait for the norm weight's
+        // LDS copies, vmcnt(0), and hold the compute waves' weight loads behind
+        // them); the empty asm statements keep LDS accesses on their side, the
+        // scheduling barriers the arithmetic on the loaded token after it
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        __asm__ volatile("" ::: "memory");
         if constexpr (XF != XF_NONE)
             rq_transform<XF, DG>(a, xv, x2v, gv, K, gpr, nqw, nq, PH, tid, lane, wave, sq, s_sync, s_amax, s_scale,
                                  s_ss);
