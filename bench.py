@@ -70,6 +70,9 @@ class Call:
 
     def __init__(self, layers, x, outs, mode=None):
         import ctypes
+        # the call holds raw device pointers: keep the tensors they point into
+        # alive for as long as the call (a graph capture empties torch's cache)
+        self.layers, self.outs = list(layers), list(outs)
         self.cs = [l.as_c() for l in layers]
         self.n = len(layers)
         self.arr = (ctypes.POINTER(bl.BtlPacked) * self.n)(*[ctypes.pointer(c) for c in self.cs])
@@ -93,6 +96,7 @@ class OpCall:
 
     def __init__(self, layers, q, s, outs):
         import ctypes
+        self.layers, self.outs = list(layers), list(outs)  # kept alive: the call holds their pointers
         self.cs = [l.as_c() for l in layers]
         self.n = len(layers)
         self.arr = (ctypes.POINTER(bl.BtlPacked) * self.n)(*[ctypes.pointer(c) for c in self.cs])

@@ -16,7 +16,9 @@
 //                     reorders pre-quantised ones).
 //   k_quant_act<XK>   per-token absmax int8 quantisation, natural layout.
 //   k_ref_f32<XK,YK>  reference-semantics fp32 path: bit-identical to the
-//                     8-lane FMA order of cpu.rs.
+//                     8-lane FMA order of cpu.rs; k_ref_f32_st is its form for
+//                     k % 64 == 0 (weights streamed through LDS, f16 coefficient
+//                     lookup by byte permute, v_fma_mix_f32).
 //   k_generic_i8<YK>  any k % 4 == 0 / any alignment, int8 activations.
 //   k_unpack          dense f32 weights (PackedTensor::unpack on the device).
 //   k_fill_zero       workspace clearing (a kernel, so it is graph-capture safe).
@@ -26,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <type_traits>
 #include <stdlib.h>
 
 #include "btl_device.hpp"
@@ -2140,6 +2143,28 @@ __device__ __forceinline__ float load_x(const void* x, int64_t i)
     return ((const float*)x)[i];
 }
 
+// x[i .. i + 3] (i % 4 == 0; 16-byte aligned f32 or 8-byte aligned bf16 rows),
+// loaded as stored (x4_raw) and widened later (x4_f32), so that a caller can
+// issue several loads before it waits for any
+template <int XK>
+struct X4 {
+    using T = typename std::conditional<XK == XK_BF16, uint2, float4>::type;
+};
+template <int XK>
+__device__ __forceinline__ typename X4<XK>::T x4_raw(const void* x, int64_t i)
+{
+    if constexpr (XK == XK_BF16) return *(const uint2*)((const uint16_t*)x + i);
+    else return *(const float4*)((const float*)x + i);
+}
+template <int XK>
+__device__ __forceinline__ float4 x4_f32(typename X4<XK>::T v)
+{
+    if constexpr (XK == XK_BF16)
+        return float4{bf16_to_f32((uint16_t)v.x), bf16_to_f32((uint16_t)(v.x >> 16)), bf16_to_f32((uint16_t)v.y),
+                      bf16_to_f32((uint16_t)(v.y >> 16))};
+    else return v;
+}
+
 template <int XK>
 __global__ __launch_bounds__(256) void k_quant_act(const void* x, int64_t k, int8_t* q, float* s)
 {
@@ -2229,21 +2254,57 @@ __global__ __launch_bounds__(256) void k_ref_f32(const void* x, int64_t m, int64
 // grid (ceil(n / 32), m), 32 outputs of one token row per workgroup, 8 lanes
 // each.  The row is staged once in LDS lane-major (sx[b][j] = x[8 j + b], rows
 // padded by 4 floats: the lanes' 16-byte reads hit distinct banks), so lane b
-// reads its inputs 8 at a time; each weight row is read 16 bytes (64 weights)
-// per load, the 8 lanes of an output sharing the address.  Lane b's code of
-// weight 8 j' + b, j' = 8 q + e, sits at bit 16 (e % 2) + 2 b of word e / 2 of
-// the q-th 16 bytes.  The FMA order per lane (increasing j') and the lane sum
-// are those of k_ref_f32 (no tail: 32 divides k).
+// reads its inputs 8 at a time.  The 32 weight rows stream in stages of 256
+// bytes per row (1024 weights): every lane loads its own 16 bytes of a stage
+// (one load of a wave = 4 rows x 256 bytes) DEPTH stages ahead into
+// registers, then writes them to one of two LDS buffers, rows 272 bytes
+// apart (the 8 rows a wave reads at once hit distinct banks).  Lane b's code of weight 8 j' + b, j' = 8 q + e, sits at
+// bit 16 (e % 2) + 2 b of word e / 2 of the q-th 16 bytes: a rotation brings
+// the pair of codes of one word to bits 8 and 24, a byte permute looks both
+// up as f16 coefficients (0x3C00 = 1, 0xBC00 = -1, 0 for codes 0 and 3: the
+// reference's (code & 1) - (code >> 1)), and v_fma_mix_f32 runs
+// fma(x, coeff, acc) on them with the f16 coefficient widened exactly.  The
+// FMA order per lane (increasing j') and the lane sum are those of k_ref_f32
+// (no tail: 32 divides k).
 //
 // Grouped (several layers reading the same x, btl_linear_group_mode): the
 // workgroups of layer i are [g.wg_begin[i], g.wg_begin[i + 1]) of the grid's x.
-template <int XK, int YK>
-__global__ __launch_bounds__(256) void k_ref_f32_lds(const void* x, int64_t k, RefGroup g)
+constexpr int kRefRows = 32;                        // outputs (weight rows) per workgroup
+constexpr int kRefStageBytes = 256;                 // bytes of each row per stage
+constexpr int kRefRowStride = kRefStageBytes + 16;  // LDS bytes per row
+constexpr int kRefDepth = 4;                        // stages loaded ahead
+
+// acc = fma(xa, c(lo code), acc); acc = fma(xb, c(hi code), acc) for the codes
+// at bits rot + 8 and rot + 24 (mod 32) of wd
+// (v_fma_mix_f32: about 7 clocks a wave back to back against 4 for v_fma_f32,
+// still cheaper than widening each coefficient with v_cvt_f32_f16 first)
+__device__ __forceinline__ float ref_step2(float acc, float xa, float xb, uint32_t wd, uint32_t rot)
 {
-    extern __shared__ __align__(16) float sxl[];
-    const int K = (int)k, S = (K >> 3) + 4;
+    const uint32_t sel = __builtin_amdgcn_alignbit(wd, wd, rot) & 0x03000300u;
+    const uint32_t c = __builtin_amdgcn_perm(0u, 0x00BC3C00u, sel);
+    acc = __builtin_fmaf(xa, (float)__builtin_bit_cast(_Float16, (uint16_t)c), acc);
+    return __builtin_fmaf(xb, (float)__builtin_bit_cast(_Float16, (uint16_t)(c >> 16)), acc);
+}
+
+// 4 waves, 32 weight rows per workgroup (measured against 2 waves, and
+// against two outputs per group of 8 lanes sharing x's reads: neither is
+// faster).  KX: the largest k of the instantiation (x's LDS rows are
+// KX / 8 + 4 floats).
+template <int XK, int YK, int DEPTH, int KX>
+__global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t k, RefGroup g)
+{
+    static_assert(DEPTH % 2 == 0, "the LDS buffer of a stage is a constant of the unrolled loop");
+    constexpr int NW = 4;
+    constexpr int S = KX / 8 + 4;
+    constexpr int ROWS = kRefRows;
+    constexpr int STAGE = ROWS * kRefRowStride;
+    constexpr int LOADS = 2;  // 16-byte loads per lane per stage (4 rows x 256 bytes each)
+    static_assert(LOADS * NW * 4 == ROWS && NW * 8 == ROWS, "the loads of a stage cover its rows");
+    __shared__ __align__(1024) uint8_t sw[2 * STAGE];
+    __shared__ __align__(16) float sx[8 * S];
+    const int K = (int)k;
     const int64_t row = blockIdx.y;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     int li = 0;
 #pragma unroll
     for (int i = 1; i < kMaxGroup; ++i)
@@ -2252,39 +2313,134 @@ __global__ __launch_bounds__(256) void k_ref_f32_lds(const void* x, int64_t k, R
     const int64_t n = g.n[li];
     const float scale = g.scale[li];
     void* y = g.y[li];
-    for (int i = tid; i < K; i += 256) sxl[(i & 7) * S + (i >> 3)] = load_x<XK>(x, row * k + i);
-    __syncthreads();
-    const int64_t col = (int64_t)((int)blockIdx.x - g.wg_begin[li]) * 32 + (tid >> 3);
-    const int b = tid & 7;
-    const bool active = col < n;
-    const uint4* wr = (const uint4*)(w + (active ? col : 0) * (k >> 2));
-    const float* xb = sxl + b * S;
-    float acc = 0.0f;
-    // 8 steps unrolled (k % 512 == 0 for the Llama shapes): their weight loads
-    // are in flight together
-#pragma unroll 8
-    for (int q = 0; q < (K >> 6); ++q) {
-        const uint4 wv = wr[q];
-        const float4 x0 = *(const float4*)(xb + 8 * q);
-        const float4 x1 = *(const float4*)(xb + 8 * q + 4);
-        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
-        const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    const int64_t col0 = (int64_t)((int)blockIdx.x - g.wg_begin[li]) * ROWS;
+    const int rb = K >> 2;  // bytes per weight row
+    const int nrows = (int)min((int64_t)ROWS, n - col0);
+    // rows past n read as zero (outside the descriptor) and are not stored
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(w + col0 * rb, (uint32_t)(nrows * rb));
+    const int nst = (rb + kRefStageBytes - 1) / kRefStageBytes;
+
+    // this lane's loads: rows 4 grp .. 4 grp + 3, grp = LOADS wave + i
+    int loff[LOADS], lds_off[LOADS];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t code = (wd[e >> 1] >> (16 * (e & 1) + 2 * b)) & 3u;
-            const float coeff = (float)((int)(code & 1u) - (int)(code >> 1));
-            acc = __builtin_fmaf(xs[e], coeff, acc);
+    for (int i = 0; i < LOADS; ++i) {
+        const int r = 4 * (LOADS * wave + i) + (lane >> 4);
+        loff[i] = r * rb + (lane & 15) * 16;
+        lds_off[i] = r * kRefRowStride + (lane & 15) * 16;
+    }
+    uint4 R[DEPTH][LOADS];
+    // stages past the row's end load from outside the descriptor: nothing is
+    // read, zeros are written and never used
+    auto load = [&](int st, uint4 (&r)[LOADS]) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i)
+            r[i] = bload(rs, st < nst ? loff[i] + st * kRefStageBytes : INT32_MIN);
+    };
+    auto put = [&](const uint4 (&r)[LOADS], int buf) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) *(uint4*)(sw + buf * STAGE + lds_off[i]) = r[i];
+    };
+    // x's loads first (4 elements per load), then the weights' first stages,
+    // then x's LDS writes: they wait for x's loads only.  The stages then
+    // stand as at the top of every later iteration: R[1 .. DEPTH - 1] hold
+    // stages 1 .. DEPTH - 1, R[0] stage DEPTH, LDS buffer 0 stage 0.
+    constexpr int XL = KX / (4 * NW * 64);  // x loads per thread
+    typename X4<XK>::T xv[XL];
+    const int kv = K >> 2;
+#pragma unroll
+    for (int j = 0; j < XL; ++j) {
+        const int t = tid + NW * 64 * j;
+        if (t < kv) xv[j] = x4_raw<XK>(x, row * k + 4 * t);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load(d, R[d]);
+#pragma unroll
+    for (int j = 0; j < XL; ++j) {
+        const int t = tid + NW * 64 * j;
+        if (t < kv) {
+            // elements 4 t .. 4 t + 3: lane rows (4 t) & 7 .. + 3, column t / 2
+            float* d = sx + ((4 * t) & 7) * S + (t >> 1);
+            const float4 v = x4_f32<XK>(xv[j]);
+            d[0] = v.x;
+            d[S] = v.y;
+            d[2 * S] = v.z;
+            d[3 * S] = v.w;
+        }
+    }
+    put(R[0], 0);
+    load(DEPTH, R[0]);
+    __syncthreads();  // x and stage 0 staged
+
+    // output o, chain b
+    const int o = wave * 8 + (lane >> 3), b = lane & 7;
+    const uint32_t rot = (uint32_t)(2 * b + 24) & 31u;
+    const float* xb = sx + b * S;
+    const int wrd = o * kRefRowStride;
+    float acc = 0.0f;
+    // one 16-byte chunk of row o (64 weights) and the 8 inputs of chain b it
+    // multiplies
+    struct Chunk {
+        uint4 w;
+        float4 x0, x1;
+    };
+    auto rd = [&](const uint8_t* wq, const float* xq) {
+        Chunk c;
+        c.w = *(const uint4*)wq;
+        c.x0 = *(const float4*)xq;
+        c.x1 = *(const float4*)(xq + 4);
+        return c;
+    };
+    auto fma8 = [&](const Chunk& c) {
+        acc = ref_step2(acc, c.x0.x, c.x0.y, c.w.x, rot);
+        acc = ref_step2(acc, c.x0.z, c.x0.w, c.w.y, rot);
+        acc = ref_step2(acc, c.x1.x, c.x1.y, c.w.z, rot);
+        acc = ref_step2(acc, c.x1.z, c.x1.w, c.w.w, rot);
+    };
+    auto compute = [&](const uint8_t* stage, int st) {
+        const int nq = min(16, (rb - st * kRefStageBytes) >> 4);
+        const uint8_t* wq = stage + wrd;
+        const float* xs = xb + st * 128;
+        if (nq == 16) {  // uniform
+            // the LDS reads of chunk q + 2 are issued before chunk q's FMAs
+            // (one wave per SIMD is common here: nothing else hides their latency)
+            Chunk cb[3];
+            cb[0] = rd(wq, xs);
+            cb[1] = rd(wq + 16, xs + 8);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                if (q + 2 < 16) cb[(q + 2) % 3] = rd(wq + 16 * (q + 2), xs + 8 * (q + 2));
+                __builtin_amdgcn_sched_barrier(0);
+                fma8(cb[q % 3]);
+            }
+        } else {
+            for (int q = 0; q < nq; ++q) fma8(rd(wq + 16 * q, xs + 8 * q));
+        }
+    };
+    // DEPTH stages per iteration: every register set and LDS buffer index is
+    // a constant.  Stage s sits in R[s % DEPTH] until it is written to LDS
+    // buffer s % 2, one stage ahead of the compute.  The stages past nst of
+    // the last iteration compute nothing (nq <= 0); they are not skipped by a
+    // branch out of the loop, whose paths would make the compiler wait for
+    // every outstanding load at the top of the loop.
+    for (int st0 = 0; st0 < nst; st0 += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            const int st = st0 + i;
+            if (st > 0) __syncthreads();  // stage st written; stage st - 1 no longer read
+            put(R[(i + 1) % DEPTH], (i + 1) & 1);
+            load(st + 1 + DEPTH, R[(i + 1) % DEPTH]);
+            compute(sw + (i & 1) * STAGE, st);
         }
     }
     float lanes[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) lanes[i] = __shfl(acc, i, 8);
-    if (!active || b != 0) return;
+    if (o >= nrows || b != 0) return;
     float r = -0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) r = __fadd_rn(r, lanes[i]);
     const float sum = __fadd_rn(0.0f, r);
-    store_y<YK>(y, row * n + col, __fmul_rn(sum, scale));
+    store_y<YK>(y, row * n + col0 + o, __fmul_rn(sum, scale));
 }
 
 hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* const* w,
@@ -2292,14 +2448,15 @@ hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, 
                                 hipStream_t st)
 {
     if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
-    bool lds_ok = k % 64 == 0 && k <= 16384 && m <= 65535;
-    int64_t wgs = 0;
+    bool lds_ok = k % 64 == 0 && k <= 16384 && m <= 65535 && ((uintptr_t)x & 15u) == 0;
+    int64_t n_total = 0;
     for (int i = 0; i < count; ++i) {
         lds_ok = lds_ok && ((uintptr_t)w[i] & 15u) == 0;
-        wgs += (n[i] + 31) / 32;
+        n_total += n[i];
     }
-    if (m <= 0 || wgs == 0) return hipSuccess;
-    if (!lds_ok || wgs > INT32_MAX) {
+    if (m <= 0 || n_total == 0) return hipSuccess;
+    const int rows = kRefRows;
+    if (!lds_ok || n_total / rows + count > INT32_MAX) {
         for (int i = 0; i < count; ++i) {
             const hipError_t e = launch_ref_f32(x, xkind, m, k, w[i], n[i], scale[i], y[i], ykind, st);
             if (e != hipSuccess) return e;
@@ -2315,21 +2472,25 @@ hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, 
         g.scale[i] = scale[i];
         g.n[i] = n[i];
         g.wg_begin[i] = b;
-        b += (int)((n[i] + 31) / 32);
+        b += (int)((n[i] + rows - 1) / rows);
     }
     g.wg_begin[count] = b;
     const dim3 grid((unsigned)b, (unsigned)m);
-    const size_t lds = (size_t)8 * ((k >> 3) + 4) * 4;
-#define BTL_REF_LDS(XKV, YKV)                                                                   \
-    if (xkind == XKV && ykind == YKV) {                                                         \
-        hipLaunchKernelGGL((k_ref_f32_lds<XKV, YKV>), grid, dim3(256), lds, st, x, k, g);      \
-        return hipGetLastError();                                                               \
+#define BTL_REF_ST(XKV, YKV, KXV)                                                                  \
+    hipLaunchKernelGGL((k_ref_f32_st<XKV, YKV, kRefDepth, KXV>), grid, dim3(256), 0, st, x, k, g);  \
+    return hipGetLastError();
+#define BTL_REF_LDS(XKV, YKV)                              \
+    if (xkind == XKV && ykind == YKV) {                    \
+        if (k <= 4096) { BTL_REF_ST(XKV, YKV, 4096) }      \
+        if (k <= 8192) { BTL_REF_ST(XKV, YKV, 8192) }      \
+        BTL_REF_ST(XKV, YKV, 16384)                        \
     }
     BTL_REF_LDS(XK_F32, YK_F32)
     BTL_REF_LDS(XK_F32, YK_BF16)
     BTL_REF_LDS(XK_BF16, YK_F32)
     BTL_REF_LDS(XK_BF16, YK_BF16)
 #undef BTL_REF_LDS
+#undef BTL_REF_ST
     return hipErrorInvalidValue;
 }
 
@@ -2338,7 +2499,8 @@ hipError_t launch_ref_f32(const void* x, int xkind, int64_t m, int64_t k, const 
 {
     const int64_t threads = m * n * 8;
     if (threads <= 0) return hipSuccess;
-    if (k % 64 == 0 && k <= 16384 && ((uintptr_t)w & 15u) == 0 && m <= 65535 && (n + 31) / 32 <= INT32_MAX)
+    if (k % 64 == 0 && k <= 16384 && ((uintptr_t)w & 15u) == 0 && ((uintptr_t)x & 15u) == 0 && m <= 65535 &&
+        (n + 31) / 32 <= INT32_MAX)
         return launch_ref_f32_group(x, xkind, m, k, &w, &n, &scale, &y, 1, ykind, st);
     dim3 grid((unsigned)((threads + 255) / 256));
 #define BTL_REF_CASE(XKV, YKV)                                                                  \

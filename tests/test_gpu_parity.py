@@ -564,11 +564,14 @@ def test_linear_f32_ref_order_cases():
 
 
 # k % 64 == 0 and k <= 16384: the LDS-staged form of the reference-order kernel
-# (inputs lane-major in LDS, 16-byte weight loads).  Inputs spanning 40 binades
-# make every sum order-sensitive, so a lane or step mismatch shows; codes 3
-# appear; m > 1 reads each token row's staging; bf16 in and out; k = 16448 takes
-# the general form.
-@pytest.mark.parametrize("m,k,n", [(1, 64, 40), (3, 192, 33), (2, 4096, 70), (1, 16384, 24), (2, 16448, 9)])
+# (inputs lane-major in LDS, weight rows streamed through LDS in stages of 1024
+# weights).  Inputs spanning 40 binades make every sum order-sensitive, so a
+# lane or step mismatch shows; codes 3 appear; m > 1 reads each token row's
+# staging; bf16 in and out; the three LDS sizes of x (k <= 4096, 8192, 16384),
+# a last stage of one 16-byte chunk (k = 64) and of half a stage (k = 5632),
+# several stages per loop trip (k = 14336); k = 16448 takes the general form.
+@pytest.mark.parametrize("m,k,n", [(1, 64, 40), (3, 192, 33), (2, 4096, 70), (1, 5632, 36), (2, 8192, 40),
+                                   (1, 14336, 64), (1, 16384, 24), (2, 16448, 9)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
 def test_linear_f32_ref_staged_form(m, k, n, xdt, ydt):
     print("f32 ref staged", m, k, n, xdt, ydt, flush=True)
@@ -584,6 +587,30 @@ def test_linear_f32_ref_staged_form(m, k, n, xdt, ydt):
         assert_f32_identical(y, yr)
     else:
         assert_bf16_matches(y, yr)
+
+
+# special inputs in the reference's order: subnormal inputs and partial sums
+# (fma keeps them), sums that overflow to inf, inf inputs (times a zero
+# coefficient: NaN) and a NaN input; staged (k % 64 == 0) and general forms
+@pytest.mark.parametrize("k", [4096, 14336, 100])
+def test_linear_f32_ref_special_values(k):
+    print("f32 ref special", k, flush=True)
+    rng = np.random.default_rng(k)
+    m, n = 3, 40
+    x = np.empty((m, k), np.float32)
+    x[0] = rng.standard_normal(k) * 1e-39                      # subnormal
+    x[1] = rng.standard_normal(k) * 3e37                       # partial sums overflow (inf, NaN)
+    x[2] = rng.standard_normal(k) * 1e-3
+    x[2, 5], x[2, 61], x[2, 77] = np.inf, -np.inf, np.nan
+    wb = random_codes(n, k, seed=k + 3, p3=0.1)
+    sw = np.float32(0.5)
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), float(sw), (n, k), DEV)
+    y = bl.BitLinearHip.forward(to_dev(x, torch.float32), pt, mode="f32_ref").cpu().numpy()
+    yr = orc.forward_f32(x, wb, n, sw)
+    assert np.isnan(yr[2]).any() and not np.isfinite(yr[1]).all() and (np.abs(yr[0][yr[0] != 0]) < 1.2e-38).any()
+    nan = np.isnan(yr)
+    assert np.array_equal(np.isnan(y), nan)
+    assert_f32_identical(np.where(nan, 0, y).astype(np.float32), np.where(nan, 0, yr).astype(np.float32))
 
 
 def test_linear_f32_ref_reference_bench_input():
