@@ -421,10 +421,13 @@ __global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
     const int vpr = hd >> 4, nvec = nrows * vpr;  // hd % 16 == 0 (host)
     uint4 kvv[8], vvv[8];
     float ks[8], vs[8];
+    // a uniform bound and every lane loading (a lane past the chunk reloads its
+    // last vector): a per-lane condition here made the compiler copy a loaded
+    // scale between registers, waiting for it before the next loads issued
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
-        const int idx = tid + it * nthr;
-        if (idx < nvec) {
+        if (it * nthr < nvec) {  // uniform
+            const int idx = min(tid + it * nthr, nvec - 1);
             const int j = idx / vpr;
             kvv[it] = ((const uint4*)(a.kc + (base + j) * hd))[idx - j * vpr];
             vvv[it] = ((const uint4*)(a.vc + (base + j) * hd))[idx - j * vpr];
