@@ -192,10 +192,10 @@ __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], co
     const bool h0 = d0 < hd, h1 = d1 < hd;
     const int c0 = h0 ? d0 : 0, c1 = h1 ? d1 : 0;  // clamped columns (values unused when out of range)
     int j = 0;
-    for (; j + 4 <= nj; j += 4) {
-        const float4 p4 = *(const float4*)&sp[j];
-        const float a0 = s_v[j][c0], a1 = s_v[j + 1][c0], a2 = s_v[j + 2][c0], a3 = s_v[j + 3][c0];
-        const float b0 = s_v[j][c1], b1 = s_v[j + 1][c1], b2 = s_v[j + 2][c1], b3 = s_v[j + 3][c1];
+    auto four = [&](int jj) {
+        const float4 p4 = *(const float4*)&sp[jj];
+        const float a0 = s_v[jj][c0], a1 = s_v[jj + 1][c0], a2 = s_v[jj + 2][c0], a3 = s_v[jj + 3][c0];
+        const float b0 = s_v[jj][c1], b1 = s_v[jj + 1][c1], b2 = s_v[jj + 2][c1], b3 = s_v[jj + 3][c1];
         o0 = __fadd_rn(o0, __fmul_rn(p4.x, a0));
         o0 = __fadd_rn(o0, __fmul_rn(p4.y, a1));
         o0 = __fadd_rn(o0, __fmul_rn(p4.z, a2));
@@ -204,6 +204,15 @@ __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], co
         o1 = __fadd_rn(o1, __fmul_rn(p4.y, b1));
         o1 = __fadd_rn(o1, __fmul_rn(p4.z, b2));
         o1 = __fadd_rn(o1, __fmul_rn(p4.w, b3));
+    };
+    if (HD != 0 && nj == kAttnChunk) {
+        // a full chunk: unrolled, so the LDS reads of later keys issue ahead of
+        // the sums (the runtime loop waited for each group's reads in turn)
+#pragma unroll
+        for (int jj = 0; jj < kAttnChunk; jj += 4) four(jj);
+        j = kAttnChunk;
+    } else {
+        for (; j + 4 <= nj; j += 4) four(j);
     }
     for (; j < nj; ++j) {
         const float pj = sp[j];
