@@ -2274,24 +2274,30 @@ constexpr int kRefStageBytes = 256;                 // bytes of each row per sta
 constexpr int kRefRowStride = kRefStageBytes + 16;  // LDS bytes per row
 constexpr int kRefDepth = 4;                        // stages loaded ahead
 
-// acc = fma(xa, c(lo code), acc); acc = fma(xb, c(hi code), acc) for the codes
-// at bits rot + 8 and rot + 24 (mod 32) of wd
-// (v_fma_mix_f32: about 7 clocks a wave back to back against 4 for v_fma_f32,
-// still cheaper than widening each coefficient with v_cvt_f32_f16 first)
-__device__ __forceinline__ float ref_step2(float acc, float xa, float xb, uint32_t wd, uint32_t rot)
+// the f16 coefficients of the codes at bits rot + 8 and rot + 24 (mod 32) of wd,
+// in the low and high halves
+__device__ __forceinline__ uint32_t ref_coeffs(uint32_t wd, uint32_t rot)
 {
     const uint32_t sel = __builtin_amdgcn_alignbit(wd, wd, rot) & 0x03000300u;
-    const uint32_t c = __builtin_amdgcn_perm(0u, 0x00BC3C00u, sel);
+    return __builtin_amdgcn_perm(0u, 0x00BC3C00u, sel);
+}
+// acc = fma(xa, c.lo, acc); acc = fma(xb, c.hi, acc) (v_fma_mix_f32: about 7
+// clocks a wave back to back against 4 for v_fma_f32, still cheaper than
+// widening each coefficient with v_cvt_f32_f16 first)
+__device__ __forceinline__ float ref_apply2(float acc, float xa, float xb, uint32_t c)
+{
     acc = __builtin_fmaf(xa, (float)__builtin_bit_cast(_Float16, (uint16_t)c), acc);
     return __builtin_fmaf(xb, (float)__builtin_bit_cast(_Float16, (uint16_t)(c >> 16)), acc);
 }
 
 // 4 waves, 32 weight rows per workgroup (measured against 2 waves, and
 // against two outputs per group of 8 lanes sharing x's reads: neither is
-// faster).  KX: the largest k of the instantiation (x's LDS rows are
-// KX / 8 + 4 floats).
-template <int XK, int YK, int DEPTH, int KX>
-__global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t k, RefGroup g)
+// faster).  TR token rows per workgroup (grid.y = ceil(m / TR)): every lane
+// runs its chain for each of them, so a weight chunk's read and coefficient
+// lookup serve TR rows.  KX: the largest k of the instantiation (x's LDS rows
+// are KX / 8 + 4 floats, TR of them per lane row).
+template <int XK, int YK, int DEPTH, int KX, int TR>
+__global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t m, int64_t k, RefGroup g)
 {
     static_assert(DEPTH % 2 == 0, "the LDS buffer of a stage is a constant of the unrolled loop");
     constexpr int NW = 4;
@@ -2301,9 +2307,9 @@ __global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t k, Re
     constexpr int LOADS = 2;  // 16-byte loads per lane per stage (4 rows x 256 bytes each)
     static_assert(LOADS * NW * 4 == ROWS && NW * 8 == ROWS, "the loads of a stage cover its rows");
     __shared__ __align__(1024) uint8_t sw[2 * STAGE];
-    __shared__ __align__(16) float sx[8 * S];
+    __shared__ __align__(16) float sx[TR * 8 * S];
     const int K = (int)k;
-    const int64_t row = blockIdx.y;
+    const int64_t row0 = (int64_t)blockIdx.y * TR;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     int li = 0;
 #pragma unroll
@@ -2344,29 +2350,34 @@ __global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t k, Re
     // then x's LDS writes: they wait for x's loads only.  The stages then
     // stand as at the top of every later iteration: R[1 .. DEPTH - 1] hold
     // stages 1 .. DEPTH - 1, R[0] stage DEPTH, LDS buffer 0 stage 0.
-    constexpr int XL = KX / (4 * NW * 64);  // x loads per thread
-    typename X4<XK>::T xv[XL];
+    // (a token row past m is not loaded: its lanes' sums are not stored)
+    constexpr int XL = KX / (4 * NW * 64);  // x loads per thread and token row
+    typename X4<XK>::T xv[TR][XL];
     const int kv = K >> 2;
 #pragma unroll
-    for (int j = 0; j < XL; ++j) {
-        const int t = tid + NW * 64 * j;
-        if (t < kv) xv[j] = x4_raw<XK>(x, row * k + 4 * t);
-    }
+    for (int r = 0; r < TR; ++r)
+#pragma unroll
+        for (int j = 0; j < XL; ++j) {
+            const int t = tid + NW * 64 * j;
+            if (t < kv && row0 + r < m) xv[r][j] = x4_raw<XK>(x, (row0 + r) * k + 4 * t);
+        }
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) load(d, R[d]);
 #pragma unroll
-    for (int j = 0; j < XL; ++j) {
-        const int t = tid + NW * 64 * j;
-        if (t < kv) {
-            // elements 4 t .. 4 t + 3: lane rows (4 t) & 7 .. + 3, column t / 2
-            float* d = sx + ((4 * t) & 7) * S + (t >> 1);
-            const float4 v = x4_f32<XK>(xv[j]);
-            d[0] = v.x;
-            d[S] = v.y;
-            d[2 * S] = v.z;
-            d[3 * S] = v.w;
+    for (int r = 0; r < TR; ++r)
+#pragma unroll
+        for (int j = 0; j < XL; ++j) {
+            const int t = tid + NW * 64 * j;
+            if (t < kv && row0 + r < m) {
+                // elements 4 t .. 4 t + 3: lane rows (4 t) & 7 .. + 3, column t / 2
+                float* d = sx + (r * 8 + ((4 * t) & 7)) * S + (t >> 1);
+                const float4 v = x4_f32<XK>(xv[r][j]);
+                d[0] = v.x;
+                d[S] = v.y;
+                d[2 * S] = v.z;
+                d[3 * S] = v.w;
+            }
         }
-    }
     put(R[0], 0);
     load(DEPTH, R[0]);
     __syncthreads();  // x and stage 0 staged
@@ -2376,25 +2387,35 @@ __global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t k, Re
     const uint32_t rot = (uint32_t)(2 * b + 24) & 31u;
     const float* xb = sx + b * S;
     const int wrd = o * kRefRowStride;
-    float acc = 0.0f;
+    float acc[TR];
+#pragma unroll
+    for (int r = 0; r < TR; ++r) acc[r] = 0.0f;
     // one 16-byte chunk of row o (64 weights) and the 8 inputs of chain b it
-    // multiplies
+    // multiplies in each token row
     struct Chunk {
         uint4 w;
-        float4 x0, x1;
+        float4 x0[TR], x1[TR];
     };
     auto rd = [&](const uint8_t* wq, const float* xq) {
         Chunk c;
         c.w = *(const uint4*)wq;
-        c.x0 = *(const float4*)xq;
-        c.x1 = *(const float4*)(xq + 4);
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            c.x0[r] = *(const float4*)(xq + r * 8 * S);
+            c.x1[r] = *(const float4*)(xq + r * 8 * S + 4);
+        }
         return c;
     };
     auto fma8 = [&](const Chunk& c) {
-        acc = ref_step2(acc, c.x0.x, c.x0.y, c.w.x, rot);
-        acc = ref_step2(acc, c.x0.z, c.x0.w, c.w.y, rot);
-        acc = ref_step2(acc, c.x1.x, c.x1.y, c.w.z, rot);
-        acc = ref_step2(acc, c.x1.z, c.x1.w, c.w.w, rot);
+        const uint32_t c0 = ref_coeffs(c.w.x, rot), c1 = ref_coeffs(c.w.y, rot);
+        const uint32_t c2 = ref_coeffs(c.w.z, rot), c3 = ref_coeffs(c.w.w, rot);
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            acc[r] = ref_apply2(acc[r], c.x0[r].x, c.x0[r].y, c0);
+            acc[r] = ref_apply2(acc[r], c.x0[r].z, c.x0[r].w, c1);
+            acc[r] = ref_apply2(acc[r], c.x1[r].x, c.x1[r].y, c2);
+            acc[r] = ref_apply2(acc[r], c.x1[r].z, c.x1[r].w, c3);
+        }
     };
     auto compute = [&](const uint8_t* stage, int st) {
         const int nq = min(16, (rb - st * kRefStageBytes) >> 4);
@@ -2432,15 +2453,19 @@ __global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t k, Re
             compute(sw + (i & 1) * STAGE, st);
         }
     }
-    float lanes[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) lanes[i] = __shfl(acc, i, 8);
-    if (o >= nrows || b != 0) return;
-    float r = -0.0f;
+    for (int t = 0; t < TR; ++t) {
+        float lanes[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r = __fadd_rn(r, lanes[i]);
-    const float sum = __fadd_rn(0.0f, r);
-    store_y<YK>(y, row * n + col0 + o, __fmul_rn(sum, scale));
+        for (int i = 0; i < 8; ++i) lanes[i] = __shfl(acc[t], i, 8);
+        if (o < nrows && b == 0 && row0 + t < m) {
+            float r = -0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r = __fadd_rn(r, lanes[i]);
+            const float sum = __fadd_rn(0.0f, r);
+            store_y<YK>(y, (row0 + t) * n + col0 + o, __fmul_rn(sum, scale));
+        }
+    }
 }
 
 hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* const* w,
@@ -2475,9 +2500,13 @@ hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, 
         b += (int)((n[i] + rows - 1) / rows);
     }
     g.wg_begin[count] = b;
-    const dim3 grid((unsigned)b, (unsigned)m);
-#define BTL_REF_ST(XKV, YKV, KXV)                                                                  \
-    hipLaunchKernelGGL((k_ref_f32_st<XKV, YKV, kRefDepth, KXV>), grid, dim3(256), 0, st, x, k, g);  \
+    // two token rows per workgroup from m = 2 on (the weight chunk's read and
+    // coefficient lookup shared; x of both rows in LDS: at most 2 x 64 KB)
+    const int tr = m >= 2 ? 2 : 1;
+    const dim3 grid((unsigned)b, (unsigned)((m + tr - 1) / tr));
+#define BTL_REF_ST(XKV, YKV, KXV)                                                                              \
+    if (tr == 2) hipLaunchKernelGGL((k_ref_f32_st<XKV, YKV, kRefDepth, KXV, 2>), grid, dim3(256), 0, st, x, m, k, g); \
+    else hipLaunchKernelGGL((k_ref_f32_st<XKV, YKV, kRefDepth, KXV, 1>), grid, dim3(256), 0, st, x, m, k, g);         \
     return hipGetLastError();
 #define BTL_REF_LDS(XKV, YKV)                              \
     if (xkind == XKV && ykind == YKV) {                    \

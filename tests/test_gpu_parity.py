@@ -566,12 +566,13 @@ def test_linear_f32_ref_order_cases():
 # k % 64 == 0 and k <= 16384: the LDS-staged form of the reference-order kernel
 # (inputs lane-major in LDS, weight rows streamed through LDS in stages of 1024
 # weights).  Inputs spanning 40 binades make every sum order-sensitive, so a
-# lane or step mismatch shows; codes 3 appear; m > 1 reads each token row's
-# staging; bf16 in and out; the three LDS sizes of x (k <= 4096, 8192, 16384),
-# a last stage of one 16-byte chunk (k = 64) and of half a stage (k = 5632),
-# several stages per loop trip (k = 14336); k = 16448 takes the general form.
+# lane or step mismatch shows; codes 3 appear; m > 1 runs two token rows per
+# workgroup (odd m: the last workgroup's second row is past m); bf16 in and
+# out; the three LDS sizes of x (k <= 4096, 8192, 16384), a last stage of one
+# 16-byte chunk (k = 64) and of half a stage (k = 5632), several stages per
+# loop trip (k = 14336); k = 16448 takes the general form.
 @pytest.mark.parametrize("m,k,n", [(1, 64, 40), (3, 192, 33), (2, 4096, 70), (1, 5632, 36), (2, 8192, 40),
-                                   (1, 14336, 64), (1, 16384, 24), (2, 16448, 9)])
+                                   (1, 14336, 64), (1, 16384, 24), (2, 16448, 9), (9, 4096, 40), (5, 14336, 33)])
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16)])
 def test_linear_f32_ref_staged_form(m, k, n, xdt, ydt):
     print("f32 ref staged", m, k, n, xdt, ydt, flush=True)
