@@ -41,6 +41,7 @@ EXPORTS = (
     "btl_embedding", "btl_greedy_next", "btl_add_rmsnorm", "btl_swiglu", "btl_dense_linear",
     "btl_add_rmsnorm_linear_group", "btl_add_rmsnorm_swiglu",
     "btl_add_rmsnorm_swiglu_workspace_bytes", "btl_linear_residual",
+    "btl_add_rmsnorm_linear_group_ref",
     "btl_stream_create", "btl_stream_stage_words", "btl_stream_run", "btl_stream_destroy",
 )
 
@@ -118,6 +119,7 @@ def _load():
         "btl_add_rmsnorm": (i32, [vp, vp, vp, vp, f32, i64, i64, vp, vp]),
         "btl_dense_linear": (i32, [vp, i32, i64, i64, vp, i64, vp, vp]),
         "btl_swiglu": (i32, [vp, vp, i64, vp, vp]),
+        "btl_add_rmsnorm_linear_group_ref": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, vp, vp, f32, i64, i64, vp]),
         "btl_add_rmsnorm_linear_group": (i32, [P(P(BtlPacked)), P(vp), i32, vp, vp, vp, vp, f32, i64, i64, i32, vp,
                                                sz, vp]),
         "btl_add_rmsnorm_swiglu": (i32, [P(BtlPacked), P(BtlPacked), vp, vp, vp, vp, f32, i64, i64, vp, vp, sz, vp]),

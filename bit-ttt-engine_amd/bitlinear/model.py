@@ -265,13 +265,42 @@ class BitLlamaHip:
         """The blocks and the head in the reference's own arithmetic: every BitLinear
         as BitLinearCpu::forward (btl_linear_group_mode, BTL_ACT_F32_REF), the
         residual adds and norms through btl_add_rmsnorm (the add of a block's output
-        is done by the next norm), SwiGLU's activation through btl_swiglu."""
+        is done by the next norm), SwiGLU's activation through btl_swiglu.  For one
+        token row with a hidden width that is a multiple of 64 up to 16384 the norms
+        run inside the q|k|v and gate|up launches (btl_add_rmsnorm_linear_group_ref:
+        the same bits, six launches per block instead of eight)."""
         c = self.cfg
         hid, qd = c.hidden, c.n_heads * c.head_dim
         F, R = BTL_F32, BTL_ACT_F32_REF
         cur, nxt = self.h, self.h2
         delta = None  # the block output still to be added to cur
+        # one token row: the norms run inside the projections' launches (more
+        # rows measured slower that way: every workgroup normalises its rows again)
+        fused = m == 1 and hid % 64 == 0 and 64 <= hid <= 16384
         for li, L in enumerate(self._layers):
+            if fused:
+                dl = delta.data_ptr() if delta is not None else None
+                ho = nxt.data_ptr() if delta is not None else None
+                check(lib.btl_add_rmsnorm_linear_group_ref(L["qkv"], self._y_qkv, 3, cur.data_ptr(), dl, ho, L["n1"],
+                                                           c.eps, m, hid, st))
+                if delta is not None:
+                    cur, nxt = nxt, cur
+                check(lib.btl_rope_append_attention(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), m,
+                                                    c.n_heads, ctypes.byref(self.caches[li].c), pos, dp,
+                                                    self.rope_cos.data_ptr(), self.rope_sin.data_ptr(),
+                                                    self.attn.data_ptr(), self._ws, self._ws_n, st))
+                check(lib.btl_linear_group_mode(L["o"], self._y_o, 1, self.attn.data_ptr(), F, m, qd, F, R, None, 0,
+                                                st))
+                check(lib.btl_add_rmsnorm_linear_group_ref(L["gu"], self._y_gu, 2, cur.data_ptr(),
+                                                           self.o.data_ptr(), nxt.data_ptr(), L["n2"], c.eps, m, hid,
+                                                           st))
+                cur, nxt = nxt, cur
+                check(lib.btl_swiglu(self.gate.data_ptr(), self.up.data_ptr(), m * c.intermediate, self.hs.data_ptr(),
+                                     st))
+                check(lib.btl_linear_group_mode(L["down"], self._y_down, 1, self.hs.data_ptr(), F, m, c.intermediate,
+                                                F, R, None, 0, st))
+                delta = self.down
+                continue
             if delta is None:
                 check(lib.btl_add_rmsnorm(cur.data_ptr(), None, None, L["n1"], c.eps, m, hid, self.xn.data_ptr(), st))
             else:

@@ -172,6 +172,9 @@ extern "C" {
                                         h: *const f32, delta: *const f32, h_out: *mut f32, g: *const f32,
                                         eps: f32, m: i64, k: i64, ydtype: c_int, ws: *mut c_void,
                                         ws_bytes: usize, stream: *mut c_void) -> c_int;
+    pub fn btl_add_rmsnorm_linear_group_ref(w: *const *const btl_packed_t, y: *const *mut c_void, count: c_int,
+                                            h: *const f32, delta: *const f32, h_out: *mut f32, g: *const f32,
+                                            eps: f32, m: i64, k: i64, stream: *mut c_void) -> c_int;
     pub fn btl_linear_residual(w: *const btl_packed_t, x: *const c_void, xdtype: c_int, m: i64, k: i64,
                                resid: *const f32, y: *mut f32, ws: *mut c_void, ws_bytes: usize,
                                stream: *mut c_void) -> c_int;

@@ -1028,6 +1028,76 @@ int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, i
                   ws_bytes, (hipStream_t)stream, &xf);
 }
 
+namespace {
+// the reference-order group behind a transform (xf 1): f32 rows of k staged
+// by the kernel itself (k % 64 == 0, 64 <= k <= 16384, 16-byte aligned rows)
+int run_ref_xf(const btl_packed_t* const* w, void* const* y, int count, int64_t m, int64_t k, int xf,
+               const btl::RefXf& t, const void* const* ins, int nin, void* stream)
+{
+    if (count < 1 || count > btl::kMaxGroup) return fail(BTL_ERR_ARG, "count %d not in 1..%d", count, btl::kMaxGroup);
+    if (!w || !y) return fail(BTL_ERR_ARG, "null layer array");
+    if (m < 0 || m > 65535) return fail(BTL_ERR_SHAPE, "m = %lld: need 0 <= m <= 65535", (long long)m);
+    if (k < 64 || k % 64 || k > 16384)
+        return fail(BTL_ERR_SHAPE, "k = %lld: need a multiple of 64 in [64, 16384]", (long long)k);
+    const uint8_t* wd[btl::kMaxGroup];
+    int64_t n[btl::kMaxGroup];
+    float sc[btl::kMaxGroup];
+    void* yy[btl::kMaxGroup];
+    int64_t nsum = 0;
+    int rc;
+    for (int i = 0; i < count; ++i) {
+        if ((rc = check_packed(w[i], m, k))) return rc;
+        if (!aligned16(w[i]->data)) return fail(BTL_ERR_LAYOUT, "weights %d must be 16-byte aligned", i);
+        if (!y[i] && m > 0 && w[i]->n > 0) return fail(BTL_ERR_LAYOUT, "null output %d", i);
+        wd[i] = w[i]->data;
+        n[i] = w[i]->n;
+        sc[i] = w[i]->scale;
+        yy[i] = y[i];
+        nsum += w[i]->n;
+    }
+    if (m == 0 || nsum == 0) return BTL_OK;
+    const uintptr_t rows = (uintptr_t)(m * k * 4);
+    for (int j = 0; j < nin; ++j) {
+        if (!ins[j] && j == 0) return fail(BTL_ERR_LAYOUT, "null input");
+        if (ins[j] && !aligned16(ins[j])) return fail(BTL_ERR_LAYOUT, "inputs must be 16-byte aligned");
+        for (int i = 0; i < count; ++i) {  // no output row overlaps an input the launch still reads
+            const uintptr_t a = (uintptr_t)ins[j], b = (uintptr_t)yy[i], nb = (uintptr_t)(m * n[i] * 4);
+            if (a && a < b + nb && b < a + rows) return fail(BTL_ERR_LAYOUT, "output %d overlaps an input", i);
+        }
+    }
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    const hipError_t e = btl::launch_ref_f32_group(nullptr, btl::XK_F32, m, k, wd, n, sc, yy, count, btl::YK_F32,
+                                                   (hipStream_t)stream, xf, &t);
+    if (e != hipSuccess) return hip_fail(e, "reference-order kernel launch");
+    return BTL_OK;
+}
+}  // namespace
+
+int btl_add_rmsnorm_linear_group_ref(const btl_packed_t* const* w, void* const* y, int count, const float* h,
+                                     const float* delta, float* h_out, const float* g, float eps, int64_t m,
+                                     int64_t k, void* stream)
+{
+    if (!h || !g) return fail(BTL_ERR_LAYOUT, "null residual or norm weight");
+    if (!aligned16(g) || (h_out && !aligned16(h_out))) return fail(BTL_ERR_LAYOUT, "g and h_out must be 16-byte aligned");
+    if (h_out) {  // the launch's other workgroups still read h and delta while h_out is written
+        const uintptr_t o = (uintptr_t)h_out, nb = (uintptr_t)(m * k * 4);
+        const uintptr_t ins[3] = {(uintptr_t)h, (uintptr_t)delta, (uintptr_t)g};
+        const uintptr_t len[3] = {nb, nb, (uintptr_t)(k * 4)};
+        for (int j = 0; j < 3; ++j)
+            if (ins[j] && ins[j] < o + nb && o < ins[j] + len[j])
+                return fail(BTL_ERR_LAYOUT, "h_out overlaps h, delta or g");
+        for (int i = 0; i < count && y; ++i) {
+            const uintptr_t b = (uintptr_t)y[i];
+            if (b && w && w[i] && b < o + nb && o < b + (uintptr_t)(m * w[i]->n * 4))
+                return fail(BTL_ERR_LAYOUT, "h_out overlaps output %d", i);
+        }
+    }
+    const btl::RefXf t{h, delta, h_out, g, eps};
+    const void* ins[4] = {h, delta, h_out, nullptr};
+    return run_ref_xf(w, y, count, m, k, 1, t, ins, 3, stream);
+}
+
 int btl_linear_residual(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int64_t k, const float* resid,
                         float* y, void* ws, size_t ws_bytes, void* stream)
 {

@@ -223,9 +223,18 @@ struct RefGroup {
     int wg_begin[kMaxGroup + 1];  // 32-output workgroups of each layer
     int count;
 };
+// the transform ahead of a reference-order launch (xf 1: residual add +
+// RMSNorm; f32 rows of k, 16-byte aligned)
+struct RefXf {
+    const float* a;  // h
+    const float* b;  // delta (or null)
+    float* h_out;    // h (+ delta), stored by the first output tile's workgroups (or null)
+    const float* g;  // the norm weight
+    float eps;
+};
 hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* const* w,
                                 const int64_t* n, const float* scale, void* const* y, int count, int ykind,
-                                hipStream_t st);
+                                hipStream_t st, int xf = 0, const RefXf* t = nullptr);
 
 hipError_t launch_generic_i8(const int8_t* q, const float* xs, int64_t m, int64_t k,
                              const uint8_t* w, int64_t n, float sw, void* y, int ykind,

@@ -2270,6 +2270,7 @@ __global__ __launch_bounds__(256) void k_ref_f32(const void* x, int64_t m, int64
 // Grouped (several layers reading the same x, btl_linear_group_mode): the
 // workgroups of layer i are [g.wg_begin[i], g.wg_begin[i + 1]) of the grid's x.
 constexpr int kRefRows = 32;                        // outputs (weight rows) per workgroup
+constexpr int kRefMaxBlocks = 4;                    // 4096-element blocks of a staged row (k <= 16384)
 constexpr int kRefStageBytes = 256;                 // bytes of each row per stage
 constexpr int kRefRowStride = kRefStageBytes + 16;  // LDS bytes per row
 constexpr int kRefDepth = 4;                        // stages loaded ahead
@@ -2296,8 +2297,17 @@ __device__ __forceinline__ float ref_apply2(float acc, float xa, float xb, uint3
 // runs its chain for each of them, so a weight chunk's read and coefficient
 // lookup serve TR rows.  KX: the largest k of the instantiation (x's LDS rows
 // are KX / 8 + 4 floats, TR of them per lane row).
-template <int XK, int YK, int DEPTH, int KX, int TR>
-__global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t m, int64_t k, RefGroup g)
+//
+// XF: the transform that makes x in the staging (f32 inputs, the same bits as
+// the separate launch it replaces): 0 none; 1 the residual add and RMSNorm of
+// k_rmsnorm_f32 (s = h (+ delta), the sum of s*s in its pairwise tree, d =
+// sqrt(sum * (f32)(1/k) + eps), x = (s / d) * g; the workgroups of grid.x 0
+// store s to h_out).  Thread t then holds the 16 consecutive elements
+// 16 (256 b + t) .. of every 4096-element block b, as k_rmsnorm_f32's threads
+// do.  (SwiGLU's activation staged by the down projection's workgroups measured
+// slower than its own launch: every workgroup recomputes the whole row's exp.)
+template <int XK, int YK, int DEPTH, int KX, int TR, int XF = 0>
+__global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t m, int64_t k, RefGroup g, RefXf xf)
 {
     static_assert(DEPTH % 2 == 0, "the LDS buffer of a stage is a constant of the unrolled loop");
     constexpr int NW = 4;
@@ -2351,33 +2361,140 @@ __global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t m, in
     // stand as at the top of every later iteration: R[1 .. DEPTH - 1] hold
     // stages 1 .. DEPTH - 1, R[0] stage DEPTH, LDS buffer 0 stage 0.
     // (a token row past m is not loaded: its lanes' sums are not stored)
-    constexpr int XL = KX / (4 * NW * 64);  // x loads per thread and token row
-    typename X4<XK>::T xv[TR][XL];
-    const int kv = K >> 2;
+    if constexpr (XF == 0) {
+        constexpr int XL = KX / (4 * NW * 64);  // x loads per thread and token row
+        typename X4<XK>::T xv[TR][XL];
+        const int kv = K >> 2;
 #pragma unroll
-    for (int r = 0; r < TR; ++r)
+        for (int r = 0; r < TR; ++r)
 #pragma unroll
-        for (int j = 0; j < XL; ++j) {
-            const int t = tid + NW * 64 * j;
-            if (t < kv && row0 + r < m) xv[r][j] = x4_raw<XK>(x, (row0 + r) * k + 4 * t);
-        }
+            for (int j = 0; j < XL; ++j) {
+                const int t = tid + NW * 64 * j;
+                if (t < kv && row0 + r < m) xv[r][j] = x4_raw<XK>(x, (row0 + r) * k + 4 * t);
+            }
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) load(d, R[d]);
+        for (int d = 0; d < DEPTH; ++d) load(d, R[d]);
 #pragma unroll
-    for (int r = 0; r < TR; ++r)
+        for (int r = 0; r < TR; ++r)
 #pragma unroll
-        for (int j = 0; j < XL; ++j) {
-            const int t = tid + NW * 64 * j;
-            if (t < kv && row0 + r < m) {
-                // elements 4 t .. 4 t + 3: lane rows (4 t) & 7 .. + 3, column t / 2
-                float* d = sx + (r * 8 + ((4 * t) & 7)) * S + (t >> 1);
-                const float4 v = x4_f32<XK>(xv[r][j]);
-                d[0] = v.x;
-                d[S] = v.y;
-                d[2 * S] = v.z;
-                d[3 * S] = v.w;
+            for (int j = 0; j < XL; ++j) {
+                const int t = tid + NW * 64 * j;
+                if (t < kv && row0 + r < m) {
+                    // elements 4 t .. 4 t + 3: lane rows (4 t) & 7 .. + 3, column t / 2
+                    float* d = sx + (r * 8 + ((4 * t) & 7)) * S + (t >> 1);
+                    const float4 v = x4_f32<XK>(xv[r][j]);
+                    d[0] = v.x;
+                    d[S] = v.y;
+                    d[2 * S] = v.z;
+                    d[3 * S] = v.w;
+                }
+            }
+    } else {
+        constexpr int NB = KX / 4096;  // 4096-element blocks
+        static_assert(NB * 4096 == KX && NB <= kRefMaxBlocks, "KX is a multiple of 4096");
+        float v[TR][NB][16];
+#pragma unroll
+        for (int r = 0; r < TR; ++r)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int e0 = 16 * (256 * b + tid);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (row0 + r < m && e0 + 4 * q < K) {
+                        const int64_t e = (row0 + r) * k + e0 + 4 * q;
+                        a = *(const float4*)(xf.a + e);
+                        if (xf.b) {
+                            const float4 c = *(const float4*)(xf.b + e);
+                            a = make_float4(__fadd_rn(a.x, c.x), __fadd_rn(a.y, c.y), __fadd_rn(a.z, c.z),
+                                            __fadd_rn(a.w, c.w));
+                        }
+                    }
+                    v[r][b][4 * q] = a.x;
+                    v[r][b][4 * q + 1] = a.y;
+                    v[r][b][4 * q + 2] = a.z;
+                    v[r][b][4 * q + 3] = a.w;
+                }
+            }
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) load(d, R[d]);
+        {
+            __shared__ float s_w[TR][4];
+            __shared__ float s_blk[TR][kRefMaxBlocks];
+            __shared__ float s_d[TR];
+            const int nblk = (K + 4095) >> 12;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if (b < nblk) {  // uniform
+#pragma unroll
+                    for (int r = 0; r < TR; ++r) {
+                        float sq[16];
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) sq[e] = __fmul_rn(v[r][b][e], v[r][b][e]);
+#pragma unroll
+                        for (int len = 16; len > 1; len >>= 1)
+#pragma unroll
+                            for (int i = 0; i < len / 2; ++i) sq[i] = __fadd_rn(sq[2 * i], sq[2 * i + 1]);
+                        const float ws = wave_pairwise_sum(sq[0]);
+                        if (lane == 0) s_w[r][wave] = ws;
+                    }
+                    __syncthreads();
+                    if (tid < TR)
+                        s_blk[tid][b] = __fadd_rn(__fadd_rn(s_w[tid][0], s_w[tid][1]), __fadd_rn(s_w[tid][2], s_w[tid][3]));
+                    __syncthreads();
+                }
+            }
+            if (tid < TR) {
+                float p[kRefMaxBlocks];
+#pragma unroll
+                for (int b = 0; b < kRefMaxBlocks; ++b) p[b] = b < nblk ? s_blk[tid][b] : 0.0f;
+#pragma unroll
+                for (int len = kRefMaxBlocks; len > 1; len >>= 1)
+#pragma unroll
+                    for (int i = 0; i < len / 2; ++i) p[i] = __fadd_rn(p[2 * i], p[2 * i + 1]);
+                const float inv_k = (float)(1.0 / (double)K);
+                s_d[tid] = sqrt_rn(__fadd_rn(__fmul_rn(p[0], inv_k), xf.eps));
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < TR; ++r) {
+                const float dr = s_d[r];
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const int e0 = 16 * (256 * b + tid);
+                    if (row0 + r < m && e0 < K) {
+                        const int64_t e = (row0 + r) * k + e0;
+                        if (xf.h_out && blockIdx.x == 0) {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q)
+                                *(float4*)(xf.h_out + e + 4 * q) = make_float4(
+                                    v[r][b][4 * q], v[r][b][4 * q + 1], v[r][b][4 * q + 2], v[r][b][4 * q + 3]);
+                        }
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float4 gv = *(const float4*)(xf.g + e0 + 4 * q);
+                            v[r][b][4 * q] = __fmul_rn(__fdiv_rn(v[r][b][4 * q], dr), gv.x);
+                            v[r][b][4 * q + 1] = __fmul_rn(__fdiv_rn(v[r][b][4 * q + 1], dr), gv.y);
+                            v[r][b][4 * q + 2] = __fmul_rn(__fdiv_rn(v[r][b][4 * q + 2], dr), gv.z);
+                            v[r][b][4 * q + 3] = __fmul_rn(__fdiv_rn(v[r][b][4 * q + 3], dr), gv.w);
+                        }
+                    }
+                }
             }
         }
+        // x into LDS lane-major: element e at lane row e & 7, column e / 8
+#pragma unroll
+        for (int r = 0; r < TR; ++r)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int e0 = 16 * (256 * b + tid);
+                if (row0 + r < m && e0 < K) {
+                    float* d = sx + r * 8 * S + (e0 >> 3);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) d[(e & 7) * S + (e >> 3)] = v[r][b][e];
+                }
+            }
+    }
     put(R[0], 0);
     load(DEPTH, R[0]);
     __syncthreads();  // x and stage 0 staged
@@ -2468,12 +2585,29 @@ __global__ __launch_bounds__(256) void k_ref_f32_st(const void* x, int64_t m, in
     }
 }
 
+// the staged kernel's launch; the transform (xf 1) exists for f32 inputs only
+template <int XK, int YK, int KX, int TR>
+static void launch_ref_st(dim3 grid, hipStream_t st, const void* x, int64_t m, int64_t k, const RefGroup& g,
+                          const RefXf& tx, int xf)
+{
+    if constexpr (XK == XK_F32) {
+        if (xf == 1) {
+            hipLaunchKernelGGL((k_ref_f32_st<XK, YK, kRefDepth, KX, TR, 1>), grid, dim3(256), 0, st, x, m, k, g, tx);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_ref_f32_st<XK, YK, kRefDepth, KX, TR>), grid, dim3(256), 0, st, x, m, k, g, tx);
+}
+
 hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* const* w,
                                 const int64_t* n, const float* scale, void* const* y, int count, int ykind,
-                                hipStream_t st)
+                                hipStream_t st, int xf, const RefXf* t)
 {
     if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
-    bool lds_ok = k % 64 == 0 && k <= 16384 && m <= 65535 && ((uintptr_t)x & 15u) == 0;
+    // a transform runs only in the staged form, on f32 rows the caller checked
+    // (k % 64 == 0, k <= 16384, 16-byte aligned)
+    if (xf != 0 && (!t || xkind != XK_F32 || k % 64 != 0 || k > 16384 || m > 65535)) return hipErrorInvalidValue;
+    bool lds_ok = k % 64 == 0 && k <= 16384 && m <= 65535 && (xf != 0 || ((uintptr_t)x & 15u) == 0);
     int64_t n_total = 0;
     for (int i = 0; i < count; ++i) {
         lds_ok = lds_ok && ((uintptr_t)w[i] & 15u) == 0;
@@ -2481,6 +2615,7 @@ hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, 
     }
     if (m <= 0 || n_total == 0) return hipSuccess;
     const int rows = kRefRows;
+    if (xf != 0 && (!lds_ok || n_total / rows + count > INT32_MAX)) return hipErrorInvalidValue;
     if (!lds_ok || n_total / rows + count > INT32_MAX) {
         for (int i = 0; i < count; ++i) {
             const hipError_t e = launch_ref_f32(x, xkind, m, k, w[i], n[i], scale[i], y[i], ykind, st);
@@ -2504,9 +2639,10 @@ hipError_t launch_ref_f32_group(const void* x, int xkind, int64_t m, int64_t k, 
     // coefficient lookup shared; x of both rows in LDS: at most 2 x 64 KB)
     const int tr = m >= 2 ? 2 : 1;
     const dim3 grid((unsigned)b, (unsigned)((m + tr - 1) / tr));
-#define BTL_REF_ST(XKV, YKV, KXV)                                                                              \
-    if (tr == 2) hipLaunchKernelGGL((k_ref_f32_st<XKV, YKV, kRefDepth, KXV, 2>), grid, dim3(256), 0, st, x, m, k, g); \
-    else hipLaunchKernelGGL((k_ref_f32_st<XKV, YKV, kRefDepth, KXV, 1>), grid, dim3(256), 0, st, x, m, k, g);         \
+    const RefXf tx = t ? *t : RefXf{};
+#define BTL_REF_ST(XKV, YKV, KXV)                                                          \
+    if (tr == 2) launch_ref_st<XKV, YKV, KXV, 2>(grid, st, x, m, k, g, tx, xf);              \
+    else launch_ref_st<XKV, YKV, KXV, 1>(grid, st, x, m, k, g, tx, xf);                      \
     return hipGetLastError();
 #define BTL_REF_LDS(XKV, YKV)                              \
     if (xkind == XKV && ykind == YKV) {                    \

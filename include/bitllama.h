@@ -181,6 +181,23 @@ int btl_add_rmsnorm_linear_group(const btl_packed_t* const* w, void* const* y, i
                                  int ydtype, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The same in the reference's arithmetic (the BitLinears as BitLinearCpu::forward,
+ * kernels/cpu.rs:17-127), in one launch: the same bits as
+ * btl_add_rmsnorm(h, delta, h_out, g, eps, m, k, xn) followed by
+ * btl_linear_group_mode(w, y, count, xn, BTL_F32, m, k, BTL_F32, BTL_ACT_F32_REF, ...).
+ * Every workgroup forms the normalised rows it needs while staging them; the
+ * first output tile's workgroups store s = h (+ delta) to h_out (when not NULL).
+ * h, delta (or NULL), h_out (or NULL) [m, k] f32, g [k] f32, y[i] [m, n_i] f32;
+ * k % 64 == 0, 64 <= k <= 16384, m <= 65535; h, delta, h_out, g and the packed
+ * rows 16-byte aligned; h_out overlaps none of h, delta, g and y, and y no input.
+ * No reference function of its own: the norm ahead of a block's projections
+ * (block.rs:122-123,137) fused with them.
+ */
+int btl_add_rmsnorm_linear_group_ref(const btl_packed_t* const* w, void* const* y, int count, const float* h,
+                                     const float* delta, float* h_out, const float* g, float eps, int64_t m,
+                                     int64_t k, void* stream);
+
+/*
  * A BitLinear with the residual connection after it (block.rs:119,131:
  * residual + mixed_out): y = resid + x W^T, the W1.58-A8 product as
  * btl_linear's then one f32 add per element.  x [m, k] f32 or bf16 (xdtype),

@@ -716,6 +716,80 @@ def test_add_rmsnorm_rows(m, k, mode):
         assert_same(ht, s, "h in place")
 
 
+# the reference's arithmetic with the residual add + RMSNorm staged by the
+# projections' own launch: the same bits as btl_add_rmsnorm followed by
+# btl_linear_group_mode (BTL_ACT_F32_REF) and as the oracle; h_out from the
+# first output tile's workgroups, h and delta untouched; m = 3 runs a second
+# token-row pair with one row past m; k = 14336 stages four 4096-element blocks
+@pytest.mark.parametrize("m,k,ns", [(1, 4096, (96, 40, 33)), (3, 4096, (700,)), (2, 14336, (64, 50)), (1, 64, (40,)),
+                                    (3, 2112, (130, 33))])
+@pytest.mark.parametrize("mode", ["plain", "delta", "delta_out", "plain_out"])
+def test_add_rmsnorm_linear_group_ref(m, k, ns, mode):
+    print("add_rmsnorm_linear_group_ref", m, k, ns, mode, flush=True)
+    rng = np.random.default_rng(m * 3 + k + len(ns))
+    h = (rng.standard_normal((m, k)) * np.exp2(rng.integers(-8, 8, (m, k)))).astype(np.float32)
+    d = rng.standard_normal((m, k)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    layers = []
+    for i, n in enumerate(ns):
+        wb, sw = orc.pack((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        layers.append((bl.PackedTensor(torch.from_numpy(wb).to(DEV), sw, (n, k), DEV), wb, sw, n))
+    ht, dt, gt = (torch.from_numpy(a).to(DEV) for a in (h, d, g))
+    ho = torch.full_like(ht, 5.0)
+    cnt = len(layers)
+    cs = [L[0].as_c() for L in layers]
+    arr = (ctypes.POINTER(bl.BtlPacked) * cnt)(*[ctypes.pointer(c) for c in cs])
+    outs = [torch.full((m, n), 7.0, device=DEV) for (_, _, _, n) in layers]
+    ys = (ctypes.c_void_p * cnt)(*[o.data_ptr() for o in outs])
+    delta = dt.data_ptr() if mode.startswith("delta") else None
+    hout = ho.data_ptr() if mode.endswith("_out") else None
+    bl.check(bl.lib.btl_add_rmsnorm_linear_group_ref(arr, ys, cnt, ht.data_ptr(), delta, hout, gt.data_ptr(), 1e-5,
+                                                     m, k, stream()))
+    s_ = (h + d).astype(np.float32) if delta else h
+    xn = orc.rmsnorm(s_, g, 1e-5)
+    for o, (_, wb, sw, n) in zip(outs, layers):
+        assert_same(o, orc.forward_f32(xn, wb, n, np.float32(sw)), "layer")
+    assert_same(ht, h, "h untouched")
+    assert_same(ho, s_ if hout else np.full((m, k), 5.0, np.float32), "h_out")
+    # the two launches it replaces give the same bits
+    xt = torch.empty((m, k), device=DEV)
+    bl.check(bl.lib.btl_add_rmsnorm(ht.data_ptr(), delta, None, gt.data_ptr(), 1e-5, m, k, xt.data_ptr(), stream()))
+    outs2 = [torch.empty((m, n), device=DEV) for (_, _, _, n) in layers]
+    ys2 = (ctypes.c_void_p * cnt)(*[o.data_ptr() for o in outs2])
+    bl.check(bl.lib.btl_linear_group_mode(arr, ys2, cnt, xt.data_ptr(), bl.BTL_F32, m, k, bl.BTL_F32,
+                                          bl.BTL_ACT_F32_REF, None, 0, stream()))
+    for a, b in zip(outs, outs2):
+        assert torch.equal(a, b)
+
+
+def test_fused_ref_rejects_bad_shapes_and_overlap():
+    k, m = 4096, 2
+    h = torch.zeros((m, k), device=DEV)
+    g = torch.ones(k, device=DEV)
+    wb, sw = orc.pack(np.full((8, k), 0.01, np.float32))
+    pt = bl.PackedTensor(torch.from_numpy(wb).to(DEV), sw, (8, k), DEV)
+    c = pt.as_c()
+    arr = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(c))
+    y = torch.empty((m, 8), device=DEV)
+    ys = (ctypes.c_void_p * 1)(y.data_ptr())
+    # h_out over h: the launch's other workgroups still read h
+    assert bl.lib.btl_add_rmsnorm_linear_group_ref(arr, ys, 1, h.data_ptr(), None, h.data_ptr(), g.data_ptr(), 1e-5,
+                                                   m, k, stream()) == bl.BTL_ERR_LAYOUT
+    # y over the input
+    ys_bad = (ctypes.c_void_p * 1)(h.data_ptr())
+    assert bl.lib.btl_add_rmsnorm_linear_group_ref(arr, ys_bad, 1, h.data_ptr(), None, None, g.data_ptr(), 1e-5,
+                                                   m, k, stream()) == bl.BTL_ERR_LAYOUT
+    # k past the staged form
+    h2 = torch.zeros((1, 16448), device=DEV)
+    g2 = torch.ones(16448, device=DEV)
+    w2, s2 = orc.pack(np.full((8, 16448), 0.01, np.float32))
+    p2 = bl.PackedTensor(torch.from_numpy(w2).to(DEV), s2, (8, 16448), DEV)
+    c2 = p2.as_c()
+    arr2 = (ctypes.POINTER(bl.BtlPacked) * 1)(ctypes.pointer(c2))
+    assert bl.lib.btl_add_rmsnorm_linear_group_ref(arr2, ys, 1, h2.data_ptr(), None, None, g2.data_ptr(), 1e-5, 1,
+                                                   16448, stream()) == bl.BTL_ERR_SHAPE
+
+
 def test_add_rmsnorm_rejects_overlap():
     h = torch.zeros((2, 256), device=DEV)
     g = torch.ones(256, device=DEV)
