@@ -104,6 +104,7 @@ constexpr KnobDef kKnobs[btl::KN_COUNT] = {
     {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1}, {"BTL_SPLIT_MERGE", 1},
     {"BTL_SPLIT_MERGE_MAX_M", 16}, {"BTL_GEMV_BAT_NW", 0}, {"BTL_GEMV_BAT_KS", 0},
     {"BTL_GEMM_TILE", 0}, {"BTL_GEMM_TM64", 1}, {"BTL_GEMM_TM64_STAGES", 0}, {"BTL_GEMM_STAGES", 0},
+    {"BTL_DEC_RQ2_MAX_K", 16384},
 };
 std::atomic<int> g_knob[btl::KN_COUNT];
 std::once_flag g_knob_once;
@@ -310,11 +311,11 @@ int dec_waves(int64_t m, int64_t k, int* rb_out)
 // pairing (pair_n = the rows of gate and of up) the count is even: half the
 // waves take gate's rows, half the same rows of up.  BTL_DEC_RQ_WPC overrides
 // it (tuning).
-int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n, bool xform, int m)
+int rq_waves_per_group(int64_t rb_total, int64_t k, int cus, int64_t pair_n, int dg, int m)
 {
     const int rows = k <= 4096 ? 4 : 2;
     const int64_t waves = pair_n ? 2 * ceil_div(pair_n, rows) : rb_total * (16 / rows);
-    const int hi = 16 - btl::rq_quant_waves((int)k, xform ? 1 : 2, m);
+    const int hi = 16 - btl::rq_quant_waves((int)k, dg, m);
     const int step = pair_n ? 2 : 1;
     const int forced = env_int(btl::KN_DEC_RQ_WPC);
     if (forced >= step && forced <= hi && forced % step == 0) return forced;
@@ -484,13 +485,14 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     // 4096, no SwiGLU epilogue, at most KN_FUSE_MAX_WG workgroups: each repeats
     // it); the SwiGLU pairing takes tokens transformed by a launch of their own.
     const bool rq_on = dec && k % 64 == 0 && k >= env_int(btl::KN_DEC_RQ_MIN_K) && env_int(btl::KN_DEC_RQ) != 0 &&
-                       ((m == 1 && k <= 16384) || (m == 2 && k <= 4096 && !xf && !swiglu_out));
+                       ((m == 1 && k <= 16384) ||
+                        (m == 2 && k <= 16384 && k <= env_int(btl::KN_DEC_RQ2_MAX_K) && !xf && !swiglu_out));
     bool rqx = false;
     int rqx_wpc = 0;
     if (rq_on && xf_ok && k <= 4096 && (!swiglu_out || xf->kind == btl::XF_RMSNORM)) {
         // with the SwiGLU pairing (RMSNorm only): two groups per quantising thread
         const int64_t pn = swiglu_out ? layers[0].w->n : 0;
-        rqx_wpc = rq_waves_per_group(dec_rb, k, g_dev[dev].cus, pn, !swiglu_out, 1);
+        rqx_wpc = rq_waves_per_group(dec_rb, k, g_dev[dev].cus, pn, swiglu_out ? 2 : 1, 1);
         rqx = (swiglu_out ? ceil_div(ceil_div(pn, 4), rqx_wpc / 2) : ceil_div(dec_rb * 4, rqx_wpc)) <= fuse_max_wg;
     }
     // Otherwise the K-part / row-contiguous decode kernel applies a transform in
@@ -560,8 +562,11 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
         a.rowc = rowc;
         a.spin = env_int(btl::KN_WAIT_SPIN);
         if (rq) {
+            // two token rows of k > 4096: four token groups per quantising
+            // thread (two would take 14 quantising waves of the 16)
+            const int dg2 = m == 2 && (k > 4096 || env_int(btl::KN_DEC_RQ_DG) == 4) ? 4 : 2;
             a.parts = rqx ? rqx_wpc
-                          : rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0, false, (int)m);
+                          : rq_waves_per_group(rb, k, g_dev[dev].cus, swiglu_out ? a.p[0].n : 0, dg2, (int)m);
             // one token group per quantising thread when the workgroup has room
             // for the quantising waves that takes (one token row, k <= 4096): a
             // shorter prologue for the launches of few compute waves
@@ -569,7 +574,7 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
                               (!rqx && m == 1 && k <= 4096 && !swiglu_out &&
                                btl::rq_quant_waves((int)k, 1) + a.parts <= 16 && env_int(btl::KN_DEC_RQ_DG) != 2)
                           ? 1
-                          : 2;
+                          : dg2;
             a.resid = count == 1 ? resid : nullptr;
             e = btl::launch_gemv_rq(a, pre ? (int)btl::XK_I8O : xkind, rqx ? xform : (int)btl::XF_NONE, st);
             if (e != hipSuccess) return hip_fail(e, "decode gemv kernel launch");

@@ -27,7 +27,7 @@ enum Knob {
     KN_FUSE_DEC,             // 0 turns transform fusion into the decode kernels off (1)
     KN_DEC_RQ_MIN_K,         // row-group decode form from this k on (1024)
     KN_DEC_RQ,               // 0 turns the row-group decode form off (1)
-    KN_DEC_RQ_DG,            // 2 forces two token groups per quantising thread (0 = rule)
+    KN_DEC_RQ_DG,            // 2 forces two token groups per quantising thread, 4 four for two token rows (0 = rule)
     KN_GEMM_MAX_SPLITS,      // cap on the K splits of the GEMM (0 = none; 1 turns split-K off)
     KN_GEMM_WIDE_MIN_TILES,  // 256-row GEMM tiles from this many workgroups on (512)
     KN_WAIT_SPIN,            // polls before a kernel's internal wait gives up (2^22; the only
@@ -42,6 +42,7 @@ enum Knob {
     KN_GEMM_TM64,            // 0: the GEMM keeps 128-token tiles for m <= 64 (1: 64-token tiles)
     KN_GEMM_TM64_STAGES,     // force the LDS stages of the 64-token tiles (2 or 4; 0 = rule)
     KN_GEMM_STAGES,          // force the LDS stages of the 128-token tiles (2 or 3; 0 = rule)
+    KN_DEC_RQ2_MAX_K,        // two token rows take the row-group decode form up to this k (16384)
     KN_COUNT
 };
 int knob(Knob k);
@@ -127,10 +128,11 @@ constexpr int kDecGroups = 4;  // 16-element token groups per thread in the prol
 hipError_t launch_gemv_dec(const GemvArgs& a, int xkind, int xform, hipStream_t s);
 
 // Decode, row-group form (k_gemv_rq): m == 1, k % 64 == 0, k <= 16384, or m == 2
-// token rows with k <= 4096 (no transform, no SwiGLU epilogue, dg = 2).
+// token rows (no transform, no SwiGLU epilogue; dg = 2 for k <= 4096, else 4).
 // R = 4 rows per compute wave for k <= 4096, else 2.  A workgroup is
 // rq_quant_waves(k, dg) quantising waves, dg = a.tiles 16-element token groups
-// per thread (1 for k <= 4096 only, else 2), and a.parts compute waves, at most
+// per thread (1 for k <= 4096 only, else 2; 4 for two rows of k > 4096, or
+// of any k), and a.parts compute waves, at most
 // 16 in all; a.kpart unused.  The SwiGLU epilogue (a.swiglu_out) takes
 // operand-order int8 tokens, dg = 2 and an even a.parts; a transform (xform,
 // the fields of the decode kernel's) takes f32 tokens, k <= 4096 and dg = 1.

@@ -782,12 +782,12 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
 
 template <int XK, int R, int ST, bool PAIR = false, int XF = XF_NONE, int DG = 2, int MT = 1>
 __global__ __launch_bounds__(1024)
-__attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) void k_gemv_rq(GemvArgs a)
+__attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) && !(DG == 4 && XK == XK_F32) ? 8 : 4))) void k_gemv_rq(GemvArgs a)
 {
     static_assert(XF == XF_NONE || (XK == XK_F32 && R == 4 && MT == 1 && (PAIR ? XF == XF_RMSNORM && DG == 2 : DG == 1)),
                   "transforms: one f32 token row, k <= 4096; with the SwiGLU pairing RMSNorm only");
-    static_assert(DG == 1 || DG == 2, "one or two token groups per quantising thread");
-    static_assert(MT == 1 || (MT == 2 && R == 4 && !PAIR), "two token rows: k <= 4096, no SwiGLU epilogue");
+    static_assert(DG == 1 || DG == 2 || (DG == 4 && MT == 2), "one, two or (two token rows) four token groups per thread");
+    static_assert(MT == 1 || (MT == 2 && !PAIR && XF == XF_NONE), "two token rows: no transform, no SwiGLU epilogue");
     constexpr bool XN = XF == XF_RMSNORM || XF == XF_ADD_RMSNORM;   // a norm over the row
     constexpr bool X2 = XF == XF_ADD_RMSNORM || XF == XF_SWIGLU;    // a second input row
     constexpr int SUB = RqShape<R>::kSub, RB = RqShape<R>::kBytes;
@@ -1011,7 +1011,8 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) ? 8 : 4))) 
 
 // Loads per compute wave: ceil(k * R / 4096); R = 4 for k <= 4096 (ST 1..4),
 // R = 2 above (ST 3..8, k <= 16384).  Workgroup: rq_quant_waves(k) + a.parts
-// waves, at most 16.
+// waves, at most 16.  Two token rows: two or four groups per quantising
+// thread for k <= 4096, four above (the quantising waves of one row's two groups).
 hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s)
 {
     const int R = a.k <= 4096 ? 4 : 2;
@@ -1019,9 +1020,10 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
     const int dg = a.tiles;
     const int nqw = rq_quant_waves(a.k, dg, a.m);
     const bool pair = a.swiglu_out != nullptr;
-    if ((dg != 1 && dg != 2) || (dg == 1 && (R != 4 || pair)) || (xform != XF_NONE && dg != (pair ? 2 : 1)))
+    if ((dg != 1 && dg != 2 && dg != 4) || (dg == 1 && (R != 4 || pair)) || (dg == 4 && a.m != 2) ||
+        (xform != XF_NONE && dg != (pair ? 2 : 1)))
         return hipErrorInvalidValue;
-    if (a.m < 1 || a.m > 2 || (a.m > 1 && (R != 4 || pair || xform != XF_NONE || dg != 2)) || a.k % 64 != 0 ||
+    if (a.m < 1 || a.m > 2 || (a.m > 1 && (pair || xform != XF_NONE || (dg != 4 && (R != 4 || dg != 2)))) || a.k % 64 != 0 ||
         a.k < 64 || a.k > 16384 || a.parts < 1 || nqw + a.parts > 16 || a.rb_total < 1 ||
         (xkind != XK_F32 && xkind != XK_BF16 && xkind != XK_I8 && xkind != XK_I8O))
         return hipErrorInvalidValue;
@@ -1064,7 +1066,8 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
     const int mt = a.m;
     const size_t lds = (size_t)mt * (a.k + 16);
 #define BTL_RQ_DG(XKV, RV, STV)                                                                                    \
-    if (RV == 4 && mt == 2) hipLaunchKernelGGL((k_gemv_rq<XKV, 4, STV, false, XF_NONE, 2, 2>), grid, block, lds, s, a); \
+    if (RV == 4 && mt == 2 && dg == 2) hipLaunchKernelGGL((k_gemv_rq<XKV, 4, STV, false, XF_NONE, 2, 2>), grid, block, lds, s, a); \
+    else if (mt == 2) hipLaunchKernelGGL((k_gemv_rq<XKV, RV, STV, false, XF_NONE, 4, 2>), grid, block, lds, s, a); \
     else if (RV == 4 && dg == 1) hipLaunchKernelGGL((k_gemv_rq<XKV, RV, STV, false, XF_NONE, 1>), grid, block, lds, s, a); \
     else hipLaunchKernelGGL((k_gemv_rq<XKV, RV, STV>), grid, block, lds, s, a);
 #define BTL_RQ_XK(RV, STV)                                                                                       \

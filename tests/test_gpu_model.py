@@ -446,7 +446,8 @@ def test_one_token_transforms_both_forms(k, kind, form, tune):
 
 @pytest.mark.parametrize("m,k,n,xdt", [(1, 4096, 4096, "f32"), (1, 14336, 4096, "f32"), (1, 4096, 1000, "f32"),
                                         (1, 1024, 150, "bf16"), (1, 512, 96, "f32"), (1, 1000, 40, "f32"),
-                                        (2, 4096, 300, "f32"), (2, 2048, 200, "bf16"), (3, 1024, 100, "f32"),
+                                        (2, 4096, 300, "f32"), (2, 2048, 200, "bf16"), (2, 14336, 300, "f32"),
+                                        (2, 6144, 90, "bf16"), (3, 1024, 100, "f32"),
                                         (70, 512, 200, "f32")])
 def test_linear_residual(m, k, n, xdt):
     # y = resid + x W^T.  One row, 1024 <= k <= 16384 (and two rows, k <= 4096):

@@ -269,12 +269,14 @@ def test_decode_row_group_form_exact(k, wpc, xdt, dg, tune):
     assert torch.equal(acc, acc2) and torch.equal(y, y2)
 
 
-# Two token rows, k <= 4096: the row-group form with one accumulator per token
-# row (every unpacked weight word feeds each row's MFMA) and a per-row absmax
-# over the quantising waves; three and four rows take the batched route.  Every
-# route gives the oracle's bits and those of the K-part form.
+# Two token rows: the row-group form with one accumulator per token row (every
+# unpacked weight word feeds each row's MFMA) and a per-row absmax over the
+# quantising waves (two token groups per quantising thread for k <= 4096, four
+# above: R = 2 rows per compute wave, 3..8 loads); three and four rows take the
+# batched route.  Every route gives the oracle's bits and those of the K-part
+# form.
 @pytest.mark.parametrize("m", [2, 3, 4])
-@pytest.mark.parametrize("k", [1024, 1088, 2048, 3072, 4096])
+@pytest.mark.parametrize("k", [1024, 1088, 2048, 3072, 4096, 4160, 6144, 8192, 12352, 14336, 16384])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
 def test_decode_row_group_form_token_rows(m, k, xdt, tune):
     print("row-group form, token rows", m, k, xdt, flush=True)
@@ -299,6 +301,24 @@ def test_decode_row_group_form_token_rows(m, k, xdt, tune):
     acc2 = torch.empty_like(acc)
     y2 = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc2)
     assert torch.equal(acc, acc2) and torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("k", [1024, 1088, 4096])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_decode_row_group_form_two_rows_four_groups(k, xdt, tune):
+    # two token rows of k <= 4096 with four token groups per quantising thread
+    # (half the quantising waves, room for twice the compute waves)
+    m, n = 2, 330
+    x = activations(m, k, seed=k + 41)
+    x[1, 5] = np.float32(30.0)
+    pt, wb, sw = make_layer(n, k, seed=k + 42)
+    xt = to_dev(x, xdt)
+    tune("BTL_DEC_RQ_DG", "4")
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, out_dtype=torch.float32, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert_f32_identical(y, yr)
 
 
 @pytest.mark.parametrize("k", [4096, 14336])
