@@ -477,9 +477,10 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     const bool xf_ok = xf && m == 1 && xkind == btl::XK_F32 && env_int(btl::KN_FUSE_DEC) != 0 &&
                        !(xf->kind == btl::XF_ADD_RMSNORM && (const void*)xf->hout == x);
 
-    // One token row (two for k <= 4096; measured on MI355X, Llama-3-8B MLP: the
-    // K-part form is faster from three rows on, where the quantising waves
-    // take half of every workgroup): the row-group form (R whole rows per
+    // One or two token rows (measured on MI355X, Llama-3-8B MLP: down at m = 2
+    // 8.1 against 9.1 us through the K-part form; from three rows on the
+    // batched kernel is faster, with four rows the row-group form takes four
+    // MFMAs per packed word): the row-group form (R whole rows per
     // wave, one accumulator per token row, workgroups of up to 16 waves of
     // which only the first few quantise the tokens).  Its quantising waves also apply a transform (k <=
     // 4096, no SwiGLU epilogue, at most KN_FUSE_MAX_WG workgroups: each repeats
