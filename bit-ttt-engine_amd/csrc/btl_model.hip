@@ -237,7 +237,7 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
     const int g = blockIdx.x, c = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nthr = blockDim.x;
-    const int hd = a.hd, rep = a.nh / a.nkv;
+    const int hd = HD ? HD : a.hd, rep = a.nh / a.nkv;  // HD > 0: launched for a.hd == HD
     const int h = g * rep + wave;
     const int pos0 = a.d_pos ? *a.d_pos : a.pos;
     const int i_begin = blockIdx.z * a.qb;
@@ -255,10 +255,12 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
         const int vpr = hd >> 4, nvec = nstage * vpr;
         uint4 kv[8], vv[8];
         float ks[8], vs[8];
+        // a uniform bound and every lane loading (a lane past the chunk
+        // reloads its last vector), as in k_attn_dec1
 #pragma unroll
         for (int it = 0; it < 8; ++it) {
-            const int idx = tid + it * nthr;
-            if (idx < nvec) {
+            if (it * nthr < nvec) {  // uniform
+                const int idx = min(tid + it * nthr, nvec - 1);
                 const int j = idx / vpr;
                 kv[it] = ((const uint4*)(a.kc + (base + j) * hd))[idx - j * vpr];
                 vv[it] = ((const uint4*)(a.vc + (base + j) * hd))[idx - j * vpr];
@@ -415,7 +417,10 @@ __global__ __launch_bounds__(1024) void k_attn_dec1(AttnArgs a, DecKv kv)
     const int g = blockIdx.x, c = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nthr = blockDim.x;
-    const int hd = a.hd, half = hd >> 1, rep = a.nh / a.nkv;
+    // HD > 0 (the host launches it for a.hd == HD): the head size is a
+    // constant, so the rows' lane predicates fold and their loads issue
+    // back to back instead of in one branch each
+    const int hd = HD ? HD : a.hd, half = hd >> 1, rep = a.nh / a.nkv;
     const int h = g * rep + wave;
     const int j0 = c * kAttnChunk;
     if (j0 >= a.max_seq) return;  // uniform
