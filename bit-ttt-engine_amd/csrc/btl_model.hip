@@ -336,14 +336,21 @@ __device__ __forceinline__ void attn_merge_head(const float* part, int st, int c
     const int d0 = lane, d1 = lane + 64;
     const bool h0 = d0 < hd, h1 = d1 < hd;
     constexpr int kPre = 16;
+    // every load unconditional, slots past cpre clamped to slot cpre - 1 (their
+    // values are never used): a per-lane or per-slot condition here made the
+    // compiler wait for the earlier loads before issuing the (m, l) loads
+    const int clast = max(cpre, 1) - 1;
+    const int cl = min(lane, clast);
+    const float m_pre = ld_part<SC1>(&part[cl * st]);
+    const float l_pre = ld_part<SC1>(&part[cl * st + 1]);
     float p0[kPre], p1[kPre];
 #pragma unroll
     for (int c = 0; c < kPre; ++c) {
-        p0[c] = (c < cpre && h0) ? ld_part<SC1>(&part[c * st + 2 + d0]) : 0.0f;
-        p1[c] = (c < cpre && h1) ? ld_part<SC1>(&part[c * st + 2 + d1]) : 0.0f;
+        const int cc = min(c, clast);
+        p0[c] = h0 ? ld_part<SC1>(&part[cc * st + 2 + d0]) : 0.0f;
+        p1[c] = h1 ? ld_part<SC1>(&part[cc * st + 2 + d1]) : 0.0f;
     }
-    const float m_pre = lane < cpre ? ld_part<SC1>(&part[lane * st]) : 0.0f;
-    const float l_pre = lane < cpre ? ld_part<SC1>(&part[lane * st + 1]) : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);  // all of them issue before the first use
     const int C = cfun();
     if (C <= 0) {
         if (h0) y[d0] = __builtin_nanf("");
