@@ -203,7 +203,7 @@ int btl_add_rmsnorm_linear_group_ref(const btl_packed_t* const* w, void* const* 
  * btl_linear's then one f32 add per element.  x [m, k] f32 or bf16 (xdtype),
  * resid and y [m, n] f32; y must overlap neither resid nor x.  On the decode
  * kernel of whole weight rows (one token row with k % 64 == 0 and
- * 1024 <= k <= 16384, two with k <= 4096) the add runs in its epilogue (one
+ * 1024 <= k <= 16384, one or two token rows) the add runs in its epilogue (one
  * launch), otherwise in an elementwise launch after the product.  It lets the
  * decoder drop the add from the next residual + RMSNorm:
  * btl_add_rmsnorm_linear_group / btl_add_rmsnorm_swiglu on y with delta = NULL
