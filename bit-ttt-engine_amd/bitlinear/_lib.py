@@ -28,7 +28,7 @@ BTL_ACT_I8 = 1
 # Every symbol include/bitlinear.h declares.
 EXPORTS = (
     "btl_version", "btl_last_error", "btl_status_string", "btl_init", "btl_set_tuning", "btl_get_tuning",
-    "btl_check_faults", "btl_packed_bytes",
+    "btl_check_faults", "btl_last_gemm_form", "btl_packed_bytes",
     "btl_pack_host", "btl_unpack_host", "btl_pack_device", "btl_pack_workspace_bytes", "btl_unpack_device",
     "btl_quantize_act", "btl_linear", "btl_linear_noalloc",
     "btl_linear_i8", "btl_linear_group", "btl_linear_group_mode", "btl_quantize_act_op", "btl_linear_i8_op",
@@ -86,6 +86,7 @@ def _load():
         "btl_set_tuning": (i32, [ctypes.c_char_p, i32]),
         "btl_get_tuning": (i32, [ctypes.c_char_p, P(i32)]),
         "btl_check_faults": (i32, [vp]),
+        "btl_last_gemm_form": (ctypes.c_char_p, []),
         "btl_packed_bytes": (i64, [i64, i64]),
         "btl_pack_host": (i32, [vp, i64, i64, vp, P(f32)]),
         "btl_unpack_host": (i32, [vp, i64, i64, f32, vp]),

@@ -60,6 +60,7 @@ extern "C" {
     pub fn btl_set_tuning(name: *const c_char, value: c_int) -> c_int;
     pub fn btl_get_tuning(name: *const c_char, value: *mut c_int) -> c_int;
     pub fn btl_check_faults(stream: *mut c_void) -> c_int;
+    pub fn btl_last_gemm_form() -> *const c_char;
 
     pub fn btl_packed_bytes(n: i64, k: i64) -> i64;
     pub fn btl_pack_host(w: *const f32, n: i64, k: i64, out: *mut u8, scale: *mut f32) -> c_int;

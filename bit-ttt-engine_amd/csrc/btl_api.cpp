@@ -687,6 +687,8 @@ int btl_get_tuning(const char* name, int* value)
     return BTL_OK;
 }
 
+const char* btl_last_gemm_form(void) { return btl::last_gemm_form(); }
+
 int btl_check_faults(void* stream)
 {
     int dev;

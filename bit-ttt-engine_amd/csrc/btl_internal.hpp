@@ -6,7 +6,31 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace btl {
+
+// Keys (a workspace or an output address) -> slots of a device counter array,
+// one table per device.  A key keeps its slot for the life of the process and a
+// slot never passes to another key, so two launches share counters only when
+// they share the key -- and calls that share a workspace or an output are
+// already ordered by their caller.  When every slot has a key, find() returns
+// -1 and the caller takes a route that needs no counters.
+template <int Slots>
+struct KeySlots {
+    std::mutex mu;
+    const void* key[Slots] = {};
+    int used = 0;
+    int find(const void* k)
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        for (int i = 0; i < used; ++i)
+            if (key[i] == k) return i;
+        if (used == Slots) return -1;
+        key[used] = k;
+        return used++;
+    }
+};
 
 // Routing and tuning knobs.  Each starts from the environment variable of its
 // name ("BTL_" + the enumerator's suffix) when set, read once at the first
@@ -179,6 +203,9 @@ constexpr int kGemmWideMinTiles = 512;  // 256-row GEMM tiles from this many wor
 // the output has few tiles (small m); 1 when it already has kGemmSplitTarget.
 int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps);
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s);
+// "k_gemm_i8<TN,WGN,NW,TM,NS>" of the calling thread's last launch_gemm_i8
+// ("" before the first)
+const char* last_gemm_form();
 
 // Batched decode (k_gemv_bat): the GemmArgs of a GEMM with m <= 64, k % 64
 // == 0; bat_nw, split_steps (4, 8 or 16 steps of 256 weights per K split)
@@ -191,9 +218,9 @@ BatPlan gemv_bat_plan(int64_t m, int64_t rows, int64_t k);
 hipError_t launch_gemv_bat(const GemmArgs& a, hipStream_t s);
 
 // The split-K merge of k_gemv_bat inside the launch: a slot of kSplitCounters
-// per workspace (calls that share a workspace are ordered by the caller, so
-// they may share counters), one counter per row block; the current device
-// must be `dev`.
+// per workspace (KeySlots), one counter per row block; *out = NULL when every
+// slot belongs to another workspace (the caller then adds the splits in a
+// reduce launch).  The current device must be `dev`.
 constexpr int kSplitCounters = 2048;
 constexpr int kSplitSlots = 128;
 constexpr int kMergeMaxSplits = 16;  // K ranges of >= 1024 weights, k <= 16384
@@ -293,8 +320,11 @@ struct AttnArgs {
     uint32_t* ctr;         // one-token attention: the per-KV-head merge counters (attn_counters), or NULL
 };
 constexpr int kAttnMaxCtr = 64;  // KV heads the one-launch decode attention counts
-// the device's merge counters (the current device must be `dev`)
-hipError_t attn_counters(int dev, uint32_t** out);
+constexpr int kAttnSlots = 64;   // workspaces with counters of their own, per device
+// the merge counters of the workspace `ws_key` (KeySlots), or *out = NULL when
+// every slot belongs to another workspace: the merge then runs in a second
+// launch.  The current device must be `dev`.
+hipError_t attn_counters(int dev, const void* ws_key, uint32_t** out);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 // One decode token: RoPE of q and of the new k, the Q8 append of k / v and the
 // attention chunk partials in one kernel, then the merge (m == 1, hd % 16 == 0).

@@ -27,6 +27,7 @@
 // written (the oracle restates the same operations in C).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 #include <stdlib.h>
@@ -1747,6 +1748,12 @@ int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps)
     return (int)((steps + per - 1) / per);  // no empty split
 }
 
+namespace {
+thread_local const char* t_gemm_form = "";
+}
+
+const char* last_gemm_form() { return t_gemm_form; }
+
 hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
 {
     // Tiles of 256 output rows when there is no K split and they still give
@@ -1799,20 +1806,43 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     // CU (3 stages fit two, 2 stages three): measured on MI355X, Llama-3-8B
     // M = 2048, o 37.5 -> 36.5 and down 116.2 -> 111.5 us with 3 (512
     // workgroups); q|k|v (768) 48.9 -> 51.6 and gate|up (1792) 194.6 -> 200.2 keep 2
+    // The 256-row tile has no 3-stage form: its 32 accumulator blocks and a third
+    // stage's addressing do not fit the 256 registers of two waves per SIMD
+    // (the compiler spilled to scratch), so it takes 2 stages where the rule
+    // says 3, and a forced 3 means 4.
     const int fps = knob(KN_GEMM_STAGES);
     const int64_t wgs = tiles * g.splits;
-    const int pns = fps == 2 || fps == 3 || (fps == 4 && TN == 256) ? fps
-                    : deep                                         ? 4
-                    : (g.cus > 0 && wgs <= 2 * g.cus ? 3 : 2);
-    if (TN == 256 && tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64, 4>), grid, dim3(256), 0, s, g);
-    else if (TN == 256 && tm64) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64>), grid, dim3(256), 0, s, g);
-    else if (TN == 256 && pns == 4) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 128, 4>), grid, dim3(256), 0, s, g);
-    else if (TN == 256 && pns == 3) hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 128, 3>), grid, dim3(256), 0, s, g);
-    else if (TN == 256) hipLaunchKernelGGL((k_gemm_i8<256, 4>), grid, dim3(256), 0, s, g);
-    else if (tm64 && ns == 4) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64, 4>), grid, dim3(256), 0, s, g);
-    else if (!tm64 && pns == 3) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 128, 3>), grid, dim3(256), 0, s, g);
-    else if (tm64) hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64>), grid, dim3(256), 0, s, g);
-    else hipLaunchKernelGGL((k_gemm_i8<128, 2>), grid, dim3(256), 0, s, g);
+    int pns = fps == 2 || fps == 3 || (fps == 4 && TN == 256) ? fps
+              : deep                                         ? 4
+              : (g.cus > 0 && wgs <= 2 * g.cus ? 3 : 2);
+    if (TN == 256 && pns == 3) pns = fps == 3 ? 4 : 2;
+    const char* form;
+    if (TN == 256 && tm64 && ns == 4) {
+        form = "k_gemm_i8<256,4,4,64,4>";
+        hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64, 4>), grid, dim3(256), 0, s, g);
+    } else if (TN == 256 && tm64) {
+        form = "k_gemm_i8<256,4,4,64,2>";
+        hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64>), grid, dim3(256), 0, s, g);
+    } else if (TN == 256 && pns == 4) {
+        form = "k_gemm_i8<256,4,4,128,4>";
+        hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 128, 4>), grid, dim3(256), 0, s, g);
+    } else if (TN == 256) {
+        form = "k_gemm_i8<256,4,4,128,2>";
+        hipLaunchKernelGGL((k_gemm_i8<256, 4>), grid, dim3(256), 0, s, g);
+    } else if (tm64 && ns == 4) {
+        form = "k_gemm_i8<128,2,4,64,4>";
+        hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64, 4>), grid, dim3(256), 0, s, g);
+    } else if (!tm64 && pns == 3) {
+        form = "k_gemm_i8<128,2,4,128,3>";
+        hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 128, 3>), grid, dim3(256), 0, s, g);
+    } else if (tm64) {
+        form = "k_gemm_i8<128,2,4,64,2>";
+        hipLaunchKernelGGL((k_gemm_i8<128, 2, 4, 64>), grid, dim3(256), 0, s, g);
+    } else {
+        form = "k_gemm_i8<128,2,4,128,2>";
+        hipLaunchKernelGGL((k_gemm_i8<128, 2>), grid, dim3(256), 0, s, g);
+    }
+    t_gemm_form = form;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || g.splits == 1) return e;
     const int64_t outs = (int64_t)g.m * cols;
@@ -2109,30 +2139,19 @@ static __device__ uint32_t g_split_ctr[kSplitSlots * kSplitCounters];
 
 hipError_t split_counters(int dev, const void* ws_key, uint32_t** out)
 {
-    struct Slots {
-        std::mutex mu;
-        uint32_t* base = nullptr;
-        const void* key[kSplitSlots] = {};
-        int next = 0;
-    };
-    static Slots slots[64];
+    static KeySlots<kSplitSlots> slots[64];
+    static std::atomic<uint32_t*> base[64];
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    Slots& S = slots[dev];
-    std::lock_guard<std::mutex> lk(S.mu);
-    if (!S.base) {
+    uint32_t* b = base[dev].load(std::memory_order_acquire);
+    if (!b) {
         void* p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_split_ctr));
         if (e != hipSuccess) return e;
-        S.base = (uint32_t*)p;
+        b = (uint32_t*)p;
+        base[dev].store(b, std::memory_order_release);
     }
-    int i = 0;
-    while (i < kSplitSlots && S.key[i] != ws_key) ++i;
-    if (i == kSplitSlots) {  // a new workspace: the next slot in turn
-        i = S.next;
-        S.next = (S.next + 1) % kSplitSlots;
-        S.key[i] = ws_key;
-    }
-    *out = S.base + (size_t)i * kSplitCounters;
+    const int i = slots[dev].find(ws_key);
+    *out = i < 0 ? nullptr : b + (size_t)i * kSplitCounters;
     return hipSuccess;
 }
 

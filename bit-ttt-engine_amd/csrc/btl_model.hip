@@ -593,12 +593,15 @@ hipError_t launch_attention_dec1(const AttnArgs& a, const DecKv& kv, hipStream_t
 }
 
 // The merge counters of the one-launch decode attention: kAttnMaxCtr words per
-// device, zero at load and left at zero by every launch (the last workgroup of
-// a KV head resets its word).  Calls that overlap on one device share them.
-static __device__ uint32_t g_attn_ctr[kAttnMaxCtr];
+// workspace slot (KeySlots), zero at load and left at zero by every launch (the
+// last workgroup of a KV head resets its word).  Launches that share a
+// workspace share counters; they are ordered by their caller anyway (they also
+// write the same chunk partials).
+static __device__ uint32_t g_attn_ctr[kAttnSlots * kAttnMaxCtr];
 
-hipError_t attn_counters(int dev, uint32_t** out)
+hipError_t attn_counters(int dev, const void* ws_key, uint32_t** out)
 {
+    static KeySlots<kAttnSlots> slots[64];
     static std::atomic<uint32_t*> ptr[64];
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
     uint32_t* p = ptr[dev].load(std::memory_order_acquire);
@@ -609,7 +612,8 @@ hipError_t attn_counters(int dev, uint32_t** out)
         p = (uint32_t*)q;
         ptr[dev].store(p, std::memory_order_release);
     }
-    *out = p;
+    const int i = slots[dev].find(ws_key);
+    *out = i < 0 ? nullptr : p + (size_t)i * kAttnMaxCtr;
     return hipSuccess;
 }
 
@@ -856,7 +860,10 @@ struct GreedyState {
     uint64_t best;   // the running maximum word of the launch
     uint32_t count;  // workgroups done
 };
-static __device__ GreedyState g_greedy;
+// one state per output word next_id (KeySlots): launches that write the same
+// next_id are ordered by their caller, others never share a state
+constexpr int kGreedySlots = 64;
+static __device__ GreedyState g_greedy[kGreedySlots];
 
 constexpr int kGreedyU = 4;       // float4 loads in flight per thread
 constexpr int kGreedyMaxWg = 256;
@@ -900,12 +907,15 @@ __global__ __launch_bounds__(256) void k_greedy(const float* x, int n, int32_t* 
     __syncthreads();
     if (tid != 0) return;
     for (int w = 1; w < 4; ++w) best = max(best, s_best[w]);
-    __hip_atomic_fetch_max(&gs->best, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the maximum is folded in before the arrival counts
-    const uint32_t old = __hip_atomic_fetch_add(&gs->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old + 1u != (uint32_t)G) return;
-    const uint64_t win = __hip_atomic_exchange(&gs->best, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&gs->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint64_t win = best;  // one workgroup (gs == NULL): its maximum is the answer
+    if (gs) {
+        __hip_atomic_fetch_max(&gs->best, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the maximum is folded in before the arrival counts
+        const uint32_t old = __hip_atomic_fetch_add(&gs->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u != (uint32_t)G) return;
+        win = __hip_atomic_exchange(&gs->best, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&gs->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const int32_t id = (int32_t)(uint32_t)win;
     next_id[0] = id;
     if (d_pos) {
@@ -919,20 +929,25 @@ hipError_t launch_greedy(const float* x, int64_t n, int32_t* next_id, int32_t* d
                          hipStream_t st)
 {
     static std::atomic<GreedyState*> ptr[64];
+    static KeySlots<kGreedySlots> slots[64];
     if (n <= 0 || n > INT32_MAX) return hipErrorInvalidValue;
     int dev;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    GreedyState* gs = ptr[dev].load(std::memory_order_acquire);
-    if (!gs) {
+    GreedyState* base = ptr[dev].load(std::memory_order_acquire);
+    if (!base) {
         void* q = nullptr;
         if ((e = hipGetSymbolAddress(&q, HIP_SYMBOL(g_greedy))) != hipSuccess) return e;
-        gs = (GreedyState*)q;
-        ptr[dev].store(gs, std::memory_order_release);
+        base = (GreedyState*)q;
+        ptr[dev].store(base, std::memory_order_release);
     }
+    const int slot = slots[dev].find(next_id);
+    // no state of its own left for this output: one workgroup, no shared state
+    GreedyState* gs = slot < 0 ? nullptr : base + slot;
     const int64_t n4 = n >> 2;
-    const int G = (int)std::min<int64_t>(kGreedyMaxWg, std::max<int64_t>(1, (n4 + 256 * kGreedyU - 1) / (256 * kGreedyU)));
+    const int G = gs ? (int)std::min<int64_t>(kGreedyMaxWg, std::max<int64_t>(1, (n4 + 256 * kGreedyU - 1) / (256 * kGreedyU)))
+                     : 1;
     hipLaunchKernelGGL(k_greedy, dim3((unsigned)G), dim3(256), 0, st, x, (int)n, next_id, d_pos, log,
                        (int)(log_len > INT32_MAX ? INT32_MAX : log_len), gs);
     return hipGetLastError();

@@ -216,8 +216,9 @@ int btl_rope_append_attention(const float* q, const float* k, const float* v, in
         btl::DecKv kv{q, k, v, rope_cos, rope_sin, cache->k, cache->v, cache->k_scale, cache->v_scale};
         a.q = q;
         if (a.nkv <= btl::kAttnMaxCtr && btl::knob(btl::KN_ATTN_MERGE)) {
-            // the merge in the same launch (per-KV-head counters of this device)
-            if ((e = btl::attn_counters(dev, &a.ctr)) != hipSuccess) return hip_error(e, "attention merge counters");
+            // the merge in the same launch (per-KV-head counters of this workspace;
+            // NULL when every counter slot has another workspace: a second launch)
+            if ((e = btl::attn_counters(dev, wsp, &a.ctr)) != hipSuccess) return hip_error(e, "attention merge counters");
         }
         e = btl::launch_attention_dec1(a, kv, (hipStream_t)stream);
         if (e != hipSuccess) return hip_error(e, "decode attention kernel launch");

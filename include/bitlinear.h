@@ -133,6 +133,14 @@ int btl_get_tuning(const char* name, int* value);
  */
 int btl_check_faults(void* stream);
 
+/*
+ * The instantiation ("k_gemm_i8<TN,WGN,NW,TM,NS>": output rows and waves
+ * along them per tile, waves, token rows, LDS stages) of the last prefill
+ * GEMM this thread launched, "" before the first.  A diagnostic for tests and
+ * tuning, no reference counterpart.
+ */
+const char* btl_last_gemm_form(void);
+
 /* Number of packed bytes for an [n, k] weight: ceil(n*k/4) (packing.rs:36,71). */
 int64_t btl_packed_bytes(int64_t n, int64_t k);
 

@@ -435,21 +435,24 @@ def test_small_m_gemm_split_forms(m, k, n, stages, tile, tune):
     assert torch.equal(y, y0)
 
 
-# the prefill GEMM (128-token tiles) with 2 and 3 LDS stages, and 256-row tiles
-# with 4: k = 1088 (9 steps, the last one half: unrolled rounds and a tail),
-# k = 4096, k = 8256 (64.5 steps); ragged m and n; one split launch (m = 130 x 300
-# rows has few tiles)
+# the prefill GEMM's 128-row tiles with 2 and 3 LDS stages, and its 256-row tiles
+# with 2 (the form the M = 2048 gate|up launch takes) and 4 (a forced 3 takes 4:
+# the 256-row tile has no 3-stage form): k = 1088 (9 steps, the last one half:
+# unrolled rounds and a tail), k = 4096, k = 8256 (64.5 steps); ragged m and n;
+# one split launch (m = 130 x 300 rows has few tiles)
 @pytest.mark.parametrize("m,k,n", [(256, 1088, 1000), (130, 4096, 300), (300, 2048, 2560), (200, 8256, 700)])
 def test_prefill_gemm_stages(m, k, n, tune):
     print("prefill gemm stages", m, k, n, flush=True)
     x = to_dev(activations(m, k, seed=m * 7 + k), torch.bfloat16)
     pt, wb, sw = make_layer(n, k, seed=n + 2 * k)
     ys, accs = [], []
-    for tile, stages in ((0, 2), (0, 3), (2, 4)):
+    for tile, stages, form in ((1, 2, "<128,2,4,128,2>"), (1, 3, "<128,2,4,128,3>"), (2, 2, "<256,4,4,128,2>"),
+                               (2, 3, "<256,4,4,128,4>"), (2, 4, "<256,4,4,128,4>")):
         tune("BTL_GEMM_TILE", tile)
         tune("BTL_GEMM_STAGES", stages)
         acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
         ys.append(bl.BitLinearHip.forward(x, pt, out_dtype=torch.float32, acc_out=acc))
+        assert bl.lib.btl_last_gemm_form().decode() == "k_gemm_i8" + form
         accs.append(acc)
     for a, y in zip(accs[1:], ys[1:]):
         assert torch.equal(accs[0], a) and torch.equal(ys[0], y)
