@@ -36,16 +36,42 @@ KERNEL_SOURCES = ["btl_kernels.hip", "btl_model.hip", "btl_noalloc.hip", "btl_st
 HOST_SOURCES = ["btl_api.cpp", "btl_model_api.cpp", "btl_stream_api.cpp"]
 
 
+# Every kernel must run without scratch memory (register spills or private
+# arrays indexed at run time go to scratch, slow and easy to miss): the kernel
+# sources are compiled with the compiler's per-kernel resource remarks and the
+# build fails on any kernel whose scratch size is not zero.
+RESOURCE_REMARKS = ["-Rpass-analysis=kernel-resource-usage"]
+
+
 def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(l for l in res.stdout.splitlines()
-                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    lines = [l for l in res.stdout.splitlines() if "packed-fp32-ops' is not a recognized feature" not in l]
+    remarks = [l for l in lines if "[-Rpass-analysis=kernel-resource-usage]" in l]
+    out = "\n".join(l for l in lines if "[-Rpass-analysis=kernel-resource-usage]" not in l)
     if res.returncode != 0:
         raise RuntimeError("command failed (%d): %s\n%s" % (res.returncode, " ".join(cmd), out))
     if verbose and out.strip():
         print(out)
+    return remarks
+
+
+def scratch_kernels(remarks):
+    """(kernel, scratch bytes per lane, spilled VGPRs) of every kernel with scratch,
+    from the compiler's kernel-resource-usage remarks."""
+    bad, name, spill = [], None, 0
+    for line in remarks:
+        body = line.split("remark:", 1)[-1].strip()
+        if body.startswith("Function Name:"):
+            name = body.split(":", 1)[1].split("[")[0].strip()
+        elif body.startswith("VGPRs Spill:"):
+            spill = int(body.split(":", 1)[1].split("[")[0])
+        elif body.startswith("ScratchSize [bytes/lane]:"):
+            size = int(body.split(":", 1)[1].split("[")[0])
+            if size:
+                bad.append((name, size, spill))
+    return bad
 
 
 def build(verbose=False):
@@ -53,10 +79,16 @@ def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     objs = []
     inc = ["-I" + INCLUDE, "-I" + CSRC]
+    bad = []
     for src in KERNEL_SOURCES:
         obj = os.path.join(BUILD, src + ".o")
-        _run([HIPCC] + HIP_FLAGS + inc + ["-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        remarks = _run([HIPCC] + HIP_FLAGS + RESOURCE_REMARKS + inc + ["-c", os.path.join(CSRC, src), "-o", obj],
+                       verbose)
+        bad += [(src,) + b for b in scratch_kernels(remarks)]
         objs.append(obj)
+    if bad:
+        raise RuntimeError("kernels with scratch memory (spills or private arrays):\n" + "\n".join(
+            "  %s: %s: %d bytes/lane, %d VGPRs spilled" % b for b in bad))
     cxx = shutil.which("g++") or "g++"
     for src in HOST_SOURCES:
         obj = os.path.join(BUILD, src + ".o")

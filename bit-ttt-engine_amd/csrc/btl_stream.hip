@@ -490,9 +490,10 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
     const int rep = w % kSReplicas;
     const int nqkv = a.nq + a.nk + a.nv;
     // this workgroup's groups per slot, their first output rows and counts
-    const GroupPos gp[4] = {group_pos(nqkv / 4, a.nwg, w), group_pos(a.H / 4, a.nwg, w),
-                            group_pos(a.I / 4, a.nwg, w), group_pos(a.H / rd, a.nwg, w)};
-    const int gr[4] = {4, 4, 4, rd};
+    // (selected by value, not indexed: a runtime index into a private array
+    // would put it in scratch memory)
+    const GroupPos gp0 = group_pos(nqkv / 4, a.nwg, w), gp1 = group_pos(a.H / 4, a.nwg, w),
+                   gp2 = group_pos(a.I / 4, a.nwg, w), gp3 = group_pos(a.H / rd, a.nwg, w);
     uint32_t cum = 0;  // compute-wave arrivals expected through the current stage
     const __amdgpu_buffer_rsrc_t fr = make_rsrc(a.flags + (size_t)rep * a.nwg, (uint32_t)(a.nwg * 8));
     for (int s = 0; s < S; ++s) {
@@ -598,13 +599,15 @@ __device__ void control_wave(const StreamArgs& a, Shared& sh, uint8_t* rows_lds,
         // 5. wave 0: once this stage's compute waves are done, publish the outputs
         //    (q|k|v: the absmax of q only, the rows o reads)
         const int cap = j == 0 ? kSQkvWaves : (j == 1 ? kSOWaves : (j == 2 ? kSComp : kSComp - kSDWave0));
-        const int np = min(gp[j].ng, cap);
+        const GroupPos gpj = j == 0 ? gp0 : (j == 1 ? gp1 : (j == 2 ? gp2 : gp3));
+        const int grj = j == 3 ? rd : 4;
+        const int np = min(gpj.ng, cap);
         cum += (uint32_t)np;
         if (cw == 0) {
             lds_wait(&sh.cdone, cum, clk);
-            publish(a, sh, io.out_off, gp[j].g0 * gr[j], np * gr[j] < io.n_out - gp[j].g0 * gr[j]
-                                                               ? np * gr[j]
-                                                               : io.n_out - gp[j].g0 * gr[j],
+            publish(a, sh, io.out_off, gpj.g0 * grj, np * grj < io.n_out - gpj.g0 * grj
+                                                         ? np * grj
+                                                         : io.n_out - gpj.g0 * grj,
                     j == 0 ? a.nq : io.n_out, j == 3 && l + 1 == a.nl, epoch, (epoch << 10) + (uint32_t)s + 1u, lane);
         }
     }
@@ -650,17 +653,37 @@ __global__ __launch_bounds__(1024, 1) void k_dec_stream(StreamArgs a)
 // two operand rows, then the staging copy of a tagged input (whole 1 KB copies)
 size_t stream_lds_bytes(int kmax) { return (size_t)2 * (kmax + 16) + (((size_t)kmax * 4 + 1023) & ~(size_t)1023); }
 
+// The stages of the stream wait on each other's workgroups, so every workgroup
+// must be resident at once.  The occupancy of the instantiation is checked
+// first (a grid that cannot be co-resident fails with
+// hipErrorCooperativeLaunchTooLarge before anything runs); outside a stream
+// capture the launch is cooperative, which makes the runtime guarantee that all
+// workgroups run together (or fail the launch).  Under a capture it is a plain
+// launch resting on the occupancy check, and a workgroup kept off the device by
+// other work makes the bounded waits give up and set the fault word
+// (btl_check_faults) instead of hanging.
 hipError_t launch_dec_stream(const StreamArgs& a, hipStream_t s)
 {
     const size_t lds = stream_lds_bytes(a.kmax);
     if (a.I > 14336 || a.H > 4096 || a.nwg > 256) return hipErrorInvalidValue;
-    if (a.I > 4096) {
-        (void)hipFuncSetAttribute((const void*)k_dec_stream<2, 7>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL((k_dec_stream<2, 7>), dim3(a.nwg), dim3(1024), lds, s, a);
-    } else {
-        (void)hipFuncSetAttribute((const void*)k_dec_stream<4, 4>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL((k_dec_stream<4, 4>), dim3(a.nwg), dim3(1024), lds, s, a);
+    const void* fn = a.I > 4096 ? (const void*)k_dec_stream<2, 7> : (const void*)k_dec_stream<4, 4>;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    int dev = 0, cus = 0, per_cu = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess ||
+        (e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess ||
+        (e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 1024, lds)) != hipSuccess)
+        return e;
+    if ((int64_t)per_cu * cus < a.nwg) return hipErrorCooperativeLaunchTooLarge;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(s, &cap)) != hipSuccess) return e;
+    if (cap == hipStreamCaptureStatusNone) {
+        StreamArgs arg = a;
+        void* params[] = {(void*)&arg};
+        return hipLaunchCooperativeKernel(fn, dim3(a.nwg), dim3(1024), params, (unsigned)lds, s);
     }
+    if (a.I > 4096) hipLaunchKernelGGL((k_dec_stream<2, 7>), dim3(a.nwg), dim3(1024), lds, s, a);
+    else hipLaunchKernelGGL((k_dec_stream<4, 4>), dim3(a.nwg), dim3(1024), lds, s, a);
     return hipGetLastError();
 }
 

@@ -251,10 +251,14 @@ size_t btl_add_rmsnorm_swiglu_workspace_bytes(int64_t m, int64_t n, int64_t k);
  * btl_stream_run: x bf16 [H] (device, 16-byte aligned) -> y bf16 [H]; stage_out
  *   NULL, or a bf16 buffer of btl_stream_stage_words(plan) elements that
  *   receives every stage's output (per layer: [q|k|v], o, h, down).  The launch
- *   takes every CU (one workgroup each, all resident): nothing else may run on
- *   the device meanwhile.  Its waits are bounded in time (BTL_WAIT_SPIN); a
- *   wait that gives up is reported by btl_check_faults.  Runs on one plan must
- *   be ordered on one stream.
+ *   takes every CU (one workgroup each, all resident): its occupancy is checked
+ *   first (BTL_ERR_HIP, hipErrorCooperativeLaunchTooLarge, when the workgroups
+ *   cannot all be resident), and outside a stream capture it is a cooperative
+ *   launch, so the runtime runs every workgroup at once or fails the launch.
+ *   Under a capture it is a plain launch: nothing else may then run on the
+ *   device meanwhile.  Its waits are bounded in time (BTL_WAIT_SPIN); a wait
+ *   that gives up is reported by btl_check_faults.  Runs on one plan must be
+ *   ordered on one stream.
  * btl_stream_destroy: synchronises the device and frees the plan.
  */
 typedef struct btl_stream_layer {

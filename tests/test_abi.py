@@ -300,3 +300,21 @@ def test_pack_device_validation():
     assert ws(0, 5) == 0 and ws(-1, 5) == 0
     assert ws(1, 4096) == 8 and ws(1, 4097) == 3 * 8
     assert ws(4096, 14336) == (14336 + 4 + 1) * 8
+
+
+def test_build_rejects_kernels_with_scratch():
+    # build.py reads the compiler's kernel-resource-usage remarks and fails on any
+    # kernel with scratch memory; its parser on remark lines of both kinds
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("btl_build", os.path.join(ROOT, "bit-ttt-engine_amd", "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    tail = " [-Rpass-analysis=kernel-resource-usage]"
+    lines = ["f.hip:1:1: remark: Function Name: _Z5k_onev" + tail,
+             "f.hip:1:1: remark:     VGPRs Spill: 0" + tail,
+             "f.hip:1:1: remark:     ScratchSize [bytes/lane]: 0" + tail,
+             "f.hip:9:1: remark: Function Name: _Z5k_twov" + tail,
+             "f.hip:9:1: remark:     VGPRs Spill: 4" + tail,
+             "f.hip:9:1: remark:     ScratchSize [bytes/lane]: 20" + tail]
+    assert mod.scratch_kernels(lines) == [("_Z5k_twov", 20, 4)]
+    assert mod.scratch_kernels(lines[:3]) == []
