@@ -74,3 +74,13 @@ impl HipPackedTensor {
         Tensor::from_vec(y, (m, n), &Device::Cpu)
     }
 }
+
+// HipPackedTensor becomes a field of the reference's BitLinear, which lives in
+// AdaptiveBitLinear inside BitLlama inside the #[pyclass] PyBitLlama
+// (python.rs:18): pyo3 requires Send there, and a model shared across threads
+// needs Sync.  Fails to compile if a field loses either.
+#[allow(dead_code)]
+fn _assert_send_sync() {
+    fn check<T: Send + Sync>() {}
+    check::<HipPackedTensor>();
+}

@@ -114,6 +114,15 @@ impl DeviceBuffer {
     }
 }
 
+// HIP device pointers and streams are plain handles that the HIP runtime lets
+// any host thread use (its API is thread-safe), so the owning wrappers may move
+// between threads and be shared: every method that writes through one takes
+// `&mut self`, and shared `&self` use only reads device memory or enqueues work
+// on a stream, which HIP orders itself.  The reference's BitLinear sits inside
+// a #[pyclass] (python.rs:18), which pyo3 requires to be Send.
+unsafe impl Send for DeviceBuffer {}
+unsafe impl Sync for DeviceBuffer {}
+
 impl Drop for DeviceBuffer {
     fn drop(&mut self) {
         if !self.ptr.is_null() {
@@ -142,6 +151,9 @@ impl Stream {
         hip(unsafe { hipStreamSynchronize(self.0) }, "hipStreamSynchronize")
     }
 }
+
+unsafe impl Send for Stream {}
+unsafe impl Sync for Stream {}
 
 impl Drop for Stream {
     fn drop(&mut self) {
@@ -174,6 +186,11 @@ pub struct PackedWeights {
     buf: DeviceBuffer,
     raw: btl_packed_t,
 }
+
+// `raw` points into `buf`, which the value owns; the bytes are read-only after
+// the upload.
+unsafe impl Send for PackedWeights {}
+unsafe impl Sync for PackedWeights {}
 
 impl PackedWeights {
     /// Upload the bytes of a PackedTensor (its `data`, flat [ceil(n k / 4)] u8) and scale.
@@ -296,4 +313,14 @@ impl BitLinearHip {
         self.y.download(&mut out)?;
         Ok(out)
     }
+}
+
+// Compile-time check that the wrappers can live inside the reference's layers.
+#[allow(dead_code)]
+fn _assert_send_sync() {
+    fn check<T: Send + Sync>() {}
+    check::<DeviceBuffer>();
+    check::<Stream>();
+    check::<PackedWeights>();
+    check::<BitLinearHip>();
 }
