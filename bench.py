@@ -167,8 +167,10 @@ def profiled_traffic(name):
 
 def cpu_baseline(host_layers, seconds):
     """The reference's CPU BitLinear (cpu.rs, restated with AVX2 intrinsics and a
-    thread pool, oracle/) on a bounded sample: the 7 projections of 4 of the 32
-    layers, fp32 activations, repeated for about `seconds`."""
+    thread pool, oracle/) on a bounded sample: whole tokens through the 7
+    projections of all 32 layers (1.745 GB of packed weights, streamed from host
+    DRAM: far beyond any CPU cache), fp32 activations, repeated for about
+    `seconds`."""
     from oracle import oracle as orc
     threads = max(1, min(16, os.cpu_count() or 1))
     rng = np.random.default_rng(0)
@@ -191,7 +193,7 @@ def cpu_baseline(host_layers, seconds):
         pass
     return {"value": round(1.0 / per_token, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "cpu": "%s, %d logical CPUs visible" % (model, os.cpu_count() or 0),
-            "sample": "%d reps of layers 0-%d of 32 (7 projections each, %.0f MB packed), M=1 fp32, "
+            "sample": "%d tokens through layers 0-%d of 32 (7 projections each, %.0f MB packed), M=1 fp32, "
                       "cpu.rs algorithm restated in C with AVX2+FMA intrinsics, %d threads; %.1f s"
                       % (reps, len(host_layers) - 1,
                          sum(wb.size for p in host_layers for (wb, _, _, _) in p) / 1e6, threads, el)}
@@ -276,6 +278,7 @@ def run_decode(args):
         kern[name] = {"us": round(us, 2), "bytes": b, "GB_s": round(b / us / 1e3, 1),
                       "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
     f32_ref = run_decode_f32_ref(layers, gen, dev, args)
+    ceilings = run_ceilings(dev, args)
     dom = kern["gate_up"]
     result = {
         "metric": METRIC, "value": round(1000.0 / ms, 2), "unit": "tok/s", "n_gpus": 1,
@@ -301,6 +304,7 @@ def run_decode(args):
                      **_trace_frac(profiled_trace_us("k_gemv_rq_decode_llama3-8b_m1.md"), dom["bytes"], HBM_PEAK_GBS,
                                    1e3)},
         "kernels": kern,
+        "ceilings": ceilings,
         "f32_ref": f32_ref,
     }
     if args.prefill:
@@ -319,7 +323,7 @@ def run_decode(args):
     if args.cpu_baseline:
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
         host = []
-        for L in layers[:4]:
+        for L in layers:
             host.append([(L[nm].data.cpu().numpy(), shapes[nm][0], shapes[nm][1], L[nm].scale)
                          for nm in ("q", "k", "v", "o", "gate", "up", "down")])
         result["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
@@ -863,6 +867,55 @@ def run_pack(gen, dev):
             "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3), "kernels": "k_abs_sum x2 levels + k_pack_codes"}
 
 
+def run_ceilings(dev, args):
+    """The ceilings of the cfg2 decode chain, from the probe kernels
+    (bit-ttt-engine_amd/probe/btl_probe.hip, not part of the library): a plain
+    streaming read (non-temporal 16-byte loads, every load in flight before the
+    first use) of exactly the packed bytes of each launch of the step, over the
+    same 32-layer footprint (1.745 GB, far beyond the 256 MB Infinity Cache), as
+    the same 128 dependent launches in one HIP graph; the same per launch kind (32
+    launches of one kind in a graph); and an empty kernel in a chain of 128
+    dependent launches (1 and 1792 workgroups): the cost of a launch boundary."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "bit-ttt-engine_amd", "probe", "libbtl_probe.so"))
+    lib.probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    lib.probe_stream_read_words.restype = ctypes.c_int64
+    lib.probe_stream_read_words.argtypes = [ctypes.c_int64]
+    lib.probe_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    kinds = {"qkv": (HIDDEN + 2 * KV) * HIDDEN // 4, "o": HIDDEN * HIDDEN // 4, "gate_up": 2 * INTER * HIDDEN // 4,
+             "down": HIDDEN * INTER // 4}
+    per_layer = sum(kinds.values())
+    buf = torch.empty(LAYERS * per_layer, dtype=torch.uint8, device=dev).fill_(0x5A)
+    out = torch.empty(lib.probe_stream_read_words(max(kinds.values())), dtype=torch.int32, device=dev)
+    reads = {k: [] for k in kinds}
+    off = 0
+    for _ in range(LAYERS):
+        for k, b in kinds.items():
+            reads[k].append(lambda st, o=off, b=b: lib.probe_stream_read(buf.data_ptr() + o, b, out.data_ptr(), st))
+            off += b
+    order = [reads[k][l] for l in range(LAYERS) for k in kinds]
+    cap = torch.cuda.Stream()
+    for fn in order:
+        fn(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    chain_us = _graph_us(order, 10, cap)
+    res = {"what": "probe kernels (bit-ttt-engine_amd/probe/btl_probe.hip): streaming read of each launch's packed "
+                   "bytes over the 32-layer footprint, and empty launches; HIP graphs, HIP events",
+           "stream_read_step_us": round(chain_us, 1),
+           "stream_read_step_frac_hbm": round(LAYERS * per_layer / chain_us / 1e3 / HBM_PEAK_GBS, 3)}
+    for k, b in kinds.items():
+        us = _graph_us(reads[k], 10, cap) / LAYERS
+        res["stream_read_" + k] = {"us": round(us, 2), "bytes": b, "GB_s": round(b / us / 1e3, 1),
+                                   "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+    for wgs in (1, 1792):
+        us = _graph_us([lambda st, w=wgs: lib.probe_empty(w, st)] * 128, 10, cap) / 128
+        res["empty_launch_us_%dwg" % wgs] = round(us, 3)
+    del buf
+    print("bench: ceilings: streaming-read step %.1f us, empty launch %.2f us" % (
+        chain_us, res["empty_launch_us_1wg"]), file=sys.stderr, flush=True)
+    return res
+
+
 def run_probe(args):
     """A few launches of one workload, plus a plain copy of known size, for
     counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy reads and
@@ -874,6 +927,9 @@ def run_probe(args):
     gen.manual_seed(0xB17EB17E)
     stream = torch.cuda.current_stream().cuda_stream
     gate, up = synth_packed(INTER, HIDDEN, gen, dev), synth_packed(INTER, HIDDEN, gen, dev)
+    if args.probe == "ceilings":
+        print(json.dumps({"probe": "ceilings", **run_ceilings(dev, args)}), flush=True)
+        return
     if args.probe == "decode_gate_up":
         x = synth_act(1, HIDDEN, gen, dev)
         outs = [torch.empty((1, INTER), dtype=torch.bfloat16, device=dev) for _ in range(2)]
@@ -910,8 +966,10 @@ def main():
                     help="skip the device-pack (PackedTensor::pack) timing")
     ap.add_argument("--no-sweep", dest="sweep", action="store_false",
                     help="skip the cfg3 batched-decode section of the JSON line")
-    ap.add_argument("--probe", choices=["decode_gate_up", "prefill_gate_up"], default=None,
-                    help="counter-run mode: --steps launches of one workload and a 256 MiB copy; no JSON")
+    ap.add_argument("--probe", choices=["decode_gate_up", "prefill_gate_up", "ceilings"], default=None,
+                    help="decode_gate_up / prefill_gate_up: counter-run mode, --steps launches of one workload and "
+                         "a 256 MiB copy, no JSON; ceilings: the decode chain's streaming-read and launch-floor "
+                         "probes alone, one JSON line")
     ap.add_argument("--no-e2e", dest="e2e", action="store_false",
                     help="skip the cfg5 end-to-end decoder section of the JSON line")
     ap.add_argument("--no-cfg1", dest="cfg1", action="store_false",

@@ -17,6 +17,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libbitlinear_hip.so")
+PROBE = os.path.join(HERE, "probe")
+PROBE_LIB = os.path.join(PROBE, "libbtl_probe.so")
 
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
@@ -98,6 +100,11 @@ def build(verbose=False):
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp] + objs +
          ["-Wl,-soname,libbitlinear_hip.so"], verbose)
     os.replace(tmp, LIB)
+    # the measurement kernels of bench.py --probe, a library of their own
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC] + HIP_FLAGS + ["-shared", os.path.join(PROBE, "btl_probe.hip"), "-o", tmp,
+                                "-Wl,-soname,libbtl_probe.so"], verbose)
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 
