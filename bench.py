@@ -113,7 +113,10 @@ class OpCall:
 
 def time_launches(fn, reps, stream_obj):
     """Average µs of `fn(stream)` over `reps` back-to-back launches, HIP events
-    recorded on the stream the kernels run on."""
+    recorded on the stream the kernels run on.  Synchronises first: the inputs
+    were made on another stream, and memory that stream's pending kernels still
+    use may already back tensors that `fn` reads or writes."""
+    torch.cuda.synchronize()
     with torch.cuda.stream(stream_obj):
         s = stream_obj.cuda_stream
         fn(s)
@@ -333,7 +336,9 @@ def run_decode(args):
 
 
 def _graph_us(fns, reps, cap):
-    """us per replay of one HIP graph holding fns (each fn(stream)) in order."""
+    """us per replay of one HIP graph holding fns (each fn(stream)) in order
+    (synchronises first, as time_launches)."""
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(cap):
         with torch.cuda.graph(g, stream=cap):
@@ -916,31 +921,37 @@ def run_ceilings(dev, args):
     return res
 
 
+PROBE_KINDS = {"qkv": ((HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN)), "o": ((HIDDEN, HIDDEN),),
+               "gate_up": ((INTER, HIDDEN), (INTER, HIDDEN)), "down": ((HIDDEN, INTER),)}
+
+
 def run_probe(args):
     """A few launches of one workload, plus a plain copy of known size, for
-    counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the copy reads and
-    writes 256 MiB per dispatch and calibrates the counters.  Prints what ran."""
+    counter runs (rocprofv3 --pmc ...): --probe decode_<kind> is btl_linear_group
+    at M=1 (the decode kernel), prefill_<kind> btl_linear_i8_op at M=--prefill-m
+    (the GEMM alone), kind one of qkv, o, gate_up, down (the Llama-3-8B calls of a
+    layer).  The copy reads and writes 256 MiB per dispatch and calibrates the
+    memory counters.  Prints what ran."""
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     bl.check(bl.lib.btl_init(0))
     gen = torch.Generator(device=dev)
     gen.manual_seed(0xB17EB17E)
     stream = torch.cuda.current_stream().cuda_stream
-    gate, up = synth_packed(INTER, HIDDEN, gen, dev), synth_packed(INTER, HIDDEN, gen, dev)
-    if args.probe == "ceilings":
-        print(json.dumps({"probe": "ceilings", **run_ceilings(dev, args)}), flush=True)
-        return
-    if args.probe == "decode_gate_up":
-        x = synth_act(1, HIDDEN, gen, dev)
-        outs = [torch.empty((1, INTER), dtype=torch.bfloat16, device=dev) for _ in range(2)]
-        call = Call([gate, up], x, outs)
-        what = "btl_linear_group gate|up, M=1, 4096 -> 2 x 14336, bf16 (k_gemv_rq)"
+    phase, kind = args.probe.split("_", 1)
+    shp = PROBE_KINDS[kind]
+    k = shp[0][1]
+    ws = [synth_packed(n, kk, gen, dev) for (n, kk) in shp]
+    m = 1 if phase == "decode" else args.prefill_m
+    x = synth_act(m, k, gen, dev)
+    outs = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for (n, _) in shp]
+    if phase == "decode":
+        call = Call(ws, x, outs)
+        what = "btl_linear_group %s, M=1, %d -> %s, bf16 (decode kernel)" % (kind, k, "+".join(str(n) for n, _ in shp))
     else:
-        x = synth_act(args.prefill_m, HIDDEN, gen, dev)
         q, s = bl.quantize_act_op(x)
-        outs = [torch.empty((args.prefill_m, INTER), dtype=torch.bfloat16, device=dev) for _ in range(2)]
-        call = OpCall([gate, up], q, s, outs)
-        what = "btl_linear_i8_op gate|up, M=%d, 4096 -> 2 x 14336, bf16 (k_gemm_i8)" % args.prefill_m
+        call = OpCall(ws, q, s, outs)
+        what = "btl_linear_i8_op %s, M=%d, %d -> %s, bf16 (k_gemm_i8)" % (kind, m, k, "+".join(str(n) for n, _ in shp))
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(7)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -966,10 +977,11 @@ def main():
                     help="skip the device-pack (PackedTensor::pack) timing")
     ap.add_argument("--no-sweep", dest="sweep", action="store_false",
                     help="skip the cfg3 batched-decode section of the JSON line")
-    ap.add_argument("--probe", choices=["decode_gate_up", "prefill_gate_up", "ceilings"], default=None,
-                    help="decode_gate_up / prefill_gate_up: counter-run mode, --steps launches of one workload and "
-                         "a 256 MiB copy, no JSON; ceilings: the decode chain's streaming-read and launch-floor "
-                         "probes alone, one JSON line")
+    ap.add_argument("--probe", default=None,
+                    choices=["ceilings"] + ["%s_%s" % (p, k) for p in ("decode", "prefill") for k in PROBE_KINDS],
+                    help="decode_<kind> / prefill_<kind> (kind qkv, o, gate_up, down): counter-run mode, --steps "
+                         "launches of one workload and a 256 MiB copy, no JSON; ceilings: the decode chain's "
+                         "streaming-read and launch-floor probes alone, one JSON line")
     ap.add_argument("--no-e2e", dest="e2e", action="store_false",
                     help="skip the cfg5 end-to-end decoder section of the JSON line")
     ap.add_argument("--no-cfg1", dest="cfg1", action="store_false",
@@ -987,6 +999,11 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         sys.exit(1)
+    if args.probe == "ceilings":
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        print(json.dumps({"probe": "ceilings", **run_ceilings(dev, args)}), flush=True)
+        return
     if args.probe:
         run_probe(args)
         return
