@@ -198,6 +198,42 @@ def test_attn_decode_matches_float64(T, nh, nkv, hd):
     assert np.all(np.abs(y.reshape(nh, hd) - e.reshape(nh, hd)) <= 2e-6 * scale + 1e-30)
 
 
+def test_attn_decode_score_order_known_answer():
+    # the fixed order of a score: sequential over d.  With q = [2^24, 1, -2^24, 1, 1, 0, 0, 0]
+    # against a key of ones the f32 sum is 2 (2^24 + 1 rounds to 2^24), where an order
+    # of four interleaved chains combined pairwise would give 1 and the exact value is 3.
+    # A second key of zeros scores 0, values 1 and 0: y = 1 / (1 + exp(-s0)).
+    hd, S, T = 8, 4, 2
+    kq = np.full((1, S, hd), 128, np.uint8)
+    kq[0, 0] = 129                      # key 0: all ones (scale 1)
+    ks = np.ones((1, S), np.float32)
+    vq = np.full((1, S, hd), 128, np.uint8)
+    vq[0, 0] = 129                      # value 0: ones, value 1: zeros
+    vs = np.ones((1, S), np.float32)
+    q = np.array([2.0 ** 24, 1, -2.0 ** 24, 1, 1, 0, 0, 0], np.float32)
+    y = orc.attn_decode(q, kq, ks, vq, vs, 1, T)
+    scal = float(np.float32(1.0 / np.sqrt(8.0)))
+    for score, want in ((2.0, True), (1.0, False), (3.0, False)):
+        e = 1.0 / (1.0 + np.exp(-score * scal))
+        assert (abs(float(y[0]) - e) < 1e-6) == want, (score, float(y[0]), e)
+    assert np.all(y == y[0])
+
+
+def test_attn_decode_value_order_known_answer():
+    # the fixed order of a chunk's value sum: sequential over the keys.  Five keys of
+    # equal score (p = 1 each, l = 5) with values 2^24, 1, -2^24, 1, 1: the f32 sum is 2
+    # (y = 0.4); four interleaved chains combined pairwise would give 1 (y = 0.2), the
+    # exact value is 3 (y = 0.6)
+    hd, S, T = 4, 8, 5
+    kq = np.full((1, S, hd), 128, np.uint8)
+    ks = np.ones((1, S), np.float32)
+    vq = np.full((1, S, hd), 129, np.uint8)
+    vs = np.array([[2.0 ** 24, 1, 2.0 ** 24, 1, 1, 1, 1, 1]], np.float32)
+    vq[0, 2] = 127                       # -1 * 2^24 with a positive scale
+    y = orc.attn_decode(np.ones(hd, np.float32), kq, ks, vq, vs, 1, T)
+    assert np.all(y == np.float32(2.0) / np.float32(5.0)), y
+
+
 def test_attn_decode_gqa_head_map():
     # each KV head holds one constant value vector: output of head h must be that of kv head h // rep
     nh, nkv, hd, S, T = 8, 2, 64, 70, 70
