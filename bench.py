@@ -880,7 +880,8 @@ def run_ceilings(dev, args):
     same 32-layer footprint (1.745 GB, far beyond the 256 MB Infinity Cache), as
     the same 128 dependent launches in one HIP graph; the same per launch kind (32
     launches of one kind in a graph); and an empty kernel in a chain of 128
-    dependent launches (1 and 1792 workgroups): the cost of a launch boundary."""
+    dependent launches (1 and 1792 workgroups): the cost of a launch boundary.
+    Then the int8 MFMA ceilings (mfma_ceilings)."""
     import ctypes
     lib = ctypes.CDLL(os.path.join(ROOT, "bit-ttt-engine_amd", "probe", "libbtl_probe.so"))
     lib.probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
@@ -916,6 +917,7 @@ def run_ceilings(dev, args):
         us = _graph_us([lambda st, w=wgs: lib.probe_empty(w, st)] * 128, 10, cap) / 128
         res["empty_launch_us_%dwg" % wgs] = round(us, 3)
     del buf
+    res.update(mfma_ceilings(lib, dev, cap))
     print("bench: ceilings: streaming-read step %.1f us, empty launch %.2f us" % (
         chain_us, res["empty_launch_us_1wg"]), file=sys.stderr, flush=True)
     return res
@@ -923,6 +925,50 @@ def run_ceilings(dev, args):
 
 PROBE_KINDS = {"qkv": ((HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN)), "o": ((HIDDEN, HIDDEN),),
                "gate_up": ((INTER, HIDDEN), (INTER, HIDDEN)), "down": ((HIDDEN, INTER),)}
+
+
+def mfma_ceilings(lib, dev, cap):
+    """What the int8 matrix cores and the vendor library reach on this box: the
+    probe's MFMA loop (8 independent v_mfma_i32_16x16x64_i8 per round, two waves
+    per SIMD on every CU, operands held in registers) with random int8 x ternary
+    operands (the prefill GEMM's data), random x random, and one constant byte;
+    and hipBLASLt's dense int8 GEMM (torch._int_mm) on the M=2048 gate|up shape
+    with the weights stored as dense int8 {-1, 0, +1} (4x the packed bytes)."""
+    import ctypes
+    lib.probe_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    wgs, iters = 2 * cus, 4000
+    ops = wgs * 4 * 8 * iters * 2.0 * 16 * 16 * 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    rnd = torch.randint(-128, 128, (65536, 16), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
+    ter = torch.randint(-1, 2, (65536, 16), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
+    lane = torch.arange(65536, device=dev).unsqueeze(1) % 8
+    srcs = {"random_x_ternary": torch.where(lane < 4, rnd, ter).contiguous(), "random_x_random": rnd,
+            "constant": torch.full((65536, 16), 1, dtype=torch.int8, device=dev)}
+    out = torch.empty(wgs * 256, dtype=torch.int32, device=dev)
+    res = {}
+    for name, src in srcs.items():
+        fn = lambda st, src=src: lib.probe_mfma_loop(src.data_ptr(), iters, wgs, out.data_ptr(), st)
+        us = time_launches(fn, 5, cap)
+        res["mfma_loop_" + name] = {"TOPS": round(ops / us / 1e6, 1), "frac_int8": round(ops / us / 1e6 / INT8_PEAK_TOPS, 3)}
+    m, k, n = 2048, HIDDEN, 2 * INTER
+    a = torch.randint(-128, 128, (m, k), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
+    w = torch.randint(-1, 2, (n, k), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
+    best = None
+    for layout, b in (("k-major", w.t()), ("n-major", w.t().contiguous())):
+        try:
+            us = time_launches(lambda st, b=b: torch._int_mm(a, b), 10, cap)
+        except RuntimeError:
+            continue
+        if best is None or us < best[1]:
+            best = (layout, us)
+    if best is not None:
+        op = 2.0 * m * n * k
+        res["hipblaslt_int8_gate_up_m2048"] = {"us": round(best[1], 1), "TOPS": round(op / best[1] / 1e6, 1),
+                                               "frac_int8": round(op / best[1] / 1e6 / INT8_PEAK_TOPS, 3),
+                                               "weights": "dense int8 [28672, 4096], %s" % best[0]}
+    return res
 
 
 def run_probe(args):
