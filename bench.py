@@ -741,7 +741,7 @@ def run_cfg1(gen, dev, args):
                        "back to back in a HIP graph",
            "algorithmic_bytes": n * k // 4 + k * 4 + n * 4 + 4}
     b = out["algorithmic_bytes"]
-    for mode_name, mode in (("f32_ref", bl.BTL_ACT_F32_REF), ("i8", bl.BTL_ACT_I8)):
+    for mode_name, mode in (("f32_ref", bl.BTL_ACT_F32_REF), ("f32_seq", bl.BTL_ACT_F32_SEQ), ("i8", bl.BTL_ACT_I8)):
         def one(stream, c):
             bl.check(bl.lib.btl_linear(ctypes.byref(c), x.data_ptr(), bl.BTL_F32, 1, k, y.data_ptr(), bl.BTL_F32,
                                        mode, None, None, 0, stream))
@@ -769,8 +769,8 @@ def run_cfg1(gen, dev, args):
         us = 1000.0 * e0.elapsed_time(e1) / (reps * copies)
         out[mode_name] = {"us": round(us, 2), "GB_s": round(b / us / 1e3, 1),
                           "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
-    print("bench: cfg1 f32_ref %.2f us, i8 %.2f us" % (out["f32_ref"]["us"], out["i8"]["us"]), file=sys.stderr,
-          flush=True)
+    print("bench: cfg1 f32_ref %.2f us, f32_seq %.2f us, i8 %.2f us" % (out["f32_ref"]["us"], out["f32_seq"]["us"],
+                                                                       out["i8"]["us"]), file=sys.stderr, flush=True)
     if args.cpu_baseline:
         from oracle import oracle as orc
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -797,7 +797,8 @@ def run_anchor(dev, args):
     calls, then the mean of 100 timed calls; GOps/s = M*N*K/t and GB/s =
     (4MK + NK/4 + 4MN)/t, the reference's formulas.  On the GPU in both
     arithmetic modes (f32 in/out), and the reference's CPU algorithm (cpu.rs
-    restated with AVX2 intrinsics) on the host cores."""
+    restated with AVX2 intrinsics) on the host cores.  gpu_f32_seq: the same in the
+    order of a host without AVX2/FMA (one sequential chain of K adds per output)."""
     import ctypes
     m, k, n = 1, 8192, 8192
     wb = (np.arange(n * k // 4) % 255).astype(np.uint8)
@@ -813,7 +814,8 @@ def run_anchor(dev, args):
 
     out = {"workload": "bench_cpu_kernel.rs: M=1, K=N=8192, x=0.5, weight bytes i % 255, scale 1; 10 warm-ups, "
                        "mean of 100 calls; GOps/s = M*N*K/t, GB/s = (4MK + NK/4 + 4MN)/t"}
-    for name, mode in (("gpu_f32_ref", bl.BTL_ACT_F32_REF), ("gpu_i8", bl.BTL_ACT_I8)):
+    for name, mode in (("gpu_f32_ref", bl.BTL_ACT_F32_REF), ("gpu_f32_seq", bl.BTL_ACT_F32_SEQ),
+                       ("gpu_i8", bl.BTL_ACT_I8)):
         def call(stream):
             bl.check(bl.lib.btl_linear(ctypes.byref(c), x.data_ptr(), bl.BTL_F32, m, k, y.data_ptr(), bl.BTL_F32,
                                        mode, None, None, 0, stream))
@@ -842,8 +844,8 @@ def run_anchor(dev, args):
                           nproc=os.cpu_count() or 0,
                           sample="cpu.rs restated in C with AVX2+FMA intrinsics, %d threads (the box's CPU share; "
                                  "the reference's rayon pool would take nproc)" % threads)
-    print("bench: anchor (M=1, K=N=8192): gpu f32_ref %.4f ms, gpu i8 %.4f ms%s" %
-          (out["gpu_f32_ref"]["ms"], out["gpu_i8"]["ms"],
+    print("bench: anchor (M=1, K=N=8192): gpu f32_ref %.4f ms, gpu f32_seq %.4f ms, gpu i8 %.4f ms%s" %
+          (out["gpu_f32_ref"]["ms"], out["gpu_f32_seq"]["ms"], out["gpu_i8"]["ms"],
            ", cpu %.3f ms" % out["cpu"]["ms"] if "cpu" in out else ""), file=sys.stderr, flush=True)
     return out
 

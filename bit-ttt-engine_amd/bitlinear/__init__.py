@@ -12,7 +12,7 @@ package (a CPU tensor reaching a packed forward is an error, as for an
 unsupported device in bit_linear.rs:76-84).
 """
 from ._lib import (  # noqa: F401
-    BTL_ACT_F32_REF, BTL_ACT_I8, BTL_BF16, BTL_ERR_ARG, BTL_ERR_DEVICE, BTL_ERR_DTYPE, BTL_ERR_FAULT,
+    BTL_ACT_F32_REF, BTL_ACT_F32_SEQ, BTL_ACT_I8, BTL_BF16, BTL_ERR_ARG, BTL_ERR_DEVICE, BTL_ERR_DTYPE, BTL_ERR_FAULT,
     BTL_ERR_HIP, BTL_ERR_LAYOUT, BTL_ERR_SHAPE, BTL_ERR_WORKSPACE, BTL_F32, BTL_OK, EXPORTS,
     LIB_PATH, BitLinearError, BtlKvQ8, BtlPacked, BtlStreamLayer, check, check_faults, get_tuning, lib, set_tuning, tuning,
 )

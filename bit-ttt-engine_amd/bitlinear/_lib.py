@@ -24,6 +24,7 @@ BTL_BF16 = 1
 
 BTL_ACT_F32_REF = 0
 BTL_ACT_I8 = 1
+BTL_ACT_F32_SEQ = 2
 
 # Every symbol include/bitlinear.h declares.
 EXPORTS = (

@@ -6,13 +6,13 @@ import numpy as np
 import torch
 
 from ._lib import (
-    BTL_ACT_F32_REF, BTL_ACT_I8, BTL_BF16, BTL_ERR_DEVICE, BTL_ERR_DTYPE, BTL_ERR_LAYOUT, BTL_F32,
+    BTL_ACT_F32_REF, BTL_ACT_F32_SEQ, BTL_ACT_I8, BTL_BF16, BTL_ERR_DEVICE, BTL_ERR_DTYPE, BTL_ERR_LAYOUT, BTL_F32,
     BitLinearError, BtlPacked, check, lib,
 )
 from .packed import PackedTensor
 
 _DT = {torch.float32: BTL_F32, torch.bfloat16: BTL_BF16}
-_MODES = {"i8": BTL_ACT_I8, "f32_ref": BTL_ACT_F32_REF}
+_MODES = {"i8": BTL_ACT_I8, "f32_ref": BTL_ACT_F32_REF, "f32_seq": BTL_ACT_F32_SEQ}
 
 
 def _stream(device):
@@ -59,7 +59,8 @@ class BitLinearHip:
         """Y = X W^T.  input [M, K] float32/bfloat16 on the GPU, weights a PackedTensor
         [N, K] on the GPU.  Returns a new [M, N] tensor (dtype out_dtype, default
         the input's).  mode "i8": W1.58-A8; mode "f32_ref": the reference's fp32
-        semantics and summation order.  acc_out: optional int32 [M, N] tensor that
+        semantics and summation order (its AVX2/FMA lanes); mode "f32_seq": the same
+        semantics in the order of a host without AVX2/FMA.  acc_out: optional int32 [M, N] tensor that
         receives the exact accumulators (mode "i8")."""
         if input.dim() != 2:
             raise BitLinearError(1, "input must be 2-D, got %s" % (tuple(input.shape),))
@@ -187,7 +188,8 @@ def swiglu_linear_group(weights, gate, up, out_dtype=None, workspace=None, outpu
 
 def linear_group(weights, x, out_dtype=None, workspace=None, outputs=None, mode="i8"):
     """Several layers reading the same input in one launch (q|k|v, w1|w3), in
-    W1.58-A8 (mode "i8") or the reference's fp32 order (mode "f32_ref")."""
+    W1.58-A8 (mode "i8") or the reference's fp32 order (mode "f32_ref", or "f32_seq"
+    for its non-AVX2 order, one launch per layer)."""
     if mode not in _MODES:
         raise BitLinearError(BTL_ERR_DTYPE, "unknown mode %r" % (mode,))
     _on_gpu(x, "input")

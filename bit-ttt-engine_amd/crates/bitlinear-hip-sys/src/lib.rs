@@ -36,9 +36,11 @@ pub const BTL_ERR_FAULT: c_int = 8;
 pub const BTL_F32: c_int = 0;
 pub const BTL_BF16: c_int = 1;
 
-/// arithmetic modes: the reference's fp32 order (cpu.rs, bit for bit) and W1.58-A8
+/// arithmetic modes: the reference's fp32 order (cpu.rs, bit for bit: AVX2/FMA
+/// lanes, or the sequential loop of a host without them) and W1.58-A8
 pub const BTL_ACT_F32_REF: c_int = 0;
 pub const BTL_ACT_I8: c_int = 1;
+pub const BTL_ACT_F32_SEQ: c_int = 2;
 
 /// `btl_packed_t`: the reference's PackedTensor (packing.rs:14-21) with its bytes
 /// on the device: row-major [n, k] ternary weights, 4 per byte (code 01 = +1,

@@ -838,9 +838,9 @@ int btl_linear(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int6
     int rc = check_packed(w, m, k);
     if (rc) return rc;
     if ((rc = check_dtype(xdtype, "input")) || (rc = check_dtype(ydtype, "output"))) return rc;
-    if (mode != BTL_ACT_F32_REF && mode != BTL_ACT_I8) return fail(BTL_ERR_DTYPE, "unknown mode %d", mode);
-    if (mode == BTL_ACT_F32_REF && acc_out)
-        return fail(BTL_ERR_ARG, "acc_out is only defined for BTL_ACT_I8");
+    if (mode != BTL_ACT_F32_REF && mode != BTL_ACT_I8 && mode != BTL_ACT_F32_SEQ)
+        return fail(BTL_ERR_DTYPE, "unknown mode %d", mode);
+    if (mode != BTL_ACT_I8 && acc_out) return fail(BTL_ERR_ARG, "acc_out is only defined for BTL_ACT_I8");
     if (m == 0 || w->n == 0) return BTL_OK;
     if (!y || (k > 0 && !x)) return fail(BTL_ERR_LAYOUT, "null input or output");
     const hipStream_t st = (hipStream_t)stream;
@@ -852,6 +852,14 @@ int btl_linear(const btl_packed_t* w, const void* x, int xdtype, int64_t m, int6
         if (rc) return rc;
         hipError_t e = btl::launch_ref_f32(x, xk, m, k, w->data, w->n, w->scale, y, yk, st);
         if (e != hipSuccess) return hip_fail(e, "reference-order kernel launch");
+        return BTL_OK;
+    }
+    if (mode == BTL_ACT_F32_SEQ) {
+        int dev;
+        rc = current_device(&dev);
+        if (rc) return rc;
+        hipError_t e = btl::launch_ref_seq(x, xk, m, k, w->data, w->n, w->scale, y, yk, st);
+        if (e != hipSuccess) return hip_fail(e, "sequential reference-order kernel launch");
         return BTL_OK;
     }
     Layer l = {w, y, acc_out};
@@ -878,7 +886,7 @@ int btl_linear_noalloc(const btl_packed_t* w, const void* x, int xdtype, int64_t
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress (scratch)");
         return btl_linear(w, x, xdtype, m, k, y, ydtype, mode, acc_out, scratch, btl::kScratchBytes, stream);
     }
-    // the reference-order mode and empty calls use no scratch
+    // the reference-order modes and empty calls use no scratch
     return btl_linear(w, x, xdtype, m, k, y, ydtype, mode, acc_out, nullptr, 0, stream);
 }
 
@@ -917,7 +925,7 @@ int btl_linear_group_mode(const btl_packed_t* const* w, void* const* y, int coun
                           int64_t m, int64_t k, int ydtype, int mode, void* ws, size_t ws_bytes, void* stream)
 {
     if (mode == BTL_ACT_I8) return btl_linear_group(w, y, count, x, xdtype, m, k, ydtype, ws, ws_bytes, stream);
-    if (mode != BTL_ACT_F32_REF) return fail(BTL_ERR_DTYPE, "unknown mode %d", mode);
+    if (mode != BTL_ACT_F32_REF && mode != BTL_ACT_F32_SEQ) return fail(BTL_ERR_DTYPE, "unknown mode %d", mode);
     if (count < 1 || count > btl::kMaxGroup) return fail(BTL_ERR_ARG, "count %d not in 1..%d", count, btl::kMaxGroup);
     if (!w || !y) return fail(BTL_ERR_ARG, "null layer array");
     int rc;
@@ -940,9 +948,16 @@ int btl_linear_group_mode(const btl_packed_t* const* w, void* const* y, int coun
     if (k > 0 && !x) return fail(BTL_ERR_LAYOUT, "null input");
     int dev;
     if ((rc = current_device(&dev))) return rc;
-    const hipError_t e = btl::launch_ref_f32_group(x, xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32, m, k, wd, n, sc,
-                                                   yy, count, ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32,
-                                                   (hipStream_t)stream);
+    const int xk = xdtype == BTL_BF16 ? btl::XK_BF16 : btl::XK_F32;
+    const int yk = ydtype == BTL_BF16 ? btl::YK_BF16 : btl::YK_F32;
+    if (mode == BTL_ACT_F32_SEQ) {  // one launch per layer
+        for (int i = 0; i < count; ++i) {
+            const hipError_t e = btl::launch_ref_seq(x, xk, m, k, wd[i], n[i], sc[i], yy[i], yk, (hipStream_t)stream);
+            if (e != hipSuccess) return hip_fail(e, "sequential reference-order kernel launch");
+        }
+        return BTL_OK;
+    }
+    const hipError_t e = btl::launch_ref_f32_group(x, xk, m, k, wd, n, sc, yy, count, yk, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "reference-order kernel launch");
     return BTL_OK;
 }
@@ -1295,7 +1310,7 @@ int btl_swiglu_linear_group(const btl_packed_t* const* w, void* const* y, int co
 size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)
 {
     if (m < 0 || n < 0 || k < 0) return 0;
-    if (mode == BTL_ACT_F32_REF) return 0;
+    if (mode == BTL_ACT_F32_REF || mode == BTL_ACT_F32_SEQ) return 0;
     // split-K partials of the GEMM / batched-decode routes; a group's layers
     // have at least ceil(n / 128) (ceil(n / 64)) output tiles in total and the
     // splits only fall as tiles are added, so this bounds them

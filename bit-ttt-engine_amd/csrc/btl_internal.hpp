@@ -242,6 +242,9 @@ hipError_t launch_quant_act(const void* x, int xkind, int64_t m, int64_t k, int8
 
 hipError_t launch_ref_f32(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* w,
                           int64_t n, float scale, void* y, int ykind, hipStream_t st);
+// the reference's order without AVX2/FMA (one sequential chain per output)
+hipError_t launch_ref_seq(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* w,
+                          int64_t n, float scale, void* y, int ykind, hipStream_t st);
 // several layers over the same x (count <= kMaxGroup): one launch when the
 // LDS form applies, else one launch per layer
 struct RefGroup {

@@ -2704,6 +2704,125 @@ hipError_t launch_ref_f32(const void* x, int xkind, int64_t m, int64_t k, const 
 }
 
 // ---------------------------------------------------------------------------
+// k_ref_seq: the reference's contraction on a host without AVX2/FMA
+// ---------------------------------------------------------------------------
+// cpu.rs:62-66 leaves the vector loop out, so the scalar loop of
+// cpu.rs:105-122 covers every input: sum = +0.0f, then sum = sum + x[l] *
+// coeff(l) in increasing l, the product and the sum each rounded to f32, and
+// y = sum * scale (cpu.rs:123).  coeff is 0, 1 or -1, so the product is exact
+// (x, -x, a signed zero, or NaN for an infinite or NaN x) and fma(x, coeff,
+// sum) rounds once to the same value as the two operations (sum is never -0:
+// it starts at +0 and a round-to-nearest add only gives -0 from two -0s).
+// The chain cannot be split without changing the bits, so one thread owns one
+// output: grid (ceil(n / 256), min(m, 65535)), a thread per weight row of one
+// token row (rows past grid.y by a loop).  VEC (k % 64 == 0, w and x 16-byte
+// aligned, the row's x under 2 GiB): each thread streams its weight row, 64
+// weights per 16-byte load, and the token's 64 inputs of a block through a
+// buffer descriptor (the same address in every lane, in-order vector loads),
+// both one block ahead; the coefficients of a word's codes j and j + 8 are
+// looked up together as f16 (ref_coeffs) and applied by v_fma_mix_f32.  Else
+// one byte per 4 weights and plain loads.
+template <int XK>
+struct SeqX {
+    static constexpr int ES = XK == XK_BF16 ? 2 : 4;  // bytes per input
+    static constexpr int L = 4 * ES;                  // 16-byte loads per 64 inputs
+};
+
+// input j (a constant after unrolling) of a block held as loaded
+template <int XK>
+__device__ __forceinline__ float seq_elem(const uint4 (&r)[SeqX<XK>::L], int j)
+{
+    if (XK == XK_BF16) {
+        const uint4 v = r[j >> 3];
+        const int h = (j & 7) >> 1;
+        const uint32_t wd = h == 0 ? v.x : (h == 1 ? v.y : (h == 2 ? v.z : v.w));
+        return __uint_as_float((j & 1) ? (wd & 0xFFFF0000u) : (wd << 16));
+    }
+    const uint4 v = r[j >> 2];
+    const int h = j & 3;
+    return __uint_as_float(h == 0 ? v.x : (h == 1 ? v.y : (h == 2 ? v.z : v.w)));
+}
+
+template <int XK, int YK, bool VEC>
+__global__ __launch_bounds__(256) void k_ref_seq(const void* __restrict__ x, int64_t m, int64_t k,
+                                                 const uint8_t* __restrict__ w, int64_t n, float scale,
+                                                 void* __restrict__ y)
+{
+    constexpr int ES = SeqX<XK>::ES, XL = SeqX<XK>::L;
+    const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool active = col < n;
+    const uint8_t* wr = w + (active ? col : 0) * (k >> 2);
+    for (int64_t row = blockIdx.y; row < m; row += gridDim.y) {
+        const int64_t xb = row * k;
+        float sum = 0.0f;
+        if (VEC) {
+            // offsets past the row read as zero (the last block's look-ahead)
+            const __amdgpu_buffer_rsrc_t xr = make_rsrc((const uint8_t*)x + xb * ES, (uint32_t)(k * ES));
+            // one block: the chain over its 64 inputs (xc, weights qc) while the
+            // next block's loads (xn, qn) are in flight
+            auto block = [&](int64_t l, const uint4(&xc)[XL], uint4(&xn)[XL], const uint4& qc, uint4& qn) {
+                if (l + 64 < k) qn = *(const uint4*)(wr + ((l + 64) >> 2));
+#pragma unroll
+                for (int i = 0; i < XL; ++i) xn[i] = bload(xr, (int)((l + 64) * ES) + 16 * i);
+#pragma unroll
+                for (int wi = 0; wi < 4; ++wi) {
+                    const uint32_t wd = wi == 0 ? qc.x : (wi == 1 ? qc.y : (wi == 2 ? qc.z : qc.w));
+                    uint32_t c[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) c[j] = ref_coeffs(wd, (uint32_t)((2 * j + 24) & 31));
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const uint16_t h = j < 8 ? (uint16_t)c[j] : (uint16_t)(c[j - 8] >> 16);
+                        sum = __builtin_fmaf(seq_elem<XK>(xc, 16 * wi + j), (float)__builtin_bit_cast(_Float16, h),
+                                             sum);
+                    }
+                }
+            };
+            uint4 qa = make_uint4(0, 0, 0, 0), qb = qa, xa[XL], xbuf[XL];
+            if (k > 0) qa = *(const uint4*)wr;
+#pragma unroll
+            for (int i = 0; i < XL; ++i) xa[i] = bload(xr, 16 * i);
+            for (int64_t l = 0; l < k; l += 128) {  // two blocks, buffers alternating
+                block(l, xa, xbuf, qa, qb);
+                if (l + 64 < k) block(l + 64, xbuf, xa, qb, qa);
+            }
+        } else {
+            for (int64_t l = 0; l < k; l += 4) {
+                const uint32_t b = wr[l >> 2];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int code = (int)((b >> (2 * j)) & 3u);
+                    const float coeff = (float)((code & 1) - (code >> 1));
+                    sum = __fadd_rn(sum, __fmul_rn(load_x<XK>(x, xb + l + j), coeff));
+                }
+            }
+        }
+        if (active) store_y<YK>(y, row * n + col, __fmul_rn(sum, scale));
+    }
+}
+
+hipError_t launch_ref_seq(const void* x, int xkind, int64_t m, int64_t k, const uint8_t* w, int64_t n,
+                          float scale, void* y, int ykind, hipStream_t st)
+{
+    if (m <= 0 || n <= 0) return hipSuccess;
+    if ((n + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)(m < 65535 ? m : 65535));
+    const bool vec = k % 64 == 0 && ((uintptr_t)w & 15u) == 0 && ((uintptr_t)x & 15u) == 0 && k * 4 <= INT32_MAX - 1024;
+#define BTL_SEQ_CASE(XKV, YKV)                                                                             \
+    if (xkind == XKV && ykind == YKV) {                                                                    \
+        if (vec) hipLaunchKernelGGL((k_ref_seq<XKV, YKV, true>), grid, dim3(256), 0, st, x, m, k, w, n, scale, y); \
+        else hipLaunchKernelGGL((k_ref_seq<XKV, YKV, false>), grid, dim3(256), 0, st, x, m, k, w, n, scale, y);   \
+        return hipGetLastError();                                                                          \
+    }
+    BTL_SEQ_CASE(XK_F32, YK_F32)
+    BTL_SEQ_CASE(XK_F32, YK_BF16)
+    BTL_SEQ_CASE(XK_BF16, YK_F32)
+    BTL_SEQ_CASE(XK_BF16, YK_BF16)
+#undef BTL_SEQ_CASE
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
 // k_generic_i8: one wave per output, any k % 4 == 0, any alignment
 // ---------------------------------------------------------------------------
 template <int YK>

@@ -68,6 +68,9 @@ extern "C" {
                              the exact summation order of cpu.rs:86-123 */
 #define BTL_ACT_I8 1      /* W1.58-A8: per-token absmax int8 x, exact int32 sum,
                              y = (float)acc * (s_x * s_w) */
+#define BTL_ACT_F32_SEQ 2 /* reference semantics in the order of a host without
+                             AVX2/FMA (cpu.rs:62-66,105-123): sum = sum + x*t over
+                             k in increasing order, from +0.0f */
 
 /*
  * Packed ternary weights: the reference's PackedTensor (kernels/packing.rs:14-21).
@@ -191,6 +194,8 @@ int btl_quantize_act(const void* x, int xdtype, int64_t m, int64_t k, int8_t* xq
  *      reference's "Shape mismatch: Input [m, k] vs Weight [n, k_w]").
  * x:   [m, k] of xdtype;  y: [m, w->n] of ydtype.
  * mode BTL_ACT_F32_REF: reference semantics (bf16 x is widened exactly first).
+ * mode BTL_ACT_F32_SEQ: the same in the reference's non-AVX2 order (one
+ *                       sequential chain of k adds per output: latency-bound).
  * mode BTL_ACT_I8:      W1.58-A8 (quantisation as btl_quantize_act).
  * acc_out: optional [m, n] int32 accumulators (BTL_ACT_I8 only; else NULL).
  * ws / ws_bytes: optional workspace, see btl_workspace_bytes.
@@ -240,8 +245,9 @@ int btl_linear_group(const btl_packed_t* const* w, void* const* y, int count, co
  * BTL_ACT_F32_REF runs every layer in the reference's own fp32 semantics and
  * summation order (BitLinearCpu::forward, cpu.rs:17-127; the results of
  * btl_linear with that mode, bit for bit), all layers in one launch when k % 64
- * == 0, k <= 16384 and the weights are 16-byte aligned.  ws is unused in that
- * mode.  count in 1..4.
+ * == 0, k <= 16384 and the weights are 16-byte aligned; BTL_ACT_F32_SEQ the
+ * reference's non-AVX2 order, one launch per layer.  ws is unused in those
+ * modes.  count in 1..4.
  */
 int btl_linear_group_mode(const btl_packed_t* const* w, void* const* y, int count, const void* x, int xdtype,
                           int64_t m, int64_t k, int ydtype, int mode, void* ws, size_t ws_bytes, void* stream);

@@ -77,3 +77,41 @@ def test_adaptive_rejects_bad_shapes():
     y = torch.zeros((1, 16), device=DEV)
     st = bl.lib.btl_adaptive_linear(arr, 2, x.data_ptr(), bl.BTL_F32, 1, 32, y.data_ptr(), bl.BTL_F32, None, 0, None)
     assert st == bl.BTL_ERR_SHAPE and b"Shape mismatch" in bl.lib.btl_last_error()
+
+
+@pytest.mark.parametrize("m,nb", [(1, 1), (9, 3), (70, 5), (33, 8)])
+def test_adaptive_f32_ref_forward(m, nb):
+    # the reference's arithmetic: dense weights rebuilt at load (adaptive_linear.rs:86-124),
+    # then x . w_recon^T per forward (:141-151); bit-exact against the oracle's
+    # reconstruction and dense product, and within an fp32 sum's bound of float64
+    n, k = 200, 512
+    print("adaptive f32_ref", m, nb, flush=True)
+    packed, s = model(n, k, nb, seed=m + 7 * nb)
+    layer = bl.AdaptiveBitLinear.load(k, n, torch.from_numpy(packed), list(s), mode="f32_ref")
+    assert layer.bases is None and layer.reconstructed_weight.device.type == "cuda"
+    rec = orc.adaptive_reconstruct(packed, s, n, k)
+    assert np.array_equal(layer.reconstructed_weight.cpu().numpy().view(np.uint32), rec.view(np.uint32))
+    x = activations(m, k, seed=m + 1)
+    y = layer.forward(torch.from_numpy(x).to(DEV))
+    assert y.dtype == torch.float32 and tuple(y.shape) == (m, n)
+    got = y.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), orc.dense_linear(x, rec).view(np.uint32))
+    ref = x.astype(np.float64) @ rec.T.astype(np.float64)
+    tol = k * 2.0 ** -24 * (np.abs(x.astype(np.float64)) @ np.abs(rec.T.astype(np.float64))) + 1e-30
+    assert np.all(np.abs(got - ref) <= tol)
+
+
+def test_adaptive_f32_ref_llama_shape_rank3_and_bf16():
+    n, k, nb, m = 1024, 4096, 3, 6
+    packed, s = model(n, k, nb, seed=11)
+    layer = bl.AdaptiveBitLinear.load(k, n, torch.from_numpy(packed).to(DEV), list(s), mode="f32_ref")
+    rec = orc.adaptive_reconstruct(packed, s, n, k)
+    xt = torch.from_numpy(activations(m, k, seed=12)).to(DEV).to(torch.bfloat16)
+    y = layer.forward(xt.reshape(2, 3, k))  # rank 3 flattens (adaptive_linear.rs:137-143)
+    assert y.shape == (2, 3, n) and y.dtype == torch.float32
+    e = orc.dense_linear(xt.float().cpu().numpy(), rec)  # bf16 widens exactly
+    assert np.array_equal(y.reshape(m, n).cpu().numpy().view(np.uint32), e.view(np.uint32))
+    with pytest.raises(bl.BitLinearError):
+        layer.forward(xt, out_dtype=torch.bfloat16)
+    with pytest.raises(bl.BitLinearError):
+        layer.forward(torch.zeros((1, k - 4), device=DEV))

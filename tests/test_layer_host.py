@@ -89,3 +89,13 @@ def test_bitlinear_ste_forward_and_gradient():
         y1 = layer.forward(x[0, 0])
     assert tuple(y1.shape) == (40,)
     np.testing.assert_allclose(y1.detach().numpy(), ref[0], rtol=1e-5, atol=1e-5)
+
+
+def test_adaptive_layer_state_and_mode_checks():
+    # adaptive_linear.rs:126-127,159: no weights at all / a layer without either form
+    with pytest.raises(bl.BitLinearError, match="neither legacy nor adaptive"):
+        bl.AdaptiveBitLinear.load(64, 16)
+    with pytest.raises(bl.BitLinearError, match="unknown mode"):
+        bl.AdaptiveBitLinear.load(64, 16, np.zeros(16 * 16 * 2, np.uint8), [0.5, 0.25], mode="f16")
+    with pytest.raises(bl.BitLinearError, match="Invalid State"):
+        bl.AdaptiveBitLinear(64, 16).forward(torch.zeros((1, 64)))
