@@ -586,6 +586,14 @@ struct RqShape {
     static constexpr int kBytes = 1024 / R;  // bytes of a row per load instruction
 };
 
+// The quantised token row in LDS: operand-order byte b at rq_pad(b), 16 bytes
+// of padding after every 64.  A compute wave's lanes read 16 bytes each at a
+// stride of 64 bytes (one slice per lane); unpadded, those reads fell on 4 of
+// the 16 four-bank groups (4-way conflicts with 4 rows per wave, 8-way with 2).
+// Rows of several tokens are rq_row_bytes(k) apart (k % 64 == 0).
+__host__ __device__ constexpr int rq_pad(int b) { return b + ((b >> 6) << 4); }
+__host__ __device__ constexpr int rq_row_bytes(int k) { return k + (k >> 2) + 16; }
+
 // Fault bits of this source's kernels (kFault*), read and cleared by the host.
 __device__ uint32_t g_faults;
 
@@ -605,7 +613,7 @@ __device__ __forceinline__ void rq_wait(const uint32_t* c, uint32_t target, int 
 // holds groups t + nq gi of the MT x gpr groups of the token rows (row g /
 // gpr).  The absmax of every row over the quantising waves (LDS atomic max per
 // row, arrivals counted in s_sync[1]), then the groups in operand order into
-// sq (row stride k + 16); pre-quantised rows are only copied.  Ends with this
+// sq (rows rq_row_bytes(k) apart, bytes at rq_pad); pre-quantised rows are only copied.  Ends with this
 // wave's last arrival.
 template <int XK, int DG, int MT>
 __device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], int K, int gpr, int mt, int nqw,
@@ -655,7 +663,7 @@ __device__ __forceinline__ void rq_quantise(const uint4 (*xv)[DecX<XK>::kVec], i
         uint4 qv = group_quant<XK>(xv[gi], rm[gi]);
         if (!PREQ && rm[gi] == 0.0f) qv = uint4{0u, 0u, 0u, 0u};  // zero or non-finite row
         const int row = MT == 1 ? 0 : g / gpr;
-        if (g < ng) *(uint4*)(sq + row * (K + 16) + 16 * (g - row * gpr)) = qv;
+        if (g < ng) *(uint4*)(sq + row * rq_row_bytes(K) + rq_pad(16 * (g - row * gpr))) = qv;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -684,7 +692,7 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
     // first instructions, ahead of every weight load of the workgroup, and is
     // read from there group by group.
     constexpr bool GL = XN && DG == 2;
-    const uint4* const sg = (const uint4*)(sq + K + 16);
+    const uint4* const sg = (const uint4*)(sq + rq_row_bytes(K));
     float fv[DG][16];
 #pragma unroll
     for (int gi = 0; gi < DG; ++gi) {
@@ -775,7 +783,7 @@ __device__ __forceinline__ void rq_transform(const GemvArgs& a, const uint4 (*xv
     for (int gi = 0; gi < DG; ++gi) {
         const int g = tid + nq * gi;
         const uint4 qv = rm != 0.0f ? group_quant_f(fv[gi], rm) : uint4{0u, 0u, 0u, 0u};
-        if (g < gpr) *(uint4*)(sq + 16 * g) = qv;
+        if (g < gpr) *(uint4*)(sq + rq_pad(16 * g)) = qv;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0) __hip_atomic_fetch_add(&s_sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -795,7 +803,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) && !(DG == 
     constexpr int NV = DecX<XK>::kVec;
     constexpr int ES = XK == XK_F32 ? 4 : (XK == XK_BF16 ? 2 : 1);
     constexpr bool PREQ = DecX<XK>::kPreq;
-    extern __shared__ __align__(16) uint8_t sq[];  // [MT][k + 16], operand order
+    extern __shared__ __align__(16) uint8_t sq[];  // [MT][rq_row_bytes(k)], operand order, padded
     __shared__ uint32_t s_sync[3];                 // (unused), quantiser arrivals, gate arrivals
     __shared__ uint32_t s_amax[MT];                // absmax bits of each token row
     __shared__ float s_scale[MT];
@@ -836,7 +844,8 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) && !(DG == 
             // 1 KB copies of the norm weight into LDS after the operand row,
             // spread over the quantising waves (zeros past k)
             const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.g, (uint32_t)(K * 4));
-            for (int c = wave; c < (K * 4 + 1023) / 1024; c += nqw) copy_to_lds(gr, sq + K + 16 + c * 1024, c * 1024 + 16 * lane);
+            for (int c = wave; c < (K * 4 + 1023) / 1024; c += nqw)
+                copy_to_lds(gr, sq + rq_row_bytes(K) + c * 1024, c * 1024 + 16 * lane);
         }
 #pragma unroll
         for (int gi = 0; gi < (XF != XF_NONE && !(XN && DG == 2) ? DG : 0); ++gi) {
@@ -943,7 +952,7 @@ __attribute__((amdgpu_waves_per_eu(R == 4 && (XF == XF_NONE || PAIR) && !(DG == 
             const v4i aw = unpack16(wv[h]);
 #pragma unroll
             for (int mm = 0; mm < MT; ++mm) {
-                const uint8_t* bj = sq + (mm < mt ? mm : 0) * (K + 16) + (ko < K ? ko : 0);
+                const uint8_t* bj = sq + (mm < mt ? mm : 0) * rq_row_bytes(K) + rq_pad(ko < K ? ko : 0);
                 acc[mm] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aw, *(const v4i*)(bj + 16 * h), acc[mm], 0, 0, 0);
             }
         }
@@ -1041,7 +1050,7 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
         const int64_t per = pair ? a.parts / 2 : a.parts;
         const dim3 grid((unsigned)((groups + per - 1) / per)), block((unsigned)((nqw + a.parts) * 64));
         // the operand row; with the pairing also the norm weight (f32, whole 1 KB copies)
-        const size_t lds = (size_t)a.k + 16 + (pair ? ((size_t)a.k * 4 + 1023) / 1024 * 1024 : 0);
+        const size_t lds = (size_t)rq_row_bytes(a.k) + (pair ? ((size_t)a.k * 4 + 1023) / 1024 * 1024 : 0);
 #define BTL_RQ_XF(STV)                                                                                        \
     if (pair) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, true, XF_RMSNORM, 2>), grid, block, lds, s, a);       \
     else if (xform == XF_RMSNORM) hipLaunchKernelGGL((k_gemv_rq<XK_F32, 4, STV, false, XF_RMSNORM, 1>), grid, block, lds, s, a); \
@@ -1065,7 +1074,7 @@ hipError_t launch_gemv_rq(const GemvArgs& a, int xkind, int xform, hipStream_t s
     const int64_t per = pair ? a.parts / 2 : a.parts;
     const dim3 grid((unsigned)((groups + per - 1) / per)), block((unsigned)((nqw + a.parts) * 64));
     const int mt = a.m;
-    const size_t lds = (size_t)mt * (a.k + 16);
+    const size_t lds = (size_t)mt * rq_row_bytes(a.k);
 #define BTL_RQ_DG(XKV, RV, STV)                                                                                    \
     if (RV == 4 && mt == 2 && dg == 2) hipLaunchKernelGGL((k_gemv_rq<XKV, 4, STV, false, XF_NONE, 2, 2>), grid, block, lds, s, a); \
     else if (mt == 2) hipLaunchKernelGGL((k_gemv_rq<XKV, RV, STV, false, XF_NONE, 4, 2>), grid, block, lds, s, a); \
