@@ -62,7 +62,7 @@ enum Knob {
     KN_SPLIT_MERGE_MAX_M,    // ... up to this many token rows (16)
     KN_GEMV_BAT_NW,          // force the waves per workgroup of the batched decode kernel (1..16; 0 = rule)
     KN_GEMV_BAT_KS,          // force its K range (1024, 2048, 4096 weights; 0 = rule)
-    KN_GEMM_TILE,            // force the prefill GEMM tile (1: 128 rows, 2: 256 rows; 0 = rule)
+    KN_GEMM_TILE,            // force the prefill GEMM tile (1: 128 rows 2x2 waves, 2: 256 rows, 3: 128 rows 1x4; 0 = rule)
     KN_GEMM_TM64,            // 0: the GEMM keeps 128-token tiles for m <= 64 (1: 64-token tiles)
     KN_GEMM_TM64_STAGES,     // force the LDS stages of the 64-token tiles (2 or 4; 0 = rule)
     KN_GEMM_STAGES,          // force the LDS stages of the 128-token tiles (2 or 3; 0 = rule)

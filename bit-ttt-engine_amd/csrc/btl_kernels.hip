@@ -1775,22 +1775,20 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     const int64_t wide_min = knob(KN_GEMM_WIDE_MIN_TILES);
     int TN = g.splits <= 1 && tiles_m * tn256 >= wide_min ? 256 : 128;
     // BTL_GEMM_TILE forces the tile (tuning): 1 = 128 rows (2 x 2 waves), 2 =
-    // 256 rows (1 x 4 waves).  (A 256-row tile of 2 x 4 waves, each 64 x 64,
+    // 256 rows (1 x 4 waves), 3 = 128 rows (1 x 4 waves).  (A 256-row tile of 2 x 4 waves, each 64 x 64,
     // measured slower for every Llama-3-8B prefill shape: gate|up 227 against
     // 195 us.)
     const int ftile = knob(KN_GEMM_TILE);
-    if (ftile == 1 || ftile == 2) TN = ftile == 1 ? 128 : 256;
+    if (ftile == 1 || ftile == 2 || ftile == 3) TN = ftile == 2 ? 256 : 128;
+    // 3: 128 rows as 1 x 4 waves of 128 tokens x 32 rows (each unpacked weight
+    // word feeds 8 token blocks, as in the 256-row tile)
+    const bool w14f = ftile == 3;
     // up to 64 token rows: tiles of 64 tokens (a 128-row tile would be half
     // zero-filled, its MFMAs and LDS reads half wasted), 256 rows wide when
     // split (measured on MI355X, Llama-3-8B down at m = 24..64); BTL_GEMM_TM64
     // = 0 keeps 128
     const bool tm64 = g.m <= 64 && knob(KN_GEMM_TM64) != 0;
     if (tm64 && g.splits > 1 && ftile != 1) TN = 256;
-    // a long K whose 256-row tiles give at most one workgroup per CU: 256 rows
-    // and 4 LDS stages (the pipeline's fill amortised over many steps; measured
-    // on MI355X, Llama-3-8B down at M = 2048: 112.2 -> 105.3 us)
-    const bool deep = !tm64 && g.splits <= 1 && ftile == 0 && g.cus > 0 && tiles_m * tn256 <= g.cus && g.k >= 8192;
-    if (deep) TN = 256;
     int64_t tn = 0, cols = 0;
     for (int l = 0; l < g.nl; ++l) {
         g.L[l].tile0 = (int)tn;
@@ -1821,12 +1819,24 @@ hipError_t launch_gemm_i8(const GemmArgs& a, hipStream_t s)
     // says 3, and a forced 3 means 4.
     const int fps = knob(KN_GEMM_STAGES);
     const int64_t wgs = tiles * g.splits;
-    int pns = fps == 2 || fps == 3 || (fps == 4 && TN == 256) ? fps
-              : deep                                         ? 4
-              : (g.cus > 0 && wgs <= 2 * g.cus ? 3 : 2);
+    int pns = fps == 2 || fps == 3 || (fps == 4 && TN == 256) ? fps : (g.cus > 0 && wgs <= 2 * g.cus ? 3 : 2);
     if (TN == 256 && pns == 3) pns = fps == 3 ? 4 : 2;
+    // unsplit 128-row tiles resident at two per CU (3 stages) take 1 x 4 waves of
+    // 128 tokens x 32 rows: each unpacked weight word feeds 8 token blocks instead
+    // of 4 (measured on MI355X, Llama-3-8B M = 2048, four alternating rounds: o
+    // 34.3-35.8 -> 33.5-34.2 us against 2 x 2 waves; down 102.6-109.4 -> 98.7-101.7
+    // against its earlier 256-row tiles with 4 stages; q|k|v, whose 768
+    // workgroups take 2 stages, measured equal and keeps 2 x 2 waves)
+    const bool w14rule = ftile == 0 && TN == 128 && !tm64 && g.splits <= 1 && pns == 3;
+    const bool w14 = w14f || w14rule;
     const char* form;
-    if (TN == 256 && tm64 && ns == 4) {
+    if (w14 && !tm64 && pns == 3) {
+        form = "k_gemm_i8<128,4,4,128,3>";
+        hipLaunchKernelGGL((k_gemm_i8<128, 4, 4, 128, 3>), grid, dim3(256), 0, s, g);
+    } else if (w14 && !tm64) {
+        form = "k_gemm_i8<128,4,4,128,2>";
+        hipLaunchKernelGGL((k_gemm_i8<128, 4>), grid, dim3(256), 0, s, g);
+    } else if (TN == 256 && tm64 && ns == 4) {
         form = "k_gemm_i8<256,4,4,64,4>";
         hipLaunchKernelGGL((k_gemm_i8<256, 4, 4, 64, 4>), grid, dim3(256), 0, s, g);
     } else if (TN == 256 && tm64) {

@@ -435,9 +435,10 @@ def test_small_m_gemm_split_forms(m, k, n, stages, tile, tune):
     assert torch.equal(y, y0)
 
 
-# the prefill GEMM's 128-row tiles with 2 and 3 LDS stages, and its 256-row tiles
-# with 2 (the form the M = 2048 gate|up launch takes) and 4 (a forced 3 takes 4:
-# the 256-row tile has no 3-stage form): k = 1088 (9 steps, the last one half:
+# the prefill GEMM's 128-row tiles with 2 and 3 LDS stages (2 x 2 waves, and 1 x 4
+# waves of 128 tokens x 32 rows), and its 256-row tiles with 2 (the form the M = 2048
+# gate|up launch takes) and 4 (a forced 3 takes 4: the 256-row tile has no 3-stage
+# form): k = 1088 (9 steps, the last one half:
 # unrolled rounds and a tail), k = 4096, k = 8256 (64.5 steps); ragged m and n;
 # one split launch (m = 130 x 300 rows has few tiles)
 @pytest.mark.parametrize("m,k,n", [(256, 1088, 1000), (130, 4096, 300), (300, 2048, 2560), (200, 8256, 700)])
@@ -447,7 +448,8 @@ def test_prefill_gemm_stages(m, k, n, tune):
     pt, wb, sw = make_layer(n, k, seed=n + 2 * k)
     ys, accs = [], []
     for tile, stages, form in ((1, 2, "<128,2,4,128,2>"), (1, 3, "<128,2,4,128,3>"), (2, 2, "<256,4,4,128,2>"),
-                               (2, 3, "<256,4,4,128,4>"), (2, 4, "<256,4,4,128,4>")):
+                               (2, 3, "<256,4,4,128,4>"), (2, 4, "<256,4,4,128,4>"), (3, 2, "<128,4,4,128,2>"),
+                               (3, 3, "<128,4,4,128,3>")):
         tune("BTL_GEMM_TILE", tile)
         tune("BTL_GEMM_STAGES", stages)
         acc = torch.empty((m, n), dtype=torch.int32, device=DEV)

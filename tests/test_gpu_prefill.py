@@ -34,9 +34,9 @@ HIDDEN, INTER, KV = 4096, 14336, 1024
 # instantiation the default routing gives each on 256 CUs
 KINDS = {
     "qkv": (HIDDEN, (HIDDEN, KV, KV), "k_gemm_i8<128,2,4,128,2>"),
-    "o": (HIDDEN, (HIDDEN,), "k_gemm_i8<128,2,4,128,3>"),
+    "o": (HIDDEN, (HIDDEN,), "k_gemm_i8<128,4,4,128,3>"),
     "gate_up": (HIDDEN, (INTER, INTER), "k_gemm_i8<256,4,4,128,2>"),
-    "down": (INTER, (HIDDEN,), "k_gemm_i8<256,4,4,128,4>"),
+    "down": (INTER, (HIDDEN,), "k_gemm_i8<128,4,4,128,3>"),
 }
 
 
