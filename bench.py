@@ -976,7 +976,8 @@ def mfma_ceilings(lib, dev, cap):
 def run_probe(args):
     """A few launches of one workload, plus a plain copy of known size, for
     counter runs (rocprofv3 --pmc ...): --probe decode_<kind> is btl_linear_group
-    at M=1 (the decode kernel), prefill_<kind> btl_linear_i8_op at M=--prefill-m
+    at M=1 (the decode kernel), batched<M>_<kind> the same at M token rows (M up
+    to 64: the batched-decode routes), prefill_<kind> btl_linear_i8_op at M=--prefill-m
     (the GEMM alone), kind one of qkv, o, gate_up, down (the Llama-3-8B calls of a
     layer).  The copy reads and writes 256 MiB per dispatch and calibrates the
     memory counters.  Prints what ran."""
@@ -990,12 +991,13 @@ def run_probe(args):
     shp = PROBE_KINDS[kind]
     k = shp[0][1]
     ws = [synth_packed(n, kk, gen, dev) for (n, kk) in shp]
-    m = 1 if phase == "decode" else args.prefill_m
+    m = 1 if phase == "decode" else (int(phase[7:]) if phase.startswith("batched") else args.prefill_m)
     x = synth_act(m, k, gen, dev)
     outs = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for (n, _) in shp]
-    if phase == "decode":
+    if phase == "decode" or phase.startswith("batched"):
         call = Call(ws, x, outs)
-        what = "btl_linear_group %s, M=1, %d -> %s, bf16 (decode kernel)" % (kind, k, "+".join(str(n) for n, _ in shp))
+        what = "btl_linear_group %s, M=%d, %d -> %s, bf16 (%s route)" % (
+            kind, m, k, "+".join(str(n) for n, _ in shp), "decode" if m == 1 else "batched-decode")
     else:
         q, s = bl.quantize_act_op(x)
         call = OpCall(ws, q, s, outs)
@@ -1026,8 +1028,10 @@ def main():
     ap.add_argument("--no-sweep", dest="sweep", action="store_false",
                     help="skip the cfg3 batched-decode section of the JSON line")
     ap.add_argument("--probe", default=None,
-                    choices=["ceilings"] + ["%s_%s" % (p, k) for p in ("decode", "prefill") for k in PROBE_KINDS],
-                    help="decode_<kind> / prefill_<kind> (kind qkv, o, gate_up, down): counter-run mode, --steps "
+                    choices=["ceilings"] + ["%s_%s" % (p, k) for p in ("decode", "prefill") + tuple(
+                        "batched%d" % m for m in (2, 4, 8, 16, 32, 64)) for k in PROBE_KINDS],
+                    help="decode_<kind> / batched<M>_<kind> / prefill_<kind> (kind qkv, o, gate_up, down): "
+                         "counter-run mode, --steps "
                          "launches of one workload and a 256 MiB copy, no JSON; ceilings: the decode chain's "
                          "streaming-read and launch-floor probes alone, one JSON line")
     ap.add_argument("--no-e2e", dest="e2e", action="store_false",

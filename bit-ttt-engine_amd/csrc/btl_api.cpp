@@ -104,7 +104,8 @@ constexpr KnobDef kKnobs[btl::KN_COUNT] = {
     {"BTL_WAIT_SPIN", 1 << 22}, {"BTL_ATTN_MERGE", 1}, {"BTL_SPLIT_MERGE", 1},
     {"BTL_SPLIT_MERGE_MAX_M", 16}, {"BTL_GEMV_BAT_NW", 0}, {"BTL_GEMV_BAT_KS", 0},
     {"BTL_GEMM_TILE", 0}, {"BTL_GEMM_TM64", 1}, {"BTL_GEMM_TM64_STAGES", 0}, {"BTL_GEMM_STAGES", 0},
-    {"BTL_DEC_RQ2_MAX_K", 16384},
+    {"BTL_DEC_RQ2_MAX_K", 16384}, {"BTL_GEMV_TR", 1}, {"BTL_GEMV_TR_MIN_M", 3}, {"BTL_GEMV_TR_MAX_M", 32},
+    {"BTL_GEMV_TR_RBPW", 0}, {"BTL_GEMV_TR_K16", 8192},
 };
 std::atomic<int> g_knob[btl::KN_COUNT];
 std::once_flag g_knob_once;
@@ -142,12 +143,13 @@ struct WsLayout {
     size_t q_off, s_off, p_off, total;
 };
 
-// q [m, k] int8, s [m] f32, then `part_bytes` of split-K partial sums
-WsLayout ws_layout(int64_t m, int64_t k, size_t part_bytes)
+// q [m, k] int8 (or q_bytes, when larger: the token-register layout), s [m]
+// f32, then `part_bytes` of split-K partial sums
+WsLayout ws_layout(int64_t m, int64_t k, size_t part_bytes, size_t q_bytes = 0)
 {
     WsLayout l;
     l.q_off = 0;
-    l.s_off = align_up((size_t)(m * k), 256);
+    l.s_off = align_up((size_t)(m * k) > q_bytes ? (size_t)(m * k) : q_bytes, 256);
     l.p_off = l.s_off + align_up((size_t)(4 * m), 256);
     l.total = l.p_off + align_up(part_bytes, 256);
     return l;
@@ -443,6 +445,58 @@ int run_i8(const Layer* layers, int count, const void* x, int xkind, const float
     if (swiglu_out) {
         if (!dec || wv > 8) return fail(BTL_ERR_ARG, "SwiGLU epilogue needs the decode route");
         rbw = 2;  // workgroup w: row block w of gate and of up
+    }
+    // Batched decode of KN_GEMV_TR_MIN_M .. KN_GEMV_TR_MAX_M token rows (up to
+    // 16 rows only from k = KN_GEMV_TR_K16 on): the token-register kernel
+    // (bf16 / f32 input, no transform), tokens quantised straight into its
+    // register layout; its K splits (k > 4096) are added in the launch, so it
+    // needs this workspace's merge counters (else the routes below).  Measured
+    // on MI355X, Llama-3-8B MLP, us per call with the quantiser launch:
+    // gate|up (k = 4096) at m = 17..32 15.7-16.1 against 19.5-21.0 through
+    // k_gemv_bat / the 64-token GEMM, at m = 3..16 12.5-13.8 against 11.8-12.9;
+    // down (k = 14336) at m = 3..32 11.5-16.2 against 12.0-17.5; at m = 40
+    // (64 token columns per wave) gate|up 21.0 against 21.2, down 19.3 against 18.0.
+    if (!dec && !xf && !swiglu_out && (xkind == btl::XK_F32 || xkind == btl::XK_BF16) && k <= 65536 &&
+        m >= env_int(btl::KN_GEMV_TR_MIN_M) && m <= env_int(btl::KN_GEMV_TR_MAX_M) && m <= 64 &&
+        (m > 16 || k >= env_int(btl::KN_GEMV_TR_K16)) && env_int(btl::KN_GEMV_TR) != 0) {
+        int64_t rbs = 0;
+        for (int i = 0; i < count; ++i) rbs += ceil_div(layers[i].w->n, 16);
+        const btl::TrPlan tp = btl::gemv_tr_plan(m, rbs, k, g_dev[dev].cus);
+        const WsLayout L = ws_layout(m, k, tp.splits > 1 ? (size_t)tp.splits * m * nsum * 4 : 0,
+                                     (size_t)btl::tr_bytes(k, tp.mtb));
+        void* ws = nullptr;
+        if ((rc = get_ws(dev, ws_user, ws_bytes, L.total, &ws, st))) return rc;
+        uint32_t* ctr = nullptr;
+        if (tp.splits > 1 && ceil_div(rbs, tp.rbpw) <= btl::kSplitCounters &&
+            (e = btl::split_counters(dev, ws, &ctr)) != hipSuccess)
+            return hip_fail(e, "split-K merge counters");
+        if (tp.splits == 1 || ctr) {
+            int8_t* q = (int8_t*)ws + L.q_off;
+            float* sxp = (float*)((uint8_t*)ws + L.s_off);
+            e = btl::launch_quant_op(x, xkind, m, k, q, sxp, st, tp.mtb);
+            if (e != hipSuccess) return hip_fail(e, "quantize kernel launch");
+            btl::GemmArgs g;
+            memset(&g, 0, sizeof(g));
+            g.q = q;
+            g.sx = sxp;
+            g.m = (int)m;
+            g.k = (int)k;
+            g.ykind = ykind;
+            g.part = tp.splits > 1 ? (int32_t*)((uint8_t*)ws + L.p_off) : nullptr;
+            g.ctr = ctr;
+            for (int i = 0; i < count; ++i) {
+                if (layers[i].w->n == 0) continue;
+                btl::GemmLayer& gl = g.L[g.nl++];
+                gl.w = layers[i].w->data;
+                gl.sw = layers[i].w->scale;
+                gl.n = (int)layers[i].w->n;
+                gl.y = layers[i].y;
+                gl.acc_out = layers[i].acc;
+            }
+            e = btl::launch_gemv_tr(g, tp, st);
+            if (e != hipSuccess) return hip_fail(e, "token-register batched gemv kernel launch");
+            return resid ? add_resid(layers[0], resid, m, st) : BTL_OK;
+        }
     }
     // Batched decode up to KN_GEMV_BAT_MAX_M rows -- but from 21 rows on, a
     // layer group wide enough for the unsplit 64-token GEMM takes that
@@ -1315,11 +1369,17 @@ size_t btl_workspace_bytes(int64_t m, int64_t n, int64_t k, int mode)
     // have at least ceil(n / 128) (ceil(n / 64)) output tiles in total and the
     // splits only fall as tiles are added, so this bounds them
     int splits = btl::gemm_splits(m, ceil_div(n, 128), k, nullptr);
-    if (m <= 64) {  // any BTL_GEMV_BAT_MAX_M
+    size_t q_bytes = 0;
+    if (m <= 64) {  // any BTL_GEMV_BAT_MAX_M / BTL_GEMV_TR_MAX_M
         const int sb = btl::gemv_bat_plan(m, n, k).splits;
         splits = sb > splits ? sb : splits;
+        // the token-register route: its splits depend on k alone, its token
+        // layout pads m to 16, 32 or 64 rows and k to 512
+        const btl::TrPlan tp = btl::gemv_tr_plan(m, ceil_div(n, 16), k, 0);
+        splits = tp.splits > splits ? tp.splits : splits;
+        q_bytes = (size_t)btl::tr_bytes(k, tp.mtb);
     }
-    return ws_layout(m, k, splits > 1 ? (size_t)splits * m * n * 4 : 0).total;
+    return ws_layout(m, k, splits > 1 ? (size_t)splits * m * n * 4 : 0, q_bytes).total;
 }
 
 int btl_workspace_clear(void* ws, size_t ws_bytes, void* stream)

@@ -67,6 +67,11 @@ enum Knob {
     KN_GEMM_TM64_STAGES,     // force the LDS stages of the 64-token tiles (2 or 4; 0 = rule)
     KN_GEMM_STAGES,          // force the LDS stages of the 128-token tiles (2 or 3; 0 = rule)
     KN_DEC_RQ2_MAX_K,        // two token rows take the row-group decode form up to this k (16384)
+    KN_GEMV_TR,              // 0 turns the token-register batched decode kernel off (1)
+    KN_GEMV_TR_MIN_M,        // ... it takes launches from this many token rows (3)
+    KN_GEMV_TR_MAX_M,        // ... up to this many (32; at most 64)
+    KN_GEMV_TR_RBPW,         // force its 16-row blocks per workgroup (1..8; 0 = rule)
+    KN_GEMV_TR_K16,          // ... and launches of at most 16 rows only from this k on (8192)
     KN_COUNT
 };
 int knob(Knob k);
@@ -191,6 +196,8 @@ struct GemmArgs {
     uint32_t* ctr;     // k_gemv_bat: merge counters (split_counters) -- splits merged in the launch; NULL: reduce launch
     int bat_nw;        // k_gemv_bat: waves per workgroup (4, 8, 16), a row block of 16 bat_nw rows
     int cus;           // compute units of the device (0: unknown), for the GEMM's stage count
+    int tr_rbpw;       // k_gemv_tr: 16-row blocks per workgroup (of one layer),
+    int tr_cols;       // output columns over the layers (set by launch_gemv_tr)
 };
 
 constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for
@@ -225,10 +232,32 @@ constexpr int kSplitCounters = 2048;
 constexpr int kSplitSlots = 128;
 constexpr int kMergeMaxSplits = 16;  // K ranges of >= 1024 weights, k <= 16384
 hipError_t split_counters(int dev, const void* ws_key, uint32_t** out);
+
+// Batched decode with the tokens resident in registers (k_gemv_tr), m <= 64,
+// k % 64 == 0, k <= 65536.  The tokens are quantised into the token-register
+// layout by launch_quant_op(..., tr_mtb = plan.mtb): group g (16 weights) of
+// token t at byte tr_offset(t, g, mtb) of a buffer of tr_bytes(k, mtb).  Wave
+// w of a workgroup owns K segment (split * nw + w) of 512 weights; a launch
+// has `splits` K splits (merged in the launch through a.ctr, which must then
+// be non-null: one counter per row group, kSplitCounters at most).
+constexpr int kTrSeg = 512;  // weights of one wave's K segment
+constexpr int64_t tr_offset(int64_t t, int64_t g, int mtb)
+{
+    return (((((g >> 5) * mtb + (t >> 4)) * 8 + (g & 7)) * 64) + 16 * ((g >> 3) & 3) + (t & 15)) * 16;
+}
+constexpr int64_t tr_bytes(int64_t k, int mtb) { return (k + kTrSeg - 1) / kTrSeg * kTrSeg * 16 * mtb; }
+struct TrPlan {
+    int mtb;     // 16-token blocks held per wave (1, 2 or 4)
+    int nw;      // waves (K segments) per workgroup, 1..8
+    int splits;  // K splits
+    int rbpw;    // 16-row blocks per workgroup, 1..8
+};
+TrPlan gemv_tr_plan(int64_t m, int64_t row_blocks, int64_t k, int cus);
+hipError_t launch_gemv_tr(const GemmArgs& a, const TrPlan& p, hipStream_t s);
 // natural-order int8 rows -> operand order (k % 16 == 0, 16-byte aligned)
 hipError_t launch_op_order(const int8_t* q, int64_t m, int64_t k, int8_t* out, hipStream_t st);
 hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,
-                           hipStream_t st);
+                           hipStream_t st, int tr_mtb = 0);
 // fused transform + operand-order quantisation, one workgroup per token row:
 // XF_RMSNORM: x / sqrt(pairwise_sum(x*x) * (f32)(1/k) + eps) * g (g: [k] f32);
 // XF_SWIGLU:  silu(x) * x2;  XF_ADD_RMSNORM: hout = x + x2 (f32 both; hout may alias

@@ -27,6 +27,8 @@
 // written (the oracle restates the same operations in C).
 #include <hip/hip_runtime.h>
 
+#include <utility>
+
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -1153,9 +1155,10 @@ __global__ __launch_bounds__(256) void k_quant_op(const void* x, int k, int8_t* 
 
 // Single pass: one workgroup per token row (64 * ceil(k / 1024) threads, at
 // most 1024) holds G 16-element groups per thread in registers (k <= 16384 G),
-// so x is read once.
-template <int XK, int G>
-__global__ __launch_bounds__(1024) void k_quant_op1(const void* x, int k, int8_t* q, float* s)
+// so x is read once.  TR: group g of the row goes to tr_offset(row, g, tr_mtb)
+// (the token-register layout of k_gemv_tr) instead of row * k + 16 g.
+template <int XK, int G, bool TR = false>
+__global__ __launch_bounds__(1024) void k_quant_op1(const void* x, int k, int8_t* q, float* s, int tr_mtb)
 {
     __shared__ uint32_t s_w[16];
     const int64_t row = blockIdx.x;
@@ -1186,21 +1189,41 @@ __global__ __launch_bounds__(1024) void k_quant_op1(const void* x, int k, int8_t
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const int gi = tid + nt * g;
-        if (gi < groups) qr[gi] = qp.ok ? group_quant<XK>(v[g], qp.r) : uint4{0u, 0u, 0u, 0u};
+        if (gi < groups) {
+            const uint4 o = qp.ok ? group_quant<XK>(v[g], qp.r) : uint4{0u, 0u, 0u, 0u};
+            if (TR) *(uint4*)(q + tr_offset(row, gi, tr_mtb)) = o;
+            else qr[gi] = o;
+        }
     }
 }
 
 hipError_t launch_quant_op(const void* x, int xkind, int64_t m, int64_t k, int8_t* q, float* s,
-                           hipStream_t st)
+                           hipStream_t st, int tr_mtb)
 {
     if (m <= 0) return hipSuccess;
     const int64_t groups = k >> 4;
     const dim3 grid((unsigned)m);
     const int nt = groups <= 1024 ? (int)((groups + 63) / 64 * 64) : 1024;
-#define BTL_QOP1(XKV, GV)                                                                \
-    if (groups <= 1024 * GV) {                                                           \
-        hipLaunchKernelGGL((k_quant_op1<XKV, GV>), grid, dim3(nt), 0, st, x, (int)k, q, s); \
-        return hipGetLastError();                                                        \
+    if (tr_mtb) {
+        // the token-register layout: single pass only (k <= 65536)
+        if (m > 16 * tr_mtb || groups > 4096 || (xkind != XK_BF16 && xkind != XK_F32)) return hipErrorInvalidValue;
+#define BTL_QTR(XKV, GV)                                                                                 \
+    if (groups <= 1024 * GV) {                                                                           \
+        hipLaunchKernelGGL((k_quant_op1<XKV, GV, true>), grid, dim3(nt), 0, st, x, (int)k, q, s, tr_mtb); \
+        return hipGetLastError();                                                                        \
+    }
+        if (xkind == XK_BF16) {
+            BTL_QTR(XK_BF16, 1) BTL_QTR(XK_BF16, 2) BTL_QTR(XK_BF16, 4)
+        } else {
+            BTL_QTR(XK_F32, 1) BTL_QTR(XK_F32, 2) BTL_QTR(XK_F32, 4)
+        }
+#undef BTL_QTR
+        return hipErrorInvalidValue;
+    }
+#define BTL_QOP1(XKV, GV)                                                                   \
+    if (groups <= 1024 * GV) {                                                              \
+        hipLaunchKernelGGL((k_quant_op1<XKV, GV>), grid, dim3(nt), 0, st, x, (int)k, q, s, 0); \
+        return hipGetLastError();                                                           \
     }
     if (xkind == XK_BF16) {
         BTL_QOP1(XK_BF16, 1) BTL_QOP1(XK_BF16, 2) BTL_QOP1(XK_BF16, 4)
@@ -2172,6 +2195,318 @@ hipError_t split_counters(int dev, const void* ws_key, uint32_t** out)
     const int i = slots[dev].find(ws_key);
     *out = i < 0 ? nullptr : b + (size_t)i * kSplitCounters;
     return hipSuccess;
+}
+
+// ---------------------------------------------------------------------------
+// k_gemv_tr: batched decode with the token rows resident in registers
+// ---------------------------------------------------------------------------
+// From a few token rows on, the operand that every workgroup re-reads is the
+// token block, not the weights.  Wave w of a workgroup owns one K segment of
+// 512 weights and loads that segment of all 16 MTB token rows into registers
+// once (8 MFMA operands per 16-token block, 32 VGPRs; the quantiser writes the
+// tokens in exactly this register order, so every token load instruction reads
+// 1 KB contiguously).  The weights then stream through the wave once: per
+// 16-row block two non-temporal loads per lane, each 8 rows x 128 contiguous
+// bytes (whole cache lines), regrouped by one DPP exchange so that lane
+// 16 kq + r holds dwords 8 kq .. 8 kq + 7 of row r; each dword is unpacked once
+// and feeds MTB MFMAs (v_mfma_i32_16x16x64_i8, tokens as A, weights as B, so
+// that an output's 16 lanes hold 16 consecutive rows of one token).  The
+// loads of row block i + PD go out while row block i computes.  The NW segment
+// sums of a row block meet in LDS; one barrier per group of row blocks (all of
+// them, or 4 with 64 token columns) lets the waves add them and apply the
+// epilogue, so the weights never pass through LDS, the tokens are read once
+// per workgroup and the waves do not wait for each other between row blocks.
+// With K splits (grid.y) each split stores its exact int32 sums coherently and
+// the last split of the row group to arrive adds them (a.ctr, left at zero).
+//
+// MFMA w of a row block contracts the 16-weight groups {8 kq + w : kq = 0..3}
+// of the wave's segment: lane 16 kq + j holds token 16 tb + j's group 8 kq + w
+// (A, register tok[tb][w]) and lane 16 kq + r row r's dword 8 kq + w (B).
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}),
+// in order: a loop whose index is a constant expression in the body
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, Is...>)
+{
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+
+// The fields of the layer that workgroup wg works on (GemmLayer::tile0: the
+// layer's first workgroup), picked field by field with selects once per
+// workgroup: an indexed or conditionally copied GemmLayer made the compiler
+// copy the kernel arguments to scratch.
+struct TrLayer {
+    const uint8_t* w;
+    void* y;
+    int32_t* acc;
+    float sw;
+    int n, tile0, col0;
+};
+__device__ __forceinline__ TrLayer tr_layer(const GemmArgs& a, int wg)
+{
+    TrLayer r{a.L[0].w, a.L[0].y, a.L[0].acc_out, a.L[0].sw, a.L[0].n, a.L[0].tile0, a.L[0].col0};
+#pragma unroll
+    for (int l = 1; l < kMaxGroup; ++l) {
+        const bool in = l < a.nl && wg >= a.L[l].tile0;
+        r.w = in ? a.L[l].w : r.w;
+        r.y = in ? a.L[l].y : r.y;
+        r.acc = in ? a.L[l].acc_out : r.acc;
+        r.sw = in ? a.L[l].sw : r.sw;
+        r.n = in ? a.L[l].n : r.n;
+        r.tile0 = in ? a.L[l].tile0 : r.tile0;
+        r.col0 = in ? a.L[l].col0 : r.col0;
+    }
+    return r;
+}
+
+template <int MTB, int RBW, int PD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MTB == 1 ? 4 : 2)))
+void k_gemv_tr(GemmArgs a)
+{
+    static_assert(MTB == 1 || MTB == 2 || MTB == 4, "16, 32 or 64 token columns");
+    static_assert(PD >= 1 && PD <= RBW && RBW <= 8, "prefetch depth within the row blocks");
+    extern __shared__ __align__(16) uint8_t tr_lds[];  // [nw][G][MTB][64 lanes] x 16 B
+    v4i* red = (v4i*)tr_lds;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nw = blockDim.x >> 6;
+    const int K = a.k, M = a.m;
+    const int split = blockIdx.y;
+    const int seg = split * nw + wave;  // this wave's K segment
+    const int kb = seg * kTrSeg;
+    const bool kact = kb < K;  // uniform; past k the wave adds zeros
+    const int rbytes = K >> 2;
+    // this workgroup's layer and its row blocks rb0 .. rb0 + nrb - 1 of it
+    const TrLayer Lw = tr_layer(a, (int)blockIdx.x);
+    const int N = Lw.n;
+    const int rb0 = ((int)blockIdx.x - Lw.tile0) * a.tr_rbpw;
+    const int nrb = min(a.tr_rbpw, (N + 15) / 16 - rb0);  // uniform, >= 1
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(Lw.w + (int64_t)rb0 * 16 * rbytes,
+                                                kact ? (uint32_t)(min(16 * nrb, N - 16 * rb0) * rbytes) : 0u);
+    // load h of row block i: lane l reads row 8 h + (l & 7) of the block, bytes
+    // [16 (l >> 3), +16) of the segment's 128 bytes of that row (past k: zeros)
+    const int byte = (kb >> 2) + 16 * (lane >> 3);
+    const int woff = byte < rbytes ? (lane & 7) * rbytes + byte : kOOB;
+    auto issue = [&](int i, uint4 (&b)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            b[h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 wr, woff == kOOB ? kOOB : woff + (16 * i + 8 * h) * rbytes, 0,
+                                                 kCachePolicyNT));
+    };
+
+    // 1. row block 0's weights (HBM first), the token segment and scales, row
+    //    blocks 1 .. PD-1
+    uint4 buf[PD][2];
+    issue(0, buf[0]);
+    // (scheduling barriers keep the issue order: row block 0's weights first,
+    // row blocks 1 .. PD-1 after the tokens and scales, so that the first row
+    // block waits for neither of those)
+    __builtin_amdgcn_sched_barrier(0);
+    v4i tok[MTB][8];
+    {
+        const __amdgpu_buffer_rsrc_t tr =
+            make_rsrc(a.q + (int64_t)seg * MTB * 8192, kact ? (uint32_t)(MTB * 8192) : 0u);
+#pragma unroll
+        for (int tb = 0; tb < MTB; ++tb)
+#pragma unroll
+            for (int w = 0; w < 8; ++w)
+                tok[tb][w] = __builtin_bit_cast(
+                    v4i, bload(tr, tb * 16 + (lane & 15) < M ? ((tb * 8 + w) * 64 + lane) * 16 : kOOB));
+    }
+    // the token scales of this lane's epilogue tokens (loaded once, ahead of
+    // the row blocks)
+    float sxv[MTB][4];
+#pragma unroll
+    for (int tb = 0; tb < MTB; ++tb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sxv[tb][v] = a.sx[min(16 * tb + 4 * (lane >> 4) + v, M - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 1; i < PD; ++i) issue(i, buf[i]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. the row blocks.  Each wave's segment sums of a row block go to LDS
+    //    slot i % G right away; after every G row blocks (and the last) one
+    //    barrier (without the workgroup fence, whose release would wait for
+    //    every load in flight), then task (row block i, token block tb) of the
+    //    group goes to wave (task % nw), which adds the nw sums and applies the
+    //    epilogue.  No barrier between the row blocks of a group: each wave
+    //    streams them at its own pace.
+    constexpr int G = MTB == 4 ? (RBW < 4 ? RBW : 4) : RBW;  // row blocks per LDS round
+    const int ncols = a.tr_cols;
+    const bool hi = (lane & 8) != 0;
+    const float csw = Lw.sw;
+    // (every lambda inlined: with RBW = 8 the inliner otherwise kept the row
+    // block body out of line, and the register arrays it captures in scratch)
+    static_for([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        if (i >= nrb) return;  // uniform (and so for every later row block)
+        // (the compiler's waits before the first use of buf[i % PD] count every
+        // vector memory operation issued since)
+        const uint4 X = buf[i % PD][0], Y = buf[i % PD][1];
+        const uint32_t xw[4] = {X.x, X.y, X.z, X.w}, yw[4] = {Y.x, Y.y, Y.z, Y.w};
+        uint32_t wd[8];  // row (lane & 15), dwords 8 kq .. 8 kq + 7 of the segment
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t own = hi ? yw[w] : xw[w];
+            const uint32_t give = hi ? xw[w] : yw[w];
+            const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)give, 0x128, 0xF, 0xF, false);  // row_ror:8
+            wd[w] = hi ? got : own;
+            wd[4 + w] = hi ? own : got;
+        }
+        if (i + PD < RBW) issue(i + PD, buf[i % PD]);
+        v4i acc[MTB];
+#pragma unroll
+        for (int tb = 0; tb < MTB; ++tb) acc[tb] = v4i{0, 0, 0, 0};
+        if (kact) {
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const v4i bv = unpack16(wd[w]);
+#pragma unroll
+                for (int tb = 0; tb < MTB; ++tb)
+                    acc[tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(tok[tb][w], bv, acc[tb], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int tb = 0; tb < MTB; ++tb) red[((wave * G + i % G) * MTB + tb) * 64 + lane] = acc[tb];
+        if (i % G != G - 1 && i != nrb - 1) return;  // uniform: the group goes on
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        constexpr int i0 = i - i % G;
+#pragma unroll
+        for (int tb = 0; tb < MTB; ++tb)
+        for (int ib = 0; ib <= i - i0; ++ib) {  // row block i0 + ib
+            if ((ib * MTB + tb) % nw != wave) continue;  // uniform
+            // D lane l element v: token 16 tb + 4 (l >> 4) + v, row l & 15, so
+            // the 16 lanes of a quarter-wave store 16 consecutive outputs
+            v4i sm = red[(ib * MTB + tb) * 64 + lane];
+            for (int w = 1; w < nw; ++w) sm += red[((w * G + ib) * MTB + tb) * 64 + lane];
+            const int n = (rb0 + i0 + ib) * 16 + (lane & 15);
+            if (n >= N) continue;
+            const int t0 = 16 * tb + 4 * (lane >> 4);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int t = t0 + v;
+                if (t >= M) continue;
+                if (a.splits > 1) {
+                    st_agent((uint32_t*)a.part + ((int64_t)split * M + t) * ncols + Lw.col0 + n, (uint32_t)sm[v]);
+                } else {
+                    const float yv = __fmul_rn((float)sm[v], __fmul_rn(sxv[tb][v], csw));
+                    const int64_t o = (int64_t)t * N + n;
+                    if (a.ykind == YK_BF16) ((uint16_t*)Lw.y)[o] = f32_to_bf16(yv);
+                    else ((float*)Lw.y)[o] = yv;
+                    if (Lw.acc) Lw.acc[o] = sm[v];
+                }
+            }
+        }
+        if (i + 1 < nrb) {  // uniform: the next group writes these slots again
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            __asm__ volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            __asm__ volatile("" ::: "memory");
+        }
+    }, std::make_integer_sequence<int, RBW>{});
+    if (a.splits <= 1) return;
+
+    // 3. K splits: the last split of this row group to arrive adds every
+    //    split's sums (exact int32, any order) and applies the epilogue; its
+    //    counter goes back to zero
+    __shared__ uint32_t s_last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial sums are stored
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(a.ctr + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = old + 1u == (uint32_t)a.splits;
+        if (last) __hip_atomic_fetch_sub(a.ctr + blockIdx.x, (uint32_t)a.splits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const int64_t sstride = (int64_t)M * ncols;
+    const int per = 16 * M;  // outputs of one row block
+    for (int o = tid; o < nrb * per; o += blockDim.x) {
+        const int i = o / per, rem = o - i * per;
+        const int t = rem >> 4;
+        const int n = (rb0 + i) * 16 + (rem & 15);
+        if (n >= N) continue;
+        const uint32_t* p = (const uint32_t*)a.part + (int64_t)t * ncols + Lw.col0 + n;
+        uint32_t pv[kMergeMaxSplits];
+#pragma unroll
+        for (int sp = 0; sp < kMergeMaxSplits; ++sp) pv[sp] = sp < a.splits ? ld_agent(p + sp * sstride) : 0u;
+        int32_t sum = 0;
+#pragma unroll
+        for (int sp = 0; sp < kMergeMaxSplits; ++sp) sum += (int32_t)pv[sp];
+        const float yv = __fmul_rn((float)sum, __fmul_rn(a.sx[t], csw));
+        const int64_t oi = (int64_t)t * N + n;
+        if (a.ykind == YK_BF16) ((uint16_t*)Lw.y)[oi] = f32_to_bf16(yv);
+        else ((float*)Lw.y)[oi] = yv;
+        if (Lw.acc) Lw.acc[oi] = sum;
+    }
+}
+
+TrPlan gemv_tr_plan(int64_t m, int64_t row_blocks, int64_t k, int cus)
+{
+    // waves per CU the kernel's registers allow (MTB 2 and 4: up to 256 VGPRs,
+    // two waves per SIMD; 1: at most 128, four); the row blocks spread so that
+    // every CU holds as many workgroups as that allows, at most 8 row blocks each
+    TrPlan p;
+    p.mtb = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+    const int64_t nseg = (k + kTrSeg - 1) / kTrSeg;
+    p.splits = (int)((nseg + 7) / 8);
+    p.nw = (int)((nseg + p.splits - 1) / p.splits);
+    const int wpc = p.mtb == 1 ? 16 : 8;
+    const int64_t per_cu = wpc / p.nw > 1 ? wpc / p.nw : 1;
+    const int64_t target = (int64_t)(cus > 0 ? cus : 256) * per_cu;
+    int64_t rbpw = (row_blocks * p.splits + target - 1) / target;
+    rbpw = rbpw < 1 ? 1 : (rbpw > 8 ? 8 : rbpw);
+    const int f = knob(KN_GEMV_TR_RBPW);
+    if (f >= 1 && f <= 8) rbpw = f;
+    p.rbpw = (int)rbpw;
+    return p;
+}
+
+hipError_t launch_gemv_tr(const GemmArgs& a, const TrPlan& p, hipStream_t s)
+{
+    // workgroups never cross a layer: layer l owns workgroups tile0 ..
+    // tile0 + ceil(ceil(n / 16) / rbpw) - 1
+    GemmArgs g = a;
+    int64_t groups = 0, cols = 0, rbs = 0;
+    if (p.rbpw < 1) return hipErrorInvalidValue;
+    for (int l = 0; l < g.nl; ++l) {
+        g.L[l].tile0 = (int)groups;
+        g.L[l].col0 = (int)cols;
+        const int64_t rb = (g.L[l].n + 15) / 16;
+        rbs += rb;
+        groups += (rb + p.rbpw - 1) / p.rbpw;
+        cols += g.L[l].n;
+    }
+    if (rbs <= 0 || g.m <= 0) return hipSuccess;
+    const int64_t nseg = ((int64_t)g.k + kTrSeg - 1) / kTrSeg;
+    if (g.m > 16 * p.mtb || (p.mtb != 1 && p.mtb != 2 && p.mtb != 4) || g.nl < 1 || g.nl > kMaxGroup ||
+        g.k % 64 != 0 || g.k > 65536 || p.nw < 1 || p.nw > 8 || p.rbpw < 1 || p.rbpw > 8 || p.splits < 1 ||
+        p.splits > kMergeMaxSplits || (int64_t)p.splits * p.nw < nseg || (int64_t)(p.splits - 1) * p.nw >= nseg ||
+        rbs > INT32_MAX || cols > INT32_MAX ||
+        (p.splits > 1 && (!g.ctr || !g.part || groups > kSplitCounters)))
+        return hipErrorInvalidValue;
+    g.splits = p.splits;
+    g.tr_rbpw = p.rbpw;
+    g.tr_cols = (int)cols;
+    const dim3 grid((unsigned)groups, (unsigned)p.splits), block((unsigned)(p.nw * 64));
+    const int rbw = p.rbpw <= 2 ? 2 : (p.rbpw <= 4 ? 4 : 8);
+    const int grp = p.mtb == 4 && rbw > 4 ? 4 : rbw;  // the kernel's G
+    const size_t lds = (size_t)p.nw * grp * p.mtb * 1024;
+#define BTL_TR(MTV, RBV)                                                                                     \
+    if (p.mtb == MTV && rbw == RBV) {                                                                         \
+        hipLaunchKernelGGL((k_gemv_tr<MTV, RBV, (MTV == 1 ? 4 : 3) < RBV ? (MTV == 1 ? 4 : 3) : RBV>), grid, \
+                           block, lds, s, g);                                                                 \
+        return hipGetLastError();                                                                             \
+    }
+    BTL_TR(1, 2) BTL_TR(1, 4) BTL_TR(1, 8) BTL_TR(2, 2) BTL_TR(2, 4) BTL_TR(2, 8) BTL_TR(4, 2) BTL_TR(4, 4)
+    BTL_TR(4, 8)
+#undef BTL_TR
+    return hipErrorInvalidValue;
 }
 
 // ---------------------------------------------------------------------------

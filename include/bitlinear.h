@@ -114,8 +114,9 @@ int btl_init(int device);
  * "BTL_DEC_RQ_MIN_K", "BTL_DEC_RQ", "BTL_DEC_RQ_DG", "BTL_GEMM_MAX_SPLITS",
  * "BTL_GEMM_WIDE_MIN_TILES", "BTL_WAIT_SPIN", "BTL_ATTN_MERGE", "BTL_SPLIT_MERGE",
  * "BTL_SPLIT_MERGE_MAX_M", "BTL_GEMV_BAT_NW", "BTL_GEMV_BAT_KS", "BTL_GEMM_TILE",
- * "BTL_GEMM_TM64", "BTL_GEMM_TM64_STAGES", "BTL_GEMM_STAGES", "BTL_DEC_RQ2_MAX_K"
- * (the "BTL_" prefix may be left out).  Every route gives the same bits; knobs only choose among kernels and
+ * "BTL_GEMM_TM64", "BTL_GEMM_TM64_STAGES", "BTL_GEMM_STAGES", "BTL_DEC_RQ2_MAX_K",
+ * "BTL_GEMV_TR", "BTL_GEMV_TR_MIN_M", "BTL_GEMV_TR_MAX_M", "BTL_GEMV_TR_RBPW",
+ * "BTL_GEMV_TR_K16" (the "BTL_" prefix may be left out).  Every route gives the same bits; knobs only choose among kernels and
  * launch shapes -- except BTL_WAIT_SPIN, the number of polls after which a
  * kernel's internal wait gives up (2^22 by default; lowering it to force that
  * path is for tests: btl_check_faults then reports it).

@@ -365,6 +365,7 @@ def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, tune):
     # merge: the batched kernel adding its K splits in the launch; bat: the same
     # contraction with a reduce launch after it
     print("split-k", route, m, k, n, xdt, ydt, flush=True)
+    tune("BTL_GEMV_TR", 0)  # the token-register kernel has tests of its own
     if route == "gemm":
         tune("BTL_GEMV_BAT", "0")
     else:
@@ -383,6 +384,65 @@ def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, tune):
         assert_bf16_matches(y, yr)
 
 
+# the token-register batched decode kernel (k_gemv_tr, 3..64 token rows): one
+# K split (k <= 4096), several (k = 8192: 2, 14336: 4, merged in the launch), a
+# last K segment that ends inside its 512 weights (k = 1088, 576), ragged n; 16,
+# 32 and 64 token columns per wave (m = 3 / 16, 17 / 32, 33 / 64); the row blocks
+# per workgroup forced to 1, 3 (a workgroup with fewer blocks than its template
+# holds) and 8, or the rule (0)
+TR_SHAPES = [(4096, 300), (14336, 200), (1088, 70), (576, 33), (8192, 1000)]
+
+
+def tr_everywhere(tune):
+    # the token-register kernel for every m in 3..64 and every k (the routing
+    # rule sends it only the shapes where it measured faster)
+    tune("BTL_GEMV_TR", 1)
+    tune("BTL_GEMV_TR_MIN_M", 3)
+    tune("BTL_GEMV_TR_MAX_M", 64)
+    tune("BTL_GEMV_TR_K16", 0)
+
+
+@pytest.mark.parametrize("m", [3, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("k,n", TR_SHAPES)
+@pytest.mark.parametrize("rbpw", [0, 1, 3, 8])
+def test_token_register_kernel_matches_oracle(m, k, n, rbpw, tune):
+    print("token-register", m, k, n, rbpw, flush=True)
+    tr_everywhere(tune)
+    tune("BTL_GEMV_TR_RBPW", rbpw)
+    xdt, ydt = (torch.bfloat16, torch.bfloat16) if (m + k + rbpw) % 2 else (torch.float32, torch.float32)
+    x = activations(m, k, seed=7 * m + k + n)
+    pt, wb, sw = make_layer(n, k, seed=n * 5 + k)
+    xt = to_dev(x, xdt)
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    y = bl.BitLinearHip.forward(xt, pt, out_dtype=ydt, acc_out=acc)
+    yr, _, _, accr = orc.forward_i8(host_x(xt), wb, n, sw)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    if ydt == torch.float32:
+        assert_f32_identical(y, yr)
+    else:
+        assert_bf16_matches(y, yr)
+
+
+@pytest.mark.parametrize("m,k,ns", [(64, 4096, (14336, 14336)), (24, 4096, (300, 130, 4096)), (48, 14336, (4096,)),
+                                    (5, 2048, (100, 2000, 50, 7))])
+def test_token_register_kernel_groups(m, k, ns, tune):
+    # grouped layers (row blocks of a workgroup can cross a layer boundary): every
+    # output against the oracle of its own layer; the Llama-3-8B MLP shapes at m = 64
+    print("token-register group", m, k, ns, flush=True)
+    tr_everywhere(tune)
+    xt = to_dev(activations(m, k, seed=m + 3 * k), torch.bfloat16)
+    layers = [make_layer(n, k, seed=n + 11 * i) for i, n in enumerate(ns)]
+    outs = bl.linear_group([l[0] for l in layers], xt, out_dtype=torch.float32)
+    xh = host_x(xt)
+    for (pt, wb, sw), y in zip(layers, outs):
+        n = pt.shape[0]
+        if n * m * k > 2e9:  # the oracle on sampled token rows
+            rows = [0, m // 2, m - 1]
+            assert_f32_identical(y[rows], orc.forward_i8(xh[rows], wb, n, sw)[0])
+        else:
+            assert_f32_identical(y, orc.forward_i8(xh, wb, n, sw)[0])
+
+
 # 21..64 token rows on a layer group of at least 192 tiles of 128 rows: the
 # GEMM's 64-token tiles, unsplit, 4 LDS stages (steady loop of 4 steps + tail).
 # k = 1088: 9 steps, the last one half; k = 4096: 32 steps; n ragged.  Checked
@@ -391,6 +451,7 @@ def test_split_k_matches_oracle(m, k, n, xdt, ydt, route, tune):
 @pytest.mark.parametrize("m,k,ns", [(24, 1088, (24576 + 70,)), (64, 4096, (14336, 14336)), (40, 2048, (12288, 12288 + 130))])
 def test_small_m_gemm_unsplit_stages(m, k, ns, tune):
     print("small-m gemm", m, k, ns, flush=True)
+    tune("BTL_GEMV_TR", 0)
     x = to_dev(activations(m, k, seed=m + k), torch.bfloat16)
     layers = [make_layer(n, k, seed=n + 7 * i) for i, n in enumerate(ns)]
 
@@ -421,6 +482,7 @@ def test_small_m_gemm_unsplit_stages(m, k, ns, tune):
 def test_small_m_gemm_split_forms(m, k, n, stages, tile, tune):
     print("small-m gemm split", m, k, n, stages, tile, flush=True)
     tune("BTL_GEMV_BAT", 0)
+    tune("BTL_GEMV_TR", 0)
     x = to_dev(activations(m, k, seed=3 * m + k), torch.bfloat16)
     pt, wb, sw = make_layer(n, k, seed=n + k)
     tune("BTL_GEMM_TM64", 0)
@@ -1047,11 +1109,17 @@ def test_group_f32_ref_bitexact(m, k, ns, xdt):
         assert torch.equal(y, bl.BitLinearHip.forward(xt, pt, mode="f32_ref", out_dtype=torch.float32))
 
 
-def test_batched_merge_counters_and_graph_replays(tune):
+@pytest.mark.parametrize("kernel", ["bat", "tr"])
+def test_batched_merge_counters_and_graph_replays(kernel, tune):
     # the in-launch split merge keeps its counters per workspace and every launch
     # leaves them at zero: calls of different m and K splits on one workspace, then
     # a captured call replayed with eager calls in between, all bit for bit
-    print("split merge counters / graph", flush=True)
+    # (k_gemv_bat, or the token-register kernel: 4 K splits at k = 14336)
+    print("split merge counters / graph", kernel, flush=True)
+    if kernel == "tr":
+        tr_everywhere(tune)
+    else:
+        tune("BTL_GEMV_TR", 0)
     tune("BTL_GEMV_BAT_MAX_M", "64")
     tune("BTL_SPLIT_MERGE", 1)
     k, n = 14336, 384
