@@ -12,8 +12,9 @@
 //                    cache rows at their positions.  One wave per (token, head).
 //   k_attn_part      attention of a block of queries against one 64-key chunk of
 //                    one KV head: the chunk is dequantised once into LDS, each
-//                    wave is one query head of the GQA group.  Writes the chunk's
-//                    (max, sum, weighted values) per query and head.
+//                    wave takes one (query, head of the GQA group) pair at a
+//                    time.  Writes the chunk's (max, sum, weighted values) per
+//                    query and head.
 //   k_attn_combine   merges the chunk partials of each (query, head).
 //   k_embed          token ids -> f32 rows of the embedding table.
 //   k_rmsnorm_f32    RMSNorm of f32 rows (+ a residual) into f32 rows.
@@ -130,23 +131,28 @@ hipError_t launch_rope_kv_q8(const KvArgs& a, hipStream_t st)
 // ---------------------------------------------------------------------------
 // k_attn_part: one 64-key chunk of one KV head against a block of queries
 // ---------------------------------------------------------------------------
-// grid (nkv, cmax, ceil(m / qb)), block 64 * rep (rep = nh / nkv query heads
-// share the KV head, repeat_kv attention.rs:227-239).  Query i sits at
-// position pos0 + i and sees keys [0, pos0 + i] (the causal mask of
-// attention.rs:245-270; a single decode query sees the whole cache).
+// grid (nkv, cmax, ceil(m / qb)), block 64 * rep * qw (rep = nh / nkv query
+// heads share the KV head, repeat_kv attention.rs:227-239; qw queries of the
+// block at a time, rep * qw <= 16 waves).  Query i sits at position pos0 + i
+// and sees keys [0, pos0 + i] (the causal mask of attention.rs:245-270; a
+// single decode query sees the whole cache).  Wave w takes query head w % rep
+// of query w / rep of each pass; every (query, head) is one wave's pass over
+// the chunk, so the bits do not depend on qw.
 //   chunk keys dequantised once: kd = ((f32)code - 128) * s (kv_cache.rs:122-128)
-//   s_j   = (sum_d q[d] * kd[j][d], sequential over d) * scal      (lane j)
+//   s_j   = (fma chain over d of q[d] * kd[j][d]) * scal            (lane j)
 //   m_c   = max_j s_j;  p_j = exp(s_j - m_c);  l_c = pairwise sum over the lanes
-//   o_c[d] = sum_j p_j * vd[j][d], sequential over j                (lane: d)
+//   o_c[d] = fma chain over j of p_j * vd[j][d]                     (lane: d)
 constexpr int kAttnChunk = 64;
 constexpr int kAttnMaxHd = 128;
 constexpr int kAttnMaxRep = 16;
 constexpr int kAttnKs = kAttnMaxHd + 4;  // LDS key row stride (floats): 16-byte rows, conflict-free b128 reads
 
 // One query of one head against the staged chunk (nj valid keys):
-//   s_j   = (sum_d q[d] * kd[j][d], sequential over d) * scal      (lane j)
+//   s_j   = (fma chain over d of q[d] * kd[j][d]) * scal            (lane j)
 //   m_c   = max_j s_j;  p_j = exp(s_j - m_c);  l_c = pairwise sum over the lanes
-//   o_c[d] = sum_j p_j * vd[j][d], sequential over j                (lanes: d, d + 64)
+//   o_c[d] = fma chain over j of p_j * vd[j][d]                     (lanes: d, d + 64)
+// (an fma chain: acc = fma(a_i, b_i, acc) in index order from 0, one rounding
+// per term, half the dependent instructions of a multiply and an add)
 // and (m_c, l_c, o_c) to part.  Called by every thread of the workgroup (it
 // holds a barrier); sq / sp are this wave's rows of s_q / s_p.
 // a partial-sum store: plain, or coherent at agent scope (sc1, written through
@@ -161,7 +167,7 @@ __device__ __forceinline__ void put_part(float* p, float v)
 template <int HD, bool SC1 = false>
 __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], const float (*s_v)[kAttnMaxHd],
                                                  const float* sq, float* sp, int nj, int hd_rt, float scal, int lane,
-                                                 float* part)
+                                                 float* part, bool store = true)
 {
     const int hd = HD ? HD : hd_rt;  // HD > 0: the loops unroll and the LDS reads batch
     float sc = -__builtin_inff();
@@ -172,13 +178,13 @@ __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], co
             for (int d = 0; d < hd; d += 4) {
                 const float4 q4 = *(const float4*)&sq[d];
                 const float4 k4 = *(const float4*)&s_k[lane][d];
-                acc = __fadd_rn(acc, __fmul_rn(q4.x, k4.x));
-                acc = __fadd_rn(acc, __fmul_rn(q4.y, k4.y));
-                acc = __fadd_rn(acc, __fmul_rn(q4.z, k4.z));
-                acc = __fadd_rn(acc, __fmul_rn(q4.w, k4.w));
+                acc = __fmaf_rn(q4.x, k4.x, acc);
+                acc = __fmaf_rn(q4.y, k4.y, acc);
+                acc = __fmaf_rn(q4.z, k4.z, acc);
+                acc = __fmaf_rn(q4.w, k4.w, acc);
             }
         } else {
-            for (int d = 0; d < hd; ++d) acc = __fadd_rn(acc, __fmul_rn(sq[d], s_k[lane][d]));
+            for (int d = 0; d < hd; ++d) acc = __fmaf_rn(sq[d], s_k[lane][d], acc);
         }
         sc = __fadd_rn(__fmul_rn(acc, scal), 0.0f);  // candle affine(scal, 0)
     }
@@ -196,14 +202,14 @@ __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], co
         const float4 p4 = *(const float4*)&sp[jj];
         const float a0 = s_v[jj][c0], a1 = s_v[jj + 1][c0], a2 = s_v[jj + 2][c0], a3 = s_v[jj + 3][c0];
         const float b0 = s_v[jj][c1], b1 = s_v[jj + 1][c1], b2 = s_v[jj + 2][c1], b3 = s_v[jj + 3][c1];
-        o0 = __fadd_rn(o0, __fmul_rn(p4.x, a0));
-        o0 = __fadd_rn(o0, __fmul_rn(p4.y, a1));
-        o0 = __fadd_rn(o0, __fmul_rn(p4.z, a2));
-        o0 = __fadd_rn(o0, __fmul_rn(p4.w, a3));
-        o1 = __fadd_rn(o1, __fmul_rn(p4.x, b0));
-        o1 = __fadd_rn(o1, __fmul_rn(p4.y, b1));
-        o1 = __fadd_rn(o1, __fmul_rn(p4.z, b2));
-        o1 = __fadd_rn(o1, __fmul_rn(p4.w, b3));
+        o0 = __fmaf_rn(p4.x, a0, o0);
+        o0 = __fmaf_rn(p4.y, a1, o0);
+        o0 = __fmaf_rn(p4.z, a2, o0);
+        o0 = __fmaf_rn(p4.w, a3, o0);
+        o1 = __fmaf_rn(p4.x, b0, o1);
+        o1 = __fmaf_rn(p4.y, b1, o1);
+        o1 = __fmaf_rn(p4.z, b2, o1);
+        o1 = __fmaf_rn(p4.w, b3, o1);
     };
     if (HD != 0 && nj == kAttnChunk) {
         // a full chunk: unrolled, so the LDS reads of later keys issue ahead of
@@ -216,9 +222,10 @@ __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], co
     }
     for (; j < nj; ++j) {
         const float pj = sp[j];
-        o0 = __fadd_rn(o0, __fmul_rn(pj, s_v[j][c0]));
-        o1 = __fadd_rn(o1, __fmul_rn(pj, s_v[j][c1]));
+        o0 = __fmaf_rn(pj, s_v[j][c0], o0);
+        o1 = __fmaf_rn(pj, s_v[j][c1], o1);
     }
+    if (!store) return;  // a wave without a query this pass (it still met the barrier)
     if (h0) put_part<SC1>(&part[2 + d0], o0);
     if (h1) put_part<SC1>(&part[2 + d1], o1);
     if (lane == 0) {
@@ -238,7 +245,9 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nthr = blockDim.x;
     const int hd = HD ? HD : a.hd, rep = a.nh / a.nkv;  // HD > 0: launched for a.hd == HD
-    const int h = g * rep + wave;
+    const int qw = nthr / (64 * rep);                   // queries per pass
+    const int hw = wave % rep, qs = wave / rep;         // this wave's head and query slot
+    const int h = g * rep + hw;
     const int pos0 = a.d_pos ? *a.d_pos : a.pos;
     const int i_begin = blockIdx.z * a.qb;
     const int i_end = min(a.m, i_begin + a.qb);
@@ -300,16 +309,21 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
         }
     }
 
-    for (int i = i_begin; i < i_end; ++i) {
-        const int T = min(pos0 + i + 1, a.max_seq);
-        if (j0 >= T) continue;  // uniform
-        const int nj = min(kAttnChunk, T - j0);
-        const float* qg = a.q + ((int64_t)i * a.nh + h) * hd;
-        for (int d = lane; d < hd; d += 64) s_q[wave][d] = qg[d];
+    for (int i0 = i_begin; i0 < i_end; i0 += qw) {
+        // the last query of the pass sees the most keys (uniform)
+        if (j0 >= min(pos0 + min(i0 + qw, i_end), a.max_seq)) continue;
+        const int i = i0 + qs;
+        const int T = i < i_end ? min(pos0 + i + 1, a.max_seq) : 0;
+        const bool act = j0 < T;  // uniform per wave; an idle wave still meets the barriers
+        const int nj = act ? min(kAttnChunk, T - j0) : 0;
+        if (act) {
+            const float* qg = a.q + ((int64_t)i * a.nh + h) * hd;
+            for (int d = lane; d < hd; d += 64) s_q[wave][d] = qg[d];
+        }
         __syncthreads();
-        float* part = a.part + (((int64_t)i * a.nh + h) * a.cmax + c) * (hd + 2);
-        attn_chunk_query<HD>(s_k, s_v, s_q[wave], s_p[wave], nj, hd, a.scal, lane, part);
-        __syncthreads();  // s_q / s_p are rewritten by the next query
+        float* part = a.part + (((int64_t)(act ? i : 0) * a.nh + h) * a.cmax + c) * (hd + 2);
+        attn_chunk_query<HD>(s_k, s_v, s_q[wave], s_p[wave], nj, hd, a.scal, lane, part, act);
+        __syncthreads();  // s_q / s_p are rewritten by the next pass
     }
 }
 
@@ -625,7 +639,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st)
         a.cmax < 1)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)a.nkv, (unsigned)a.cmax, (unsigned)((a.m + a.qb - 1) / a.qb));
-    const dim3 block((unsigned)(64 * rep));
+    // qw queries of a block at a time (measured on MI355X, Llama-3-8B prefill of
+    // 512 tokens: 153 us per layer with one query at a time)
+    const int qw = std::max(1, std::min(kAttnMaxRep / rep, a.qb));
+    const dim3 block((unsigned)(64 * rep * qw));
     if (a.hd == 128) hipLaunchKernelGGL(k_attn_part<128>, grid, block, 0, st, a);
     else if (a.hd == 64) hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, a);
     else hipLaunchKernelGGL(k_attn_part<0>, grid, block, 0, st, a);

@@ -29,10 +29,12 @@
  *                    (repeat_kv, :227-239).  The reference's sums run in candle's
  *                    gemm order (not vendored); this restatement fixes the order
  *                    the GPU kernels use, so the two agree bit for bit:
- *                      dot(q, k_j) sequential over d, scaled by (f32)(1/sqrt(hd));
+ *                      dot(q, k_j) = orc_attn_dot: one fused multiply-add per
+ *                      term, sequential over d (acc = fma(q[d], k_j[d], acc)),
+ *                      scaled by (f32)(1/sqrt(hd));
  *                      keys in chunks of 64: m_c = max, p_j = exp(s_j - m_c),
  *                      l_c = pairwise tree over the 64 lanes (zero-padded),
- *                      o_c[d] = sum_j p_j * v_j[d] sequential over j;
+ *                      o_c[d] = the same fma chain over j of p_j * v_j[d];
  *                      M = max_c m_c, w_c = exp(m_c - M), L = sum_c w_c * l_c,
  *                      O[d] = sum_c w_c * o_c[d] (sequential over c), y = O / L.
  *                    exp is orc_expf (bitlinear_oracle.c).  tests/test_model_oracle.py
@@ -115,6 +117,15 @@ void orc_q8_dequant(const uint8_t* q, int64_t hd, float s, float* out)
 
 #define ORC_CHUNK 64
 
+/* The dot product of the attention scores and value sums: one fused
+ * multiply-add per term (a single rounding), sequential over the terms. */
+float orc_attn_dot(const float* a, const float* b, int64_t n, int64_t stride_b)
+{
+    float acc = 0.0f;
+    for (int64_t i = 0; i < n; ++i) acc = fmaf(a[i], b[i * stride_b], acc);
+    return acc;
+}
+
 /* q: [nh * hd] (rotated); cache arrays of ONE layer: kq/vq [nkv][max_seq][hd],
  * ks/vs [nkv][max_seq]; keys [0, T).  out: [nh * hd]. */
 void orc_attn_decode(const float* q, const uint8_t* kq, const float* ks, const uint8_t* vq, const float* vs,
@@ -127,6 +138,7 @@ void orc_attn_decode(const float* q, const uint8_t* kq, const float* ks, const u
     float* lc = (float*)malloc(sizeof(float) * (size_t)(C + 1));
     float* oc = (float*)malloc(sizeof(float) * (size_t)((C + 1) * hd));
     float* kd = (float*)malloc(sizeof(float) * (size_t)hd);
+    float* vdq = (float*)malloc(sizeof(float) * (size_t)(ORC_CHUNK * hd));
     float sc[ORC_CHUNK], p[ORC_CHUNK];
     for (int64_t h = 0; h < nh; ++h) {
         const int64_t g = h / rep;
@@ -138,23 +150,18 @@ void orc_attn_decode(const float* q, const uint8_t* kq, const float* ks, const u
             for (int64_t j = 0; j < nj; ++j) {
                 const int64_t row = g * max_seq + j0 + j;
                 orc_q8_dequant(kq + row * hd, hd, ks[row], kd);
-                float acc = 0.0f;
-                for (int64_t d = 0; d < hd; ++d) acc = acc + qh[d] * kd[d];
+                const float acc = orc_attn_dot(qh, kd, hd, 1);
                 sc[j] = acc * scal + 0.0f; /* candle affine(mul, add): v * mul + add */
                 if (sc[j] > m) m = sc[j];
             }
             for (int64_t j = 0; j < ORC_CHUNK; ++j) p[j] = j < nj ? orc_expf(sc[j] - m) : 0.0f;
             mc[c] = m;
             lc[c] = orc_pairwise_sum(p, ORC_CHUNK);
-            for (int64_t d = 0; d < hd; ++d) {
-                float acc = 0.0f;
-                for (int64_t j = 0; j < nj; ++j) {
-                    const int64_t row = g * max_seq + j0 + j;
-                    const float vd = ((float)vq[row * hd + d] - 128.0f) * vs[row];
-                    acc = acc + p[j] * vd;
-                }
-                oc[c * hd + d] = acc;
+            for (int64_t j = 0; j < nj; ++j) {
+                const int64_t row = g * max_seq + j0 + j;
+                orc_q8_dequant(vq + row * hd, hd, vs[row], vdq + j * hd);
             }
+            for (int64_t d = 0; d < hd; ++d) oc[c * hd + d] = orc_attn_dot(p, vdq + d, nj, hd);
         }
         float M = -INFINITY;
         for (int64_t c = 0; c < C; ++c)
@@ -171,6 +178,7 @@ void orc_attn_decode(const float* q, const uint8_t* kq, const float* ks, const u
     free(lc);
     free(oc);
     free(kd);
+    free(vdq);
 }
 
 int64_t orc_argmax(const float* x, int64_t n)

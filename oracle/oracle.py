@@ -45,6 +45,7 @@ def _load():
         "orc_q8_quant": (None, [vp, i64, vp, vp]),
         "orc_q8_dequant": (None, [vp, i64, f32, vp]),
         "orc_attn_decode": (None, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp]),
+        "orc_attn_dot": (ctypes.c_float, [vp, vp, i64, i64]),
         "orc_argmax": (i64, [vp, i64]),
         "orc_dense_linear": (None, [vp, i64, i64, vp, i32, i64, vp]),
         "orc_adaptive_reconstruct": (None, [vp, vp, i64, i64, i64, vp]),
@@ -266,6 +267,13 @@ def attn_decode(q, kq, ks, vq, vs, n_heads, T):
     out = np.zeros((n_heads * hd,), dtype=np.float32)
     lib.orc_attn_decode(_p(q), _p(kq), _p(ks), _p(vq), _p(vs), n_heads, nkv, hd, max_seq, T, _p(out))
     return out
+
+
+def attn_dot(a, b):
+    """The attention's dot product: acc = fma(a[i], b[i], acc), sequential, from 0."""
+    a, b = _f32(a).reshape(-1), _f32(b).reshape(-1)
+    assert a.size == b.size
+    return np.float32(lib.orc_attn_dot(_p(a), _p(b), a.size, 1))
 
 
 def dense_linear(x, w):

@@ -24,7 +24,13 @@ What pins each function (reference = imonoonoko/Bit-TTT-Engine, crates/rust_engi
                     at chunk boundaries T = 1, 63, 64, 65, 129; per-head planted values
                     that a wrong head map (h % nkv instead of h // rep) gets wrong.
                     The reference's own summation order (candle gemm) is not vendored:
-                    its last ulps are parity unpinned (tolerance above).
+                    its last ulps are parity unpinned (tolerance above).  The fixed order
+                    (orc_attn_dot: a sequential chain of fused multiply-adds for every
+                    score and value sum) is pinned by known answers: a term whose
+                    product is inexact (an fma and a multiply-then-add differ), a
+                    cancelling sequence (the sequential order and the reversed one
+                    differ), and a two-key attention whose output carries the score's
+                    fma bit.
   orc_argmax        Iterator::max_by semantics: the last of equal maxima.
   orc_dense_linear  candle_nn::Linear::forward (the dense lm_head, llama.rs:129-141):
                     exact integer-valued products and sums (no dropped term, no
@@ -196,6 +202,50 @@ def test_attn_decode_matches_float64(T, nh, nkv, hd):
     e = _attn64(q, kq, ks, vq, vs, nh, T)
     scale = np.abs(e).reshape(nh, hd).max(1, keepdims=True)
     assert np.all(np.abs(y.reshape(nh, hd) - e.reshape(nh, hd)) <= 2e-6 * scale + 1e-30)
+
+
+def test_attn_dot_is_a_sequential_fma_chain():
+    # s = 2 (1 + 2^-12): the product s * s = 4 + 2^-9 + 2^-22 is not a float; after
+    # -2 s the fma keeps the 2^-22 (2^-10 + 2^-22 exactly), a rounded multiply then
+    # an add gives 2^-10 (the product's tie rounds to 4 + 2^-9)
+    sv = np.float32(2.0 * (1.0 + 2.0 ** -12))
+    got = orc.attn_dot([-2.0, sv], [sv, sv])
+    assert got == np.float32(2.0 ** -10 + 2.0 ** -22), got
+    mul_add = np.float32(np.float32(-2.0 * sv) + np.float32(sv * sv))
+    assert mul_add == np.float32(2.0 ** -10) and mul_add != got
+    # sequential in index order: 2^24 + 1 rounds back to 2^24, so the sum is 0; the
+    # reversed order keeps the 1
+    assert orc.attn_dot([2.0 ** 24, 1.0, -2.0 ** 24], [1.0, 1.0, 1.0]) == 0.0
+    assert orc.attn_dot([-2.0 ** 24, 1.0, 2.0 ** 24], [1.0, 1.0, 1.0]) == 1.0
+    # from zero: a single term is the rounded product
+    assert orc.attn_dot([3.0], [1.0 / 3.0]) == np.float32(3.0 * np.float32(1.0 / 3.0))
+
+
+def test_attn_decode_scores_use_the_fma_chain():
+    # key 0 = [s, s] (codes 129, scale s = 64 + 2^-6) against q = [-64, s]: -64 s = -4097
+    # exactly, s * s = 4098 + 2^-12 is not a float (it rounds to 4098), so the fma chain
+    # scores 1 + 2^-12 and a multiply-then-add 1.  Key 1 is zero; values 1 and 0 give
+    # y = 1 / (1 + exp(-scal * s0)): the two scores differ in y by a relative 5.7e-5,
+    # far above the exp's rounding
+    hd, S, T = 2, 4, 2
+    sv = np.float32(64.0 + 2.0 ** -6)
+    kq = np.full((1, S, hd), 128, np.uint8)
+    kq[0, 0] = 129
+    ks = np.full((1, S), sv, np.float32)
+    vq = np.full((1, S, hd), 128, np.uint8)
+    vq[0, 0] = 129
+    vs = np.ones((1, S), np.float32)
+    q = np.array([-64.0, sv], np.float32)
+    assert np.float32(-64.0 * sv) == -4097.0 and np.float32(sv * sv) == 4098.0
+    y = orc.attn_decode(q, kq, ks, vq, vs, 1, T).astype(np.float64)
+    scal = np.float32(1.0 / np.sqrt(2.0))
+
+    def expect(s0):
+        return 1.0 / (1.0 + np.exp(-float(np.float32(np.float32(s0) * scal))))
+
+    e_fma, e_mul_add = expect(1.0 + 2.0 ** -12), expect(1.0)
+    assert np.all(np.abs(y - e_fma) <= 1e-6 * e_fma), (y, e_fma)
+    assert np.all(np.abs(y - e_mul_add) > 3e-5 * e_mul_add), (y, e_mul_add)
 
 
 def test_attn_decode_score_order_known_answer():
