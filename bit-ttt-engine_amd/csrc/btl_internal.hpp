@@ -201,6 +201,10 @@ struct GemmArgs {
 };
 
 constexpr int kGemmSplitTarget = 512;  // workgroups a split-K launch aims for
+// above 64 token rows, K is split only from this k on, for at most this many
+// 128 x 128 output tiles
+constexpr int kGemmSplitMinK = 8192;
+constexpr int kGemmSplitMaxTiles = 128;
 // up to 64 token rows, a GEMM of at least this many 128-row tiles runs unsplit
 // (64-token tiles, 4 LDS stages; measured on MI355X, Llama-3-8B gate|up at
 // m = 24..64: 19-21 us against 31 split three ways)

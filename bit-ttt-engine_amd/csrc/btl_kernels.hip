@@ -1771,6 +1771,14 @@ int gemm_splits(int64_t m, int64_t tiles_n, int64_t k, int* split_steps)
     }
     const int64_t tiles = (m + kGemmBM - 1) / kGemmBM * tiles_n;
     int64_t s = tiles >= kGemmSplitTarget || tiles <= 0 ? 1 : (kGemmSplitTarget + tiles - 1) / tiles;
+    // Above 64 token rows a split pays only for long K on few tiles: its partial
+    // sums and reduce launch cost more than the idle CUs of an unsplit launch
+    // (measured on MI355X, Llama-3-8B calls with their quantiser, us split /
+    // unsplit: q|k|v at m = 128 29.8 / 22.4, at 512 41.7 / 25.4; gate|up at 65
+    // 37.0 / 28.5; o at 65 24.0 / 25.5, at 128 29.0 / 22.0; down (k = 14336, 32
+    // tiles per 128 rows) at 65 28.8 / 60.0, at 512 56.0 / 60.5, at 1024 (256
+    // tiles) 85.2 / 69.1)
+    if (m > 64 && (k < kGemmSplitMinK || tiles > kGemmSplitMaxTiles)) s = 1;
     const int cap = knob(KN_GEMM_MAX_SPLITS);  // tuning / tests: 1 turns split-K off
     if (cap >= 1 && s > cap) s = cap;
     if (s > steps / 2) s = steps / 2;  // at least two K steps per split

@@ -353,9 +353,11 @@ def test_decode_row_group_form_prequantized(k, tune):
 # batched decode / small prefill: k_gemv_bat (m <= 64) and the GEMM, both with
 # K split over workgroups.  (m, k, n): many splits; a K range past k; a half
 # last GEMM step; m = 2..4 where the decode kernel does not fit k = 14336;
-# exactly one 128-row tile; 17..32 and 33..64 token rows (2 and 4 B blocks)
+# exactly one 128-row tile (unsplit above 64 rows at this k); 17..32 and 33..64
+# token rows (2 and 4 B blocks); above 64 rows a long K on few tiles (split,
+# a half last step)
 SPLIT_SHAPES = [(16, 14336, 256), (5, 4096, 300), (64, 1088, 1000), (2, 14336, 130), (4, 14336, 64),
-                (128, 2048, 130), (33, 256, 64), (20, 192, 70), (48, 8192, 200)]
+                (128, 2048, 130), (33, 256, 64), (20, 192, 70), (48, 8192, 200), (130, 8256, 300)]
 
 
 @pytest.mark.parametrize("route", ["merge", "bat", "gemm"])
