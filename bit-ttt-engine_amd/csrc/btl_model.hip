@@ -234,30 +234,13 @@ __device__ __forceinline__ void attn_chunk_query(const float (*s_k)[kAttnKs], co
     }
 }
 
+// Dequantise rows [j0, j0 + nstage) of KV head g's cache into LDS (every
+// thread of the workgroup takes part): kd = ((f32)code - 128) * s
+// (kv_cache.rs:122-128).
 template <int HD>
-__global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
+__device__ __forceinline__ void attn_stage_chunk(const AttnArgs& a, int g, int j0, int nstage, int hd,
+                                                 float (*s_k)[kAttnKs], float (*s_v)[kAttnMaxHd], int tid, int nthr)
 {
-    __shared__ __align__(16) float s_k[kAttnChunk][kAttnKs];
-    __shared__ __align__(16) float s_v[kAttnChunk][kAttnMaxHd];
-    __shared__ __align__(16) float s_q[kAttnMaxRep][kAttnMaxHd];
-    __shared__ __align__(16) float s_p[kAttnMaxRep][kAttnChunk];
-    const int g = blockIdx.x, c = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nthr = blockDim.x;
-    const int hd = HD ? HD : a.hd, rep = a.nh / a.nkv;  // HD > 0: launched for a.hd == HD
-    const int qw = nthr / (64 * rep);                   // queries per pass
-    const int hw = wave % rep, qs = wave / rep;         // this wave's head and query slot
-    const int h = g * rep + hw;
-    const int pos0 = a.d_pos ? *a.d_pos : a.pos;
-    const int i_begin = blockIdx.z * a.qb;
-    const int i_end = min(a.m, i_begin + a.qb);
-    const int j0 = c * kAttnChunk;
-    const int t_last = min(pos0 + i_end, a.max_seq);  // keys any query of the block sees
-    if (j0 >= t_last) return;                           // uniform
-    const int nstage = min(kAttnChunk, t_last - j0);
-
-    // dequantise the chunk's keys and values into LDS:
-    // kd = ((f32)code - 128) * s (kv_cache.rs:122-128)
     const int64_t base = (int64_t)g * a.max_seq + j0;
     if ((hd & 15) == 0) {
         // 16-byte loads, all in flight before the first conversion
@@ -309,6 +292,32 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
         }
     }
 
+}
+
+template <int HD>
+__global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
+{
+    __shared__ __align__(16) float s_k[kAttnChunk][kAttnKs];
+    __shared__ __align__(16) float s_v[kAttnChunk][kAttnMaxHd];
+    __shared__ __align__(16) float s_q[kAttnMaxRep][kAttnMaxHd];
+    __shared__ __align__(16) float s_p[kAttnMaxRep][kAttnChunk];
+    const int g = blockIdx.x, c = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = blockDim.x;
+    const int hd = HD ? HD : a.hd, rep = a.nh / a.nkv;  // HD > 0: launched for a.hd == HD
+    const int qw = nthr / (64 * rep);                   // queries per pass
+    const int hw = wave % rep, qs = wave / rep;         // this wave's head and query slot
+    const int h = g * rep + hw;
+    const int pos0 = a.d_pos ? *a.d_pos : a.pos;
+    const int i_begin = blockIdx.z * a.qb;
+    const int i_end = min(a.m, i_begin + a.qb);
+    const int j0 = c * kAttnChunk;
+    const int t_last = min(pos0 + i_end, a.max_seq);  // keys any query of the block sees
+    if (j0 >= t_last) return;                           // uniform
+    const int nstage = min(kAttnChunk, t_last - j0);
+
+    attn_stage_chunk<HD>(a, g, j0, nstage, hd, s_k, s_v, tid, nthr);
+
     for (int i0 = i_begin; i0 < i_end; i0 += qw) {
         // the last query of the pass sees the most keys (uniform)
         if (j0 >= min(pos0 + min(i0 + qw, i_end), a.max_seq)) continue;
@@ -323,6 +332,143 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
         __syncthreads();
         float* part = a.part + (((int64_t)(act ? i : 0) * a.nh + h) * a.cmax + c) * (hd + 2);
         attn_chunk_query<HD>(s_k, s_v, s_q[wave], s_p[wave], nj, hd, a.scal, lane, part, act);
+        __syncthreads();  // s_q / s_p are rewritten by the next pass
+    }
+}
+
+// k_attn_part with the G = rep query heads of a KV head in one wave: wave w
+// takes query w of each pass and every head of the group, so each dequantised
+// key and value element is read from LDS once per group instead of once per
+// head (the partials of a long prompt were bound by those reads).  Per
+// (query, head) the arithmetic is attn_chunk_query's, in the same order.
+template <int HD, int G>
+__device__ __forceinline__ void attn_chunk_query_g(const float (*s_k)[kAttnKs], const float (*s_v)[kAttnMaxHd],
+                                                   const float (*sq)[kAttnMaxHd], float (*sp)[kAttnChunk], int nj,
+                                                   float scal, int lane, float* part, int64_t hstride, bool store)
+{
+    static_assert(HD == 64 || HD == 128, "head size 64 or 128");
+    float sc[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) sc[gg] = -__builtin_inff();
+    if (lane < nj) {
+        float acc[G];
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) acc[gg] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < HD; d += 4) {
+            const float4 k4 = *(const float4*)&s_k[lane][d];
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+                const float4 q4 = *(const float4*)&sq[gg][d];
+                acc[gg] = __fmaf_rn(q4.x, k4.x, acc[gg]);
+                acc[gg] = __fmaf_rn(q4.y, k4.y, acc[gg]);
+                acc[gg] = __fmaf_rn(q4.z, k4.z, acc[gg]);
+                acc[gg] = __fmaf_rn(q4.w, k4.w, acc[gg]);
+            }
+        }
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) sc[gg] = __fadd_rn(__fmul_rn(acc[gg], scal), 0.0f);  // candle affine(scal, 0)
+    }
+    float mc[G], lc[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+        mc[gg] = wave_max_f32(sc[gg]);
+        const float p = lane < nj ? btl_expf(__fsub_rn(sc[gg], mc[gg])) : 0.0f;
+        lc[gg] = wave_pairwise_sum(p);
+        sp[gg][lane] = p;
+    }
+    __syncthreads();
+    const int d0 = lane, d1 = lane + 64;
+    const bool h1 = d1 < HD;
+    const int c1 = h1 ? d1 : 0;  // clamped column (values unused when out of range)
+    float o0[G], o1[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) o0[gg] = o1[gg] = 0.0f;
+    auto four = [&](int jj) {
+        const float a0 = s_v[jj][d0], a1 = s_v[jj + 1][d0], a2 = s_v[jj + 2][d0], a3 = s_v[jj + 3][d0];
+        const float b0 = s_v[jj][c1], b1 = s_v[jj + 1][c1], b2 = s_v[jj + 2][c1], b3 = s_v[jj + 3][c1];
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const float4 p4 = *(const float4*)&sp[gg][jj];
+            o0[gg] = __fmaf_rn(p4.x, a0, o0[gg]);
+            o0[gg] = __fmaf_rn(p4.y, a1, o0[gg]);
+            o0[gg] = __fmaf_rn(p4.z, a2, o0[gg]);
+            o0[gg] = __fmaf_rn(p4.w, a3, o0[gg]);
+            o1[gg] = __fmaf_rn(p4.x, b0, o1[gg]);
+            o1[gg] = __fmaf_rn(p4.y, b1, o1[gg]);
+            o1[gg] = __fmaf_rn(p4.z, b2, o1[gg]);
+            o1[gg] = __fmaf_rn(p4.w, b3, o1[gg]);
+        }
+    };
+    int j = 0;
+    if (nj == kAttnChunk) {
+#pragma unroll
+        for (int jj = 0; jj < kAttnChunk; jj += 4) four(jj);
+        j = kAttnChunk;
+    } else {
+        for (; j + 4 <= nj; j += 4) four(j);
+    }
+    for (; j < nj; ++j) {
+        const float a0 = s_v[j][d0], b0 = s_v[j][c1];
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const float pj = sp[gg][j];
+            o0[gg] = __fmaf_rn(pj, a0, o0[gg]);
+            o1[gg] = __fmaf_rn(pj, b0, o1[gg]);
+        }
+    }
+    if (!store) return;  // a wave without a query this pass (it still met the barrier)
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) {
+        float* pg = part + gg * hstride;
+        pg[2 + d0] = o0[gg];
+        if (h1) pg[2 + d1] = o1[gg];
+        if (lane == 0) {
+            pg[0] = mc[gg];
+            pg[1] = lc[gg];
+        }
+    }
+}
+
+// grid (nkv, cmax, ceil(m / qb)), block 64 * qw (rep = G query heads per KV
+// head, qw queries of the block at a time); otherwise as k_attn_part.
+template <int HD, int G>
+__global__ __launch_bounds__(1024) void k_attn_part_g(AttnArgs a)
+{
+    __shared__ __align__(16) float s_k[kAttnChunk][kAttnKs];
+    __shared__ __align__(16) float s_v[kAttnChunk][kAttnMaxHd];
+    __shared__ __align__(16) float s_q[kAttnMaxRep * G][kAttnMaxHd];
+    __shared__ __align__(16) float s_p[kAttnMaxRep * G][kAttnChunk];
+    const int g = blockIdx.x, c = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = blockDim.x;
+    const int qw = nthr >> 6;  // queries per pass: one per wave
+    const int pos0 = a.d_pos ? *a.d_pos : a.pos;
+    const int i_begin = blockIdx.z * a.qb;
+    const int i_end = min(a.m, i_begin + a.qb);
+    const int j0 = c * kAttnChunk;
+    const int t_last = min(pos0 + i_end, a.max_seq);  // keys any query of the block sees
+    if (j0 >= t_last) return;                           // uniform
+    const int nstage = min(kAttnChunk, t_last - j0);
+    attn_stage_chunk<HD>(a, g, j0, nstage, HD, s_k, s_v, tid, nthr);
+
+    const int64_t hstride = (int64_t)a.cmax * (HD + 2);  // consecutive heads' partial slots
+    for (int i0 = i_begin; i0 < i_end; i0 += qw) {
+        // the last query of the pass sees the most keys (uniform)
+        if (j0 >= min(pos0 + min(i0 + qw, i_end), a.max_seq)) continue;
+        const int i = i0 + wave;
+        const int T = i < i_end ? min(pos0 + i + 1, a.max_seq) : 0;
+        const bool act = j0 < T;  // uniform per wave; an idle wave still meets the barriers
+        const int nj = act ? min(kAttnChunk, T - j0) : 0;
+        if (act) {
+            const float* qg = a.q + ((int64_t)i * a.nh + g * G) * HD;  // the group's G heads, consecutive
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg)
+                for (int d = lane; d < HD; d += 64) s_q[wave * G + gg][d] = qg[gg * HD + d];
+        }
+        __syncthreads();
+        float* part = a.part + (((int64_t)(act ? i : 0) * a.nh + g * G) * a.cmax + c) * (HD + 2);
+        attn_chunk_query_g<HD, G>(s_k, s_v, &s_q[wave * G], &s_p[wave * G], nj, a.scal, lane, part, hstride, act);
         __syncthreads();  // s_q / s_p are rewritten by the next pass
     }
 }
@@ -639,13 +785,24 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st)
         a.cmax < 1)
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)a.nkv, (unsigned)a.cmax, (unsigned)((a.m + a.qb - 1) / a.qb));
-    // qw queries of a block at a time (measured on MI355X, Llama-3-8B prefill of
-    // 512 tokens: 153 us per layer with one query at a time)
-    const int qw = std::max(1, std::min(kAttnMaxRep / rep, a.qb));
-    const dim3 block((unsigned)(64 * rep * qw));
-    if (a.hd == 128) hipLaunchKernelGGL(k_attn_part<128>, grid, block, 0, st, a);
-    else if (a.hd == 64) hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, a);
-    else hipLaunchKernelGGL(k_attn_part<0>, grid, block, 0, st, a);
+    if ((rep == 2 || rep == 4) && (a.hd == 128 || a.hd == 64) && a.qb > 1) {
+        // the query heads of a KV head in one wave, up to 16 queries at a time
+        // (measured on MI355X, Llama-3-8B prefill of 512 tokens, us per layer:
+        // 153 with one wave per head walking the block's queries one by one,
+        // 130 with a wave per (query, head))
+        const dim3 block((unsigned)(64 * std::min(kAttnMaxRep, a.qb)));
+#define BTL_ATTN_G(HDV, GV) \
+    if (a.hd == HDV && rep == GV) hipLaunchKernelGGL((k_attn_part_g<HDV, GV>), grid, block, 0, st, a);
+        BTL_ATTN_G(128, 4) else BTL_ATTN_G(128, 2) else BTL_ATTN_G(64, 4) else BTL_ATTN_G(64, 2)
+#undef BTL_ATTN_G
+    } else {
+        // a wave per (query, head), qw queries of the block at a time
+        const int qw = std::max(1, std::min(kAttnMaxRep / rep, a.qb));
+        const dim3 block((unsigned)(64 * rep * qw));
+        if (a.hd == 128) hipLaunchKernelGGL(k_attn_part<128>, grid, block, 0, st, a);
+        else if (a.hd == 64) hipLaunchKernelGGL(k_attn_part<64>, grid, block, 0, st, a);
+        else hipLaunchKernelGGL(k_attn_part<0>, grid, block, 0, st, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)a.m, (unsigned)a.nh), dim3(64), 0, st, a);
