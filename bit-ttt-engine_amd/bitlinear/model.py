@@ -16,7 +16,9 @@ Mapping of the block onto the C ABI (one row of activations per token, f32 betwe
   o = BitLinear_o(attn)                                  btl_linear_group
   x' = x + o; hs = silu(W1 RMSNorm2(x')) * W3 RMSNorm2(x')  btl_add_rmsnorm_swiglu
   mlp_out = BitLinear_down(hs)                           btl_linear_group
-and after the last block logits = lm_head(RMSNorm_f(x' + mlp_out)) in one more
+(many rows: gate and up through btl_add_rmsnorm_linear_group, then
+mlp_out = BitLinear_down(silu(gate) * up) through btl_swiglu_linear_group, the
+SwiGLU in the down call's quantiser; same bits), and after the last block logits = lm_head(RMSNorm_f(x' + mlp_out)) in one more
 btl_add_rmsnorm_linear_group.  The residual stream alternates between two
 buffers (each add writes the other one).  A one-token step moves the two adds
 into the epilogues of o and down (x' = x + o and x + mlp_out through
@@ -136,6 +138,8 @@ class BitLlamaHip:
         self.down = torch.zeros((M, c.hidden), **f32)
         if mode == "f32_ref":
             self.xn = torch.zeros((M, c.hidden), **f32)         # the normed rows
+        if mode == "f32_ref" or M > 1:
+            # gate and up of many rows (SwiGLU then runs in the down call's quantiser)
             self.gate = torch.zeros((M, c.intermediate), **f32)
             self.up = torch.zeros((M, c.intermediate), **f32)
         self.logits = torch.zeros((1, c.vocab), **f32)
@@ -178,7 +182,7 @@ class BitLlamaHip:
         self._y_o = _ptrs([self.o])
         self._y_down = _ptrs([self.down])
         self._y_logits = _ptrs([self.logits])
-        if mode == "f32_ref":
+        if mode == "f32_ref" or M > 1:
             self._y_gu = _ptrs([self.gate, self.up])
         # the model's own workspace, sized for every call it makes, so captured
         # steps never depend on the library's shared workspace
@@ -187,6 +191,7 @@ class BitLlamaHip:
         need = max(lib.btl_workspace_bytes(M, qd + 2 * kvd, c.hidden, I8),
                    lib.btl_workspace_bytes(M, c.hidden, qd, I8),
                    lib.btl_add_rmsnorm_swiglu_workspace_bytes(M, c.intermediate, c.hidden),
+                   lib.btl_workspace_bytes(M, 2 * c.intermediate, c.hidden, I8),
                    lib.btl_workspace_bytes(M, c.hidden, c.intermediate, I8),
                    lib.btl_workspace_bytes(1, c.vocab, c.hidden, I8),
                    lib.btl_attention_workspace_bytes(M, c.n_heads, ctypes.byref(self.caches[0].c)))
@@ -244,11 +249,14 @@ class BitLlamaHip:
                 continue
             check(lib.btl_linear_group(L["o"], self._y_o, 1, self.attn.data_ptr(), BTL_F32, m,
                                        c.n_heads * c.head_dim, BTL_F32, ws, wn, st))
-            check(lib.btl_add_rmsnorm_swiglu(L["gate"], L["up"], cur.data_ptr(), self.o.data_ptr(), nxt.data_ptr(),
-                                             L["n2"], c.eps, m, hid, self.hs.data_ptr(), ws, wn, st))
+            # gate and up of the summed, normed rows, then down with SwiGLU in its
+            # quantiser (the same bits as silu(gate) * up written out and quantised:
+            # one elementwise pass and one row of f32 traffic fewer)
+            check(lib.btl_add_rmsnorm_linear_group(L["gu"], self._y_gu, 2, cur.data_ptr(), self.o.data_ptr(),
+                                                   nxt.data_ptr(), L["n2"], c.eps, m, hid, BTL_F32, ws, wn, st))
             cur, nxt = nxt, cur
-            check(lib.btl_linear_group(L["down"], self._y_down, 1, self.hs.data_ptr(), BTL_F32, m, c.intermediate,
-                                       BTL_F32, ws, wn, st))
+            check(lib.btl_swiglu_linear_group(L["down"], self._y_down, 1, self.gate.data_ptr(), self.up.data_ptr(),
+                                              BTL_F32, m, c.intermediate, BTL_F32, ws, wn, st))
         last = m - 1
         delta = None if one else self.down[last].data_ptr()
         if self.dense_head:
