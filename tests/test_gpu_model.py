@@ -237,6 +237,45 @@ def test_rope_append_attention_one_token_long_cache(pos, tune):
     assert np.array_equal(kq2, kq) and np.array_equal(ks2, ks), "no append"
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (32, 2, 64)])
+def test_rope_append_attention_one_token_merge_sequence(nh, nkv, hd, tune):
+    # The merge in the launch over a sequence of calls on one caller workspace:
+    # falling and rising positions (the workspace keeps the partials of earlier
+    # calls), the workspace overwritten with other bits between some calls,
+    # more key chunks than the merge loads ahead (16), the last call repeated;
+    # the counters must be back at zero after every launch, each call against
+    # the oracle.
+    print("rope_append_attention sequence", nh, nkv, hd, flush=True)
+    tune("BTL_ATTN_MERGE", 1)
+    S = 2048
+    cos, sin, dc, ds = rope_dev(500000.0, hd, S)
+    cache = Cache(nkv, S, hd)
+    _fill_cache(cache, S, seed=nh + nkv)
+    wn = bl.lib.btl_attention_workspace_bytes(1, nh, ctypes.byref(cache.c))
+    ws = torch.zeros((wn,), dtype=torch.uint8, device=DEV)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(3)
+    plan = [1500, 300, 1500, 64, 63, 2047, 1100, 1100]
+    for i, pos in enumerate(plan):
+        rng = np.random.default_rng(100 + i)
+        q = rng.standard_normal((1, nh * hd)).astype(np.float32)
+        k = rng.standard_normal((1, nkv * hd)).astype(np.float32)
+        v = rng.standard_normal((1, nkv * hd)).astype(np.float32)
+        if i in (3, 6):
+            ws.random_(0, 256, generator=gen)
+        qt, kt, vt = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
+        d_pos = torch.tensor([pos], dtype=torch.int32, device=DEV)
+        out = torch.full((1, nh * hd), 3.0, device=DEV)
+        bl.check(bl.lib.btl_rope_append_attention(qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), 1, nh,
+                                                  ctypes.byref(cache.c), 0, d_pos.data_ptr(), dc.data_ptr(),
+                                                  ds.data_ptr(), out.data_ptr(), ctypes.c_void_p(ws.data_ptr()),
+                                                  wn, stream()))
+        bl.check(bl.lib.btl_check_faults(stream()))
+        kq, ks, vq, vs = cache.host()
+        qr = orc.rope_apply(q[0].reshape(nh, hd), cos[pos], sin[pos]).reshape(-1)
+        assert_same(out[0], orc.attn_decode(qr, kq, ks, vq, vs, nh, pos + 1), "call %d pos %d" % (i, pos))
+
+
 @pytest.mark.parametrize("m,pos", [(2, 0), (17, 40), (70, 60)])
 def test_rope_append_attention_many_tokens(m, pos):
     nh, nkv, hd, S = 8, 2, 128, 200
