@@ -341,12 +341,21 @@ __global__ __launch_bounds__(1024) void k_attn_part(AttnArgs a)
 // key and value element is read from LDS once per group instead of once per
 // head (the partials of a long prompt were bound by those reads).  Per
 // (query, head) the arithmetic is attn_chunk_query's, in the same order.
+// The queries' elements come from global memory by scalar loads (qg: the G
+// heads' rows of this wave's query, consecutive, the same for every lane; read
+// only in this launch), an SGPR operand of each fma, instead of LDS broadcast
+// reads, which cost the LDS as much as the key reads (measured on MI355X,
+// Llama-3-8B shapes, a 512-token prompt through the decoder: 9.71-9.79 ->
+// 9.41-9.44 ms; the p row by readlane instead of LDS as well: 9.65-9.67).
+typedef const __attribute__((address_space(4))) float* attn_qptr;
+
 template <int HD, int G>
 __device__ __forceinline__ void attn_chunk_query_g(const float (*s_k)[kAttnKs], const float (*s_v)[kAttnMaxHd],
-                                                   const float (*sq)[kAttnMaxHd], float (*sp)[kAttnChunk], int nj,
+                                                   const float* qg, float (*sp)[kAttnChunk], int nj,
                                                    float scal, int lane, float* part, int64_t hstride, bool store)
 {
     static_assert(HD == 64 || HD == 128, "head size 64 or 128");
+    const attn_qptr qs = (attn_qptr)qg;
     float sc[G];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) sc[gg] = -__builtin_inff();
@@ -359,7 +368,8 @@ __device__ __forceinline__ void attn_chunk_query_g(const float (*s_k)[kAttnKs], 
             const float4 k4 = *(const float4*)&s_k[lane][d];
 #pragma unroll
             for (int gg = 0; gg < G; ++gg) {
-                const float4 q4 = *(const float4*)&sq[gg][d];
+                const float4 q4 = make_float4(qs[gg * HD + d], qs[gg * HD + d + 1], qs[gg * HD + d + 2],
+                                              qs[gg * HD + d + 3]);
                 acc[gg] = __fmaf_rn(q4.x, k4.x, acc[gg]);
                 acc[gg] = __fmaf_rn(q4.y, k4.y, acc[gg]);
                 acc[gg] = __fmaf_rn(q4.z, k4.z, acc[gg]);
@@ -437,10 +447,10 @@ __global__ __launch_bounds__(1024) void k_attn_part_g(AttnArgs a)
 {
     __shared__ __align__(16) float s_k[kAttnChunk][kAttnKs];
     __shared__ __align__(16) float s_v[kAttnChunk][kAttnMaxHd];
-    __shared__ __align__(16) float s_q[kAttnMaxRep * G][kAttnMaxHd];
     __shared__ __align__(16) float s_p[kAttnMaxRep * G][kAttnChunk];
     const int g = blockIdx.x, c = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the query rows' scalar loads
     const int nthr = blockDim.x;
     const int qw = nthr >> 6;  // queries per pass: one per wave
     const int pos0 = a.d_pos ? *a.d_pos : a.pos;
@@ -451,6 +461,7 @@ __global__ __launch_bounds__(1024) void k_attn_part_g(AttnArgs a)
     if (j0 >= t_last) return;                           // uniform
     const int nstage = min(kAttnChunk, t_last - j0);
     attn_stage_chunk<HD>(a, g, j0, nstage, HD, s_k, s_v, tid, nthr);
+    __syncthreads();  // the staged chunk
 
     const int64_t hstride = (int64_t)a.cmax * (HD + 2);  // consecutive heads' partial slots
     for (int i0 = i_begin; i0 < i_end; i0 += qw) {
@@ -460,16 +471,11 @@ __global__ __launch_bounds__(1024) void k_attn_part_g(AttnArgs a)
         const int T = i < i_end ? min(pos0 + i + 1, a.max_seq) : 0;
         const bool act = j0 < T;  // uniform per wave; an idle wave still meets the barriers
         const int nj = act ? min(kAttnChunk, T - j0) : 0;
-        if (act) {
-            const float* qg = a.q + ((int64_t)i * a.nh + g * G) * HD;  // the group's G heads, consecutive
-#pragma unroll
-            for (int gg = 0; gg < G; ++gg)
-                for (int d = lane; d < HD; d += 64) s_q[wave * G + gg][d] = qg[gg * HD + d];
-        }
-        __syncthreads();
+        // the group's G heads of query i, consecutive (an idle wave: query i_begin's, unused)
+        const float* qg = a.q + ((int64_t)(act ? i : i_begin) * a.nh + g * G) * HD;
         float* part = a.part + (((int64_t)(act ? i : 0) * a.nh + g * G) * a.cmax + c) * (HD + 2);
-        attn_chunk_query_g<HD, G>(s_k, s_v, &s_q[wave * G], &s_p[wave * G], nj, a.scal, lane, part, hstride, act);
-        __syncthreads();  // s_q / s_p are rewritten by the next pass
+        attn_chunk_query_g<HD, G>(s_k, s_v, qg, &s_p[wave * G], nj, a.scal, lane, part, hstride, act);
+        __syncthreads();  // s_p is rewritten by the next pass
     }
 }
 
